@@ -1,0 +1,230 @@
+"""CPU oracle for the quantized hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg import this package, and only as the checker. The product package
+(``ggmlc_amd``) never imports it.
+
+Two libraries are wrapped:
+
+* ``liboracle.so`` — this repo's C restatement (``gq_oracle.c``) of the
+  reference's quantize / mul_mat / set_rows / flash_attn_ext / soft_max.
+* ``_ref/libggmlref.so`` — the reference's own ggml 0.20.2 CPU backend compiled
+  from ``/root/reference/third_party/ggml`` by ``oracle/Makefile`` (present only
+  where that build ran; tests that need it skip otherwise).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libggmlref.so"
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+Q8_0, Q4_0 = 8, 2
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(_vp)
+
+
+def build() -> None:
+    """Compile the restatement (and the reference build where the tree exists)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not ORACLE_SO.exists():
+            build()
+        L = ctypes.CDLL(str(ORACLE_SO))
+        L.or_fp32_to_fp16.restype = ctypes.c_uint16
+        L.or_fp32_to_fp16.argtypes = [_f32]
+        L.or_fp16_to_fp32.restype = _f32
+        L.or_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        for n in ("or_fp32_to_fp16_row", "or_quantize_row_q8_0", "or_quantize_row_q8_0_ref",
+                  "or_quantize_q8_0_py", "or_quantize_q4_0_py", "or_dequantize_row_q8_0",
+                  "or_dequantize_row_q4_0"):
+            getattr(L, n).argtypes = [_vp, _vp, _i64]
+            getattr(L, n).restype = None
+        L.or_mul_mat.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32]
+        L.or_mul_mat_q8act.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32]
+        L.or_set_rows_f32_f16.argtypes = [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]
+        L.or_flash_attn_ext_f16.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
+                                            _vp, _f32, _vp, _i32, _i32]
+        L.or_soft_max_f32.argtypes = [_vp, _i64, _i64, _vp, _f32, _vp]
+        L.or_pad_kv_len.restype = _i64
+        L.or_pad_kv_len.argtypes = [_i64, _i64, _i64]
+        L.or_fill_causal_mask_f16.argtypes = [_vp, _i64, _i64, _i64]
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return REF_SO.exists()
+
+
+def ref():
+    """The compiled reference ggml CPU backend (raises if it was not built)."""
+    global _ref
+    if _ref is None:
+        if not REF_SO.exists():
+            raise FileNotFoundError(f"{REF_SO} not built (needs /root/reference)")
+        L = ctypes.CDLL(str(REF_SO))
+        L.ref_ggml_version.restype = ctypes.c_char_p
+        for n in ("ref_quantize_row_q8_0", "ref_quantize_row_q8_0_ref"):
+            getattr(L, n).argtypes = [_vp, _vp, _i64]
+            getattr(L, n).restype = None
+        L.ref_mul_mat.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32]
+        L.ref_set_rows_f32_f16.argtypes = [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32]
+        L.ref_flash_attn_ext_f16.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
+                                             _vp, _f32, _vp, _i32]
+        L.ref_soft_max_f32.argtypes = [_vp, _i64, _i64, _vp, _f32, _vp, _i32]
+        L.ref_init()
+        _ref = L
+    return _ref
+
+
+# ----------------------------------------------------------------- numpy API
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def fp32_to_fp16_bits(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().or_fp32_to_fp16_row(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def quantize_row_q8_0(x, impl: str = "oracle") -> np.ndarray:
+    """x86 activation quantizer on each row of x ([..., K]); returns uint8 [..., K/32*34]."""
+    x = _c(x, np.float32)
+    K = x.shape[-1]
+    y = np.empty(x.shape[:-1] + (K // 32 * 34,), np.uint8)
+    f = lib().or_quantize_row_q8_0 if impl == "oracle" else ref().ref_quantize_row_q8_0
+    f(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def quantize_weights(w, wtype: int) -> np.ndarray:
+    """ggmlc's Python weight quantizer semantics; w [N, K] -> uint8 [N, K/32*block]."""
+    w = _c(w, np.float32)
+    N, K = w.shape
+    y = np.empty((N, K // 32 * BLOCK_BYTES[wtype]), np.uint8)
+    f = lib().or_quantize_q8_0_py if wtype == Q8_0 else lib().or_quantize_q4_0_py
+    f(_ptr(w), _ptr(y), w.size)
+    return y
+
+
+def dequantize(wq, wtype: int, K: int) -> np.ndarray:
+    wq = _c(wq, np.uint8)
+    N = wq.size // (K // 32 * BLOCK_BYTES[wtype])
+    y = np.empty((N, K), np.float32)
+    f = lib().or_dequantize_row_q8_0 if wtype == Q8_0 else lib().or_dequantize_row_q4_0
+    f(_ptr(wq), _ptr(y), N * K)
+    return y
+
+
+def mul_mat(wq, wtype: int, K: int, x, impl: str = "oracle", n_threads: int = 8) -> np.ndarray:
+    """Y[M, N] = ggml_mul_mat(W[N rows of K], X[M, K])."""
+    wq = _c(wq, np.uint8)
+    x = _c(x, np.float32).reshape(-1, K)
+    M = x.shape[0]
+    N = wq.size // (K // 32 * BLOCK_BYTES[wtype])
+    y = np.empty((M, N), np.float32)
+    if impl == "oracle":
+        r = lib().or_mul_mat(wtype, _ptr(wq), K, N, _ptr(x), M, _ptr(y), n_threads)
+    else:
+        r = ref().ref_mul_mat(wtype, _ptr(wq), K, N, _ptr(x), M, _ptr(y), n_threads)
+    if r != 0:
+        raise RuntimeError("mul_mat failed")
+    return y
+
+
+def set_rows_f32_f16(cache: np.ndarray, src, idx, impl: str = "oracle") -> np.ndarray:
+    """cache uint16 [B, H, max_ctx, hd] (ggml [hd, max_ctx, H, B]) updated in a copy."""
+    out = np.array(cache, dtype=np.uint16, copy=True, order="C")
+    B, H, max_ctx, hd = out.shape
+    src = _c(src, np.float32)
+    s = src.shape[-2]
+    idx = _c(idx, np.int64)
+    if impl == "oracle":
+        r = lib().or_set_rows_f32_f16(_ptr(out), hd, max_ctx, H, B, _ptr(src), s, _ptr(idx))
+    else:
+        r = ref().ref_set_rows_f32_f16(_ptr(out), hd, max_ctx, H, B, _ptr(src), s, _ptr(idx), 1)
+    if r != 0:
+        raise ValueError("set_rows: index out of range")
+    return out
+
+
+def flash_attn_ext_f16(q, kc, vc, n_kv: int, mask=None, scale: float | None = None,
+                       impl: str = "oracle", mode: int = 0, n_threads: int = 1) -> np.ndarray:
+    """q fp32 [Hq, s, hd]; kc/vc uint16 [Hkv, max_ctx, hd]; mask uint16 [s, n_kv] or None.
+
+    Returns fp32 [s, Hq, hd] (the op's permuted output)."""
+    q = _c(q, np.float32)
+    Hq, s, hd = q.shape
+    kc = _c(kc, np.uint16)
+    vc = _c(vc, np.uint16)
+    Hkv, max_ctx, _ = kc.shape
+    if scale is None:
+        scale = 1.0 / float(np.sqrt(np.float32(hd)))
+    m = None if mask is None else _c(mask, np.uint16)
+    out = np.empty((s, Hq, hd), np.float32)
+    if impl == "oracle":
+        r = lib().or_flash_attn_ext_f16(_ptr(q), hd, s, Hq, _ptr(kc), _ptr(vc), max_ctx, Hkv, n_kv,
+                                        _ptr(m), scale, _ptr(out), mode, n_threads)
+    else:
+        r = ref().ref_flash_attn_ext_f16(_ptr(q), hd, s, Hq, _ptr(kc), _ptr(vc), max_ctx, Hkv, n_kv,
+                                         _ptr(m), scale, _ptr(out), n_threads)
+    if r != 0:
+        raise RuntimeError("flash_attn_ext failed")
+    return out
+
+
+def soft_max_f32(x, mask=None, scale: float = 1.0, impl: str = "oracle") -> np.ndarray:
+    x = _c(x, np.float32)
+    nrows, ncols = x.shape
+    m = None if mask is None else _c(mask, np.uint16)
+    y = np.empty_like(x)
+    if impl == "oracle":
+        lib().or_soft_max_f32(_ptr(x), ncols, nrows, _ptr(m), scale, _ptr(y))
+    else:
+        ref().ref_soft_max_f32(_ptr(x), ncols, nrows, _ptr(m), scale, _ptr(y), 1)
+    return y
+
+
+def pad_kv_len(n_kv: int, max_ctx: int, n_pad: int = 256) -> int:
+    return int(lib().or_pad_kv_len(n_kv, max_ctx, n_pad))
+
+
+def causal_mask_f16(pos: int, s_q: int, s_kv: int) -> np.ndarray:
+    m = np.empty((s_q, s_kv), np.uint16)
+    lib().or_fill_causal_mask_f16(_ptr(m), pos, s_q, s_kv)
+    return m
+
+
+def n_cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1

@@ -1,0 +1,158 @@
+// Test infrastructure only: a thin C entry layer over the reference's own ggml
+// CPU backend (ggml 0.20.2, vendored at third_party/ggml in the reference tree),
+// compiled from the reference sources by oracle/Makefile into oracle/_ref/.
+//
+// Nothing here re-implements an operator: every function builds a one-node ggml
+// graph exactly the way ggmlc's executor does (runtime/src/executor.cpp) and runs
+// it with ggml_graph_compute_with_ctx on the ggml CPU backend. The product path
+// never links or loads this library; only tests/, __graft_entry__.smoke() and
+// bench.py's cpu_baseline leg do.
+//
+// Reference call sites mirrored:
+//   quantize_row_q8_0  -> ggml_get_type_traits_cpu(Q8_0)->from_float
+//                         (ggml-cpu/ggml-cpu.c:271-279, arch/x86/quants.c:302-398)
+//   mul_mat            -> ggml_mul_mat (ggml.c:3278), executor.cpp:2362-2447
+//   set_rows           -> ggml_set_rows (ggml.c:3937), executor.cpp:2181-2184
+//   flash_attn_ext     -> ggml_flash_attn_ext (ggml.c:5402), executor.cpp:2195-2197
+//   soft_max           -> ggml_soft_max_ext (ggml.c:4081), executor.cpp:2358-2361
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "ggml.h"
+#include "ggml-cpu.h"
+
+// ggml-quants.h:23 (declared here with an opaque block pointer; same C symbol)
+extern "C" void quantize_row_q8_0_ref(const float* x, void* y, int64_t k);
+
+namespace {
+
+struct Ctx {
+    ggml_context* ctx = nullptr;
+    explicit Ctx(size_t bytes) {
+        ggml_init_params p = {bytes + 64 * 1024 * 1024, nullptr, false};
+        ctx = ggml_init(p);
+    }
+    ~Ctx() {
+        if (ctx) ggml_free(ctx);
+    }
+};
+
+int run_graph(ggml_context* ctx, ggml_tensor* out, int n_threads) {
+    ggml_cgraph* gf = ggml_new_graph(ctx);
+    ggml_build_forward_expand(gf, out);
+    return ggml_graph_compute_with_ctx(ctx, gf, n_threads) == GGML_STATUS_SUCCESS ? 0 : -1;
+}
+
+}  // namespace
+
+extern "C" {
+
+void ref_init(void) { ggml_cpu_init(); }
+
+const char* ref_ggml_version(void) { return ggml_version(); }
+
+// x86 runtime activation quantizer (the one the CPU backend runs on src1).
+void ref_quantize_row_q8_0(const float* x, void* y, int64_t k) {
+    ggml_cpu_init();
+    ggml_get_type_traits_cpu(GGML_TYPE_Q8_0)->from_float(x, y, k);
+}
+
+// ggml's scalar reference quantizers (ggml-quants.c:113-148, 276-299).
+void ref_quantize_row_q8_0_ref(const float* x, void* y, int64_t k) {
+    quantize_row_q8_0_ref(x, y, k);
+}
+
+// dst[M][N] = W(type, N rows of K) x X(M rows of K, fp32). type: 2 = Q4_0, 8 = Q8_0, 1 = F16, 0 = F32.
+int ref_mul_mat(int wtype, const void* w, int64_t K, int64_t N, const float* x, int64_t M,
+                float* dst, int n_threads) {
+    ggml_cpu_init();
+    const ggml_type t = (ggml_type)wtype;
+    const size_t wbytes = ggml_row_size(t, K) * (size_t)N;
+    Ctx c(wbytes + (size_t)(K * M + N * M) * sizeof(float) * 2 + (size_t)K * M);
+    if (!c.ctx) return -1;
+    ggml_tensor* W = ggml_new_tensor_2d(c.ctx, t, K, N);
+    ggml_tensor* X = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F32, K, M);
+    memcpy(W->data, w, wbytes);
+    memcpy(X->data, x, sizeof(float) * K * M);
+    ggml_tensor* Y = ggml_mul_mat(c.ctx, W, X);
+    if (run_graph(c.ctx, Y, n_threads) != 0) return -1;
+    memcpy(dst, Y->data, sizeof(float) * N * M);
+    return 0;
+}
+
+// KV-cache row scatter exactly as the executor wires it: dst is the F16 cache
+// [hd, max_ctx, H, B] (contiguous), src the F32 rows [hd, s, H, B], idx I64 [s].
+// The cache is updated in place (dst is input and output).
+int ref_set_rows_f32_f16(uint16_t* cache, int64_t hd, int64_t max_ctx, int64_t H, int64_t B,
+                         const float* src, int64_t s, const int64_t* idx, int n_threads) {
+    ggml_cpu_init();
+    const size_t cache_bytes = sizeof(uint16_t) * hd * max_ctx * H * B;
+    Ctx c(cache_bytes + sizeof(float) * hd * s * H * B + sizeof(int64_t) * s);
+    if (!c.ctx) return -1;
+    ggml_tensor* dst = ggml_new_tensor_4d(c.ctx, GGML_TYPE_F16, hd, max_ctx, H, B);
+    ggml_tensor* sr = ggml_new_tensor_4d(c.ctx, GGML_TYPE_F32, hd, s, H, B);
+    ggml_tensor* ix = ggml_new_tensor_1d(c.ctx, GGML_TYPE_I64, s);
+    memcpy(dst->data, cache, cache_bytes);
+    memcpy(sr->data, src, sizeof(float) * hd * s * H * B);
+    memcpy(ix->data, idx, sizeof(int64_t) * s);
+    ggml_tensor* out = ggml_set_rows(c.ctx, dst, sr, ix);
+    if (run_graph(c.ctx, out, n_threads) != 0) return -1;
+    memcpy(cache, dst->data, cache_bytes);
+    return 0;
+}
+
+// FLASH_ATTN_EXT over the active prefix of a padded KV cache, as the executor
+// builds it with set_rows (executor.cpp:2143-2197):
+//   q    F32 [hd, s, Hq, 1] contiguous
+//   kc,vc F16 caches [hd, max_ctx, Hkv, 1]; the op sees views [hd, n_kv, Hkv, 1]
+//   mask F16 [n_kv, s] contiguous, or nullptr
+//   out  F32 [hd, Hq, s, 1] (permuted layout produced by the op)
+int ref_flash_attn_ext_f16(const float* q, int64_t hd, int64_t s, int64_t Hq,
+                           const uint16_t* kc, const uint16_t* vc, int64_t max_ctx, int64_t Hkv,
+                           int64_t n_kv, const uint16_t* mask, float scale, float* out,
+                           int n_threads) {
+    ggml_cpu_init();
+    const size_t cache_bytes = sizeof(uint16_t) * hd * max_ctx * Hkv;
+    Ctx c(2 * cache_bytes + sizeof(float) * hd * s * Hq * 2 + sizeof(uint16_t) * n_kv * s +
+          (size_t)16 * 1024 * 1024);
+    if (!c.ctx) return -1;
+    ggml_tensor* Q = ggml_new_tensor_4d(c.ctx, GGML_TYPE_F32, hd, s, Hq, 1);
+    ggml_tensor* KC = ggml_new_tensor_4d(c.ctx, GGML_TYPE_F16, hd, max_ctx, Hkv, 1);
+    ggml_tensor* VC = ggml_new_tensor_4d(c.ctx, GGML_TYPE_F16, hd, max_ctx, Hkv, 1);
+    memcpy(Q->data, q, sizeof(float) * hd * s * Hq);
+    memcpy(KC->data, kc, cache_bytes);
+    memcpy(VC->data, vc, cache_bytes);
+    ggml_tensor* K = ggml_view_4d(c.ctx, KC, hd, n_kv, Hkv, 1, KC->nb[1], KC->nb[2], KC->nb[3], 0);
+    ggml_tensor* V = ggml_view_4d(c.ctx, VC, hd, n_kv, Hkv, 1, VC->nb[1], VC->nb[2], VC->nb[3], 0);
+    ggml_tensor* MK = nullptr;
+    if (mask) {
+        MK = ggml_new_tensor_4d(c.ctx, GGML_TYPE_F16, n_kv, s, 1, 1);
+        memcpy(MK->data, mask, sizeof(uint16_t) * n_kv * s);
+    }
+    ggml_tensor* O = ggml_flash_attn_ext(c.ctx, Q, K, V, MK, scale, 0.0f, 0.0f);
+    if (run_graph(c.ctx, O, n_threads) != 0) return -1;
+    memcpy(out, O->data, sizeof(float) * hd * Hq * s);
+    return 0;
+}
+
+// SOFT_MAX: y = softmax(x*scale + mask) per row of ncols; mask F16 [ncols, nrows] or nullptr.
+int ref_soft_max_f32(const float* x, int64_t ncols, int64_t nrows, const uint16_t* mask,
+                     float scale, float* y, int n_threads) {
+    ggml_cpu_init();
+    Ctx c(sizeof(float) * ncols * nrows * 2 + sizeof(uint16_t) * ncols * nrows);
+    if (!c.ctx) return -1;
+    ggml_tensor* X = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F32, ncols, nrows);
+    memcpy(X->data, x, sizeof(float) * ncols * nrows);
+    ggml_tensor* MK = nullptr;
+    if (mask) {
+        MK = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F16, ncols, nrows);
+        memcpy(MK->data, mask, sizeof(uint16_t) * ncols * nrows);
+    }
+    ggml_tensor* Y = ggml_soft_max_ext(c.ctx, X, MK, scale, 0.0f);
+    if (run_graph(c.ctx, Y, n_threads) != 0) return -1;
+    memcpy(y, Y->data, sizeof(float) * ncols * nrows);
+    return 0;
+}
+
+}  // extern "C"

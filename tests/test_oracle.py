@@ -1,0 +1,316 @@
+"""Pins the CPU oracle (oracle/gq_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against (a) the golden vectors written by the
+reference's own compiled ggml (tests/golden, from oracle/_ref), (b) the compiled
+reference directly when oracle/_ref is present, and (c) closed forms / brute
+force chosen so that a dropped term, a wrong sign or index, or a transposed
+operand fails. CPU only.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+from conftest import have_ref
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def h2f(u):
+    return np.asarray(u, np.uint16).view(np.float16).astype(np.float32)
+
+
+# ------------------------------------------------------------------ fp16 ---
+
+def test_fp16_conversion_matches_ieee_rne():
+    rng = np.random.default_rng(0)
+    parts = [rng.standard_normal(200_000).astype(np.float32) * s for s in (1e-9, 3e-7, 6e-5, 1.0, 3e3, 6.5e4, 1e5)]
+    bits = rng.integers(0, 2**32, 300_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    bits = bits[np.isfinite(bits)]
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 65504, 65519.996, 65520, 2**-24, 2**-25,
+                        np.nextafter(np.float32(2**-25), np.float32(1)), 3 * 2**-26, 1e-45, 6.097555e-5],
+                       np.float32)
+    x = np.concatenate(parts + [bits, special])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.fp32_to_fp16_bits(x), want)
+    # NaN stays NaN (quiet)
+    n = O.fp32_to_fp16_bits(np.array([np.nan], np.float32))
+    assert np.isnan(n.view(np.float16)[0])
+
+
+# ------------------------------------------------------- activation quant ---
+
+def test_quantize_q8_0_golden(golden_dir):
+    g = np.load(golden_dir / "quantize_q8_0.npz")
+    assert np.array_equal(O.quantize_row_q8_0(g["x"]), g["q"])
+
+
+def test_quantize_q8_0_closed_forms():
+    x = np.zeros((1, 128), np.float32)
+    x[0, 32:64] = np.linspace(-3, 3, 32)          # +-amax -> +-127, d = fp16(3/127)
+    x[0, 64:96] = 0.25                            # constant -> all 127
+    x[0, 96] = 127.0                              # id = 1: q = RNE(x)
+    x[0, 97:128] = np.arange(31, dtype=np.float32) - 15.5  # halves: RNE to even
+    q = O.quantize_row_q8_0(x).reshape(4, 34)
+    d = q[:, :2].copy().view(np.uint16)[:, 0]
+    qs = q[:, 2:].view(np.int8)
+    assert d[0] == 0 and not qs[0].any()
+    assert d[1] == f16(np.float32(3.0) / np.float32(127.0))[()]
+    assert qs[1, 0] == -127 and qs[1, -1] == 127
+    assert (qs[2] == 127).all()
+    assert qs[3, 0] == 127
+    want = np.round(np.arange(31, dtype=np.float64) - 15.5).astype(np.int8)  # numpy rounds half to even
+    assert np.array_equal(qs[3, 1:], want)
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built")
+def test_quantize_q8_0_vs_reference_random():
+    rng = np.random.default_rng(7)
+    for scale in (1e-4, 1.0, 50.0):
+        x = (rng.standard_normal((64, 4096)) * scale).astype(np.float32)
+        x[::3] = np.round(x[::3] * 4) / 4
+        assert np.array_equal(O.quantize_row_q8_0(x), O.quantize_row_q8_0(x, impl="ref"))
+
+
+# ------------------------------------------------------ weight quantizers ---
+
+def _np_quantize_q8_0(w):
+    """numpy statement of quantize.py:10-25 (float32 array semantics)."""
+    b = w.reshape(-1, 32).astype(np.float32)
+    mx = np.max(np.abs(b), axis=1)
+    sc = np.where(mx > 0, mx / np.float32(127.0), np.float32(0.0)).astype(np.float32)
+    inv = (np.float32(1.0) / np.where(sc != 0, sc, np.float32(1.0))).astype(np.float32)[:, None]
+    q = np.clip(np.round(b * inv), -128, 127).astype(np.int8)
+    return np.hstack([sc.astype(np.float16).view(np.uint8).reshape(-1, 2), q.view(np.uint8)]).ravel()
+
+
+def _np_quantize_q4_0(w):
+    """numpy statement of quantize.py:65-107."""
+    b = w.reshape(-1, 32).astype(np.float32)
+    i = np.argmax(np.abs(b), axis=1)
+    sm = b[np.arange(b.shape[0]), i]
+    sc = np.where(sm != 0, sm / np.float32(-8.0), np.float32(0.0)).astype(np.float32)
+    safe = np.where(sc != 0, sc, np.float32(1.0))[:, None]
+    q = np.where(sc[:, None] != 0, np.clip(np.round(b / safe) + 8, 0, 15), 8).astype(np.uint8)
+    packed = (q[:, :16] & 15) | ((q[:, 16:] & 15) << 4)
+    return np.hstack([sc.astype(np.float16).view(np.uint8).reshape(-1, 2), packed]).ravel()
+
+
+def test_weight_quantizers_match_numpy_semantics():
+    rng = np.random.default_rng(42)
+    w = (rng.standard_normal((64, 4096)) * 0.02).astype(np.float32)
+    w[0, :32] = 0
+    w[1, :32] = np.round(w[1, :32] * 1000) / 1000
+    assert np.array_equal(O.quantize_weights(w, O.Q8_0).ravel(), _np_quantize_q8_0(w))
+    assert np.array_equal(O.quantize_weights(w, O.Q4_0).ravel(), _np_quantize_q4_0(w))
+
+
+def test_weight_quantizers_hand_blocks():
+    x = np.zeros((1, 32), np.float32)
+    x[0, :6] = [1.0, -0.5, 0.25, -2.0, 0.125, 0.375]
+    # Q4_0: signed max -2 -> scale 0.25; q = RNE(x/0.25) + 8
+    q4 = O.quantize_weights(x, O.Q4_0).ravel()
+    assert q4[:2].view(np.float16)[0] == np.float16(0.25)
+    nib = np.concatenate([q4[2:] & 15, q4[2:] >> 4])
+    assert list(nib[:6]) == [12, 6, 9, 0, 8, 10]   # 0.125/0.25 = 0.5 -> 0 (even); 1.5 -> 2
+    assert (nib[6:] == 8).all()
+    # Q8_0: amax 2 -> scale 2/127; -0.5 * 63.5 = -31.75 -> -32
+    q8 = O.quantize_weights(x, O.Q8_0).ravel()
+    qs = q8[2:].view(np.int8)
+    assert qs[3] == -127 and qs[0] == 64 and qs[1] == -32
+
+
+def test_weight_quantizer_roundtrip_thresholds():
+    """The reference's own thresholds (tests/quantization/test_quantization.py:24-62)."""
+    rng = np.random.default_rng(42)
+    w = rng.standard_normal((64, 128)).astype(np.float32)
+    for wt, cos_min, err_max in ((O.Q8_0, 0.9999, 0.05), (O.Q4_0, 0.99, 0.6)):
+        d = O.dequantize(O.quantize_weights(w, wt), wt, 128)
+        cos = float((d * w).sum() / np.linalg.norm(d) / np.linalg.norm(w))
+        assert cos > cos_min and np.abs(d - w).max() < err_max
+
+
+def test_dequantize_closed_form():
+    rng = np.random.default_rng(3)
+    raw8 = rng.integers(0, 256, (5, 34), dtype=np.uint8)
+    raw8[:, :2] = f16(rng.uniform(0.01, 1, 5)).view(np.uint8).reshape(5, 2)
+    d = h2f(raw8[:, :2].copy().view(np.uint16)[:, 0])
+    want = raw8[:, 2:].view(np.int8).astype(np.float32) * d[:, None]
+    assert np.array_equal(O.dequantize(raw8.ravel(), O.Q8_0, 32 * 5).reshape(5, 32), want)
+    raw4 = rng.integers(0, 256, (5, 18), dtype=np.uint8)
+    raw4[:, :2] = raw8[:, :2]
+    lo = (raw4[:, 2:] & 15).astype(np.float32) - 8
+    hi = (raw4[:, 2:] >> 4).astype(np.float32) - 8
+    want4 = np.concatenate([lo, hi], axis=1) * d[:, None]
+    assert np.array_equal(O.dequantize(raw4.ravel(), O.Q4_0, 32 * 5).reshape(5, 32), want4)
+
+
+# ---------------------------------------------------------------- mul_mat ---
+
+def _golden_mm(golden_dir):
+    return sorted(golden_dir.glob("mul_mat_*.npz"))
+
+
+def test_mul_mat_golden(golden_dir):
+    files = _golden_mm(golden_dir)
+    assert len(files) >= 10
+    for f in files:
+        g = np.load(f)
+        y = O.mul_mat(g["w"], int(g["wtype"]), int(g["K"]), g["x"], n_threads=1)
+        rel = np.abs(y - g["y"]).max() / np.abs(g["y"]).max()
+        assert rel < 2e-6, (f.name, rel)
+
+
+def test_mul_mat_brute_force_blocks():
+    """Double-precision dot of dequantized operands with the SAME quantized activation."""
+    rng = np.random.default_rng(5)
+    K, N, M = 512, 37, 3
+    for wt in (O.Q8_0, O.Q4_0):
+        w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        wq = O.quantize_weights(w, wt)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        xq = O.quantize_row_q8_0(x)
+        wd = O.dequantize(wq, wt, K).astype(np.float64)
+        xd = O.dequantize(xq, O.Q8_0, K).astype(np.float64)
+        want = xd @ wd.T
+        got = O.mul_mat(wq, wt, K, x)
+        assert np.abs(got - want).max() <= 1e-6 * np.abs(want).max()
+        # using the unquantized activation instead is visibly different (the
+        # oracle really applies the x86 activation quantizer first)
+        assert np.abs(got - x.astype(np.float64) @ wd.T).max() > 1e-4 * np.abs(want).max()
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built")
+def test_mul_mat_vs_reference_real_shape():
+    rng = np.random.default_rng(11)
+    K, N = 4096, 256
+    for wt in (O.Q8_0, O.Q4_0):
+        w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        wq = O.quantize_weights(w, wt)
+        for M in (1, 8):
+            x = rng.standard_normal((M, K)).astype(np.float32)
+            r = O.mul_mat(wq, wt, K, x, impl="ref")
+            o = O.mul_mat(wq, wt, K, x)
+            assert np.abs(o - r).max() / np.abs(r).max() < 2e-6
+
+
+# --------------------------------------------------------------- set_rows ---
+
+def test_set_rows_golden(golden_dir):
+    g = np.load(golden_dir / "set_rows_f32_f16.npz")
+    out = O.set_rows_f32_f16(g["cache"], g["src"], g["idx"])
+    assert np.array_equal(out, g["out"])
+
+
+def test_set_rows_closed_form():
+    rng = np.random.default_rng(9)
+    cache = f16(rng.standard_normal((2, 3, 20, 16)))
+    src = (rng.standard_normal((2, 3, 4, 16)) * 100).astype(np.float32)
+    idx = np.array([5, 0, 19, 7])
+    out = O.set_rows_f32_f16(cache, src, idx)
+    touched = np.zeros(20, bool)
+    touched[idx] = True
+    assert np.array_equal(out[:, :, ~touched], cache[:, :, ~touched])
+    for i, r in enumerate(idx):
+        assert np.array_equal(out[:, :, r], f16(src[:, :, i]))
+    with pytest.raises(ValueError):
+        O.set_rows_f32_f16(cache, src, np.array([1, 2, 20, 3]))
+
+
+# -------------------------------------------------------------- attention ---
+
+def _np_attention(q, kc, vc, n_kv, mask, scale):
+    Hq, s, hd = q.shape
+    Hkv = kc.shape[0]
+    g = Hq // Hkv
+    out = np.zeros((s, Hq, hd))
+    for h in range(Hq):
+        k = h2f(kc[h // g, :n_kv]).astype(np.float64)
+        v = h2f(vc[h // g, :n_kv]).astype(np.float64)
+        sc = q[h].astype(np.float64) @ k.T * scale
+        if mask is not None:
+            sc = sc + h2f(mask).astype(np.float64)
+        sc -= sc.max(axis=1, keepdims=True)
+        p = np.exp(sc)
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ v
+    return out
+
+
+def test_flash_attn_exact_mode_brute_force():
+    rng = np.random.default_rng(13)
+    Hq, Hkv, hd, ctx, n_kv, s, pos = 6, 2, 64, 80, 64, 5, 50
+    q = rng.standard_normal((Hq, s, hd)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, ctx, hd)))
+    vc = f16(rng.standard_normal((Hkv, ctx, hd)))
+    m = O.causal_mask_f16(pos, s, n_kv)
+    sc = 1 / np.sqrt(hd)
+    got = O.flash_attn_ext_f16(q, kc, vc, n_kv, m, sc, mode=1)
+    want = _np_attention(q, kc, vc, n_kv, m, sc)
+    assert np.abs(got - want).max() < 1e-6
+    # swapping the GQA map (h % Hkv instead of h // g) must be detected
+    kc2 = kc[::-1].copy()
+    vc2 = vc[::-1].copy()
+    bad = O.flash_attn_ext_f16(q, kc2, vc2, n_kv, m, sc, mode=1)
+    assert np.abs(bad - want).max() > 1e-2
+
+
+def test_flash_attn_padding_invariance():
+    """Masked (-32768) padded columns contribute exactly nothing."""
+    rng = np.random.default_rng(17)
+    Hq, Hkv, hd, ctx, pos = 4, 2, 64, 600, 250
+    q = rng.standard_normal((Hq, 1, hd)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, ctx, hd)))
+    vc = f16(rng.standard_normal((Hkv, ctx, hd)))
+    a = O.flash_attn_ext_f16(q, kc, vc, 256, O.causal_mask_f16(pos, 1, 256), mode=1)
+    b = O.flash_attn_ext_f16(q, kc, vc, 512, O.causal_mask_f16(pos, 1, 512), mode=1)
+    assert np.array_equal(a, b)
+    c = O.flash_attn_ext_f16(q, kc, vc, 256, O.causal_mask_f16(pos, 1, 256), mode=0)
+    d = O.flash_attn_ext_f16(q, kc, vc, 512, O.causal_mask_f16(pos, 1, 512), mode=0)
+    assert np.array_equal(c, d)
+
+
+def test_flash_attn_golden(golden_dir):
+    files = sorted(golden_dir.glob("flash_attn_*.npz"))
+    assert len(files) >= 4
+    for f in files:
+        g = np.load(f)
+        n_kv = int(g["n_kv"])
+        ref = g["out"]
+        den = np.abs(ref).max()
+        emul = O.flash_attn_ext_f16(g["q"], g["kc"], g["vc"], n_kv, g["mask"], mode=0,
+                                    n_threads=int(g["n_threads"]))
+        exact = O.flash_attn_ext_f16(g["q"], g["kc"], g["vc"], n_kv, g["mask"], mode=1)
+        # the restated reference arithmetic tracks the reference closely ...
+        assert np.abs(emul - ref).max() / den < 1e-3, f.name
+        # ... and the reference itself sits within 1e-2 of the exact softmax
+        # (fp16 V accumulator for s < 64, ops.cpp:8682-8696)
+        assert np.abs(exact - ref).max() / den < 1e-2, f.name
+
+
+# ---------------------------------------------------------------- softmax ---
+
+def test_soft_max_golden(golden_dir):
+    g = np.load(golden_dir / "soft_max_f32.npz")
+    y = O.soft_max_f32(g["x"], g["mask"], float(g["scale"]))
+    assert np.abs(y - g["y"]).max() < 1e-6
+    assert np.allclose(y.sum(axis=1), 1.0, atol=1e-5)
+
+
+# --------------------------------------------------------- executor helpers ---
+
+def test_pad_kv_len_and_mask():
+    assert O.pad_kv_len(1, 4096) == 256
+    assert O.pad_kv_len(256, 4096) == 256
+    assert O.pad_kv_len(257, 4096) == 512
+    assert O.pad_kv_len(640, 4096) == 768
+    assert O.pad_kv_len(5000, 4096) == 4096
+    assert O.pad_kv_len(300, 4096, 1) == 300
+    m = h2f(O.causal_mask_f16(3, 2, 8))
+    assert (m[0, :4] == 0).all() and (m[0, 4:] == -32768).all()
+    assert (m[1, :5] == 0).all() and (m[1, 5:] == -32768).all()
