@@ -1,0 +1,94 @@
+"""ctypes binding of libgq.so (the C ABI declared in include/gq.h).
+
+The library is loaded from this package directory. There is no fallback: if
+libgq.so is missing or cannot be loaded, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libgq.so"
+
+# enum gq_type (ggml type ids)
+F32, F16, Q4_0, Q8_0, I32, I64 = 0, 1, 2, 8, 26, 27
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+
+GQ_OK = 0
+_ERR_NAMES = {-1: "GQ_ERR_INVALID", -2: "GQ_ERR_UNSUPPORTED", -3: "GQ_ERR_WORKSPACE", -4: "GQ_ERR_DEVICE"}
+
+
+class GQError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{_ERR_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class gq_tensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("pad_", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_size_t * 4),
+    ]
+
+
+_P = ctypes.POINTER(gq_tensor)
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes); exactly the entry points of include/gq.h
+SIGNATURES = {
+    "gq_abi_version": (ctypes.c_int, []),
+    "gq_last_error": (ctypes.c_char_p, []),
+    "gq_init": (ctypes.c_int, []),
+    "gq_quantize_row_q8_0": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gq_quantize_weights": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _i64, _vp]),
+    "gq_mul_mat_workspace_size": (ctypes.c_size_t, [_P, _P]),
+    "gq_mul_mat": (ctypes.c_int, [_P, _P, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_set_rows": (ctypes.c_int, [_P, _P, _P, _vp, _vp]),
+    "gq_flash_attn_ext_workspace_size": (ctypes.c_size_t, [_P, _P]),
+    "gq_flash_attn_ext": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_soft_max": (ctypes.c_int, [_P, _P, _f32, _f32, _P, _vp]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libgq.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m ggmlc_amd.build` (or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != GQ_OK:
+        raise GQError(rc, load().gq_last_error().decode(errors="replace"))
+
+
+def make_tensor(ptr: int, gtype: int, ne, nb) -> gq_tensor:
+    t = gq_tensor()
+    t.data = ptr
+    t.type = gtype
+    ne = list(ne) + [1] * (4 - len(ne))
+    nb = list(nb)
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1])
+    for i in range(4):
+        t.ne[i] = int(ne[i])
+        t.nb[i] = int(nb[i])
+    return t

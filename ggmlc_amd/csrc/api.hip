@@ -1,0 +1,301 @@
+// extern "C" entry points of libgq.so (declared in include/gq.h): argument
+// validation against the ggml op contracts, workspace carving and dispatch to
+// the kernels. Validation failures return an error before anything is
+// launched, so a rejected call leaves all device state untouched.
+#include <cmath>
+#include <cstdio>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace gq {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string& msg) { g_err = msg; }
+
+int fail(int code, const std::string& msg) {
+    set_error(msg);
+    return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return GQ_OK;
+    return fail(GQ_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+int64_t block_bytes(int t) { return t == GQ_TYPE_Q8_0 ? Q8_BYTES : (t == GQ_TYPE_Q4_0 ? Q4_BYTES : 0); }
+
+std::string shape(const gq_tensor* t) {
+    char buf[160];
+    snprintf(buf, sizeof(buf), "type=%d ne=[%lld,%lld,%lld,%lld] nb=[%zu,%zu,%zu,%zu]", t->type,
+             (long long)t->ne[0], (long long)t->ne[1], (long long)t->ne[2], (long long)t->ne[3], t->nb[0], t->nb[1],
+             t->nb[2], t->nb[3]);
+    return buf;
+}
+
+// rows of a 4-d tensor addressed as one uniform stride (dims 1..3 collapse)
+bool rows_uniform(const gq_tensor* t) {
+    return (t->ne[2] == 1 || t->nb[2] == t->nb[1] * (size_t)t->ne[1]) &&
+           (t->ne[3] == 1 || t->nb[3] == t->nb[2] * (size_t)t->ne[2]);
+}
+
+// GEMV up to this many activation rows, MFMA GEMM above
+int gemv_max_m() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("GQ_GEMV_MAX_M");
+        v = e ? atoi(e) : GEMV_MAX_M;
+        if (v < 0) v = 0;
+        if (v > GEMV_MAX_M) v = GEMV_MAX_M;
+    }
+    return v;
+}
+
+struct MulMatPlan {
+    int64_t K, N, M, x_stride, ldd;
+    bool use_gemv;
+    size_t ws;
+};
+
+int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, MulMatPlan& p) {
+    if (!a || !b) return fail(GQ_ERR_INVALID, "mul_mat: null tensor");
+    if (a->type != GQ_TYPE_Q8_0 && a->type != GQ_TYPE_Q4_0)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat: weight type must be Q8_0 or Q4_0, got " + shape(a));
+    if (b->type != GQ_TYPE_F32) return fail(GQ_ERR_UNSUPPORTED, "mul_mat: src1 must be F32, got " + shape(b));
+    const int64_t K = a->ne[0], N = a->ne[1];
+    if (K <= 0 || K % QK != 0 || N <= 0 || a->ne[2] != 1 || a->ne[3] != 1)
+        return fail(GQ_ERR_INVALID, "mul_mat: weight must be [K % 32 == 0, N, 1, 1]: " + shape(a));
+    const int64_t bb = block_bytes(a->type);
+    if (a->nb[0] != (size_t)bb || a->nb[1] != (size_t)(K / QK * bb))
+        return fail(GQ_ERR_INVALID, "mul_mat: weight rows must be contiguous blocks: " + shape(a));
+    if (b->ne[0] != K)
+        return fail(GQ_ERR_INVALID, "mul_mat shape error: in0 " + shape(a) + " in1 " + shape(b));
+    if (b->nb[0] != 4 || b->nb[1] % 4 != 0 || !rows_uniform(b))
+        return fail(GQ_ERR_INVALID, "mul_mat: src1 rows must be contiguous and uniformly strided: " + shape(b));
+    p.K = K;
+    p.N = N;
+    p.M = b->ne[1] * b->ne[2] * b->ne[3];
+    p.x_stride = (int64_t)(b->nb[1] / 4);
+    if (dst) {
+        if (dst->type != GQ_TYPE_F32 || dst->ne[0] != N || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
+            dst->ne[3] != b->ne[3])
+            return fail(GQ_ERR_INVALID, "mul_mat: dst must be F32 [N, M, ...]: " + shape(dst));
+        if (dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
+            return fail(GQ_ERR_INVALID, "mul_mat: dst rows must be uniformly strided: " + shape(dst));
+        p.ldd = (int64_t)(dst->nb[1] / 4);
+    }
+    p.use_gemv = p.M <= gemv_max_m();
+    const size_t raw = p.use_gemv ? (size_t)p.M * act_row_bytes(K) : (size_t)p.M * K * 2;
+    p.ws = (raw + 255) & ~(size_t)255;
+    return GQ_OK;
+}
+
+}  // namespace
+}  // namespace gq
+
+using namespace gq;
+
+extern "C" {
+
+int gq_abi_version(void) { return GQ_ABI_VERSION; }
+
+const char* gq_last_error(void) { return g_err.c_str(); }
+
+int gq_init(void) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    hipDeviceProp_t prop;
+    rc = check_hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
+        return fail(GQ_ERR_UNSUPPORTED, std::string("libgq is built for gfx950, device is ") + prop.gcnArchName);
+    return GQ_OK;
+}
+
+int gq_quantize_row_q8_0(const float* x, void* y, int64_t k, gq_stream_t stream) {
+    if (k < 0 || k % QK) return fail(GQ_ERR_INVALID, "quantize_row_q8_0: k must be a multiple of 32");
+    if (k == 0) return GQ_OK;
+    if (!x || !y) return fail(GQ_ERR_INVALID, "quantize_row_q8_0: null pointer");
+    if ((reinterpret_cast<uintptr_t>(y) & 1) != 0) return fail(GQ_ERR_INVALID, "quantize_row_q8_0: y must be 2-byte aligned");
+    // one row of k elements == k/32 independent blocks
+    return quantize_q8_0_blocks(x, 1, k, k, y, (hipStream_t)stream);
+}
+
+int gq_quantize_weights(int type, const float* x, void* y, int64_t n, gq_stream_t stream) {
+    if (type != GQ_TYPE_Q8_0 && type != GQ_TYPE_Q4_0)
+        return fail(GQ_ERR_UNSUPPORTED, "quantize_weights: type must be Q8_0 or Q4_0");
+    if (n < 0 || n % QK) return fail(GQ_ERR_INVALID, "quantize_weights: n must be a multiple of 32");
+    if (n && (!x || !y)) return fail(GQ_ERR_INVALID, "quantize_weights: null pointer");
+    return quantize_weights(type, x, y, n, (hipStream_t)stream);
+}
+
+size_t gq_mul_mat_workspace_size(const gq_tensor* a, const gq_tensor* b) {
+    MulMatPlan p;
+    if (plan_mul_mat(a, b, nullptr, p) != GQ_OK) return 0;
+    return p.ws;
+}
+
+int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* workspace, size_t workspace_bytes,
+               gq_stream_t stream) {
+    MulMatPlan p;
+    if (!dst) return fail(GQ_ERR_INVALID, "mul_mat: null dst");
+    int rc = plan_mul_mat(a, b, dst, p);
+    if (rc) return rc;
+    if (p.M == 0) return GQ_OK;
+    if (!workspace || workspace_bytes < p.ws)
+        return fail(GQ_ERR_WORKSPACE, "mul_mat: workspace too small (need " + std::to_string(p.ws) + " bytes)");
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+        return fail(GQ_ERR_INVALID, "mul_mat: workspace must be 256-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
+        return fail(GQ_ERR_INVALID, "mul_mat: weight data must be 4-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    const float* x = static_cast<const float*>(b->data);
+    float* y = static_cast<float*>(dst->data);
+    const uint8_t* W = static_cast<const uint8_t*>(a->data);
+    if (p.use_gemv) {
+        const int64_t ars = act_row_bytes(p.K);
+        rc = quantize_q8_0_act(x, p.M, p.K, p.x_stride, workspace, ars, s);
+        if (rc) return rc;
+        return gemv(a->type, W, p.N, p.K, static_cast<const uint8_t*>(workspace), ars, p.M, y, p.ldd, s);
+    }
+    uint16_t* A = static_cast<uint16_t*>(workspace);
+    rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, p.K, s);
+    if (rc) return rc;
+    return gemm(a->type, W, p.N, p.K, A, p.K, p.M, y, p.ldd, s);
+}
+
+int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n_bad, gq_stream_t stream) {
+    if (!a || !b || !c) return fail(GQ_ERR_INVALID, "set_rows: null tensor");
+    if (a->type != GQ_TYPE_F16 || b->type != GQ_TYPE_F32)
+        return fail(GQ_ERR_UNSUPPORTED, "set_rows: supports F32 src into F16 dst: dst " + shape(a) + " src " + shape(b));
+    if (c->type != GQ_TYPE_I64 && c->type != GQ_TYPE_I32)
+        return fail(GQ_ERR_INVALID, "set_rows: index type must be I64 or I32");
+    // ggml.c:3944-3956
+    if (a->ne[0] != b->ne[0] || a->ne[2] != b->ne[2] || a->ne[3] != b->ne[3] || b->ne[1] != c->ne[0] ||
+        c->ne[1] <= 0 || c->ne[2] <= 0 || b->ne[2] % c->ne[1] != 0 || b->ne[3] % c->ne[2] != 0 || c->ne[3] != 1)
+        return fail(GQ_ERR_INVALID, "set_rows: shape mismatch dst " + shape(a) + " src " + shape(b) + " idx " + shape(c));
+    if (a->nb[0] != 2 || b->nb[0] != 4) return fail(GQ_ERR_INVALID, "set_rows: rows must be contiguous");
+    SetRowsArgs r;
+    r.dst = static_cast<uint16_t*>(a->data);
+    r.ne0 = a->ne[0];
+    r.ne1 = a->ne[1];
+    r.ne2 = a->ne[2];
+    r.ne3 = a->ne[3];
+    r.dnb1 = (int64_t)a->nb[1];
+    r.dnb2 = (int64_t)a->nb[2];
+    r.dnb3 = (int64_t)a->nb[3];
+    r.src = static_cast<const float*>(b->data);
+    r.s = b->ne[1];
+    r.snb1 = (int64_t)b->nb[1];
+    r.snb2 = (int64_t)b->nb[2];
+    r.snb3 = (int64_t)b->nb[3];
+    r.idx = c->data;
+    r.idx64 = c->type == GQ_TYPE_I64;
+    r.ine1 = c->ne[1];
+    r.ine2 = c->ne[2];
+    r.inb0 = (int64_t)c->nb[0];
+    r.inb1 = (int64_t)c->nb[1];
+    r.inb2 = (int64_t)c->nb[2];
+    r.n_bad = n_bad;
+    return set_rows_f32_f16(r, (hipStream_t)stream);
+}
+
+size_t gq_flash_attn_ext_workspace_size(const gq_tensor* q, const gq_tensor* k) {
+    if (!q || !k || k->ne[2] <= 0) return 0;
+    return attn_workspace_bytes(q->ne[0], q->ne[1], q->ne[2], k->ne[2], k->ne[1]);
+}
+
+int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* mask, float scale,
+                      float max_bias, float logit_softcap, gq_tensor* dst, void* workspace, size_t workspace_bytes,
+                      gq_stream_t stream) {
+    if (!q || !k || !v || !dst) return fail(GQ_ERR_INVALID, "flash_attn_ext: null tensor");
+    if (q->type != GQ_TYPE_F32 || k->type != GQ_TYPE_F16 || v->type != GQ_TYPE_F16 || dst->type != GQ_TYPE_F32)
+        return fail(GQ_ERR_UNSUPPORTED, "flash_attn_ext: needs F32 q/dst and F16 k/v");
+    const int64_t D = q->ne[0], S = q->ne[1], Hq = q->ne[2], n_kv = k->ne[1], Hkv = k->ne[2];
+    if (D != 64 && D != 128) return fail(GQ_ERR_UNSUPPORTED, "flash_attn_ext: head dim must be 64 or 128");
+    if (k->ne[0] != D || v->ne[0] != D || v->ne[1] != n_kv || v->ne[2] != Hkv || Hkv <= 0 || Hq % Hkv != 0 ||
+        q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1 || n_kv <= 0 || S <= 0)
+        return fail(GQ_ERR_INVALID, "flash_attn_ext: shape mismatch q " + shape(q) + " k " + shape(k) + " v " + shape(v));
+    if (q->nb[0] != 4 || k->nb[0] != 2 || v->nb[0] != 2 || k->nb[1] % 16 || v->nb[1] % 16 || k->nb[2] % 16 ||
+        v->nb[2] % 16 || (reinterpret_cast<uintptr_t>(k->data) & 15) || (reinterpret_cast<uintptr_t>(v->data) & 15))
+        return fail(GQ_ERR_INVALID, "flash_attn_ext: k/v rows must be 16-byte aligned");
+    if (dst->ne[0] != D || dst->ne[1] != Hq || dst->ne[2] != S || dst->nb[0] != 4 || dst->nb[1] != (size_t)D * 4 ||
+        dst->nb[2] != (size_t)D * 4 * Hq)
+        return fail(GQ_ERR_INVALID, "flash_attn_ext: dst must be contiguous F32 [D, Hq, S]: " + shape(dst));
+    if (mask) {
+        if (mask->type != GQ_TYPE_F16 || mask->ne[0] < n_kv || mask->ne[1] < S || mask->nb[0] != 2 ||
+            mask->ne[2] != 1 || mask->ne[3] != 1)
+            return fail(GQ_ERR_INVALID, "flash_attn_ext: mask must be F16 [>= n_kv, >= S, 1, 1]: " + shape(mask));
+    }
+    if (max_bias > 0.0f && !mask) return fail(GQ_ERR_INVALID, "flash_attn_ext: max_bias needs a mask");
+    AttnArgs a;
+    a.q = static_cast<const float*>(q->data);
+    a.D = D;
+    a.S = S;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.qnb1 = (int64_t)q->nb[1];
+    a.qnb2 = (int64_t)q->nb[2];
+    a.k = static_cast<const uint16_t*>(k->data);
+    a.v = static_cast<const uint16_t*>(v->data);
+    a.n_kv = n_kv;
+    a.knb1 = (int64_t)k->nb[1];
+    a.knb2 = (int64_t)k->nb[2];
+    a.vnb1 = (int64_t)v->nb[1];
+    a.vnb2 = (int64_t)v->nb[2];
+    a.mask = mask ? static_cast<const uint16_t*>(mask->data) : nullptr;
+    a.mnb1 = mask ? (int64_t)mask->nb[1] : 0;
+    a.scale = scale;
+    a.max_bias = max_bias;
+    a.softcap = logit_softcap;
+    a.dst = static_cast<float*>(dst->data);
+    return attention(a, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int gq_soft_max(const gq_tensor* a, const gq_tensor* mask, float scale, float max_bias, gq_tensor* dst,
+                gq_stream_t stream) {
+    if (!a || !dst) return fail(GQ_ERR_INVALID, "soft_max: null tensor");
+    if (a->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_F32 || a->nb[0] != 4 || dst->nb[0] != 4)
+        return fail(GQ_ERR_UNSUPPORTED, "soft_max: needs F32 with contiguous rows");
+    for (int i = 0; i < 4; ++i)
+        if (a->ne[i] != dst->ne[i]) return fail(GQ_ERR_INVALID, "soft_max: dst shape differs from src");
+    SoftmaxArgs s;
+    s.x = static_cast<const float*>(a->data);
+    s.y = static_cast<float*>(dst->data);
+    s.ncols = a->ne[0];
+    s.nrows = a->ne[1];
+    s.n2 = a->ne[2];
+    s.n3 = a->ne[3];
+    s.xnb1 = (int64_t)a->nb[1];
+    s.xnb2 = (int64_t)a->nb[2];
+    s.xnb3 = (int64_t)a->nb[3];
+    s.ynb1 = (int64_t)dst->nb[1];
+    s.ynb2 = (int64_t)dst->nb[2];
+    s.ynb3 = (int64_t)dst->nb[3];
+    s.mask = nullptr;
+    s.mask_f16 = 0;
+    s.mne2 = s.mne3 = 1;
+    s.mnb1 = s.mnb2 = s.mnb3 = 0;
+    if (mask) {
+        if ((mask->type != GQ_TYPE_F16 && mask->type != GQ_TYPE_F32) || mask->ne[0] != a->ne[0] ||
+            mask->ne[1] < a->ne[1] || a->ne[2] % mask->ne[2] || a->ne[3] % mask->ne[3])
+            return fail(GQ_ERR_INVALID, "soft_max: mask shape " + shape(mask) + " vs " + shape(a));
+        s.mask = mask->data;
+        s.mask_f16 = mask->type == GQ_TYPE_F16;
+        s.mne2 = mask->ne[2];
+        s.mne3 = mask->ne[3];
+        s.mnb1 = (int64_t)mask->nb[1];
+        s.mnb2 = (int64_t)mask->nb[2];
+        s.mnb3 = (int64_t)mask->nb[3];
+    }
+    if (max_bias > 0.0f && !mask) return fail(GQ_ERR_INVALID, "soft_max: max_bias needs a mask");
+    s.scale = scale;
+    s.max_bias = max_bias;
+    return soft_max(s, (hipStream_t)stream);
+}
+
+}  // extern "C"

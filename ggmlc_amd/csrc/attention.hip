@@ -1,0 +1,308 @@
+// FLASH_ATTN_EXT over an F16 KV cache view (decode and chunked prefill).
+//
+// Semantics: ggml_compute_forward_flash_attn_ext_f16 (ggml-cpu/ops.cpp:
+// 8532-8768 one_chunk, 8770-9058 tiled, 9060-9209 split-KV decode): per query
+// row i and head h, with kv head h / (Hq / Hkv) (GQA broadcast, rk2),
+//   s_j = scale * q . k_j (softcap: c * tanh(s / c)) + slope_h * mask[i, j]
+//   out = sum_j exp(s_j - max) v_j / sum_j exp(s_j - max),
+// written to dst[i][h][:] (the op's permute(0, 2, 1, 3)). The query is rounded
+// to fp16 for S < 64 (one_chunk converts it to the K type) and kept fp32 for
+// S >= 64 (tiled path); everything is accumulated in fp32, which is closer to
+// the exact softmax than the CPU's fp16 V accumulator (ops.cpp:8682-8696).
+//
+// Split-KV ("flash decoding"): the KV range is cut into 64-row chunks;
+// a workgroup owns (split, kv head, tile of 16 query vectors) — the query
+// vectors of one kv head are the G = Hq/Hkv heads x S rows that share it, so
+// every K/V byte is read once per tile. Each workgroup streams its chunks
+// through LDS with an online softmax; when the KV range is split across
+// workgroups, unnormalised partials (O, max, sum) go to the workspace and a
+// second kernel merges them (the reduction of ops.cpp:9060-9128).
+#include "common.h"
+#include "kernels.h"
+
+namespace gq {
+
+namespace {
+
+constexpr int CH = 64;   // kv rows per chunk
+constexpr int QT = 16;   // query vectors per tile
+constexpr int TARGET_WG = 1024;
+
+struct Plan {
+    int64_t G, NQ, n_qt, n_chunks, cps, n_split;
+};
+
+Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
+    (void)D;
+    Plan p;
+    p.G = Hq / Hkv;
+    p.NQ = p.G * S;
+    p.n_qt = cdiv(p.NQ, QT);
+    p.n_chunks = cdiv(n_kv, CH);
+    const int64_t base = Hkv * p.n_qt;
+    int64_t want = base >= TARGET_WG ? 1 : cdiv(TARGET_WG, base);
+    if (want > p.n_chunks) want = p.n_chunks;
+    if (want < 1) want = 1;
+    p.cps = cdiv(p.n_chunks, want);
+    p.n_split = cdiv(p.n_chunks, p.cps);
+    return p;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps, int n_chunks, int n_split,
+                                              float m0, float m1, uint32_t n_head_log2, int q_f16,
+                                              float* __restrict__ part) {
+    constexpr int LDV = D + 8;  // halves per LDS row
+    __shared__ __align__(16) float sQ[QT][D];
+    __shared__ __align__(16) uint16_t sK[CH * LDV];
+    __shared__ __align__(16) uint16_t sV[CH * LDV];
+    __shared__ float sS[QT][CH];
+    __shared__ float sM[QT], sL[QT], sA[QT];
+
+    const int tid = threadIdx.x;
+    const int split = blockIdx.x;
+    const int hk = blockIdx.y;
+    const int qt = blockIdx.z;
+    const int Hkv = (int)a.Hkv;
+
+    // ---- query tile -> LDS
+    for (int idx = tid; idx < QT * D; idx += 256) {
+        const int qq = idx / D, d = idx % D;
+        const int qv = qt * QT + qq;
+        float val = 0.0f;
+        if (qv < NQ) {
+            const int64_t h = (int64_t)hk * G + qv % G;
+            const int64_t i = qv / G;
+            val = *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + i * a.qnb1 +
+                                                  h * a.qnb2 + (int64_t)d * 4);
+            if (q_f16) val = (float)(_Float16)val;
+        }
+        sQ[qq][d] = val;
+    }
+    if (tid < QT) {
+        sM[tid] = -INFINITY;
+        sL[tid] = 0.0f;
+    }
+
+    // phase-3 mapping: lane owns 2 dims of QPG query vectors
+    constexpr int TPQ = D / 2;          // threads per query group
+    constexpr int NQG = 256 / TPQ;      // query groups (4 or 8)
+    constexpr int QPG = QT / NQG;       // queries per group (4 or 2)
+    const int od = (tid % TPQ) * 2;
+    const int oqg = tid / TPQ;
+    float o[QPG][2];
+#pragma unroll
+    for (int u = 0; u < QPG; ++u) o[u][0] = o[u][1] = 0.0f;
+
+    // phase-1 mapping: lane owns one kv row and 4 query vectors
+    const int sr = tid & 63;
+    const int sqg = tid >> 6;
+
+    const int c_begin = split * cps;
+    const int c_end = min(n_chunks, c_begin + cps);
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.k) + (int64_t)hk * a.knb2;
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.v) + (int64_t)hk * a.vnb2;
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int64_t c0 = (int64_t)c * CH;
+        const int rows = (int)min<int64_t>(CH, a.n_kv - c0);
+        __syncthreads();
+        // ---- K/V chunk -> LDS (16-byte pieces)
+        constexpr int PPR = D / 8;  // pieces per row
+        for (int idx = tid; idx < CH * PPR; idx += 256) {
+            const int r = idx / PPR, pc = idx % PPR;
+            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+            if (r < rows) {
+                kv = *reinterpret_cast<const uint4*>(kbase + (c0 + r) * a.knb1 + pc * 16);
+                vv = *reinterpret_cast<const uint4*>(vbase + (c0 + r) * a.vnb1 + pc * 16);
+            }
+            *reinterpret_cast<uint4*>(&sK[r * LDV + pc * 8]) = kv;
+            *reinterpret_cast<uint4*>(&sV[r * LDV + pc * 8]) = vv;
+        }
+        __syncthreads();
+        // ---- scores
+        {
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+            for (int d = 0; d < D; d += 8) {
+                const uint4 kp = *reinterpret_cast<const uint4*>(&sK[sr * LDV + d]);
+                float kf[8];
+                const uint32_t kw[4] = {kp.x, kp.y, kp.z, kp.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kf[2 * e] = h2f((uint16_t)(kw[e] & 0xffff));
+                    kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4 qa = *reinterpret_cast<const float4*>(&sQ[sqg + 4 * u][d]);
+                    const float4 qb = *reinterpret_cast<const float4*>(&sQ[sqg + 4 * u][d + 4]);
+                    acc[u] += qa.x * kf[0] + qa.y * kf[1] + qa.z * kf[2] + qa.w * kf[3] + qb.x * kf[4] +
+                              qb.y * kf[5] + qb.z * kf[6] + qb.w * kf[7];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int qq = sqg + 4 * u;
+                const int qv = qt * QT + qq;
+                float s = -INFINITY;
+                if (sr < rows && qv < NQ) {
+                    s = acc[u] * a.scale;
+                    if (a.softcap != 0.0f) s = a.softcap * tanhf(s);
+                    if (a.mask) {
+                        const int64_t h = (int64_t)hk * G + qv % G;
+                        const int64_t i = qv / G;
+                        float slope = 1.0f;
+                        if (a.max_bias > 0.0f)
+                            slope = h < n_head_log2 ? powf(m0, (float)(h + 1))
+                                                    : powf(m1, (float)(2 * (h - n_head_log2) + 1));
+                        const uint16_t mv = *reinterpret_cast<const uint16_t*>(
+                            reinterpret_cast<const uint8_t*>(a.mask) + i * a.mnb1 + (c0 + sr) * 2);
+                        const float mf = slope * h2f(mv);
+                        s = mf == -INFINITY ? -INFINITY : s + mf;
+                    }
+                }
+                sS[qq][sr] = s;
+            }
+        }
+        __syncthreads();
+        // ---- online softmax update (16 lanes per query vector)
+        {
+            const int qq = tid >> 4, sub = tid & 15;
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sv[k] = sS[qq][sub + 16 * k];
+                mx = fmaxf(mx, sv[k]);
+            }
+            mx = xor_max<16>(mx);
+            const float mold = sM[qq];
+            const float mnew = fmaxf(mold, mx);
+            float ps = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float p = mnew == -INFINITY ? 0.0f : __expf(sv[k] - mnew);
+                sS[qq][sub + 16 * k] = p;
+                ps += p;
+            }
+            ps = xor_sum<16>(ps);
+            if (sub == 0) {
+                const float alpha = mnew == -INFINITY ? 1.0f : __expf(mold - mnew);
+                sA[qq] = alpha;
+                sM[qq] = mnew;
+                sL[qq] = sL[qq] * alpha + ps;
+            }
+        }
+        __syncthreads();
+        // ---- O += P V
+        {
+#pragma unroll
+            for (int u = 0; u < QPG; ++u) {
+                const float al = sA[oqg * QPG + u];
+                o[u][0] *= al;
+                o[u][1] *= al;
+            }
+            for (int r = 0; r < rows; ++r) {
+                const uint32_t vw = *reinterpret_cast<const uint32_t*>(&sV[r * LDV + od]);
+                const float v0 = h2f((uint16_t)(vw & 0xffff)), v1 = h2f((uint16_t)(vw >> 16));
+#pragma unroll
+                for (int u = 0; u < QPG; ++u) {
+                    const float p = sS[oqg * QPG + u][r];
+                    o[u][0] += p * v0;
+                    o[u][1] += p * v1;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int u = 0; u < QPG; ++u) {
+        const int qq = oqg * QPG + u;
+        const int qv = qt * QT + qq;
+        if (qv >= NQ) continue;
+        const int64_t h = (int64_t)hk * G + qv % G;
+        const int64_t i = qv / G;
+        if (n_split == 1) {
+            const float L = sL[qq];
+            const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+            float* op = a.dst + (i * a.Hq + h) * D + od;
+            op[0] = o[u][0] * inv;
+            op[1] = o[u][1] * inv;
+        } else {
+            float* pp = part + (((int64_t)split * Hkv + hk) * NQ + qv) * (D + 2);
+            pp[2 + od] = o[u][0];
+            pp[2 + od + 1] = o[u][1];
+            if (od == 0) {
+                pp[0] = sM[qq];
+                pp[1] = sL[qq];
+            }
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part, int n_split, int Hkv, int NQ,
+                                                  int G, int64_t Hq, float* __restrict__ dst) {
+    const int qv = blockIdx.x;
+    const int hk = blockIdx.y;
+    const int d = threadIdx.x;
+    float mx = -INFINITY;
+    for (int s = 0; s < n_split; ++s)
+        mx = fmaxf(mx, part[(((int64_t)s * Hkv + hk) * NQ + qv) * (D + 2)]);
+    float L = 0.0f, acc = 0.0f;
+    for (int s = 0; s < n_split; ++s) {
+        const float* pp = part + (((int64_t)s * Hkv + hk) * NQ + qv) * (D + 2);
+        if (pp[1] == 0.0f) continue;
+        const float w = __expf(pp[0] - mx);
+        L += pp[1] * w;
+        acc += pp[2 + d] * w;
+    }
+    const int64_t h = (int64_t)hk * G + qv % G;
+    const int64_t i = qv / G;
+    dst[(i * Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
+}
+
+}  // namespace
+
+size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
+    if (Hkv <= 0 || Hq % Hkv) return 0;
+    const Plan p = make_plan(D, S, Hq, Hkv, n_kv);
+    if (p.n_split <= 1) return 0;
+    return (size_t)p.n_split * Hkv * p.NQ * (D + 2) * sizeof(float);
+}
+
+int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+    const Plan p = make_plan(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
+    const size_t need = attn_workspace_bytes(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
+    if (need > 0 && (ws == nullptr || ws_bytes < need))
+        return fail(GQ_ERR_WORKSPACE, "flash_attn_ext: workspace too small (need " + std::to_string(need) + " bytes)");
+    const uint32_t n_head = (uint32_t)a.Hq;
+    const uint32_t n_head_log2 = 1u << (uint32_t)floor(log2((double)n_head));
+    const float m0 = powf(2.0f, -(a.max_bias) / n_head_log2);
+    const float m1 = powf(2.0f, -(a.max_bias / 2.0f) / n_head_log2);
+    AttnArgs b = a;
+    if (b.softcap != 0.0f) b.scale /= b.softcap;
+    const int q_f16 = a.S < 64 ? 1 : 0;
+    const dim3 grid((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)p.n_qt);
+    float* part = reinterpret_cast<float*>(ws);
+    if (a.D == 128)
+        hipLaunchKernelGGL(k_attn<128>, grid, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, (int)p.cps, (int)p.n_chunks,
+                           (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
+    else
+        hipLaunchKernelGGL(k_attn<64>, grid, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, (int)p.cps, (int)p.n_chunks,
+                           (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
+    int rc = check_hip(hipGetLastError(), "flash_attn_ext launch");
+    if (rc != GQ_OK || p.n_split == 1) return rc;
+    const dim3 g2((unsigned)p.NQ, (unsigned)a.Hkv);
+    if (a.D == 128)
+        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ,
+                           (int)p.G, a.Hq, a.dst);
+    else
+        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ,
+                           (int)p.G, a.Hq, a.dst);
+    return check_hip(hipGetLastError(), "flash_attn_ext merge launch");
+}
+
+}  // namespace gq

@@ -1,0 +1,224 @@
+// Prefill GEMM for Q8_0 / Q4_0 weights on fp16 MFMA (gfx950 v_mfma_f32_32x32x16_f16).
+//
+// Semantics: ggml_mul_mat with src1 quantized to Q8_0 (llamafile tinyBLAS_Q0
+// path, ggml-cpu/llamafile/sgemm.cpp:3805-4113, entered at ggml-cpu.c:1366-1386)
+// computes sum_b d_w d_x isum_b. Here both operands are expanded to fp16
+// before the tensor-core product: A = fp16(d_x * q_x) is written by the
+// activation quantizer, B = fp16(d_w * q_w) is expanded tile by tile in LDS.
+// Each fp16 rounding is relative 2^-12 and independent, so the result stays
+// within ~3e-4 max-abs-rel of the exact block sum (checked against the oracle
+// at 1e-3). The alternative — int8 MFMA with an fp32 rescale of every 32x32
+// tile per 32-wide block — needs ~3 VALU ops per output per block and would
+// leave the int8 matrix cores idle most of the time.
+//
+// Tiling: 128 (tokens) x 128 (weight rows) per workgroup, K step 64 (two
+// quant blocks), 4 waves each owning a 64x64 sub-tile (2x2 MFMA 32x32 tiles).
+// Next K step's global loads are held in registers while the current step
+// runs on the matrix cores. Quant blocks are loaded with one 16-bit and
+// 8 (Q8_0) or 4 (Q4_0) dword loads whose alignment is fixed per block, and
+// expanded with v_perm (0x64xx fp16 exponent trick) + packed fp16 sub/mul.
+#include "common.h"
+#include "kernels.h"
+
+namespace gq {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;  // LDS row pitch in halves (144 B)
+
+__device__ __forceinline__ uint32_t h2_fma_bits(uint32_t pair, half2v bias, half2v d) {
+    half2v h;
+    __builtin_memcpy(&h, &pair, 4);
+    h = (h - bias) * d;
+    uint32_t r;
+    __builtin_memcpy(&r, &h, 4);
+    return r;
+}
+
+// 4 bytes (values 0..255 as unsigned) -> 4 fp16 of (byte - off) * d, as 2 dwords
+__device__ __forceinline__ void expand4(uint32_t u, half2v bias, half2v d, uint32_t& lo, uint32_t& hi) {
+    const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    lo = h2_fma_bits(p01, bias, d);
+    hi = h2_fma_bits(p23, bias, d);
+}
+
+template <int QT>
+struct BlockRegs {
+    uint32_t dw[QT == GQ_TYPE_Q8_0 ? 8 : 4];
+    uint32_t u;  // the 16-bit piece
+    bool even;   // block start is 4-byte aligned
+};
+
+template <int QT>
+__device__ __forceinline__ void load_block(const uint8_t* p, bool valid, BlockRegs<QT>& r) {
+    constexpr int NW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
+    constexpr int TAIL = QT == GQ_TYPE_Q8_0 ? 32 : 16;
+    if (!valid) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) r.dw[i] = 0;
+        r.u = 0;
+        r.even = false;
+        return;
+    }
+    r.even = (reinterpret_cast<uintptr_t>(p) & 3) == 0;
+    const uint32_t* dp = reinterpret_cast<const uint32_t*>(r.even ? p : p + 2);
+    const uint16_t* up = reinterpret_cast<const uint16_t*>(r.even ? p + TAIL : p);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) r.dw[i] = dp[i];
+    r.u = *up;
+}
+
+// expand one quant block into 32 fp16 (16 dwords)
+template <int QT>
+__device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* out) {
+    constexpr int NW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
+    uint32_t q[NW];
+    uint32_t hdr;
+    if (r.even) {
+        hdr = r.dw[0] & 0xffffu;
+#pragma unroll
+        for (int i = 0; i < NW - 1; ++i) q[i] = __builtin_amdgcn_alignbyte(r.dw[i + 1], r.dw[i], 2);
+        q[NW - 1] = (r.dw[NW - 1] >> 16) | (r.u << 16);
+    } else {
+        hdr = r.u;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) q[i] = r.dw[i];
+    }
+    _Float16 dh;
+    const uint16_t hb = (uint16_t)hdr;
+    __builtin_memcpy(&dh, &hb, 2);
+    const half2v d = {dh, dh};
+    if (QT == GQ_TYPE_Q8_0) {
+        const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
+#pragma unroll
+        for (int i = 0; i < 8; ++i) expand4(q[i] ^ 0x80808080u, bias, d, out[2 * i], out[2 * i + 1]);
+    } else {
+        const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            expand4(q[i] & 0x0f0f0f0fu, bias, d, out[2 * i], out[2 * i + 1]);
+            expand4((q[i] >> 4) & 0x0f0f0f0fu, bias, d, out[8 + 2 * i], out[8 + 2 * i + 1]);
+        }
+    }
+}
+
+template <int QT>
+__global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, int64_t N, int64_t K,
+                                                 int64_t row_bytes, const uint16_t* __restrict__ A,
+                                                 int64_t lda, int64_t M, float* __restrict__ dst,
+                                                 int64_t ldd) {
+    constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
+    __shared__ __align__(16) uint16_t sA[BM * LDK];
+    __shared__ __align__(16) uint16_t sB[BN * LDK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t n0 = (int64_t)blockIdx.x * BN;
+    const int64_t m0 = (int64_t)blockIdx.y * BM;
+    const int nb = (int)(K / QK);
+    const int nk = (int)cdiv(K, BK);
+
+    // loader mapping: thread -> (row = tid / 2, half = tid % 2)
+    const int lrow = tid >> 1;
+    const int lhalf = tid & 1;
+    const int64_t am = m0 + lrow;
+    const int64_t bn = n0 + lrow;
+
+    uint4 ra[4];
+    BlockRegs<QT> rb;
+
+    auto load = [&](int kt) {
+        const int64_t k = (int64_t)kt * BK + lhalf * 32;
+        const bool av = am < M && k < K;
+        const uint4* ap = reinterpret_cast<const uint4*>(A + am * lda + k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = av ? ap[i] : make_uint4(0, 0, 0, 0);
+        const int kb = kt * 2 + lhalf;
+        const bool bv = bn < N && kb < nb;
+        load_block<QT>(W + bn * row_bytes + (int64_t)kb * BB, bv, rb);
+    };
+
+    float16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    load(0);
+    for (int kt = 0; kt < nk; ++kt) {
+        __syncthreads();
+        {
+            uint4* sa = reinterpret_cast<uint4*>(sA + lrow * LDK + lhalf * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sa[i] = ra[i];
+            uint32_t e[16];
+            expand_block<QT>(rb, e);
+            uint4* sb = reinterpret_cast<uint4*>(sB + lrow * LDK + lhalf * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sb[i] = make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3]);
+        }
+        __syncthreads();
+        if (kt + 1 < nk) load(kt + 1);
+#pragma unroll
+        for (int k16 = 0; k16 < BK / 16; ++k16) {
+            half8 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint16_t* pa = sA + (wm * 64 + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
+                a[i] = *reinterpret_cast<const half8*>(pa);
+                const uint16_t* pb = sB + (wn * 64 + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
+                b[i] = *reinterpret_cast<const half8*>(pb);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // D[i][j]: lane holds column j = lane % 32, rows i = 8*(r/4) + 4*(lane/32) + r%4
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < M) dst[m * ldd + n] = acc[i][j][r];
+            }
+        }
+}
+
+template <int QT>
+int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M, float* dst,
+           int64_t ldd, hipStream_t s) {
+    const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
+    const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM));
+    hipLaunchKernelGGL(k_gemm<QT>, grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst, ldd);
+    return check_hip(hipGetLastError(), "gemm launch");
+}
+
+}  // namespace
+
+int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
+         float* dst, int64_t ldd, hipStream_t s) {
+    if ((reinterpret_cast<uintptr_t>(W) & 3) != 0) return fail(GQ_ERR_INVALID, "gemm: weight not 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0)
+        return fail(GQ_ERR_INVALID, "gemm: activation tile misaligned");
+    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, s);
+    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, M, dst, ldd, s);
+}
+
+}  // namespace gq

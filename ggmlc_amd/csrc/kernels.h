@@ -1,0 +1,72 @@
+// Internal launchers (host side) implemented by the .hip files of libgq.
+#pragma once
+
+#include "common.h"
+
+namespace gq {
+
+// quantize.hip
+int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
+                         hipStream_t s);
+int quantize_q8_0_act(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* act,
+                      int64_t act_stride_bytes, hipStream_t s);
+int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
+                      int64_t y_stride_elems, hipStream_t s);
+int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s);
+
+// gemv.hip — dst[m * ldd + n] for m < M (M <= GEMV_MAX_M), act in the ACT_GS layout
+constexpr int GEMV_MAX_M = 4;
+int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t act_stride,
+         int64_t M, float* dst, int64_t ldd, hipStream_t s);
+
+// gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k], A fp16
+int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda,
+         int64_t M, float* dst, int64_t ldd, hipStream_t s);
+
+// set_rows.hip
+struct SetRowsArgs {
+    uint16_t* dst;
+    int64_t ne0, ne1, ne2, ne3;   // dst shape
+    int64_t dnb1, dnb2, dnb3;     // dst byte strides
+    const float* src;
+    int64_t s;                    // src rows (ne1 of src)
+    int64_t snb1, snb2, snb3;     // src byte strides
+    const void* idx;
+    int idx64;
+    int64_t ine1, ine2;           // idx broadcast extents
+    int64_t inb0, inb1, inb2;     // idx byte strides
+    int32_t* n_bad;
+};
+int set_rows_f32_f16(const SetRowsArgs& a, hipStream_t s);
+
+// attention.hip
+struct AttnArgs {
+    const float* q;
+    int64_t D, S, Hq, Hkv;
+    int64_t qnb1, qnb2;           // bytes
+    const uint16_t* k;
+    const uint16_t* v;
+    int64_t n_kv;
+    int64_t knb1, knb2, vnb1, vnb2;  // bytes
+    const uint16_t* mask;          // may be null
+    int64_t mnb1;                  // bytes
+    float scale, max_bias, softcap;
+    float* dst;                    // [S][Hq][D]
+};
+size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv);
+int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
+
+// softmax.hip
+struct SoftmaxArgs {
+    const float* x;
+    float* y;
+    int64_t ncols, nrows, n2, n3;
+    int64_t xnb1, xnb2, xnb3, ynb1, ynb2, ynb3;  // bytes
+    const void* mask;
+    int mask_f16;
+    int64_t mne2, mne3, mnb1, mnb2, mnb3;        // bytes
+    float scale, max_bias;
+};
+int soft_max(const SoftmaxArgs& a, hipStream_t s);
+
+}  // namespace gq

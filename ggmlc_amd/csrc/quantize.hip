@@ -1,0 +1,221 @@
+// Activation and weight quantizers.
+//
+// Activation: the rule of ggml's x86 quantize_row_q8_0
+// (third_party/ggml/src/ggml-cpu/arch/x86/quants.c:302-398), which the CPU
+// backend applies to MUL_MAT's src1 (ggml-cpu/ggml-cpu.c:1322-1357):
+//   amax = max|x|, d = fp16_rne(amax / 127), id = amax ? 127 / amax : 0,
+//   q = saturate_int8(round_half_even(x * id)).
+// Four lanes own one 32-element block (8 elements each, two 16-byte loads);
+// amax and the block sum of q are exchanged with two xor shuffles.
+//
+// Weights: ggmlc's compile-time quantizers (python/ggmlc/quantization/
+// quantize.py:10-47 Q8_0, :65-107 Q4_0) with numpy float32 semantics, one
+// lane per block. They only build device-resident weights for tests/benches.
+#include "common.h"
+#include "kernels.h"
+
+// x * id and x / scale must round once each, exactly as the CPU code does.
+#pragma clang fp contract(off)
+
+namespace gq {
+
+enum ActOut { OUT_BLOCKS = 0, OUT_ACT = 1, OUT_F16 = 2 };
+
+template <int MODE, bool VEC>
+__global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ x, int64_t nrows,
+                                                      int64_t K, int64_t x_stride,
+                                                      uint8_t* __restrict__ y, int64_t y_stride) {
+    const int64_t nb = K / QK;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t blk = gid >> 2;
+    const int part = (int)(gid & 3);
+    const bool valid = blk < nrows * nb;
+    const int64_t m = valid ? blk / nb : 0;
+    const int64_t b = valid ? blk - m * nb : 0;
+
+    float v[8];
+    if (valid) {
+        const float* src = x + m * x_stride + b * QK + part * 8;
+        if (VEC) {
+            const float4 a0 = *reinterpret_cast<const float4*>(src);
+            const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
+            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = src[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+
+    const float d = div_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? div_rn(127.0f, amax) : 0.0f;
+    int q[8];
+    int qsum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float r = __builtin_rintf(v[i] * id);
+        int iv = (int)r;
+        iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+        q[i] = iv;
+        qsum += iv;
+    }
+    if (MODE == OUT_ACT) {
+        qsum += __shfl_xor(qsum, 1, 64);
+        qsum += __shfl_xor(qsum, 2, 64);
+    }
+    if (!valid) return;
+
+    const uint16_t dh = f2h(d);
+    if (MODE == OUT_BLOCKS) {
+        uint8_t* blkp = y + (m * nb + b) * Q8_BYTES;
+        if (part == 0) *reinterpret_cast<uint16_t*>(blkp) = dh;
+        uint16_t* qp = reinterpret_cast<uint16_t*>(blkp + 2 + part * 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            qp[i] = (uint16_t)((q[2 * i] & 0xff) | ((q[2 * i + 1] & 0xff) << 8));
+    } else if (MODE == OUT_ACT) {
+        uint8_t* row = y + m * y_stride;
+        const int64_t g = b >> 3, bi = b & 7;
+        uint8_t* gp = row + g * ACT_GS;
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
+            hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+        }
+        *reinterpret_cast<uint2*>(gp + ACT_QS_OFF + bi * QK + part * 8) = make_uint2(lo, hi);
+        if (part == 0) {
+            reinterpret_cast<float*>(gp + ACT_D_OFF)[bi] = h2f(dh);
+            reinterpret_cast<int*>(gp + ACT_S_OFF)[bi] = qsum;
+        }
+    } else {  // OUT_F16: fp16(d * q), the GEMM's A operand
+        const float df = h2f(dh);
+        uint16_t hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hv[i] = f2h((float)q[i] * df);
+        uint4 pk;
+        pk.x = hv[0] | ((uint32_t)hv[1] << 16);
+        pk.y = hv[2] | ((uint32_t)hv[3] << 16);
+        pk.z = hv[4] | ((uint32_t)hv[5] << 16);
+        pk.w = hv[6] | ((uint32_t)hv[7] << 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + m * y_stride + b * QK + part * 8) = pk;
+    }
+}
+
+template <int MODE>
+static int launch_quant(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
+                        int64_t y_stride, hipStream_t s) {
+    const int64_t threads = nrows * (K / QK) * 4;
+    if (threads == 0) return GQ_OK;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (x_stride % 4 == 0);
+    const dim3 grid((unsigned)cdiv(threads, 256));
+    if (vec)
+        hipLaunchKernelGGL((k_quantize_act<MODE, true>), grid, dim3(256), 0, s, x, nrows, K, x_stride,
+                           (uint8_t*)y, y_stride);
+    else
+        hipLaunchKernelGGL((k_quantize_act<MODE, false>), grid, dim3(256), 0, s, x, nrows, K, x_stride,
+                           (uint8_t*)y, y_stride);
+    return check_hip(hipGetLastError(), "quantize launch");
+}
+
+int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
+                         hipStream_t s) {
+    return launch_quant<OUT_BLOCKS>(x, nrows, K, x_stride, y, 0, s);
+}
+
+int quantize_q8_0_act(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* act,
+                      int64_t act_stride_bytes, hipStream_t s) {
+    return launch_quant<OUT_ACT>(x, nrows, K, x_stride, act, act_stride_bytes, s);
+}
+
+int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
+                      int64_t y_stride_elems, hipStream_t s) {
+    return launch_quant<OUT_F16>(x, nrows, K, x_stride, y, y_stride_elems, s);
+}
+
+// ---- weight quantizers (quantize.py semantics) ------------------------------
+
+__global__ __launch_bounds__(256) void k_quant_w_q8_0(const float* __restrict__ x, uint8_t* __restrict__ y,
+                                                      int64_t nblocks) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const float* xb = x + b * QK;
+    float v[QK];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QK; ++j) {
+        v[j] = xb[j];
+        amax = fmaxf(amax, fabsf(v[j]));
+    }
+    const float scale = amax > 0.0f ? div_rn(amax, 127.0f) : 0.0f;
+    const float inv = div_rn(1.0f, scale != 0.0f ? scale : 1.0f);
+    uint8_t* o = y + b * Q8_BYTES;
+    const uint16_t dh = f2h(scale);
+    o[0] = (uint8_t)(dh & 0xff);
+    o[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+    for (int j = 0; j < QK; ++j) {
+        float r = __builtin_rintf(v[j] * inv);
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        o[2 + j] = (uint8_t)(int8_t)(int)r;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_quant_w_q4_0(const float* __restrict__ x, uint8_t* __restrict__ y,
+                                                      int64_t nblocks) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const float* xb = x + b * QK;
+    float v[QK];
+    float amax = -1.0f;
+    float smax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QK; ++j) {
+        v[j] = xb[j];
+        const float a = fabsf(v[j]);
+        if (a > amax) {  // first index of the largest magnitude (np.argmax)
+            amax = a;
+            smax = v[j];
+        }
+    }
+    const float scale = smax != 0.0f ? smax / -8.0f : 0.0f;
+    const float safe = scale != 0.0f ? scale : 1.0f;
+    uint8_t q[QK];
+#pragma unroll
+    for (int j = 0; j < QK; ++j) {
+        if (scale == 0.0f) {
+            q[j] = 8;
+        } else {
+            float r = __builtin_rintf(div_rn(v[j], safe)) + 8.0f;
+            r = fminf(fmaxf(r, 0.0f), 15.0f);
+            q[j] = (uint8_t)(int)r;
+        }
+    }
+    uint8_t* o = y + b * Q4_BYTES;
+    const uint16_t dh = f2h(scale);
+    o[0] = (uint8_t)(dh & 0xff);
+    o[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+    for (int j = 0; j < QK / 2; ++j) o[2 + j] = (uint8_t)((q[j] & 0x0f) | ((q[j + 16] & 0x0f) << 4));
+}
+
+int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s) {
+    const int64_t nb = n / QK;
+    if (nb == 0) return GQ_OK;
+    const dim3 grid((unsigned)cdiv(nb, 256));
+    if (type == GQ_TYPE_Q8_0)
+        hipLaunchKernelGGL(k_quant_w_q8_0, grid, dim3(256), 0, s, x, (uint8_t*)y, nb);
+    else
+        hipLaunchKernelGGL(k_quant_w_q4_0, grid, dim3(256), 0, s, x, (uint8_t*)y, nb);
+    return check_hip(hipGetLastError(), "quantize_weights launch");
+}
+
+}  // namespace gq

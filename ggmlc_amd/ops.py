@@ -1,0 +1,179 @@
+"""Device ops on torch tensors, each one call into libgq.so.
+
+These mirror the ggml operators ggmlc's executor emits on the quantized path
+(runtime/src/executor.cpp:2091-2447) with the same argument meaning:
+
+* ``quantize_row_q8_0(x)``           — ggml x86 ``quantize_row_q8_0`` (bit-exact)
+* ``mul_mat(w, x)``                  — ``ggml_mul_mat(W[Q8_0|Q4_0], X[f32])``
+* ``set_rows(cache, src, idx)``      — ``ggml_set_rows`` F32 -> F16 (in place)
+* ``flash_attn_ext(q, k, v, mask, scale)`` — ``ggml_flash_attn_ext`` over F16 K/V
+* ``soft_max_ext(x, mask, scale, max_bias)`` — ``ggml_soft_max_ext``
+
+Layout convention: a torch tensor of shape ``[d3, d2, d1, d0]`` is the ggml
+tensor ``ne = [d0, d1, d2, d3]`` (ggml's innermost dimension is torch's last).
+A quantized weight is a ``QWeight``: uint8 bytes ``[N, K/32 * block_bytes]``
+exactly as stored in a .gguf, plus its type and K.
+
+Work runs on torch's current HIP stream. Nothing here computes on the CPU; if
+libgq.so is not built every call raises.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import BLOCK_BYTES, F16, F32, I32, I64, Q4_0, Q8_0, check, make_tensor
+
+__all__ = [
+    "QWeight", "Q8_0", "Q4_0", "quantize_row_q8_0", "quantize_weights", "mul_mat",
+    "set_rows", "flash_attn_ext", "soft_max_ext", "Workspace",
+]
+
+_TORCH_TO_GQ = {torch.float32: F32, torch.float16: F16, torch.int64: I64, torch.int32: I32}
+
+
+@dataclass
+class QWeight:
+    """A block-quantized weight: N rows of K elements (ggml ne = [K, N])."""
+
+    data: torch.Tensor  # uint8 [N, K/32 * block_bytes], contiguous, on device
+    qtype: int
+    K: int
+
+    @property
+    def N(self) -> int:
+        return self.data.shape[0]
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+    def desc(self):
+        bb = BLOCK_BYTES[self.qtype]
+        return make_tensor(self.data.data_ptr(), self.qtype, [self.K, self.N], [bb, self.K // 32 * bb])
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _desc(t: torch.Tensor, gtype: int | None = None):
+    """ggml descriptor of a (up to 4-d) torch tensor, strides in bytes."""
+    if gtype is None:
+        gtype = _TORCH_TO_GQ[t.dtype]
+    es = t.element_size()
+    shape = list(t.shape)[::-1]
+    strides = [s * es for s in list(t.stride())[::-1]]
+    if len(shape) > 4:
+        raise ValueError("at most 4 dimensions")
+    while len(shape) < 4:
+        strides.append(strides[-1] * shape[-1] if shape else es)
+        shape.append(1)
+    return make_tensor(t.data_ptr(), gtype, shape, strides)
+
+
+class Workspace:
+    """Grow-only device scratch buffer (256-byte aligned) shared by calls on one stream."""
+
+    def __init__(self, device=None):
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes: int) -> tuple[int, int]:
+        if nbytes == 0:
+            return 0, 0
+        if self.buf is None or self.buf.numel() < nbytes:
+            dev = self.device or torch.device("cuda", torch.cuda.current_device())
+            self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        return self.buf.data_ptr(), self.buf.numel()
+
+
+_default_ws: dict[int, Workspace] = {}
+
+
+def _ws(ws: Workspace | None) -> Workspace:
+    if ws is not None:
+        return ws
+    dev = torch.cuda.current_device()
+    if dev not in _default_ws:
+        _default_ws[dev] = Workspace(torch.device("cuda", dev))
+    return _default_ws[dev]
+
+
+def quantize_row_q8_0(x: torch.Tensor) -> torch.Tensor:
+    """x: fp32 contiguous, numel % 32 == 0 -> uint8 [..., K/32*34] block_q8_0 bytes."""
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("quantize_row_q8_0: x must be contiguous float32")
+    K = x.shape[-1]
+    out = torch.empty(x.shape[:-1] + (K // 32 * 34,), dtype=torch.uint8, device=x.device)
+    L = _lib.load()
+    check(L.gq_quantize_row_q8_0(x.data_ptr(), out.data_ptr(), x.numel(), _stream()))
+    return out
+
+
+def quantize_weights(w: torch.Tensor, qtype: int) -> QWeight:
+    """ggmlc's compile-time quantizer (quantize.py) on device: w fp32 [N, K] -> QWeight."""
+    if w.dtype != torch.float32 or not w.is_contiguous() or w.dim() != 2:
+        raise ValueError("quantize_weights: w must be a contiguous float32 [N, K]")
+    N, K = w.shape
+    out = torch.empty((N, K // 32 * BLOCK_BYTES[qtype]), dtype=torch.uint8, device=w.device)
+    check(_lib.load().gq_quantize_weights(qtype, w.data_ptr(), out.data_ptr(), w.numel(), _stream()))
+    return QWeight(out, qtype, K)
+
+
+def mul_mat(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None,
+            ws: Workspace | None = None) -> torch.Tensor:
+    """ggml_mul_mat(W, X): x fp32 [..., K] -> fp32 [..., N]."""
+    if x.dtype != torch.float32:
+        raise ValueError("mul_mat: x must be float32")
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (w.N,), dtype=torch.float32, device=x.device)
+    L = _lib.load()
+    a, b, d = w.desc(), _desc(x), _desc(out)
+    need = L.gq_mul_mat_workspace_size(a, b)
+    ptr, size = _ws(ws).get(need)
+    check(L.gq_mul_mat(a, b, d, ptr, size, _stream()))
+    return out
+
+
+def set_rows(cache: torch.Tensor, src: torch.Tensor, idx: torch.Tensor,
+             n_bad: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_set_rows(cache, src, idx) in place.
+
+    cache fp16 ``[B, H, rows, hd]`` (ggml [hd, rows, H, B]); src fp32 ``[B, H, s, hd]``;
+    idx int64/int32 ``[s]`` (or broadcast ``[ne_c2, ne_c1, s]``)."""
+    L = _lib.load()
+    nb_ptr = n_bad.data_ptr() if n_bad is not None else None
+    check(L.gq_set_rows(_desc(cache), _desc(src), _desc(idx), nb_ptr, _stream()))
+    return cache
+
+
+def flash_attn_ext(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torch.Tensor | None,
+                   scale: float, max_bias: float = 0.0, logit_softcap: float = 0.0,
+                   out: torch.Tensor | None = None, ws: Workspace | None = None) -> torch.Tensor:
+    """ggml_flash_attn_ext. q fp32 ``[Hq, S, D]``; k/v fp16 ``[Hkv, n_kv, D]`` (views of a
+    cache are fine); mask fp16 ``[S, n_kv]`` or None. Returns fp32 ``[S, Hq, D]``."""
+    Hq, S, D = q.shape
+    if out is None:
+        out = torch.empty((S, Hq, D), dtype=torch.float32, device=q.device)
+    L = _lib.load()
+    qd, kd, vd, od = _desc(q), _desc(k), _desc(v), _desc(out)
+    md = _desc(mask) if mask is not None else None
+    need = L.gq_flash_attn_ext_workspace_size(qd, kd)
+    ptr, size = _ws(ws).get(need)
+    check(L.gq_flash_attn_ext(qd, kd, vd, md, scale, max_bias, logit_softcap, od, ptr, size, _stream()))
+    return out
+
+
+def soft_max_ext(x: torch.Tensor, mask: torch.Tensor | None = None, scale: float = 1.0,
+                 max_bias: float = 0.0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_soft_max_ext over the last dim of x (fp32, up to 4-d)."""
+    if out is None:
+        out = torch.empty_like(x)
+    L = _lib.load()
+    md = _desc(mask) if mask is not None else None
+    check(L.gq_soft_max(_desc(x), md, scale, max_bias, _desc(out), _stream()))
+    return out

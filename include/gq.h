@@ -1,0 +1,150 @@
+/*
+ * gq.h — C ABI of libgq.so, the MI355X (gfx950) implementation of ggmlc's
+ * quantized execution hot path.
+ *
+ * Drop-in boundary: each entry point replaces one ggml operator that ggmlc's
+ * executor emits on this path (reference citations on each declaration; paths
+ * are relative to the reference checkout). Tensors cross the boundary as
+ * gq_tensor, a plain descriptor with the same meaning as ggml_tensor's
+ * data/type/ne/nb fields (third_party/ggml/include/ggml.h: ne = elements per
+ * dimension, innermost first; nb = byte strides). Pointers are device pointers
+ * owned by the caller; every call is asynchronous on the given HIP stream
+ * (NULL = default stream); no call allocates device memory — scratch space is
+ * passed in as a workspace whose size the matching *_workspace_size function
+ * returns.
+ *
+ * Errors: every function returns GQ_OK (0) or a negative GQ_ERR_* code, and
+ * gq_last_error() returns a thread-local message for the last failure. A
+ * rejected call launches nothing, so the caller's state is untouched and the
+ * library stays usable (the reference's contract, runtime/src/executor.cpp
+ * :2411-2428 and tests/runtime/test_executor_cpu.cpp:106-119).
+ */
+#ifndef GQ_H
+#define GQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GQ_ABI_VERSION 1
+
+/* ggml type ids (third_party/ggml/include/ggml.h enum ggml_type; ggmlc
+ * python/ggmlc/dialect/ggml/ops.py:39-108) */
+enum gq_type {
+    GQ_TYPE_F32 = 0,
+    GQ_TYPE_F16 = 1,
+    GQ_TYPE_Q4_0 = 2,
+    GQ_TYPE_Q8_0 = 8,
+    GQ_TYPE_I32 = 26,
+    GQ_TYPE_I64 = 27,
+};
+
+enum gq_status {
+    GQ_OK = 0,
+    GQ_ERR_INVALID = -1,     /* bad shape / stride / type combination */
+    GQ_ERR_UNSUPPORTED = -2, /* valid ggml call this build does not implement */
+    GQ_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+    GQ_ERR_DEVICE = -4,      /* HIP runtime error (message has the HIP error string) */
+};
+
+/* opaque HIP stream (binary-compatible with hipStream_t) */
+typedef struct ihipStream_t* gq_stream_t;
+
+/* ggml_tensor's addressing fields. Shapes beyond the op's rank use ne = 1. */
+typedef struct gq_tensor {
+    void* data;
+    int32_t type; /* enum gq_type */
+    int32_t pad_;
+    int64_t ne[4];
+    size_t nb[4];
+} gq_tensor;
+
+/* ---- library ----------------------------------------------------------- */
+
+int gq_abi_version(void);
+const char* gq_last_error(void);
+/* Checks that a gfx950 device is current and loads the kernels. */
+int gq_init(void);
+
+/* ---- quantize_row_q8_0 -------------------------------------------------- */
+
+/* Replaces the x86 runtime quantizer the CPU backend runs on MUL_MAT's src1:
+ * third_party/ggml/src/ggml-cpu/arch/x86/quants.c:302-398, reached through the
+ * Q8_0 from_float trait (ggml-cpu/ggml-cpu.c:271-279) at ggml-cpu.c:1322-1357.
+ * Same signature plus a stream: k floats (k % 32 == 0) -> k/32 block_q8_0.
+ * Bit-exact: amax = max|x|; d = fp16_rne(amax/127); id = 127/amax (0 if amax
+ * == 0); q = sat_int8(rne(x*id)). */
+int gq_quantize_row_q8_0(const float* x, void* y, int64_t k, gq_stream_t stream);
+
+/* Weight quantizers with ggmlc's compile-time semantics
+ * (python/ggmlc/quantization/quantize.py:10-47 Q8_0, :65-107 Q4_0): n floats
+ * (n % 32 == 0) -> n/32 blocks of `type` (GQ_TYPE_Q8_0 or GQ_TYPE_Q4_0). Used to
+ * build device-resident weights with the exact bytes a .gguf would hold. */
+int gq_quantize_weights(int type, const float* x, void* y, int64_t n, gq_stream_t stream);
+
+/* ---- MUL_MAT ------------------------------------------------------------ */
+
+/* Replaces ggml_mul_mat(a, b) (third_party/ggml/src/ggml.c:3278) as emitted by
+ * the executor's MUL_MAT case (runtime/src/executor.cpp:2362-2447) for a
+ * Q8_0/Q4_0 weight, computed as the CPU backend does
+ * (ggml-cpu/ggml-cpu.c:1254-1452): src1 rows are quantized to Q8_0 with the
+ * rule of gq_quantize_row_q8_0, then
+ *     dst[n, m] = sum_b d_a[n,b] * d_x[m,b] * sum_{j<32} qa[n,b,j] * qx[m,b,j].
+ *   a   : weight, type Q8_0 or Q4_0, ne = [K, N, 1, 1], contiguous
+ *   b   : activation, F32, ne = [K, M, B2, B3], nb[0] = 4, rows contiguous
+ *   dst : F32, ne = [N, M, B2, B3], nb[0] = 4
+ * Small M runs an HBM-streaming GEMV over the native 34/18-byte blocks; large M
+ * an LDS-tiled MFMA GEMM. Result: within 1e-3 max-abs-rel of the reference. */
+size_t gq_mul_mat_workspace_size(const gq_tensor* a, const gq_tensor* b);
+int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* workspace,
+               size_t workspace_bytes, gq_stream_t stream);
+
+/* ---- SET_ROWS ----------------------------------------------------------- */
+
+/* Replaces ggml_set_rows(a, b, c) (ggml.c:3937-3962) with the CPU semantics of
+ * ggml-cpu/ops.cpp:5156-5259 for an F16 destination and F32 source — the KV
+ * cache write of runtime/src/executor.cpp:2181-2184:
+ *     a[:, c[i, i2 % ne_c1, i3 % ne_c2], i2, i3] = fp16_rne(b[:, i, i2, i3])
+ *   a : F16 cache ne = [hd, rows, H, B] (rows contiguous: nb[0] = 2); updated in place
+ *   b : F32 ne = [hd, s, H, B], nb[0] = 4
+ *   c : I64 (or I32) row indices ne = [s, ne_c1, ne_c2, 1]
+ * Bit-exact. Indices outside [0, rows) are skipped and counted in *n_bad when
+ * n_bad (a device int32) is non-NULL (the reference aborts on them). */
+int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n_bad,
+                gq_stream_t stream);
+
+/* ---- FLASH_ATTN_EXT ----------------------------------------------------- */
+
+/* Replaces ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap)
+ * (ggml.c:5402-5437) as the executor emits it over the padded KV view
+ * (runtime/src/executor.cpp:2143-2197): computes for each query row i and head h
+ *     out[:, h, i] = softmax_j(scale * q[:, i, h] . k[:, j, h / (Hq/Hkv)] + mask[j, i]) v[:, j, ...]
+ *   q    : F32 ne = [D, S, Hq, 1]
+ *   k, v : F16 ne = [D, n_kv, Hkv, 1] (any row/head strides, nb[0] = 2)
+ *   mask : F16 ne = [n_kv, >= S, 1, 1] or NULL
+ *   dst  : F32 ne = [D, Hq, S, 1] contiguous (the op's permuted output)
+ * D in {64, 128}. max_bias and logit_softcap follow ops.cpp:8532-8768. Query
+ * rounding follows the CPU path taken for that S (fp16 for S < 64, fp32 for
+ * S >= 64); accumulation is fp32. */
+size_t gq_flash_attn_ext_workspace_size(const gq_tensor* q, const gq_tensor* k);
+int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v,
+                      const gq_tensor* mask, float scale, float max_bias, float logit_softcap,
+                      gq_tensor* dst, void* workspace, size_t workspace_bytes,
+                      gq_stream_t stream);
+
+/* ---- SOFT_MAX ----------------------------------------------------------- */
+
+/* Replaces ggml_soft_max_ext(a, mask, scale, max_bias) (ggml.c:4081-4105;
+ * CPU ops.cpp:5519-5629): dst = softmax(a*scale + slope*mask) per row.
+ *   a, dst : F32 ne = [ncols, nrows, n2, n3], rows contiguous
+ *   mask   : F16 or F32 ne = [ncols, >= nrows, ...] (broadcast over dims 2,3) or NULL */
+int gq_soft_max(const gq_tensor* a, const gq_tensor* mask, float scale, float max_bias,
+                gq_tensor* dst, gq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GQ_H */

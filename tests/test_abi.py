@@ -1,0 +1,88 @@
+"""The C ABI library loads, exports every entry point of include/gq.h, and rejects
+bad calls on the host before touching a device. CPU only: nothing here launches
+a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ggmlc_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "gq.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gq_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libgq.so not built (python -m ggmlc_amd.build)")
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(lib, n), n
+    # the Python binding covers exactly the header's entry points
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_abi_version_and_struct_layout(lib):
+    assert lib.gq_abi_version() == 1
+    # gq_tensor: void* + 2 x int32 + 4 x int64 + 4 x size_t
+    assert ctypes.sizeof(_lib.gq_tensor) == 8 + 8 + 32 + 32
+
+
+def _t(gtype, ne, nb):
+    return _lib.make_tensor(0x1000, gtype, ne, nb)
+
+
+def test_mul_mat_rejects_bad_shapes_without_device(lib):
+    w = _t(_lib.Q8_0, [4096, 64], [34, 4352])
+    x_bad = _t(_lib.F32, [4000, 1], [4, 16000])
+    d = _t(_lib.F32, [64, 1], [4, 256])
+    rc = lib.gq_mul_mat(w, x_bad, d, None, 0, None)
+    assert rc == -1
+    assert b"shape" in lib.gq_last_error()
+    w_f32 = _t(_lib.F32, [4096, 64], [4, 16384])
+    x = _t(_lib.F32, [4096, 1], [4, 16384])
+    assert lib.gq_mul_mat(w_f32, x, d, None, 0, None) == -2
+    # workspace too small is reported before any launch
+    assert lib.gq_mul_mat_workspace_size(w, x) > 0
+    assert lib.gq_mul_mat(w, x, d, None, 0, None) == -3
+    # K not a multiple of 32
+    w33 = _t(_lib.Q8_0, [33, 4], [34, 34])
+    assert lib.gq_mul_mat(w33, _t(_lib.F32, [33, 1], [4, 132]), _t(_lib.F32, [4, 1], [4, 16]), None, 0, None) == -1
+
+
+def test_other_entry_points_validate_on_host(lib):
+    assert lib.gq_quantize_row_q8_0(None, None, 33, None) == -1
+    assert lib.gq_quantize_weights(0, None, None, 32, None) == -2
+    cache = _t(_lib.F16, [64, 16, 2, 1], [2, 128, 2048, 4096])
+    src = _t(_lib.F32, [64, 3, 2, 1], [4, 256, 768, 1536])
+    idx_bad = _t(_lib.I64, [4, 1, 1, 1], [8, 32, 32, 32])
+    assert lib.gq_set_rows(cache, src, idx_bad, None, None) == -1
+    q = _t(_lib.F32, [96, 1, 4, 1], [4, 384, 384, 1536])
+    k = _t(_lib.F16, [96, 256, 2, 1], [2, 192, 49152, 98304])
+    d = _t(_lib.F32, [96, 4, 1, 1], [4, 384, 1536, 1536])
+    assert lib.gq_flash_attn_ext(q, k, k, None, 0.1, 0.0, 0.0, d, None, 0, None) == -2
+    x = _t(_lib.F32, [10, 3, 1, 1], [4, 40, 120, 120])
+    y = _t(_lib.F32, [10, 4, 1, 1], [4, 40, 160, 160])
+    assert lib.gq_soft_max(x, None, 1.0, 0.0, y, None) == -1
+    assert lib.gq_soft_max(x, None, 1.0, 0.5, _t(_lib.F32, [10, 3, 1, 1], [4, 40, 120, 120]), None) == -1
+
+
+def test_python_binding_raises(lib):
+    with pytest.raises(_lib.GQError):
+        _lib.check(-1)

@@ -1,0 +1,268 @@
+"""Parity of the HIP path (through the C ABI) with the oracle and the reference's
+golden vectors. Needs an MI355X.
+
+Bars (north star): quantize_row_q8_0 and set_rows bit-exact; mul_mat within
+max-abs-rel 1e-3 (max|d| / max|ref|); attention within 1e-3 of the exact
+softmax, and within the reference's own deviation from it when compared to
+the reference (its decode path accumulates V in fp16).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from ggmlc_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def mar(a, b):
+    """max-abs-rel: max|a - b| / max|b|"""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def qweight(wq: np.ndarray, qtype: int, K: int) -> ops.QWeight:
+    return ops.QWeight(to_dev(wq), qtype, K)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    from ggmlc_amd import _lib
+
+    _lib.check(_lib.load().gq_init())
+    yield
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------ quantizers ---
+
+def test_quantize_row_q8_0_golden(golden_dir):
+    g = np.load(golden_dir / "quantize_q8_0.npz")
+    got = ops.quantize_row_q8_0(to_dev(g["x"])).cpu().numpy()
+    assert np.array_equal(got, g["q"])
+
+
+@pytest.mark.parametrize("shape,scale", [((1, 4096), 1.0), ((512, 4096), 1.0), ((8, 11008), 30.0),
+                                         ((3, 960), 1e-3), ((64, 2560), 1e-6)])
+def test_quantize_row_q8_0_vs_oracle(shape, scale):
+    rng = np.random.default_rng(hash(shape) % 2**32)
+    x = (rng.standard_normal(shape) * scale).astype(np.float32)
+    x[0, :64] = np.round(x[0, :64] * 4) / 4
+    x[-1, :32] = 0
+    got = ops.quantize_row_q8_0(to_dev(x)).cpu().numpy()
+    assert np.array_equal(got, O.quantize_row_q8_0(x))
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+def test_quantize_weights_vs_oracle(qtype):
+    rng = np.random.default_rng(qtype)
+    w = (rng.standard_normal((300, 1024)) * 0.02).astype(np.float32)
+    w[0, :32] = 0
+    w[1, :32] = np.round(w[1, :32] * 500) / 500
+    got = ops.quantize_weights(to_dev(w), qtype).data.cpu().numpy()
+    assert np.array_equal(got, O.quantize_weights(w, qtype))
+
+
+# --------------------------------------------------------------- mul_mat ---
+
+def test_mul_mat_golden(golden_dir):
+    files = sorted(golden_dir.glob("mul_mat_*.npz"))
+    assert files
+    for f in files:
+        g = np.load(f)
+        K = int(g["K"])
+        w = qweight(g["w"], int(g["wtype"]), K)
+        y = ops.mul_mat(w, to_dev(g["x"])).cpu().numpy()
+        r = mar(y, g["y"])
+        print(f.name, f"{r:.2e}")
+        assert r < 1e-3, (f.name, r)
+
+
+def _check_mm(qtype, K, N, M, rows_checked=256, seed=0):
+    rng = np.random.default_rng(seed)
+    w = (torch.randn((N, K), generator=torch.Generator().manual_seed(seed)) * 0.02).to(DEV)
+    qw = ops.quantize_weights(w.contiguous(), qtype)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    y = ops.mul_mat(qw, to_dev(x)).cpu().numpy()
+    sel = np.sort(rng.choice(N, size=min(rows_checked, N), replace=False))
+    sel[-1] = N - 1
+    wq_sel = qw.data.cpu().numpy()[sel]
+    msel = np.unique(np.concatenate([[0, M - 1], rng.choice(M, size=min(M, 64), replace=False)]))
+    want = O.mul_mat(wq_sel, qtype, K, x[msel])
+    r = mar(y[np.ix_(msel, sel)], want)
+    print(f"qtype={qtype} K={K} N={N} M={M}: max-abs-rel {r:.2e}")
+    assert r < 1e-3
+    return r
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_gemv_c1_q8_0(M):
+    """config 1: Linear 4096 -> 4096, Q8_0 (decode GEMV)."""
+    _check_mm(O.Q8_0, 4096, 4096, M)
+
+
+@pytest.mark.parametrize("M", [1, 8, 128, 512])
+def test_mlp_c2_q4_0(M):
+    """config 2: SwiGLU MLP 4096/11008, Q4_0: fused gate_up 4096 -> 22016, down 11008 -> 4096."""
+    _check_mm(O.Q4_0, 4096, 22016, M, seed=1)
+    _check_mm(O.Q4_0, 11008, 4096, M, seed=2)
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("K,N,M", [(960, 1600, 1), (960, 5120, 3), (2560, 960, 1), (960, 960, 37),
+                                   (1536, 2048, 16), (8960, 1536, 1), (256, 130, 5), (32, 7, 2)])
+def test_mul_mat_shapes(qtype, K, N, M):
+    _check_mm(qtype, K, N, M, seed=K + N + M)
+
+
+def test_mul_mat_strided_rows():
+    """src1 with a row stride wider than K (a view) and batch dims."""
+    K, N = 512, 96
+    rng = np.random.default_rng(4)
+    w = (torch.randn((N, K), generator=torch.Generator().manual_seed(4)) * 0.02).to(DEV)
+    qw = ops.quantize_weights(w, O.Q8_0)
+    big = rng.standard_normal((2, 3, K + 64)).astype(np.float32)
+    xt = to_dev(big)[:, :, :K]
+    y = ops.mul_mat(qw, xt).cpu().numpy()
+    want = O.mul_mat(qw.data.cpu().numpy(), O.Q8_0, K, big[:, :, :K].reshape(-1, K)).reshape(2, 3, N)
+    assert mar(y, want) < 1e-3
+
+
+# --------------------------------------------------------------- set_rows ---
+
+def test_set_rows_golden(golden_dir):
+    g = np.load(golden_dir / "set_rows_f32_f16.npz")
+    cache = to_dev(g["cache"]).view(torch.float16)
+    ops.set_rows(cache, to_dev(g["src"]), to_dev(g["idx"]))
+    assert np.array_equal(cache.view(torch.int16).cpu().numpy().view(np.uint16), g["out"])
+
+
+@pytest.mark.parametrize("B,H,ctx,hd,s", [(1, 32, 2048, 128, 1), (1, 5, 1024, 64, 512), (2, 2, 300, 128, 7),
+                                          (1, 3, 50, 6, 4)])
+def test_set_rows_vs_oracle(B, H, ctx, hd, s):
+    rng = np.random.default_rng(s + hd)
+    cache = f16(rng.standard_normal((B, H, ctx, hd)))
+    src = (rng.standard_normal((B, H, s, hd)) * 50).astype(np.float32)
+    src.reshape(-1)[:6] = [65519.0, 65520.0, -1e-8, 3e-6, -0.0, 7e4]
+    idx = rng.choice(ctx, size=s, replace=False).astype(np.int64)
+    want = O.set_rows_f32_f16(cache, src, idx)
+    dc = to_dev(cache).view(torch.float16)
+    ops.set_rows(dc, to_dev(src), to_dev(idx))
+    assert np.array_equal(dc.view(torch.int16).cpu().numpy().view(np.uint16), want)
+    # i32 indices give the same bytes
+    dc2 = to_dev(cache).view(torch.float16)
+    ops.set_rows(dc2, to_dev(src), to_dev(idx.astype(np.int32)))
+    assert torch.equal(dc2, dc)
+
+
+def test_set_rows_out_of_range_is_skipped_and_counted():
+    cache = torch.zeros((1, 2, 8, 64), dtype=torch.float16, device=DEV)
+    src = torch.ones((1, 2, 3, 64), dtype=torch.float32, device=DEV)
+    idx = torch.tensor([1, 8, -1], dtype=torch.int64, device=DEV)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.set_rows(cache, src, idx, n_bad=bad)
+    c = cache.cpu()
+    assert int(bad.item()) == 2 * 2  # two bad rows x two heads
+    assert (c[0, :, 1] == 1).all() and c[0, :, [0] + list(range(2, 8))].abs().sum() == 0
+
+
+# -------------------------------------------------------------- attention ---
+
+def _attn_dev(q, kc, vc, n_kv, mask, scale=None):
+    Hq, S, D = q.shape
+    scale = 1.0 / np.sqrt(np.float32(D)) if scale is None else scale
+    kd = to_dev(kc).view(torch.float16)[:, :n_kv]
+    vd = to_dev(vc).view(torch.float16)[:, :n_kv]
+    md = to_dev(mask).view(torch.float16) if mask is not None else None
+    return ops.flash_attn_ext(to_dev(q), kd, vd, md, float(scale)).cpu().numpy()
+
+
+def test_flash_attn_golden(golden_dir):
+    files = sorted(golden_dir.glob("flash_attn_*.npz"))
+    assert files
+    for f in files:
+        g = np.load(f)
+        n_kv = int(g["n_kv"])
+        got = _attn_dev(g["q"], g["kc"], g["vc"], n_kv, g["mask"])
+        exact = O.flash_attn_ext_f16(g["q"], g["kc"], g["vc"], n_kv, g["mask"], mode=1)
+        r_exact, r_ref = mar(got, exact), mar(got, g["out"])
+        ref_dev = mar(g["out"], exact)
+        print(f.name, f"vs exact {r_exact:.2e}  vs reference {r_ref:.2e}  (reference vs exact {ref_dev:.2e})")
+        assert r_exact < 1e-3
+        assert r_ref < ref_dev + 1e-3
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
+    (32, 32, 128, 1, 1100, 2048),   # config 4 decode (MHA)
+    (15, 5, 64, 1, 600, 1024),      # config 3 decode (GQA 3)
+    (12, 2, 128, 1, 4000, 4352),    # config 5 decode, long context (GQA 6)
+    (15, 5, 64, 4, 300, 1024),      # small chunk
+    (8, 2, 128, 64, 200, 512),      # prefill chunk, tiled-path precision
+    (32, 32, 128, 512, 0, 1024),    # config 4 pp512 first chunk
+])
+def test_flash_attn_vs_exact(Hq, Hkv, D, S, pos, ctx):
+    rng = np.random.default_rng(Hq * S + pos)
+    n_kv = O.pad_kv_len(pos + S, ctx)
+    q = rng.standard_normal((Hq, S, D)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, ctx, D)))
+    vc = f16(rng.standard_normal((Hkv, ctx, D)))
+    mask = O.causal_mask_f16(pos, S, n_kv)
+    got = _attn_dev(q, kc, vc, n_kv, mask)
+    exact = O.flash_attn_ext_f16(q, kc, vc, n_kv, mask, mode=1)
+    r = mar(got, exact)
+    print(f"Hq={Hq} Hkv={Hkv} D={D} S={S} n_kv={n_kv}: vs exact {r:.2e}")
+    assert r < 1e-3
+
+
+def test_flash_attn_padding_and_gqa_invariants():
+    rng = np.random.default_rng(21)
+    Hq, Hkv, D, ctx, pos = 6, 2, 64, 1024, 300
+    q = rng.standard_normal((Hq, 1, D)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, ctx, D)))
+    vc = f16(rng.standard_normal((Hkv, ctx, D)))
+    a = _attn_dev(q, kc, vc, 512, O.causal_mask_f16(pos, 1, 512))
+    b = _attn_dev(q, kc, vc, 768, O.causal_mask_f16(pos, 1, 768))
+    assert np.abs(a - b).max() < 1e-6  # masked padding contributes nothing
+    # GQA head h reads kv head h // 3: expanding K/V to MHA gives the same result
+    ke = np.repeat(kc, 3, axis=0)
+    ve = np.repeat(vc, 3, axis=0)
+    c = _attn_dev(q, ke, ve, 512, O.causal_mask_f16(pos, 1, 512))
+    assert np.abs(a - c).max() < 1e-6
+
+
+# ---------------------------------------------------------------- softmax ---
+
+def test_soft_max_golden(golden_dir):
+    g = np.load(golden_dir / "soft_max_f32.npz")
+    y = ops.soft_max_ext(to_dev(g["x"]), to_dev(g["mask"]).view(torch.float16), float(g["scale"]))
+    assert np.abs(y.cpu().numpy() - g["y"]).max() < 1e-6
+
+
+def test_soft_max_alibi_vs_torch():
+    rng = np.random.default_rng(5)
+    H, R, C = 6, 5, 77
+    x = rng.standard_normal((H, R, C)).astype(np.float32)
+    m = rng.standard_normal((R, C)).astype(np.float32)
+    mb = 8.0
+    y = ops.soft_max_ext(to_dev(x), to_dev(m).half(), 0.5, mb).cpu().numpy()
+    n_log2 = 1 << int(np.floor(np.log2(H)))
+    m0, m1 = 2.0 ** (-mb / n_log2), 2.0 ** (-mb / 2 / n_log2)
+    slopes = np.array([m0 ** (h + 1) if h < n_log2 else m1 ** (2 * (h - n_log2) + 1) for h in range(H)])
+    z = x * 0.5 + slopes[:, None, None] * m.astype(np.float16).astype(np.float32)[None]
+    z = np.exp(z - z.max(-1, keepdims=True))
+    assert np.abs(y - z / z.sum(-1, keepdims=True)).max() < 1e-6
