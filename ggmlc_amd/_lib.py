@@ -53,6 +53,14 @@ SIGNATURES = {
     "gq_flash_attn_ext_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_flash_attn_ext": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp, ctypes.c_size_t, _vp]),
     "gq_soft_max": (ctypes.c_int, [_P, _P, _f32, _f32, _P, _vp]),
+    "gq_swiglu": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _vp]),
+    "gq_rms_norm": (ctypes.c_int, [_P, _f32, _P, _vp]),
+    "gq_rope_ext": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _f32, _f32, _f32,
+                                   _f32, _P, _vp]),
+    "gq_add": (ctypes.c_int, [_P, _P, _P, _vp]),
+    "gq_get_rows": (ctypes.c_int, [_P, _P, _P, _vp]),
+    "gq_argmax": (ctypes.c_int, [_P, _P, _vp]),
+    "gq_probe_stream_read": (ctypes.c_int, [_vp, ctypes.c_size_t, _vp, _vp]),
 }
 
 _lib = None

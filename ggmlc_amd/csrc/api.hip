@@ -88,7 +88,8 @@ int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, M
         p.ldd = (int64_t)(dst->nb[1] / 4);
     }
     p.use_gemv = p.M <= gemv_max_m();
-    const size_t raw = p.use_gemv ? (size_t)p.M * act_row_bytes(K) : (size_t)p.M * K * 2;
+    // the GEMV quantizes the activation in LDS; the GEMM takes it as fp16 from the workspace
+    const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 2;
     p.ws = (raw + 255) & ~(size_t)255;
     return GQ_OK;
 }
@@ -146,9 +147,9 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     int rc = plan_mul_mat(a, b, dst, p);
     if (rc) return rc;
     if (p.M == 0) return GQ_OK;
-    if (!workspace || workspace_bytes < p.ws)
+    if (p.ws && (!workspace || workspace_bytes < p.ws))
         return fail(GQ_ERR_WORKSPACE, "mul_mat: workspace too small (need " + std::to_string(p.ws) + " bytes)");
-    if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    if (p.ws && (reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat: workspace must be 256-byte aligned");
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat: weight data must be 4-byte aligned");
@@ -156,12 +157,7 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     const float* x = static_cast<const float*>(b->data);
     float* y = static_cast<float*>(dst->data);
     const uint8_t* W = static_cast<const uint8_t*>(a->data);
-    if (p.use_gemv) {
-        const int64_t ars = act_row_bytes(p.K);
-        rc = quantize_q8_0_act(x, p.M, p.K, p.x_stride, workspace, ars, s);
-        if (rc) return rc;
-        return gemv(a->type, W, p.N, p.K, static_cast<const uint8_t*>(workspace), ars, p.M, y, p.ldd, s);
-    }
+    if (p.use_gemv) return gemv(a->type, W, p.N, p.K, x, p.x_stride, p.M, y, p.ldd, s);
     uint16_t* A = static_cast<uint16_t*>(workspace);
     rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, p.K, s);
     if (rc) return rc;
@@ -296,6 +292,117 @@ int gq_soft_max(const gq_tensor* a, const gq_tensor* mask, float scale, float ma
     s.scale = scale;
     s.max_bias = max_bias;
     return soft_max(s, (hipStream_t)stream);
+}
+
+// ---- decoder ops ----------------------------------------------------------
+
+int gq_swiglu(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, int swapped, gq_stream_t stream) {
+    if (!a || !dst) return fail(GQ_ERR_INVALID, "swiglu: null tensor");
+    if (a->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_F32 || (b && b->type != GQ_TYPE_F32))
+        return fail(GQ_ERR_UNSUPPORTED, "swiglu: F32 only");
+    if (a->nb[0] != 4 || dst->nb[0] != 4 || !rows_uniform(a) || !rows_uniform(dst) || (b && (b->nb[0] != 4 || !rows_uniform(b))))
+        return fail(GQ_ERR_INVALID, "swiglu: rows must be contiguous and uniformly strided");
+    const int64_t nc = b ? a->ne[0] : a->ne[0] / 2;
+    const int64_t nrows = a->ne[1] * a->ne[2] * a->ne[3];
+    if ((!b && a->ne[0] % 2) || dst->ne[0] != nc || dst->ne[1] * dst->ne[2] * dst->ne[3] != nrows ||
+        (b && (b->ne[0] != nc || b->ne[1] * b->ne[2] * b->ne[3] != nrows)))
+        return fail(GQ_ERR_INVALID, "swiglu: shape mismatch a " + shape(a) + " dst " + shape(dst));
+    const float* A = static_cast<const float*>(a->data);
+    const float* x = A;
+    const float* g = b ? static_cast<const float*>(b->data) : A + nc;
+    int64_t gnb1 = b ? (int64_t)b->nb[1] : (int64_t)a->nb[1];
+    if (!b && swapped) {
+        x = A + nc;
+        g = A;
+    }
+    return swiglu(x, (int64_t)a->nb[1], g, gnb1, static_cast<float*>(dst->data), (int64_t)dst->nb[1], nc, nrows,
+                  (hipStream_t)stream);
+}
+
+int gq_rms_norm(const gq_tensor* a, float eps, gq_tensor* dst, gq_stream_t stream) {
+    if (!a || !dst) return fail(GQ_ERR_INVALID, "rms_norm: null tensor");
+    if (a->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_F32) return fail(GQ_ERR_UNSUPPORTED, "rms_norm: F32 only");
+    if (a->nb[0] != 4 || dst->nb[0] != 4 || !rows_uniform(a) || !rows_uniform(dst))
+        return fail(GQ_ERR_INVALID, "rms_norm: rows must be contiguous and uniformly strided");
+    for (int i = 0; i < 4; ++i)
+        if (a->ne[i] != dst->ne[i]) return fail(GQ_ERR_INVALID, "rms_norm: dst shape differs");
+    return rms_norm(static_cast<const float*>(a->data), (int64_t)a->nb[1], static_cast<float*>(dst->data),
+                    (int64_t)dst->nb[1], a->ne[0], a->ne[1] * a->ne[2] * a->ne[3], eps, (hipStream_t)stream);
+}
+
+int gq_rope_ext(const gq_tensor* a, const gq_tensor* pos, int n_dims, int mode, int n_ctx_orig, float freq_base,
+                float freq_scale, float ext_factor, float attn_factor, float beta_fast, float beta_slow,
+                gq_tensor* dst, gq_stream_t stream) {
+    (void)n_ctx_orig;
+    (void)beta_fast;
+    (void)beta_slow;
+    if (!a || !pos || !dst) return fail(GQ_ERR_INVALID, "rope: null tensor");
+    if (a->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_F32 || pos->type != GQ_TYPE_I32)
+        return fail(GQ_ERR_UNSUPPORTED, "rope: F32 data and I32 positions only");
+    if (mode != 0 && mode != 2) return fail(GQ_ERR_UNSUPPORTED, "rope: modes 0 (normal) and 2 (neox) only");
+    if (ext_factor != 0.0f) return fail(GQ_ERR_UNSUPPORTED, "rope: YaRN (ext_factor != 0) not implemented");
+    if (n_dims <= 0 || n_dims % 2 || n_dims > a->ne[0] || pos->ne[0] < a->ne[2] || a->nb[0] != 4 || dst->nb[0] != 4)
+        return fail(GQ_ERR_INVALID, "rope: bad n_dims / positions / strides for " + shape(a));
+    for (int i = 0; i < 4; ++i)
+        if (a->ne[i] != dst->ne[i]) return fail(GQ_ERR_INVALID, "rope: dst shape differs");
+    return rope(static_cast<const float*>(a->data), a->ne[0], a->ne[1], a->ne[2], a->ne[3], (int64_t)a->nb[1],
+                (int64_t)a->nb[2], (int64_t)a->nb[3], static_cast<const int32_t*>(pos->data),
+                static_cast<float*>(dst->data), (int64_t)dst->nb[1], (int64_t)dst->nb[2], (int64_t)dst->nb[3], n_dims,
+                mode == 2, freq_base, freq_scale, attn_factor, (hipStream_t)stream);
+}
+
+int gq_add(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream) {
+    if (!a || !b || !dst) return fail(GQ_ERR_INVALID, "add: null tensor");
+    if (a->type != GQ_TYPE_F32 || b->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_F32)
+        return fail(GQ_ERR_UNSUPPORTED, "add: F32 only");
+    for (int i = 0; i < 4; ++i) {
+        if (b->ne[i] <= 0 || a->ne[i] % b->ne[i] != 0 || dst->ne[i] != a->ne[i])
+            return fail(GQ_ERR_INVALID, "add: b must repeat into a: a " + shape(a) + " b " + shape(b));
+    }
+    if (a->nb[0] != 4 || b->nb[0] != 4 || dst->nb[0] != 4) return fail(GQ_ERR_INVALID, "add: rows must be contiguous");
+    int64_t ane[4], anb[4], bne[4], bnb[4], ynb[4];
+    for (int i = 0; i < 4; ++i) {
+        ane[i] = a->ne[i];
+        anb[i] = (int64_t)a->nb[i];
+        bne[i] = b->ne[i];
+        bnb[i] = (int64_t)b->nb[i];
+        ynb[i] = (int64_t)dst->nb[i];
+    }
+    return add(static_cast<const float*>(a->data), ane, anb, static_cast<const float*>(b->data), bne, bnb,
+               static_cast<float*>(dst->data), ynb, (hipStream_t)stream);
+}
+
+int gq_get_rows(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream) {
+    if (!a || !b || !dst) return fail(GQ_ERR_INVALID, "get_rows: null tensor");
+    if (a->type != GQ_TYPE_F32 && a->type != GQ_TYPE_F16 && a->type != GQ_TYPE_Q8_0 && a->type != GQ_TYPE_Q4_0)
+        return fail(GQ_ERR_UNSUPPORTED, "get_rows: table type must be F32, F16, Q8_0 or Q4_0");
+    if (b->type != GQ_TYPE_I32 && b->type != GQ_TYPE_I64) return fail(GQ_ERR_INVALID, "get_rows: ids must be I32/I64");
+    if (dst->type != GQ_TYPE_F32 || dst->ne[0] != a->ne[0] || dst->ne[1] != b->ne[0] || a->ne[2] != 1 || a->ne[3] != 1 ||
+        b->ne[1] != 1 || b->ne[2] != 1 || dst->nb[0] != 4)
+        return fail(GQ_ERR_INVALID, "get_rows: shape mismatch a " + shape(a) + " b " + shape(b) + " dst " + shape(dst));
+    if ((a->type == GQ_TYPE_Q8_0 || a->type == GQ_TYPE_Q4_0) && a->ne[0] % QK)
+        return fail(GQ_ERR_INVALID, "get_rows: quantized rows must be whole blocks");
+    if (b->nb[0] != (size_t)(b->type == GQ_TYPE_I64 ? 8 : 4)) return fail(GQ_ERR_INVALID, "get_rows: ids must be contiguous");
+    return get_rows(static_cast<const uint8_t*>(a->data), a->type, a->ne[0], (int64_t)a->nb[1], a->ne[1], b->data,
+                    b->type == GQ_TYPE_I64, b->ne[0], static_cast<float*>(dst->data), (int64_t)dst->nb[1],
+                    (hipStream_t)stream);
+}
+
+int gq_argmax(const gq_tensor* a, gq_tensor* dst, gq_stream_t stream) {
+    if (!a || !dst) return fail(GQ_ERR_INVALID, "argmax: null tensor");
+    if (a->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_I32 || a->nb[0] != 4 || a->ne[2] != 1 || a->ne[3] != 1 ||
+        dst->ne[0] != a->ne[1])
+        return fail(GQ_ERR_INVALID, "argmax: a F32 [n, rows] -> dst I32 [rows]");
+    return argmax(static_cast<const float*>(a->data), (int64_t)a->nb[1], a->ne[0], a->ne[1],
+                  static_cast<int32_t*>(dst->data), (hipStream_t)stream);
+}
+
+// ---- measurement aid ------------------------------------------------------
+
+int gq_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, gq_stream_t stream) {
+    if (!p || !sink || bytes < 16 || (reinterpret_cast<uintptr_t>(p) & 15))
+        return fail(GQ_ERR_INVALID, "probe_stream_read: needs a 16-byte aligned buffer and a sink");
+    return read_probe(p, bytes, sink, (hipStream_t)stream);
 }
 
 }  // extern "C"

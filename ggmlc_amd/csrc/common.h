@@ -25,7 +25,7 @@ constexpr int ACT_QS_OFF = 0;
 constexpr int ACT_D_OFF = 256;
 constexpr int ACT_S_OFF = 288;
 
-inline int64_t act_row_bytes(int64_t K) { return ((K / QK + 7) / 8) * ACT_GS; }
+__host__ __device__ inline int64_t act_row_bytes(int64_t K) { return ((K / QK + 7) / 8) * ACT_GS; }
 
 // ---- error reporting -----------------------------------------------------
 void set_error(const std::string& msg);
@@ -84,5 +84,92 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- activation quantizer core ----------------------------------------------
+// ggml x86 quantize_row_q8_0 (ggml-cpu/arch/x86/quants.c:302-398) for one 32-wide
+// block spread over 4 consecutive lanes of a wave (8 elements each):
+//   amax = max|x|, d = fp16_rne(amax / 127), id = amax ? 127 / amax : 0,
+//   q = saturate_int8(rne(x * id)).
+// Every lane of the wave must call it (xor shuffles); lanes without data pass
+// zeros. Returns the lane's 8 quants, the block's fp16 scale bits and the
+// block sum of the quants (used by Q4_0 dot products).
+// The callers' translation units are built with fp contraction off for this.
+__device__ __forceinline__ void quant8_block(const float (&v)[8], int (&q)[8], uint16_t& dh, int& qsum) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float d = div_rn(amax, 127.0f);
+    const float id = amax != 0.0f ? div_rn(127.0f, amax) : 0.0f;
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float r = __builtin_rintf(v[i] * id);
+        int iv = (int)r;
+        iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+        q[i] = iv;
+        s += iv;
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    qsum = s;
+    dh = f2h(d);
+}
+
+// load the 8 floats of one lane's part of a block (16-byte loads when aligned)
+template <bool VEC>
+__device__ __forceinline__ void load8(const float* src, bool valid, float (&v)[8]) {
+    if (!valid) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        return;
+    }
+    if (VEC) {
+        const float4 a0 = *reinterpret_cast<const float4*>(src);
+        const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
+        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = src[i];
+    }
+}
+
+// Quantize M activation rows (K elements, row stride x_stride floats) into the
+// ACT_GS layout at dst (row stride act_bytes), cooperatively by a 256-lane block.
+template <bool VEC>
+__device__ __forceinline__ void quantize_rows_to_act(const float* __restrict__ x, int64_t x_stride, int M, int K,
+                                                     uint8_t* dst, int act_bytes) {
+    const int nb = K / QK;
+    for (int m = 0; m < M; ++m) {
+        for (int base = 0; base < nb * 4; base += 256) {
+            const int t = base + (int)threadIdx.x;
+            const int b = t >> 2, part = t & 3;
+            const bool valid = b < nb;
+            float v[8];
+            load8<VEC>(x + (int64_t)m * x_stride + (int64_t)b * QK + part * 8, valid, v);
+            int q[8];
+            uint16_t dh;
+            int qsum;
+            quant8_block(v, q, dh, qsum);
+            if (valid) {
+                uint8_t* gp = dst + m * act_bytes + (b >> 3) * ACT_GS;
+                const int bi = b & 7;
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
+                    hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+                }
+                *reinterpret_cast<uint2*>(gp + ACT_QS_OFF + bi * QK + part * 8) = make_uint2(lo, hi);
+                if (part == 0) {
+                    reinterpret_cast<float*>(gp + ACT_D_OFF)[bi] = h2f(dh);
+                    reinterpret_cast<int*>(gp + ACT_S_OFF)[bi] = qsum;
+                }
+            }
+        }
+    }
+}
 
 }  // namespace gq

@@ -1,0 +1,230 @@
+// The decoder ops around the quantized path (the graph nodes between the
+// MUL_MATs and FLASH_ATTN_EXT that ggmlc's executor emits for a LLaMA-style
+// layer, runtime/src/executor.cpp:2034-2090, 2355-2357, 2742-2756):
+//   GET_ROWS (Q8_0/Q4_0/F16/F32 table -> F32), RMS_NORM, ROPE (normal / NEOX),
+//   GLU SWIGLU, ADD (broadcast), ARGMAX.
+// Each follows the CPU semantics of ggml-cpu/ops.cpp (cited per kernel); all
+// are memory-bound elementwise/row kernels.
+#include "common.h"
+#include "kernels.h"
+
+namespace gq {
+
+namespace {
+
+__device__ __forceinline__ const uint8_t* at(const void* p, int64_t off) {
+    return reinterpret_cast<const uint8_t*>(p) + off;
+}
+
+// ---- SWIGLU: y[i] = silu(a[i]) * a[i + nc] per row (ggml_compute_forward_swiglu_f32,
+// ops.cpp:3246; swapped exchanges the halves). silu(x) = x / (1 + exp(-x)).
+__global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ a, int64_t anb1, const float* __restrict__ b,
+                                                int64_t bnb1, float* __restrict__ y, int64_t ynb1, int64_t nc,
+                                                int64_t nrows) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= nc * nrows) return;
+    const int64_t r = gid / nc, c = gid % nc;
+    const float x = *reinterpret_cast<const float*>(at(a, r * anb1) + c * 4);
+    const float g = *reinterpret_cast<const float*>(at(b, r * bnb1) + c * 4);
+    const float s = x / (1.0f + expf(-x));
+    *reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + r * ynb1 + c * 4) = s * g;
+}
+
+// ---- RMS_NORM: y = x / sqrt(mean(x^2) + eps) per row (ops.cpp rms_norm_f32, sum in double)
+__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, int64_t xnb1, float* __restrict__ y,
+                                                  int64_t ynb1, int64_t n, float eps) {
+    __shared__ double red[4];
+    const int64_t r = blockIdx.x;
+    const float* xr = reinterpret_cast<const float*>(at(x, r * xnb1));
+    float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + r * ynb1);
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) s += (double)(xr[i] * xr[i]);
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    s = red[0] + red[1] + red[2] + red[3];
+    const float mean = (float)(s / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * scale;
+}
+
+// ---- ROPE (ops.cpp:5886-6120, ext_factor = 0): theta_i = p * theta_scale^i built by
+// repeated multiplication like ggml_rope_cache_init; NEOX pairs (i, i + n_dims/2),
+// NORMAL pairs (2i, 2i+1); dims >= n_dims are copied.
+__global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, int64_t ne0, int64_t ne1, int64_t ne2,
+                                              int64_t xnb1, int64_t xnb2, int64_t xnb3, const int32_t* __restrict__ pos,
+                                              float* __restrict__ y, int64_t ynb1, int64_t ynb2, int64_t ynb3,
+                                              int n_dims, int neox, float freq_scale, float attn_factor,
+                                              float theta_scale, int64_t total_rows) {
+    const int64_t row = blockIdx.x;
+    if (row >= total_rows) return;
+    const int64_t i1 = row % ne1;
+    const int64_t i2 = (row / ne1) % ne2;
+    const int64_t i3 = row / (ne1 * ne2);
+    const float* xr = reinterpret_cast<const float*>(at(x, i1 * xnb1 + i2 * xnb2 + i3 * xnb3));
+    float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + i1 * ynb1 + i2 * ynb2 + i3 * ynb3);
+    const float p = (float)pos[i2];
+    const int half = n_dims / 2;
+    for (int j = threadIdx.x; j < half; j += blockDim.x) {
+        float theta = p;
+        for (int t = 0; t < j; ++t) theta *= theta_scale;
+        theta *= freq_scale;
+        const float c = cosf(theta) * attn_factor;
+        const float s = sinf(theta) * attn_factor;
+        const int i0 = neox ? j : 2 * j;
+        const int i1p = neox ? j + half : 2 * j + 1;
+        const float x0 = xr[i0], x1 = xr[i1p];
+        yr[i0] = x0 * c - x1 * s;
+        yr[i1p] = x0 * s + x1 * c;
+    }
+    for (int64_t j = n_dims + threadIdx.x; j < ne0; j += blockDim.x) yr[j] = xr[j];
+}
+
+// ---- ADD with broadcast of b over a (ggml_can_repeat): y = a + b[i % ne_b]
+__global__ __launch_bounds__(256) void k_add(const float* __restrict__ a, const float* __restrict__ b,
+                                             float* __restrict__ y, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3,
+                                             int64_t anb1, int64_t anb2, int64_t anb3, int64_t bne0, int64_t bne1,
+                                             int64_t bne2, int64_t bne3, int64_t bnb1, int64_t bnb2, int64_t bnb3,
+                                             int64_t ynb1, int64_t ynb2, int64_t ynb3) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = ne0 * ne1 * ne2 * ne3;
+    if (gid >= total) return;
+    const int64_t i0 = gid % ne0;
+    int64_t r = gid / ne0;
+    const int64_t i1 = r % ne1;
+    r /= ne1;
+    const int64_t i2 = r % ne2;
+    const int64_t i3 = r / ne2;
+    const float va = *reinterpret_cast<const float*>(at(a, i1 * anb1 + i2 * anb2 + i3 * anb3) + i0 * 4);
+    const float vb = *reinterpret_cast<const float*>(
+        at(b, (i1 % bne1) * bnb1 + (i2 % bne2) * bnb2 + (i3 % bne3) * bnb3) + (i0 % bne0) * 4);
+    *reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + i1 * ynb1 + i2 * ynb2 + i3 * ynb3 + i0 * 4) = va + vb;
+}
+
+// ---- GET_ROWS: y[:, i] = dequant(a[:, idx[i]]) (ggml_compute_forward_get_rows_q / _f16 / _f32)
+__global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ a, int atype, int64_t ne0, int64_t anb1,
+                                                  int64_t arows, const void* __restrict__ idx, int idx64,
+                                                  int64_t n, float* __restrict__ y, int64_t ynb1) {
+    const int64_t i = blockIdx.y;
+    if (i >= n) return;
+    const int64_t r = idx64 ? reinterpret_cast<const int64_t*>(idx)[i] : reinterpret_cast<const int32_t*>(idx)[i];
+    float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + i * ynb1);
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= ne0) return;
+    if (r < 0 || r >= arows) {
+        yr[c] = 0.0f;
+        return;
+    }
+    const uint8_t* row = a + r * anb1;
+    float v;
+    if (atype == GQ_TYPE_F32) {
+        v = reinterpret_cast<const float*>(row)[c];
+    } else if (atype == GQ_TYPE_F16) {
+        v = h2f(reinterpret_cast<const uint16_t*>(row)[c]);
+    } else if (atype == GQ_TYPE_Q8_0) {
+        const uint8_t* blk = row + (c / QK) * Q8_BYTES;
+        v = (float)(int8_t)blk[2 + c % QK] * h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    } else {
+        const uint8_t* blk = row + (c / QK) * Q4_BYTES;
+        const int j = (int)(c % QK);
+        const int qv = j < 16 ? (blk[2 + j] & 0x0f) : (blk[2 + j - 16] >> 4);
+        v = (float)(qv - 8) * h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    }
+    yr[c] = v;
+}
+
+// ---- ARGMAX per row (first index of the maximum, ggml_vec_argmax_f32)
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int64_t xnb1, int64_t n,
+                                                int32_t* __restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int64_t r = blockIdx.x;
+    const float* xr = reinterpret_cast<const float*>(at(x, r * xnb1));
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const float v = xr[i];
+        if (v > best) {
+            best = v;
+            bi = (int)i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = sv[0];
+        bi = si[0];
+        for (int w = 1; w < 4; ++w)
+            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        out[r] = bi == 0x7fffffff ? 0 : bi;
+    }
+}
+
+}  // namespace
+
+int swiglu(const float* a, int64_t anb1, const float* b, int64_t bnb1, float* y, int64_t ynb1, int64_t nc,
+           int64_t nrows, hipStream_t s) {
+    const int64_t total = nc * nrows;
+    if (total == 0) return GQ_OK;
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, a, anb1, b, bnb1, y, ynb1, nc,
+                       nrows);
+    return check_hip(hipGetLastError(), "swiglu launch");
+}
+
+int rms_norm(const float* x, int64_t xnb1, float* y, int64_t ynb1, int64_t n, int64_t nrows, float eps,
+             hipStream_t s) {
+    if (nrows == 0) return GQ_OK;
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)nrows), dim3(256), 0, s, x, xnb1, y, ynb1, n, eps);
+    return check_hip(hipGetLastError(), "rms_norm launch");
+}
+
+int rope(const float* x, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int64_t xnb1, int64_t xnb2, int64_t xnb3,
+         const int32_t* pos, float* y, int64_t ynb1, int64_t ynb2, int64_t ynb3, int n_dims, int neox, float freq_base,
+         float freq_scale, float attn_factor, hipStream_t s) {
+    const int64_t rows = ne1 * ne2 * ne3;
+    if (rows == 0) return GQ_OK;
+    const float theta_scale = powf(freq_base, -2.0f / n_dims);
+    hipLaunchKernelGGL(k_rope, dim3((unsigned)rows), dim3(64), 0, s, x, ne0, ne1, ne2, xnb1, xnb2, xnb3, pos, y, ynb1,
+                       ynb2, ynb3, n_dims, neox, freq_scale, attn_factor, theta_scale, rows);
+    return check_hip(hipGetLastError(), "rope launch");
+}
+
+int add(const float* a, const int64_t* ane, const int64_t* anb, const float* b, const int64_t* bne,
+        const int64_t* bnb, float* y, const int64_t* ynb, hipStream_t s) {
+    const int64_t total = ane[0] * ane[1] * ane[2] * ane[3];
+    if (total == 0) return GQ_OK;
+    hipLaunchKernelGGL(k_add, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, a, b, y, ane[0], ane[1], ane[2],
+                       ane[3], anb[1], anb[2], anb[3], bne[0], bne[1], bne[2], bne[3], bnb[1], bnb[2], bnb[3], ynb[1],
+                       ynb[2], ynb[3]);
+    return check_hip(hipGetLastError(), "add launch");
+}
+
+int get_rows(const uint8_t* a, int atype, int64_t ne0, int64_t anb1, int64_t arows, const void* idx, int idx64,
+             int64_t n, float* y, int64_t ynb1, hipStream_t s) {
+    if (n == 0 || ne0 == 0) return GQ_OK;
+    hipLaunchKernelGGL(k_get_rows, dim3((unsigned)cdiv(ne0, 256), (unsigned)n), dim3(256), 0, s, a, atype, ne0, anb1,
+                       arows, idx, idx64, n, y, ynb1);
+    return check_hip(hipGetLastError(), "get_rows launch");
+}
+
+int argmax(const float* x, int64_t xnb1, int64_t n, int64_t nrows, int32_t* out, hipStream_t s) {
+    if (nrows == 0) return GQ_OK;
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)nrows), dim3(256), 0, s, x, xnb1, n, out);
+    return check_hip(hipGetLastError(), "argmax launch");
+}
+
+}  // namespace gq

@@ -17,13 +17,20 @@
 // unsigned and corrected with the precomputed block sum of the activation
 // (isum = dot(n, a) - 8 * sum(a)), which keeps the block sum exact.
 // The next iteration's global loads are issued before the current group is
-// decoded (register double buffer). The quantized activation (ACT_GS layout,
-// written by the quantizer) is copied to LDS once per workgroup.
+// decoded (register double buffer). Each workgroup first quantizes the fp32
+// activation rows into LDS itself (ACT_GS layout, the exact rule of
+// quantize_row_q8_0), so a decode MUL_MAT is a single launch.
 // A 16-lane xor reduction finishes each row.
 //
-// Fallback (any K % 32 == 0): one lane per block with 16-bit loads.
+// Fallback (any K % 32 == 0): one lane per block with 16-bit loads, activation
+// quantized into LDS the same way.
+#include <mutex>
+#include <unordered_map>
+
 #include "common.h"
 #include "kernels.h"
+
+#pragma clang fp contract(off)
 
 namespace gq {
 
@@ -41,6 +48,8 @@ struct QTraits<GQ_TYPE_Q8_0> {
     static constexpr int GB = 8 * BB;   // 272
     static constexpr int CPG = GB / 16; // 17
     static constexpr int NQW = 8;       // quant dwords per block
+    static constexpr int HC = 9;        // 16-byte chunks of a half-group window
+    static constexpr int H1 = 8;        // first chunk of the second window (byte 128)
 };
 template <>
 struct QTraits<GQ_TYPE_Q4_0> {
@@ -48,20 +57,24 @@ struct QTraits<GQ_TYPE_Q4_0> {
     static constexpr int GB = 8 * BB;   // 144
     static constexpr int CPG = GB / 16; // 9
     static constexpr int NQW = 4;
+    static constexpr int HC = 5;        // windows: bytes [0, 80) and [64, 144)
+    static constexpr int H1 = 4;
 };
 
+// Block at byte offset o (even) of a dword window w: its fp16 scale and quant
+// dwords. o % 4 == 0 puts the scale in the low half of w[o/4] and the quants two
+// bytes later (realigned with v_alignbyte); o % 4 == 2 puts the scale in the
+// high half and the quants on a dword boundary.
 template <int QT>
-__device__ __forceinline__ void decode_block(const uint32_t* w, int b, uint32_t& hdr, uint32_t* q) {
-    constexpr int BB = QTraits<QT>::BB;
-    constexpr int NQW = QT == GQ_TYPE_Q8_0 ? 8 : 4;  // quant dwords per block
-    constexpr int DWB = BB / 2;                      // dwords per 2 blocks (17 / 9)
-    if ((b & 1) == 0) {
-        const int base = (b / 2) * DWB;
+__device__ __forceinline__ void decode_at(const uint32_t* w, int o, uint32_t& hdr, uint32_t* q) {
+    constexpr int NQW = QTraits<QT>::NQW;
+    if ((o & 3) == 0) {
+        const int base = o >> 2;
         hdr = w[base] & 0xffffu;
 #pragma unroll
         for (int i = 0; i < NQW; ++i) q[i] = __builtin_amdgcn_alignbyte(w[base + i + 1], w[base + i], 2);
     } else {
-        const int base = (b / 2) * DWB + DWB / 2;  // (BB*b - 2)/4
+        const int base = (o - 2) >> 2;
         hdr = w[base] >> 16;
 #pragma unroll
         for (int i = 0; i < NQW; ++i) q[i] = w[base + 1 + i];
@@ -95,15 +108,16 @@ __device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, con
     }
 }
 
-template <int QT, int M>
+template <int QT, int M, bool XVEC, int PF>
 __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__ W, int64_t N,
                                                      int64_t row_bytes, int G,
-                                                     const uint8_t* __restrict__ act,
-                                                     int64_t act_stride, float* __restrict__ dst,
+                                                     const float* __restrict__ x,
+                                                     int64_t x_stride, float* __restrict__ dst,
                                                      int64_t ldd) {
     constexpr int GB = QTraits<QT>::GB;
     constexpr int CPG = QTraits<QT>::CPG;
     constexpr int SEG = LPR * CPG;  // chunks of one row per iteration
+    constexpr int XPMAX = 2;        // activation passes held in registers
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int lane = threadIdx.x & 63;
@@ -112,20 +126,40 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     uint8_t* s_act = smem;
     uint8_t* s_stage = smem + M * act_bytes + wave * 64 * GB;
 
-    // activation rows -> LDS (whole ACT_GS groups, 16-byte copies)
-    for (int m = 0; m < M; ++m)
-        for (int off = threadIdx.x * 16; off < act_bytes; off += 256 * 16)
-            *reinterpret_cast<uint4*>(s_act + m * act_bytes + off) =
-                *reinterpret_cast<const uint4*>(act + m * act_stride + off);
-
-    const int64_t row0 = ((int64_t)blockIdx.x * WAVES + wave) * RPW;
     const int rsub = lane / LPR;
     const int gsub = lane % LPR;
-    const int64_t row = row0 + rsub;
     const int J = (G + LPR - 1) / LPR;
+    const int nb = G * 8;
+    const int XP = (nb * 4 + 255) / 256;  // quantizer passes per activation row
 
-    uint4 pre[CPG];
-    auto load_iter = [&](int j) {
+    // persistent waves: wave-tile t = RPW rows, tiles gw, gw + total, ...; the
+    // (tile, K-iteration) sequence of a wave is one flat pipeline
+    const int64_t n_tiles = (N + RPW - 1) / RPW;
+    const int64_t total = (int64_t)gridDim.x * WAVES;
+    const int64_t gw = (int64_t)blockIdx.x * WAVES + wave;
+    const int64_t my_tiles = gw < n_tiles ? (n_tiles - gw + total - 1) / total : 0;
+    const int64_t F = my_tiles * J;
+
+    // 1) activation loads first (they are needed first), into registers when small
+    float xr[XPMAX][8];
+    const bool xpre = M * XP <= XPMAX;
+    if (xpre) {
+#pragma unroll
+        for (int p = 0; p < XPMAX; ++p) {
+            if (p < M * XP) {
+                const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
+                load8<XVEC>(x + (int64_t)m * x_stride + (int64_t)(t >> 2) * QK + (t & 3) * 8, (t >> 2) < nb, xr[p]);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2) weight loads for the first PF steps (coalesced 16-byte chunks)
+    uint4 pre[PF][CPG];
+    auto load_step = [&](int64_t f, uint4(&dstv)[CPG]) {
+        const int64_t tile = gw + (f / J) * total;
+        const int j = (int)(f % J);
+        const int64_t row0 = tile * RPW;
 #pragma unroll
         for (int c = 0; c < CPG; ++c) {
             const int ci = lane + 64 * c;
@@ -133,42 +167,91 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             const int within = ci - r * SEG;
             const int64_t rr = row0 + r;
             const int64_t boff = (int64_t)j * (LPR * GB) + (int64_t)within * 16;
-            if (rr < N && boff < row_bytes)
-                pre[c] = ld_nt16(W + rr * row_bytes + boff);
-            else
-                pre[c] = make_uint4(0, 0, 0, 0);
+            const bool ok = rr < N && boff < row_bytes;
+            // always-valid address, zeroed after the load: no branch per chunk
+            uint4 v = ld_nt16(W + (ok ? rr * row_bytes + boff : 0));
+            if (!ok) v = make_uint4(0, 0, 0, 0);
+            dstv[c] = v;
         }
     };
+#pragma unroll
+    for (int s = 0; s < PF; ++s)
+        if (s < F) load_step(s, pre[s]);
+    __builtin_amdgcn_sched_barrier(0);
 
-    load_iter(0);
-    __syncthreads();  // activation in LDS
+    // 3) quantize the activation into LDS while the weights are in flight
+    if (xpre) {
+#pragma unroll
+        for (int p = 0; p < XPMAX; ++p) {
+            if (p < M * XP) {  // uniform across the workgroup
+                const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
+                const int b = t >> 2, part = t & 3;
+                int q[8];
+                uint16_t dh;
+                int qsum;
+                quant8_block(xr[p], q, dh, qsum);
+                if (b < nb) {
+                    uint8_t* gp = s_act + m * act_bytes + (b >> 3) * ACT_GS;
+                    const int bi = b & 7;
+                    uint32_t lo = 0, hi = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
+                        hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+                    }
+                    *reinterpret_cast<uint2*>(gp + ACT_QS_OFF + bi * QK + part * 8) = make_uint2(lo, hi);
+                    if (part == 0) {
+                        reinterpret_cast<float*>(gp + ACT_D_OFF)[bi] = h2f(dh);
+                        reinterpret_cast<int*>(gp + ACT_S_OFF)[bi] = qsum;
+                    }
+                }
+            }
+        }
+    } else {
+        quantize_rows_to_act<XVEC>(x, x_stride, M, G * 256, s_act, act_bytes);
+    }
+    __syncthreads();  // quantized activation visible to all waves
 
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
 
-    for (int j = 0; j < J; ++j) {
+    for (int64_t f = 0; f < F; ++f) {
+        const int64_t tile = gw + (f / J) * total;
+        const int j = (int)(f % J);
+        const int64_t row = tile * RPW + rsub;
 #pragma unroll
-        for (int c = 0; c < CPG; ++c) *reinterpret_cast<uint4*>(s_stage + (lane + 64 * c) * 16) = pre[c];
+        for (int c = 0; c < CPG; ++c) *reinterpret_cast<uint4*>(s_stage + (lane + 64 * c) * 16) = pre[0][c];
         wave_lds_sync();
-        if (j + 1 < J) load_iter(j + 1);
-        uint32_t w[4 * CPG];
+        // rotate the register pipeline and issue step f + PF
 #pragma unroll
-        for (int c = 0; c < CPG; ++c) {
-            const uint4 t = *reinterpret_cast<const uint4*>(s_stage + lane * GB + 16 * c);
-            w[4 * c + 0] = t.x;
-            w[4 * c + 1] = t.y;
-            w[4 * c + 2] = t.z;
-            w[4 * c + 3] = t.w;
-        }
-        wave_lds_sync();
+        for (int s = 0; s + 1 < PF; ++s)
+#pragma unroll
+            for (int c = 0; c < CPG; ++c) pre[s][c] = pre[s + 1][c];
+        if (f + PF < F) load_step(f + PF, pre[PF - 1]);
         const int g = j * LPR + gsub;
-        if (row < N && g < G) {
+        const bool live = row < N && g < G;
+        // decode the group in two windows of HC chunks (blocks 0-3, then 4-7)
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
+        for (int h = 0; h < 2; ++h) {
+            constexpr int HC = QTraits<QT>::HC;
+            const int c0 = h ? QTraits<QT>::H1 : 0;
+            uint32_t w[4 * HC];
+#pragma unroll
+            for (int c = 0; c < HC; ++c) {
+                const uint4 t = *reinterpret_cast<const uint4*>(s_stage + lane * GB + 16 * (c0 + c));
+                w[4 * c + 0] = t.x;
+                w[4 * c + 1] = t.y;
+                w[4 * c + 2] = t.z;
+                w[4 * c + 3] = t.w;
+            }
+            if (!live) continue;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const int b = 4 * h + bb;
                 uint32_t hdr;
                 uint32_t q[QTraits<QT>::NQW];
-                decode_block<QT>(w, b, hdr, q);
+                decode_at<QT>(w, QTraits<QT>::BB * b - 16 * c0, hdr, q);
                 const float dw = h2f((uint16_t)hdr);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
@@ -181,24 +264,138 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                 }
             }
         }
-    }
+        wave_lds_sync();  // this step's staging slice is fully read before it is refilled
+        if (j == J - 1) {  // tile finished: reduce the 16 lanes of each row and store
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const float v = xor_sum<LPR>(acc[m]);
-        if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
+            for (int m = 0; m < M; ++m) {
+                const float v = xor_sum<LPR>(acc[m]);
+                if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
+                acc[m] = 0.0f;
+            }
+        }
+    }
+}
+
+// ---- direct variant: each lane loads its own group (no LDS staging) ---------------
+// The 9 (Q4_0) or 17 (Q8_0) 16-byte loads of a lane are contiguous; across the
+// wave one instruction touches 64 lines, and the following instructions hit the
+// same lines while their misses are still pending (merged in the L1 miss queue).
+// Without the staging slice the kernel needs far fewer registers and only the
+// activation in LDS, so more waves are resident.
+template <int QT, int M, bool XVEC, int PF, bool COPY>
+__global__ __launch_bounds__(256) void k_gemv_dir(const uint8_t* __restrict__ W, int64_t N,
+                                                  int64_t row_bytes, int G,
+                                                  const float* __restrict__ x,
+                                                  int64_t x_stride, float* __restrict__ dst,
+                                                  int64_t ldd) {
+    constexpr int GB = QTraits<QT>::GB;
+    constexpr int CPG = QTraits<QT>::CPG;
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int act_bytes = G * ACT_GS;
+    uint8_t* s_act = smem;
+
+    const int rsub = lane / LPR;
+    const int gsub = lane % LPR;
+    const int J = (G + LPR - 1) / LPR;
+
+    const int64_t n_tiles = (N + RPW - 1) / RPW;
+    const int64_t total = (int64_t)gridDim.x * WAVES;
+    const int64_t gw = (int64_t)blockIdx.x * WAVES + wave;
+    const int64_t my_tiles = gw < n_tiles ? (n_tiles - gw + total - 1) / total : 0;
+    const int64_t F = my_tiles * J;
+
+    uint4 pre[PF][CPG];
+    auto load_step = [&](int64_t f, uint4(&dstv)[CPG]) {
+        const int64_t tile = gw + (f / J) * total;
+        const int j = (int)(f % J);
+        const int64_t rr = tile * RPW + rsub;
+        const int g = j * LPR + gsub;
+        const uint8_t* p = W + rr * row_bytes + (int64_t)g * GB;
+        const bool ok = rr < N && g < G;
+#pragma unroll
+        for (int c = 0; c < CPG; ++c) dstv[c] = ok ? ld_nt16(p + 16 * c) : make_uint4(0, 0, 0, 0);
+    };
+#pragma unroll
+    for (int s = 0; s < PF; ++s)
+        if (s < F) load_step(s, pre[s]);
+
+    quantize_rows_to_act<XVEC>(x, x_stride, M, G * 256, s_act, act_bytes);
+    __syncthreads();
+
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+
+    for (int64_t f = 0; f < F; ++f) {
+        const int64_t tile = gw + (f / J) * total;
+        const int j = (int)(f % J);
+        const int64_t row = tile * RPW + rsub;
+        uint32_t w[4 * CPG];
+#pragma unroll
+        for (int c = 0; c < CPG; ++c) {
+            w[4 * c + 0] = pre[0][c].x;
+            w[4 * c + 1] = pre[0][c].y;
+            w[4 * c + 2] = pre[0][c].z;
+            w[4 * c + 3] = pre[0][c].w;
+        }
+        if constexpr (COPY) {  // issue the next step before decoding this one
+#pragma unroll
+            for (int s = 0; s + 1 < PF; ++s)
+#pragma unroll
+                for (int c = 0; c < CPG; ++c) pre[s][c] = pre[s + 1][c];
+            if (f + PF < F) load_step(f + PF, pre[PF - 1]);
+        }
+        const int g = j * LPR + gsub;
+        if (row < N && g < G) {
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                uint32_t hdr;
+                uint32_t q[QTraits<QT>::NQW];
+                decode_at<QT>(w, QTraits<QT>::BB * b, hdr, q);
+                const float dw = h2f((uint16_t)hdr);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint8_t* ag = s_act + m * act_bytes + g * ACT_GS;
+                    const uint4 a0 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b);
+                    const uint4 a1 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b + 16);
+                    const float da = reinterpret_cast<const float*>(ag + ACT_D_OFF)[b];
+                    const int s = block_dot<QT>(q, a0, a1, ag, b);
+                    acc[m] += (float)s * (dw * da);
+                }
+            }
+        }
+        if constexpr (!COPY) {  // registers are free again: issue the next step
+            if (f + 1 < F) load_step(f + 1, pre[0]);
+        }
+        if (j == J - 1) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float v = xor_sum<LPR>(acc[m]);
+                if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
+                acc[m] = 0.0f;
+            }
+        }
     }
 }
 
 // ---- fallback: one lane per block, 16-bit loads (any K % 32 == 0) ---------------
 
-template <int QT, int M>
+template <int QT, int M, bool XVEC>
 __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W, int64_t N,
                                                   int64_t row_bytes, int nb,
-                                                  const uint8_t* __restrict__ act,
-                                                  int64_t act_stride, float* __restrict__ dst,
+                                                  const float* __restrict__ x,
+                                                  int64_t x_stride, float* __restrict__ dst,
                                                   int64_t ldd) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int NQW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int act_stride = (int)act_row_bytes((int64_t)nb * QK);
+    const uint8_t* act = smem;
+    quantize_rows_to_act<XVEC>(x, x_stride, M, nb * QK, smem, act_stride);
+    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
     const int sub = lane % LPR;
@@ -232,60 +429,145 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
     }
 }
 
-template <int QT, int M>
-int launch_grp(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t act_stride,
-               float* dst, int64_t ldd, hipStream_t s) {
+constexpr size_t LDS_MAX = 160 * 1024;
+
+template <typename KFn>
+int allow_big_lds(KFn* fn, bool& done) {
+    if (done) return GQ_OK;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
+    if (e != hipSuccess) return check_hip(e, "gemv: set LDS attribute");
+    done = true;
+    return GQ_OK;
+}
+
+// persistent grid: as many workgroups as can be resident, never more than
+// tiles (residency depends on the kernel and its LDS size: cached per pair)
+template <typename KFn>
+int resident_wgs(KFn* fn, size_t lds, int& out) {
+    static std::mutex mu;
+    static std::unordered_map<size_t, int> cache;
+    const size_t key = lds * 1315423911u ^ reinterpret_cast<uintptr_t>(fn);
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = cache.find(key);
+        if (it != cache.end()) {
+            out = it->second;
+            return GQ_OK;
+        }
+    }
+    int per_cu = 0, ncu = 0, dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    rc = check_hip(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+    if (rc) return rc;
+    rc = check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, lds), "gemv occupancy");
+    if (rc) return rc;
+    out = (per_cu > 0 ? per_cu : 1) * ncu;
+    std::lock_guard<std::mutex> lk(mu);
+    cache[key] = out;
+    return GQ_OK;
+}
+
+// Weight-load scheme (GQ_GEMV_VARIANT, for measurement): 0 stage (LDS transpose,
+// register pipeline), 1 direct + copy (next step issued before decoding),
+// 2 direct without copy (next step issued after decoding), 3 direct, 2 steps.
+// Measured on MI355X the direct variants run ~2.4x slower than the staged one.
+int gemv_variant() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("GQ_GEMV_VARIANT");
+        v = e ? atoi(e) : 0;
+        if (v < 0 || v > 3) v = 0;
+    }
+    return v;
+}
+
+template <int QT, int M, bool XVEC, int PF>
+int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+                  float* dst, int64_t ldd, hipStream_t s) {
     const int G = (int)(K / 256);
     const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
-    const size_t lds = (size_t)M * G * ACT_GS + (size_t)WAVES * 64 * QTraits<QT>::GB;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_grp<QT, M>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return check_hip(e, "gemv set LDS attribute");
-        attr_set = true;
+    const int variant = gemv_variant();
+    const bool direct = variant != 0;
+    const size_t lds = (size_t)M * G * ACT_GS + (direct ? 0 : (size_t)WAVES * 64 * QTraits<QT>::GB);
+    if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
+    decltype(&k_gemv_grp<QT, M, XVEC, PF>) fn;
+    switch (variant) {
+        case 1: fn = &k_gemv_dir<QT, M, XVEC, 1, true>; break;
+        case 2: fn = &k_gemv_dir<QT, M, XVEC, 1, false>; break;
+        case 3: fn = &k_gemv_dir<QT, M, XVEC, 2, true>; break;
+        default: fn = &k_gemv_grp<QT, M, XVEC, PF>; break;
     }
-    if (lds > 160 * 1024) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
-    const dim3 grid((unsigned)cdiv(N, WAVES * RPW));
-    hipLaunchKernelGGL((k_gemv_grp<QT, M>), grid, dim3(256), lds, s, W, N, row_bytes, G, act,
-                       act_stride, dst, ldd);
+    static bool attr[4] = {false, false, false, false};
+    int rc = allow_big_lds(fn, attr[variant]);
+    if (rc) return rc;
+    int resident = 0;
+    rc = resident_wgs(fn, lds, resident);
+    if (rc) return rc;
+    const int64_t wg_needed = cdiv(N, WAVES * RPW);
+    const dim3 grid((unsigned)(wg_needed < resident ? wg_needed : resident));
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, x, x_stride, dst, ldd);
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
-template <int QT, int M>
-int launch_blk(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t act_stride,
+// Q4_0 keeps two steps of weight loads in flight per wave
+template <int QT, int M, bool XVEC>
+int launch_grp(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+               float* dst, int64_t ldd, hipStream_t s) {
+    if constexpr (QT == GQ_TYPE_Q8_0) {
+        return launch_grp_pf<QT, M, XVEC, 1>(W, N, K, x, x_stride, dst, ldd, s);
+    } else {
+        return launch_grp_pf<QT, M, XVEC, 2>(W, N, K, x, x_stride, dst, ldd, s);
+    }
+}
+
+template <int QT, int M, bool XVEC>
+int launch_blk(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
                float* dst, int64_t ldd, hipStream_t s) {
     const int nb = (int)(K / QK);
     const int64_t row_bytes = (int64_t)nb * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
+    const size_t lds = (size_t)M * act_row_bytes(K);
+    if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
+    static bool attr = false;
+    int rc = allow_big_lds(&k_gemv_blk<QT, M, XVEC>, attr);
+    if (rc) return rc;
     const dim3 grid((unsigned)cdiv(N, 256 / LPR));
-    hipLaunchKernelGGL((k_gemv_blk<QT, M>), grid, dim3(256), 0, s, W, N, row_bytes, nb, act,
-                       act_stride, dst, ldd);
+    hipLaunchKernelGGL((k_gemv_blk<QT, M, XVEC>), grid, dim3(256), lds, s, W, N, row_bytes, nb, x,
+                       x_stride, dst, ldd);
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
-template <int QT>
-int gemv_t(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t act_stride, int64_t M,
-           float* dst, int64_t ldd, hipStream_t s) {
+template <int QT, int M>
+int launch_m(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride, float* dst,
+             int64_t ldd, hipStream_t s) {
     const bool grp = (K % 256 == 0) && ((reinterpret_cast<uintptr_t>(W) & 15) == 0);
+    const bool xvec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (x_stride % 4 == 0);
+    if (grp)
+        return xvec ? launch_grp<QT, M, true>(W, N, K, x, x_stride, dst, ldd, s)
+                    : launch_grp<QT, M, false>(W, N, K, x, x_stride, dst, ldd, s);
+    return xvec ? launch_blk<QT, M, true>(W, N, K, x, x_stride, dst, ldd, s)
+                : launch_blk<QT, M, false>(W, N, K, x, x_stride, dst, ldd, s);
+}
+
+template <int QT>
+int gemv_t(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride, int64_t M,
+           float* dst, int64_t ldd, hipStream_t s) {
     switch (M) {
-        case 1: return grp ? launch_grp<QT, 1>(W, N, K, act, act_stride, dst, ldd, s)
-                           : launch_blk<QT, 1>(W, N, K, act, act_stride, dst, ldd, s);
-        case 2: return grp ? launch_grp<QT, 2>(W, N, K, act, act_stride, dst, ldd, s)
-                           : launch_blk<QT, 2>(W, N, K, act, act_stride, dst, ldd, s);
-        case 3: return grp ? launch_grp<QT, 3>(W, N, K, act, act_stride, dst, ldd, s)
-                           : launch_blk<QT, 3>(W, N, K, act, act_stride, dst, ldd, s);
-        case 4: return grp ? launch_grp<QT, 4>(W, N, K, act, act_stride, dst, ldd, s)
-                           : launch_blk<QT, 4>(W, N, K, act, act_stride, dst, ldd, s);
+        case 1: return launch_m<QT, 1>(W, N, K, x, x_stride, dst, ldd, s);
+        case 2: return launch_m<QT, 2>(W, N, K, x, x_stride, dst, ldd, s);
+        case 3: return launch_m<QT, 3>(W, N, K, x, x_stride, dst, ldd, s);
+        case 4: return launch_m<QT, 4>(W, N, K, x, x_stride, dst, ldd, s);
         default: return fail(GQ_ERR_INVALID, "gemv: M out of range");
     }
 }
 
 }  // namespace
 
-int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t act_stride,
+int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
          int64_t M, float* dst, int64_t ldd, hipStream_t s) {
-    if (type == GQ_TYPE_Q8_0) return gemv_t<GQ_TYPE_Q8_0>(W, N, K, act, act_stride, M, dst, ldd, s);
-    return gemv_t<GQ_TYPE_Q4_0>(W, N, K, act, act_stride, M, dst, ldd, s);
+    if (type == GQ_TYPE_Q8_0) return gemv_t<GQ_TYPE_Q8_0>(W, N, K, x, x_stride, M, dst, ldd, s);
+    return gemv_t<GQ_TYPE_Q4_0>(W, N, K, x, x_stride, M, dst, ldd, s);
 }
 
 }  // namespace gq

@@ -8,15 +8,14 @@ namespace gq {
 // quantize.hip
 int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
                          hipStream_t s);
-int quantize_q8_0_act(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* act,
-                      int64_t act_stride_bytes, hipStream_t s);
 int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
                       int64_t y_stride_elems, hipStream_t s);
 int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s);
 
-// gemv.hip — dst[m * ldd + n] for m < M (M <= GEMV_MAX_M), act in the ACT_GS layout
+// gemv.hip — dst[m * ldd + n] for m < M (M <= GEMV_MAX_M); x fp32 rows (stride x_stride),
+// quantized inside the kernel
 constexpr int GEMV_MAX_M = 4;
-int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t act_stride,
+int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
          int64_t M, float* dst, int64_t ldd, hipStream_t s);
 
 // gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k], A fp16
@@ -68,5 +67,22 @@ struct SoftmaxArgs {
     float scale, max_bias;
 };
 int soft_max(const SoftmaxArgs& a, hipStream_t s);
+
+// decoder_ops.hip
+int swiglu(const float* a, int64_t anb1, const float* b, int64_t bnb1, float* y, int64_t ynb1, int64_t nc,
+           int64_t nrows, hipStream_t s);
+int rms_norm(const float* x, int64_t xnb1, float* y, int64_t ynb1, int64_t n, int64_t nrows, float eps,
+             hipStream_t s);
+int rope(const float* x, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int64_t xnb1, int64_t xnb2, int64_t xnb3,
+         const int32_t* pos, float* y, int64_t ynb1, int64_t ynb2, int64_t ynb3, int n_dims, int neox, float freq_base,
+         float freq_scale, float attn_factor, hipStream_t s);
+int add(const float* a, const int64_t* ane, const int64_t* anb, const float* b, const int64_t* bne,
+        const int64_t* bnb, float* y, const int64_t* ynb, hipStream_t s);
+int get_rows(const uint8_t* a, int atype, int64_t ne0, int64_t anb1, int64_t arows, const void* idx, int idx64,
+             int64_t n, float* y, int64_t ynb1, hipStream_t s);
+int argmax(const float* x, int64_t xnb1, int64_t n, int64_t nrows, int32_t* out, hipStream_t s);
+
+// probe.hip
+int read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t s);
 
 }  // namespace gq

@@ -6,7 +6,8 @@
 //   amax = max|x|, d = fp16_rne(amax / 127), id = amax ? 127 / amax : 0,
 //   q = saturate_int8(round_half_even(x * id)).
 // Four lanes own one 32-element block (8 elements each, two 16-byte loads);
-// amax and the block sum of q are exchanged with two xor shuffles.
+// amax is exchanged with two xor shuffles (quant8_block, common.h). The GEMV
+// path runs the same code inside its own kernel (quantize_rows_to_act).
 //
 // Weights: ggmlc's compile-time quantizers (python/ggmlc/quantization/
 // quantize.py:10-47 Q8_0, :65-107 Q4_0) with numpy float32 semantics, one
@@ -19,8 +20,9 @@
 
 namespace gq {
 
-enum ActOut { OUT_BLOCKS = 0, OUT_ACT = 1, OUT_F16 = 2 };
+enum ActOut { OUT_BLOCKS = 0, OUT_F16 = 2 };
 
+// One lane per 8 elements, 4 lanes per block (quant8_block in common.h).
 template <int MODE, bool VEC>
 __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ x, int64_t nrows,
                                                       int64_t K, int64_t x_stride,
@@ -34,46 +36,13 @@ __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ 
     const int64_t b = valid ? blk - m * nb : 0;
 
     float v[8];
-    if (valid) {
-        const float* src = x + m * x_stride + b * QK + part * 8;
-        if (VEC) {
-            const float4 a0 = *reinterpret_cast<const float4*>(src);
-            const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
-            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = src[i];
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-
-    const float d = div_rn(amax, 127.0f);
-    const float id = amax != 0.0f ? div_rn(127.0f, amax) : 0.0f;
+    load8<VEC>(x + m * x_stride + b * QK + part * 8, valid, v);
     int q[8];
-    int qsum = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float r = __builtin_rintf(v[i] * id);
-        int iv = (int)r;
-        iv = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
-        q[i] = iv;
-        qsum += iv;
-    }
-    if (MODE == OUT_ACT) {
-        qsum += __shfl_xor(qsum, 1, 64);
-        qsum += __shfl_xor(qsum, 2, 64);
-    }
+    uint16_t dh;
+    int qsum;
+    quant8_block(v, q, dh, qsum);
     if (!valid) return;
 
-    const uint16_t dh = f2h(d);
     if (MODE == OUT_BLOCKS) {
         uint8_t* blkp = y + (m * nb + b) * Q8_BYTES;
         if (part == 0) *reinterpret_cast<uint16_t*>(blkp) = dh;
@@ -81,21 +50,6 @@ __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             qp[i] = (uint16_t)((q[2 * i] & 0xff) | ((q[2 * i + 1] & 0xff) << 8));
-    } else if (MODE == OUT_ACT) {
-        uint8_t* row = y + m * y_stride;
-        const int64_t g = b >> 3, bi = b & 7;
-        uint8_t* gp = row + g * ACT_GS;
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo |= (uint32_t)(q[i] & 0xff) << (8 * i);
-            hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
-        }
-        *reinterpret_cast<uint2*>(gp + ACT_QS_OFF + bi * QK + part * 8) = make_uint2(lo, hi);
-        if (part == 0) {
-            reinterpret_cast<float*>(gp + ACT_D_OFF)[bi] = h2f(dh);
-            reinterpret_cast<int*>(gp + ACT_S_OFF)[bi] = qsum;
-        }
     } else {  // OUT_F16: fp16(d * q), the GEMM's A operand
         const float df = h2f(dh);
         uint16_t hv[8];
@@ -129,11 +83,6 @@ static int launch_quant(const float* x, int64_t nrows, int64_t K, int64_t x_stri
 int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
                          hipStream_t s) {
     return launch_quant<OUT_BLOCKS>(x, nrows, K, x_stride, y, 0, s);
-}
-
-int quantize_q8_0_act(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* act,
-                      int64_t act_stride_bytes, hipStream_t s) {
-    return launch_quant<OUT_ACT>(x, nrows, K, x_stride, act, act_stride_bytes, s);
 }
 
 int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,

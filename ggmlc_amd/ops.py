@@ -30,6 +30,7 @@ from ._lib import BLOCK_BYTES, F16, F32, I32, I64, Q4_0, Q8_0, check, make_tenso
 __all__ = [
     "QWeight", "Q8_0", "Q4_0", "quantize_row_q8_0", "quantize_weights", "mul_mat",
     "set_rows", "flash_attn_ext", "soft_max_ext", "Workspace",
+    "swiglu", "rms_norm", "rope_ext", "add", "get_rows", "argmax",
 ]
 
 _TORCH_TO_GQ = {torch.float32: F32, torch.float16: F16, torch.int64: I64, torch.int32: I32}
@@ -176,4 +177,65 @@ def soft_max_ext(x: torch.Tensor, mask: torch.Tensor | None = None, scale: float
     L = _lib.load()
     md = _desc(mask) if mask is not None else None
     check(L.gq_soft_max(_desc(x), md, scale, max_bias, _desc(out), _stream()))
+    return out
+
+
+# ---------------------------------------------------------------- decoder ops
+
+def swiglu(a: torch.Tensor, b: torch.Tensor | None = None, swapped: bool = False,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_swiglu(a): silu(a[..., :n]) * a[..., n:] (or ggml_swiglu_split(a, b))."""
+    nc = a.shape[-1] if b is not None else a.shape[-1] // 2
+    if out is None:
+        out = torch.empty(a.shape[:-1] + (nc,), dtype=torch.float32, device=a.device)
+    bd = _desc(b) if b is not None else None
+    check(_lib.load().gq_swiglu(_desc(a), bd, _desc(out), int(swapped), _stream()))
+    return out
+
+
+def rms_norm(x: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_rms_norm(x, eps) over the last dim."""
+    if out is None:
+        out = torch.empty_like(x)
+    check(_lib.load().gq_rms_norm(_desc(x), eps, _desc(out), _stream()))
+    return out
+
+
+def rope_ext(x: torch.Tensor, pos: torch.Tensor, n_dims: int, mode: int = 2, freq_base: float = 10000.0,
+             freq_scale: float = 1.0, attn_factor: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_rope_ext: x fp32 ``[B, seq, heads, hd]`` (ggml [hd, heads, seq, B]), pos int32 ``[seq]``."""
+    if out is None:
+        out = torch.empty_like(x)
+    check(_lib.load().gq_rope_ext(_desc(x), _desc(pos), n_dims, mode, 0, freq_base, freq_scale, 0.0,
+                                  attn_factor, 0.0, 0.0, _desc(out), _stream()))
+    return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_add(a, b) with b repeated over a."""
+    if out is None:
+        out = torch.empty_like(a)
+    check(_lib.load().gq_add(_desc(a), _desc(b), _desc(out), _stream()))
+    return out
+
+
+def get_rows(table, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_get_rows(table, ids): table is a QWeight (rows of K) or an fp32/fp16 [rows, K] tensor."""
+    if isinstance(table, QWeight):
+        td, K = table.desc(), table.K
+        dev = table.data.device
+    else:
+        td, K = _desc(table), table.shape[-1]
+        dev = table.device
+    if out is None:
+        out = torch.empty((ids.shape[0], K), dtype=torch.float32, device=dev)
+    check(_lib.load().gq_get_rows(td, _desc(ids), _desc(out), _stream()))
+    return out
+
+
+def argmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_argmax over the last dim of a 2-d fp32 tensor -> int32 [rows]."""
+    if out is None:
+        out = torch.empty((x.shape[0],), dtype=torch.int32, device=x.device)
+    check(_lib.load().gq_argmax(_desc(x), _desc(out), _stream()))
     return out

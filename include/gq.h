@@ -144,6 +144,45 @@ int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v
 int gq_soft_max(const gq_tensor* a, const gq_tensor* mask, float scale, float max_bias,
                 gq_tensor* dst, gq_stream_t stream);
 
+/* ---- decoder ops around the quantized path -------------------------------
+ * The remaining nodes of a LLaMA-style layer as the executor emits them
+ * (runtime/src/executor.cpp:2034-2090, 2355-2357, 2742-2756). F32 activations;
+ * rows (dim 0) contiguous; all other dims may be strided. */
+
+/* ggml_swiglu(a) / ggml_swiglu_swapped(a) (ggml.c:3048-3058; CPU ops.cpp:3246):
+ * per row, y = silu(a[0:nc]) * a[nc:2nc] (halves exchanged when swapped). With
+ * b != NULL it is ggml_swiglu_split(a, b): y = silu(a) * b. dst ne = [nc, rows]. */
+int gq_swiglu(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, int swapped, gq_stream_t stream);
+
+/* ggml_rms_norm(a, eps) (CPU ops.cpp rms_norm_f32): y = x / sqrt(mean(x^2) + eps) per row. */
+int gq_rms_norm(const gq_tensor* a, float eps, gq_tensor* dst, gq_stream_t stream);
+
+/* ggml_rope_ext(a, pos, NULL, n_dims, mode, n_ctx_orig, freq_base, freq_scale,
+ * ext_factor, attn_factor, beta_fast, beta_slow) (ggml.c; CPU ops.cpp:5886-6120)
+ * for mode 0 (NORMAL) and 2 (NEOX) with ext_factor == 0 (no YaRN ramp; n_ctx_orig
+ * and the betas only enter through it). a F32 ne = [hd, heads, seq, B],
+ * pos I32 [seq]. */
+int gq_rope_ext(const gq_tensor* a, const gq_tensor* pos, int n_dims, int mode, int n_ctx_orig, float freq_base,
+                float freq_scale, float ext_factor, float attn_factor, float beta_fast, float beta_slow,
+                gq_tensor* dst, gq_stream_t stream);
+
+/* ggml_add(a, b) with b repeated over a (ggml_can_repeat). */
+int gq_add(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream);
+
+/* ggml_get_rows(a, b): a (Q8_0, Q4_0, F16 or F32) ne = [n_embd, rows], b I32/I64 [n]
+ * -> dst F32 [n_embd, n]. Out-of-range ids give zero rows. */
+int gq_get_rows(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream);
+
+/* ggml_argmax(a): first index of the row maximum, dst I32 [rows]. */
+int gq_argmax(const gq_tensor* a, gq_tensor* dst, gq_stream_t stream);
+
+/* ---- measurement aid ------------------------------------------------------
+ * No counterpart in the reference. Reads `bytes` (16-byte aligned) once with
+ * the coalesced 16-byte streaming loads the GEMV uses, so a benchmark can
+ * report the read bandwidth the device sustains beside the datasheet peak.
+ * `sink` is a device uint32 that is (practically) never written. */
+int gq_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, gq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

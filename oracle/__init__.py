@@ -97,6 +97,18 @@ def ref():
         L.ref_flash_attn_ext_f16.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
                                              _vp, _f32, _vp, _i32]
         L.ref_soft_max_f32.argtypes = [_vp, _i64, _i64, _vp, _f32, _vp, _i32]
+        L.ref_mm_create.restype = _vp
+        L.ref_mm_create.argtypes = [_i32, _vp, _i64, _i64, _i64]
+        L.ref_mlp_create.restype = _vp
+        L.ref_mlp_create.argtypes = [_i32, _vp, _vp, _i64, _i64, _i64]
+        L.ref_graph_run.argtypes = [_vp, _vp, _vp, _i32]
+        L.ref_graph_free.argtypes = [_vp]
+        L.ref_graph_free.restype = None
+        L.ref_swiglu.argtypes = [_vp, _i64, _i64, _vp]
+        L.ref_rms_norm.argtypes = [_vp, _i64, _i64, _f32, _vp]
+        L.ref_rope.argtypes = [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _f32, _vp]
+        L.ref_get_rows.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp]
+        L.ref_argmax.argtypes = [_vp, _i64, _i64, _vp]
         L.ref_init()
         _ref = L
     return _ref
@@ -228,3 +240,93 @@ def n_cpu_threads() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         return os.cpu_count() or 1
+
+
+class RefGraph:
+    """A persistent one-input graph on the reference ggml CPU backend (timing only)."""
+
+    def __init__(self, handle, x_shape, y_shape, keep):
+        self.h = handle
+        self.x_shape = x_shape
+        self.y_shape = y_shape
+        self._keep = keep  # weight buffers referenced until creation copied them
+
+    def run(self, x: np.ndarray, n_threads: int) -> np.ndarray:
+        x = _c(x, np.float32)
+        y = np.empty(self.y_shape, np.float32)
+        if ref().ref_graph_run(self.h, _ptr(x), _ptr(y), n_threads) != 0:
+            raise RuntimeError("ref graph run failed")
+        return y
+
+    def close(self):
+        if self.h:
+            ref().ref_graph_free(self.h)
+            self.h = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def ref_mm_graph(wq: np.ndarray, wtype: int, K: int, M: int) -> RefGraph:
+    wq = _c(wq, np.uint8)
+    N = wq.size // (K // 32 * BLOCK_BYTES[wtype])
+    h = ref().ref_mm_create(wtype, _ptr(wq), K, N, M)
+    if not h:
+        raise RuntimeError("ref_mm_create failed")
+    return RefGraph(h, (M, K), (M, N), None)
+
+
+def ref_mlp_graph(w_gate_up: np.ndarray, w_down: np.ndarray, wtype: int, K: int, F: int, M: int) -> RefGraph:
+    a = _c(w_gate_up, np.uint8)
+    b = _c(w_down, np.uint8)
+    h = ref().ref_mlp_create(wtype, _ptr(a), _ptr(b), K, F, M)
+    if not h:
+        raise RuntimeError("ref_mlp_create failed")
+    return RefGraph(h, (M, K), (M, K), None)
+
+
+def ref_swiglu(a) -> np.ndarray:
+    a = _c(a, np.float32)
+    nrows, n2 = a.shape
+    y = np.empty((nrows, n2 // 2), np.float32)
+    ref().ref_swiglu(_ptr(a), n2 // 2, nrows, _ptr(y))
+    return y
+
+
+def ref_rms_norm(x, eps: float) -> np.ndarray:
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    ref().ref_rms_norm(_ptr(x), x.shape[-1], x.size // x.shape[-1], eps, _ptr(y))
+    return y
+
+
+def ref_rope(x, pos, n_dims: int, mode: int = 2, freq_base: float = 10000.0) -> np.ndarray:
+    """x fp32 [seq, heads, hd] (ggml [hd, heads, seq]), pos int32 [seq]."""
+    x = _c(x, np.float32)
+    p = _c(pos, np.int32)
+    seq, heads, hd = x.shape
+    y = np.empty_like(x)
+    ref().ref_rope(_ptr(x), hd, heads, seq, _ptr(p), n_dims, mode, freq_base, _ptr(y))
+    return y
+
+
+def ref_get_rows(table: np.ndarray, wtype: int, n_embd: int, ids) -> np.ndarray:
+    t = _c(table, np.uint8 if wtype in BLOCK_BYTES else (np.float16 if wtype == 1 else np.float32))
+    ids = _c(ids, np.int32)
+    if wtype in BLOCK_BYTES:
+        rows = t.size // (n_embd // 32 * BLOCK_BYTES[wtype])
+    else:
+        rows = t.size // n_embd
+    y = np.empty((ids.size, n_embd), np.float32)
+    ref().ref_get_rows(wtype, _ptr(t), n_embd, rows, _ptr(ids), ids.size, _ptr(y))
+    return y
+
+
+def ref_argmax(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape[0], np.int32)
+    ref().ref_argmax(_ptr(x), x.shape[1], x.shape[0], _ptr(out))
+    return out

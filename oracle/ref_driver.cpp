@@ -155,4 +155,145 @@ int ref_soft_max_f32(const float* x, int64_t ncols, int64_t nrows, const uint16_
     return 0;
 }
 
+// ---- persistent graphs for timing the CPU baseline --------------------------
+// The weights are copied into the ggml context once; ref_graph_run only copies
+// the activation in, runs ggml_graph_compute_with_ctx and copies the result out.
+
+struct RefGraph {
+    ggml_context* ctx = nullptr;
+    ggml_cgraph* gf = nullptr;
+    ggml_tensor* x = nullptr;
+    ggml_tensor* y = nullptr;
+};
+
+static RefGraph* new_graph(size_t bytes) {
+    RefGraph* g = new RefGraph;
+    ggml_init_params p = {bytes + 256 * 1024 * 1024, nullptr, false};
+    g->ctx = ggml_init(p);
+    if (!g->ctx) {
+        delete g;
+        return nullptr;
+    }
+    return g;
+}
+
+// y[M][N] = W x (the decode GEMV / prefill GEMM node alone)
+void* ref_mm_create(int wtype, const void* w, int64_t K, int64_t N, int64_t M) {
+    ggml_cpu_init();
+    const ggml_type t = (ggml_type)wtype;
+    const size_t wbytes = ggml_row_size(t, K) * (size_t)N;
+    RefGraph* g = new_graph(wbytes + sizeof(float) * (K + N) * M * 2);
+    if (!g) return nullptr;
+    ggml_tensor* W = ggml_new_tensor_2d(g->ctx, t, K, N);
+    memcpy(W->data, w, wbytes);
+    g->x = ggml_new_tensor_2d(g->ctx, GGML_TYPE_F32, K, M);
+    g->y = ggml_mul_mat(g->ctx, W, g->x);
+    g->gf = ggml_new_graph(g->ctx);
+    ggml_build_forward_expand(g->gf, g->y);
+    return g;
+}
+
+// LLaMA MLP block as ggmlc's fused graph runs it (fusion.py:1224-1546 concatenates
+// [W_gate; W_up]): y = W_down . swiglu(W_gate_up . x)   (MUL_MAT -> GLU -> MUL_MAT)
+void* ref_mlp_create(int wtype, const void* w_gate_up, const void* w_down, int64_t K, int64_t F, int64_t M) {
+    ggml_cpu_init();
+    const ggml_type t = (ggml_type)wtype;
+    const size_t b1 = ggml_row_size(t, K) * (size_t)(2 * F);
+    const size_t b2 = ggml_row_size(t, F) * (size_t)K;
+    RefGraph* g = new_graph(b1 + b2 + sizeof(float) * (K + 3 * F + K) * M * 2);
+    if (!g) return nullptr;
+    ggml_tensor* Wgu = ggml_new_tensor_2d(g->ctx, t, K, 2 * F);
+    ggml_tensor* Wd = ggml_new_tensor_2d(g->ctx, t, F, K);
+    memcpy(Wgu->data, w_gate_up, b1);
+    memcpy(Wd->data, w_down, b2);
+    g->x = ggml_new_tensor_2d(g->ctx, GGML_TYPE_F32, K, M);
+    ggml_tensor* h = ggml_mul_mat(g->ctx, Wgu, g->x);
+    ggml_tensor* a = ggml_swiglu(g->ctx, h);
+    g->y = ggml_mul_mat(g->ctx, Wd, a);
+    g->gf = ggml_new_graph(g->ctx);
+    ggml_build_forward_expand(g->gf, g->y);
+    return g;
+}
+
+int ref_graph_run(void* h, const float* x, float* y, int n_threads) {
+    RefGraph* g = (RefGraph*)h;
+    memcpy(g->x->data, x, ggml_nbytes(g->x));
+    if (ggml_graph_compute_with_ctx(g->ctx, g->gf, n_threads) != GGML_STATUS_SUCCESS) return -1;
+    if (y) memcpy(y, g->y->data, ggml_nbytes(g->y));
+    return 0;
+}
+
+void ref_graph_free(void* h) {
+    RefGraph* g = (RefGraph*)h;
+    if (!g) return;
+    ggml_free(g->ctx);
+    delete g;
+}
+
+// ---- decoder ops (one node each, executor.cpp:2034-2090, 2742-2756) -----------
+
+int ref_swiglu(const float* a, int64_t nc, int64_t nrows, float* y) {
+    ggml_cpu_init();
+    Ctx c(sizeof(float) * nc * nrows * 3);
+    ggml_tensor* A = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F32, 2 * nc, nrows);
+    memcpy(A->data, a, sizeof(float) * 2 * nc * nrows);
+    ggml_tensor* Y = ggml_swiglu(c.ctx, A);
+    if (run_graph(c.ctx, Y, 1) != 0) return -1;
+    memcpy(y, Y->data, sizeof(float) * nc * nrows);
+    return 0;
+}
+
+int ref_rms_norm(const float* x, int64_t n, int64_t nrows, float eps, float* y) {
+    ggml_cpu_init();
+    Ctx c(sizeof(float) * n * nrows * 2);
+    ggml_tensor* X = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F32, n, nrows);
+    memcpy(X->data, x, sizeof(float) * n * nrows);
+    ggml_tensor* Y = ggml_rms_norm(c.ctx, X, eps);
+    if (run_graph(c.ctx, Y, 1) != 0) return -1;
+    memcpy(y, Y->data, sizeof(float) * n * nrows);
+    return 0;
+}
+
+// x [hd, heads, seq] F32, pos I32 [seq]
+int ref_rope(const float* x, int64_t hd, int64_t heads, int64_t seq, const int32_t* pos, int n_dims, int mode,
+             float freq_base, float* y) {
+    ggml_cpu_init();
+    Ctx c(sizeof(float) * hd * heads * seq * 2 + sizeof(int32_t) * seq);
+    ggml_tensor* X = ggml_new_tensor_3d(c.ctx, GGML_TYPE_F32, hd, heads, seq);
+    ggml_tensor* P = ggml_new_tensor_1d(c.ctx, GGML_TYPE_I32, seq);
+    memcpy(X->data, x, sizeof(float) * hd * heads * seq);
+    memcpy(P->data, pos, sizeof(int32_t) * seq);
+    ggml_tensor* Y = ggml_rope_ext(c.ctx, X, P, nullptr, n_dims, mode, 0, freq_base, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f);
+    if (run_graph(c.ctx, Y, 1) != 0) return -1;
+    memcpy(y, Y->data, sizeof(float) * hd * heads * seq);
+    return 0;
+}
+
+// table [n_embd, rows] of type wtype, ids I32 [n] -> y F32 [n_embd, n]
+int ref_get_rows(int wtype, const void* table, int64_t n_embd, int64_t rows, const int32_t* ids, int64_t n, float* y) {
+    ggml_cpu_init();
+    const ggml_type t = (ggml_type)wtype;
+    const size_t tb = ggml_row_size(t, n_embd) * (size_t)rows;
+    Ctx c(tb + sizeof(float) * n_embd * n + sizeof(int32_t) * n);
+    ggml_tensor* T = ggml_new_tensor_2d(c.ctx, t, n_embd, rows);
+    ggml_tensor* I = ggml_new_tensor_1d(c.ctx, GGML_TYPE_I32, n);
+    memcpy(T->data, table, tb);
+    memcpy(I->data, ids, sizeof(int32_t) * n);
+    ggml_tensor* Y = ggml_get_rows(c.ctx, T, I);
+    if (run_graph(c.ctx, Y, 1) != 0) return -1;
+    memcpy(y, Y->data, sizeof(float) * n_embd * n);
+    return 0;
+}
+
+int ref_argmax(const float* x, int64_t n, int64_t nrows, int32_t* out) {
+    ggml_cpu_init();
+    Ctx c(sizeof(float) * n * nrows + sizeof(int32_t) * nrows);
+    ggml_tensor* X = ggml_new_tensor_2d(c.ctx, GGML_TYPE_F32, n, nrows);
+    memcpy(X->data, x, sizeof(float) * n * nrows);
+    ggml_tensor* Y = ggml_argmax(c.ctx, X);
+    if (run_graph(c.ctx, Y, 1) != 0) return -1;
+    memcpy(out, Y->data, sizeof(int32_t) * nrows);
+    return 0;
+}
+
 }  // extern "C"

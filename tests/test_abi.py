@@ -58,9 +58,13 @@ def test_mul_mat_rejects_bad_shapes_without_device(lib):
     w_f32 = _t(_lib.F32, [4096, 64], [4, 16384])
     x = _t(_lib.F32, [4096, 1], [4, 16384])
     assert lib.gq_mul_mat(w_f32, x, d, None, 0, None) == -2
-    # workspace too small is reported before any launch
-    assert lib.gq_mul_mat_workspace_size(w, x) > 0
-    assert lib.gq_mul_mat(w, x, d, None, 0, None) == -3
+    # decode (M <= 4) needs no workspace; prefill does, and a missing one is
+    # reported before any launch
+    assert lib.gq_mul_mat_workspace_size(w, x) == 0
+    x64 = _t(_lib.F32, [4096, 64], [4, 16384])
+    d64 = _t(_lib.F32, [64, 64], [4, 256])
+    assert lib.gq_mul_mat_workspace_size(w, x64) >= 64 * 4096 * 2
+    assert lib.gq_mul_mat(w, x64, d64, None, 0, None) == -3
     # K not a multiple of 32
     w33 = _t(_lib.Q8_0, [33, 4], [34, 34])
     assert lib.gq_mul_mat(w33, _t(_lib.F32, [33, 1], [4, 132]), _t(_lib.F32, [4, 1], [4, 16]), None, 0, None) == -1
