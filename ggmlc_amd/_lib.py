@@ -60,6 +60,8 @@ SIGNATURES = {
     "gq_add": (ctypes.c_int, [_P, _P, _P, _vp]),
     "gq_get_rows": (ctypes.c_int, [_P, _P, _P, _vp]),
     "gq_argmax": (ctypes.c_int, [_P, _P, _vp]),
+    "gq_kv_step_inputs": (ctypes.c_int, [_vp, _i64, _vp, _vp, _P, _vp]),
+    "gq_kv_advance": (ctypes.c_int, [_vp, _i64, _vp]),
     "gq_probe_stream_read": (ctypes.c_int, [_vp, ctypes.c_size_t, _vp, _vp]),
 }
 

@@ -397,6 +397,28 @@ int gq_argmax(const gq_tensor* a, gq_tensor* dst, gq_stream_t stream) {
                   static_cast<int32_t*>(dst->data), (hipStream_t)stream);
 }
 
+// ---- persistent-KV step inputs ------------------------------------------------
+
+int gq_kv_step_inputs(const int32_t* pos, int64_t s, int32_t* pos_ids, int64_t* kv_idx, gq_tensor* mask,
+                      gq_stream_t stream) {
+    if (!pos || s <= 0) return fail(GQ_ERR_INVALID, "kv_step_inputs: needs a device position and s > 0");
+    uint16_t* m = nullptr;
+    int64_t n_kv = 0, ms = 0;
+    if (mask) {
+        if (mask->type != GQ_TYPE_F16 || mask->nb[0] != 2 || mask->ne[1] < s || mask->nb[1] % 2)
+            return fail(GQ_ERR_INVALID, "kv_step_inputs: mask must be F16 [n_kv, >= s]: " + shape(mask));
+        m = static_cast<uint16_t*>(mask->data);
+        n_kv = mask->ne[0];
+        ms = (int64_t)(mask->nb[1] / 2);
+    }
+    return kv_step_inputs(pos, s, pos_ids, kv_idx, m, n_kv, ms, (hipStream_t)stream);
+}
+
+int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream) {
+    if (!pos) return fail(GQ_ERR_INVALID, "kv_advance: null position");
+    return kv_advance(pos, s, (hipStream_t)stream);
+}
+
 // ---- measurement aid ------------------------------------------------------
 
 int gq_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, gq_stream_t stream) {

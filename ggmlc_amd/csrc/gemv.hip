@@ -108,7 +108,7 @@ __device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, con
     }
 }
 
-template <int QT, int M, bool XVEC, int PF>
+template <int QT, int M, bool XVEC, int PF, int KS>
 __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__ W, int64_t N,
                                                      int64_t row_bytes, int G,
                                                      const float* __restrict__ x,
@@ -116,9 +116,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                                                      int64_t ldd) {
     constexpr int GB = QTraits<QT>::GB;
     constexpr int CPG = QTraits<QT>::CPG;
-    constexpr int SEG = LPR * CPG;  // chunks of one row per iteration
-    constexpr int XPMAX = 2;        // activation passes held in registers
+    constexpr int SEG = LPR * CPG;       // chunks of one row per step
+    constexpr int XPMAX = 2;             // activation passes held in registers
+    constexpr int RG = WAVES / KS;       // row groups (of RPW rows) per workgroup tile
+    constexpr int ROWS = RG * RPW;       // rows per workgroup tile
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float red[WAVES][M][RPW];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -128,19 +131,25 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
 
     const int rsub = lane / LPR;
     const int gsub = lane % LPR;
-    const int J = (G + LPR - 1) / LPR;
     const int nb = G * 8;
-    const int XP = (nb * 4 + 255) / 256;  // quantizer passes per activation row
+    const int XP = (nb * 4 + 255) / 256;
 
-    // persistent waves: wave-tile t = RPW rows, tiles gw, gw + total, ...; the
-    // (tile, K-iteration) sequence of a wave is one flat pipeline
-    const int64_t n_tiles = (N + RPW - 1) / RPW;
-    const int64_t total = (int64_t)gridDim.x * WAVES;
-    const int64_t gw = (int64_t)blockIdx.x * WAVES + wave;
-    const int64_t my_tiles = gw < n_tiles ? (n_tiles - gw + total - 1) / total : 0;
-    const int64_t F = my_tiles * J;
+    // wave -> (row group, K part); K parts are whole steps of LPR groups so every
+    // step stays a full 64-group slice (a part may be empty: it then runs one
+    // masked step so that all waves meet the same reduction barriers)
+    const int rg = wave / KS;
+    const int kp = wave % KS;
+    const int J = (G + LPR - 1) / LPR;
+    const int SP = (J + KS - 1) / KS;  // steps per part
+    const int g_begin = min(G, kp * SP * LPR);
+    const int g_end = min(G, (kp + 1) * SP * LPR);
+    const int S = max(1, (g_end - g_begin + LPR - 1) / LPR);  // steps per tile for this wave
 
-    // 1) activation loads first (they are needed first), into registers when small
+    // persistent workgroups over workgroup tiles; one flat (tile, step) pipeline per wave
+    const int64_t n_wgt = (N + ROWS - 1) / ROWS;
+    const int64_t my_wgt = blockIdx.x < n_wgt ? (n_wgt - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    const int64_t F = my_wgt * S;
+
     float xr[XPMAX][8];
     const bool xpre = M * XP <= XPMAX;
     if (xpre) {
@@ -154,20 +163,21 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2) weight loads for the first PF steps (coalesced 16-byte chunks)
     uint4 pre[PF][CPG];
     auto load_step = [&](int64_t f, uint4(&dstv)[CPG]) {
-        const int64_t tile = gw + (f / J) * total;
-        const int j = (int)(f % J);
-        const int64_t row0 = tile * RPW;
+        const int64_t t = (int64_t)blockIdx.x + (f / S) * gridDim.x;
+        const int j = (int)(f % S);
+        const int64_t row0 = t * ROWS + rg * RPW;
+        const int gfirst = g_begin + j * LPR;             // first group of this step
+        const int ngr = min(LPR, g_end - gfirst);          // groups of this step
 #pragma unroll
         for (int c = 0; c < CPG; ++c) {
             const int ci = lane + 64 * c;
             const int r = ci / SEG;
             const int within = ci - r * SEG;
             const int64_t rr = row0 + r;
-            const int64_t boff = (int64_t)j * (LPR * GB) + (int64_t)within * 16;
-            const bool ok = rr < N && boff < row_bytes;
+            const bool ok = rr < N && within < ngr * CPG;
+            const int64_t boff = (int64_t)gfirst * GB + (int64_t)within * 16;
             // always-valid address, zeroed after the load: no branch per chunk
             uint4 v = ld_nt16(W + (ok ? rr * row_bytes + boff : 0));
             if (!ok) v = make_uint4(0, 0, 0, 0);
@@ -179,7 +189,6 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         if (s < F) load_step(s, pre[s]);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3) quantize the activation into LDS while the weights are in flight
     if (xpre) {
 #pragma unroll
         for (int p = 0; p < XPMAX; ++p) {
@@ -217,9 +226,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
 
     for (int64_t f = 0; f < F; ++f) {
-        const int64_t tile = gw + (f / J) * total;
-        const int j = (int)(f % J);
-        const int64_t row = tile * RPW + rsub;
+        const int64_t t = (int64_t)blockIdx.x + (f / S) * gridDim.x;
+        const int j = (int)(f % S);
+        const int64_t row = t * ROWS + rg * RPW + rsub;
 #pragma unroll
         for (int c = 0; c < CPG; ++c) *reinterpret_cast<uint4*>(s_stage + (lane + 64 * c) * 16) = pre[0][c];
         wave_lds_sync();
@@ -229,8 +238,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
 #pragma unroll
             for (int c = 0; c < CPG; ++c) pre[s][c] = pre[s + 1][c];
         if (f + PF < F) load_step(f + PF, pre[PF - 1]);
-        const int g = j * LPR + gsub;
-        const bool live = row < N && g < G;
+        const int g = g_begin + j * LPR + gsub;
+        const bool live = row < N && g < g_end;
         // decode the group in two windows of HC chunks (blocks 0-3, then 4-7)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -239,11 +248,11 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             uint32_t w[4 * HC];
 #pragma unroll
             for (int c = 0; c < HC; ++c) {
-                const uint4 t = *reinterpret_cast<const uint4*>(s_stage + lane * GB + 16 * (c0 + c));
-                w[4 * c + 0] = t.x;
-                w[4 * c + 1] = t.y;
-                w[4 * c + 2] = t.z;
-                w[4 * c + 3] = t.w;
+                const uint4 tt = *reinterpret_cast<const uint4*>(s_stage + gsub * GB + rsub * (LPR * GB) + 16 * (c0 + c));
+                w[4 * c + 0] = tt.x;
+                w[4 * c + 1] = tt.y;
+                w[4 * c + 2] = tt.z;
+                w[4 * c + 3] = tt.w;
             }
             if (!live) continue;
 #pragma unroll
@@ -259,18 +268,35 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                     const uint4 a0 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b);
                     const uint4 a1 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b + 16);
                     const float da = reinterpret_cast<const float*>(ag + ACT_D_OFF)[b];
-                    const int s = block_dot<QT>(q, a0, a1, ag, b);
-                    acc[m] += (float)s * (dw * da);
+                    const int sdot = block_dot<QT>(q, a0, a1, ag, b);
+                    acc[m] += (float)sdot * (dw * da);
                 }
             }
         }
         wave_lds_sync();  // this step's staging slice is fully read before it is refilled
-        if (j == J - 1) {  // tile finished: reduce the 16 lanes of each row and store
+        if (j == S - 1) {  // tile finished: reduce the 16 lanes of each row, then the K parts
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 const float v = xor_sum<LPR>(acc[m]);
-                if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
                 acc[m] = 0.0f;
+                if constexpr (KS == 1) {
+                    if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
+                } else {
+                    if (gsub == 0) red[wave][m][rsub] = v;
+                }
+            }
+            if constexpr (KS > 1) {
+                __syncthreads();
+                if (kp == 0 && gsub == 0 && row < N) {
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        float v = red[wave][m][rsub];
+#pragma unroll
+                        for (int k = 1; k < KS; ++k) v += red[wave + k][m][rsub];
+                        dst[(int64_t)m * ldd + row] = v;
+                    }
+                }
+                __syncthreads();
             }
         }
     }
@@ -431,13 +457,15 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
 
 constexpr size_t LDS_MAX = 160 * 1024;
 
+// dynamic LDS above 64 KiB must be allowed per kernel; `allowed` remembers the
+// largest size granted so far (the attribute excludes the kernel's static LDS)
 template <typename KFn>
-int allow_big_lds(KFn* fn, bool& done) {
-    if (done) return GQ_OK;
+int allow_big_lds(KFn* fn, size_t& allowed, size_t need) {
+    if (need <= allowed || need <= 64 * 1024) return GQ_OK;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_MAX);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)need);
     if (e != hipSuccess) return check_hip(e, "gemv: set LDS attribute");
-    done = true;
+    allowed = need;
     return GQ_OK;
 }
 
@@ -483,6 +511,21 @@ int gemv_variant() {
     return v;
 }
 
+template <int QT, int M, bool XVEC, int PF, int KS>
+int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+                  float* dst, int64_t ldd, hipStream_t s, size_t lds, int resident) {
+    const int G = (int)(K / 256);
+    const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
+    auto* fn = &k_gemv_grp<QT, M, XVEC, PF, KS>;
+    static size_t allowed = 0;
+    int rc = allow_big_lds(fn, allowed, lds);
+    if (rc) return rc;
+    const int64_t tiles = cdiv(N, (WAVES / KS) * RPW);
+    const dim3 grid((unsigned)(tiles < resident ? tiles : resident));
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, x, x_stride, dst, ldd);
+    return check_hip(hipGetLastError(), "gemv launch");
+}
+
 template <int QT, int M, bool XVEC, int PF>
 int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
                   float* dst, int64_t ldd, hipStream_t s) {
@@ -492,15 +535,29 @@ int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_
     const bool direct = variant != 0;
     const size_t lds = (size_t)M * G * ACT_GS + (direct ? 0 : (size_t)WAVES * 64 * QTraits<QT>::GB);
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
-    decltype(&k_gemv_grp<QT, M, XVEC, PF>) fn;
+    if (!direct) {
+        // residency is the same for every KS (same registers and LDS)
+        int resident = 0;
+        int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1>, lds, resident);
+        if (rc) return rc;
+        // split K over the waves of a workgroup (whole steps per wave) only when
+        // the row tiles leave most CUs without a workgroup (measured: splitting a
+        // 4096-row down projection is slower, a 1536-row one faster)
+        const int64_t t1 = cdiv(N, WAVES * RPW);
+        const int J = (G + LPR - 1) / LPR;
+        if (4 * t1 >= resident || J < 2)
+            return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, x, x_stride, dst, ldd, s, lds, resident);
+        if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, x, x_stride, dst, ldd, s, lds, resident);
+        return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, x, x_stride, dst, ldd, s, lds, resident);
+    }
+    decltype(&k_gemv_dir<QT, M, XVEC, 1, true>) fn;
     switch (variant) {
-        case 1: fn = &k_gemv_dir<QT, M, XVEC, 1, true>; break;
         case 2: fn = &k_gemv_dir<QT, M, XVEC, 1, false>; break;
         case 3: fn = &k_gemv_dir<QT, M, XVEC, 2, true>; break;
-        default: fn = &k_gemv_grp<QT, M, XVEC, PF>; break;
+        default: fn = &k_gemv_dir<QT, M, XVEC, 1, true>; break;
     }
-    static bool attr[4] = {false, false, false, false};
-    int rc = allow_big_lds(fn, attr[variant]);
+    static size_t allowed[4] = {0, 0, 0, 0};
+    int rc = allow_big_lds(fn, allowed[variant], lds);
     if (rc) return rc;
     int resident = 0;
     rc = resident_wgs(fn, lds, resident);
@@ -529,8 +586,8 @@ int launch_blk(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x
     const int64_t row_bytes = (int64_t)nb * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
     const size_t lds = (size_t)M * act_row_bytes(K);
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
-    static bool attr = false;
-    int rc = allow_big_lds(&k_gemv_blk<QT, M, XVEC>, attr);
+    static size_t allowed = 0;
+    int rc = allow_big_lds(&k_gemv_blk<QT, M, XVEC>, allowed, lds);
     if (rc) return rc;
     const dim3 grid((unsigned)cdiv(N, 256 / LPR));
     hipLaunchKernelGGL((k_gemv_blk<QT, M, XVEC>), grid, dim3(256), lds, s, W, N, row_bytes, nb, x,

@@ -82,6 +82,11 @@ int get_rows(const uint8_t* a, int atype, int64_t ne0, int64_t anb1, int64_t aro
              int64_t n, float* y, int64_t ynb1, hipStream_t s);
 int argmax(const float* x, int64_t xnb1, int64_t n, int64_t nrows, int32_t* out, hipStream_t s);
 
+// kv_step.hip
+int kv_step_inputs(const int32_t* pos_dev, int64_t s, int32_t* pos_ids, int64_t* kv_idx, uint16_t* mask,
+                   int64_t n_kv, int64_t mask_stride, hipStream_t st);
+int kv_advance(int32_t* pos_dev, int64_t s, hipStream_t st);
+
 // probe.hip
 int read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t s);
 

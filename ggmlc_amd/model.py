@@ -1,0 +1,270 @@
+"""LLaMA-style decoder executed over libgq, the way ggmlc's executor runs it.
+
+Per layer, the graph ggmlc compiles for a LLaMA block (runtime/src/executor.cpp
+:1738-2810 after python/ggmlc/transforms/fusion.py:1224-1546 fuses Q/K/V and
+gate/up and bakes the RMSNorm weight into the following Linear):
+
+    h = RMS_NORM(x) ; qkv = MUL_MAT(Wqkv, h) ; q, k = ROPE_NEOX(q, k)
+    SET_ROWS(Kcache, k), SET_ROWS(Vcache, v)          # persistent KV, rows pos..pos+s-1
+    a = FLASH_ATTN_EXT(q, K[:, :n_kv], V[:, :n_kv], mask[n_kv, s], 1/sqrt(hd))
+    x = x + MUL_MAT(Wo, a)
+    x = x + MUL_MAT(Wdown, SWIGLU(MUL_MAT(Wgate_up, RMS_NORM(x))))
+
+then RMS_NORM -> MUL_MAT(lm_head) on the last token only (logits_last_only,
+executor.cpp:2396-2410) -> ARGMAX for greedy decoding. n_kv follows
+pad_kv_len (executor.cpp:58-64): max(256, roundup(pos + s, 256)) capped at max_ctx.
+
+Every op is one libgq call on device tensors; a whole step (embedding to the
+argmax of the next token, plus pos += s) can be captured as one HIP graph per
+(s, n_kv) bucket and replayed without host work.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import ops
+
+
+@dataclass
+class LlamaConfig:
+    name: str
+    n_layer: int
+    n_embd: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    n_ff: int
+    n_vocab: int
+    qtype: int
+    tied_embeddings: bool = False
+    rms_eps: float = 1e-5
+    rope_base: float = 10000.0
+
+    @property
+    def q_dim(self) -> int:
+        return self.n_head * self.head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_head_kv * self.head_dim
+
+
+# BASELINE.json configs[2] and configs[3]
+SMOLLM2_360M = LlamaConfig("smollm2-360m-shape", 32, 960, 15, 5, 64, 2560, 49152, ops.Q8_0, tied_embeddings=True)
+LLAMA_7B = LlamaConfig("llama-7b-shape", 32, 4096, 32, 32, 128, 11008, 32000, ops.Q4_0)
+# configs[4] (used for its shapes; continuous batching is not built)
+QWEN25_1_5B = LlamaConfig("qwen2.5-1.5b-shape", 28, 1536, 12, 2, 128, 8960, 151936, ops.Q8_0, tied_embeddings=True)
+
+
+def pad_kv_len(n: int, max_ctx: int, n_pad: int = 256) -> int:
+    """executor.cpp:58-64"""
+    n = max(n, 1)
+    if n_pad <= 1:
+        return min(n, max_ctx)
+    return min(max(n_pad, ((n + n_pad - 1) // n_pad) * n_pad), max_ctx)
+
+
+@dataclass
+class LayerWeights:
+    qkv: ops.QWeight
+    o: ops.QWeight
+    gate_up: ops.QWeight
+    down: ops.QWeight
+
+
+@dataclass
+class ModelWeights:
+    cfg: LlamaConfig
+    embed: ops.QWeight
+    lm_head: ops.QWeight
+    layers: list[LayerWeights] = field(default_factory=list)
+
+    @property
+    def nbytes(self) -> int:
+        n = self.embed.nbytes + (0 if self.cfg.tied_embeddings else self.lm_head.nbytes)
+        for L in self.layers:
+            n += L.qkv.nbytes + L.o.nbytes + L.gate_up.nbytes + L.down.nbytes
+        return n
+
+    @property
+    def decode_bytes(self) -> int:
+        """weight bytes one decode token streams (the embedding row is negligible)"""
+        n = self.lm_head.nbytes
+        for L in self.layers:
+            n += L.qkv.nbytes + L.o.nbytes + L.gate_up.nbytes + L.down.nbytes
+        return n
+
+
+def random_weights(cfg: LlamaConfig, device, seed: int = 0, std: float = 0.02) -> ModelWeights:
+    """Random-init weights N(0, std) quantized on the device with ggmlc's quantizer
+    (quantize.py semantics). RMSNorm weights are 1 at init, so the fused graph's
+    baked-in gamma leaves the Linear weights unchanged."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def q(n, k):
+        w = torch.randn((n, k), generator=g, device=device) * std
+        out = ops.quantize_weights(w, cfg.qtype)
+        del w
+        return out
+
+    embed = q(cfg.n_vocab, cfg.n_embd)
+    lm_head = embed if cfg.tied_embeddings else q(cfg.n_vocab, cfg.n_embd)
+    layers = []
+    for _ in range(cfg.n_layer):
+        layers.append(LayerWeights(
+            qkv=q(cfg.q_dim + 2 * cfg.kv_dim, cfg.n_embd),
+            o=q(cfg.n_embd, cfg.q_dim),
+            gate_up=q(2 * cfg.n_ff, cfg.n_embd),
+            down=q(cfg.n_embd, cfg.n_ff),
+        ))
+    return ModelWeights(cfg, embed, lm_head, layers)
+
+
+class Decoder:
+    """Executor for one sequence with a persistent F16 KV cache of max_ctx rows."""
+
+    def __init__(self, w: ModelWeights, max_ctx: int, device, n_pad: int = 256):
+        self.w = w
+        self.cfg = cfg = w.cfg
+        self.dev = device
+        self.max_ctx = max_ctx
+        self.n_pad = n_pad
+        self.k_cache = [torch.zeros((1, cfg.n_head_kv, max_ctx, cfg.head_dim), dtype=torch.float16, device=device)
+                        for _ in range(cfg.n_layer)]
+        self.v_cache = [torch.zeros_like(k) for k in self.k_cache]
+        self.pos = torch.zeros(1, dtype=torch.int32, device=device)  # device-resident position
+        self.ws = ops.Workspace(device)
+        self._bufs: dict[int, dict[str, torch.Tensor]] = {}
+        self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
+
+    # -- state ---------------------------------------------------------------
+    def reset(self, pos: int = 0) -> None:
+        """Rewind the position (the cache rows past it are rewritten before use)."""
+        self.pos.fill_(pos)
+
+    def _buffers(self, s: int) -> dict[str, torch.Tensor]:
+        if s not in self._bufs:
+            c, d = self.cfg, self.dev
+            f32 = dict(dtype=torch.float32, device=d)
+            self._bufs[s] = {
+                "ids": torch.zeros(s, dtype=torch.int32, device=d),
+                "x": torch.empty((s, c.n_embd), **f32),
+                "h": torch.empty((s, c.n_embd), **f32),
+                "qkv": torch.empty((s, c.q_dim + 2 * c.kv_dim), **f32),
+                "q": torch.empty((1, s, c.n_head, c.head_dim), **f32),
+                "k": torch.empty((1, s, c.n_head_kv, c.head_dim), **f32),
+                "attn": torch.empty((s, c.n_head, c.head_dim), **f32),
+                "proj": torch.empty((s, c.n_embd), **f32),
+                "gu": torch.empty((s, 2 * c.n_ff), **f32),
+                "act": torch.empty((s, c.n_ff), **f32),
+                "logits": torch.empty((1, c.n_vocab), **f32),
+                "next": torch.zeros(1, dtype=torch.int32, device=d),
+                "pos_ids": torch.zeros(s, dtype=torch.int32, device=d),
+                "kv_idx": torch.zeros(s, dtype=torch.int64, device=d),
+                "mask": torch.zeros((s, self.max_ctx), dtype=torch.float16, device=d),
+            }
+        return self._bufs[s]
+
+    # -- one step -------------------------------------------------------------
+    def step(self, s: int, n_kv: int, ids: torch.Tensor | None = None, advance: bool = True,
+             trace: list | None = None) -> torch.Tensor:
+        """Run s tokens (ids int32 [s], default: this bucket's ids buffer) at the device
+        position; returns the argmax of the last token's logits (device int32 [1]).
+
+        trace (eager only): receives (name, layer, copy) of every op's output, so a
+        checker can recompute each op from the inputs this step actually used."""
+        c, b, ws = self.cfg, self._buffers(s), self.ws
+
+        def rec(name, li, t):
+            if trace is not None:
+                trace.append((name, li, t.detach().clone()))
+
+        if n_kv > self.max_ctx:
+            raise ValueError("n_kv exceeds the KV cache")
+        ids = b["ids"] if ids is None else ids
+        self.ws.get(self._ws_need(s))
+        mask = b["mask"][:, :n_kv]
+        ops.kv_step_inputs(self.pos, s, b["pos_ids"], b["kv_idx"], mask)
+        x = b["x"]
+        ops.get_rows(self.w.embed, ids, out=x)
+        rec("pos", -1, self.pos)
+        scale = 1.0 / math.sqrt(c.head_dim)
+        qd, kvd = c.q_dim, c.kv_dim
+        for li, L in enumerate(self.w.layers):
+            rec("x_in", li, x)
+            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+            rec("h1", li, h)
+            qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
+            rec("qkv", li, qkv)
+            # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
+            qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
+            kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
+            vv = qkv[:, qd + kvd:].view(1, s, c.n_head_kv, c.head_dim)
+            q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
+            k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
+            # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
+            ops.set_rows(self.k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
+            ops.set_rows(self.v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
+            rec("q", li, q), rec("k", li, k), rec("kc", li, self.k_cache[li]), rec("vc", li, self.v_cache[li])
+            ops.flash_attn_ext(q[0].permute(1, 0, 2), self.k_cache[li][0, :, :n_kv], self.v_cache[li][0, :, :n_kv],
+                               mask, scale, out=b["attn"], ws=ws)
+            rec("attn", li, b["attn"])
+            o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
+            ops.add(x, o, out=x)
+            rec("x_mid", li, x)
+            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+            rec("h2", li, h)
+            gu = ops.mul_mat(L.gate_up, h, out=b["gu"], ws=ws)
+            rec("gu", li, gu)
+            a = ops.swiglu(gu, out=b["act"])
+            rec("act", li, a)
+            d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
+            ops.add(x, d, out=x)
+            rec("x_out", li, x)
+        h = ops.rms_norm(x[s - 1:], c.rms_eps, out=b["h"][:1])
+        rec("hf", -1, h)
+        logits = ops.mul_mat(self.w.lm_head, h, out=b["logits"], ws=ws)
+        ops.argmax(logits, out=b["next"])
+        rec("logits", -1, logits), rec("next", -1, b["next"])
+        if advance:
+            ops.kv_advance(self.pos, s)
+        return b["next"]
+
+    # -- graphs -----------------------------------------------------------------
+    def capture(self, s: int, n_kv: int, ids: torch.Tensor | None = None) -> torch.cuda.CUDAGraph:
+        """HIP graph of one step for the (s, n_kv) bucket (ids: the input buffer the
+        graph reads; for decode pass the graph's own "next" buffer to chain tokens)."""
+        key = (s, n_kv)
+        if key in self.graphs:
+            return self.graphs[key]
+        self.ws.get(self._ws_need(s))
+        saved = self.pos.clone()
+        self.step(s, n_kv, ids)  # warm-up (kernel attributes, occupancy caches)
+        torch.cuda.synchronize()
+        self.pos.copy_(saved)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step(s, n_kv, ids)
+        torch.cuda.synchronize()
+        self.pos.copy_(saved)
+        self.graphs[key] = g
+        return g
+
+    def _ws_need(self, s: int) -> int:
+        """Largest workspace any op of an s-token step can ask for (attention's
+        split count grows with n_kv, so it is sized at max_ctx)."""
+        c, L = self.cfg, self.w.layers[0]
+        need = [ops.mul_mat_workspace_size(wt, s) for wt in (L.qkv, L.o, L.gate_up, L.down)]
+        need.append(ops.mul_mat_workspace_size(self.w.lm_head, 1))
+        need.append(ops.flash_attn_workspace_size(c.head_dim, s, c.n_head, c.n_head_kv, self.max_ctx))
+        return max(need)
+
+    def decode_buffers(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(ids, next) of the s = 1 bucket: chaining next -> ids makes replays generate."""
+        b = self._buffers(1)
+        return b["ids"], b["next"]

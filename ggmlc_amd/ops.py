@@ -31,6 +31,7 @@ __all__ = [
     "QWeight", "Q8_0", "Q4_0", "quantize_row_q8_0", "quantize_weights", "mul_mat",
     "set_rows", "flash_attn_ext", "soft_max_ext", "Workspace",
     "swiglu", "rms_norm", "rope_ext", "add", "get_rows", "argmax",
+    "kv_step_inputs", "kv_advance",
 ]
 
 _TORCH_TO_GQ = {torch.float32: F32, torch.float16: F16, torch.int64: I64, torch.int32: I32}
@@ -87,6 +88,9 @@ class Workspace:
         if nbytes == 0:
             return 0, 0
         if self.buf is None or self.buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                # a graph captured earlier may still point at the current buffer
+                raise RuntimeError(f"Workspace: {nbytes} bytes needed during graph capture; size it first")
             dev = self.device or torch.device("cuda", torch.cuda.current_device())
             self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         return self.buf.data_ptr(), self.buf.numel()
@@ -239,3 +243,32 @@ def argmax(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         out = torch.empty((x.shape[0],), dtype=torch.int32, device=x.device)
     check(_lib.load().gq_argmax(_desc(x), _desc(out), _stream()))
     return out
+
+
+# ------------------------------------------------------------ KV step inputs
+
+def kv_step_inputs(pos: torch.Tensor, s: int, pos_ids: torch.Tensor | None = None,
+                   kv_idx: torch.Tensor | None = None, mask: torch.Tensor | None = None) -> None:
+    """Fill pos_ids (int32 [s]), kv_idx (int64 [s]) and the fp16 causal mask [s, n_kv]
+    from the device position ``pos`` (int32 [1])."""
+    md = _desc(mask) if mask is not None else None
+    check(_lib.load().gq_kv_step_inputs(pos.data_ptr(), s, pos_ids.data_ptr() if pos_ids is not None else None,
+                                        kv_idx.data_ptr() if kv_idx is not None else None, md, _stream()))
+
+
+def kv_advance(pos: torch.Tensor, s: int) -> None:
+    """pos += s on the device."""
+    check(_lib.load().gq_kv_advance(pos.data_ptr(), s, _stream()))
+
+
+def mul_mat_workspace_size(w: QWeight, M: int) -> int:
+    """Workspace bytes gq_mul_mat needs for M activation rows of this weight."""
+    x = make_tensor(0, F32, [w.K, M], [4, w.K * 4])
+    return int(_lib.load().gq_mul_mat_workspace_size(w.desc(), x))
+
+
+def flash_attn_workspace_size(D: int, S: int, Hq: int, Hkv: int, n_kv: int) -> int:
+    """Workspace bytes gq_flash_attn_ext needs for this shape."""
+    q = make_tensor(0, F32, [D, S, Hq, 1], [4, D * 4, D * 4 * S, D * 4 * S * Hq])
+    k = make_tensor(0, F16, [D, n_kv, Hkv, 1], [2, D * 2, D * 2 * n_kv, D * 2 * n_kv * Hkv])
+    return int(_lib.load().gq_flash_attn_ext_workspace_size(q, k))

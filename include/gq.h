@@ -176,6 +176,19 @@ int gq_get_rows(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_strea
 /* ggml_argmax(a): first index of the row maximum, dst I32 [rows]. */
 int gq_argmax(const gq_tensor* a, gq_tensor* dst, gq_stream_t stream);
 
+/* ---- persistent-KV step inputs --------------------------------------------
+ * The per-step inputs ggmlc's executor writes on the host before each run —
+ * set_decode_pos / set_chunk_pos (runtime/src/executor.cpp:1181-1393) and
+ * fill_f16_causal_mask (:136-148) — computed on the device from a position that
+ * lives in device memory (*pos, int32), so a captured step graph replays without
+ * host work:
+ *   pos_ids[i] = kv_idx[i] = *pos + i for i < s   (either may be NULL)
+ *   mask F16 [n_kv, >= s]: mask[j, i] = 0 if j <= *pos + i else -32768 (NULL: none).
+ * gq_kv_advance adds s to *pos (the last node of a decode-step graph). */
+int gq_kv_step_inputs(const int32_t* pos, int64_t s, int32_t* pos_ids, int64_t* kv_idx, gq_tensor* mask,
+                      gq_stream_t stream);
+int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream);
+
 /* ---- measurement aid ------------------------------------------------------
  * No counterpart in the reference. Reads `bytes` (16-byte aligned) once with
  * the coalesced 16-byte streaming loads the GEMV uses, so a benchmark can

@@ -101,6 +101,27 @@ def main() -> None:
     np.savez_compressed(OUT / "soft_max_f32.npz", x=xs, mask=ms, y=ys, scale=np.float32(0.125))
     manifest["files"]["soft_max_f32.npz"] = "x fp32 [16,300], mask uint16 [16,300], scale 0.125 -> y"
 
+    # ---- decoder ops around the path (one ggml node each)
+    a = (rng.standard_normal((5, 2 * 96)) * 3).astype(np.float32)
+    np.savez_compressed(OUT / "swiglu.npz", a=a, y=O.ref_swiglu(a))
+    xr = (rng.standard_normal((7, 960)) * 2).astype(np.float32)
+    np.savez_compressed(OUT / "rms_norm.npz", x=xr, eps=np.float32(1e-5), y=O.ref_rms_norm(xr, 1e-5))
+    for mode, name in ((2, "neox"), (0, "normal")):
+        xq = rng.standard_normal((6, 5, 64)).astype(np.float32)     # [seq, heads, hd]
+        pos = np.array([0, 1, 17, 255, 1000, 4095], np.int32)
+        np.savez_compressed(OUT / f"rope_{name}.npz", x=xq, pos=pos, n_dims=np.int32(64), mode=np.int32(mode),
+                            freq_base=np.float32(10000.0), y=O.ref_rope(xq, pos, 64, mode, 10000.0))
+    for wt, name in ((O.Q8_0, "q8_0"), (O.Q4_0, "q4_0")):
+        tab = O.quantize_weights((rng.standard_normal((50, 960)) * 0.02).astype(np.float32), wt)
+        ids = np.array([0, 49, 7, 7, 23], np.int32)
+        np.savez_compressed(OUT / f"get_rows_{name}.npz", table=tab, wtype=np.int32(wt), n_embd=np.int64(960), ids=ids,
+                            y=O.ref_get_rows(tab, wt, 960, ids))
+    xa = rng.standard_normal((4, 1000)).astype(np.float32)
+    xa[2, 10] = xa[2, 500] = 99.0  # tie: first index wins
+    np.savez_compressed(OUT / "argmax.npz", x=xa, y=O.ref_argmax(xa))
+    manifest["files"]["decoder ops"] = ("swiglu / rms_norm / rope_{neox,normal} / get_rows_{q8_0,q4_0} / argmax: "
+                                        "one ggml node each on the CPU backend")
+
     (OUT / "MANIFEST.json").write_text(json.dumps(manifest, indent=1) + "\n")
     print("wrote", len(list(OUT.glob("*.npz"))), "fixtures")
 
