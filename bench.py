@@ -1,23 +1,31 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized hot path on one MI355X (gfx950).
 
-Workload: the LLaMA SwiGLU MLP block, hidden 4096,
-FFN 11008, Q4_0 weights drawn N(0, 0.02) (ggmlc's fused graph: gate_up
-4096 -> 22016, SWIGLU, down 11008 -> 4096), fp32 activations N(0, 1).
+Workload: a LLaMA-7B-shape decoder (32 layers, hidden
+4096, 32 heads MHA, head_dim 128, FFN 11008, vocab 32000), random-init weights
+N(0, 0.02) quantized to Q4_0 on the device, F16 KV cache, batch 1. A 1024-token
+uniform-random prompt runs in ubatches of 512 (pp512 = the first ubatch, pp1024 =
+both), then greedy decode; the first decode token is untimed (ggmlc_bench.cpp
+methodology, runtime/tools/ggmlc_bench.cpp:295-560).
 
-* step      = one decode token through the block (M = 1: quantize + GEMV,
-              SWIGLU, quantize + GEMV); value = tokens/s = tg throughput.
-* pp512     = 512 tokens through the block as one prefill batch (MFMA GEMM).
-* m_sweep   = tokens/s at M in {1, 8, 128, 512} (GEMV -> GEMM crossover).
-* roofline  = the dominant decode kernel, the gate_up GEMV (Q4_0, 4096 ->
-              22016, M = 1), timed alone with HIP events on the launch stream;
-              algorithmic bytes = weight bytes + fp32 activation in + fp32 out.
-* cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, built from
-              the reference sources) running the same block on the same
-              weights with all host cores, for a bounded ~10 s sample.
+* step      = one greedy decode token through the whole model (embedding ->
+              32 layers -> lm_head -> argmax), replayed from the (1, n_kv) bucket's
+              HIP graph whose input is its own previous output; value = tg tokens/s
+              over exactly --steps tokens (tg128 by default).
+* roofline  = the decode GEMV (k_gemv_grp<Q4_0, M=1>), the dominant kernel: the
+              129 GEMV launches of one decode token (qkv, o, gate_up, down per layer,
+              lm_head) captured in one graph with the model's own weights and timed
+              with HIP events on the launch stream; achieved = their algorithmic bytes
+              (weights + fp32 x + fp32 y) / their time. rocprofv3's average for
+              k_gemv_grp<Q4_0> over this command covers the same launch mix.
+* roofline_prefill_gemm = the 128 prefill GEMMs (M = 512) of one ubatch, same way.
+* gemv_c1_q8_0 = configs[0], the Q8_0 Linear 4096 -> 4096 GEMV (16 rotating copies).
+* cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, built from the
+              reference sources) running the same decoder graph on the same weights
+              with the host's cores: pp512 then decode tokens for a bounded sample.
 
-Weights rotate over 8 distinct device copies (608 MB > the 256 MB Infinity
-Cache) so every step streams from HBM. Inputs are resident before timing.
+Weights (3.7 GB) far exceed the 256 MB Infinity Cache, so every decode token
+streams them from HBM. Inputs are resident before timing.
 """
 
 from __future__ import annotations
@@ -35,18 +43,19 @@ sys.path.insert(0, str(ROOT))
 METRIC = "pp512 & tg128 tokens/sec (1 GPU, Q8_0/Q4_0); GEMV HBM GB/s as % of peak"
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
-HIDDEN, FFN = 4096, 11008
-N_COPIES = 8
+UBATCH = 512
 
 
 def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200, help="timed decode steps")
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=128, help="timed decode tokens (tg128)")
+    p.add_argument("--warmup", type=int, default=2, help="untimed decode tokens before the timed ones")
+    p.add_argument("--prompt", type=int, default=1024, help="prompt tokens (multiple of 512)")
+    p.add_argument("--pp-reps", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--roofline-launches", type=int, default=400)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="decode budget of the CPU sample")
+    p.add_argument("--c1-launches", type=int, default=400)
     return p.parse_args()
 
 
@@ -57,173 +66,225 @@ def log(msg: str) -> None:
 def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the hot path is single-GPU; "
+        print("bench.py: this build measures one GPU only (every GPU box here has one; "
               "run with --gpus 1)", file=sys.stderr)
+        return 2
+    if args.prompt % UBATCH or args.prompt <= 0:
+        print("bench.py: --prompt must be a positive multiple of 512", file=sys.stderr)
         return 2
 
     import numpy as np
     import torch
 
     from ggmlc_amd import _lib, ops
+    from ggmlc_amd.model import LLAMA_7B, Decoder, pad_kv_len, random_weights
 
     torch.cuda.set_device(0)
     _lib.check(_lib.load().gq_init())
     dev = torch.device("cuda", 0)
+    cfg = LLAMA_7B
+    stream = torch.cuda.current_stream()
+
+    log(f"building {cfg.name} Q4_0 weights on device")
+    w = random_weights(cfg, dev, seed=1234)
+    torch.cuda.synchronize()
+    n_ctx = args.prompt + args.warmup + args.steps
+    max_ctx = pad_kv_len(n_ctx, 1 << 30)
+    dec = Decoder(w, max_ctx, dev)
+    log(f"weights {w.nbytes / 1e9:.3f} GB, KV cache {2 * cfg.n_layer * cfg.kv_dim * max_ctx * 2 / 1e9:.3f} GB "
+        f"(max_ctx {max_ctx})")
+
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    # ---- prefill graphs: one per ubatch bucket, reading its slice of the prompt
     gen = torch.Generator(device=dev)
-    gen.manual_seed(1234)
+    gen.manual_seed(99)
+    prompt = torch.randint(0, cfg.n_vocab, (args.prompt,), generator=gen, device=dev, dtype=torch.int32)
+    n_ub = args.prompt // UBATCH
+    pp_graphs = []
+    for u in range(n_ub):
+        dec.reset(u * UBATCH)
+        pp_graphs.append(dec.capture(UBATCH, pad_kv_len((u + 1) * UBATCH, max_ctx),
+                                     ids=prompt[u * UBATCH:(u + 1) * UBATCH]))
+    b_pp = dec._buffers(UBATCH)
 
-    # ---- weights: N_COPIES distinct Q4_0 copies of the fused MLP block
-    log(f"building {N_COPIES} weight copies on device")
-    copies = []
-    for _ in range(N_COPIES):
-        w = torch.randn((2 * FFN, HIDDEN), generator=gen, device=dev) * 0.02
-        gu = ops.quantize_weights(w, ops.Q4_0)
-        w = torch.randn((HIDDEN, FFN), generator=gen, device=dev) * 0.02
-        dn = ops.quantize_weights(w, ops.Q4_0)
-        del w
-        copies.append((gu, dn))
+    # ---- decode graphs: (1, n_kv) buckets; each reads the s=1 bucket's "next" and
+    # overwrites it with the new token, so replays generate without host work
+    _, next1 = dec.decode_buffers()
+    tg_graphs = {}
+    for i in range(args.warmup + args.steps):
+        n_kv = pad_kv_len(args.prompt + i + 1, max_ctx)
+        if n_kv not in tg_graphs:
+            dec.reset(args.prompt + i)
+            tg_graphs[n_kv] = dec.capture(1, n_kv, ids=next1)
     torch.cuda.synchronize()
-    wbytes = copies[0][0].nbytes + copies[0][1].nbytes
 
-    ws = ops.Workspace(dev)
-    x1 = torch.randn((1, HIDDEN), generator=gen, device=dev)
+    def prefill():
+        dec.reset(0)
+        for g in pp_graphs:
+            g.replay()
 
-    def block(x, r):
-        gu, dn = copies[r % N_COPIES]
-        h = ops.mul_mat(gu, x, ws=ws)
-        a = ops.swiglu(h)
-        return ops.mul_mat(dn, a, ws=ws)
-
-    def time_block(x, n, warm):
-        for i in range(warm):
-            block(x, i)
+    # ---- pp: time each ubatch (pp512 = the first, ppN = all)
+    log(f"prefill: {n_ub} ubatch(es) of {UBATCH}, {args.pp_reps} reps")
+    prefill()
+    torch.cuda.synchronize()
+    t_first, t_all = [], []
+    for _ in range(args.pp_reps):
+        dec.reset(0)
+        es = [ev() for _ in range(n_ub + 1)]
+        es[0].record()
+        for u, g in enumerate(pp_graphs):
+            g.replay()
+            es[u + 1].record()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(n):
-            block(x, i)
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n  # ms per step
+        t_first.append(es[0].elapsed_time(es[1]))
+        t_all.append(es[0].elapsed_time(es[-1]))
+    pp512_tok_s = UBATCH * 1000.0 / float(np.median(t_first))
+    ppN_tok_s = args.prompt * 1000.0 / float(np.median(t_all))
+    log(f"pp512 {pp512_tok_s:.0f} tok/s, pp{args.prompt} {ppN_tok_s:.0f} tok/s")
 
-    def capture(fn):
-        """HIP graph of fn() (the kernels it launches on the current stream)."""
-        fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            fn()
-        return g
-
-    def time_replays(graphs, n):
-        for i in range(3):
-            graphs[i % len(graphs)].replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(n):
-            graphs[i % len(graphs)].replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n
-
-    # one decode step per weight copy, each captured as a HIP graph (the
-    # executor's per-bucket graph; launches then cost no Python time)
-    ws.get(64 << 20)  # pre-size the workspace outside capture
-    outs = [None] * N_COPIES
-    step_graphs = []
-    for r in range(N_COPIES):
-        def one(r=r):
-            outs[r] = block(x1, r)
-        step_graphs.append(capture(one))
-
-    # ---- decode steps (the timed region of the contract)
-    log(f"decode: {args.warmup} warmup + {args.steps} timed steps (graph replay)")
+    # ---- tg: the prompt's KV is in the cache (last prefill rep); decode from its token
+    prefill()
+    next1.copy_(b_pp["next"])
+    torch.cuda.synchronize()
+    if int(dec.pos[0]) != args.prompt:
+        raise RuntimeError("device position after prefill is wrong")
+    tokens = []
+    pos = args.prompt
     for i in range(args.warmup):
-        step_graphs[i % N_COPIES].replay()
+        tg_graphs[pad_kv_len(pos + 1, max_ctx)].replay()
+        pos += 1
     torch.cuda.synchronize()
+    log(f"decode: {args.warmup} warmup + {args.steps} timed tokens (graph replay)")
+    e0, e1 = ev(), ev()
     t0 = time.perf_counter()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(args.steps):
-        step_graphs[i % N_COPIES].replay()
+        tg_graphs[pad_kv_len(pos + 1, max_ctx)].replay()
+        pos += 1
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = e0.elapsed_time(e1) / args.steps
     tg_tok_s = 1000.0 / ms_step
-    eager_ms = time_block(x1, 50, 5)
+    logits = dec._buffers(1)["logits"]
+    if int(dec.pos[0]) != pos or not bool(torch.isfinite(logits).all()):
+        raise RuntimeError("decode produced a wrong position or non-finite logits")
+    tokens.append(int(next1[0]))
+    kv_bytes_last = 2 * cfg.n_layer * cfg.kv_dim * 2 * pos  # valid K+V rows read by the last token
+    log(f"tg {tg_tok_s:.1f} tok/s ({ms_step:.3f} ms/token)")
 
-    # ---- prefill and the M sweep (graph replay per M)
-    sweep = {}
-    for M in (1, 8, 128, 512):
-        xm = torch.randn((M, HIDDEN), generator=gen, device=dev)
-        gs = [capture(lambda r=r: block(xm, r)) for r in range(N_COPIES)]
-        ms = time_replays(gs, 40 if M <= 8 else 16)
-        sweep[str(M)] = round(M * 1000.0 / ms, 1)
-        log(f"M={M}: {ms:.4f} ms/step -> {sweep[str(M)]} tok/s")
-        del gs
-    pp512_tok_s = sweep["512"]
+    # ---- roofline: the 129 decode GEMVs of one token, one graph, HIP events
+    x_h = torch.randn((1, cfg.n_embd), generator=gen, device=dev)
+    x_f = torch.randn((1, cfg.n_ff), generator=gen, device=dev)
+    mats = []
+    for L in w.layers:
+        mats += [(L.qkv, x_h), (L.o, x_h), (L.gate_up, x_h), (L.down, x_f)]
+    mats.append((w.lm_head, x_h))
+    outs = [torch.empty((1, m.N), device=dev) for m, _ in mats]
+    ws = ops.Workspace(dev)
+    ws.get(1 << 20)
 
-    # ---- roofline: gate_up GEMV alone (one kernel per mul_mat at M = 1),
-    # L launches captured in one graph, timed with events on the launch stream
-    L = args.roofline_launches
-    out = torch.empty((1, 2 * FFN), device=dev)
+    def gemv_token():
+        for (m, x), o in zip(mats, outs):
+            ops.mul_mat(m, x, out=o, ws=ws)
 
-    def gemv_loop():
-        for i in range(L):
-            ops.mul_mat(copies[i % N_COPIES][0], x1, out=out, ws=ws)
-    gl = capture(gemv_loop)
-    gemv_ms = time_replays([gl], 3) / L
-    del gl
-    gemv_bytes = copies[0][0].nbytes + HIDDEN * 4 + 2 * FFN * 4
-    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
-
-    # ---- GEMM (prefill) MFMA rate for the same weight at M = 512
-    x512 = torch.randn((512, HIDDEN), generator=gen, device=dev)
-    out512 = torch.empty((512, 2 * FFN), device=dev)
-    nG = 16
-
-    def gemm_loop():
-        for i in range(nG):
-            ops.mul_mat(copies[i % N_COPIES][0], x512, out=out512, ws=ws)
-    gg = capture(gemm_loop)
-    gemm_ms = time_replays([gg], 3) / nG
+    gemv_token()
+    torch.cuda.synchronize()
+    gg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gg):
+        gemv_token()
+    for _ in range(3):
+        gg.replay()
+    torch.cuda.synchronize()
+    R = 20
+    e0.record()
+    for _ in range(R):
+        gg.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    gemv_ms_token = e0.elapsed_time(e1) / R
+    gemv_bytes_token = sum(m.nbytes + m.K * 4 + m.N * 4 for m, _ in mats)
+    n_gemv = len(mats)
+    gemv_gbs = gemv_bytes_token / (gemv_ms_token * 1e-3) / 1e9
     del gg
-    gemm_tflops = 2.0 * 512 * 2 * FFN * HIDDEN / (gemm_ms * 1e-3) / 1e12
 
-    # ---- config 1 GEMV: Linear 4096 -> 4096, Q8_0, M = 1 (17.8 MB per launch)
+    # ---- prefill GEMM rate: the 128 GEMMs of one ubatch (M = 512)
+    xs = {k: torch.randn((UBATCH, k), generator=gen, device=dev) for k in (cfg.n_embd, cfg.q_dim, cfg.n_ff)}
+    gmats = []
+    for L in w.layers:
+        gmats += [(L.qkv, xs[cfg.n_embd]), (L.o, xs[cfg.q_dim]), (L.gate_up, xs[cfg.n_embd]), (L.down, xs[cfg.n_ff])]
+    gout = {n: torch.empty((UBATCH, n), device=dev) for n in {m.N for m, _ in gmats}}
+    ws.get(max(ops.mul_mat_workspace_size(m, UBATCH) for m, _ in gmats))
+
+    def gemm_ubatch():
+        for m, x in gmats:
+            ops.mul_mat(m, x, out=gout[m.N], ws=ws)
+
+    gemm_ubatch()
+    torch.cuda.synchronize()
+    gm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gm):
+        gemm_ubatch()
+    gm.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(3):
+        gm.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    gemm_ms = e0.elapsed_time(e1) / 3
+    gemm_flops = sum(2.0 * UBATCH * m.N * m.K for m, _ in gmats)
+    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    del gm, gout, xs
+
+    # ---- Linear 4096 -> 4096, Q8_0, M = 1 (17.8 MB per launch)
+    gc1 = torch.Generator(device=dev)
+    gc1.manual_seed(7)
     c1 = []
     for _ in range(16):  # 16 x 17.8 MB = 285 MB > Infinity Cache
-        w = torch.randn((HIDDEN, HIDDEN), generator=gen, device=dev) * 0.02
-        c1.append(ops.quantize_weights(w, ops.Q8_0))
-        del w
-    out1 = torch.empty((1, HIDDEN), device=dev)
+        t = torch.randn((4096, 4096), generator=gc1, device=dev) * 0.02
+        c1.append(ops.quantize_weights(t, ops.Q8_0))
+        del t
+    x1 = torch.randn((1, 4096), generator=gc1, device=dev)
+    out1 = torch.empty((1, 4096), device=dev)
+    Lc = args.c1_launches
 
     def c1_loop():
-        for i in range(L):
+        for i in range(Lc):
             ops.mul_mat(c1[i % 16], x1, out=out1, ws=ws)
-    gc = capture(c1_loop)
-    c1_ms = time_replays([gc], 3) / L
-    del gc
-    c1_bytes = c1[0].nbytes + HIDDEN * 4 + HIDDEN * 4
-    c1_gbs = c1_bytes / (c1_ms * 1e-3) / 1e9
-    del c1
 
-    # ---- measured ceilings (context for the 8 TB/s datasheet peak): the
-    # streaming-read probe (same 16-byte nontemporal loads as the GEMV) and a copy
+    c1_loop()
+    torch.cuda.synchronize()
+    gq = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gq):
+        c1_loop()
+    gq.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(3):
+        gq.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    c1_ms = e0.elapsed_time(e1) / (3 * Lc)
+    c1_bytes = c1[0].nbytes + 4096 * 4 + 4096 * 4
+    c1_gbs = c1_bytes / (c1_ms * 1e-3) / 1e9
+    del gq, c1
+
+    # ---- measured ceilings next to the datasheet peak: the streaming-read probe
+    # (the GEMV's 16-byte nontemporal load pattern) and a device copy
     big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
-    L_ = _lib.load()
-    for _ in range(2):
-        _lib.check(L_.gq_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(),
-                                           torch.cuda.current_stream().cuda_stream))
+    Lib = _lib.load()
+
+    def probe():
+        _lib.check(Lib.gq_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(), stream.cuda_stream))
+
+    probe(), probe()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(10):
-        _lib.check(L_.gq_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(),
-                                           torch.cuda.current_stream().cuda_stream))
+        probe()
     e1.record()
     torch.cuda.synchronize()
     read_gbs = big.numel() * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
@@ -238,9 +299,10 @@ def main() -> int:
     copy_gbs = 2 * big.numel() * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
     del big, big2
 
+    decode_bytes = w.decode_bytes
     result = {
         "metric": METRIC,
-        "value": round(tg_tok_s, 1),
+        "value": round(tg_tok_s, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -249,42 +311,45 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 x q8_0 int8 dot, f32 accum (prefill: f16 MFMA)",
-        "data": "synthetic (weights N(0,0.02) -> Q4_0, activations N(0,1))",
+        "dtype": "q4_0 weights x q8_0 activations, int8 dot, f32 accum (prefill: f16 MFMA); f16 KV",
+        "data": "synthetic (random-init weights N(0,0.02) -> Q4_0; uniform-random prompt ids)",
         "config": {
-            "workload": "configs[1] SwiGLU MLP block hidden 4096 / FFN 11008, Q4_0, decode M=1 per step",
+            "workload": f"configs[3] {cfg.name} decoder, Q4_0, batch 1: pp{args.prompt} (ubatch 512) then "
+                        f"greedy decode; value = tg{args.steps} tokens/s",
             "global_batch": 1,
+            "seq_len": args.prompt,
             "parallelism": "single GPU",
-            "weight_copies_rotated": N_COPIES,
-            "weight_bytes_per_step": wbytes,
+            "weight_bytes": w.nbytes,
         },
-        "tg_tok_s": round(tg_tok_s, 1),
-        "pp512_tok_s": pp512_tok_s,
-        "m_sweep_tok_s": sweep,
-        "block_decode_GBps": round(wbytes / (ms_step * 1e-3) / 1e9, 1),
-        "eager_tok_s": round(1000.0 / eager_ms, 1),
+        "tg_tok_s": round(tg_tok_s, 2),
+        "pp512_tok_s": round(pp512_tok_s, 1),
+        f"pp{args.prompt}_tok_s": round(ppN_tok_s, 1),
+        "decode_weight_GBps": round(decode_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "decode_weight_plus_kv_GBps": round((decode_bytes + kv_bytes_last) / (ms_step * 1e-3) / 1e9, 1),
         "roofline": {
-            "kernel": "k_gemv_grp<Q4_0, M=1> (gate_up 4096->22016)",
+            "kernel": "k_gemv_grp<Q4_0, M=1>: the 129 decode GEMVs of one token (qkv, o, gate_up, down x 32, lm_head)",
             "bound": "hbm",
             "achieved": round(gemv_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "bytes_per_launch": gemv_bytes,
-            "us_per_launch": round(gemv_ms * 1e3, 3),
+            "bytes_per_launch": round(gemv_bytes_token / n_gemv),
+            "us_per_launch": round(gemv_ms_token * 1e3 / n_gemv, 3),
+            "launches_per_token": n_gemv,
+            "gemv_ms_per_token": round(gemv_ms_token, 4),
         },
         "roofline_prefill_gemm": {
-            "kernel": "k_gemm<Q4_0> (gate_up 4096->22016, M=512) + fp16 activation quantize",
+            "kernel": "k_gemm<Q4_0>: the 128 GEMMs of one 512-token ubatch (activation quantize excluded)",
             "bound": "mfma",
             "achieved": round(gemm_tflops, 1),
             "peak": FP16_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
-            "us_per_launch": round(gemm_ms * 1e3, 2),
+            "ms_per_ubatch": round(gemm_ms, 3),
         },
         "gemv_c1_q8_0": {
-            "kernel": "k_gemv_grp<Q8_0, M=1> (Linear 4096->4096)",
+            "kernel": "k_gemv_grp<Q8_0, M=1> (configs[0] Linear 4096->4096)",
             "achieved_GBps": round(c1_gbs, 1),
             "frac_of_peak": round(c1_gbs / HBM_PEAK_GBS, 4),
             "us_per_launch": round(c1_ms * 1e3, 3),
@@ -294,46 +359,55 @@ def main() -> int:
         "measured_copy_GBps": round(copy_gbs, 1),
         "wall_s_timed": round(wall, 3),
     }
+    log(f"gemv {gemv_gbs:.0f} GB/s, gemm {gemm_tflops:.0f} TFLOP/s, c1 {c1_gbs:.0f} GB/s, read {read_gbs:.0f} GB/s")
 
     if not args.no_cpu:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(copies[0], x1, seconds=args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
 
 
-def cpu_baseline(copy, x1, seconds: float = 10.0) -> dict:
-    """Reference ggml CPU backend on the same block and weights (tokens/s at M = 1)."""
+def cpu_baseline(w, cfg, seconds: float) -> dict:
+    """The reference ggml CPU backend running the same decoder on the same weights:
+    pp512 (one ubatch from position 0), then greedy decode tokens for ~`seconds`."""
     import numpy as np
 
     import oracle as O
 
-    gu, dn = copy
-    wgu = gu.data.cpu().numpy()
-    wdn = dn.data.cpu().numpy()
-    x = x1.cpu().numpy()
     cores = O.n_cpu_threads()
+    host = (w.embed.data.cpu().numpy(), w.lm_head.data.cpu().numpy(),
+            [tuple(m.data.cpu().numpy() for m in (L.qkv, L.o, L.gate_up, L.down)) for L in w.layers])
+    prompt = np.random.default_rng(5).integers(0, cfg.n_vocab, UBATCH).astype(np.int32)
     if O.ref_available():
-        g = O.ref_mlp_graph(wgu, wdn, O.Q4_0, HIDDEN, FFN, 1)
-        g.run(x, cores)
+        rl = O.RefLlama(cfg, host, 1024, n_threads=cores)
+        t0 = time.perf_counter()
+        _, tok = rl.step(prompt)
+        pp_s = time.perf_counter() - t0
+        rl.step([tok])  # first decode token untimed
         n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
-            g.run(x, cores)
+        while time.perf_counter() - t0 < seconds and rl.pos < 1024:
+            _, tok = rl.step([tok])
             n += 1
         dt = (time.perf_counter() - t0) / n
-        g.close()
-        kind, sample = "reference", f"{n} decode steps (M=1) of the MLP block through ggml's CPU graph"
-    else:  # the C restatement (scalar, one row split per thread)
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds and n < 50:
-            h = O.mul_mat(wgu, O.Q4_0, HIDDEN, x, n_threads=cores)
-            a = h[:, :FFN] / (1 + np.exp(-h[:, :FFN])) * h[:, FFN:]
-            O.mul_mat(wdn, O.Q4_0, FFN, a, n_threads=cores)
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-        kind, sample = "port", f"{n} decode steps (M=1) of the MLP block through the C restatement"
-    return {"value": round(1.0 / dt, 2), "unit": "tokens/s", "cores": cores, "kind": kind,
-            "sample": sample, "ms_per_step": round(dt * 1e3, 3)}
+        del rl
+        return {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": cores, "kind": "reference",
+                "sample": f"ggml CPU backend ({cores} threads) on the same {cfg.name} Q4_0 weights: one 512-token "
+                          f"prefill ubatch, then {n} timed greedy decode tokens at context ~{UBATCH}",
+                "ms_per_step": round(dt * 1e3, 2), "pp512_tok_s": round(UBATCH / pp_s, 2)}
+    # no reference build: the C restatement's MUL_MATs of one decode token (the bulk of its work)
+    x = np.random.default_rng(6).standard_normal((1, cfg.n_ff)).astype(np.float32)
+    mats = [(m, cfg.n_embd if i != 3 else cfg.n_ff) for L in host[2] for i, m in enumerate(L)]
+    mats.append((host[1], cfg.n_embd))
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < 20:
+        for m, K in mats:
+            O.mul_mat(m, cfg.qtype, K, x[:, :K], n_threads=cores)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n} decode tokens' MUL_MATs (the {len(mats)} GEMVs) through the C restatement",
+            "ms_per_step": round(dt * 1e3, 2)}
 
 
 if __name__ == "__main__":

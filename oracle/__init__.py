@@ -109,6 +109,11 @@ def ref():
         L.ref_rope.argtypes = [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _f32, _vp]
         L.ref_get_rows.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp]
         L.ref_argmax.argtypes = [_vp, _i64, _i64, _vp]
+        L.ref_llama_create.restype = _vp
+        L.ref_llama_create.argtypes = [_vp, _i32, _f32, _f32, _vp, _vp, _vp, _vp]
+        L.ref_llama_step.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32]
+        L.ref_llama_free.argtypes = [_vp]
+        L.ref_llama_free.restype = None
         L.ref_init()
         _ref = L
     return _ref
@@ -330,3 +335,49 @@ def ref_argmax(x) -> np.ndarray:
     out = np.empty(x.shape[0], np.int32)
     ref().ref_argmax(_ptr(x), x.shape[1], x.shape[0], _ptr(out))
     return out
+
+
+class RefLlama:
+    """The reference ggml CPU backend running ggmlc's LLaMA decoder graph
+    (ref_driver.cpp ref_llama_*): persistent F16 KV caches held here, weights
+    referenced in place (the caller keeps the arrays alive).
+
+    cfg needs n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, qtype,
+    rms_eps, rope_base; weights = (embed, lm_head, [(qkv, o, gate_up, down), ...])
+    as uint8 GGUF block bytes."""
+
+    def __init__(self, cfg, weights, max_ctx: int, n_threads: int = 8):
+        embed, lm_head, layers = weights
+        self.cfg, self.max_ctx, self.n_threads = cfg, max_ctx, n_threads
+        self._w = [_c(embed, np.uint8), _c(lm_head, np.uint8)] + [_c(m, np.uint8) for L in layers for m in L]
+        self.kc = [np.zeros((cfg.n_head_kv, max_ctx, cfg.head_dim), np.uint16) for _ in layers]
+        self.vc = [np.zeros_like(k) for k in self.kc]
+        dims = np.array([cfg.n_layer, cfg.n_embd, cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.n_ff,
+                         cfg.n_vocab, max_ctx], np.int64)
+        lw = (_vp * (4 * len(layers)))(*[a.ctypes.data for a in self._w[2:]])
+        kv = (_vp * (2 * len(layers)))(*[a.ctypes.data for pair in zip(self.kc, self.vc) for a in pair])
+        self.h = ref().ref_llama_create(_ptr(dims), cfg.qtype, cfg.rms_eps, cfg.rope_base, _ptr(self._w[0]),
+                                        _ptr(self._w[1]), lw, kv)
+        if not self.h:
+            raise RuntimeError("ref_llama_create failed")
+        self.pos = 0
+
+    def step(self, ids):
+        """Run the tokens at the current position; returns (last-token logits, argmax)."""
+        ids = _c(ids, np.int32)
+        s = ids.size
+        n_kv = pad_kv_len(self.pos + s, self.max_ctx)
+        mask = causal_mask_f16(self.pos, s, n_kv)
+        logits = np.empty(self.cfg.n_vocab, np.float32)
+        nxt = np.zeros(1, np.int32)
+        if ref().ref_llama_step(self.h, _ptr(ids), s, self.pos, n_kv, _ptr(mask), _ptr(logits), _ptr(nxt),
+                                self.n_threads) != 0:
+            raise RuntimeError("ref_llama_step failed")
+        self.pos += s
+        return logits, int(nxt[0])
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            ref().ref_llama_free(self.h)
+            self.h = None
+

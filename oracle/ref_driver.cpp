@@ -15,11 +15,18 @@
 //   set_rows           -> ggml_set_rows (ggml.c:3937), executor.cpp:2181-2184
 //   flash_attn_ext     -> ggml_flash_attn_ext (ggml.c:5402), executor.cpp:2195-2197
 //   soft_max           -> ggml_soft_max_ext (ggml.c:4081), executor.cpp:2358-2361
+//   whole LLaMA decoder -> the graph the executor builds for a fused LLaMA block
+//                         (executor.cpp:1738-2810; KV wiring :2130-2197), run by
+//                         ggml_graph_compute on the CPU backend
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "ggml.h"
+#include "ggml-alloc.h"
+#include "ggml-backend.h"
 #include "ggml-cpu.h"
 
 // ggml-quants.h:23 (declared here with an opaque block pointer; same C symbol)
@@ -294,6 +301,154 @@ int ref_argmax(const float* x, int64_t n, int64_t nrows, int32_t* out) {
     if (run_graph(c.ctx, Y, 1) != 0) return -1;
     memcpy(out, Y->data, sizeof(int32_t) * nrows);
     return 0;
+}
+
+// ---- whole decoder (CPU baseline of the model-level benchmark) -------------------
+// Weights and KV caches stay in the caller's memory (tensors point at it); each step
+// builds the executor's graph for (s, n_kv), allocates its intermediates with
+// ggml-alloc and runs ggml_graph_compute on n_threads.
+//
+// Per layer (gamma of RMSNorm baked into the following Linear, Q/K/V and gate/up
+// fused, as ggmlc's fusion pass emits them):
+//   h = rms_norm(x); qkv = mul_mat(Wqkv, h); q, k = rope_ext(NEOX)(views of qkv)
+//   set_rows(Kc, k^T, idx); set_rows(Vc, v^T, idx)          (executor.cpp:2181-2184)
+//   a = flash_attn_ext(q^T, Kc[:n_kv], Vc[:n_kv], mask, 1/sqrt(hd))  (:2195-2197)
+//   x += mul_mat(Wo, a); x += mul_mat(Wdown, swiglu(mul_mat(Wgate_up, rms_norm(x))))
+// then rms_norm(x[s-1]) -> mul_mat(lm_head) -> argmax.
+
+struct RefLlama {
+    int64_t n_layer, n_embd, n_head, n_head_kv, hd, n_ff, n_vocab, max_ctx;
+    ggml_type wt;
+    float eps, base;
+    ggml_context* wctx = nullptr;
+    ggml_tensor *embed = nullptr, *lm_head = nullptr;
+    std::vector<ggml_tensor*> wqkv, wo, wgu, wd, kc, vc;
+    ggml_gallocr_t galloc = nullptr;
+    std::vector<uint8_t> work;
+};
+
+static ggml_tensor* ext2d(ggml_context* c, ggml_type t, int64_t ne0, int64_t ne1, const void* p) {
+    ggml_tensor* x = ggml_new_tensor_2d(c, t, ne0, ne1);
+    x->data = const_cast<void*>(p);
+    return x;
+}
+
+// dims: n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, max_ctx
+// layer_w: 4 pointers per layer (qkv, o, gate_up, down); kv: 2 per layer (K, V caches,
+// F16 [max_ctx][hd] per head, heads outermost)
+void* ref_llama_create(const int64_t* dims, int wtype, float eps, float rope_base, const void* embed,
+                       const void* lm_head, const void* const* layer_w, void* const* kv) {
+    ggml_cpu_init();
+    RefLlama* m = new RefLlama;
+    m->n_layer = dims[0], m->n_embd = dims[1], m->n_head = dims[2], m->n_head_kv = dims[3];
+    m->hd = dims[4], m->n_ff = dims[5], m->n_vocab = dims[6], m->max_ctx = dims[7];
+    m->wt = (ggml_type)wtype, m->eps = eps, m->base = rope_base;
+    ggml_init_params p = {ggml_tensor_overhead() * (size_t)(8 * m->n_layer + 8), nullptr, true};
+    m->wctx = ggml_init(p);
+    if (!m->wctx) {
+        delete m;
+        return nullptr;
+    }
+    const int64_t E = m->n_embd, qd = m->n_head * m->hd, kvd = m->n_head_kv * m->hd;
+    m->embed = ext2d(m->wctx, m->wt, E, m->n_vocab, embed);
+    m->lm_head = ext2d(m->wctx, m->wt, E, m->n_vocab, lm_head);
+    for (int64_t l = 0; l < m->n_layer; ++l) {
+        m->wqkv.push_back(ext2d(m->wctx, m->wt, E, qd + 2 * kvd, layer_w[4 * l + 0]));
+        m->wo.push_back(ext2d(m->wctx, m->wt, qd, E, layer_w[4 * l + 1]));
+        m->wgu.push_back(ext2d(m->wctx, m->wt, E, 2 * m->n_ff, layer_w[4 * l + 2]));
+        m->wd.push_back(ext2d(m->wctx, m->wt, m->n_ff, E, layer_w[4 * l + 3]));
+        for (int j = 0; j < 2; ++j) {
+            ggml_tensor* c = ggml_new_tensor_4d(m->wctx, GGML_TYPE_F16, m->hd, m->max_ctx, m->n_head_kv, 1);
+            c->data = kv[2 * l + j];
+            (j ? m->vc : m->kc).push_back(c);
+        }
+    }
+    m->galloc = ggml_gallocr_new(ggml_backend_cpu_buffer_type());
+    return m;
+}
+
+// ids I32 [s]; mask F16 [s][n_kv] (row i = query pos+i); logits F32 [n_vocab] of the
+// last token; next = its argmax. Returns 0 on success.
+int ref_llama_step(void* h, const int32_t* ids, int64_t s, int64_t pos, int64_t n_kv, const uint16_t* mask,
+                   float* logits, int32_t* next, int n_threads) {
+    RefLlama* m = (RefLlama*)h;
+    if (pos + s > m->max_ctx || n_kv > m->max_ctx || pos + s > n_kv) return -1;
+    const size_t graph_size = 64 * (size_t)m->n_layer + 64;
+    ggml_init_params p = {ggml_tensor_overhead() * graph_size * 2 + ggml_graph_overhead_custom(graph_size, false),
+                          nullptr, true};
+    ggml_context* c = ggml_init(p);
+    if (!c) return -1;
+    ggml_cgraph* gf = ggml_new_graph_custom(c, graph_size, false);
+    const int64_t E = m->n_embd, hd = m->hd, H = m->n_head, Hk = m->n_head_kv;
+    const int64_t qd = H * hd, kvd = Hk * hd;
+
+    ggml_tensor* t_ids = ggml_new_tensor_1d(c, GGML_TYPE_I32, s);
+    ggml_tensor* t_pos = ggml_new_tensor_1d(c, GGML_TYPE_I32, s);
+    ggml_tensor* t_idx = ggml_new_tensor_1d(c, GGML_TYPE_I64, s);
+    ggml_tensor* t_mask = ggml_new_tensor_2d(c, GGML_TYPE_F16, n_kv, s);
+    for (ggml_tensor* t : {t_ids, t_pos, t_idx, t_mask}) ggml_set_input(t);
+
+    ggml_tensor* x = ggml_get_rows(c, m->embed, t_ids);  // [E, s]
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int64_t l = 0; l < m->n_layer; ++l) {
+        ggml_tensor* hn = ggml_rms_norm(c, x, m->eps);
+        ggml_tensor* qkv = ggml_mul_mat(c, m->wqkv[l], hn);  // [qd + 2 kvd, s]
+        const size_t es = sizeof(float);
+        ggml_tensor* q = ggml_view_3d(c, qkv, hd, H, s, hd * es, qkv->nb[1], 0);
+        ggml_tensor* k = ggml_view_3d(c, qkv, hd, Hk, s, hd * es, qkv->nb[1], qd * es);
+        ggml_tensor* v = ggml_view_3d(c, qkv, hd, Hk, s, hd * es, qkv->nb[1], (qd + kvd) * es);
+        q = ggml_rope_ext(c, q, t_pos, nullptr, (int)hd, GGML_ROPE_TYPE_NEOX, 0, m->base, 1.0f, 0.0f, 1.0f,
+                          0.0f, 0.0f);
+        k = ggml_rope_ext(c, k, t_pos, nullptr, (int)hd, GGML_ROPE_TYPE_NEOX, 0, m->base, 1.0f, 0.0f, 1.0f,
+                          0.0f, 0.0f);
+        // [hd, heads, s] -> [hd, s, heads] (rows stay contiguous, as set_rows requires)
+        ggml_tensor* ks = ggml_permute(c, k, 0, 2, 1, 3);
+        ggml_tensor* vs = ggml_permute(c, v, 0, 2, 1, 3);
+        ggml_build_forward_expand(gf, ggml_set_rows(c, m->kc[l], ks, t_idx));
+        ggml_build_forward_expand(gf, ggml_set_rows(c, m->vc[l], vs, t_idx));
+        ggml_tensor* K = ggml_view_4d(c, m->kc[l], hd, n_kv, Hk, 1, m->kc[l]->nb[1], m->kc[l]->nb[2],
+                                      m->kc[l]->nb[3], 0);
+        ggml_tensor* V = ggml_view_4d(c, m->vc[l], hd, n_kv, Hk, 1, m->vc[l]->nb[1], m->vc[l]->nb[2],
+                                      m->vc[l]->nb[3], 0);
+        ggml_tensor* a = ggml_flash_attn_ext(c, ggml_permute(c, q, 0, 2, 1, 3), K, V, t_mask, scale, 0.0f, 0.0f);
+        a = ggml_reshape_2d(c, a, qd, s);  // the op's output is [hd, H, s]
+        x = ggml_add(c, x, ggml_mul_mat(c, m->wo[l], a));
+        ggml_tensor* gu = ggml_mul_mat(c, m->wgu[l], ggml_rms_norm(c, x, m->eps));
+        x = ggml_add(c, x, ggml_mul_mat(c, m->wd[l], ggml_swiglu(c, gu)));
+    }
+    ggml_tensor* xl = ggml_view_2d(c, x, E, 1, x->nb[1], (size_t)(s - 1) * x->nb[1]);
+    ggml_tensor* lo = ggml_mul_mat(c, m->lm_head, ggml_rms_norm(c, xl, m->eps));
+    ggml_tensor* am = ggml_argmax(c, lo);
+    ggml_set_output(lo);
+    ggml_set_output(am);
+    ggml_build_forward_expand(gf, am);
+
+    int rc = -1;
+    if (ggml_gallocr_alloc_graph(m->galloc, gf)) {
+        memcpy(t_ids->data, ids, sizeof(int32_t) * s);
+        int32_t* pp = (int32_t*)t_pos->data;
+        int64_t* ip = (int64_t*)t_idx->data;
+        for (int64_t i = 0; i < s; ++i) pp[i] = (int32_t)(pos + i), ip[i] = pos + i;
+        memcpy(t_mask->data, mask, sizeof(uint16_t) * n_kv * s);
+        ggml_cplan plan = ggml_graph_plan(gf, n_threads, nullptr);
+        if (m->work.size() < plan.work_size) m->work.resize(plan.work_size);
+        plan.work_data = m->work.data();
+        if (ggml_graph_compute(gf, &plan) == GGML_STATUS_SUCCESS) {
+            memcpy(logits, lo->data, sizeof(float) * m->n_vocab);
+            *next = *(const int32_t*)am->data;
+            rc = 0;
+        }
+    }
+    ggml_free(c);
+    return rc;
+}
+
+void ref_llama_free(void* h) {
+    RefLlama* m = (RefLlama*)h;
+    if (!m) return;
+    if (m->galloc) ggml_gallocr_free(m->galloc);
+    ggml_free(m->wctx);
+    delete m;
 }
 
 }  // extern "C"

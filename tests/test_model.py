@@ -142,6 +142,28 @@ def test_noise_floor_of_quantized_pipeline(qtype):
     assert _cos(exact, RefModel(c, w, 512, perturb=1e-9).step(ids)) == pytest.approx(1.0, abs=1e-12)
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="reference ggml build (oracle/_ref) absent")
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+def test_reference_graph_matches_restatement(qtype):
+    """The reference's own ggml CPU backend running the decoder graph (oracle.RefLlama)
+    against RefModel: the same greedy token where the margin is clear, and agreement at
+    the pipeline's noise floor (ggml's decode attention also accumulates V in fp16)."""
+    c = _tiny(qtype)
+    w = _cpu_weights(c, 7)
+    rm, rl = RefModel(c, w, 512), O.RefLlama(c, w, 512, n_threads=4)
+    toks = list(np.random.default_rng(3).integers(0, c.n_vocab, 37))
+    for i in range(4):
+        want = rm.step(toks)
+        got, nxt = rl.step(toks)
+        assert _cos(got, want) >= 0.9999, (i, _cos(got, want))
+        assert nxt == int(np.argmax(got))
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > 2 * np.abs(got - want).max():
+            assert nxt == int(np.argmax(want))
+        toks = [nxt]
+    assert rl.pos == rm.pos == 40
+
+
 # ------------------------------------------------------------------- GPU
 
 def _gpu_model(cfg, max_ctx, seed):
@@ -267,13 +289,25 @@ def _run(cfg, prompt_len, n_new, max_ctx, graphs):
         tokens.append(int(next1[0]))
         ids1.copy_(next1)
     torch.cuda.synchronize()
+    if O.ref_available():
+        # the same token sequence through the reference's own ggml CPU graph
+        rl = O.RefLlama(cfg, host, max_ctx, n_threads=8)
+        seq = [list(prompt)] + [[t] for t in tokens[:-1]]
+        for i, ids in enumerate(seq):
+            want, _ = rl.step(ids)
+            res[i] = res[i] + (want,)
     return res, tokens, int(dec.pos[0])
 
 
 def _check_end_to_end(res, tokens, min_cos):
-    for i, (got, want) in enumerate(res):
+    for i, r in enumerate(res):
+        got, want = r[0], r[1]
         cos, mar = _cos(got, want), _mar(got, want)
-        print(f"step {i}: cos {cos:.7f} max-abs-rel {mar:.2e}")
+        line = f"step {i}: cos {cos:.7f} max-abs-rel {mar:.2e}"
+        if len(r) > 2:  # against the reference ggml graph as well
+            line += f" | ggml cos {_cos(got, r[2]):.7f}"
+            assert _cos(got, r[2]) >= min_cos, (i, "ggml", _cos(got, r[2]))
+        print(line)
         assert cos >= min_cos, (i, cos, mar)
         # the greedy token agrees with the reference unless the reference's top two are
         # closer than the step's own deviation
