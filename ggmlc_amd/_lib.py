@@ -35,6 +35,15 @@ class gq_tensor(ctypes.Structure):
     ]
 
 
+class gq_mul_mat_fusion(ctypes.Structure):
+    _fields_ = [
+        ("rms_norm", ctypes.c_int32),
+        ("rms_eps", ctypes.c_float),
+        ("swiglu", ctypes.c_int32),
+        ("add", ctypes.POINTER(gq_tensor)),
+    ]
+
+
 _P = ctypes.POINTER(gq_tensor)
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -49,6 +58,7 @@ SIGNATURES = {
     "gq_quantize_weights": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _i64, _vp]),
     "gq_mul_mat_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_mul_mat": (ctypes.c_int, [_P, _P, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_mul_mat_fused": (ctypes.c_int, [_P, _P, _P, ctypes.POINTER(gq_mul_mat_fusion), _vp]),
     "gq_set_rows": (ctypes.c_int, [_P, _P, _P, _vp, _vp]),
     "gq_flash_attn_ext_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_flash_attn_ext": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp, ctypes.c_size_t, _vp]),

@@ -157,11 +157,50 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     const float* x = static_cast<const float*>(b->data);
     float* y = static_cast<float*>(dst->data);
     const uint8_t* W = static_cast<const uint8_t*>(a->data);
-    if (p.use_gemv) return gemv(a->type, W, p.N, p.K, x, p.x_stride, p.M, y, p.ldd, s);
+    if (p.use_gemv) return gemv(a->type, W, p.N, p.K, x, p.x_stride, p.M, y, p.ldd, GemvFuse{}, s);
     uint16_t* A = static_cast<uint16_t*>(workspace);
     rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, p.K, s);
     if (rc) return rc;
     return gemm(a->type, W, p.N, p.K, A, p.K, p.M, y, p.ldd, s);
+}
+
+int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
+                     gq_stream_t stream) {
+    if (!dst || !f) return fail(GQ_ERR_INVALID, "mul_mat_fused: null dst or fusion");
+    if (f->swiglu && f->add) return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu and add are exclusive");
+    MulMatPlan p;
+    int rc = plan_mul_mat(a, b, nullptr, p);
+    if (rc) return rc;
+    if (p.M > GEMV_MAX_M)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: only the GEMV path (M <= 4) is fused, M = " + std::to_string(p.M));
+    const int64_t n_out = f->swiglu ? p.N / 2 : p.N;
+    if (f->swiglu && p.N % 2) return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu needs an even row count: " + shape(a));
+    if (dst->type != GQ_TYPE_F32 || dst->ne[0] != n_out || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
+        dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [" + std::to_string(n_out) + ", M, ...]: " +
+                                        shape(dst));
+    GemvFuse fz;
+    if (f->rms_norm) {
+        fz.rms = 1;
+        fz.eps = f->rms_eps;
+    }
+    if (f->swiglu) {
+        fz.glu = 1;
+        fz.glu_half = p.N / 2;
+    }
+    if (f->add) {
+        const gq_tensor* r = f->add;
+        if (r->type != GQ_TYPE_F32 || r->ne[0] != p.N || r->ne[1] != dst->ne[1] || r->ne[2] != dst->ne[2] ||
+            r->ne[3] != dst->ne[3] || r->nb[0] != 4 || r->nb[1] % 4 != 0 || !rows_uniform(r))
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: add must be F32 shaped like dst: " + shape(r));
+        fz.res = static_cast<const float*>(r->data);
+        fz.ldr = (int64_t)(r->nb[1] / 4);
+    }
+    if (p.M == 0) return GQ_OK;
+    if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
+    return gemv(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, static_cast<const float*>(b->data),
+                p.x_stride, p.M, static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), fz, (hipStream_t)stream);
 }
 
 int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n_bad, gq_stream_t stream) {

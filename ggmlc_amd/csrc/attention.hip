@@ -28,24 +28,214 @@ constexpr int CH = 64;   // kv rows per chunk
 constexpr int QT = 16;   // query vectors per tile
 constexpr int TARGET_WG = 1024;
 
+constexpr int DEC_MAX_NQ = 8;     // query vectors per kv head served by the decode kernel
+constexpr int DEC_TARGET_WG = 512;
+constexpr int MAX_SPLIT = 1024;
+
 struct Plan {
     int64_t G, NQ, n_qt, n_chunks, cps, n_split;
+    bool dec;               // k_attn_dec: one workgroup per (split, kv head), all NQ queries
+    int64_t rows_per_split;  // dec only
 };
 
 Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
-    (void)D;
     Plan p;
     p.G = Hq / Hkv;
     p.NQ = p.G * S;
     p.n_qt = cdiv(p.NQ, QT);
     p.n_chunks = cdiv(n_kv, CH);
+    p.dec = p.NQ <= DEC_MAX_NQ && (D == 64 || D == 128);
+    if (p.dec) {
+        const int64_t rows_it = 4 * (64 / (D / 8));  // rows one iteration of 4 waves covers
+        const int64_t want = cdiv(DEC_TARGET_WG, Hkv);
+        int64_t rps = cdiv(cdiv(n_kv, want), rows_it) * rows_it;
+        if (rps < 2 * rows_it) rps = 2 * rows_it;
+        if (cdiv(n_kv, rps) > MAX_SPLIT) rps = cdiv(cdiv(n_kv, MAX_SPLIT), rows_it) * rows_it;
+        p.rows_per_split = rps;
+        p.n_split = cdiv(n_kv, rps);
+        p.cps = 0;
+        return p;
+    }
     const int64_t base = Hkv * p.n_qt;
     int64_t want = base >= TARGET_WG ? 1 : cdiv(TARGET_WG, base);
     if (want > p.n_chunks) want = p.n_chunks;
     if (want < 1) want = 1;
     p.cps = cdiv(p.n_chunks, want);
     p.n_split = cdiv(p.n_chunks, p.cps);
+    p.rows_per_split = 0;
     return p;
+}
+
+__device__ __forceinline__ void h8_to_f(const uint4 w, float* f) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        f[2 * e] = h2f((uint16_t)(u[e] & 0xffff));
+        f[2 * e + 1] = h2f((uint16_t)(u[e] >> 16));
+    }
+}
+
+// Decode attention: few query vectors per kv head (G*S <= 8). A workgroup owns
+// (split, kv head) and rows [split*rps, (split+1)*rps) of the KV view. Each
+// wave instruction reads 64/(D/8) whole K (or V) rows, 16 bytes per lane, so
+// every lane group of D/8 lanes is a row stream with its own online-softmax
+// state (m, l, o[8 dims] per query); rows whose mask is -inf for every query
+// are not read. Streams merge by shuffles inside the wave and through LDS across
+// the 4 waves; the result is the output (one split) or an fp32 partial
+// (O, max, sum) for k_attn_merge.
+template <int D, int NQ>
+__global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int64_t rps, int n_split, float m0,
+                                                  float m1, uint32_t n_head_log2, int q_f16,
+                                                  float* __restrict__ part) {
+    constexpr int LPR = D / 8;       // lanes per row
+    constexpr int RPI = 64 / LPR;    // rows per wave instruction
+    constexpr int ROWS_IT = 4 * RPI;
+    __shared__ float sM[4][NQ], sL[4][NQ];
+    __shared__ __align__(16) float sO[4][NQ][D];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = lane / LPR, d0 = (lane % LPR) * 8;
+    const int split = blockIdx.x, hk = blockIdx.y;
+    const int Hkv = (int)a.Hkv;
+
+    float q[NQ][8], slope[NQ];
+    const uint16_t* mrow[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+        const int uu = u < nq ? u : 0;
+        const int64_t h = (int64_t)hk * G + uu % G, i = uu / G;
+        const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + i * a.qnb1 +
+                                                         h * a.qnb2) + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            q[u][e] = qp[e];  // q rows need only 4-byte alignment
+            if (q_f16) q[u][e] = (float)(_Float16)q[u][e];
+            q[u][e] *= a.scale;  // folded: (q*scale).k, the order ggml's tiled path uses is irrelevant at 1e-6
+        }
+        slope[u] = 1.0f;
+        if (a.max_bias > 0.0f)
+            slope[u] = h < n_head_log2 ? powf(m0, (float)(h + 1)) : powf(m1, (float)(2 * (h - n_head_log2) + 1));
+        mrow[u] = a.mask ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(a.mask) + i * a.mnb1)
+                         : nullptr;
+    }
+
+    float m[NQ], l[NQ], o[NQ][8];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+        m[u] = -INFINITY, l[u] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[u][e] = 0.0f;
+    }
+
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.k) + (int64_t)hk * a.knb2 + d0 * 2;
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.v) + (int64_t)hk * a.vnb2 + d0 * 2;
+    const int64_t r_begin = (int64_t)split * rps;
+    const int64_t r_end = min<int64_t>(a.n_kv, r_begin + rps);
+
+    // two rows per lane stream in flight: rows r and r + ROWS_IT
+    for (int64_t r = r_begin + wave * RPI + grp; r < r_end; r += 2 * ROWS_IT) {
+        int64_t rr[2] = {r, r + ROWS_IT};
+        float mk[2][NQ];
+        bool live[2];
+        uint4 kw[2], vw[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const bool in = rr[t] < r_end;
+            live[t] = false;
+#pragma unroll
+            for (int u = 0; u < NQ; ++u) {
+                float mv = 0.0f;
+                if (!in || u >= nq) mv = -INFINITY;
+                else if (mrow[u]) {
+                    const float x = h2f(mrow[u][rr[t]]);
+                    mv = x == -INFINITY ? -INFINITY : slope[u] * x;
+                }
+                mk[t][u] = mv;
+                live[t] = live[t] || mv != -INFINITY;
+            }
+            kw[t] = make_uint4(0, 0, 0, 0), vw[t] = make_uint4(0, 0, 0, 0);
+            if (live[t]) {
+                kw[t] = *reinterpret_cast<const uint4*>(kbase + rr[t] * a.knb1);
+                vw[t] = *reinterpret_cast<const uint4*>(vbase + rr[t] * a.vnb1);
+            }
+        }
+        float kf[2][8], vf[2][8];
+        h8_to_f(kw[0], kf[0]), h8_to_f(kw[1], kf[1]);
+        h8_to_f(vw[0], vf[0]), h8_to_f(vw[1], vf[1]);
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            float sc[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = fmaf(q[u][e], kf[t][e], acc);
+                acc = xor_sum<LPR>(acc);
+                if (a.softcap != 0.0f) acc = a.softcap * tanhf(acc);
+                sc[t] = mk[t][u] == -INFINITY ? -INFINITY : acc + mk[t][u];
+            }
+            const float mn = fmaxf(m[u], fmaxf(sc[0], sc[1]));
+            if (mn == -INFINITY) continue;
+            const float al = __expf(m[u] - mn);  // exp(-inf) = 0 for an empty stream
+            const float p0 = __expf(sc[0] - mn), p1 = __expf(sc[1] - mn);
+            l[u] = l[u] * al + p0 + p1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[u][e] = fmaf(p1, vf[1][e], fmaf(p0, vf[0][e], o[u][e] * al));
+            m[u] = mn;
+        }
+    }
+
+    // merge the row streams of the wave (lanes xor LPR, 2 LPR, ...)
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            const float mo = __shfl_xor(m[u], off, 64), lo = __shfl_xor(l[u], off, 64);
+            float oo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) oo[e] = __shfl_xor(o[u][e], off, 64);
+            const float mn = fmaxf(m[u], mo);
+            if (mn == -INFINITY) continue;
+            const float a1 = __expf(m[u] - mn), a2 = __expf(mo - mn);
+            l[u] = l[u] * a1 + lo * a2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[u][e] = o[u][e] * a1 + oo[e] * a2;
+            m[u] = mn;
+        }
+    }
+    if (grp == 0) {
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+            *reinterpret_cast<float4*>(&sO[wave][u][d0]) = make_float4(o[u][0], o[u][1], o[u][2], o[u][3]);
+            *reinterpret_cast<float4*>(&sO[wave][u][d0 + 4]) = make_float4(o[u][4], o[u][5], o[u][6], o[u][7]);
+            if (lane == 0) sM[wave][u] = m[u], sL[wave][u] = l[u];
+        }
+    }
+    __syncthreads();
+    // merge the 4 waves and write
+    for (int idx = tid; idx < nq * D; idx += 256) {
+        const int u = idx / D, d = idx % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sM[w][u]);
+        float L = 0.0f, acc = 0.0f;
+        if (mx != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = __expf(sM[w][u] - mx);
+                L += sL[w][u] * f;
+                acc += sO[w][u][d] * f;
+            }
+        }
+        const int64_t h = (int64_t)hk * G + u % G, i = u / G;
+        if (n_split == 1) {
+            a.dst[(i * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
+        } else {
+            float* pp = part + (((int64_t)split * Hkv + hk) * nq + u) * (D + 2);
+            pp[2 + d] = acc;
+            if (d == 0) pp[0] = mx, pp[1] = L;
+        }
+    }
 }
 
 template <int D>
@@ -242,22 +432,40 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps
     }
 }
 
+// Merge of split partials (ops.cpp:9060-9128): weights w_s = exp(m_s - max) are
+// computed once in LDS, then each thread sums its dimension over the splits with
+// independent loads.
 template <int D>
 __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part, int n_split, int Hkv, int NQ,
                                                   int G, int64_t Hq, float* __restrict__ dst) {
+    __shared__ float sW[MAX_SPLIT];
+    __shared__ float sRed[D / 64 > 0 ? D / 64 : 1];
     const int qv = blockIdx.x;
     const int hk = blockIdx.y;
     const int d = threadIdx.x;
+    const int64_t stride = (int64_t)Hkv * NQ * (D + 2);
+    const float* base = part + ((int64_t)hk * NQ + qv) * (D + 2);
     float mx = -INFINITY;
-    for (int s = 0; s < n_split; ++s)
-        mx = fmaxf(mx, part[(((int64_t)s * Hkv + hk) * NQ + qv) * (D + 2)]);
+    for (int s = d; s < n_split; s += D) {
+        const float ms = base[s * stride], ls = base[s * stride + 1];
+        const float mv = ls == 0.0f ? -INFINITY : ms;
+        sW[s] = mv;
+        mx = fmaxf(mx, mv);
+    }
+    mx = xor_max<64>(mx);
+    if ((d & 63) == 0) sRed[d >> 6] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < D / 64; ++w) mx = fmaxf(mx, sRed[w]);
+    __syncthreads();
+    for (int s = d; s < n_split; s += D) sW[s] = sW[s] == -INFINITY ? 0.0f : __expf(sW[s] - mx);
+    __syncthreads();
     float L = 0.0f, acc = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < n_split; ++s) {
-        const float* pp = part + (((int64_t)s * Hkv + hk) * NQ + qv) * (D + 2);
-        if (pp[1] == 0.0f) continue;
-        const float w = __expf(pp[0] - mx);
-        L += pp[1] * w;
-        acc += pp[2 + d] * w;
+        const float w = sW[s];
+        L += base[s * stride + 1] * w;
+        acc += base[s * stride + 2 + d] * w;
     }
     const int64_t h = (int64_t)hk * G + qv % G;
     const int64_t i = qv / G;
@@ -285,14 +493,34 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     AttnArgs b = a;
     if (b.softcap != 0.0f) b.scale /= b.softcap;
     const int q_f16 = a.S < 64 ? 1 : 0;
-    const dim3 grid((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)p.n_qt);
     float* part = reinterpret_cast<float*>(ws);
+    if (p.dec) {
+        const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv);
+        const int nq = (int)p.NQ, G = (int)p.G, ns = (int)p.n_split;
+#define GQ_DEC(DD, NN)                                                                                         \
+    hipLaunchKernelGGL((k_attn_dec<DD, NN>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
+                       n_head_log2, q_f16, part)
+        if (a.D == 128) {
+            if (nq == 1) GQ_DEC(128, 1);
+            else if (nq == 2) GQ_DEC(128, 2);
+            else if (nq <= 4) GQ_DEC(128, 4);
+            else GQ_DEC(128, 8);
+        } else {
+            if (nq == 1) GQ_DEC(64, 1);
+            else if (nq == 2) GQ_DEC(64, 2);
+            else if (nq <= 4) GQ_DEC(64, 4);
+            else GQ_DEC(64, 8);
+        }
+#undef GQ_DEC
+    } else {
+    const dim3 grid((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)p.n_qt);
     if (a.D == 128)
         hipLaunchKernelGGL(k_attn<128>, grid, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, (int)p.cps, (int)p.n_chunks,
                            (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
     else
         hipLaunchKernelGGL(k_attn<64>, grid, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, (int)p.cps, (int)p.n_chunks,
                            (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
+    }
     int rc = check_hip(hipGetLastError(), "flash_attn_ext launch");
     if (rc != GQ_OK || p.n_split == 1) return rc;
     const dim3 g2((unsigned)p.NQ, (unsigned)a.Hkv);

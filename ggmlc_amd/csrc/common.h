@@ -85,6 +85,39 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---- RMS_NORM sum of squares in one fixed order ----------------------------------
+// Shared by k_rms_norm and the GEMV prologue, so RMS_NORM -> MUL_MAT fused gives the
+// bits of the two ops: lane t of a 256-lane block owns elements [2048 p + 8 t,
+// 2048 p + 8 t + 8) of pass p; each lane sums the fp32 squares in double in element
+// order (passes ascending), then the wave by xor shuffles, then the 4 waves in order
+// (ggml sums in double too: ops.cpp rms_norm_f32, ggml_float).
+__device__ __forceinline__ double sumsq8(const float (&v)[8], double s) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p = v[i] * v[i];
+        s += (double)p;
+    }
+    return s;
+}
+
+// all 256 lanes call it; red: 4 doubles of LDS (free again on return)
+__device__ __forceinline__ double block_sum_d(double s, double* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double r = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return r;
+}
+
+// y = x * rms_scale(...): scale = 1 / sqrt(mean(x^2) + eps), mean rounded to fp32
+__device__ __forceinline__ float rms_scale(double sumsq, int64_t n, float eps) {
+    const float mean = (float)(sumsq / (double)n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
 // ---- activation quantizer core ----------------------------------------------
 // ggml x86 quantize_row_q8_0 (ggml-cpu/arch/x86/quants.c:302-398) for one 32-wide
 // block spread over 4 consecutive lanes of a wave (8 elements each):
@@ -136,19 +169,43 @@ __device__ __forceinline__ void load8(const float* src, bool valid, float (&v)[8
     }
 }
 
+// RMS scales of M activation rows (K % 32 == 0) read from global memory, in the
+// order of sumsq8 / block_sum_d; all 256 lanes call it.
+template <bool VEC, int MM>
+__device__ __forceinline__ void rms_scales(const float* __restrict__ x, int64_t x_stride, int M, int K, float eps,
+                                           float (&scale)[MM], double* red) {
+    const int nb = K / QK;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        if (m >= M) break;
+        double s = 0.0;
+        for (int base = 0; base < nb * 4; base += 256) {
+            const int t = base + (int)threadIdx.x;
+            float v[8];
+            load8<VEC>(x + (int64_t)m * x_stride + (int64_t)t * 8, (t >> 2) < nb, v);
+            s = sumsq8(v, s);
+        }
+        scale[m] = rms_scale(block_sum_d(s, red), K, eps);
+    }
+}
+
 // Quantize M activation rows (K elements, row stride x_stride floats) into the
-// ACT_GS layout at dst (row stride act_bytes), cooperatively by a 256-lane block.
-template <bool VEC>
+// ACT_GS layout at dst (row stride act_bytes), cooperatively by a 256-lane block;
+// row m is multiplied by scale[m] first (1 leaves it unchanged: RMS_NORM fusion).
+template <bool VEC, int MM = 1>
 __device__ __forceinline__ void quantize_rows_to_act(const float* __restrict__ x, int64_t x_stride, int M, int K,
-                                                     uint8_t* dst, int act_bytes) {
+                                                     uint8_t* dst, int act_bytes, const float* scale = nullptr) {
     const int nb = K / QK;
     for (int m = 0; m < M; ++m) {
+        const float sc = scale ? scale[m] : 1.0f;
         for (int base = 0; base < nb * 4; base += 256) {
             const int t = base + (int)threadIdx.x;
             const int b = t >> 2, part = t & 3;
             const bool valid = b < nb;
             float v[8];
             load8<VEC>(x + (int64_t)m * x_stride + (int64_t)b * QK + part * 8, valid, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = v[i] * sc;
             int q[8];
             uint16_t dh;
             int qsum;

@@ -38,13 +38,14 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, i
     const float* xr = reinterpret_cast<const float*>(at(x, r * xnb1));
     float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + r * ynb1);
     double s = 0.0;
-    for (int64_t i = threadIdx.x; i < n; i += 256) s += (double)(xr[i] * xr[i]);
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-    __syncthreads();
-    s = red[0] + red[1] + red[2] + red[3];
-    const float mean = (float)(s / (double)n);
-    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t base = 0; base < n; base += 2048) {  // the order of sumsq8 (shared with the GEMV)
+        const int64_t e0 = base + 8 * (int64_t)threadIdx.x;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = e0 + i < n ? xr[e0 + i] : 0.0f;
+        s = sumsq8(v, s);
+    }
+    const float scale = rms_scale(block_sum_d(s, red), n, eps);
     for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = xr[i] * scale;
 }
 

@@ -108,12 +108,38 @@ __device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, con
     }
 }
 
+// Physical weight row of logical row r: with the SWIGLU epilogue, logical rows
+// 2c and 2c+1 are the gate row c and the up row c + N/2, so both land in the same
+// wave (rows of a wave are 4 consecutive logical rows).
+__device__ __forceinline__ int64_t phys_row(const GemvFuse& fz, int64_t r) {
+    return fz.glu ? (r >> 1) + (r & 1) * fz.glu_half : r;
+}
+
+// silu(g) * u with the arithmetic of k_swiglu (x / (1 + expf(-x)) * g)
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float sg = g / (1.0f + expf(-g));
+    return sg * u;
+}
+
+// Write logical row `row` of activation m: plain, residual-added (res + v: the
+// operand order of ADD(x, MUL_MAT)), or, for the SWIGLU epilogue, from the even
+// row with its partner's value vp.
+__device__ __forceinline__ void emit(const GemvFuse& fz, float* dst, int64_t ldd, int m, int64_t row, float v,
+                                     float vp) {
+    if (fz.glu) {
+        if ((row & 1) == 0) dst[(int64_t)m * ldd + (row >> 1)] = swiglu1(v, vp);
+        return;
+    }
+    if (fz.res) v = fz.res[(int64_t)m * fz.ldr + row] + v;
+    dst[(int64_t)m * ldd + row] = v;
+}
+
 template <int QT, int M, bool XVEC, int PF, int KS>
 __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__ W, int64_t N,
                                                      int64_t row_bytes, int G,
                                                      const float* __restrict__ x,
-                                                     int64_t x_stride, float* __restrict__ dst,
-                                                     int64_t ldd) {
+                                                     int64_t x_stride, float* dst,
+                                                     int64_t ldd, GemvFuse fz) {
     constexpr int GB = QTraits<QT>::GB;
     constexpr int CPG = QTraits<QT>::CPG;
     constexpr int SEG = LPR * CPG;       // chunks of one row per step
@@ -122,6 +148,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     constexpr int ROWS = RG * RPW;       // rows per workgroup tile
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float red[WAVES][M][RPW];
+    __shared__ double red_d[4];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -179,7 +206,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             const bool ok = rr < N && within < ngr * CPG;
             const int64_t boff = (int64_t)gfirst * GB + (int64_t)within * 16;
             // always-valid address, zeroed after the load: no branch per chunk
-            uint4 v = ld_nt16(W + (ok ? rr * row_bytes + boff : 0));
+            uint4 v = ld_nt16(W + (ok ? phys_row(fz, rr) * row_bytes + boff : 0));
             if (!ok) v = make_uint4(0, 0, 0, 0);
             dstv[c] = v;
         }
@@ -189,12 +216,27 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         if (s < F) load_step(s, pre[s]);
     __builtin_amdgcn_sched_barrier(0);
 
+    float scale[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) scale[m] = 1.0f;
     if (xpre) {
+        if (fz.rms) {  // RMS_NORM fused: the rows' squares are already in registers
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                double sq = 0.0;
+#pragma unroll
+                for (int p = 0; p < XPMAX; ++p)
+                    if (p < M * XP && p / XP == m) sq = sumsq8(xr[p], sq);
+                scale[m] = rms_scale(block_sum_d(sq, red_d), (int64_t)G * 256, fz.eps);
+            }
+        }
 #pragma unroll
         for (int p = 0; p < XPMAX; ++p) {
             if (p < M * XP) {  // uniform across the workgroup
                 const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
                 const int b = t >> 2, part = t & 3;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xr[p][i] = xr[p][i] * scale[m];
                 int q[8];
                 uint16_t dh;
                 int qsum;
@@ -217,7 +259,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             }
         }
     } else {
-        quantize_rows_to_act<XVEC>(x, x_stride, M, G * 256, s_act, act_bytes);
+        if (fz.rms) rms_scales<XVEC, M>(x, x_stride, M, G * 256, fz.eps, scale, red_d);
+        quantize_rows_to_act<XVEC, M>(x, x_stride, M, G * 256, s_act, act_bytes, scale);
     }
     __syncthreads();  // quantized activation visible to all waves
 
@@ -280,7 +323,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                 const float v = xor_sum<LPR>(acc[m]);
                 acc[m] = 0.0f;
                 if constexpr (KS == 1) {
-                    if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
+                    const float vp = __shfl_xor(v, LPR, 64);  // the next row's value (SWIGLU pairs)
+                    if (gsub == 0 && row < N) emit(fz, dst, ldd, m, row, v, vp);
                 } else {
                     if (gsub == 0) red[wave][m][rsub] = v;
                 }
@@ -290,118 +334,13 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                 if (kp == 0 && gsub == 0 && row < N) {
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
-                        float v = red[wave][m][rsub];
+                        float v = red[wave][m][rsub], vp = red[wave][m][rsub ^ 1];
 #pragma unroll
-                        for (int k = 1; k < KS; ++k) v += red[wave + k][m][rsub];
-                        dst[(int64_t)m * ldd + row] = v;
+                        for (int k = 1; k < KS; ++k) v += red[wave + k][m][rsub], vp += red[wave + k][m][rsub ^ 1];
+                        emit(fz, dst, ldd, m, row, v, vp);
                     }
                 }
                 __syncthreads();
-            }
-        }
-    }
-}
-
-// ---- direct variant: each lane loads its own group (no LDS staging) ---------------
-// The 9 (Q4_0) or 17 (Q8_0) 16-byte loads of a lane are contiguous; across the
-// wave one instruction touches 64 lines, and the following instructions hit the
-// same lines while their misses are still pending (merged in the L1 miss queue).
-// Without the staging slice the kernel needs far fewer registers and only the
-// activation in LDS, so more waves are resident.
-template <int QT, int M, bool XVEC, int PF, bool COPY>
-__global__ __launch_bounds__(256) void k_gemv_dir(const uint8_t* __restrict__ W, int64_t N,
-                                                  int64_t row_bytes, int G,
-                                                  const float* __restrict__ x,
-                                                  int64_t x_stride, float* __restrict__ dst,
-                                                  int64_t ldd) {
-    constexpr int GB = QTraits<QT>::GB;
-    constexpr int CPG = QTraits<QT>::CPG;
-    extern __shared__ __align__(16) uint8_t smem[];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int act_bytes = G * ACT_GS;
-    uint8_t* s_act = smem;
-
-    const int rsub = lane / LPR;
-    const int gsub = lane % LPR;
-    const int J = (G + LPR - 1) / LPR;
-
-    const int64_t n_tiles = (N + RPW - 1) / RPW;
-    const int64_t total = (int64_t)gridDim.x * WAVES;
-    const int64_t gw = (int64_t)blockIdx.x * WAVES + wave;
-    const int64_t my_tiles = gw < n_tiles ? (n_tiles - gw + total - 1) / total : 0;
-    const int64_t F = my_tiles * J;
-
-    uint4 pre[PF][CPG];
-    auto load_step = [&](int64_t f, uint4(&dstv)[CPG]) {
-        const int64_t tile = gw + (f / J) * total;
-        const int j = (int)(f % J);
-        const int64_t rr = tile * RPW + rsub;
-        const int g = j * LPR + gsub;
-        const uint8_t* p = W + rr * row_bytes + (int64_t)g * GB;
-        const bool ok = rr < N && g < G;
-#pragma unroll
-        for (int c = 0; c < CPG; ++c) dstv[c] = ok ? ld_nt16(p + 16 * c) : make_uint4(0, 0, 0, 0);
-    };
-#pragma unroll
-    for (int s = 0; s < PF; ++s)
-        if (s < F) load_step(s, pre[s]);
-
-    quantize_rows_to_act<XVEC>(x, x_stride, M, G * 256, s_act, act_bytes);
-    __syncthreads();
-
-    float acc[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
-
-    for (int64_t f = 0; f < F; ++f) {
-        const int64_t tile = gw + (f / J) * total;
-        const int j = (int)(f % J);
-        const int64_t row = tile * RPW + rsub;
-        uint32_t w[4 * CPG];
-#pragma unroll
-        for (int c = 0; c < CPG; ++c) {
-            w[4 * c + 0] = pre[0][c].x;
-            w[4 * c + 1] = pre[0][c].y;
-            w[4 * c + 2] = pre[0][c].z;
-            w[4 * c + 3] = pre[0][c].w;
-        }
-        if constexpr (COPY) {  // issue the next step before decoding this one
-#pragma unroll
-            for (int s = 0; s + 1 < PF; ++s)
-#pragma unroll
-                for (int c = 0; c < CPG; ++c) pre[s][c] = pre[s + 1][c];
-            if (f + PF < F) load_step(f + PF, pre[PF - 1]);
-        }
-        const int g = j * LPR + gsub;
-        if (row < N && g < G) {
-#pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                uint32_t hdr;
-                uint32_t q[QTraits<QT>::NQW];
-                decode_at<QT>(w, QTraits<QT>::BB * b, hdr, q);
-                const float dw = h2f((uint16_t)hdr);
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const uint8_t* ag = s_act + m * act_bytes + g * ACT_GS;
-                    const uint4 a0 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b);
-                    const uint4 a1 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b + 16);
-                    const float da = reinterpret_cast<const float*>(ag + ACT_D_OFF)[b];
-                    const int s = block_dot<QT>(q, a0, a1, ag, b);
-                    acc[m] += (float)s * (dw * da);
-                }
-            }
-        }
-        if constexpr (!COPY) {  // registers are free again: issue the next step
-            if (f + 1 < F) load_step(f + 1, pre[0]);
-        }
-        if (j == J - 1) {
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float v = xor_sum<LPR>(acc[m]);
-                if (gsub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
-                acc[m] = 0.0f;
             }
         }
     }
@@ -413,14 +352,19 @@ template <int QT, int M, bool XVEC>
 __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W, int64_t N,
                                                   int64_t row_bytes, int nb,
                                                   const float* __restrict__ x,
-                                                  int64_t x_stride, float* __restrict__ dst,
-                                                  int64_t ldd) {
+                                                  int64_t x_stride, float* dst,
+                                                  int64_t ldd, GemvFuse fz) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int NQW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double red_d[4];
     const int act_stride = (int)act_row_bytes((int64_t)nb * QK);
     const uint8_t* act = smem;
-    quantize_rows_to_act<XVEC>(x, x_stride, M, nb * QK, smem, act_stride);
+    float scale[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) scale[m] = 1.0f;
+    if (fz.rms) rms_scales<XVEC, M>(x, x_stride, M, nb * QK, fz.eps, scale, red_d);
+    quantize_rows_to_act<XVEC, M>(x, x_stride, M, nb * QK, smem, act_stride, scale);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
@@ -429,7 +373,7 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
     if (row < N) {
-        const uint8_t* rp = W + row * row_bytes;
+        const uint8_t* rp = W + phys_row(fz, row) * row_bytes;
         for (int b = sub; b < nb; b += LPR) {
             const uint16_t* bp = reinterpret_cast<const uint16_t*>(rp + (int64_t)b * BB);
             const float dw = h2f(bp[0]);
@@ -451,7 +395,8 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         const float v = xor_sum<LPR>(acc[m]);
-        if (sub == 0 && row < N) dst[(int64_t)m * ldd + row] = v;
+        const float vp = __shfl_xor(v, LPR, 64);
+        if (sub == 0 && row < N) emit(fz, dst, ldd, m, row, v, vp);
     }
 }
 
@@ -497,23 +442,9 @@ int resident_wgs(KFn* fn, size_t lds, int& out) {
     return GQ_OK;
 }
 
-// Weight-load scheme (GQ_GEMV_VARIANT, for measurement): 0 stage (LDS transpose,
-// register pipeline), 1 direct + copy (next step issued before decoding),
-// 2 direct without copy (next step issued after decoding), 3 direct, 2 steps.
-// Measured on MI355X the direct variants run ~2.4x slower than the staged one.
-int gemv_variant() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("GQ_GEMV_VARIANT");
-        v = e ? atoi(e) : 0;
-        if (v < 0 || v > 3) v = 0;
-    }
-    return v;
-}
-
 template <int QT, int M, bool XVEC, int PF, int KS>
 int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-                  float* dst, int64_t ldd, hipStream_t s, size_t lds, int resident) {
+                  float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s, size_t lds, int resident) {
     const int G = (int)(K / 256);
     const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
     auto* fn = &k_gemv_grp<QT, M, XVEC, PF, KS>;
@@ -522,66 +453,45 @@ int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_
     if (rc) return rc;
     const int64_t tiles = cdiv(N, (WAVES / KS) * RPW);
     const dim3 grid((unsigned)(tiles < resident ? tiles : resident));
-    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, x, x_stride, dst, ldd);
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, x, x_stride, dst, ldd, fz);
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
 template <int QT, int M, bool XVEC, int PF>
 int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-                  float* dst, int64_t ldd, hipStream_t s) {
+                  float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int G = (int)(K / 256);
-    const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
-    const int variant = gemv_variant();
-    const bool direct = variant != 0;
-    const size_t lds = (size_t)M * G * ACT_GS + (direct ? 0 : (size_t)WAVES * 64 * QTraits<QT>::GB);
+    const size_t lds = (size_t)M * G * ACT_GS + (size_t)WAVES * 64 * QTraits<QT>::GB;
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
-    if (!direct) {
-        // residency is the same for every KS (same registers and LDS)
-        int resident = 0;
-        int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1>, lds, resident);
-        if (rc) return rc;
-        // split K over the waves of a workgroup (whole steps per wave) only when
-        // the row tiles leave most CUs without a workgroup (measured: splitting a
-        // 4096-row down projection is slower, a 1536-row one faster)
-        const int64_t t1 = cdiv(N, WAVES * RPW);
-        const int J = (G + LPR - 1) / LPR;
-        if (4 * t1 >= resident || J < 2)
-            return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, x, x_stride, dst, ldd, s, lds, resident);
-        if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, x, x_stride, dst, ldd, s, lds, resident);
-        return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, x, x_stride, dst, ldd, s, lds, resident);
-    }
-    decltype(&k_gemv_dir<QT, M, XVEC, 1, true>) fn;
-    switch (variant) {
-        case 2: fn = &k_gemv_dir<QT, M, XVEC, 1, false>; break;
-        case 3: fn = &k_gemv_dir<QT, M, XVEC, 2, true>; break;
-        default: fn = &k_gemv_dir<QT, M, XVEC, 1, true>; break;
-    }
-    static size_t allowed[4] = {0, 0, 0, 0};
-    int rc = allow_big_lds(fn, allowed[variant], lds);
-    if (rc) return rc;
+    // residency is the same for every KS (same registers and LDS)
     int resident = 0;
-    rc = resident_wgs(fn, lds, resident);
+    int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1>, lds, resident);
     if (rc) return rc;
-    const int64_t wg_needed = cdiv(N, WAVES * RPW);
-    const dim3 grid((unsigned)(wg_needed < resident ? wg_needed : resident));
-    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, x, x_stride, dst, ldd);
-    return check_hip(hipGetLastError(), "gemv launch");
+    // split K over the waves of a workgroup (whole steps per wave) only when
+    // the row tiles leave most CUs without a workgroup (measured: splitting a
+    // 4096-row down projection is slower, a 1536-row one faster)
+    const int64_t t1 = cdiv(N, WAVES * RPW);
+    const int J = (G + LPR - 1) / LPR;
+    if (4 * t1 >= resident || J < 2)
+        return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, x, x_stride, dst, ldd, fz, s, lds, resident);
+    if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, x, x_stride, dst, ldd, fz, s, lds, resident);
+    return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, x, x_stride, dst, ldd, fz, s, lds, resident);
 }
 
 // Q4_0 keeps two steps of weight loads in flight per wave
 template <int QT, int M, bool XVEC>
 int launch_grp(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-               float* dst, int64_t ldd, hipStream_t s) {
+               float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     if constexpr (QT == GQ_TYPE_Q8_0) {
-        return launch_grp_pf<QT, M, XVEC, 1>(W, N, K, x, x_stride, dst, ldd, s);
+        return launch_grp_pf<QT, M, XVEC, 1>(W, N, K, x, x_stride, dst, ldd, fz, s);
     } else {
-        return launch_grp_pf<QT, M, XVEC, 2>(W, N, K, x, x_stride, dst, ldd, s);
+        return launch_grp_pf<QT, M, XVEC, 2>(W, N, K, x, x_stride, dst, ldd, fz, s);
     }
 }
 
 template <int QT, int M, bool XVEC>
 int launch_blk(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-               float* dst, int64_t ldd, hipStream_t s) {
+               float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int nb = (int)(K / QK);
     const int64_t row_bytes = (int64_t)nb * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
     const size_t lds = (size_t)M * act_row_bytes(K);
@@ -591,30 +501,30 @@ int launch_blk(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x
     if (rc) return rc;
     const dim3 grid((unsigned)cdiv(N, 256 / LPR));
     hipLaunchKernelGGL((k_gemv_blk<QT, M, XVEC>), grid, dim3(256), lds, s, W, N, row_bytes, nb, x,
-                       x_stride, dst, ldd);
+                       x_stride, dst, ldd, fz);
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
 template <int QT, int M>
 int launch_m(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride, float* dst,
-             int64_t ldd, hipStream_t s) {
+             int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const bool grp = (K % 256 == 0) && ((reinterpret_cast<uintptr_t>(W) & 15) == 0);
     const bool xvec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (x_stride % 4 == 0);
     if (grp)
-        return xvec ? launch_grp<QT, M, true>(W, N, K, x, x_stride, dst, ldd, s)
-                    : launch_grp<QT, M, false>(W, N, K, x, x_stride, dst, ldd, s);
-    return xvec ? launch_blk<QT, M, true>(W, N, K, x, x_stride, dst, ldd, s)
-                : launch_blk<QT, M, false>(W, N, K, x, x_stride, dst, ldd, s);
+        return xvec ? launch_grp<QT, M, true>(W, N, K, x, x_stride, dst, ldd, fz, s)
+                    : launch_grp<QT, M, false>(W, N, K, x, x_stride, dst, ldd, fz, s);
+    return xvec ? launch_blk<QT, M, true>(W, N, K, x, x_stride, dst, ldd, fz, s)
+                : launch_blk<QT, M, false>(W, N, K, x, x_stride, dst, ldd, fz, s);
 }
 
 template <int QT>
 int gemv_t(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride, int64_t M,
-           float* dst, int64_t ldd, hipStream_t s) {
+           float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     switch (M) {
-        case 1: return launch_m<QT, 1>(W, N, K, x, x_stride, dst, ldd, s);
-        case 2: return launch_m<QT, 2>(W, N, K, x, x_stride, dst, ldd, s);
-        case 3: return launch_m<QT, 3>(W, N, K, x, x_stride, dst, ldd, s);
-        case 4: return launch_m<QT, 4>(W, N, K, x, x_stride, dst, ldd, s);
+        case 1: return launch_m<QT, 1>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        case 2: return launch_m<QT, 2>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        case 3: return launch_m<QT, 3>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        case 4: return launch_m<QT, 4>(W, N, K, x, x_stride, dst, ldd, fz, s);
         default: return fail(GQ_ERR_INVALID, "gemv: M out of range");
     }
 }
@@ -622,9 +532,9 @@ int gemv_t(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_str
 }  // namespace
 
 int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-         int64_t M, float* dst, int64_t ldd, hipStream_t s) {
-    if (type == GQ_TYPE_Q8_0) return gemv_t<GQ_TYPE_Q8_0>(W, N, K, x, x_stride, M, dst, ldd, s);
-    return gemv_t<GQ_TYPE_Q4_0>(W, N, K, x, x_stride, M, dst, ldd, s);
+         int64_t M, float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
+    if (type == GQ_TYPE_Q8_0) return gemv_t<GQ_TYPE_Q8_0>(W, N, K, x, x_stride, M, dst, ldd, fz, s);
+    return gemv_t<GQ_TYPE_Q4_0>(W, N, K, x, x_stride, M, dst, ldd, fz, s);
 }
 
 }  // namespace gq

@@ -14,9 +14,11 @@ then RMS_NORM -> MUL_MAT(lm_head) on the last token only (logits_last_only,
 executor.cpp:2396-2410) -> ARGMAX for greedy decoding. n_kv follows
 pad_kv_len (executor.cpp:58-64): max(256, roundup(pos + s, 256)) capped at max_ctx.
 
-Every op is one libgq call on device tensors; a whole step (embedding to the
-argmax of the next token, plus pos += s) can be captured as one HIP graph per
-(s, n_kv) bucket and replayed without host work.
+Every op is one libgq call on device tensors; decode steps (s <= 4) fuse
+RMS_NORM into the following MUL_MAT, the residual ADD into O / down and SWIGLU into
+gate_up (gq_mul_mat_fused, bit-identical to the separate ops). A whole step
+(embedding to the argmax of the next token, plus pos += s) can be captured as one
+HIP graph per (s, n_kv) bucket and replayed without host work.
 """
 
 from __future__ import annotations
@@ -172,13 +174,17 @@ class Decoder:
 
     # -- one step -------------------------------------------------------------
     def step(self, s: int, n_kv: int, ids: torch.Tensor | None = None, advance: bool = True,
-             trace: list | None = None) -> torch.Tensor:
+             trace: list | None = None, fused: bool | None = None) -> torch.Tensor:
         """Run s tokens (ids int32 [s], default: this bucket's ids buffer) at the device
         position; returns the argmax of the last token's logits (device int32 [1]).
 
+        fused (default: s <= 4 without a trace): run RMS_NORM -> MUL_MAT, MUL_MAT -> ADD
+        and MUL_MAT -> SWIGLU as single GEMV launches (gq_mul_mat_fused, bit-identical).
         trace (eager only): receives (name, layer, copy) of every op's output, so a
         checker can recompute each op from the inputs this step actually used."""
         c, b, ws = self.cfg, self._buffers(s), self.ws
+        if fused is None:
+            fused = s <= 4 and trace is None
 
         def rec(name, li, t):
             if trace is not None:
@@ -197,9 +203,12 @@ class Decoder:
         qd, kvd = c.q_dim, c.kv_dim
         for li, L in enumerate(self.w.layers):
             rec("x_in", li, x)
-            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
-            rec("h1", li, h)
-            qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
+            if fused:
+                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps)
+            else:
+                h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+                rec("h1", li, h)
+                qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
             rec("qkv", li, qkv)
             # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
             qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
@@ -214,21 +223,31 @@ class Decoder:
             ops.flash_attn_ext(q[0].permute(1, 0, 2), self.k_cache[li][0, :, :n_kv], self.v_cache[li][0, :, :n_kv],
                                mask, scale, out=b["attn"], ws=ws)
             rec("attn", li, b["attn"])
-            o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
-            ops.add(x, o, out=x)
-            rec("x_mid", li, x)
-            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
-            rec("h2", li, h)
-            gu = ops.mul_mat(L.gate_up, h, out=b["gu"], ws=ws)
-            rec("gu", li, gu)
-            a = ops.swiglu(gu, out=b["act"])
-            rec("act", li, a)
-            d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
-            ops.add(x, d, out=x)
+            if fused:
+                ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=x, add=x)
+                rec("x_mid", li, x)
+                a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True)
+                rec("act", li, a)
+                ops.mul_mat_fused(L.down, a, out=x, add=x)
+            else:
+                o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
+                ops.add(x, o, out=x)
+                rec("x_mid", li, x)
+                h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+                rec("h2", li, h)
+                gu = ops.mul_mat(L.gate_up, h, out=b["gu"], ws=ws)
+                rec("gu", li, gu)
+                a = ops.swiglu(gu, out=b["act"])
+                rec("act", li, a)
+                d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
+                ops.add(x, d, out=x)
             rec("x_out", li, x)
-        h = ops.rms_norm(x[s - 1:], c.rms_eps, out=b["h"][:1])
-        rec("hf", -1, h)
-        logits = ops.mul_mat(self.w.lm_head, h, out=b["logits"], ws=ws)
+        if fused:
+            logits = ops.mul_mat_fused(self.w.lm_head, x[s - 1:], out=b["logits"], rms_eps=c.rms_eps)
+        else:
+            h = ops.rms_norm(x[s - 1:], c.rms_eps, out=b["h"][:1])
+            rec("hf", -1, h)
+            logits = ops.mul_mat(self.w.lm_head, h, out=b["logits"], ws=ws)
         ops.argmax(logits, out=b["next"])
         rec("logits", -1, logits), rec("next", -1, b["next"])
         if advance:

@@ -20,6 +20,7 @@ libgq.so is not built every call raises.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -141,6 +142,27 @@ def mul_mat(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None,
     need = L.gq_mul_mat_workspace_size(a, b)
     ptr, size = _ws(ws).get(need)
     check(L.gq_mul_mat(a, b, d, ptr, size, _stream()))
+    return out
+
+
+def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
+                  swiglu: bool = False, add: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode MUL_MAT (x has at most 4 rows) fused with its graph neighbours, bit-identical
+    to the unfused ops: rms_eps -> RMS_NORM(x) first; swiglu -> SWIGLU of the result's
+    two halves (out [..., N/2]); add -> add + result (add may be out)."""
+    if x.dtype != torch.float32:
+        raise ValueError("mul_mat_fused: x must be float32")
+    n_out = w.N // 2 if swiglu else w.N
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (n_out,), dtype=torch.float32, device=x.device)
+    f = _lib.gq_mul_mat_fusion()
+    if rms_eps is not None:
+        f.rms_norm, f.rms_eps = 1, float(rms_eps)
+    f.swiglu = 1 if swiglu else 0
+    ad = _desc(add) if add is not None else None
+    if ad is not None:
+        f.add = ctypes.pointer(ad)
+    check(_lib.load().gq_mul_mat_fused(w.desc(), _desc(x), _desc(out), ctypes.byref(f), _stream()))
     return out
 
 

@@ -90,3 +90,20 @@ def test_other_entry_points_validate_on_host(lib):
 def test_python_binding_raises(lib):
     with pytest.raises(_lib.GQError):
         _lib.check(-1)
+
+
+def test_mul_mat_fused_rejects_without_device(lib):
+    w = _t(_lib.Q4_0, [4096, 64], [18, 2304])
+    x5 = _t(_lib.F32, [4096, 5], [4, 16384])
+    d5 = _t(_lib.F32, [64, 5], [4, 256])
+    f = _lib.gq_mul_mat_fusion(1, 1e-5, 0, None)
+    assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(f), None) == -2  # M > 4: not the GEMV path
+    assert b"M <= 4" in lib.gq_last_error()
+    x = _t(_lib.F32, [4096, 1], [4, 16384])
+    d64 = _t(_lib.F32, [64, 1], [4, 256])
+    g = _lib.gq_mul_mat_fusion(0, 0.0, 1, None)
+    assert lib.gq_mul_mat_fused(w, x, d64, ctypes.byref(g), None) == -1  # swiglu output is N/2 wide
+    r = _t(_lib.F32, [64, 1], [4, 256])
+    h = _lib.gq_mul_mat_fusion(0, 0.0, 1, ctypes.pointer(r))
+    assert lib.gq_mul_mat_fused(w, x, _t(_lib.F32, [32, 1], [4, 128]), ctypes.byref(h), None) == -1
+    assert b"exclusive" in lib.gq_last_error()

@@ -143,6 +143,44 @@ def test_mul_mat_strided_rows():
     assert mar(y, want) < 1e-3
 
 
+@pytest.mark.parametrize("qtype,K,N,M,rms,glu,add", [
+    (O.Q4_0, 4096, 12288, 1, True, False, False),   # 7B qkv: RMS_NORM -> MUL_MAT
+    (O.Q4_0, 4096, 22016, 1, True, True, False),    # 7B gate_up: RMS_NORM -> MUL_MAT -> SWIGLU
+    (O.Q4_0, 11008, 4096, 1, False, False, True),   # 7B down: MUL_MAT -> ADD (in place)
+    (O.Q4_0, 4096, 4096, 3, True, False, True),     # three rows, both ends fused
+    (O.Q8_0, 960, 5120, 1, True, True, False),      # K % 256 != 0 (block-wise kernel)
+    (O.Q8_0, 2560, 960, 2, False, False, True),     # SmolLM2 down shape
+    (O.Q8_0, 8960, 1536, 1, False, False, True),    # split-K over waves (KS = 4)
+    (O.Q8_0, 8192, 1536, 1, True, True, False),     # split-K (KS = 2) with SWIGLU pairs
+    (O.Q4_0, 4096, 4096, 4, True, True, False),
+])
+def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add):
+    """gq_mul_mat_fused gives exactly the bits of RMS_NORM / MUL_MAT / SWIGLU / ADD run
+    one by one (those are pinned against the oracle above)."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV) * 3.0
+    eps = 1e-5
+    h = ops.rms_norm(x, eps) if rms else x
+    y = ops.mul_mat(w, h)
+    if glu:
+        want = ops.swiglu(y)
+    elif add:
+        r = torch.randn((M, N), generator=g, device=DEV)
+        want = ops.add(r, y)
+    else:
+        want = y
+    if add:
+        got = r.clone()
+        ops.mul_mat_fused(w, x, out=got, rms_eps=eps if rms else None, add=got)  # in place, as the decoder runs it
+    else:
+        got = ops.mul_mat_fused(w, x, rms_eps=eps if rms else None, swiglu=glu)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    assert torch.equal(got, want), (got - want).abs().max().item()
+
+
 # --------------------------------------------------------------- set_rows ---
 
 def test_set_rows_golden(golden_dir):
@@ -214,6 +252,10 @@ def test_flash_attn_golden(golden_dir):
     (15, 5, 64, 4, 300, 1024),      # small chunk
     (8, 2, 128, 64, 200, 512),      # prefill chunk, tiled-path precision
     (32, 32, 128, 512, 0, 1024),    # config 4 pp512 first chunk
+    (4, 2, 128, 2, 100, 512),       # two query rows per kv head pair: per-row masks in the decode kernel
+    (8, 8, 128, 1, 5, 32),          # one split (no merge)
+    (10, 2, 64, 1, 777, 1024),      # G = 5 (decode kernel with 8 query slots, 5 used)
+    (4, 4, 64, 1, 700, 1024),       # D = 64, MHA
 ])
 def test_flash_attn_vs_exact(Hq, Hkv, D, S, pos, ctx):
     rng = np.random.default_rng(Hq * S + pos)

@@ -341,3 +341,39 @@ def test_smollm2_shape_two_layers():
     cfg = replace(SMOLLM2_360M, n_layer=2, n_vocab=4096)
     res, tokens, _ = _run(cfg, prompt_len=20, n_new=3, max_ctx=512, graphs=True)
     _check_end_to_end(res, tokens, 0.9995)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["tiny_q8", "tiny_q4", "smollm2"])
+def test_fused_decode_steps_bit_identical(shape):
+    """Decode steps with RMS_NORM / ADD / SWIGLU fused into the GEMVs give exactly the
+    bits of the unfused graph (logits, next token and the KV rows written), for 1 and 3
+    new tokens; the K = 960 rows of SmolLM2 take the block-wise GEMV."""
+    import torch
+    from dataclasses import replace
+
+    from ggmlc_amd.model import SMOLLM2_360M, LlamaConfig, pad_kv_len
+
+    if shape == "smollm2":
+        cfg = replace(SMOLLM2_360M, n_layer=2, n_vocab=4096)
+    else:
+        cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q8_0 if shape == "tiny_q8" else O.Q4_0)
+    dec, _ = _gpu_model(cfg, 512, seed=11)
+    prompt = torch.from_numpy(np.random.default_rng(4).integers(0, cfg.n_vocab, 40).astype(np.int32)).cuda()
+    dec.step(40, pad_kv_len(40, 512), ids=prompt)
+    for s in (1, 3):
+        p0 = int(dec.pos[0])
+        ids = prompt[:s].clone()
+        n_kv = pad_kv_len(p0 + s, 512)
+        outs = []
+        for fused in (False, True):
+            dec.reset(p0)
+            nxt = dec.step(s, n_kv, ids=ids, fused=fused).clone()
+            logits = dec._buffers(s)["logits"].clone()
+            rows = [torch.cat([kc[0, :, p0:p0 + s], vc[0, :, p0:p0 + s]]) for kc, vc in zip(dec.k_cache, dec.v_cache)]
+            outs.append((logits, nxt, torch.stack(rows)))
+        torch.cuda.synchronize()
+        (la, na, ra), (lb, nb, rb) = outs
+        assert torch.equal(la, lb), (s, (la - lb).abs().max().item())
+        assert torch.equal(na, nb) and torch.equal(ra, rb)
+        assert int(dec.pos[0]) == p0 + s
