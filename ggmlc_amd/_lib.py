@@ -67,6 +67,8 @@ SIGNATURES = {
     "gq_rms_norm": (ctypes.c_int, [_P, _f32, _P, _vp]),
     "gq_rope_ext": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _f32, _f32, _f32,
                                    _f32, _P, _vp]),
+    "gq_rope_kv_store": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, _f32, _f32, _f32, _P, _P, _P,
+                                        _P, _vp, _vp]),
     "gq_add": (ctypes.c_int, [_P, _P, _P, _vp]),
     "gq_get_rows": (ctypes.c_int, [_P, _P, _P, _vp]),
     "gq_argmax": (ctypes.c_int, [_P, _P, _vp]),

@@ -390,6 +390,46 @@ int gq_rope_ext(const gq_tensor* a, const gq_tensor* pos, int n_dims, int mode, 
                 mode == 2, freq_base, freq_scale, attn_factor, (hipStream_t)stream);
 }
 
+int gq_rope_kv_store(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* pos, int n_dims,
+                     int mode, float freq_base, float freq_scale, float attn_factor, const gq_tensor* kv_idx,
+                     gq_tensor* q_out, gq_tensor* k_cache, gq_tensor* v_cache, int32_t* n_bad, gq_stream_t stream) {
+    if (!q || !k || !v || !pos || !kv_idx || !q_out || !k_cache || !v_cache)
+        return fail(GQ_ERR_INVALID, "rope_kv_store: null tensor");
+    for (const gq_tensor* t : {q, k, v, (const gq_tensor*)q_out})
+        if (t->type != GQ_TYPE_F32 || t->nb[0] != 4 || t->ne[3] != 1)
+            return fail(GQ_ERR_INVALID, "rope_kv_store: q/k/v/q_out must be F32 [hd, H, s, 1] with contiguous rows: " +
+                                            shape(t));
+    for (const gq_tensor* t : {(const gq_tensor*)k_cache, (const gq_tensor*)v_cache})
+        if (t->type != GQ_TYPE_F16 || t->nb[0] != 2 || t->ne[3] != 1)
+            return fail(GQ_ERR_INVALID, "rope_kv_store: caches must be F16 [hd, rows, Hkv, 1]: " + shape(t));
+    const int64_t hd = q->ne[0], Hq = q->ne[1], Hkv = k->ne[1], S = q->ne[2];
+    if (k->ne[0] != hd || v->ne[0] != hd || v->ne[1] != Hkv || k->ne[2] != S || v->ne[2] != S ||
+        q_out->ne[0] != hd || q_out->ne[1] != Hq || q_out->ne[2] != S || k_cache->ne[0] != hd ||
+        v_cache->ne[0] != hd || k_cache->ne[2] != Hkv || v_cache->ne[2] != Hkv || k_cache->ne[1] != v_cache->ne[1])
+        return fail(GQ_ERR_INVALID, "rope_kv_store: shape mismatch q " + shape(q) + " k " + shape(k) + " cache " +
+                                        shape(k_cache));
+    if (pos->type != GQ_TYPE_I32 || pos->ne[0] < S || pos->nb[0] != 4 || kv_idx->type != GQ_TYPE_I64 ||
+        kv_idx->ne[0] != S || kv_idx->nb[0] != 8)
+        return fail(GQ_ERR_INVALID, "rope_kv_store: pos must be I32 [>= s], kv_idx I64 [s]");
+    if (mode != 0 && mode != 2) return fail(GQ_ERR_UNSUPPORTED, "rope_kv_store: modes 0 (normal) and 2 (neox) only");
+    if (n_dims <= 0 || n_dims % 2 || n_dims > hd) return fail(GQ_ERR_INVALID, "rope_kv_store: bad n_dims");
+    RopeKvArgs a{};
+    a.q = static_cast<const float*>(q->data), a.qnb1 = (int64_t)q->nb[1], a.qnb2 = (int64_t)q->nb[2];
+    a.k = static_cast<const float*>(k->data), a.knb1 = (int64_t)k->nb[1], a.knb2 = (int64_t)k->nb[2];
+    a.v = static_cast<const float*>(v->data), a.vnb1 = (int64_t)v->nb[1], a.vnb2 = (int64_t)v->nb[2];
+    a.hd = hd, a.Hq = Hq, a.Hkv = Hkv, a.s = S;
+    a.pos = static_cast<const int32_t*>(pos->data);
+    a.qo = static_cast<float*>(q_out->data), a.qonb1 = (int64_t)q_out->nb[1], a.qonb2 = (int64_t)q_out->nb[2];
+    a.kc = static_cast<uint16_t*>(k_cache->data), a.kcnb1 = (int64_t)k_cache->nb[1], a.kcnb2 = (int64_t)k_cache->nb[2];
+    a.vc = static_cast<uint16_t*>(v_cache->data), a.vcnb1 = (int64_t)v_cache->nb[1], a.vcnb2 = (int64_t)v_cache->nb[2];
+    a.rows = k_cache->ne[1];
+    a.idx = static_cast<const int64_t*>(kv_idx->data);
+    a.n_bad = n_bad;
+    a.n_dims = n_dims, a.neox = mode == 2;
+    a.freq_scale = freq_scale, a.attn_factor = attn_factor;
+    return rope_kv(a, freq_base, (hipStream_t)stream);
+}
+
 int gq_add(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream) {
     if (!a || !b || !dst) return fail(GQ_ERR_INVALID, "add: null tensor");
     if (a->type != GQ_TYPE_F32 || b->type != GQ_TYPE_F32 || dst->type != GQ_TYPE_F32)

@@ -52,6 +52,19 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, i
 // ---- ROPE (ops.cpp:5886-6120, ext_factor = 0): theta_i = p * theta_scale^i built by
 // repeated multiplication like ggml_rope_cache_init; NEOX pairs (i, i + n_dims/2),
 // NORMAL pairs (2i, 2i+1); dims >= n_dims are copied.
+// one rotated pair, shared by k_rope and k_rope_kv so the two give the same bits
+__device__ __forceinline__ void rope_pair(float p, int j, float theta_scale, float freq_scale, float attn_factor,
+                                          float x0, float x1, float& y0, float& y1) {
+#pragma clang fp contract(off)
+    float theta = p;
+    for (int t = 0; t < j; ++t) theta *= theta_scale;
+    theta *= freq_scale;
+    const float c = cosf(theta) * attn_factor;
+    const float s = sinf(theta) * attn_factor;
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+
 __global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, int64_t ne0, int64_t ne1, int64_t ne2,
                                               int64_t xnb1, int64_t xnb2, int64_t xnb3, const int32_t* __restrict__ pos,
                                               float* __restrict__ y, int64_t ynb1, int64_t ynb2, int64_t ynb3,
@@ -67,18 +80,59 @@ __global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, int64
     const float p = (float)pos[i2];
     const int half = n_dims / 2;
     for (int j = threadIdx.x; j < half; j += blockDim.x) {
-        float theta = p;
-        for (int t = 0; t < j; ++t) theta *= theta_scale;
-        theta *= freq_scale;
-        const float c = cosf(theta) * attn_factor;
-        const float s = sinf(theta) * attn_factor;
         const int i0 = neox ? j : 2 * j;
         const int i1p = neox ? j + half : 2 * j + 1;
-        const float x0 = xr[i0], x1 = xr[i1p];
-        yr[i0] = x0 * c - x1 * s;
-        yr[i1p] = x0 * s + x1 * c;
+        float y0, y1;
+        rope_pair(p, j, theta_scale, freq_scale, attn_factor, xr[i0], xr[i1p], y0, y1);
+        yr[i0] = y0;
+        yr[i1p] = y1;
     }
     for (int64_t j = n_dims + threadIdx.x; j < ne0; j += blockDim.x) yr[j] = xr[j];
+}
+
+// ROPE(q), ROPE(k), SET_ROWS(k_cache, k), SET_ROWS(v_cache, v) in one launch: block
+// (token i, head h) with h < Hq a query head, then Hkv key heads, then Hkv value heads.
+__global__ __launch_bounds__(64) void k_rope_kv(RopeKvArgs a) {
+    const int64_t i = blockIdx.x;
+    const int64_t h = blockIdx.y;
+    const float p = (float)a.pos[i];
+    const int half = a.n_dims / 2;
+    if (h < a.Hq) {
+        const float* xr = reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1));
+        float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1);
+        for (int j = threadIdx.x; j < half; j += blockDim.x) {
+            const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
+            float y0, y1;
+            rope_pair(p, j, a.theta_scale, a.freq_scale, a.attn_factor, xr[i0], xr[i1], y0, y1);
+            yr[i0] = y0;
+            yr[i1] = y1;
+        }
+        for (int64_t j = a.n_dims + threadIdx.x; j < a.hd; j += blockDim.x) yr[j] = xr[j];
+        return;
+    }
+    const bool is_k = h < a.Hq + a.Hkv;
+    const int64_t kh = is_k ? h - a.Hq : h - a.Hq - a.Hkv;
+    const int64_t row = a.idx[i];
+    if (row < 0 || row >= a.rows) {
+        if (threadIdx.x == 0 && a.n_bad) atomicAdd(a.n_bad, 1);
+        return;
+    }
+    if (is_k) {
+        const float* xr = reinterpret_cast<const float*>(at(a.k, i * a.knb2 + kh * a.knb1));
+        uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + kh * a.kcnb2);
+        for (int j = threadIdx.x; j < half; j += blockDim.x) {
+            const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
+            float y0, y1;
+            rope_pair(p, j, a.theta_scale, a.freq_scale, a.attn_factor, xr[i0], xr[i1], y0, y1);
+            yr[i0] = f2h(y0);
+            yr[i1] = f2h(y1);
+        }
+        for (int64_t j = a.n_dims + threadIdx.x; j < a.hd; j += blockDim.x) yr[j] = f2h(xr[j]);
+    } else {
+        const float* xr = reinterpret_cast<const float*>(at(a.v, i * a.vnb2 + kh * a.vnb1));
+        uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.vc) + row * a.vcnb1 + kh * a.vcnb2);
+        for (int64_t j = threadIdx.x; j < a.hd; j += blockDim.x) yr[j] = f2h(xr[j]);
+    }
 }
 
 // ---- ADD with broadcast of b over a (ggml_can_repeat): y = a + b[i % ne_b]
@@ -135,20 +189,25 @@ __global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ a,
 }
 
 // ---- ARGMAX per row (first index of the maximum, ggml_vec_argmax_f32)
-__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int64_t xnb1, int64_t n,
-                                                int32_t* __restrict__ out) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t xnb1, int64_t n,
+                                                 int32_t* __restrict__ out) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
     const int64_t r = blockIdx.x;
     const float* xr = reinterpret_cast<const float*>(at(x, r * xnb1));
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
-        const float v = xr[i];
-        if (v > best) {
-            best = v;
-            bi = (int)i;
-        }
+    // each lane walks its indices in increasing order (first maximum wins), four loads in flight
+    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 4 * 1024) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = i0 + u * 1024 < n ? xr[i0 + u * 1024] : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (v[u] > best) {
+                best = v[u];
+                bi = (int)(i0 + u * 1024);
+            }
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -166,7 +225,7 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ x, int
     if (threadIdx.x == 0) {
         best = sv[0];
         bi = si[0];
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < 16; ++w)
             if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
                 best = sv[w];
                 bi = si[w];
@@ -204,6 +263,14 @@ int rope(const float* x, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int
     return check_hip(hipGetLastError(), "rope launch");
 }
 
+int rope_kv(const RopeKvArgs& a, float freq_base, hipStream_t s) {
+    if (a.s == 0) return GQ_OK;
+    RopeKvArgs b = a;
+    b.theta_scale = powf(freq_base, -2.0f / a.n_dims);
+    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)a.s, (unsigned)(a.Hq + 2 * a.Hkv)), dim3(64), 0, s, b);
+    return check_hip(hipGetLastError(), "rope_kv launch");
+}
+
 int add(const float* a, const int64_t* ane, const int64_t* anb, const float* b, const int64_t* bne,
         const int64_t* bnb, float* y, const int64_t* ynb, hipStream_t s) {
     const int64_t total = ane[0] * ane[1] * ane[2] * ane[3];
@@ -224,7 +291,7 @@ int get_rows(const uint8_t* a, int atype, int64_t ne0, int64_t anb1, int64_t aro
 
 int argmax(const float* x, int64_t xnb1, int64_t n, int64_t nrows, int32_t* out, hipStream_t s) {
     if (nrows == 0) return GQ_OK;
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)nrows), dim3(256), 0, s, x, xnb1, n, out);
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)nrows), dim3(1024), 0, s, x, xnb1, n, out);
     return check_hip(hipGetLastError(), "argmax launch");
 }
 

@@ -84,6 +84,29 @@ int swiglu(const float* a, int64_t anb1, const float* b, int64_t bnb1, float* y,
            int64_t nrows, hipStream_t s);
 int rms_norm(const float* x, int64_t xnb1, float* y, int64_t ynb1, int64_t n, int64_t nrows, float eps,
              hipStream_t s);
+// ROPE of q and k + SET_ROWS of k and v (F16 caches) in one launch
+struct RopeKvArgs {
+    const float* q;
+    int64_t qnb1, qnb2;  // bytes per head, per token
+    const float* k;
+    int64_t knb1, knb2;
+    const float* v;
+    int64_t vnb1, vnb2;
+    int64_t hd, Hq, Hkv, s;
+    const int32_t* pos;
+    float* qo;
+    int64_t qonb1, qonb2;
+    uint16_t* kc;
+    int64_t kcnb1, kcnb2;  // bytes per cache row, per head
+    uint16_t* vc;
+    int64_t vcnb1, vcnb2;
+    int64_t rows;
+    const int64_t* idx;
+    int32_t* n_bad;
+    int n_dims, neox;
+    float theta_scale, freq_scale, attn_factor;
+};
+int rope_kv(const RopeKvArgs& a, float freq_base, hipStream_t s);
 int rope(const float* x, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int64_t xnb1, int64_t xnb2, int64_t xnb3,
          const int32_t* pos, float* y, int64_t ynb1, int64_t ynb2, int64_t ynb3, int n_dims, int neox, float freq_base,
          float freq_scale, float attn_factor, hipStream_t s);

@@ -14,9 +14,10 @@ then RMS_NORM -> MUL_MAT(lm_head) on the last token only (logits_last_only,
 executor.cpp:2396-2410) -> ARGMAX for greedy decoding. n_kv follows
 pad_kv_len (executor.cpp:58-64): max(256, roundup(pos + s, 256)) capped at max_ctx.
 
-Every op is one libgq call on device tensors; decode steps (s <= 4) fuse
+Every op is one libgq call on device tensors. ROPE(q), ROPE(k) and the two
+SET_ROWS run as one launch (gq_rope_kv_store); decode steps (s <= 4) also fuse
 RMS_NORM into the following MUL_MAT, the residual ADD into O / down and SWIGLU into
-gate_up (gq_mul_mat_fused, bit-identical to the separate ops). A whole step
+gate_up (gq_mul_mat_fused). Both fusions are bit-identical to the separate ops. A whole step
 (embedding to the argmax of the next token, plus pos += s) can be captured as one
 HIP graph per (s, n_kv) bucket and replayed without host work.
 """
@@ -214,12 +215,16 @@ class Decoder:
             qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
             kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
             vv = qkv[:, qd + kvd:].view(1, s, c.n_head_kv, c.head_dim)
-            q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
-            k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
-            # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
-            ops.set_rows(self.k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
-            ops.set_rows(self.v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
-            rec("q", li, q), rec("k", li, k), rec("kc", li, self.k_cache[li]), rec("vc", li, self.v_cache[li])
+            if trace is None:  # ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
+                q = ops.rope_kv_store(qv, kv, vv, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"], b["q"],
+                                      self.k_cache[li], self.v_cache[li])
+            else:
+                q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
+                k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
+                # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
+                ops.set_rows(self.k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
+                ops.set_rows(self.v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
+                rec("q", li, q), rec("k", li, k), rec("kc", li, self.k_cache[li]), rec("vc", li, self.v_cache[li])
             ops.flash_attn_ext(q[0].permute(1, 0, 2), self.k_cache[li][0, :, :n_kv], self.v_cache[li][0, :, :n_kv],
                                mask, scale, out=b["attn"], ws=ws)
             rec("attn", li, b["attn"])

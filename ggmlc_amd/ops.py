@@ -237,6 +237,19 @@ def rope_ext(x: torch.Tensor, pos: torch.Tensor, n_dims: int, mode: int = 2, fre
     return out
 
 
+def rope_kv_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.Tensor, n_dims: int, mode: int,
+                  freq_base: float, kv_idx: torch.Tensor, q_out: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, freq_scale: float = 1.0, attn_factor: float = 1.0,
+                  n_bad: torch.Tensor | None = None) -> torch.Tensor:
+    """rope_ext(q) -> q_out and rope_ext(k), v -> set_rows into the F16 caches, one launch.
+    q/k/v ``[1, s, H, hd]`` fp32 views; caches ``[1, Hkv, rows, hd]`` fp16; kv_idx int64 [s]."""
+    nb_ptr = n_bad.data_ptr() if n_bad is not None else None
+    check(_lib.load().gq_rope_kv_store(_desc(q), _desc(k), _desc(v), _desc(pos), n_dims, mode, freq_base, freq_scale,
+                                       attn_factor, _desc(kv_idx), _desc(q_out), _desc(k_cache), _desc(v_cache),
+                                       nb_ptr, _stream()))
+    return q_out
+
+
 def add(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """ggml_add(a, b) with b repeated over a."""
     if out is None:

@@ -186,6 +186,21 @@ int gq_rope_ext(const gq_tensor* a, const gq_tensor* pos, int n_dims, int mode, 
                 float freq_scale, float ext_factor, float attn_factor, float beta_fast, float beta_slow,
                 gq_tensor* dst, gq_stream_t stream);
 
+/* ROPE of q and k plus SET_ROWS of k and v: the node sequence between the fused QKV
+ * projection and FLASH_ATTN_EXT (executor.cpp:2034-2090 rope, :2181-2184 set_rows) in
+ * one launch, bit-identical to
+ *   q_out = gq_rope_ext(q); k' = gq_rope_ext(k);
+ *   gq_set_rows(k_cache, permute(k', 0, 2, 1, 3), kv_idx); gq_set_rows(v_cache, permute(v, ...), kv_idx)
+ *   q, k, v  F32 [hd, H, s, 1] (rows contiguous; e.g. views of the QKV output)
+ *   pos      I32 [>= s]; kv_idx I64 [s]
+ *   q_out    F32 [hd, Hq, s, 1]
+ *   k_cache, v_cache F16 [hd, rows, Hkv, 1]
+ * Modes 0 and 2, ext_factor 0. Out-of-range indices are skipped and counted (per
+ * token and head) in *n_bad when it is non-null. */
+int gq_rope_kv_store(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* pos, int n_dims,
+                     int mode, float freq_base, float freq_scale, float attn_factor, const gq_tensor* kv_idx,
+                     gq_tensor* q_out, gq_tensor* k_cache, gq_tensor* v_cache, int32_t* n_bad, gq_stream_t stream);
+
 /* ggml_add(a, b) with b repeated over a (ggml_can_repeat). */
 int gq_add(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream);
 

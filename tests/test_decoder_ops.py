@@ -114,3 +114,38 @@ def test_argmax_add_gpu(golden_dir, dev):
     y = ops.add(_t(a, dev), _t(b, dev)).cpu().numpy()
     assert np.array_equal(y, a + b)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,n_dims,Hq,Hkv,hd,s", [(2, 128, 32, 32, 128, 1), (2, 64, 15, 5, 64, 7),
+                                                     (0, 96, 4, 2, 128, 3)])
+def test_rope_kv_store_bit_identical(dev, mode, n_dims, Hq, Hkv, hd, s):
+    """gq_rope_kv_store == rope_ext(q), rope_ext(k), set_rows(k), set_rows(v), bit for bit,
+    including the skipped out-of-range index and its count."""
+    import torch
+    from ggmlc_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(hd + s)
+    qkv = torch.randn((s, (Hq + 2 * Hkv) * hd), generator=g, device=dev) * 4
+    qv = qkv[:, :Hq * hd].view(1, s, Hq, hd)
+    kv = qkv[:, Hq * hd:(Hq + Hkv) * hd].view(1, s, Hkv, hd)
+    vv = qkv[:, (Hq + Hkv) * hd:].view(1, s, Hkv, hd)
+    pos = torch.arange(1000, 1000 + s, dtype=torch.int32, device=dev)
+    idx = torch.tensor(([5, -1, 9, 63, 0, 7, 2])[:s], dtype=torch.int64, device=dev)
+    kc1 = (torch.randn((1, Hkv, 64, hd), generator=g, device=dev)).half()
+    vc1 = (torch.randn((1, Hkv, 64, hd), generator=g, device=dev)).half()
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    bad1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    bad2 = torch.zeros(1, dtype=torch.int32, device=dev)
+    q1 = ops.rope_ext(qv, pos, n_dims, mode, 10000.0)
+    k1 = ops.rope_ext(kv, pos, n_dims, mode, 10000.0)
+    ops.set_rows(kc1, k1.permute(0, 2, 1, 3), idx, n_bad=bad1)
+    ops.set_rows(vc1, vv.permute(0, 2, 1, 3), idx, n_bad=bad1)
+    q2 = torch.empty_like(q1)
+    ops.rope_kv_store(qv, kv, vv, pos, n_dims, mode, 10000.0, idx, q2, kc2, vc2, n_bad=bad2)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    assert int(bad1.item()) == int(bad2.item()) == (2 * Hkv if s > 1 else 0)
