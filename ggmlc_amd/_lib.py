@@ -41,6 +41,8 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("rms_eps", ctypes.c_float),
         ("swiglu", ctypes.c_int32),
         ("add", ctypes.POINTER(gq_tensor)),
+        ("b_add", ctypes.POINTER(gq_tensor)),
+        ("b_sum", ctypes.POINTER(gq_tensor)),
     ]
 
 

@@ -157,7 +157,8 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     const float* x = static_cast<const float*>(b->data);
     float* y = static_cast<float*>(dst->data);
     const uint8_t* W = static_cast<const uint8_t*>(a->data);
-    if (p.use_gemv) return gemv(a->type, W, p.N, p.K, x, p.x_stride, p.M, y, p.ldd, GemvFuse{}, s);
+    if (p.use_gemv) return gemv(a->type, W, p.N, p.K, ActSrc{x, p.x_stride, nullptr, 0, nullptr, 0}, p.M, y, p.ldd,
+                                GemvFuse{}, s);
     uint16_t* A = static_cast<uint16_t*>(workspace);
     rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, p.K, s);
     if (rc) return rc;
@@ -196,11 +197,32 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
         fz.res = static_cast<const float*>(r->data);
         fz.ldr = (int64_t)(r->nb[1] / 4);
     }
+    ActSrc act{static_cast<const float*>(b->data), p.x_stride, nullptr, 0, nullptr, 0};
+    if (f->b_add) {
+        const gq_tensor* r = f->b_add;
+        if (r->type != GQ_TYPE_F32 || r->ne[0] != p.K || r->ne[1] != b->ne[1] || r->ne[2] != b->ne[2] ||
+            r->ne[3] != b->ne[3] || r->nb[0] != 4 || r->nb[1] % 4 != 0 || !rows_uniform(r))
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: b_add must be F32 shaped like b: " + shape(r));
+        act.d = static_cast<const float*>(r->data);
+        act.ds = (int64_t)(r->nb[1] / 4);
+        if (f->b_sum) {
+            const gq_tensor* o = f->b_sum;
+            if (o->type != GQ_TYPE_F32 || o->ne[0] != p.K || o->ne[1] != b->ne[1] || o->ne[2] != b->ne[2] ||
+                o->ne[3] != b->ne[3] || o->nb[0] != 4 || o->nb[1] % 4 != 0 || !rows_uniform(o))
+                return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum must be F32 shaped like b: " + shape(o));
+            if (o->data == b->data || o->data == r->data)
+                return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum must not alias b or b_add");
+            act.out = static_cast<float*>(o->data);
+            act.os = (int64_t)(o->nb[1] / 4);
+        }
+    } else if (f->b_sum) {
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum needs b_add");
+    }
     if (p.M == 0) return GQ_OK;
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
-    return gemv(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, static_cast<const float*>(b->data),
-                p.x_stride, p.M, static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), fz, (hipStream_t)stream);
+    return gemv(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M, static_cast<float*>(dst->data),
+                (int64_t)(dst->nb[1] / 4), fz, (hipStream_t)stream);
 }
 
 int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n_bad, gq_stream_t stream) {

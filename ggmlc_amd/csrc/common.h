@@ -17,13 +17,12 @@ constexpr int Q8_BYTES = 34;  // fp16 d + 32 x int8
 constexpr int Q4_BYTES = 18;  // fp16 d + 16 bytes of nibbles
 
 // Activation layout handed from the quantizer to the GEMV kernels, per token row:
-// groups of 8 blocks, each group GS bytes: [256 B int8 qs][8 x f32 d][8 x i32 sum(qs)][16 B pad].
+// groups of 8 blocks, each group GS bytes: [256 B int8 qs][8 x (f32 d, i32 sum(qs))][16 B pad].
 // The 336-byte stride keeps ds_read_b128 of lanes reading consecutive groups
 // free of LDS bank conflicts (84 dwords = 20 mod 32).
 constexpr int ACT_GS = 336;
 constexpr int ACT_QS_OFF = 0;
-constexpr int ACT_D_OFF = 256;
-constexpr int ACT_S_OFF = 288;
+constexpr int ACT_DS_OFF = 256;  // (d, s) pairs of the 8 blocks
 
 __host__ __device__ inline int64_t act_row_bytes(int64_t K) { return ((K / QK + 7) / 8) * ACT_GS; }
 
@@ -133,8 +132,8 @@ __device__ __forceinline__ void quant8_block(const float (&v)[8], int (&q)[8], u
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    const float d = div_rn(amax, 127.0f);
-    const float id = amax != 0.0f ? div_rn(127.0f, amax) : 0.0f;
+    const float d = amax / 127.0f;  // IEEE division, correctly rounded (no fast-math)
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     int s = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -169,11 +168,48 @@ __device__ __forceinline__ void load8(const float* src, bool valid, float (&v)[8
     }
 }
 
+// The activation rows a GEMV consumes: x, or x + d (an ADD node fused in front; its
+// sum is also written to `out` by the workgroup that has `writer` set, since later
+// nodes read it).
+struct ActSrc {
+    const float* x;
+    int64_t xs;        // row stride (floats)
+    const float* d;    // null: no ADD
+    int64_t ds;
+    float* out;        // null: the sum is not stored
+    int64_t os;
+};
+
+template <bool VEC>
+__device__ __forceinline__ void act_load8(const ActSrc& a, int m, int64_t e0, bool valid, float (&v)[8]) {
+    load8<VEC>(a.x + (int64_t)m * a.xs + e0, valid, v);
+    if (a.d) {
+        float w[8];
+        load8<VEC>(a.d + (int64_t)m * a.ds + e0, valid, w);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] + w[i];  // ADD(x, d): x + d
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void act_store_sum(const ActSrc& a, bool writer, int m, int64_t e0, bool valid,
+                                              const float (&v)[8]) {
+    if (!a.out || !writer || !valid) return;
+    float* o = a.out + (int64_t)m * a.os + e0;
+    if (VEC) {
+        *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = v[i];
+    }
+}
+
 // RMS scales of M activation rows (K % 32 == 0) read from global memory, in the
 // order of sumsq8 / block_sum_d; all 256 lanes call it.
 template <bool VEC, int MM>
-__device__ __forceinline__ void rms_scales(const float* __restrict__ x, int64_t x_stride, int M, int K, float eps,
-                                           float (&scale)[MM], double* red) {
+__device__ __forceinline__ void rms_scales(const ActSrc& a, int M, int K, float eps, float (&scale)[MM],
+                                           double* red) {
     const int nb = K / QK;
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
@@ -182,19 +218,19 @@ __device__ __forceinline__ void rms_scales(const float* __restrict__ x, int64_t 
         for (int base = 0; base < nb * 4; base += 256) {
             const int t = base + (int)threadIdx.x;
             float v[8];
-            load8<VEC>(x + (int64_t)m * x_stride + (int64_t)t * 8, (t >> 2) < nb, v);
+            act_load8<VEC>(a, m, (int64_t)t * 8, (t >> 2) < nb, v);
             s = sumsq8(v, s);
         }
         scale[m] = rms_scale(block_sum_d(s, red), K, eps);
     }
 }
 
-// Quantize M activation rows (K elements, row stride x_stride floats) into the
-// ACT_GS layout at dst (row stride act_bytes), cooperatively by a 256-lane block;
-// row m is multiplied by scale[m] first (1 leaves it unchanged: RMS_NORM fusion).
+// Quantize M activation rows (K elements) into the ACT_GS layout at dst (row stride
+// act_bytes), cooperatively by a 256-lane block; row m is multiplied by scale[m]
+// first (1 leaves it unchanged: RMS_NORM fusion).
 template <bool VEC, int MM = 1>
-__device__ __forceinline__ void quantize_rows_to_act(const float* __restrict__ x, int64_t x_stride, int M, int K,
-                                                     uint8_t* dst, int act_bytes, const float* scale = nullptr) {
+__device__ __forceinline__ void quantize_rows_to_act(const ActSrc& a, bool writer, int M, int K, uint8_t* dst,
+                                                     int act_bytes, const float* scale = nullptr) {
     const int nb = K / QK;
     for (int m = 0; m < M; ++m) {
         const float sc = scale ? scale[m] : 1.0f;
@@ -203,7 +239,8 @@ __device__ __forceinline__ void quantize_rows_to_act(const float* __restrict__ x
             const int b = t >> 2, part = t & 3;
             const bool valid = b < nb;
             float v[8];
-            load8<VEC>(x + (int64_t)m * x_stride + (int64_t)b * QK + part * 8, valid, v);
+            act_load8<VEC>(a, m, (int64_t)b * QK + part * 8, valid, v);
+            act_store_sum<VEC>(a, writer, m, (int64_t)b * QK + part * 8, valid, v);
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = v[i] * sc;
             int q[8];
@@ -221,8 +258,8 @@ __device__ __forceinline__ void quantize_rows_to_act(const float* __restrict__ x
                 }
                 *reinterpret_cast<uint2*>(gp + ACT_QS_OFF + bi * QK + part * 8) = make_uint2(lo, hi);
                 if (part == 0) {
-                    reinterpret_cast<float*>(gp + ACT_D_OFF)[bi] = h2f(dh);
-                    reinterpret_cast<int*>(gp + ACT_S_OFF)[bi] = qsum;
+                    *reinterpret_cast<float2*>(gp + ACT_DS_OFF + 8 * bi) =
+                        make_float2(h2f(dh), __int_as_float(qsum));
                 }
             }
         }

@@ -82,11 +82,12 @@ __device__ __forceinline__ void decode_at(const uint32_t* w, int o, uint32_t& hd
 }
 
 // integer dot of one weight block (decoded quant dwords q) with the activation
-// block (a0, a1 = its 32 int8); Q4_0 nibbles are biased by 8 via the block sum
+// block (a0, a1 = its 32 int8; sa = their sum); Q4_0 nibbles are dotted unsigned
+// and biased by 8 through the block sum, so the block sum stays an exact integer
 template <int QT>
-__device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, const uint4& a1,
-                                         const uint8_t* ag, int bi) {
+__device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, const uint4& a1, int sa) {
     if constexpr (QT == GQ_TYPE_Q8_0) {
+        (void)sa;
         int s = dot4(q[0], a0.x, 0);
         s = dot4(q[1], a0.y, s);
         s = dot4(q[2], a0.z, s);
@@ -96,7 +97,6 @@ __device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, con
         s = dot4(q[6], a1.z, s);
         return dot4(q[7], a1.w, s);
     } else {
-        const int sa = reinterpret_cast<const int*>(ag + ACT_S_OFF)[bi];
         int s = dot4(q[0] & 0x0f0f0f0fu, a0.x, -8 * sa);
         s = dot4(q[1] & 0x0f0f0f0fu, a0.y, s);
         s = dot4(q[2] & 0x0f0f0f0fu, a0.z, s);
@@ -106,6 +106,20 @@ __device__ __forceinline__ int block_dot(const uint32_t* q, const uint4& a0, con
         s = dot4((q[2] >> 4) & 0x0f0f0f0fu, a1.z, s);
         return dot4((q[3] >> 4) & 0x0f0f0f0fu, a1.w, s);
     }
+}
+
+// sum over the 16 lanes of a row (DPP within rows of 16 lanes: every lane ends
+// with the row total; pairs, quads, half-row mirror, row mirror)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    return v;
 }
 
 // Physical weight row of logical row r: with the SWIGLU epilogue, logical rows
@@ -136,16 +150,16 @@ __device__ __forceinline__ void emit(const GemvFuse& fz, float* dst, int64_t ldd
 
 template <int QT, int M, bool XVEC, int PF, int KS>
 __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__ W, int64_t N,
-                                                     int64_t row_bytes, int G,
-                                                     const float* __restrict__ x,
-                                                     int64_t x_stride, float* dst,
+                                                     int64_t row_bytes, int G, ActSrc act, float* dst,
                                                      int64_t ldd, GemvFuse fz) {
     constexpr int GB = QTraits<QT>::GB;
     constexpr int CPG = QTraits<QT>::CPG;
     constexpr int SEG = LPR * CPG;       // chunks of one row per step
-    constexpr int XPMAX = 2;             // activation passes held in registers
+    constexpr int XPMAX = 6;             // activation passes held in registers (K <= 12288 at M = 1)
+    constexpr int XAMAX = 2;             // of which can carry a fused ADD operand
     constexpr int RG = WAVES / KS;       // row groups (of RPW rows) per workgroup tile
     constexpr int ROWS = RG * RPW;       // rows per workgroup tile
+    constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any matrix: load returns 0, no fetch
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float red[WAVES][M][RPW];
     __shared__ double red_d[4];
@@ -172,54 +186,95 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     const int g_end = min(G, (kp + 1) * SP * LPR);
     const int S = max(1, (g_end - g_begin + LPR - 1) / LPR);  // steps per tile for this wave
 
-    // persistent workgroups over workgroup tiles; one flat (tile, step) pipeline per wave
+    // persistent workgroups over workgroup tiles of ROWS rows; each wave walks its
+    // (tile, step) sequence with a PF-deep register pipeline. (Measured: contiguous
+    // per-wave row ranges sized N / waves, which balance bytes exactly, ran slower:
+    // partial row sets cost more steps.)
     const int64_t n_wgt = (N + ROWS - 1) / ROWS;
-    const int64_t my_wgt = blockIdx.x < n_wgt ? (n_wgt - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
-    const int64_t F = my_wgt * S;
+    const int my_wgt = blockIdx.x < n_wgt ? (int)((n_wgt - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0;
 
-    float xr[XPMAX][8];
-    const bool xpre = M * XP <= XPMAX;
+    // activation loads first, then the weight prefetch: the activation can then be
+    // waited for while the weight loads stay in flight (vector loads complete in order)
+    float xr[XPMAX][8], ar[XAMAX][8];
+    const bool xpre = M * XP <= XPMAX && (!act.d || M * XP <= XAMAX);
     if (xpre) {
 #pragma unroll
         for (int p = 0; p < XPMAX; ++p) {
             if (p < M * XP) {
                 const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
-                load8<XVEC>(x + (int64_t)m * x_stride + (int64_t)(t >> 2) * QK + (t & 3) * 8, (t >> 2) < nb, xr[p]);
+                load8<XVEC>(act.x + (int64_t)m * act.xs + (int64_t)t * 8, (t >> 2) < nb, xr[p]);
+                if (p < XAMAX && act.d)
+                    load8<XVEC>(act.d + (int64_t)m * act.ds + (int64_t)t * 8, (t >> 2) < nb, ar[p]);
             }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // Weight loads are raw buffer loads: per step one wave-uniform base (the step's
+    // 4-row slice at its first group) plus a per-lane constant offset, so a load costs
+    // no address arithmetic. Offsets past the resource's size return 0 without a
+    // memory access: rows past N, chunks past the K range of a tail step and steps
+    // past the end of the wave's sequence never touch memory.
+    // Chunk c of a lane is byte 16 * within of slice row r (r, within from lane + 64 c);
+    // with the SWIGLU epilogue slice rows 2i, 2i+1 are gate row i and up row i + N/2.
+    const int64_t mat_bytes = (fz.glu ? fz.glu_half : N) * row_bytes * (fz.glu ? 2 : 1);
+    uint32_t voff[CPG];
+#pragma unroll
+    for (int c = 0; c < CPG; ++c) {
+        const int ci = lane + 64 * c, r = ci / SEG, within = ci - r * SEG;
+        const int64_t roff = fz.glu ? (int64_t)(r >> 1) + (r & 1) * fz.glu_half : (int64_t)r;
+        voff[c] = (uint32_t)(roff * row_bytes + within * 16);
+    }
+    const int ngr_tail = g_end - g_begin - (S - 1) * LPR;  // groups of the last step of a tile
     uint4 pre[PF][CPG];
-    auto load_step = [&](int64_t f, uint4(&dstv)[CPG]) {
-        const int64_t t = (int64_t)blockIdx.x + (f / S) * gridDim.x;
-        const int j = (int)(f % S);
-        const int64_t row0 = t * ROWS + rg * RPW;
-        const int gfirst = g_begin + j * LPR;             // first group of this step
-        const int ngr = min(LPR, g_end - gfirst);          // groups of this step
+    // load cursor: tile k, step j (wave-uniform)
+    int lk = 0, lj = 0;
+    auto issue = [&](uint4(&buf)[CPG]) {
+        const int64_t row0 = ((int64_t)blockIdx.x + (int64_t)lk * gridDim.x) * ROWS + rg * RPW;
+        const int64_t prow = fz.glu ? row0 >> 1 : row0;
+        const int gfirst = g_begin + lj * LPR;
+        const int64_t off0 = prow * row_bytes + (int64_t)gfirst * GB;
+        const int64_t left = lk < my_wgt ? mat_bytes - off0 : 0;
+        const uint32_t nrec = left <= 0 ? 0u : (left > 0x7fffffff ? 0x7fffffffu : (uint32_t)left);
+        // the resource lives in SGPRs: make its wave-uniformity explicit
+        const uint64_t base = reinterpret_cast<uint64_t>(W) + (uint64_t)off0;
+        const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+        const uint32_t bhi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+        __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(((uint64_t)bhi << 32) | blo), (short)0,
+            (int)__builtin_amdgcn_readfirstlane(nrec), 0x00020000);
+        const bool tail = lj == S - 1 && ngr_tail < LPR;
 #pragma unroll
         for (int c = 0; c < CPG; ++c) {
-            const int ci = lane + 64 * c;
-            const int r = ci / SEG;
-            const int within = ci - r * SEG;
-            const int64_t rr = row0 + r;
-            const bool ok = rr < N && within < ngr * CPG;
-            const int64_t boff = (int64_t)gfirst * GB + (int64_t)within * 16;
-            // always-valid address, zeroed after the load: no branch per chunk
-            uint4 v = ld_nt16(W + (ok ? phys_row(fz, rr) * row_bytes + boff : 0));
-            if (!ok) v = make_uint4(0, 0, 0, 0);
-            dstv[c] = v;
+            uint32_t vo = voff[c];
+            if (tail) {  // chunks of groups past the K range
+                const int ci = lane + 64 * c, within = ci - (ci / SEG) * SEG;
+                vo = within < ngr_tail * CPG ? vo : OOB;
+            }
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, 0, 2 /* nt */);
+            buf[c] = make_uint4(v.x, v.y, v.z, v.w);
         }
+        if (++lj == S) lj = 0, ++lk;
     };
 #pragma unroll
-    for (int s = 0; s < PF; ++s)
-        if (s < F) load_step(s, pre[s]);
+    for (int s = 0; s < PF; ++s) issue(pre[s]);
     __builtin_amdgcn_sched_barrier(0);
 
     float scale[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) scale[m] = 1.0f;
     if (xpre) {
+        if (act.d) {  // ADD fused in front: x + d, stored once for the nodes that read the sum
+#pragma unroll
+            for (int p = 0; p < XAMAX; ++p) {
+                if (p < M * XP) {
+                    const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xr[p][i] = xr[p][i] + ar[p][i];
+                    act_store_sum<XVEC>(act, blockIdx.x == 0, m, (int64_t)t * 8, (t >> 2) < nb, xr[p]);
+                }
+            }
+        }
         if (fz.rms) {  // RMS_NORM fused: the rows' squares are already in registers
 #pragma unroll
             for (int m = 0; m < M; ++m) {
@@ -251,16 +306,15 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                         hi |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
                     }
                     *reinterpret_cast<uint2*>(gp + ACT_QS_OFF + bi * QK + part * 8) = make_uint2(lo, hi);
-                    if (part == 0) {
-                        reinterpret_cast<float*>(gp + ACT_D_OFF)[bi] = h2f(dh);
-                        reinterpret_cast<int*>(gp + ACT_S_OFF)[bi] = qsum;
-                    }
+                    if (part == 0)
+                        *reinterpret_cast<float2*>(gp + ACT_DS_OFF + 8 * bi) =
+                            make_float2(h2f(dh), __int_as_float(qsum));
                 }
             }
         }
     } else {
-        if (fz.rms) rms_scales<XVEC, M>(x, x_stride, M, G * 256, fz.eps, scale, red_d);
-        quantize_rows_to_act<XVEC, M>(x, x_stride, M, G * 256, s_act, act_bytes, scale);
+        if (fz.rms) rms_scales<XVEC, M>(act, M, G * 256, fz.eps, scale, red_d);
+        quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, G * 256, s_act, act_bytes, scale);
     }
     __syncthreads();  // quantized activation visible to all waves
 
@@ -268,20 +322,18 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
 
-    for (int64_t f = 0; f < F; ++f) {
-        const int64_t t = (int64_t)blockIdx.x + (f / S) * gridDim.x;
-        const int j = (int)(f % S);
-        const int64_t row = t * ROWS + rg * RPW + rsub;
+    // consume cursor: tile k, step j (wave-uniform)
+    int ck = 0, cj = 0;
+    // One step: park buffer `buf` in the wave's LDS slice, refill it with the step PF
+    // ahead, decode. The PF buffers are used round-robin by an unrolled loop so no
+    // register copy of a pending load forces an early wait.
+    auto body = [&](uint4(&buf)[CPG]) {
+        const int64_t row = ((int64_t)blockIdx.x + (int64_t)ck * gridDim.x) * ROWS + rg * RPW + rsub;
 #pragma unroll
-        for (int c = 0; c < CPG; ++c) *reinterpret_cast<uint4*>(s_stage + (lane + 64 * c) * 16) = pre[0][c];
+        for (int c = 0; c < CPG; ++c) *reinterpret_cast<uint4*>(s_stage + (lane + 64 * c) * 16) = buf[c];
         wave_lds_sync();
-        // rotate the register pipeline and issue step f + PF
-#pragma unroll
-        for (int s = 0; s + 1 < PF; ++s)
-#pragma unroll
-            for (int c = 0; c < CPG; ++c) pre[s][c] = pre[s + 1][c];
-        if (f + PF < F) load_step(f + PF, pre[PF - 1]);
-        const int g = g_begin + j * LPR + gsub;
+        issue(buf);
+        const int g = g_begin + cj * LPR + gsub;
         const bool live = row < N && g < g_end;
         // decode the group in two windows of HC chunks (blocks 0-3, then 4-7)
 #pragma unroll
@@ -299,31 +351,34 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             }
             if (!live) continue;
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                const int b = 4 * h + bb;
-                uint32_t hdr;
-                uint32_t q[QTraits<QT>::NQW];
-                decode_at<QT>(w, QTraits<QT>::BB * b - 16 * c0, hdr, q);
-                const float dw = h2f((uint16_t)hdr);
+            for (int m = 0; m < M; ++m) {
+                const uint8_t* ag = s_act + m * act_bytes + g * ACT_GS;
+                const float4 ds01 = *reinterpret_cast<const float4*>(ag + ACT_DS_OFF + 32 * h);
+                const float4 ds23 = *reinterpret_cast<const float4*>(ag + ACT_DS_OFF + 32 * h + 16);
+                const float dsv[8] = {ds01.x, ds01.y, ds01.z, ds01.w, ds23.x, ds23.y, ds23.z, ds23.w};
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const uint8_t* ag = s_act + m * act_bytes + g * ACT_GS;
+                for (int bb = 0; bb < 4; ++bb) {
+                    const int b = 4 * h + bb;
+                    uint32_t hdr;
+                    uint32_t q[QTraits<QT>::NQW];
+                    decode_at<QT>(w, QTraits<QT>::BB * b - 16 * c0, hdr, q);
+                    const float dw = h2f((uint16_t)hdr);
                     const uint4 a0 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b);
                     const uint4 a1 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * b + 16);
-                    const float da = reinterpret_cast<const float*>(ag + ACT_D_OFF)[b];
-                    const int sdot = block_dot<QT>(q, a0, a1, ag, b);
-                    acc[m] += (float)sdot * (dw * da);
+                    const int sdot = block_dot<QT>(q, a0, a1, __float_as_int(dsv[2 * bb + 1]));
+                    acc[m] += (float)sdot * (dw * dsv[2 * bb]);
                 }
             }
         }
         wave_lds_sync();  // this step's staging slice is fully read before it is refilled
-        if (j == S - 1) {  // tile finished: reduce the 16 lanes of each row, then the K parts
+        if (cj == S - 1) {  // tile finished: reduce the 16 lanes of each row, then the K parts
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float v = xor_sum<LPR>(acc[m]);
+                const float v = row16_sum(acc[m]);
                 acc[m] = 0.0f;
                 if constexpr (KS == 1) {
-                    const float vp = __shfl_xor(v, LPR, 64);  // the next row's value (SWIGLU pairs)
+                    float vp = 0.0f;
+                    if (fz.glu) vp = __shfl_xor(v, LPR, 64);  // the next row's value (SWIGLU pairs)
                     if (gsub == 0 && row < N) emit(fz, dst, ldd, m, row, v, vp);
                 } else {
                     if (gsub == 0) red[wave][m][rsub] = v;
@@ -343,6 +398,19 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                 __syncthreads();
             }
         }
+        if (++cj == S) cj = 0, ++ck;
+    };
+    const int F = my_wgt * S;
+    if constexpr (PF == 1) {
+        for (int f = 0; f < F; ++f) body(pre[0]);
+    } else {
+        static_assert(PF == 2, "prefetch depth 1 or 2");
+        int f = 0;
+        for (; f + 1 < F; f += 2) {
+            body(pre[0]);
+            body(pre[1]);
+        }
+        if (f < F) body(pre[0]);
     }
 }
 
@@ -350,21 +418,19 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
 
 template <int QT, int M, bool XVEC>
 __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W, int64_t N,
-                                                  int64_t row_bytes, int nb,
-                                                  const float* __restrict__ x,
-                                                  int64_t x_stride, float* dst,
+                                                  int64_t row_bytes, int nb, ActSrc act, float* dst,
                                                   int64_t ldd, GemvFuse fz) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int NQW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red_d[4];
     const int act_stride = (int)act_row_bytes((int64_t)nb * QK);
-    const uint8_t* act = smem;
+    const uint8_t* s_act = smem;
     float scale[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) scale[m] = 1.0f;
-    if (fz.rms) rms_scales<XVEC, M>(x, x_stride, M, nb * QK, fz.eps, scale, red_d);
-    quantize_rows_to_act<XVEC, M>(x, x_stride, M, nb * QK, smem, act_stride, scale);
+    if (fz.rms) rms_scales<XVEC, M>(act, M, nb * QK, fz.eps, scale, red_d);
+    quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, nb * QK, smem, act_stride, scale);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
@@ -383,18 +449,19 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
             const int g = b >> 3, bi = b & 7;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const uint8_t* ag = act + m * act_stride + (int64_t)g * ACT_GS;
+                const uint8_t* ag = s_act + m * act_stride + (int64_t)g * ACT_GS;
                 const uint4 a0 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * bi);
                 const uint4 a1 = *reinterpret_cast<const uint4*>(ag + ACT_QS_OFF + 32 * bi + 16);
-                const float da = reinterpret_cast<const float*>(ag + ACT_D_OFF)[bi];
-                const int s = block_dot<QT>(q, a0, a1, ag, bi);
+                const float2 ds = *reinterpret_cast<const float2*>(ag + ACT_DS_OFF + 8 * bi);
+                const float da = ds.x;
+                const int s = block_dot<QT>(q, a0, a1, __float_as_int(ds.y));
                 acc[m] += (float)s * (dw * da);
             }
         }
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const float v = xor_sum<LPR>(acc[m]);
+        const float v = row16_sum(acc[m]);
         const float vp = __shfl_xor(v, LPR, 64);
         if (sub == 0 && row < N) emit(fz, dst, ldd, m, row, v, vp);
     }
@@ -442,8 +509,19 @@ int resident_wgs(KFn* fn, size_t lds, int& out) {
     return GQ_OK;
 }
 
+// GQ_GEMV_KS=1|2|4 pins the split-K factor (tuning measurements); unset: heuristic
+int gemv_ks_override() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("GQ_GEMV_KS");
+        v = e ? atoi(e) : 0;
+        if (v != 1 && v != 2 && v != 4) v = 0;
+    }
+    return v;
+}
+
 template <int QT, int M, bool XVEC, int PF, int KS>
-int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s, size_t lds, int resident) {
     const int G = (int)(K / 256);
     const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
@@ -453,12 +531,12 @@ int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_
     if (rc) return rc;
     const int64_t tiles = cdiv(N, (WAVES / KS) * RPW);
     const dim3 grid((unsigned)(tiles < resident ? tiles : resident));
-    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, x, x_stride, dst, ldd, fz);
+    hipLaunchKernelGGL(fn, grid, dim3(256), lds, s, W, N, row_bytes, G, act, dst, ldd, fz);
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
 template <int QT, int M, bool XVEC, int PF>
-int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int G = (int)(K / 256);
     const size_t lds = (size_t)M * G * ACT_GS + (size_t)WAVES * 64 * QTraits<QT>::GB;
@@ -472,25 +550,31 @@ int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_
     // 4096-row down projection is slower, a 1536-row one faster)
     const int64_t t1 = cdiv(N, WAVES * RPW);
     const int J = (G + LPR - 1) / LPR;
+    const int ks_force = gemv_ks_override();
+    if (ks_force == 1 || (ks_force == 2 && J >= 2) || (ks_force == 4 && J >= 2)) {
+        if (ks_force == 1) return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+        if (ks_force == 2) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+        return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+    }
     if (4 * t1 >= resident || J < 2)
-        return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, x, x_stride, dst, ldd, fz, s, lds, resident);
-    if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, x, x_stride, dst, ldd, fz, s, lds, resident);
-    return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, x, x_stride, dst, ldd, fz, s, lds, resident);
+        return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+    if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+    return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, act, dst, ldd, fz, s, lds, resident);
 }
 
 // Q4_0 keeps two steps of weight loads in flight per wave
 template <int QT, int M, bool XVEC>
-int launch_grp(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+int launch_grp(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     if constexpr (QT == GQ_TYPE_Q8_0) {
-        return launch_grp_pf<QT, M, XVEC, 1>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        return launch_grp_pf<QT, M, XVEC, 1>(W, N, K, act, dst, ldd, fz, s);
     } else {
-        return launch_grp_pf<QT, M, XVEC, 2>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        return launch_grp_pf<QT, M, XVEC, 2>(W, N, K, act, dst, ldd, fz, s);
     }
 }
 
 template <int QT, int M, bool XVEC>
-int launch_blk(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
+int launch_blk(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int nb = (int)(K / QK);
     const int64_t row_bytes = (int64_t)nb * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
@@ -500,41 +584,45 @@ int launch_blk(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x
     int rc = allow_big_lds(&k_gemv_blk<QT, M, XVEC>, allowed, lds);
     if (rc) return rc;
     const dim3 grid((unsigned)cdiv(N, 256 / LPR));
-    hipLaunchKernelGGL((k_gemv_blk<QT, M, XVEC>), grid, dim3(256), lds, s, W, N, row_bytes, nb, x,
-                       x_stride, dst, ldd, fz);
+    hipLaunchKernelGGL((k_gemv_blk<QT, M, XVEC>), grid, dim3(256), lds, s, W, N, row_bytes, nb, act, dst, ldd,
+                       fz);
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
+inline bool vec_ok(const float* p, int64_t stride) {
+    return p == nullptr || (((reinterpret_cast<uintptr_t>(p) & 15) == 0) && (stride % 4 == 0));
+}
+
 template <int QT, int M>
-int launch_m(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride, float* dst,
-             int64_t ldd, const GemvFuse& fz, hipStream_t s) {
+int launch_m(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, float* dst, int64_t ldd,
+             const GemvFuse& fz, hipStream_t s) {
     const bool grp = (K % 256 == 0) && ((reinterpret_cast<uintptr_t>(W) & 15) == 0);
-    const bool xvec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (x_stride % 4 == 0);
+    const bool xvec = vec_ok(act.x, act.xs) && vec_ok(act.d, act.ds) && vec_ok(act.out, act.os);
     if (grp)
-        return xvec ? launch_grp<QT, M, true>(W, N, K, x, x_stride, dst, ldd, fz, s)
-                    : launch_grp<QT, M, false>(W, N, K, x, x_stride, dst, ldd, fz, s);
-    return xvec ? launch_blk<QT, M, true>(W, N, K, x, x_stride, dst, ldd, fz, s)
-                : launch_blk<QT, M, false>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        return xvec ? launch_grp<QT, M, true>(W, N, K, act, dst, ldd, fz, s)
+                    : launch_grp<QT, M, false>(W, N, K, act, dst, ldd, fz, s);
+    return xvec ? launch_blk<QT, M, true>(W, N, K, act, dst, ldd, fz, s)
+                : launch_blk<QT, M, false>(W, N, K, act, dst, ldd, fz, s);
 }
 
 template <int QT>
-int gemv_t(const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride, int64_t M,
-           float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
+int gemv_t(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
+           const GemvFuse& fz, hipStream_t s) {
     switch (M) {
-        case 1: return launch_m<QT, 1>(W, N, K, x, x_stride, dst, ldd, fz, s);
-        case 2: return launch_m<QT, 2>(W, N, K, x, x_stride, dst, ldd, fz, s);
-        case 3: return launch_m<QT, 3>(W, N, K, x, x_stride, dst, ldd, fz, s);
-        case 4: return launch_m<QT, 4>(W, N, K, x, x_stride, dst, ldd, fz, s);
+        case 1: return launch_m<QT, 1>(W, N, K, act, dst, ldd, fz, s);
+        case 2: return launch_m<QT, 2>(W, N, K, act, dst, ldd, fz, s);
+        case 3: return launch_m<QT, 3>(W, N, K, act, dst, ldd, fz, s);
+        case 4: return launch_m<QT, 4>(W, N, K, act, dst, ldd, fz, s);
         default: return fail(GQ_ERR_INVALID, "gemv: M out of range");
     }
 }
 
 }  // namespace
 
-int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-         int64_t M, float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
-    if (type == GQ_TYPE_Q8_0) return gemv_t<GQ_TYPE_Q8_0>(W, N, K, x, x_stride, M, dst, ldd, fz, s);
-    return gemv_t<GQ_TYPE_Q4_0>(W, N, K, x, x_stride, M, dst, ldd, fz, s);
+int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
+         const GemvFuse& fz, hipStream_t s) {
+    if (type == GQ_TYPE_Q8_0) return gemv_t<GQ_TYPE_Q8_0>(W, N, K, act, M, dst, ldd, fz, s);
+    return gemv_t<GQ_TYPE_Q4_0>(W, N, K, act, M, dst, ldd, fz, s);
 }
 
 }  // namespace gq

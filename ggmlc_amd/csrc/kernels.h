@@ -16,8 +16,9 @@ int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s
 // quantized inside the kernel
 constexpr int GEMV_MAX_M = 4;
 // Fusions of the decoder graph's neighbours of MUL_MAT into the GEMV (each gives the
-// bits of the unfused ops): RMS_NORM of the activation rows, SWIGLU over the two
-// halves of the weight rows (output N/2 wide), ADD of a residual (may alias dst).
+// bits of the unfused ops): ADD in front of the activation (ActSrc.d), RMS_NORM of
+// the activation rows, SWIGLU over the two halves of the weight rows (output N/2
+// wide), ADD of a residual to the output (may alias dst).
 struct GemvFuse {
     int rms = 0;
     float eps = 0.0f;
@@ -26,8 +27,8 @@ struct GemvFuse {
     const float* res = nullptr;
     int64_t ldr = 0;
 };
-int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const float* x, int64_t x_stride,
-         int64_t M, float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s);
+int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
+         const GemvFuse& fz, hipStream_t s);
 
 // gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k], A fp16
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda,

@@ -157,6 +157,7 @@ class Decoder:
             self._bufs[s] = {
                 "ids": torch.zeros(s, dtype=torch.int32, device=d),
                 "x": torch.empty((s, c.n_embd), **f32),
+                "x_alt": torch.empty((s, c.n_embd), **f32),
                 "h": torch.empty((s, c.n_embd), **f32),
                 "qkv": torch.empty((s, c.q_dim + 2 * c.kv_dim), **f32),
                 "q": torch.empty((1, s, c.n_head, c.head_dim), **f32),
@@ -202,11 +203,17 @@ class Decoder:
         rec("pos", -1, self.pos)
         scale = 1.0 / math.sqrt(c.head_dim)
         qd, kvd = c.q_dim, c.kv_dim
+        # fused path: the residual ADD after O and after down is done by the next GEMV's
+        # prologue (x_next = x + proj, stored for the following ADD), alternating buffers
+        other = {id(b["x"]): b["x_alt"], id(b["x_alt"]): b["x"]}
+        pending = None  # proj still to be added to x
         for li, L in enumerate(self.w.layers):
-            rec("x_in", li, x)
             if fused:
-                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps)
+                nx = other[id(x)] if pending is not None else None
+                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps, x_add=pending, x_sum=nx)
+                x = nx if nx is not None else x
             else:
+                rec("x_in", li, x)
                 h = ops.rms_norm(x, c.rms_eps, out=b["h"])
                 rec("h1", li, h)
                 qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
@@ -229,11 +236,11 @@ class Decoder:
                                mask, scale, out=b["attn"], ws=ws)
             rec("attn", li, b["attn"])
             if fused:
-                ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=x, add=x)
-                rec("x_mid", li, x)
-                a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True)
-                rec("act", li, a)
-                ops.mul_mat_fused(L.down, a, out=x, add=x)
+                o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"])
+                nx = other[id(x)]
+                a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx)
+                x = nx
+                pending = ops.mul_mat_fused(L.down, a, out=b["proj"])
             else:
                 o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
                 ops.add(x, o, out=x)
@@ -248,7 +255,8 @@ class Decoder:
                 ops.add(x, d, out=x)
             rec("x_out", li, x)
         if fused:
-            logits = ops.mul_mat_fused(self.w.lm_head, x[s - 1:], out=b["logits"], rms_eps=c.rms_eps)
+            logits = ops.mul_mat_fused(self.w.lm_head, x[s - 1:], out=b["logits"], rms_eps=c.rms_eps,
+                                       x_add=pending[s - 1:] if pending is not None else None)
         else:
             h = ops.rms_norm(x[s - 1:], c.rms_eps, out=b["h"][:1])
             rec("hf", -1, h)

@@ -146,10 +146,12 @@ def mul_mat(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None,
 
 
 def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
-                  swiglu: bool = False, add: torch.Tensor | None = None) -> torch.Tensor:
+                  swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
+                  x_sum: torch.Tensor | None = None) -> torch.Tensor:
     """Decode MUL_MAT (x has at most 4 rows) fused with its graph neighbours, bit-identical
-    to the unfused ops: rms_eps -> RMS_NORM(x) first; swiglu -> SWIGLU of the result's
-    two halves (out [..., N/2]); add -> add + result (add may be out)."""
+    to the unfused ops: x_add -> x + x_add first (stored to x_sum when given); rms_eps ->
+    RMS_NORM; swiglu -> SWIGLU of the result's two halves (out [..., N/2]); add -> add +
+    result (add may be out)."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
     n_out = w.N // 2 if swiglu else w.N
@@ -162,6 +164,12 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     ad = _desc(add) if add is not None else None
     if ad is not None:
         f.add = ctypes.pointer(ad)
+    xa = _desc(x_add) if x_add is not None else None
+    if xa is not None:
+        f.b_add = ctypes.pointer(xa)
+    xs = _desc(x_sum) if x_sum is not None else None
+    if xs is not None:
+        f.b_sum = ctypes.pointer(xs)
     check(_lib.load().gq_mul_mat_fused(w.desc(), _desc(x), _desc(out), ctypes.byref(f), _stream()))
     return out
 

@@ -104,20 +104,25 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
 
 /* Decode MUL_MAT fused with its neighbours in ggmlc's LLaMA graph (the node runs
  * executor.cpp:2034-2090 RMS_NORM, :2362-2447 MUL_MAT, GLU SWIGLU and ADD emit),
- * giving the bits of the unfused calls in one launch:
- *   rms_norm: b's rows are RMS-normalized first (gq_rms_norm with rms_eps)
+ * giving the bits of the unfused calls in one launch, applied in this order:
+ *   b_add:    b := b + b_add first (gq_add(b, b_add): the residual ADD feeding the
+ *             next RMS_NORM); the sum is also stored to b_sum when it is non-null
+ *             (b_sum must not alias b or b_add)
+ *   rms_norm: b's rows are RMS-normalized (gq_rms_norm with rms_eps)
  *   swiglu:   dst = SWIGLU(MUL_MAT(a, b)) over the two halves of a's rows
  *             (gq_swiglu of the [N, M] result): dst ne0 = N / 2
  *   add:      dst = add + MUL_MAT(a, b) (gq_add); add may be dst itself
  * (swiglu excludes add.) Only the GEMV path (M <= 4 activation rows) is fused;
  * larger M returns GQ_ERR_UNSUPPORTED and the caller runs the ops unfused. No
- * workspace. The ggml CUDA backend fuses the same neighbours (RMS_NORM+MUL,
+ * workspace. The ggml CUDA backend fuses the same neighbours (ADD+RMS_NORM+MUL,
  * MUL_MAT+GLU, MUL_MAT+ADD) for the same reason: decode steps are launch-bound. */
 typedef struct gq_mul_mat_fusion {
     int32_t rms_norm;
     float rms_eps;
     int32_t swiglu;
     const gq_tensor* add;
+    const gq_tensor* b_add;
+    gq_tensor* b_sum;
 } gq_mul_mat_fusion;
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                      gq_stream_t stream);

@@ -107,3 +107,19 @@ def test_mul_mat_fused_rejects_without_device(lib):
     h = _lib.gq_mul_mat_fusion(0, 0.0, 1, ctypes.pointer(r))
     assert lib.gq_mul_mat_fused(w, x, _t(_lib.F32, [32, 1], [4, 128]), ctypes.byref(h), None) == -1
     assert b"exclusive" in lib.gq_last_error()
+
+
+def test_mul_mat_fused_pre_add_validation(lib):
+    w = _t(_lib.Q8_0, [4096, 64], [34, 4352])
+    x = _t(_lib.F32, [4096, 1], [4, 16384])
+    d = _t(_lib.F32, [64, 1], [4, 256])
+    s = _lib.make_tensor(0x2000, _lib.F32, [4096, 1], [4, 16384])
+    f = _lib.gq_mul_mat_fusion(0, 0.0, 0, None, None, ctypes.pointer(s))
+    assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(f), None) == -1  # b_sum needs b_add
+    a = _lib.make_tensor(0x3000, _lib.F32, [4096, 1], [4, 16384])
+    g = _lib.gq_mul_mat_fusion(0, 0.0, 0, None, ctypes.pointer(a), ctypes.pointer(x))
+    assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(g), None) == -1  # b_sum aliases b
+    assert b"alias" in lib.gq_last_error()
+    bad = _lib.make_tensor(0x3000, _lib.F32, [2048, 1], [4, 8192])
+    h = _lib.gq_mul_mat_fusion(0, 0.0, 0, None, ctypes.pointer(bad), None)
+    assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(h), None) == -1  # b_add shaped like b

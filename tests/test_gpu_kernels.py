@@ -154,7 +154,8 @@ def test_mul_mat_strided_rows():
     (O.Q8_0, 8192, 1536, 1, True, True, False),     # split-K (KS = 2) with SWIGLU pairs
     (O.Q4_0, 4096, 4096, 4, True, True, False),
 ])
-def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add):
+@pytest.mark.parametrize("pre_add", [False, True])
+def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add, pre_add):
     """gq_mul_mat_fused gives exactly the bits of RMS_NORM / MUL_MAT / SWIGLU / ADD run
     one by one (those are pinned against the oracle above)."""
     g = torch.Generator(device=DEV)
@@ -162,7 +163,12 @@ def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add):
     w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
     x = torch.randn((M, K), generator=g, device=DEV) * 3.0
     eps = 1e-5
-    h = ops.rms_norm(x, eps) if rms else x
+    xin = x
+    if pre_add:  # ADD(x, d) feeding the node; the sum is stored for later nodes
+        d = torch.randn((M, K), generator=g, device=DEV)
+        x_sum_want = ops.add(x, d)
+        xin = x_sum_want
+    h = ops.rms_norm(xin, eps) if rms else xin
     y = ops.mul_mat(w, h)
     if glu:
         want = ops.swiglu(y)
@@ -171,14 +177,21 @@ def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add):
         want = ops.add(r, y)
     else:
         want = y
+    kw = dict(rms_eps=eps if rms else None)
+    x_sum = None
+    if pre_add:
+        x_sum = torch.full_like(x, float("nan"))
+        kw.update(x_add=d, x_sum=x_sum)
     if add:
         got = r.clone()
-        ops.mul_mat_fused(w, x, out=got, rms_eps=eps if rms else None, add=got)  # in place, as the decoder runs it
+        ops.mul_mat_fused(w, x, out=got, add=got, **kw)  # in place
     else:
-        got = ops.mul_mat_fused(w, x, rms_eps=eps if rms else None, swiglu=glu)
+        got = ops.mul_mat_fused(w, x, swiglu=glu, **kw)
     torch.cuda.synchronize()
     assert got.shape == want.shape
     assert torch.equal(got, want), (got - want).abs().max().item()
+    if pre_add:
+        assert torch.equal(x_sum, x_sum_want)
 
 
 # --------------------------------------------------------------- set_rows ---
