@@ -36,6 +36,7 @@ struct Plan {
     int64_t G, NQ, n_qt, n_chunks, cps, n_split;
     bool dec;               // k_attn_dec: one workgroup per (split, kv head), all NQ queries
     int64_t rows_per_split;  // dec only
+    int dec_u;               // dec only: rows per lane stream
 };
 
 Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
@@ -44,15 +45,22 @@ Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     p.NQ = p.G * S;
     p.n_qt = cdiv(p.NQ, QT);
     p.n_chunks = cdiv(n_kv, CH);
-    p.dec = p.NQ <= DEC_MAX_NQ && (D == 64 || D == 128);
+    // (contexts past MAX_SPLIT splits of the largest rows-per-split take the tiled kernel)
+    p.dec = p.NQ <= DEC_MAX_NQ && (D == 64 || D == 128) && n_kv <= (int64_t)MAX_SPLIT * 8 * 4 * (64 / (D / 8));
     if (p.dec) {
-        const int64_t rows_it = 4 * (64 / (D / 8));  // rows one iteration of 4 waves covers
-        const int64_t want = cdiv(DEC_TARGET_WG, Hkv);
-        int64_t rps = cdiv(cdiv(n_kv, want), rows_it) * rows_it;
-        if (rps < 2 * rows_it) rps = 2 * rows_it;
-        if (cdiv(n_kv, rps) > MAX_SPLIT) rps = cdiv(cdiv(n_kv, MAX_SPLIT), rows_it) * rows_it;
-        p.rows_per_split = rps;
-        p.n_split = cdiv(n_kv, rps);
+        // rows per split = U rows per lane stream x (4 waves x rows per wave instruction);
+        // the largest U (8, 4, 2) that still gives DEC_TARGET_WG / 2 workgroups
+        const int64_t rows_it = 4 * (64 / (D / 8));
+        const int umax = p.NQ > 4 ? 4 : 8;
+        int u = umax;
+        while (u > 2 && Hkv * cdiv(n_kv, u * rows_it) < DEC_TARGET_WG / 2) u >>= 1;
+        if (const char* e = getenv("GQ_ATTN_U")) {  // tuning measurements
+            const int f = atoi(e);
+            if (f == 2 || f == 4 || (f == 8 && umax == 8)) u = f;
+        }
+        p.dec_u = u;
+        p.rows_per_split = u * rows_it;
+        p.n_split = cdiv(n_kv, p.rows_per_split);
         p.cps = 0;
         return p;
     }
@@ -64,6 +72,51 @@ Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     p.n_split = cdiv(p.n_chunks, p.cps);
     p.rows_per_split = 0;
     return p;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// sum over aligned groups of W lanes (W = 8 or 16) with DPP; every lane gets its group's total
+template <int W>
+__device__ __forceinline__ float lanes_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror: 8-lane totals
+    if constexpr (W == 16) v += dpp_f<0x140>(v);  // row_mirror: 16-lane totals
+    return v;
+}
+
+// value pairs {own, partner} for partner = lane ^ 8 (within rows of 16), lane ^ 16, lane ^ 32
+struct Pair {
+    float a, b;
+};
+__device__ __forceinline__ Pair xchg_row8(float x) { return {x, dpp_f<0x128>(x)}; }  // row_ror:8
+__device__ __forceinline__ Pair xchg_16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ Pair xchg_32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+
+// online-softmax states (m, l, o[8]) of two lanes merged into both
+template <typename X>
+__device__ __forceinline__ void merge_pair(float& m, float& l, float (&o)[8], X xchg) {
+    const Pair pm = xchg(m), pl = xchg(l);
+    const float mn = fmaxf(pm.a, pm.b);
+    const float a1 = mn == -INFINITY ? 0.0f : __expf(pm.a - mn);
+    const float a2 = mn == -INFINITY ? 0.0f : __expf(pm.b - mn);
+    l = pl.a * a1 + pl.b * a2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const Pair po = xchg(o[e]);
+        o[e] = po.a * a1 + po.b * a2;
+    }
+    m = mn;
 }
 
 __device__ __forceinline__ void h8_to_f(const uint4 w, float* f) {
@@ -83,7 +136,7 @@ __device__ __forceinline__ void h8_to_f(const uint4 w, float* f) {
 // are not read. Streams merge by shuffles inside the wave and through LDS across
 // the 4 waves; the result is the output (one split) or an fp32 partial
 // (O, max, sum) for k_attn_merge.
-template <int D, int NQ>
+template <int D, int NQ, int U>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int64_t rps, int n_split, float m0,
                                                   float m1, uint32_t n_head_log2, int q_f16,
                                                   float* __restrict__ part) {
@@ -127,81 +180,86 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         for (int e = 0; e < 8; ++e) o[u][e] = 0.0f;
     }
 
-    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.k) + (int64_t)hk * a.knb2 + d0 * 2;
-    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.v) + (int64_t)hk * a.vnb2 + d0 * 2;
     const int64_t r_begin = (int64_t)split * rps;
     const int64_t r_end = min<int64_t>(a.n_kv, r_begin + rps);
 
-    // two rows per lane stream in flight: rows r and r + ROWS_IT
-    for (int64_t r = r_begin + wave * RPI + grp; r < r_end; r += 2 * ROWS_IT) {
-        int64_t rr[2] = {r, r + ROWS_IT};
-        float mk[2][NQ];
-        bool live[2];
-        uint4 kw[2], vw[2];
+    // All U rows of this lane's stream (rows r0 + t * ROWS_IT) are requested at once,
+    // together with their mask values: one memory round trip per workgroup. K/V rows
+    // are raw buffer loads over [0, n_kv) of this head, so rows past n_kv return 0
+    // without a fetch; masked rows are read and then weigh exp(-inf) = 0.
+    const int64_t r0 = r_begin + wave * RPI + grp;
+    auto rsrc = [&](const void* p, int64_t nb2, int64_t nb1) {
+        const uint64_t base = reinterpret_cast<uint64_t>(p) + (uint64_t)(hk * nb2);
+        const int64_t bytes = a.n_kv * nb1;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+        const uint32_t n = (uint32_t)(bytes > 0x7fffffff ? 0x7fffffff : bytes);
+        return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                                 (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t krs = rsrc(a.k, a.knb2, a.knb1), vrs = rsrc(a.v, a.vnb2, a.vnb1);
+    u32x4 kw[U], vw[U];
+    float mk[U][NQ];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const bool in = rr[t] < r_end;
-            live[t] = false;
-#pragma unroll
-            for (int u = 0; u < NQ; ++u) {
-                float mv = 0.0f;
-                if (!in || u >= nq) mv = -INFINITY;
-                else if (mrow[u]) {
-                    const float x = h2f(mrow[u][rr[t]]);
-                    mv = x == -INFINITY ? -INFINITY : slope[u] * x;
-                }
-                mk[t][u] = mv;
-                live[t] = live[t] || mv != -INFINITY;
-            }
-            kw[t] = make_uint4(0, 0, 0, 0), vw[t] = make_uint4(0, 0, 0, 0);
-            if (live[t]) {
-                kw[t] = *reinterpret_cast<const uint4*>(kbase + rr[t] * a.knb1);
-                vw[t] = *reinterpret_cast<const uint4*>(vbase + rr[t] * a.vnb1);
-            }
-        }
-        float kf[2][8], vf[2][8];
-        h8_to_f(kw[0], kf[0]), h8_to_f(kw[1], kf[1]);
-        h8_to_f(vw[0], vf[0]), h8_to_f(vw[1], vf[1]);
+    for (int t = 0; t < U; ++t) {
+        const int64_t r = r0 + (int64_t)t * ROWS_IT;
+        const bool in = r < r_end;
+        const uint32_t ko = in ? (uint32_t)(r * a.knb1 + d0 * 2) : 0x80000000u;
+        const uint32_t vo = in ? (uint32_t)(r * a.vnb1 + d0 * 2) : 0x80000000u;
+        kw[t] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
+        vw[t] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
 #pragma unroll
         for (int u = 0; u < NQ; ++u) {
-            float sc[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc = fmaf(q[u][e], kf[t][e], acc);
-                acc = xor_sum<LPR>(acc);
-                if (a.softcap != 0.0f) acc = a.softcap * tanhf(acc);
-                sc[t] = mk[t][u] == -INFINITY ? -INFINITY : acc + mk[t][u];
+            float mv = 0.0f;
+            if (!in || u >= nq) mv = -INFINITY;
+            else if (mrow[u]) {
+                const float x = h2f(mrow[u][r]);
+                mv = x == -INFINITY ? -INFINITY : slope[u] * x;
             }
-            const float mn = fmaxf(m[u], fmaxf(sc[0], sc[1]));
-            if (mn == -INFINITY) continue;
-            const float al = __expf(m[u] - mn);  // exp(-inf) = 0 for an empty stream
-            const float p0 = __expf(sc[0] - mn), p1 = __expf(sc[1] - mn);
-            l[u] = l[u] * al + p0 + p1;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[u][e] = fmaf(p1, vf[1][e], fmaf(p0, vf[0][e], o[u][e] * al));
-            m[u] = mn;
+            mk[t][u] = mv;
         }
     }
-
-    // merge the row streams of the wave (lanes xor LPR, 2 LPR, ...)
 #pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
+    for (int u = 0; u < NQ; ++u) {
+        float sc[U];
+        float mx = m[u];
 #pragma unroll
-        for (int u = 0; u < NQ; ++u) {
-            const float mo = __shfl_xor(m[u], off, 64), lo = __shfl_xor(l[u], off, 64);
-            float oo[8];
+        for (int t = 0; t < U; ++t) {
+            float kf[8];
+            h8_to_f(make_uint4(kw[t].x, kw[t].y, kw[t].z, kw[t].w), kf);
+            float acc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) oo[e] = __shfl_xor(o[u][e], off, 64);
-            const float mn = fmaxf(m[u], mo);
-            if (mn == -INFINITY) continue;
-            const float a1 = __expf(m[u] - mn), a2 = __expf(mo - mn);
-            l[u] = l[u] * a1 + lo * a2;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[u][e] = o[u][e] * a1 + oo[e] * a2;
-            m[u] = mn;
+            for (int e = 0; e < 8; ++e) acc = fmaf(q[u][e], kf[e], acc);
+            acc = lanes_sum<LPR>(acc);
+            if (a.softcap != 0.0f) acc = a.softcap * tanhf(acc);
+            sc[t] = mk[t][u] == -INFINITY ? -INFINITY : acc + mk[t][u];
+            mx = fmaxf(mx, sc[t]);
         }
+        if (mx == -INFINITY) continue;
+        const float al = __expf(m[u] - mx);  // exp(-inf) = 0 for an empty stream
+        l[u] *= al;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[u][e] *= al;
+#pragma unroll
+        for (int t = 0; t < U; ++t) {
+            const float p = __expf(sc[t] - mx);
+            float vf[8];
+            h8_to_f(make_uint4(vw[t].x, vw[t].y, vw[t].z, vw[t].w), vf);
+            l[u] += p;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[u][e] = fmaf(p, vf[e], o[u][e]);
+        }
+        m[u] = mx;
+    }
+
+    // merge the row streams of the wave: partner lanes (xor 8 for D = 64, then xor 16,
+    // xor 32) exchanged with DPP / permlane swaps (VALU, no LDS); the merge of two
+    // (m, l, o) states is symmetric, so each lane may combine the pair in any order
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+        if constexpr (LPR == 8) merge_pair(m[u], l[u], o[u], xchg_row8);
+        merge_pair(m[u], l[u], o[u], xchg_16);
+        merge_pair(m[u], l[u], o[u], xchg_32);
     }
     if (grp == 0) {
 #pragma unroll
@@ -497,20 +555,29 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     if (p.dec) {
         const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv);
         const int nq = (int)p.NQ, G = (int)p.G, ns = (int)p.n_split;
-#define GQ_DEC(DD, NN)                                                                                         \
-    hipLaunchKernelGGL((k_attn_dec<DD, NN>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
+#define GQ_DEC(DD, NN, UU)                                                                                       \
+    hipLaunchKernelGGL((k_attn_dec<DD, NN, UU>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
                        n_head_log2, q_f16, part)
+#define GQ_DEC_U(DD, NN)                           \
+    do {                                           \
+        if (p.dec_u == 8) GQ_DEC(DD, NN, 8);       \
+        else if (p.dec_u == 4) GQ_DEC(DD, NN, 4);  \
+        else GQ_DEC(DD, NN, 2);                    \
+    } while (0)
         if (a.D == 128) {
-            if (nq == 1) GQ_DEC(128, 1);
-            else if (nq == 2) GQ_DEC(128, 2);
-            else if (nq <= 4) GQ_DEC(128, 4);
-            else GQ_DEC(128, 8);
+            if (nq == 1) GQ_DEC_U(128, 1);
+            else if (nq == 2) GQ_DEC_U(128, 2);
+            else if (nq <= 4) GQ_DEC_U(128, 4);
+            else if (p.dec_u == 4) GQ_DEC(128, 8, 4);  // u <= 4 for more than 4 query vectors
+            else GQ_DEC(128, 8, 2);
         } else {
-            if (nq == 1) GQ_DEC(64, 1);
-            else if (nq == 2) GQ_DEC(64, 2);
-            else if (nq <= 4) GQ_DEC(64, 4);
-            else GQ_DEC(64, 8);
+            if (nq == 1) GQ_DEC_U(64, 1);
+            else if (nq == 2) GQ_DEC_U(64, 2);
+            else if (nq <= 4) GQ_DEC_U(64, 4);
+            else if (p.dec_u == 4) GQ_DEC(64, 8, 4);
+            else GQ_DEC(64, 8, 2);
         }
+#undef GQ_DEC_U
 #undef GQ_DEC
     } else {
     const dim3 grid((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)p.n_qt);
