@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="decode budget of the CPU sample")
     p.add_argument("--c1-launches", type=int, default=400)
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="only launch one token's decode GEMVs and a 256 MiB device copy, eagerly, 3 times each "
+                        "(the workload of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs behind roofline.traffic)")
     return p.parse_args()
 
 
@@ -88,6 +91,8 @@ def main() -> int:
     log(f"building {cfg.name} Q4_0 weights on device")
     w = random_weights(cfg, dev, seed=1234)
     torch.cuda.synchronize()
+    if args.traffic_probe:
+        return traffic_probe(w, cfg, dev)
     n_ctx = args.prompt + args.warmup + args.steps
     max_ctx = pad_kv_len(n_ctx, 1 << 30)
     dec = Decoder(w, max_ctx, dev)
@@ -175,13 +180,7 @@ def main() -> int:
     log(f"tg {tg_tok_s:.1f} tok/s ({ms_step:.3f} ms/token)")
 
     # ---- roofline: the 129 decode GEMVs of one token, one graph, HIP events
-    x_h = torch.randn((1, cfg.n_embd), generator=gen, device=dev)
-    x_f = torch.randn((1, cfg.n_ff), generator=gen, device=dev)
-    mats = []
-    for L in w.layers:
-        mats += [(L.qkv, x_h), (L.o, x_h), (L.gate_up, x_h), (L.down, x_f)]
-    mats.append((w.lm_head, x_h))
-    outs = [torch.empty((1, m.N), device=dev) for m, _ in mats]
+    mats, outs = decode_gemvs(w, cfg, dev, gen)
     ws = ops.Workspace(dev)
     ws.get(1 << 20)
 
@@ -333,7 +332,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": load_traffic("k_gemv_grp<Q4_0, M=1> decode mix"),
             "bytes_per_launch": round(gemv_bytes_token / n_gemv),
             "us_per_launch": round(gemv_ms_token * 1e3 / n_gemv, 3),
             "launches_per_token": n_gemv,
@@ -366,6 +365,54 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def decode_gemvs(w, cfg, dev, gen):
+    """The 129 decode GEMVs of one token (qkv, o, gate_up, down per layer; lm_head)
+    with activations of the right widths."""
+    import torch
+
+    x_h = torch.randn((1, cfg.n_embd), generator=gen, device=dev)
+    x_f = torch.randn((1, cfg.n_ff), generator=gen, device=dev)
+    mats = []
+    for L in w.layers:
+        mats += [(L.qkv, x_h), (L.o, x_h), (L.gate_up, x_h), (L.down, x_f)]
+    mats.append((w.lm_head, x_h))
+    outs = [torch.empty((1, m.N), device=dev) for m, _ in mats]
+    return mats, outs
+
+
+def traffic_probe(w, cfg, dev) -> int:
+    """Eager launches for the PMC runs (per-dispatch counters do not survive graph
+    replay under the profiler): 3 x the decode GEMV mix, then 3 x a 256 MiB device copy
+    whose FETCH_SIZE / WRITE_SIZE calibrate the counters (256 MiB each way)."""
+    import torch
+
+    from ggmlc_amd import ops
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    mats, outs = decode_gemvs(w, cfg, dev, gen)
+    for _ in range(3):
+        for (m, x), o in zip(mats, outs):
+            ops.mul_mat(m, x, out=o)
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"traffic probe: {3 * len(mats)} GEMV launches, 3 copies of {a.numel()} bytes")
+    return 0
+
+
+def load_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of `kernel` measured by the PMC runs and summarised in
+    profiles/gemv_traffic.json (null when absent)."""
+    f = ROOT / "profiles" / "gemv_traffic.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text()).get(kernel)
+    return None if d is None else float(d["hbm_bytes_per_launch"])
 
 
 def cpu_baseline(w, cfg, seconds: float) -> dict:
