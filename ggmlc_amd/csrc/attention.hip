@@ -296,6 +296,251 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
     }
 }
 
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// Prefill attention on the matrix cores (v_mfma_f32_16x16x32_f16), no ALiBi / softcap.
+// A workgroup owns 64 query vectors of one kv head (4 waves x 16), walks the KV range
+// in blocks of 64 keys staged in LDS (K as [key][dim], V transposed to [dim][key]),
+// and keeps an online softmax per query in registers:
+//   S^T (16 keys x 16 queries tiles) = K_blk . Q^T, with Q = q_hi + q_lo split into two
+//   fp16 parts (q_lo = 0 when the query is rounded to fp16), so the scores carry fp32
+//   accuracy; s = S * scale + mask; O^T += V^T . P^T with P = p_hi + p_lo split the same
+//   way (fp32-level products, accumulated in fp32).
+// MFMA 16x16x32 operand layouts (lane l, j = l % 16, g = l / 16): A[i][k]: i = j,
+// k = 8g..8g+7; B[k][n]: n = j, k = 8g..8g+7; C[i][n]: n = j, i = 4g..4g+3. The
+// S^T accumulator of lane l therefore holds query j and keys 16t + 4g + r; used as the
+// B operand of the PV product (K = 32 keys of tiles t0, t1) its 8 values are keys
+// (4g..4g+3, 16+4g..16+4g+3), and the V^T operand is read in that same key order.
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int q_f16) {
+    constexpr int BKV = 64;
+    constexpr int LDK = D + 8;      // halves per K row in LDS
+    constexpr int LDV = BKV + 8;    // halves per V^T row in LDS
+    constexpr int KS = D / 32;      // k-steps of the QK product
+    constexpr int DT = D / 16;      // 16-dim tiles of O^T
+    __shared__ __align__(16) _Float16 sK[BKV * LDK];
+    __shared__ __align__(16) _Float16 sVT[D * LDV];
+    __shared__ int s_vote[2][4];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int hk = blockIdx.y;
+    const int qv = blockIdx.x * 64 + wave * 16 + j;  // this lane's query vector
+    const bool qok = qv < NQ;
+    const int64_t h = (int64_t)hk * G + (qok ? qv % G : 0);
+    const int64_t qi = qok ? qv / G : 0;             // its query row (mask row, output row)
+
+    // Q^T operand: dims 32 ks + 8 g .. +7 of query qv, hi and lo fp16 parts
+    half8_t qh[KS], ql[KS];
+    {
+        const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + qi * a.qnb1 +
+                                                         h * a.qnb2);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = qok ? qp[32 * ks + 8 * g + e] : 0.0f;
+                const _Float16 hi = (_Float16)x;
+                qh[ks][e] = hi;
+                ql[ks][e] = q_f16 ? (_Float16)0.0f : (_Float16)(x - (float)hi);
+            }
+    }
+    float4_t o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    // K/V rows of this kv head as raw buffers over [0, n_kv): rows past n_kv read 0
+    auto rsrc = [&](const void* p, int64_t nb2, int64_t nb1) {
+        const uint64_t base = reinterpret_cast<uint64_t>(p) + (uint64_t)(hk * nb2);
+        const int64_t bytes = a.n_kv * nb1;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+        const uint32_t n = (uint32_t)(bytes > 0x7fffffff ? 0x7fffffff : bytes);
+        return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                                 (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t krs = rsrc(a.k, a.knb2, a.knb1), vrs = rsrc(a.v, a.vnb2, a.vnb1);
+    // staging: the block's 64 rows x D halves of K and of V in 16-byte pieces
+    constexpr int PPR = D / 8;                 // pieces per row
+    constexpr int NPC = BKV * PPR / 256;       // pieces per thread per matrix (2 or 4)
+    u32x4 kreg[NPC], vreg[NPC];
+    auto fetch = [&](int64_t c0) {
+#pragma unroll
+        for (int u = 0; u < NPC; ++u) {
+            const int idx = tid + 256 * u, r = idx / PPR, pc = idx % PPR;
+            const int64_t row = c0 + r;
+            const uint32_t ko = row < a.n_kv ? (uint32_t)(row * a.knb1 + pc * 16) : 0x80000000u;
+            const uint32_t vo = row < a.n_kv ? (uint32_t)(row * a.vnb1 + pc * 16) : 0x80000000u;
+            kreg[u] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
+            vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
+        }
+    };
+    auto park = [&]() {
+#pragma unroll
+        for (int u = 0; u < NPC; ++u) {
+            const int idx = tid + 256 * u, r = idx / PPR, pc = idx % PPR;
+            *reinterpret_cast<u32x4*>(&sK[r * LDK + pc * 8]) = kreg[u];
+            const uint32_t w4[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint16_t lo16 = (uint16_t)(w4[e] & 0xffff), hi16 = (uint16_t)(w4[e] >> 16);
+                __builtin_memcpy(&sVT[(pc * 8 + 2 * e) * LDV + r], &lo16, 2);
+                __builtin_memcpy(&sVT[(pc * 8 + 2 * e + 1) * LDV + r], &hi16, 2);
+            }
+        }
+    };
+
+    const uint8_t* mrow = a.mask && qok ? reinterpret_cast<const uint8_t*>(a.mask) + qi * a.mnb1 : nullptr;
+    const int nblk = (int)((a.n_kv + BKV - 1) / BKV);
+    // mask values of this lane's keys (16 t + 4 g + r) of the block at c0, as fp16 bits
+    // (0xFC00 = -inf for keys past n_kv and for lanes without a query)
+    auto load_mask = [&](int64_t c0, uint16_t (&mh)[4][4]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int64_t key = c0 + 16 * t + 4 * g;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                uint16_t v = 0;
+                if (key + r >= a.n_kv || !qok) v = 0xFC00;
+                else if (mrow) v = reinterpret_cast<const uint16_t*>(mrow)[key + r];
+                mh[t][r] = v;
+            }
+        }
+    };
+    // A block is skipped when every mask value the tile sees in it is -32768 or below
+    // (the executor's masked value) and every query of the tile already holds a
+    // running max from an unmasked key: exp(s - 32768 - m) is exactly 0 in fp32 then,
+    // so the result is unchanged. (Causal prefill skips the blocks past the diagonal.)
+    auto needed = [&](const uint16_t (&mh)[4][4]) -> int {
+        bool any = qok && !(m > -16384.0f);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) any = any || h2f(mh[t][r]) > -32768.0f;
+        return any ? 1 : 0;
+    };
+    uint16_t mk[4][4];
+    fetch(0);
+    load_mask(0, mk);
+    int need = needed(mk);
+    for (int bi = 0; bi < nblk; ++bi) {
+        const int64_t c0 = (int64_t)bi * BKV;
+        // barrier: the previous block's LDS is fully read; and the skip decision (wave
+        // votes in a slot per block parity: the next write to a slot follows a barrier
+        // every wave passes only after reading it)
+        if (lane == 0) s_vote[bi & 1][wave] = __any(need) ? 1 : 0;
+        __syncthreads();
+        const bool run = (s_vote[bi & 1][0] | s_vote[bi & 1][1] | s_vote[bi & 1][2] | s_vote[bi & 1][3]) != 0;
+        if (run) {
+            park();
+            __syncthreads();
+        }
+        if (bi + 1 < nblk) fetch(c0 + BKV);
+        if (run) {
+            // S^T tiles: keys 16 t .. 16 t + 15 x this wave's 16 queries
+            float4_t st[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const half8_t kf = *reinterpret_cast<const half8_t*>(&sK[(16 * t + j) * LDK + 32 * ks + 8 * g]);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], c, 0, 0, 0);
+                    if (!q_f16) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], c, 0, 0, 0);
+                }
+                st[t] = c;
+            }
+            // online softmax for query j: this lane's 16 keys, then lanes j + 16 g'
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float mv = h2f(mk[t][r]);
+                    const float sv = mv == -INFINITY ? -INFINITY : st[t][r] * a.scale + mv;
+                    st[t][r] = sv;
+                    bmax = fmaxf(bmax, sv);
+                }
+            {
+                const Pair p16 = xchg_16(bmax);
+                bmax = fmaxf(p16.a, p16.b);
+                const Pair p32 = xchg_32(bmax);
+                bmax = fmaxf(p32.a, p32.b);
+            }
+            const float mn = fmaxf(m, bmax);
+            const float al = mn == -INFINITY ? 1.0f : __expf(m - mn);  // m = -inf: nothing accumulated yet
+            // P^T operands: keys (32 kk + 4 g .. +3, 32 kk + 16 + 4 g .. +3), p = p_hi + p_lo in fp16
+            half8_t pb[2], pl[2];
+            float psum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pv = mn == -INFINITY ? 0.0f : __expf(st[t][r] - mn);
+                    const _Float16 ph = (_Float16)pv;
+                    psum += pv;
+                    pb[t >> 1][4 * (t & 1) + r] = ph;
+                    pl[t >> 1][4 * (t & 1) + r] = (_Float16)(pv - (float)ph);
+                }
+            {
+                const Pair p16 = xchg_16(psum);
+                psum = p16.a + p16.b;
+                const Pair p32 = xchg_32(psum);
+                psum = p32.a + p32.b;
+            }
+            l = l * al + psum;
+            m = mn;
+            // O^T (dims x queries) += V^T . P^T; V^T operand in the key order of pb
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                float4_t c = o[dt] * al;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const _Float16* vr = &sVT[(16 * dt + j) * LDV + 32 * kk + 4 * g];
+                    half8_t vf;
+                    __builtin_memcpy(&vf, vr, 8);
+                    __builtin_memcpy(reinterpret_cast<_Float16*>(&vf) + 4, vr + 16, 8);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb[kk], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[kk], c, 0, 0, 0);
+                }
+                o[dt] = c;
+            }
+        }
+        if (bi + 1 < nblk) {
+            load_mask(c0 + BKV, mk);
+            need = needed(mk);
+        }
+    }
+    if (!qok) return;
+    const float inv = l == 0.0f ? 0.0f : 1.0f / l;
+    float* op = a.dst + (qi * a.Hq + h) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) op[16 * dt + 4 * g + r] = o[dt][r] * inv;
+}
+
+// GQ_ATTN_NO_MMA=1 keeps prefill attention on the VALU kernel (comparison runs)
+bool mma_disabled() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("GQ_ATTN_NO_MMA");
+        v = e && atoi(e) ? 1 : 0;
+    }
+    return v == 1;
+}
+
+// the matrix-core prefill kernel: no ALiBi / softcap, 16-byte aligned K/V rows,
+// buffer offsets within 2 GiB
+bool mma_ok(const AttnArgs& a) {
+    if (mma_disabled()) return false;
+    if (a.max_bias != 0.0f || a.softcap != 0.0f || (a.D != 64 && a.D != 128)) return false;
+    if (a.knb1 % 16 || a.vnb1 % 16) return false;
+    return a.n_kv * a.knb1 < 0x7fff0000LL && a.n_kv * a.vnb1 < 0x7fff0000LL;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps, int n_chunks, int n_split,
                                               float m0, float m1, uint32_t n_head_log2, int q_f16,
@@ -579,6 +824,13 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         }
 #undef GQ_DEC_U
 #undef GQ_DEC
+    } else if (mma_ok(a)) {
+        const dim3 gm((unsigned)cdiv(p.NQ, 64), (unsigned)a.Hkv);
+        if (a.D == 128)
+            hipLaunchKernelGGL(k_attn_mma<128>, gm, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, q_f16);
+        else
+            hipLaunchKernelGGL(k_attn_mma<64>, gm, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, q_f16);
+        return check_hip(hipGetLastError(), "flash_attn_ext (mfma) launch");
     } else {
     const dim3 grid((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)p.n_qt);
     if (a.D == 128)

@@ -284,6 +284,28 @@ def test_flash_attn_vs_exact(Hq, Hkv, D, S, pos, ctx):
     assert r < 1e-3
 
 
+@pytest.mark.parametrize("D,G,masked", [(128, 1, 0xF800), (64, 4, 0xF800), (128, 2, 0xFC00)])
+def test_flash_attn_banded_mask_prefill(D, G, masked):
+    """Prefill (matrix-core path) under a band mask: query row i sees keys
+    (pos + i - 150, pos + i], so each query tile meets fully masked KV blocks before
+    its band (nothing accumulated yet: they must be computed) and after it (skipped),
+    with -32768 or -inf as the masked value."""
+    rng = np.random.default_rng(D + G)
+    Hkv, S, pos, n_kv = 2, 256, 300, 640
+    Hq = Hkv * G
+    q = rng.standard_normal((Hq, S, D)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, n_kv, D)))
+    vc = f16(rng.standard_normal((Hkv, n_kv, D)))
+    i = np.arange(S)[:, None]
+    jj = np.arange(n_kv)[None, :]
+    mask = np.where((jj <= pos + i) & (jj > pos + i - 150), 0, masked).astype(np.uint16)
+    got = _attn_dev(q, kc, vc, n_kv, mask)
+    exact = O.flash_attn_ext_f16(q, kc, vc, n_kv, mask, mode=1)
+    r = mar(got, exact)
+    print(f"D={D} G={G} masked={masked:#x}: vs exact {r:.2e}")
+    assert r < 1e-3
+
+
 def test_flash_attn_padding_and_gqa_invariants():
     rng = np.random.default_rng(21)
     Hq, Hkv, D, ctx, pos = 6, 2, 64, 1024, 300
