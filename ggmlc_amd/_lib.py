@@ -35,6 +35,25 @@ class gq_tensor(ctypes.Structure):
     ]
 
 
+class gq_rope_kv_epilogue(ctypes.Structure):
+    _fields_ = [
+        ("n_head", ctypes.c_int32),
+        ("n_head_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("pos", ctypes.POINTER(gq_tensor)),
+        ("n_dims", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("freq_base", ctypes.c_float),
+        ("freq_scale", ctypes.c_float),
+        ("attn_factor", ctypes.c_float),
+        ("kv_idx", ctypes.POINTER(gq_tensor)),
+        ("q_out", ctypes.POINTER(gq_tensor)),
+        ("k_cache", ctypes.POINTER(gq_tensor)),
+        ("v_cache", ctypes.POINTER(gq_tensor)),
+        ("n_bad", ctypes.c_void_p),
+    ]
+
+
 class gq_mul_mat_fusion(ctypes.Structure):
     _fields_ = [
         ("rms_norm", ctypes.c_int32),
@@ -43,6 +62,7 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("add", ctypes.POINTER(gq_tensor)),
         ("b_add", ctypes.POINTER(gq_tensor)),
         ("b_sum", ctypes.POINTER(gq_tensor)),
+        ("rope_kv", ctypes.POINTER(gq_rope_kv_epilogue)),
     ]
 
 

@@ -165,29 +165,83 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     return gemm(a->type, W, p.N, p.K, A, p.K, p.M, y, p.ldd, s);
 }
 
+// The rope + KV-store epilogue of gq_mul_mat_fused: the checks of gq_rope_kv_store
+// for q/k/v given as the rows of the product, plus the pairing conditions.
+static int rope_kv_epilogue(const gq_rope_kv_epilogue& e, const MulMatPlan& p, const gq_tensor* b, GemvFuse& fz) {
+    const int64_t hd = e.head_dim, Hq = e.n_head, Hkv = e.n_head_kv, S = p.M;
+    if (hd <= 0 || Hq <= 0 || Hkv <= 0 || p.N != (Hq + 2 * Hkv) * hd)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv heads do not match the product rows: N = " +
+                                        std::to_string(p.N));
+    if (b->ne[2] != 1 || b->ne[3] != 1) return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv needs b [K, M, 1, 1]");
+    if (!e.pos || !e.kv_idx || !e.q_out || !e.k_cache || !e.v_cache)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv: null tensor");
+    const gq_tensor *qo = e.q_out, *kc = e.k_cache, *vc = e.v_cache;
+    if (qo->type != GQ_TYPE_F32 || qo->nb[0] != 4 || qo->ne[0] != hd || qo->ne[1] != Hq || qo->ne[2] != S ||
+        qo->ne[3] != 1)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv q_out must be F32 [hd, n_head, M, 1]: " + shape(qo));
+    for (const gq_tensor* t : {kc, vc})
+        if (t->type != GQ_TYPE_F16 || t->nb[0] != 2 || t->ne[0] != hd || t->ne[2] != Hkv || t->ne[3] != 1 ||
+            t->ne[1] != kc->ne[1])
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv caches must be F16 [hd, rows, n_head_kv, 1]: " +
+                                            shape(t));
+    if (e.pos->type != GQ_TYPE_I32 || e.pos->ne[0] < S || e.pos->nb[0] != 4 || e.kv_idx->type != GQ_TYPE_I64 ||
+        e.kv_idx->ne[0] != S || e.kv_idx->nb[0] != 8)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv pos must be I32 [>= M], kv_idx I64 [M]");
+    if (e.mode != 0 && e.mode != 2) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: rope_kv modes 0 and 2 only");
+    if (e.n_dims <= 0 || e.n_dims % 2 || e.n_dims > hd) return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv bad n_dims");
+    if (hd % 4 || (e.mode == 2 && e.n_dims != hd))
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: rope_kv needs head_dim % 4 == 0 and (mode 2) n_dims == head_dim");
+    GemvRope& r = fz.rp;
+    r.pos = static_cast<const int32_t*>(e.pos->data);
+    r.hd = hd, r.Hq = Hq, r.Hkv = Hkv;
+    r.n_dims = e.n_dims, r.neox = e.mode == 2;
+    r.theta_scale = powf(e.freq_base, -2.0f / e.n_dims);
+    r.freq_scale = e.freq_scale, r.attn_factor = e.attn_factor;
+    r.qo = static_cast<float*>(qo->data), r.qonb1 = (int64_t)qo->nb[1], r.qonb2 = (int64_t)qo->nb[2];
+    r.kc = static_cast<uint16_t*>(kc->data), r.kcnb1 = (int64_t)kc->nb[1], r.kcnb2 = (int64_t)kc->nb[2];
+    r.vc = static_cast<uint16_t*>(vc->data), r.vcnb1 = (int64_t)vc->nb[1], r.vcnb2 = (int64_t)vc->nb[2];
+    r.rows = kc->ne[1];
+    r.idx = static_cast<const int64_t*>(e.kv_idx->data);
+    r.n_bad = e.n_bad;
+    fz.rope = 1;
+    fz.pair_b = r.neox ? hd : 0;
+    fz.pair_h = r.neox ? hd / 2 : 0;
+    return GQ_OK;
+}
+
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                      gq_stream_t stream) {
-    if (!dst || !f) return fail(GQ_ERR_INVALID, "mul_mat_fused: null dst or fusion");
-    if (f->swiglu && f->add) return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu and add are exclusive");
+    if (!f) return fail(GQ_ERR_INVALID, "mul_mat_fused: null fusion");
+    if ((f->swiglu != 0) + (f->add != nullptr) + (f->rope_kv != nullptr) > 1)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu, add and rope_kv are exclusive");
+    if (f->rope_kv ? dst != nullptr : dst == nullptr)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be NULL with rope_kv and given otherwise");
     MulMatPlan p;
     int rc = plan_mul_mat(a, b, nullptr, p);
     if (rc) return rc;
     if (p.M > GEMV_MAX_M)
         return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: only the GEMV path (M <= 4) is fused, M = " + std::to_string(p.M));
-    const int64_t n_out = f->swiglu ? p.N / 2 : p.N;
-    if (f->swiglu && p.N % 2) return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu needs an even row count: " + shape(a));
-    if (dst->type != GQ_TYPE_F32 || dst->ne[0] != n_out || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
-        dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
-        return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [" + std::to_string(n_out) + ", M, ...]: " +
-                                        shape(dst));
     GemvFuse fz;
+    if (f->rope_kv) {
+        rc = rope_kv_epilogue(*f->rope_kv, p, b, fz);
+        if (rc) return rc;
+    } else {
+        const int64_t n_out = f->swiglu ? p.N / 2 : p.N;
+        if (f->swiglu && p.N % 2)
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu needs an even row count: " + shape(a));
+        if (dst->type != GQ_TYPE_F32 || dst->ne[0] != n_out || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
+            dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [" + std::to_string(n_out) + ", M, ...]: " +
+                                            shape(dst));
+    }
     if (f->rms_norm) {
         fz.rms = 1;
         fz.eps = f->rms_eps;
     }
     if (f->swiglu) {
         fz.glu = 1;
-        fz.glu_half = p.N / 2;
+        fz.pair_b = p.N;
+        fz.pair_h = p.N / 2;
     }
     if (f->add) {
         const gq_tensor* r = f->add;
@@ -221,8 +275,9 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     if (p.M == 0) return GQ_OK;
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
-    return gemv(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M, static_cast<float*>(dst->data),
-                (int64_t)(dst->nb[1] / 4), fz, (hipStream_t)stream);
+    return gemv(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M,
+                dst ? static_cast<float*>(dst->data) : nullptr, dst ? (int64_t)(dst->nb[1] / 4) : 0, fz,
+                (hipStream_t)stream);
 }
 
 int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n_bad, gq_stream_t stream) {

@@ -111,6 +111,31 @@ __device__ __forceinline__ double block_sum_d(double s, double* red) {
     return r;
 }
 
+// ROPE (ops.cpp:5886-6120, ext_factor = 0) of one pair j at position p: theta =
+// p * theta_scale^j built by repeated multiplication like ggml_rope_cache_init,
+// then (cos, sin) * attn_factor and the rotation. Every kernel that rotates (k_rope,
+// k_rope_kv, the GEMV's rope epilogue) uses these, so all give the same bits.
+__device__ __forceinline__ void rope_cs(float p, int j, float theta_scale, float freq_scale, float attn_factor,
+                                        float& c, float& s) {
+#pragma clang fp contract(off)
+    float theta = p;
+    for (int t = 0; t < j; ++t) theta *= theta_scale;
+    theta *= freq_scale;
+    c = cosf(theta) * attn_factor;
+    s = sinf(theta) * attn_factor;
+}
+__device__ __forceinline__ void rope_rotate(float c, float s, float x0, float x1, float& y0, float& y1) {
+#pragma clang fp contract(off)
+    y0 = x0 * c - x1 * s;
+    y1 = x0 * s + x1 * c;
+}
+__device__ __forceinline__ void rope_pair(float p, int j, float theta_scale, float freq_scale, float attn_factor,
+                                          float x0, float x1, float& y0, float& y1) {
+    float c, s;
+    rope_cs(p, j, theta_scale, freq_scale, attn_factor, c, s);
+    rope_rotate(c, s, x0, x1, y0, y1);
+}
+
 // y = x * rms_scale(...): scale = 1 / sqrt(mean(x^2) + eps), mean rounded to fp32
 __device__ __forceinline__ float rms_scale(double sumsq, int64_t n, float eps) {
     const float mean = (float)(sumsq / (double)n);

@@ -52,19 +52,6 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, i
 // ---- ROPE (ops.cpp:5886-6120, ext_factor = 0): theta_i = p * theta_scale^i built by
 // repeated multiplication like ggml_rope_cache_init; NEOX pairs (i, i + n_dims/2),
 // NORMAL pairs (2i, 2i+1); dims >= n_dims are copied.
-// one rotated pair, shared by k_rope and k_rope_kv so the two give the same bits
-__device__ __forceinline__ void rope_pair(float p, int j, float theta_scale, float freq_scale, float attn_factor,
-                                          float x0, float x1, float& y0, float& y1) {
-#pragma clang fp contract(off)
-    float theta = p;
-    for (int t = 0; t < j; ++t) theta *= theta_scale;
-    theta *= freq_scale;
-    const float c = cosf(theta) * attn_factor;
-    const float s = sinf(theta) * attn_factor;
-    y0 = x0 * c - x1 * s;
-    y1 = x0 * s + x1 * c;
-}
-
 __global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, int64_t ne0, int64_t ne1, int64_t ne2,
                                               int64_t xnb1, int64_t xnb2, int64_t xnb3, const int32_t* __restrict__ pos,
                                               float* __restrict__ y, int64_t ynb1, int64_t ynb2, int64_t ynb3,

@@ -122,11 +122,13 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Physical weight row of logical row r: with the SWIGLU epilogue, logical rows
-// 2c and 2c+1 are the gate row c and the up row c + N/2, so both land in the same
-// wave (rows of a wave are 4 consecutive logical rows).
+// Physical weight row of logical row r. Paired epilogues (SWIGLU, rope) need the two
+// rows of a pair in one wave (rows of a wave are 4 consecutive logical rows), so
+// logical rows 2c, 2c+1 of a pair block read the physical rows of the pair.
 __device__ __forceinline__ int64_t phys_row(const GemvFuse& fz, int64_t r) {
-    return fz.glu ? (r >> 1) + (r & 1) * fz.glu_half : r;
+    if (fz.pair_b == 0) return r;
+    const int64_t b0 = (r / fz.pair_b) * fz.pair_b;
+    return b0 + ((r - b0) >> 1) + (r & 1) * fz.pair_h;
 }
 
 // silu(g) * u with the arithmetic of k_swiglu (x / (1 + expf(-x)) * g)
@@ -135,13 +137,65 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
     return sg * u;
 }
 
+// (cos, sin) of every rotated pair of the M positions, computed once per workgroup
+// into LDS (tab[m * n_dims/2 + j]) while the first weight loads are in flight
+template <int M>
+__device__ __forceinline__ void rope_table(const GemvRope& r, float2* tab) {
+    const int np = r.n_dims >> 1;
+    for (int idx = threadIdx.x; idx < M * np; idx += blockDim.x) {
+        const int m = idx / np, j = idx - m * np;
+        float c, s;
+        rope_cs((float)r.pos[m], j, r.theta_scale, r.freq_scale, r.attn_factor, c, s);
+        tab[idx] = make_float2(c, s);
+    }
+}
+
+// Rope epilogue of a fused QKV product, from the even logical row of a pair (v0, v1:
+// the pair's two dims i0, i1 of head `head`): the work of k_rope_kv for those dims
+// with the same arithmetic (q rotated into qo; k rotated, v copied, both rounded
+// to fp16 into cache row idx[m]; bad rows counted once per token and kv head).
+__device__ __forceinline__ void rope_emit(const GemvRope& r, const float2* tab, int m, int64_t row, float v0,
+                                          float v1) {
+    const int64_t head = row / r.hd;
+    const int c = (int)((row - head * r.hd) >> 1);
+    const int i0 = r.neox ? c : 2 * c;
+    const int i1 = r.neox ? c + (int)(r.hd >> 1) : 2 * c + 1;
+    float y0 = v0, y1 = v1;
+    if (head < r.Hq + r.Hkv && 2 * c < r.n_dims) {
+        const float2 cs = tab[m * (r.n_dims >> 1) + c];
+        rope_rotate(cs.x, cs.y, v0, v1, y0, y1);
+    }
+    if (head < r.Hq) {
+        float* q = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(r.qo) + m * r.qonb2 + head * r.qonb1);
+        q[i0] = y0;
+        q[i1] = y1;
+        return;
+    }
+    const int64_t kv = r.idx[m];
+    if (kv < 0 || kv >= r.rows) {
+        if (c == 0 && r.n_bad) atomicAdd(r.n_bad, 1);
+        return;
+    }
+    const bool is_k = head < r.Hq + r.Hkv;
+    uint16_t* y = is_k ? reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(r.kc) + kv * r.kcnb1 +
+                                                      (head - r.Hq) * r.kcnb2)
+                       : reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(r.vc) + kv * r.vcnb1 +
+                                                      (head - r.Hq - r.Hkv) * r.vcnb2);
+    y[i0] = f2h(y0);
+    y[i1] = f2h(y1);
+}
+
 // Write logical row `row` of activation m: plain, residual-added (res + v: the
-// operand order of ADD(x, MUL_MAT)), or, for the SWIGLU epilogue, from the even
-// row with its partner's value vp.
-__device__ __forceinline__ void emit(const GemvFuse& fz, float* dst, int64_t ldd, int m, int64_t row, float v,
-                                     float vp) {
+// operand order of ADD(x, MUL_MAT)), or, for the paired epilogues (SWIGLU, rope),
+// from the even row with its partner's value vp.
+__device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, float* dst, int64_t ldd, int m,
+                                     int64_t row, float v, float vp) {
     if (fz.glu) {
         if ((row & 1) == 0) dst[(int64_t)m * ldd + (row >> 1)] = swiglu1(v, vp);
+        return;
+    }
+    if (fz.rope) {
+        if ((row & 1) == 0) rope_emit(fz.rp, rtab, m, row, v, vp);
         return;
     }
     if (fz.res) v = fz.res[(int64_t)m * fz.ldr + row] + v;
@@ -169,6 +223,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     const int act_bytes = G * ACT_GS;
     uint8_t* s_act = smem;
     uint8_t* s_stage = smem + M * act_bytes + wave * 64 * GB;
+    float2* rtab = reinterpret_cast<float2*>(smem + M * act_bytes + WAVES * 64 * GB);  // rope epilogue only
 
     const int rsub = lane / LPR;
     const int gsub = lane % LPR;
@@ -216,13 +271,15 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     // memory access: rows past N, chunks past the K range of a tail step and steps
     // past the end of the wave's sequence never touch memory.
     // Chunk c of a lane is byte 16 * within of slice row r (r, within from lane + 64 c);
-    // with the SWIGLU epilogue slice rows 2i, 2i+1 are gate row i and up row i + N/2.
-    const int64_t mat_bytes = (fz.glu ? fz.glu_half : N) * row_bytes * (fz.glu ? 2 : 1);
+    // with paired rows (phys_row) slice rows 2i, 2i+1 are physical rows i and i + pair_h
+    // past the slice's first physical row (a slice never straddles a pair block: pair_b
+    // is N or a multiple of 4).
+    const int64_t mat_bytes = N * row_bytes;
     uint32_t voff[CPG];
 #pragma unroll
     for (int c = 0; c < CPG; ++c) {
         const int ci = lane + 64 * c, r = ci / SEG, within = ci - r * SEG;
-        const int64_t roff = fz.glu ? (int64_t)(r >> 1) + (r & 1) * fz.glu_half : (int64_t)r;
+        const int64_t roff = fz.pair_b ? (int64_t)(r >> 1) + (r & 1) * fz.pair_h : (int64_t)r;
         voff[c] = (uint32_t)(roff * row_bytes + within * 16);
     }
     const int ngr_tail = g_end - g_begin - (S - 1) * LPR;  // groups of the last step of a tile
@@ -231,7 +288,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     int lk = 0, lj = 0;
     auto issue = [&](uint4(&buf)[CPG]) {
         const int64_t row0 = ((int64_t)blockIdx.x + (int64_t)lk * gridDim.x) * ROWS + rg * RPW;
-        const int64_t prow = fz.glu ? row0 >> 1 : row0;
+        const int64_t prow = fz.pair_b ? phys_row(fz, row0) : row0;
         const int gfirst = g_begin + lj * LPR;
         const int64_t off0 = prow * row_bytes + (int64_t)gfirst * GB;
         const int64_t left = lk < my_wgt ? mat_bytes - off0 : 0;
@@ -316,7 +373,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         if (fz.rms) rms_scales<XVEC, M>(act, M, G * 256, fz.eps, scale, red_d);
         quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, G * 256, s_act, act_bytes, scale);
     }
-    __syncthreads();  // quantized activation visible to all waves
+    if (fz.rope) rope_table<M>(fz.rp, rtab);
+    __syncthreads();  // quantized activation (and rope table) visible to all waves
 
     float acc[M];
 #pragma unroll
@@ -378,8 +436,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                 acc[m] = 0.0f;
                 if constexpr (KS == 1) {
                     float vp = 0.0f;
-                    if (fz.glu) vp = __shfl_xor(v, LPR, 64);  // the next row's value (SWIGLU pairs)
-                    if (gsub == 0 && row < N) emit(fz, dst, ldd, m, row, v, vp);
+                    if (fz.glu | fz.rope) vp = __shfl_xor(v, LPR, 64);  // the next row's value (pairs)
+                    if (gsub == 0 && row < N) emit(fz, rtab, dst, ldd, m, row, v, vp);
                 } else {
                     if (gsub == 0) red[wave][m][rsub] = v;
                 }
@@ -392,7 +450,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                         float v = red[wave][m][rsub], vp = red[wave][m][rsub ^ 1];
 #pragma unroll
                         for (int k = 1; k < KS; ++k) v += red[wave + k][m][rsub], vp += red[wave + k][m][rsub ^ 1];
-                        emit(fz, dst, ldd, m, row, v, vp);
+                        emit(fz, rtab, dst, ldd, m, row, v, vp);
                     }
                 }
                 __syncthreads();
@@ -431,6 +489,8 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
     for (int m = 0; m < M; ++m) scale[m] = 1.0f;
     if (fz.rms) rms_scales<XVEC, M>(act, M, nb * QK, fz.eps, scale, red_d);
     quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, nb * QK, smem, act_stride, scale);
+    float2* rtab = reinterpret_cast<float2*>(smem + M * act_stride);  // rope epilogue only
+    if (fz.rope) rope_table<M>(fz.rp, rtab);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
@@ -463,11 +523,16 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
     for (int m = 0; m < M; ++m) {
         const float v = row16_sum(acc[m]);
         const float vp = __shfl_xor(v, LPR, 64);
-        if (sub == 0 && row < N) emit(fz, dst, ldd, m, row, v, vp);
+        if (sub == 0 && row < N) emit(fz, rtab, dst, ldd, m, row, v, vp);
     }
 }
 
 constexpr size_t LDS_MAX = 160 * 1024;
+
+// LDS of the rope epilogue's (cos, sin) table
+size_t rope_lds(const GemvFuse& fz, int64_t M) {
+    return fz.rope ? (size_t)M * (fz.rp.n_dims / 2) * sizeof(float2) : 0;
+}
 
 // dynamic LDS above 64 KiB must be allowed per kernel; `allowed` remembers the
 // largest size granted so far (the attribute excludes the kernel's static LDS)
@@ -539,7 +604,7 @@ template <int QT, int M, bool XVEC, int PF>
 int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int G = (int)(K / 256);
-    const size_t lds = (size_t)M * G * ACT_GS + (size_t)WAVES * 64 * QTraits<QT>::GB;
+    const size_t lds = (size_t)M * G * ACT_GS + (size_t)WAVES * 64 * QTraits<QT>::GB + rope_lds(fz, M);
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
     // residency is the same for every KS (same registers and LDS)
     int resident = 0;
@@ -578,7 +643,7 @@ int launch_blk(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int nb = (int)(K / QK);
     const int64_t row_bytes = (int64_t)nb * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
-    const size_t lds = (size_t)M * act_row_bytes(K);
+    const size_t lds = (size_t)M * act_row_bytes(K) + rope_lds(fz, M);
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
     static size_t allowed = 0;
     int rc = allow_big_lds(&k_gemv_blk<QT, M, XVEC>, allowed, lds);

@@ -19,13 +19,39 @@ constexpr int GEMV_MAX_M = 4;
 // bits of the unfused ops): ADD in front of the activation (ActSrc.d), RMS_NORM of
 // the activation rows, SWIGLU over the two halves of the weight rows (output N/2
 // wide), ADD of a residual to the output (may alias dst).
+// ROPE of the q and k rows plus SET_ROWS of k and v, applied to the rows of a fused
+// QKV product ((Hq + 2 Hkv) heads of hd rows): the work of k_rope_kv as an epilogue
+struct GemvRope {
+    const int32_t* pos;  // [M] positions
+    int64_t hd, Hq, Hkv;
+    int n_dims, neox;
+    float theta_scale, freq_scale, attn_factor;
+    float* qo;
+    int64_t qonb1, qonb2;  // bytes per head, per token
+    uint16_t* kc;
+    int64_t kcnb1, kcnb2;  // bytes per cache row, per head
+    uint16_t* vc;
+    int64_t vcnb1, vcnb2;
+    int64_t rows;
+    const int64_t* idx;  // [M] cache rows
+    int32_t* n_bad;
+};
+
+// Fusions of the decode GEMV. Paired epilogues see logical rows 2c, 2c+1 in one
+// wave: with pair_b > 0 (N, or a multiple of 4) logical row r reads physical row
+//   (r / pair_b) * pair_b + (r % pair_b) / 2 + (r & 1) * pair_h
+// (SWIGLU: pair_b = N, pair_h = N/2, gate row c with up row c + N/2; NEOX rope:
+// pair_b = hd, pair_h = hd/2, dims c and c + hd/2 of a head; normal rope pairs
+// adjacent dims: pair_b = 0, the identity).
 struct GemvFuse {
     int rms = 0;
     float eps = 0.0f;
     int glu = 0;
-    int64_t glu_half = 0;
+    int rope = 0;
+    int64_t pair_b = 0, pair_h = 0;
     const float* res = nullptr;
     int64_t ldr = 0;
+    GemvRope rp{};
 };
 int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
          const GemvFuse& fz, hipStream_t s);

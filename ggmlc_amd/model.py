@@ -15,9 +15,10 @@ executor.cpp:2396-2410) -> ARGMAX for greedy decoding. n_kv follows
 pad_kv_len (executor.cpp:58-64): max(256, roundup(pos + s, 256)) capped at max_ctx.
 
 Every op is one libgq call on device tensors. ROPE(q), ROPE(k) and the two
-SET_ROWS run as one launch (gq_rope_kv_store); decode steps (s <= 4) also fuse
-RMS_NORM into the following MUL_MAT, the residual ADD into O / down and SWIGLU into
-gate_up (gq_mul_mat_fused). Both fusions are bit-identical to the separate ops. A whole step
+SET_ROWS run as one launch (gq_rope_kv_store); decode steps (s <= 4) also fuse the
+residual ADD and RMS_NORM into the following MUL_MAT, ROPE + SET_ROWS into the QKV
+projection's epilogue and SWIGLU into gate_up (gq_mul_mat_fused). The fusions are
+bit-identical to the separate ops. A whole step
 (embedding to the argmax of the next token, plus pos += s) can be captured as one
 HIP graph per (s, n_kv) bucket and replayed without host work.
 """
@@ -180,8 +181,9 @@ class Decoder:
         """Run s tokens (ids int32 [s], default: this bucket's ids buffer) at the device
         position; returns the argmax of the last token's logits (device int32 [1]).
 
-        fused (default: s <= 4 without a trace): run RMS_NORM -> MUL_MAT, MUL_MAT -> ADD
-        and MUL_MAT -> SWIGLU as single GEMV launches (gq_mul_mat_fused, bit-identical).
+        fused (default: s <= 4 without a trace): run ADD -> RMS_NORM -> MUL_MAT (-> ROPE
+        + SET_ROWS for QKV, -> SWIGLU for gate_up) as single GEMV launches
+        (gq_mul_mat_fused, bit-identical).
         trace (eager only): receives (name, layer, copy) of every op's output, so a
         checker can recompute each op from the inputs this step actually used."""
         c, b, ws = self.cfg, self._buffers(s), self.ws
@@ -208,30 +210,33 @@ class Decoder:
         other = {id(b["x"]): b["x_alt"], id(b["x_alt"]): b["x"]}
         pending = None  # proj still to be added to x
         for li, L in enumerate(self.w.layers):
-            if fused:
+            if fused:  # ADD + RMS_NORM + QKV + ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
                 nx = other[id(x)] if pending is not None else None
-                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps, x_add=pending, x_sum=nx)
+                ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=ops.RopeKv(
+                    c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"],
+                    b["q"], self.k_cache[li], self.v_cache[li]))
                 x = nx if nx is not None else x
+                q = b["q"]
             else:
                 rec("x_in", li, x)
                 h = ops.rms_norm(x, c.rms_eps, out=b["h"])
                 rec("h1", li, h)
                 qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
-            rec("qkv", li, qkv)
-            # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
-            qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
-            kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
-            vv = qkv[:, qd + kvd:].view(1, s, c.n_head_kv, c.head_dim)
-            if trace is None:  # ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
-                q = ops.rope_kv_store(qv, kv, vv, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"], b["q"],
-                                      self.k_cache[li], self.v_cache[li])
-            else:
-                q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
-                k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
-                # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
-                ops.set_rows(self.k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
-                ops.set_rows(self.v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
-                rec("q", li, q), rec("k", li, k), rec("kc", li, self.k_cache[li]), rec("vc", li, self.v_cache[li])
+                rec("qkv", li, qkv)
+                # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
+                qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
+                kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
+                vv = qkv[:, qd + kvd:].view(1, s, c.n_head_kv, c.head_dim)
+                if trace is None:  # ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
+                    q = ops.rope_kv_store(qv, kv, vv, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"], b["q"],
+                                          self.k_cache[li], self.v_cache[li])
+                else:
+                    q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
+                    k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
+                    # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
+                    ops.set_rows(self.k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
+                    ops.set_rows(self.v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
+                    rec("q", li, q), rec("k", li, k), rec("kc", li, self.k_cache[li]), rec("vc", li, self.v_cache[li])
             ops.flash_attn_ext(q[0].permute(1, 0, 2), self.k_cache[li][0, :, :n_kv], self.v_cache[li][0, :, :n_kv],
                                mask, scale, out=b["attn"], ws=ws)
             rec("attn", li, b["attn"])
@@ -288,12 +293,13 @@ class Decoder:
         return g
 
     def _ws_need(self, s: int) -> int:
-        """Largest workspace any op of an s-token step can ask for (attention's
-        split count grows with n_kv, so it is sized at max_ctx)."""
+        """Largest workspace any op of an s-token step can ask for (attention's split
+        plan depends on n_kv, not monotonically: every bucket size is checked)."""
         c, L = self.cfg, self.w.layers[0]
         need = [ops.mul_mat_workspace_size(wt, s) for wt in (L.qkv, L.o, L.gate_up, L.down)]
         need.append(ops.mul_mat_workspace_size(self.w.lm_head, 1))
-        need.append(ops.flash_attn_workspace_size(c.head_dim, s, c.n_head, c.n_head_kv, self.max_ctx))
+        for n_kv in sorted(set(list(range(256, self.max_ctx + 1, 256)) + [self.max_ctx])):
+            need.append(ops.flash_attn_workspace_size(c.head_dim, s, c.n_head, c.n_head_kv, n_kv))
         return max(need)
 
     def decode_buffers(self) -> tuple[torch.Tensor, torch.Tensor]:

@@ -145,19 +145,51 @@ def mul_mat(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None,
     return out
 
 
+@dataclass
+class RopeKv:
+    """The rope + KV-store epilogue of :func:`mul_mat_fused` (the arguments of
+    :func:`rope_kv_store`, with q/k/v being the rows of the fused QKV product)."""
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    pos: torch.Tensor
+    n_dims: int
+    mode: int
+    freq_base: float
+    kv_idx: torch.Tensor
+    q_out: torch.Tensor
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    freq_scale: float = 1.0
+    attn_factor: float = 1.0
+    n_bad: torch.Tensor | None = None
+
+
 def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
                   swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
-                  x_sum: torch.Tensor | None = None) -> torch.Tensor:
+                  x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None) -> torch.Tensor | None:
     """Decode MUL_MAT (x has at most 4 rows) fused with its graph neighbours, bit-identical
     to the unfused ops: x_add -> x + x_add first (stored to x_sum when given); rms_eps ->
     RMS_NORM; swiglu -> SWIGLU of the result's two halves (out [..., N/2]); add -> add +
-    result (add may be out)."""
+    result (add may be out); rope_kv -> the result's q/k/v rows go through
+    :func:`rope_kv_store` instead of being written (returns None)."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
     n_out = w.N // 2 if swiglu else w.N
-    if out is None:
+    if out is None and rope_kv is None:
         out = torch.empty(x.shape[:-1] + (n_out,), dtype=torch.float32, device=x.device)
     f = _lib.gq_mul_mat_fusion()
+    keep = []  # descriptors the fusion struct points at
+    if rope_kv is not None:
+        r = rope_kv
+        descs = [_desc(t) for t in (r.pos, r.kv_idx, r.q_out, r.k_cache, r.v_cache)]
+        keep += descs
+        e = _lib.gq_rope_kv_epilogue(r.n_head, r.n_head_kv, r.head_dim, ctypes.pointer(descs[0]), r.n_dims, r.mode,
+                                     r.freq_base, r.freq_scale, r.attn_factor, ctypes.pointer(descs[1]),
+                                     ctypes.pointer(descs[2]), ctypes.pointer(descs[3]), ctypes.pointer(descs[4]),
+                                     r.n_bad.data_ptr() if r.n_bad is not None else None)
+        keep.append(e)
+        f.rope_kv = ctypes.pointer(e)
     if rms_eps is not None:
         f.rms_norm, f.rms_eps = 1, float(rms_eps)
     f.swiglu = 1 if swiglu else 0
@@ -170,7 +202,9 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     xs = _desc(x_sum) if x_sum is not None else None
     if xs is not None:
         f.b_sum = ctypes.pointer(xs)
-    check(_lib.load().gq_mul_mat_fused(w.desc(), _desc(x), _desc(out), ctypes.byref(f), _stream()))
+    od = _desc(out) if out is not None else None
+    check(_lib.load().gq_mul_mat_fused(w.desc(), _desc(x), od, ctypes.byref(f), _stream()))
+    del keep
     return out
 
 

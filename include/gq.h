@@ -112,10 +112,29 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  *   swiglu:   dst = SWIGLU(MUL_MAT(a, b)) over the two halves of a's rows
  *             (gq_swiglu of the [N, M] result): dst ne0 = N / 2
  *   add:      dst = add + MUL_MAT(a, b) (gq_add); add may be dst itself
- * (swiglu excludes add.) Only the GEMV path (M <= 4 activation rows) is fused;
- * larger M returns GQ_ERR_UNSUPPORTED and the caller runs the ops unfused. No
+ *   rope_kv:  the rows of MUL_MAT(a, b) are a fused QKV projection,
+ *             (n_head + 2 n_head_kv) heads of head_dim rows (q heads, k heads, v
+ *             heads), and go through gq_rope_kv_store with the epilogue's
+ *             arguments instead of being written: q rotated into q_out, k rotated
+ *             and v copied into the caches at rows kv_idx (fp16). dst must be NULL.
+ *             Modes 0 and 2; mode 2 needs n_dims == head_dim; head_dim % 4 == 0.
+ * (swiglu, add and rope_kv exclude each other.) Only the GEMV path (M <= 4
+ * activation rows) is fused; larger M, and rope_kv shapes outside the conditions
+ * above, return GQ_ERR_UNSUPPORTED and the caller runs the ops unfused. No
  * workspace. The ggml CUDA backend fuses the same neighbours (ADD+RMS_NORM+MUL,
- * MUL_MAT+GLU, MUL_MAT+ADD) for the same reason: decode steps are launch-bound. */
+ * MUL_MAT+GLU, MUL_MAT+ADD, ROPE+SET_ROWS) for the same reason: decode steps are
+ * launch-bound. */
+typedef struct gq_rope_kv_epilogue {
+    int32_t n_head, n_head_kv, head_dim;
+    const gq_tensor* pos;   /* I32 [>= M] */
+    int32_t n_dims, mode;
+    float freq_base, freq_scale, attn_factor;
+    const gq_tensor* kv_idx; /* I64 [M] */
+    gq_tensor* q_out;        /* F32 [head_dim, n_head, M, 1] */
+    gq_tensor* k_cache;      /* F16 [head_dim, rows, n_head_kv, 1] */
+    gq_tensor* v_cache;
+    int32_t* n_bad;          /* device int32 or NULL */
+} gq_rope_kv_epilogue;
 typedef struct gq_mul_mat_fusion {
     int32_t rms_norm;
     float rms_eps;
@@ -123,6 +142,7 @@ typedef struct gq_mul_mat_fusion {
     const gq_tensor* add;
     const gq_tensor* b_add;
     gq_tensor* b_sum;
+    const gq_rope_kv_epilogue* rope_kv;
 } gq_mul_mat_fusion;
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                      gq_stream_t stream);

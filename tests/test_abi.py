@@ -123,3 +123,37 @@ def test_mul_mat_fused_pre_add_validation(lib):
     bad = _lib.make_tensor(0x3000, _lib.F32, [2048, 1], [4, 8192])
     h = _lib.gq_mul_mat_fusion(0, 0.0, 0, None, ctypes.pointer(bad), None)
     assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(h), None) == -1  # b_add shaped like b
+
+
+def test_mul_mat_fused_rope_kv_validation(lib):
+    """The rope + KV-store epilogue: dst must be NULL, the product rows must be the
+    q/k/v heads, NEOX needs n_dims == head_dim (else the caller runs it unfused)."""
+    Hq, Hkv, hd, M = 4, 2, 64, 1
+    N = (Hq + 2 * Hkv) * hd
+    w = _t(_lib.Q8_0, [256, N], [34, 272])
+    x = _t(_lib.F32, [256, M], [4, 1024])
+    pos = _lib.make_tensor(0x1000, _lib.I32, [M], [4])
+    idx = _lib.make_tensor(0x2000, _lib.I64, [M], [8])
+    qo = _lib.make_tensor(0x3000, _lib.F32, [hd, Hq, M, 1], [4, 4 * hd, 4 * hd * Hq, 4 * hd * Hq * M])
+    kc = _lib.make_tensor(0x4000, _lib.F16, [hd, 32, Hkv, 1], [2, 2 * hd, 64 * hd, 128 * hd])
+    vc = _lib.make_tensor(0x5000, _lib.F16, [hd, 32, Hkv, 1], [2, 2 * hd, 64 * hd, 128 * hd])
+
+    def epi(**kw):
+        a = dict(n_head=Hq, n_head_kv=Hkv, head_dim=hd, n_dims=hd, mode=2)
+        a.update(kw)
+        return _lib.gq_rope_kv_epilogue(a["n_head"], a["n_head_kv"], a["head_dim"], ctypes.pointer(pos), a["n_dims"],
+                                        a["mode"], 10000.0, 1.0, 1.0, ctypes.pointer(idx), ctypes.pointer(qo),
+                                        ctypes.pointer(kc), ctypes.pointer(vc), None)
+
+    def call(e, dst=None, swiglu=0):
+        f = _lib.gq_mul_mat_fusion(1, 1e-5, swiglu, None, None, None, ctypes.pointer(e))
+        return lib.gq_mul_mat_fused(w, x, dst, ctypes.byref(f), None)
+
+    d = _t(_lib.F32, [N, M], [4, 4 * N])
+    assert call(epi(), dst=d) == -1 and b"NULL" in lib.gq_last_error()
+    assert call(epi(), swiglu=1) == -1 and b"exclusive" in lib.gq_last_error()
+    assert call(epi(n_head_kv=3)) == -1  # rows are not (Hq + 2 Hkv) * hd
+    assert call(epi(n_dims=32)) == -2    # NEOX with partial rotation: unfused
+    assert call(epi(mode=1)) == -2
+    f = _lib.gq_mul_mat_fusion(0, 0.0, 0, None, None, None, None)
+    assert lib.gq_mul_mat_fused(w, x, None, ctypes.byref(f), None) == -1  # no epilogue: dst required

@@ -194,6 +194,51 @@ def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add, p
         assert torch.equal(x_sum, x_sum_want)
 
 
+@pytest.mark.parametrize("qtype,K,Hq,Hkv,hd,M,mode,n_dims", [
+    (O.Q4_0, 4096, 32, 32, 128, 1, 2, 128),   # 7B QKV (MHA)
+    (O.Q8_0, 1536, 12, 2, 128, 3, 2, 128),    # Qwen2.5-1.5B QKV (GQA 6), three tokens
+    (O.Q8_0, 960, 15, 5, 64, 2, 2, 64),       # SmolLM2 QKV: K = 960, block-wise kernel
+    (O.Q4_0, 1024, 4, 2, 128, 4, 0, 96),      # normal rope, partial n_dims, four tokens
+])
+def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_dims):
+    """The QKV GEMV with the rope + KV-store epilogue gives exactly the bits of
+    RMS_NORM -> MUL_MAT -> gq_rope_kv_store (pinned by the decoder-op tests): q_out,
+    both caches (untouched rows included) and the count of out-of-range rows."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + Hq + M)
+    N = (Hq + 2 * Hkv) * hd
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV) * 3.0
+    d = torch.randn((M, K), generator=g, device=DEV)
+    pos = torch.arange(700, 700 + M, dtype=torch.int32, device=DEV)
+    idx = torch.tensor([5, 63, -1, 64][:M], dtype=torch.int64, device=DEV)
+    kc1 = torch.randn((1, Hkv, 64, hd), generator=g, device=DEV).half()
+    vc1 = torch.randn((1, Hkv, 64, hd), generator=g, device=DEV).half()
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    bad1 = torch.zeros(1, dtype=torch.int32, device=DEV)
+    bad2 = torch.zeros(1, dtype=torch.int32, device=DEV)
+    eps = 1e-5
+    # unfused: ADD, RMS_NORM, MUL_MAT, then the rope/set_rows node
+    y = ops.mul_mat(w, ops.rms_norm(ops.add(x, d), eps))
+    qv = y[:, :Hq * hd].view(1, M, Hq, hd)
+    kv = y[:, Hq * hd:(Hq + Hkv) * hd].view(1, M, Hkv, hd)
+    vv = y[:, (Hq + Hkv) * hd:].view(1, M, Hkv, hd)
+    q1 = torch.empty((1, M, Hq, hd), device=DEV)
+    ops.rope_kv_store(qv, kv, vv, pos, n_dims, mode, 10000.0, idx, q1, kc1, vc1, n_bad=bad1)
+    # fused
+    q2 = torch.full_like(q1, float("nan"))
+    x_sum = torch.empty_like(x)
+    ret = ops.mul_mat_fused(w, x, rms_eps=eps, x_add=d, x_sum=x_sum, rope_kv=ops.RopeKv(
+        Hq, Hkv, hd, pos, n_dims, mode, 10000.0, idx, q2, kc2, vc2, n_bad=bad2))
+    torch.cuda.synchronize()
+    assert ret is None
+    assert torch.equal(q1, q2), (q1 - q2).abs().max().item()
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    n_bad_rows = int(((idx < 0) | (idx >= 64)).sum())
+    assert int(bad1.item()) == int(bad2.item()) == 2 * Hkv * n_bad_rows
+
+
 # --------------------------------------------------------------- set_rows ---
 
 def test_set_rows_golden(golden_dir):
@@ -304,6 +349,51 @@ def test_flash_attn_banded_mask_prefill(D, G, masked):
     r = mar(got, exact)
     print(f"D={D} G={G} masked={masked:#x}: vs exact {r:.2e}")
     assert r < 1e-3
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
+    (32, 32, 128, 1, 1100, 2048),   # 7B decode: 10 splits per kv head
+    (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, many splits
+])
+def test_flash_attn_decode_workspace_and_replays(Hq, Hkv, D, S, pos, ctx):
+    """Split decode (partials in the workspace, then the merge) needs no clean
+    workspace: a workspace full of random bytes gives the same bits, and a captured
+    graph of three calls sharing one workspace replays to the eager bits every time,
+    with eager calls between the replays."""
+    rng = np.random.default_rng(Hq + S)
+    n_kv = O.pad_kv_len(pos + S, ctx)
+    kc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
+    vc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
+    mask = to_dev(O.causal_mask_f16(pos, S, n_kv)).view(torch.float16)
+    qs = [to_dev(rng.standard_normal((Hq, S, D)).astype(np.float32)) for _ in range(3)]
+    need = ops.flash_attn_workspace_size(D, S, Hq, Hkv, n_kv)
+    assert need > 0
+    ws = ops.Workspace(torch.device(DEV))
+    ws.get(need)
+    ws.buf.zero_()
+    scale = 1.0 / np.sqrt(D)
+    clean = [ops.flash_attn_ext(q, kc, vc, mask, scale, ws=ws).clone() for q in qs]
+    exact = O.flash_attn_ext_f16(qs[0].cpu().numpy(), kc.view(torch.int16).cpu().numpy().view(np.uint16),
+                                 vc.view(torch.int16).cpu().numpy().view(np.uint16), n_kv,
+                                 mask.view(torch.int16).cpu().numpy().view(np.uint16), mode=1)
+    assert mar(clean[0].cpu().numpy(), exact) < 1e-3
+    ws.buf.copy_(torch.randint(0, 256, ws.buf.shape, dtype=torch.uint8, device=DEV))
+    dirty = ops.flash_attn_ext(qs[0], kc, vc, mask, scale, ws=ws)
+    assert torch.equal(dirty, clean[0])
+    outs = [torch.empty_like(c) for c in clean]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for q, o in zip(qs, outs):
+            ops.flash_attn_ext(q, kc, vc, mask, scale, out=o, ws=ws)
+    for r in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for o, c in zip(outs, clean):
+            assert torch.equal(o, c), r
+        again = ops.flash_attn_ext(qs[1], kc, vc, mask, scale, ws=ws)  # eager call between replays
+        assert torch.equal(again, clean[1])
 
 
 def test_flash_attn_padding_and_gqa_invariants():
