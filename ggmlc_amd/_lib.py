@@ -51,6 +51,7 @@ class gq_rope_kv_epilogue(ctypes.Structure):
         ("k_cache", ctypes.POINTER(gq_tensor)),
         ("v_cache", ctypes.POINTER(gq_tensor)),
         ("n_bad", ctypes.c_void_p),
+        ("rope_cache", ctypes.POINTER(gq_tensor)),
     ]
 
 
@@ -81,6 +82,7 @@ SIGNATURES = {
     "gq_mul_mat_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_mul_mat": (ctypes.c_int, [_P, _P, _P, _vp, ctypes.c_size_t, _vp]),
     "gq_mul_mat_fused": (ctypes.c_int, [_P, _P, _P, ctypes.POINTER(gq_mul_mat_fusion), _vp]),
+    "gq_rope_cache": (ctypes.c_int, [_P, ctypes.c_int, _f32, _f32, _f32, _P, _vp]),
     "gq_set_rows": (ctypes.c_int, [_P, _P, _P, _vp, _vp]),
     "gq_flash_attn_ext_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_flash_attn_ext": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp, ctypes.c_size_t, _vp]),

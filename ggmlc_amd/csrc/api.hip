@@ -189,11 +189,22 @@ static int rope_kv_epilogue(const gq_rope_kv_epilogue& e, const MulMatPlan& p, c
         return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv pos must be I32 [>= M], kv_idx I64 [M]");
     if (e.mode != 0 && e.mode != 2) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: rope_kv modes 0 and 2 only");
     if (e.n_dims <= 0 || e.n_dims % 2 || e.n_dims > hd) return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_kv bad n_dims");
-    if (hd % 4 || (e.mode == 2 && e.n_dims != hd))
-        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: rope_kv needs head_dim % 4 == 0 and (mode 2) n_dims == head_dim");
+    if (hd < 4 || (hd & (hd - 1)) || (e.mode == 2 && e.n_dims != hd))
+        return fail(GQ_ERR_UNSUPPORTED,
+                    "mul_mat_fused: rope_kv needs a power-of-two head_dim >= 4 and (mode 2) n_dims == head_dim");
     GemvRope& r = fz.rp;
     r.pos = static_cast<const int32_t*>(e.pos->data);
+    r.cache = nullptr;
+    r.cache_nb1 = 0;
+    if (const gq_tensor* c = e.rope_cache) {
+        if (c->type != GQ_TYPE_F32 || c->nb[0] != 4 || c->ne[0] != e.n_dims || c->ne[1] < S || c->nb[1] % 8)
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: rope_cache must be F32 [n_dims, >= M]: " + shape(c));
+        r.cache = static_cast<const float*>(c->data);
+        r.cache_nb1 = (int64_t)c->nb[1];
+    }
     r.hd = hd, r.Hq = Hq, r.Hkv = Hkv;
+    r.hd_log2 = 0;
+    while ((int64_t)1 << r.hd_log2 < hd) ++r.hd_log2;
     r.n_dims = e.n_dims, r.neox = e.mode == 2;
     r.theta_scale = powf(e.freq_base, -2.0f / e.n_dims);
     r.freq_scale = e.freq_scale, r.attn_factor = e.attn_factor;
@@ -204,7 +215,7 @@ static int rope_kv_epilogue(const gq_rope_kv_epilogue& e, const MulMatPlan& p, c
     r.idx = static_cast<const int64_t*>(e.kv_idx->data);
     r.n_bad = e.n_bad;
     fz.rope = 1;
-    fz.pair_b = r.neox ? hd : 0;
+    fz.pair_lo = r.neox ? hd - 1 : 0;
     fz.pair_h = r.neox ? hd / 2 : 0;
     return GQ_OK;
 }
@@ -240,7 +251,7 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     }
     if (f->swiglu) {
         fz.glu = 1;
-        fz.pair_b = p.N;
+        fz.pair_lo = ~(int64_t)0;
         fz.pair_h = p.N / 2;
     }
     if (f->add) {
@@ -505,6 +516,19 @@ int gq_rope_kv_store(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v,
     a.n_dims = n_dims, a.neox = mode == 2;
     a.freq_scale = freq_scale, a.attn_factor = attn_factor;
     return rope_kv(a, freq_base, (hipStream_t)stream);
+}
+
+int gq_rope_cache(const gq_tensor* pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
+                  gq_tensor* dst, gq_stream_t stream) {
+    if (!pos || !dst) return fail(GQ_ERR_INVALID, "rope_cache: null tensor");
+    if (pos->type != GQ_TYPE_I32 || pos->nb[0] != 4 || pos->ne[1] != 1 || pos->ne[2] != 1 || pos->ne[3] != 1)
+        return fail(GQ_ERR_INVALID, "rope_cache: pos must be I32 [n]");
+    if (n_dims <= 0 || n_dims % 2) return fail(GQ_ERR_INVALID, "rope_cache: bad n_dims");
+    if (dst->type != GQ_TYPE_F32 || dst->nb[0] != 4 || dst->ne[0] != n_dims || dst->ne[1] != pos->ne[0] ||
+        dst->ne[2] != 1 || dst->ne[3] != 1 || dst->nb[1] % 8)
+        return fail(GQ_ERR_INVALID, "rope_cache: dst must be F32 [n_dims, n]: " + shape(dst));
+    return rope_cache(static_cast<const int32_t*>(pos->data), pos->ne[0], n_dims, freq_base, freq_scale, attn_factor,
+                      static_cast<float*>(dst->data), (int64_t)dst->nb[1], (hipStream_t)stream);
 }
 
 int gq_add(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream) {

@@ -52,6 +52,22 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, i
 // ---- ROPE (ops.cpp:5886-6120, ext_factor = 0): theta_i = p * theta_scale^i built by
 // repeated multiplication like ggml_rope_cache_init; NEOX pairs (i, i + n_dims/2),
 // NORMAL pairs (2i, 2i+1); dims >= n_dims are copied.
+// ---- ROPE cache: (cos, sin) * attn_factor of every rotated pair j < n_dims/2 at each
+// position, the table ggml_rope_cache_init fills per position (ops.cpp:5910)
+__global__ __launch_bounds__(64) void k_rope_cache(const int32_t* __restrict__ pos, int np, float theta_scale,
+                                                   float freq_scale, float attn_factor, float* __restrict__ y,
+                                                   int64_t ynb1) {
+    const int64_t i = blockIdx.x;
+    float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + i * ynb1);
+    const float p = (float)pos[i];
+    for (int j = threadIdx.x; j < np; j += blockDim.x) {
+        float c, sn;
+        rope_cs(p, j, theta_scale, freq_scale, attn_factor, c, sn);
+        yr[2 * j] = c;
+        yr[2 * j + 1] = sn;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, int64_t ne0, int64_t ne1, int64_t ne2,
                                               int64_t xnb1, int64_t xnb2, int64_t xnb3, const int32_t* __restrict__ pos,
                                               float* __restrict__ y, int64_t ynb1, int64_t ynb2, int64_t ynb3,
@@ -248,6 +264,15 @@ int rope(const float* x, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int
     hipLaunchKernelGGL(k_rope, dim3((unsigned)rows), dim3(64), 0, s, x, ne0, ne1, ne2, xnb1, xnb2, xnb3, pos, y, ynb1,
                        ynb2, ynb3, n_dims, neox, freq_scale, attn_factor, theta_scale, rows);
     return check_hip(hipGetLastError(), "rope launch");
+}
+
+int rope_cache(const int32_t* pos, int64_t n, int n_dims, float freq_base, float freq_scale, float attn_factor,
+               float* y, int64_t ynb1, hipStream_t s) {
+    if (n == 0) return GQ_OK;
+    const float theta_scale = powf(freq_base, -2.0f / n_dims);
+    hipLaunchKernelGGL(k_rope_cache, dim3((unsigned)n), dim3(64), 0, s, pos, n_dims / 2, theta_scale, freq_scale,
+                       attn_factor, y, ynb1);
+    return check_hip(hipGetLastError(), "rope_cache launch");
 }
 
 int rope_kv(const RopeKvArgs& a, float freq_base, hipStream_t s) {

@@ -126,9 +126,8 @@ __device__ __forceinline__ float row16_sum(float v) {
 // rows of a pair in one wave (rows of a wave are 4 consecutive logical rows), so
 // logical rows 2c, 2c+1 of a pair block read the physical rows of the pair.
 __device__ __forceinline__ int64_t phys_row(const GemvFuse& fz, int64_t r) {
-    if (fz.pair_b == 0) return r;
-    const int64_t b0 = (r / fz.pair_b) * fz.pair_b;
-    return b0 + ((r - b0) >> 1) + (r & 1) * fz.pair_h;
+    if (fz.pair_lo == 0) return r;
+    return (r & ~fz.pair_lo) + ((r & fz.pair_lo) >> 1) + (r & 1) * fz.pair_h;
 }
 
 // silu(g) * u with the arithmetic of k_swiglu (x / (1 + expf(-x)) * g)
@@ -137,16 +136,76 @@ __device__ __forceinline__ float swiglu1(float g, float u) {
     return sg * u;
 }
 
-// (cos, sin) of every rotated pair of the M positions, computed once per workgroup
-// into LDS (tab[m * n_dims/2 + j]) while the first weight loads are in flight
+// (cos, sin) of every rotated pair of the M positions (tab[m * n_dims/2 + j]) and
+// the M cache rows (after the pairs), computed once per workgroup into LDS while
+// the first weight loads are in flight
+// With a rope cache (the (cos, sin) table of the M positions, gq_rope_cache) each
+// thread holds at most RC of its entries; larger tables are computed here.
+constexpr int RC = 2;
 template <int M>
-__device__ __forceinline__ void rope_table(const GemvRope& r, float2* tab) {
+struct RopeIn {
+    int32_t pos[M];
+    int64_t row[M];
+    float2 cs[RC];
+};
+__device__ __forceinline__ bool rope_cached(const GemvFuse& fz, int M) {
+    return fz.rope && fz.rp.cache && M * (fz.rp.n_dims >> 1) <= RC * 256;
+}
+// the cached (cos, sin) entries of this thread: raw buffer loads issued whether or not
+// the launch uses them (an empty resource returns 0 without a fetch), so the vector
+// memory counter stays exact for the weight loads issued after them
+template <int M>
+__device__ __forceinline__ void rope_cache_loads(const GemvFuse& fz, RopeIn<M>& in) {
+    const bool use = rope_cached(fz, M);
+    const int np = fz.rp.n_dims >> 1;
+    const uint64_t base = reinterpret_cast<uint64_t>(fz.rp.cache);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    const uint32_t n = use ? (uint32_t)(M * fz.rp.cache_nb1) : 0u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)__builtin_amdgcn_readfirstlane(n),
+        0x00020000);
+#pragma unroll
+    for (int k = 0; k < RC; ++k) {
+        const int idx = (int)threadIdx.x + k * 256;
+        const int m = use ? idx / np : 0, j = idx - m * np;
+        const uint32_t off = use && idx < M * np ? (uint32_t)(m * fz.rp.cache_nb1 + j * 8) : 0x80000000u;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)off, 0, 0);
+        in.cs[k] = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+    }
+}
+// the positions and cache rows (wave-uniform loads), read first thing
+template <int M>
+__device__ __forceinline__ void rope_inputs(const GemvRope& r, RopeIn<M>& in) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) in.pos[m] = r.pos[m], in.row[m] = r.idx[m];
+}
+// (cos, sin) of every rotated pair of the M positions (tab[m * n_dims/2 + j]) and the
+// M cache rows (after the pairs) into LDS
+template <int M>
+__device__ __forceinline__ void rope_table(const GemvFuse& fz, const RopeIn<M>& in, float2* tab) {
+    const GemvRope& r = fz.rp;
     const int np = r.n_dims >> 1;
-    for (int idx = threadIdx.x; idx < M * np; idx += blockDim.x) {
-        const int m = idx / np, j = idx - m * np;
-        float c, s;
-        rope_cs((float)r.pos[m], j, r.theta_scale, r.freq_scale, r.attn_factor, c, s);
-        tab[idx] = make_float2(c, s);
+    if (rope_cached(fz, M)) {
+#pragma unroll
+        for (int k = 0; k < RC; ++k) {
+            const int idx = (int)threadIdx.x + k * (int)blockDim.x;
+            if (idx < M * np) tab[idx] = in.cs[k];
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < M * np; idx += blockDim.x) {
+            const int m = idx / np, j = idx - m * np;
+            int32_t p = in.pos[0];
+#pragma unroll
+            for (int mm = 1; mm < M; ++mm) p = m == mm ? in.pos[mm] : p;
+            float c, s;
+            rope_cs((float)p, j, r.theta_scale, r.freq_scale, r.attn_factor, c, s);
+            tab[idx] = make_float2(c, s);
+        }
+    }
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) reinterpret_cast<int64_t*>(tab + M * np)[m] = in.row[m];
     }
 }
 
@@ -154,10 +213,11 @@ __device__ __forceinline__ void rope_table(const GemvRope& r, float2* tab) {
 // the pair's two dims i0, i1 of head `head`): the work of k_rope_kv for those dims
 // with the same arithmetic (q rotated into qo; k rotated, v copied, both rounded
 // to fp16 into cache row idx[m]; bad rows counted once per token and kv head).
+template <int M>
 __device__ __forceinline__ void rope_emit(const GemvRope& r, const float2* tab, int m, int64_t row, float v0,
                                           float v1) {
-    const int64_t head = row / r.hd;
-    const int c = (int)((row - head * r.hd) >> 1);
+    const int64_t head = row >> r.hd_log2;
+    const int c = (int)((row & (r.hd - 1)) >> 1);
     const int i0 = r.neox ? c : 2 * c;
     const int i1 = r.neox ? c + (int)(r.hd >> 1) : 2 * c + 1;
     float y0 = v0, y1 = v1;
@@ -171,7 +231,7 @@ __device__ __forceinline__ void rope_emit(const GemvRope& r, const float2* tab, 
         q[i1] = y1;
         return;
     }
-    const int64_t kv = r.idx[m];
+    const int64_t kv = reinterpret_cast<const int64_t*>(tab + M * (r.n_dims >> 1))[m];
     if (kv < 0 || kv >= r.rows) {
         if (c == 0 && r.n_bad) atomicAdd(r.n_bad, 1);
         return;
@@ -188,6 +248,7 @@ __device__ __forceinline__ void rope_emit(const GemvRope& r, const float2* tab, 
 // Write logical row `row` of activation m: plain, residual-added (res + v: the
 // operand order of ADD(x, MUL_MAT)), or, for the paired epilogues (SWIGLU, rope),
 // from the even row with its partner's value vp.
+template <int M>
 __device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, float* dst, int64_t ldd, int m,
                                      int64_t row, float v, float vp) {
     if (fz.glu) {
@@ -195,7 +256,7 @@ __device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, flo
         return;
     }
     if (fz.rope) {
-        if ((row & 1) == 0) rope_emit(fz.rp, rtab, m, row, v, vp);
+        if ((row & 1) == 0) rope_emit<M>(fz.rp, rtab, m, row, v, vp);
         return;
     }
     if (fz.res) v = fz.res[(int64_t)m * fz.ldr + row] + v;
@@ -250,6 +311,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
 
     // activation loads first, then the weight prefetch: the activation can then be
     // waited for while the weight loads stay in flight (vector loads complete in order)
+    RopeIn<M> rin{};
+    rope_cache_loads<M>(fz, rin);
+    if (fz.rope) rope_inputs<M>(fz.rp, rin);
     float xr[XPMAX][8], ar[XAMAX][8];
     const bool xpre = M * XP <= XPMAX && (!act.d || M * XP <= XAMAX);
     if (xpre) {
@@ -272,14 +336,14 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     // past the end of the wave's sequence never touch memory.
     // Chunk c of a lane is byte 16 * within of slice row r (r, within from lane + 64 c);
     // with paired rows (phys_row) slice rows 2i, 2i+1 are physical rows i and i + pair_h
-    // past the slice's first physical row (a slice never straddles a pair block: pair_b
-    // is N or a multiple of 4).
+    // past the slice's first physical row (a slice never straddles a pair block: blocks
+    // are the whole matrix or a multiple of 4 rows).
     const int64_t mat_bytes = N * row_bytes;
     uint32_t voff[CPG];
 #pragma unroll
     for (int c = 0; c < CPG; ++c) {
         const int ci = lane + 64 * c, r = ci / SEG, within = ci - r * SEG;
-        const int64_t roff = fz.pair_b ? (int64_t)(r >> 1) + (r & 1) * fz.pair_h : (int64_t)r;
+        const int64_t roff = fz.pair_lo ? (int64_t)(r >> 1) + (r & 1) * fz.pair_h : (int64_t)r;
         voff[c] = (uint32_t)(roff * row_bytes + within * 16);
     }
     const int ngr_tail = g_end - g_begin - (S - 1) * LPR;  // groups of the last step of a tile
@@ -288,7 +352,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     int lk = 0, lj = 0;
     auto issue = [&](uint4(&buf)[CPG]) {
         const int64_t row0 = ((int64_t)blockIdx.x + (int64_t)lk * gridDim.x) * ROWS + rg * RPW;
-        const int64_t prow = fz.pair_b ? phys_row(fz, row0) : row0;
+        const int64_t prow = phys_row(fz, row0);
         const int gfirst = g_begin + lj * LPR;
         const int64_t off0 = prow * row_bytes + (int64_t)gfirst * GB;
         const int64_t left = lk < my_wgt ? mat_bytes - off0 : 0;
@@ -316,6 +380,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
 #pragma unroll
     for (int s = 0; s < PF; ++s) issue(pre[s]);
     __builtin_amdgcn_sched_barrier(0);
+    if (fz.rope) rope_table<M>(fz, rin, rtab);  // while the loads are in flight
 
     float scale[M];
 #pragma unroll
@@ -373,7 +438,6 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         if (fz.rms) rms_scales<XVEC, M>(act, M, G * 256, fz.eps, scale, red_d);
         quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, G * 256, s_act, act_bytes, scale);
     }
-    if (fz.rope) rope_table<M>(fz.rp, rtab);
     __syncthreads();  // quantized activation (and rope table) visible to all waves
 
     float acc[M];
@@ -437,7 +501,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                 if constexpr (KS == 1) {
                     float vp = 0.0f;
                     if (fz.glu | fz.rope) vp = __shfl_xor(v, LPR, 64);  // the next row's value (pairs)
-                    if (gsub == 0 && row < N) emit(fz, rtab, dst, ldd, m, row, v, vp);
+                    if (gsub == 0 && row < N) emit<M>(fz, rtab, dst, ldd, m, row, v, vp);
                 } else {
                     if (gsub == 0) red[wave][m][rsub] = v;
                 }
@@ -450,7 +514,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
                         float v = red[wave][m][rsub], vp = red[wave][m][rsub ^ 1];
 #pragma unroll
                         for (int k = 1; k < KS; ++k) v += red[wave + k][m][rsub], vp += red[wave + k][m][rsub ^ 1];
-                        emit(fz, rtab, dst, ldd, m, row, v, vp);
+                        emit<M>(fz, rtab, dst, ldd, m, row, v, vp);
                     }
                 }
                 __syncthreads();
@@ -490,7 +554,12 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
     if (fz.rms) rms_scales<XVEC, M>(act, M, nb * QK, fz.eps, scale, red_d);
     quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, nb * QK, smem, act_stride, scale);
     float2* rtab = reinterpret_cast<float2*>(smem + M * act_stride);  // rope epilogue only
-    if (fz.rope) rope_table<M>(fz.rp, rtab);
+    if (fz.rope) {
+        RopeIn<M> rin{};
+        rope_cache_loads<M>(fz, rin);
+        rope_inputs<M>(fz.rp, rin);
+        rope_table<M>(fz, rin, rtab);
+    }
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
@@ -523,7 +592,7 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
     for (int m = 0; m < M; ++m) {
         const float v = row16_sum(acc[m]);
         const float vp = __shfl_xor(v, LPR, 64);
-        if (sub == 0 && row < N) emit(fz, rtab, dst, ldd, m, row, v, vp);
+        if (sub == 0 && row < N) emit<M>(fz, rtab, dst, ldd, m, row, v, vp);
     }
 }
 
@@ -531,7 +600,7 @@ constexpr size_t LDS_MAX = 160 * 1024;
 
 // LDS of the rope epilogue's (cos, sin) table
 size_t rope_lds(const GemvFuse& fz, int64_t M) {
-    return fz.rope ? (size_t)M * (fz.rp.n_dims / 2) * sizeof(float2) : 0;
+    return fz.rope ? (size_t)M * (fz.rp.n_dims / 2) * sizeof(float2) + (size_t)M * sizeof(int64_t) : 0;
 }
 
 // dynamic LDS above 64 KiB must be allowed per kernel; `allowed` remembers the

@@ -22,8 +22,11 @@ constexpr int GEMV_MAX_M = 4;
 // ROPE of the q and k rows plus SET_ROWS of k and v, applied to the rows of a fused
 // QKV product ((Hq + 2 Hkv) heads of hd rows): the work of k_rope_kv as an epilogue
 struct GemvRope {
-    const int32_t* pos;  // [M] positions
+    const int32_t* pos;   // [M] positions
+    const float* cache;   // [M][n_dims/2][2] (cos, sin) of the positions, or null: computed here
+    int64_t cache_nb1;    // bytes per position
     int64_t hd, Hq, Hkv;
+    int hd_log2;          // hd is a power of two
     int n_dims, neox;
     float theta_scale, freq_scale, attn_factor;
     float* qo;
@@ -38,17 +41,18 @@ struct GemvRope {
 };
 
 // Fusions of the decode GEMV. Paired epilogues see logical rows 2c, 2c+1 in one
-// wave: with pair_b > 0 (N, or a multiple of 4) logical row r reads physical row
-//   (r / pair_b) * pair_b + (r % pair_b) / 2 + (r & 1) * pair_h
-// (SWIGLU: pair_b = N, pair_h = N/2, gate row c with up row c + N/2; NEOX rope:
-// pair_b = hd, pair_h = hd/2, dims c and c + hd/2 of a head; normal rope pairs
-// adjacent dims: pair_b = 0, the identity).
+// wave: with pair_lo != 0 (a block of pair_lo + 1 rows, a power of two >= 4, or
+// all ones for one block) logical row r reads physical row
+//   (r & ~pair_lo) + ((r & pair_lo) >> 1) + (r & 1) * pair_h
+// (SWIGLU: pair_lo = ~0, pair_h = N/2, gate row c with up row c + N/2; NEOX rope:
+// pair_lo = hd - 1, pair_h = hd/2, dims c and c + hd/2 of a head; normal rope
+// pairs adjacent dims: pair_lo = 0, the identity).
 struct GemvFuse {
     int rms = 0;
     float eps = 0.0f;
     int glu = 0;
     int rope = 0;
-    int64_t pair_b = 0, pair_h = 0;
+    int64_t pair_lo = 0, pair_h = 0;
     const float* res = nullptr;
     int64_t ldr = 0;
     GemvRope rp{};
@@ -134,6 +138,8 @@ struct RopeKvArgs {
     float theta_scale, freq_scale, attn_factor;
 };
 int rope_kv(const RopeKvArgs& a, float freq_base, hipStream_t s);
+int rope_cache(const int32_t* pos, int64_t n, int n_dims, float freq_base, float freq_scale, float attn_factor,
+               float* y, int64_t ynb1, hipStream_t s);
 int rope(const float* x, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, int64_t xnb1, int64_t xnb2, int64_t xnb3,
          const int32_t* pos, float* y, int64_t ynb1, int64_t ynb2, int64_t ynb3, int n_dims, int neox, float freq_base,
          float freq_scale, float attn_factor, hipStream_t s);

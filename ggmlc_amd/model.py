@@ -171,6 +171,7 @@ class Decoder:
                 "next": torch.zeros(1, dtype=torch.int32, device=d),
                 "pos_ids": torch.zeros(s, dtype=torch.int32, device=d),
                 "kv_idx": torch.zeros(s, dtype=torch.int64, device=d),
+                "rope_cs": torch.zeros((s, c.head_dim), dtype=torch.float32, device=d),
                 "mask": torch.zeros((s, self.max_ctx), dtype=torch.float16, device=d),
             }
         return self._bufs[s]
@@ -200,6 +201,8 @@ class Decoder:
         self.ws.get(self._ws_need(s))
         mask = b["mask"][:, :n_kv]
         ops.kv_step_inputs(self.pos, s, b["pos_ids"], b["kv_idx"], mask)
+        if fused:  # the rope (cos, sin) table of this step's positions, shared by all layers
+            ops.rope_cache(b["pos_ids"], c.head_dim, c.rope_base, out=b["rope_cs"])
         x = b["x"]
         ops.get_rows(self.w.embed, ids, out=x)
         rec("pos", -1, self.pos)
@@ -214,7 +217,7 @@ class Decoder:
                 nx = other[id(x)] if pending is not None else None
                 ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=ops.RopeKv(
                     c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"],
-                    b["q"], self.k_cache[li], self.v_cache[li]))
+                    b["q"], self.k_cache[li], self.v_cache[li], cache=b["rope_cs"]))
                 x = nx if nx is not None else x
                 q = b["q"]
             else:

@@ -32,7 +32,7 @@ __all__ = [
     "QWeight", "Q8_0", "Q4_0", "quantize_row_q8_0", "quantize_weights", "mul_mat",
     "set_rows", "flash_attn_ext", "soft_max_ext", "Workspace",
     "swiglu", "rms_norm", "rope_ext", "add", "get_rows", "argmax",
-    "kv_step_inputs", "kv_advance",
+    "kv_step_inputs", "kv_advance", "rope_cache",
 ]
 
 _TORCH_TO_GQ = {torch.float32: F32, torch.float16: F16, torch.int64: I64, torch.int32: I32}
@@ -163,6 +163,7 @@ class RopeKv:
     freq_scale: float = 1.0
     attn_factor: float = 1.0
     n_bad: torch.Tensor | None = None
+    cache: torch.Tensor | None = None  # rope_cache(pos, ...) of the same arguments
 
 
 def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
@@ -183,11 +184,13 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     if rope_kv is not None:
         r = rope_kv
         descs = [_desc(t) for t in (r.pos, r.kv_idx, r.q_out, r.k_cache, r.v_cache)]
-        keep += descs
+        cd = _desc(r.cache) if r.cache is not None else None
+        keep += descs + [cd]
         e = _lib.gq_rope_kv_epilogue(r.n_head, r.n_head_kv, r.head_dim, ctypes.pointer(descs[0]), r.n_dims, r.mode,
                                      r.freq_base, r.freq_scale, r.attn_factor, ctypes.pointer(descs[1]),
                                      ctypes.pointer(descs[2]), ctypes.pointer(descs[3]), ctypes.pointer(descs[4]),
-                                     r.n_bad.data_ptr() if r.n_bad is not None else None)
+                                     r.n_bad.data_ptr() if r.n_bad is not None else None,
+                                     ctypes.pointer(cd) if cd is not None else None)
         keep.append(e)
         f.rope_kv = ctypes.pointer(e)
     if rms_eps is not None:
@@ -290,6 +293,15 @@ def rope_kv_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos: torch.
                                        attn_factor, _desc(kv_idx), _desc(q_out), _desc(k_cache), _desc(v_cache),
                                        nb_ptr, _stream()))
     return q_out
+
+
+def rope_cache(pos: torch.Tensor, n_dims: int, freq_base: float, freq_scale: float = 1.0, attn_factor: float = 1.0,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """ggml_rope_cache_init for each position: fp32 [n, n_dims] of interleaved (cos, sin)."""
+    if out is None:
+        out = torch.empty((pos.shape[0], n_dims), dtype=torch.float32, device=pos.device)
+    check(_lib.load().gq_rope_cache(_desc(pos), n_dims, freq_base, freq_scale, attn_factor, _desc(out), _stream()))
+    return out
 
 
 def add(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -117,7 +117,8 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  *             heads), and go through gq_rope_kv_store with the epilogue's
  *             arguments instead of being written: q rotated into q_out, k rotated
  *             and v copied into the caches at rows kv_idx (fp16). dst must be NULL.
- *             Modes 0 and 2; mode 2 needs n_dims == head_dim; head_dim % 4 == 0.
+ *             Modes 0 and 2; mode 2 needs n_dims == head_dim; head_dim a power of
+ *             two (>= 4).
  * (swiglu, add and rope_kv exclude each other.) Only the GEMV path (M <= 4
  * activation rows) is fused; larger M, and rope_kv shapes outside the conditions
  * above, return GQ_ERR_UNSUPPORTED and the caller runs the ops unfused. No
@@ -134,6 +135,9 @@ typedef struct gq_rope_kv_epilogue {
     gq_tensor* k_cache;      /* F16 [head_dim, rows, n_head_kv, 1] */
     gq_tensor* v_cache;
     int32_t* n_bad;          /* device int32 or NULL */
+    const gq_tensor* rope_cache; /* gq_rope_cache of pos with the same n_dims/freq/attn
+                                    arguments, F32 [n_dims, >= M], or NULL (computed
+                                    in the launch: slower) */
 } gq_rope_kv_epilogue;
 typedef struct gq_mul_mat_fusion {
     int32_t rms_norm;
@@ -225,6 +229,15 @@ int gq_rope_ext(const gq_tensor* a, const gq_tensor* pos, int n_dims, int mode, 
 int gq_rope_kv_store(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* pos, int n_dims,
                      int mode, float freq_base, float freq_scale, float attn_factor, const gq_tensor* kv_idx,
                      gq_tensor* q_out, gq_tensor* k_cache, gq_tensor* v_cache, int32_t* n_bad, gq_stream_t stream);
+
+/* The ROPE cache of ggml_rope_cache_init (CPU ops.cpp:5910-5925) for modes 0/2 with
+ * ext_factor 0: dst[2j, i], dst[2j+1, i] = cos, sin(pos[i] * theta_scale^j * freq_scale)
+ * * attn_factor for j < n_dims/2, theta_scale = freq_base^(-2/n_dims), built by repeated
+ * multiplication as there. pos I32 [n]; dst F32 [n_dims, n], rows contiguous. Every
+ * layer's rope at these positions uses the same table, so a decode step computes it
+ * once for the QKV epilogue (gq_rope_kv_epilogue.rope_cache); same bits as in-kernel. */
+int gq_rope_cache(const gq_tensor* pos, int n_dims, float freq_base, float freq_scale, float attn_factor,
+                  gq_tensor* dst, gq_stream_t stream);
 
 /* ggml_add(a, b) with b repeated over a (ggml_can_repeat). */
 int gq_add(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, gq_stream_t stream);

@@ -91,6 +91,33 @@ def test_rope_gpu(golden_dir, dev, name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", ["neox", "normal"])
+def test_rope_cache_gpu(golden_dir, dev, name):
+    """gq_rope_cache is the table the rope kernels rotate with: rotating the golden
+    input by it in float32 numpy (y0 = x0 c - x1 s, y1 = x0 s + x1 c, each product
+    rounded) gives exactly the bits of gq_rope_ext, and stays within the golden bar."""
+    from ggmlc_amd import ops
+
+    g = np.load(golden_dir / f"rope_{name}.npz")
+    n_dims, mode = int(g["n_dims"]), int(g["mode"])
+    pos = _t(g["pos"], dev)
+    cs = ops.rope_cache(pos, n_dims, float(g["freq_base"])).cpu().numpy()  # [seq, n_dims]
+    x = g["x"].astype(np.float32)  # [seq, heads, hd]
+    y = ops.rope_ext(_t(x, dev).unsqueeze(0), pos, n_dims, mode, float(g["freq_base"]))[0].cpu().numpy()
+    half = n_dims // 2
+    j = np.arange(half)
+    i0, i1 = (j, j + half) if mode == 2 else (2 * j, 2 * j + 1)
+    c = cs[:, None, 0::2]
+    s_ = cs[:, None, 1::2]
+    want = x.copy()
+    x0, x1 = x[..., i0], x[..., i1]
+    want[..., i0] = np.float32(x0 * c) - np.float32(x1 * s_)
+    want[..., i1] = np.float32(x0 * s_) + np.float32(x1 * c)
+    assert np.array_equal(want, y)
+    assert np.abs(want - g["y"]).max() < 1e-4
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name", ["q8_0", "q4_0"])
 def test_get_rows_gpu(golden_dir, dev, name):
     from ggmlc_amd import ops

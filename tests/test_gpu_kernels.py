@@ -200,7 +200,8 @@ def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add, p
     (O.Q8_0, 960, 15, 5, 64, 2, 2, 64),       # SmolLM2 QKV: K = 960, block-wise kernel
     (O.Q4_0, 1024, 4, 2, 128, 4, 0, 96),      # normal rope, partial n_dims, four tokens
 ])
-def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_dims):
+@pytest.mark.parametrize("cached", [False, True])
+def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_dims, cached):
     """The QKV GEMV with the rope + KV-store epilogue gives exactly the bits of
     RMS_NORM -> MUL_MAT -> gq_rope_kv_store (pinned by the decoder-op tests): q_out,
     both caches (untouched rows included) and the count of out-of-range rows."""
@@ -228,8 +229,9 @@ def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_d
     # fused
     q2 = torch.full_like(q1, float("nan"))
     x_sum = torch.empty_like(x)
+    cache = ops.rope_cache(pos, n_dims, 10000.0) if cached else None
     ret = ops.mul_mat_fused(w, x, rms_eps=eps, x_add=d, x_sum=x_sum, rope_kv=ops.RopeKv(
-        Hq, Hkv, hd, pos, n_dims, mode, 10000.0, idx, q2, kc2, vc2, n_bad=bad2))
+        Hq, Hkv, hd, pos, n_dims, mode, 10000.0, idx, q2, kc2, vc2, n_bad=bad2, cache=cache))
     torch.cuda.synchronize()
     assert ret is None
     assert torch.equal(q1, q2), (q1 - q2).abs().max().item()
