@@ -207,6 +207,9 @@ def main() -> int:
     n_gemv = len(mats)
     gemv_gbs = gemv_bytes_token / (gemv_ms_token * 1e-3) / 1e9
     del gg
+    # the same launches as plain streaming reads of the same weight buffers: the
+    # ceiling a kernel that only reads its weights reaches at these per-launch sizes
+    probe_ms_token = time_probe_launches([m.data for m, _ in mats], e0, e1)
 
     # ---- prefill GEMM rate: the 128 GEMMs of one ubatch (M = 512)
     xs = {k: torch.randn((UBATCH, k), generator=gen, device=dev) for k in (cfg.n_embd, cfg.q_dim, cfg.n_ff)}
@@ -268,6 +271,7 @@ def main() -> int:
     c1_ms = e0.elapsed_time(e1) / (3 * Lc)
     c1_bytes = c1[0].nbytes + 4096 * 4 + 4096 * 4
     c1_gbs = c1_bytes / (c1_ms * 1e-3) / 1e9
+    c1_probe_ms = time_probe_launches([c1[i % 16].data for i in range(Lc)], e0, e1) / Lc
     del gq, c1
 
     # ---- measured ceilings next to the datasheet peak: the streaming-read probe
@@ -337,6 +341,8 @@ def main() -> int:
             "us_per_launch": round(gemv_ms_token * 1e3 / n_gemv, 3),
             "launches_per_token": n_gemv,
             "gemv_ms_per_token": round(gemv_ms_token, 4),
+            "read_probe_same_launches_ms": round(probe_ms_token, 4),
+            "frac_of_same_size_read": round(probe_ms_token / gemv_ms_token, 4),
         },
         "roofline_prefill_gemm": {
             "kernel": "k_gemm<Q4_0>: the 128 GEMMs of one 512-token ubatch (activation quantize excluded)",
@@ -353,6 +359,8 @@ def main() -> int:
             "frac_of_peak": round(c1_gbs / HBM_PEAK_GBS, 4),
             "us_per_launch": round(c1_ms * 1e3, 3),
             "bytes_per_launch": c1_bytes,
+            "read_probe_same_size_us": round(c1_probe_ms * 1e3, 3),
+            "frac_of_same_size_read": round(c1_probe_ms / c1_ms, 4),
         },
         "measured_read_GBps": round(read_gbs, 1),
         "measured_copy_GBps": round(copy_gbs, 1),
@@ -365,6 +373,36 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def time_probe_launches(bufs, e0, e1, reps: int = 5) -> float:
+    """ms for one pass of streaming-read probes, one launch per buffer (each read once,
+    whole), captured in a graph and timed like the GEMV graphs."""
+    import torch
+
+    from ggmlc_amd import _lib
+
+    Lib = _lib.load()
+    sink = torch.zeros(4, dtype=torch.int32, device=bufs[0].device)
+
+    def run():
+        st = torch.cuda.current_stream().cuda_stream  # the capture stream inside the graph
+        for b in bufs:
+            _lib.check(Lib.gq_probe_stream_read(b.data_ptr(), b.numel() // 16 * 16, sink.data_ptr(), st))
+
+    run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def decode_gemvs(w, cfg, dev, gen):

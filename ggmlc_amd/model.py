@@ -178,7 +178,7 @@ class Decoder:
 
     # -- one step -------------------------------------------------------------
     def step(self, s: int, n_kv: int, ids: torch.Tensor | None = None, advance: bool = True,
-             trace: list | None = None, fused: bool | None = None) -> torch.Tensor:
+             trace: list | None = None, fused: bool | None = None, logits_all: bool = False) -> torch.Tensor:
         """Run s tokens (ids int32 [s], default: this bucket's ids buffer) at the device
         position; returns the argmax of the last token's logits (device int32 [1]).
 
@@ -186,7 +186,9 @@ class Decoder:
         + SET_ROWS for QKV, -> SWIGLU for gate_up) as single GEMV launches
         (gq_mul_mat_fused, bit-identical).
         trace (eager only): receives (name, layer, copy) of every op's output, so a
-        checker can recompute each op from the inputs this step actually used."""
+        checker can recompute each op from the inputs this step actually used.
+        logits_all: compute the logits of all s tokens into this bucket's "logits_all"
+        buffer [s, vocab] (the graph output of the reference runtime), not only the last."""
         c, b, ws = self.cfg, self._buffers(s), self.ws
         if fused is None:
             fused = s <= 4 and trace is None
@@ -262,14 +264,22 @@ class Decoder:
                 d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
                 ops.add(x, d, out=x)
             rec("x_out", li, x)
-        if fused:
-            logits = ops.mul_mat_fused(self.w.lm_head, x[s - 1:], out=b["logits"], rms_eps=c.rms_eps,
-                                       x_add=pending[s - 1:] if pending is not None else None)
+        r0 = 0 if logits_all else s - 1  # first row that gets logits
+        if logits_all:
+            if "logits_all" not in b:
+                b["logits_all"] = torch.empty((s, c.n_vocab), dtype=torch.float32, device=self.dev)
+            out = b["logits_all"]
+            self.ws.get(ops.mul_mat_workspace_size(self.w.lm_head, s))
         else:
-            h = ops.rms_norm(x[s - 1:], c.rms_eps, out=b["h"][:1])
+            out = b["logits"]
+        if fused:
+            logits = ops.mul_mat_fused(self.w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps,
+                                       x_add=pending[r0:] if pending is not None else None)
+        else:
+            h = ops.rms_norm(x[r0:], c.rms_eps, out=b["h"][:s - r0])
             rec("hf", -1, h)
-            logits = ops.mul_mat(self.w.lm_head, h, out=b["logits"], ws=ws)
-        ops.argmax(logits, out=b["next"])
+            logits = ops.mul_mat(self.w.lm_head, h, out=out, ws=ws)
+        ops.argmax(logits[s - 1 - r0:], out=b["next"])
         rec("logits", -1, logits), rec("next", -1, b["next"])
         if advance:
             ops.kv_advance(self.pos, s)

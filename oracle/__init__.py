@@ -114,6 +114,19 @@ def ref():
         L.ref_llama_step.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32]
         L.ref_llama_free.argtypes = [_vp]
         L.ref_llama_free.restype = None
+        L.ref_rt_last_error.restype = ctypes.c_char_p
+        L.ref_rt_load.restype = _vp
+        L.ref_rt_load.argtypes = [ctypes.c_char_p]
+        L.ref_rt_free.argtypes = [_vp]
+        L.ref_rt_free.restype = None
+        L.ref_rt_describe.restype = _i64
+        L.ref_rt_describe.argtypes = [_vp, ctypes.c_char_p, _i64]
+        L.ref_rt_init_kv.argtypes = [_vp, _i64]
+        L.ref_rt_reset_kv.argtypes = [_vp]
+        L.ref_rt_run.argtypes = [_vp, ctypes.POINTER(ctypes.c_char_p), _vp, _i32, _vp, ctypes.POINTER(_vp), _vp,
+                                 _i32, _i32]
+        L.ref_rt_output.restype = _i64
+        L.ref_rt_output.argtypes = [_vp, ctypes.c_uint32, _vp, _vp, _i64]
         L.ref_init()
         _ref = L
     return _ref
@@ -381,3 +394,56 @@ class RefLlama:
             ref().ref_llama_free(self.h)
             self.h = None
 
+
+
+class RefRuntime:
+    """ggmlc's own runtime (ref_runtime.cpp over the reference's loader.cpp and
+    executor.cpp) on the CPU: load a .gguf with the reference loader, run it with
+    the reference executor (prepare(symbols) -> set_input -> run, the calls of
+    python/ggmlc/runtime/runner.py:97-214)."""
+
+    def __init__(self, path, max_ctx: int | None = None, n_threads: int = 8):
+        self.h = ref().ref_rt_load(str(path).encode())
+        if not self.h:
+            raise RuntimeError("reference loader: " + ref().ref_rt_last_error().decode())
+        self.n_threads = n_threads
+        if max_ctx is not None and ref().ref_rt_init_kv(self.h, max_ctx) != 0:
+            raise RuntimeError("reference init_kv_cache: " + ref().ref_rt_last_error().decode())
+
+    def describe(self) -> list[str]:
+        """The loaded graph as the reference loader sees it (ref_rt_describe lines)."""
+        n = ref().ref_rt_describe(self.h, None, 0)
+        buf = ctypes.create_string_buffer(int(n))
+        ref().ref_rt_describe(self.h, buf, n)
+        return buf.value.decode().splitlines()
+
+    def reset_kv(self) -> None:
+        ref().ref_rt_reset_kv(self.h)
+
+    def run(self, inputs: dict, symbols: dict | None = None) -> None:
+        """inputs: tensor id -> numpy array (raw bytes are passed)."""
+        symbols = symbols or {}
+        names = (ctypes.c_char_p * max(1, len(symbols)))(*[k.encode() for k in symbols])
+        vals = np.array(list(symbols.values()) or [0], np.int64)
+        arrs = [np.ascontiguousarray(a) for a in inputs.values()]
+        tids = np.array(list(inputs.keys()) or [0], np.uint32)
+        datas = (_vp * max(1, len(arrs)))(*[a.ctypes.data for a in arrs])
+        sizes = np.array([a.nbytes for a in arrs] or [0], np.int64)
+        if ref().ref_rt_run(self.h, names, vals.ctypes.data, len(symbols), tids.ctypes.data, datas,
+                            sizes.ctypes.data, len(arrs), self.n_threads) != 0:
+            raise RuntimeError("reference executor: " + ref().ref_rt_last_error().decode())
+
+    def output(self, tid: int, dtype=np.float32) -> np.ndarray:
+        """Output tensor bytes as a C-order array of shape reversed(ne)."""
+        ne = np.zeros(4, np.int64)
+        n = ref().ref_rt_output(self.h, tid, ne.ctypes.data, None, 0)
+        if n < 0:
+            raise RuntimeError("reference output: " + ref().ref_rt_last_error().decode())
+        out = np.empty(int(n), np.uint8)
+        ref().ref_rt_output(self.h, tid, ne.ctypes.data, out.ctypes.data, n)
+        return out.view(dtype).reshape([int(d) for d in ne[::-1]])
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            ref().ref_rt_free(self.h)
+            self.h = None
