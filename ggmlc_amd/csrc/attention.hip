@@ -392,41 +392,66 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
         }
     };
 
-    const uint8_t* mrow = a.mask && qok ? reinterpret_cast<const uint8_t*>(a.mask) + qi * a.mnb1 : nullptr;
     const int nblk = (int)((a.n_kv + BKV - 1) / BKV);
-    // mask values of this lane's keys (16 t + 4 g + r) of the block at c0, as fp16 bits
-    // (0xFC00 = -inf for keys past n_kv and for lanes without a query)
-    auto load_mask = [&](int64_t c0, uint16_t (&mh)[4][4]) {
+    // Mask values of this lane's keys (16 t + 4 g + r) of a block: one 8-byte raw buffer
+    // load per t, issued with the block's K/V prefetch (rows past S and missing masks
+    // read 0 without a fetch; keys past n_kv and lanes without a query become -inf when
+    // unpacked). With n_kv % 4 == 0 every 4-key group of a row lies inside the row;
+    // other shapes, and row strides that are not a multiple of 8 bytes, take 2-byte loads.
+    const bool m8 = a.mask && a.mnb1 % 8 == 0 && a.n_kv % 4 == 0 && (reinterpret_cast<uintptr_t>(a.mask) & 7) == 0;
+    const __amdgpu_buffer_rsrc_t mrs = [&] {
+        const uint64_t base = reinterpret_cast<uint64_t>(a.mask);
+        const int64_t bytes = m8 ? a.S * a.mnb1 : 0;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+        const uint32_t n = (uint32_t)(bytes > 0x7fffffff ? 0x7fffffff : bytes);
+        return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                                 (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
+    }();
+    const uint8_t* mrow = a.mask && qok ? reinterpret_cast<const uint8_t*>(a.mask) + qi * a.mnb1 : nullptr;
+    auto load_mask = [&](int64_t c0, uint32_t (&mw)[4][2]) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int64_t key = c0 + 16 * t + 4 * g;
+            if (m8) {
+                const uint32_t off = qok && key < a.n_kv ? (uint32_t)(qi * a.mnb1 + key * 2) : 0x80000000u;
+                const auto v = __builtin_amdgcn_raw_buffer_load_b64(mrs, (int)off, 0, 0);
+                mw[t][0] = v[0];
+                mw[t][1] = v[1];
+            } else {
+                uint16_t h[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint16_t v = 0;
-                if (key + r >= a.n_kv || !qok) v = 0xFC00;
-                else if (mrow) v = reinterpret_cast<const uint16_t*>(mrow)[key + r];
-                mh[t][r] = v;
+                for (int r = 0; r < 4; ++r) h[r] = mrow && key + r < a.n_kv ? reinterpret_cast<const uint16_t*>(mrow)[key + r] : 0;
+                mw[t][0] = h[0] | ((uint32_t)h[1] << 16);
+                mw[t][1] = h[2] | ((uint32_t)h[3] << 16);
             }
         }
+    };
+    auto mask_val = [&](const uint32_t (&mw)[4][2], int64_t c0, int t, int r) -> float {
+        const int64_t key = c0 + 16 * t + 4 * g + r;
+        if (key >= a.n_kv || !qok) return -INFINITY;
+        return h2f((uint16_t)(mw[t][r >> 1] >> (16 * (r & 1))));
     };
     // A block is skipped when every mask value the tile sees in it is -32768 or below
     // (the executor's masked value) and every query of the tile already holds a
     // running max from an unmasked key: exp(s - 32768 - m) is exactly 0 in fp32 then,
     // so the result is unchanged. (Causal prefill skips the blocks past the diagonal.)
-    auto needed = [&](const uint16_t (&mh)[4][4]) -> int {
+    auto needed = [&](const uint32_t (&mw)[4][2], int64_t c0) -> int {
         bool any = qok && !(m > -16384.0f);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) any = any || h2f(mh[t][r]) > -32768.0f;
+            for (int r = 0; r < 4; ++r) any = any || mask_val(mw, c0, t, r) > -32768.0f;
         return any ? 1 : 0;
     };
-    uint16_t mk[4][4];
+    uint32_t mk[4][2], mkn[4][2];
     fetch(0);
-    load_mask(0, mk);
-    int need = needed(mk);
+    load_mask(0, mkn);
     for (int bi = 0; bi < nblk; ++bi) {
         const int64_t c0 = (int64_t)bi * BKV;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) mk[t][0] = mkn[t][0], mk[t][1] = mkn[t][1];
+        const int need = needed(mk, c0);
         // barrier: the previous block's LDS is fully read; and the skip decision (wave
         // votes in a slot per block parity: the next write to a slot follows a barrier
         // every wave passes only after reading it)
@@ -437,7 +462,10 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
             park();
             __syncthreads();
         }
-        if (bi + 1 < nblk) fetch(c0 + BKV);
+        if (bi + 1 < nblk) {
+            fetch(c0 + BKV);
+            load_mask(c0 + BKV, mkn);
+        }
         if (run) {
             // S^T tiles: keys 16 t .. 16 t + 15 x this wave's 16 queries
             float4_t st[4];
@@ -458,7 +486,7 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float mv = h2f(mk[t][r]);
+                    const float mv = mask_val(mk, c0, t, r);
                     const float sv = mv == -INFINITY ? -INFINITY : st[t][r] * a.scale + mv;
                     st[t][r] = sv;
                     bmax = fmaxf(bmax, sv);
@@ -507,10 +535,6 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
                 }
                 o[dt] = c;
             }
-        }
-        if (bi + 1 < nblk) {
-            load_mask(c0 + BKV, mk);
-            need = needed(mk);
         }
     }
     if (!qok) return;
