@@ -28,7 +28,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;  // LDS row pitch in halves (144 B)
+constexpr int BN = 128, BK = 64, LDK = BK + 8;  // LDS row pitch in halves (144 B)
+constexpr int GEMM_PF_128 = 2, GEMM_PF_64 = 3;   // K steps of loads in flight per tile height
 
 __device__ __forceinline__ uint32_t h2_fma_bits(uint32_t pair, half2v bias, half2v d) {
     half2v h;
@@ -73,6 +74,21 @@ __device__ __forceinline__ void load_block(const uint8_t* p, bool valid, BlockRe
     r.u = *up;
 }
 
+// The block at p, loaded unconditionally (callers pass a valid block address; a
+// step past the matrix loads block 0 and is zeroed where it is used), so the loads of
+// the register ring stay in order for the compiler's memory-counter waits.
+template <int QT>
+__device__ __forceinline__ void load_block_any(const uint8_t* p, BlockRegs<QT>& r) {
+    constexpr int NW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
+    constexpr int TAIL = QT == GQ_TYPE_Q8_0 ? 32 : 16;
+    r.even = (reinterpret_cast<uintptr_t>(p) & 3) == 0;
+    const uint32_t* dp = reinterpret_cast<const uint32_t*>(r.even ? p : p + 2);
+    const uint16_t* up = reinterpret_cast<const uint16_t*>(r.even ? p + TAIL : p);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) r.dw[i] = dp[i];
+    r.u = *up;
+}
+
 // expand one quant block into 32 fp16 (16 dwords)
 template <int QT>
 __device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* out) {
@@ -107,12 +123,16 @@ __device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* o
     }
 }
 
-template <int QT>
+// BM = 128 or 64 tokens per workgroup (64 doubles the grid of small-N shapes); PF K
+// steps of global loads are in flight while a step runs on the matrix cores
+template <int QT, int BM, int PF>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                  int64_t row_bytes, const uint16_t* __restrict__ A,
                                                  int64_t lda, int64_t M, float* __restrict__ dst,
                                                  int64_t ldd) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
+    constexpr int MI = BM / 64;        // 32-row MFMA tiles per wave along M
+    constexpr int AQ = BM / 32;        // 16-byte activation pieces per thread per K step
     __shared__ __align__(16) uint16_t sA[BM * LDK];
     __shared__ __align__(16) uint16_t sB[BN * LDK];
 
@@ -125,88 +145,125 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     const int nb = (int)(K / QK);
     const int nk = (int)cdiv(K, BK);
 
-    // loader mapping: thread -> (row = tid / 2, half = tid % 2)
+    // loader mapping: B: thread -> (weight row tid / 2, block tid % 2); A: thread ->
+    // (token row, AQ consecutive 16-byte pieces of the row's 128-byte K step)
     const int lrow = tid >> 1;
     const int lhalf = tid & 1;
-    const int64_t am = m0 + lrow;
+    const int arow = tid / (8 / AQ);
+    const int apiece = (tid % (8 / AQ)) * AQ;
+    const int64_t am = m0 + arow;
     const int64_t bn = n0 + lrow;
 
-    uint4 ra[4];
-    BlockRegs<QT> rb;
+    // register ring: PF K steps in flight; loads from clamped (always valid) addresses,
+    // the validity travels with the slot and zeroes the data when it is parked in LDS
+    uint4 ra[PF][AQ];
+    BlockRegs<QT> rb[PF];
+    bool av[PF], bv[PF];
 
-    auto load = [&](int kt) {
-        const int64_t k = (int64_t)kt * BK + lhalf * 32;
-        const bool av = am < M && k < K;
-        const uint4* ap = reinterpret_cast<const uint4*>(A + am * lda + k);
+    auto load = [&](int kt, int slot) {
+        const int64_t k = (int64_t)kt * BK + apiece * 8;
+        av[slot] = am < M && k < K;
+        const uint4* ap = reinterpret_cast<const uint4*>(av[slot] ? A + am * lda + k : A);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = av ? ap[i] : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < AQ; ++i) ra[slot][i] = ap[i];
         const int kb = kt * 2 + lhalf;
-        const bool bv = bn < N && kb < nb;
-        load_block<QT>(W + bn * row_bytes + (int64_t)kb * BB, bv, rb);
+        bv[slot] = bn < N && kb < nb;
+        load_block_any<QT>(bv[slot] ? W + bn * row_bytes + (int64_t)kb * BB : W, rb[slot]);
     };
 
-    float16v acc[2][2];
+    float16v acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    load(0);
-    for (int kt = 0; kt < nk; ++kt) {
-        __syncthreads();
+    auto step = [&](int kt, int slot) {
+        __syncthreads();  // the previous step's LDS tiles are fully read
         {
-            uint4* sa = reinterpret_cast<uint4*>(sA + lrow * LDK + lhalf * 32);
+            uint4* sa = reinterpret_cast<uint4*>(sA + arow * LDK + apiece * 8);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sa[i] = ra[i];
+            for (int i = 0; i < AQ; ++i) sa[i] = av[slot] ? ra[slot][i] : make_uint4(0, 0, 0, 0);
             uint32_t e[16];
-            expand_block<QT>(rb, e);
+            expand_block<QT>(rb[slot], e);
             uint4* sb = reinterpret_cast<uint4*>(sB + lrow * LDK + lhalf * 32);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sb[i] = make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3]);
+            for (int i = 0; i < 4; ++i)
+                sb[i] = bv[slot] ? make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3])
+                                 : make_uint4(0, 0, 0, 0);
         }
         __syncthreads();
-        if (kt + 1 < nk) load(kt + 1);
+        if (kt + PF < nk) load(kt + PF, slot);
 #pragma unroll
         for (int k16 = 0; k16 < BK / 16; ++k16) {
-            half8 a[2], b[2];
+            half8 a[MI], b[2];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const uint16_t* pa = sA + (wm * (BM / 2) + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
+                a[i] = *reinterpret_cast<const half8*>(pa);
+            }
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const uint16_t* pa = sA + (wm * 64 + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
-                a[i] = *reinterpret_cast<const half8*>(pa);
                 const uint16_t* pb = sB + (wn * 64 + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
                 b[i] = *reinterpret_cast<const half8*>(pb);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
+    };
+
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+        if (p < nk) load(p, p);
+    for (int kt = 0; kt < nk; kt += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p)
+            if (kt + p < nk) step(kt + p, p);
     }
 
     // D[i][j]: lane holds column j = lane % 32, rows i = 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
             if (n >= N) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int64_t m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (m < M) dst[m * ldd + n] = acc[i][j][r];
             }
         }
+}
+
+// 128-token tiles unless they leave CUs without a workgroup (small N): then 64
+int gemm_bm(int64_t N, int64_t M) {
+    if (const char* e = getenv("GQ_GEMM_BM")) {  // tuning measurements
+        const int v = atoi(e);
+        if (v == 64 || v == 128) return v;
+    }
+    int dev = 0, ncu = 256;
+    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    return cdiv(N, BN) * cdiv(M, 128) < ncu ? 64 : 128;
 }
 
 template <int QT>
 int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M, float* dst,
            int64_t ldd, hipStream_t s) {
     const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
-    const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM));
-    hipLaunchKernelGGL(k_gemm<QT>, grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst, ldd);
+    if (gemm_bm(N, M) == 64) {
+        const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 64));
+        hipLaunchKernelGGL((k_gemm<QT, 64, GEMM_PF_64>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
+                           ldd);
+    } else {
+        const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 128));
+        hipLaunchKernelGGL((k_gemm<QT, 128, GEMM_PF_128>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
+                           ldd);
+    }
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
