@@ -179,7 +179,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    auto step = [&](int kt, int slot) {
+    // one K step from ring slot `slot`; with PREFETCH the slot is refilled with step kt + PF
+    // (always issued, past the matrix from clamped addresses, so every step of the main
+    // loop has the same loads in flight and the memory-counter waits stay exact)
+    auto step = [&](int kt, int slot, auto prefetch) {
         __syncthreads();  // the previous step's LDS tiles are fully read
         {
             uint4* sa = reinterpret_cast<uint4*>(sA + arow * LDK + apiece * 8);
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
                                  : make_uint4(0, 0, 0, 0);
         }
         __syncthreads();
-        if (kt + PF < nk) load(kt + PF, slot);
+        if constexpr (decltype(prefetch)::value) load(kt + PF, slot);
 #pragma unroll
         for (int k16 = 0; k16 < BK / 16; ++k16) {
             half8 a[MI], b[2];
@@ -217,13 +220,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     };
 
 #pragma unroll
-    for (int p = 0; p < PF; ++p)
-        if (p < nk) load(p, p);
-    for (int kt = 0; kt < nk; kt += PF) {
+    for (int p = 0; p < PF; ++p) load(p, p);
+    int kt = 0;
+    for (; kt + PF <= nk; kt += PF) {
 #pragma unroll
-        for (int p = 0; p < PF; ++p)
-            if (kt + p < nk) step(kt + p, p);
+        for (int p = 0; p < PF; ++p) step(kt + p, p, std::true_type{});
     }
+    // tail: the last nk % PF steps consume their slots without refilling
+#pragma unroll
+    for (int p = 0; p < PF - 1; ++p)
+        if (kt + p < nk) step(kt + p, p, std::false_type{});
 
     // D[i][j]: lane holds column j = lane % 32, rows i = 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
