@@ -98,6 +98,11 @@ SIGNATURES = {
     "gq_argmax": (ctypes.c_int, [_P, _P, _vp]),
     "gq_kv_step_inputs": (ctypes.c_int, [_vp, _i64, _vp, _vp, _P, _vp]),
     "gq_kv_advance": (ctypes.c_int, [_vp, _i64, _vp]),
+    "gq_flash_attn_paged_workspace_size": (ctypes.c_size_t, [_P, _P, _i64, _i64]),
+    "gq_flash_attn_paged": (ctypes.c_int, [_P, _P, _P, _P, _P, _i64, _i64, _f32, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_paged_step_inputs": (ctypes.c_int, [_vp, _i64, _P, _i64, _i64, _vp, _vp, _vp]),
+    "gq_paged_advance": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "gq_kv_pages_copy": (ctypes.c_int, [_P, _P, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "gq_probe_stream_read": (ctypes.c_int, [_vp, ctypes.c_size_t, _vp, _vp]),
 }
 

@@ -599,6 +599,119 @@ int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream) {
     return kv_advance(pos, s, (hipStream_t)stream);
 }
 
+// ---- paged KV (batched decode) ---------------------------------------------
+
+namespace {
+int page_log2(int64_t page_size) {
+    if (page_size < 64 || (page_size & (page_size - 1)) || page_size > (1 << 20)) return -1;
+    int l = 0;
+    while ((int64_t(1) << l) < page_size) ++l;
+    return l;
+}
+}  // namespace
+
+size_t gq_flash_attn_paged_workspace_size(const gq_tensor* q, const gq_tensor* k_pool, int64_t max_len,
+                                          int64_t page_size) {
+    if (!q || !k_pool || k_pool->ne[2] <= 0 || page_log2(page_size) < 0) return 0;
+    return attn_paged_workspace_bytes(q->ne[0], q->ne[1], q->ne[2], k_pool->ne[2], max_len, page_size);
+}
+
+int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
+                        const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
+                        float scale, gq_tensor* dst, void* workspace, size_t workspace_bytes, gq_stream_t stream) {
+    if (!q || !k_pool || !v_pool || !page_table || !seq_len || !dst)
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: null tensor");
+    if (q->type != GQ_TYPE_F32 || k_pool->type != GQ_TYPE_F16 || v_pool->type != GQ_TYPE_F16 ||
+        dst->type != GQ_TYPE_F32 || page_table->type != GQ_TYPE_I32 || seq_len->type != GQ_TYPE_I32)
+        return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged: needs F32 q/dst, F16 pools, I32 page table and lengths");
+    const int64_t D = q->ne[0], B = q->ne[1], Hq = q->ne[2], rows = k_pool->ne[1], Hkv = k_pool->ne[2];
+    const int lp = page_log2(page_size);
+    if (lp < 0) return fail(GQ_ERR_INVALID, "flash_attn_paged: page_size must be a power of two >= 64");
+    if (D != 64 && D != 128) return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged: head dim must be 64 or 128");
+    if (Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > 8)
+        return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged: needs Hq a multiple of Hkv with at most 8 q heads per kv head");
+    if (k_pool->ne[0] != D || v_pool->ne[0] != D || v_pool->ne[1] != rows || v_pool->ne[2] != Hkv ||
+        q->ne[3] != 1 || k_pool->ne[3] != 1 || v_pool->ne[3] != 1 || B <= 0 || rows <= 0 || max_len <= 0)
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: shape mismatch q " + shape(q) + " k " + shape(k_pool) + " v " +
+                                        shape(v_pool));
+    if (q->nb[0] != 4 || k_pool->nb[0] != 2 || v_pool->nb[0] != 2 || k_pool->nb[1] % 16 || v_pool->nb[1] % 16 ||
+        k_pool->nb[2] % 16 || v_pool->nb[2] % 16 || (reinterpret_cast<uintptr_t>(k_pool->data) & 15) ||
+        (reinterpret_cast<uintptr_t>(v_pool->data) & 15))
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: pool rows must be 16-byte aligned");
+    if ((int64_t)k_pool->nb[1] * rows > 0x7fffffff || (int64_t)v_pool->nb[1] * rows > 0x7fffffff)
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: one head of a pool must stay below 2 GiB");
+    if (page_table->ne[1] < B || page_table->nb[0] != 4 || page_table->nb[1] % 4 || page_table->ne[0] <= 0 ||
+        page_table->nb[1] / 4 < (size_t)page_table->ne[0])
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: page table must be I32 [max_pages, >= B]: " + shape(page_table));
+    if (page_table->ne[0] * page_size < max_len)
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: max_len exceeds the page table");
+    if (seq_len->ne[0] < B || seq_len->nb[0] != 4)
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: seq_len must be I32 [>= B]: " + shape(seq_len));
+    if (dst->ne[0] != D || dst->ne[1] != Hq || dst->ne[2] != B || dst->nb[0] != 4 || dst->nb[1] != (size_t)D * 4 ||
+        dst->nb[2] != (size_t)D * 4 * Hq)
+        return fail(GQ_ERR_INVALID, "flash_attn_paged: dst must be contiguous F32 [D, Hq, B]: " + shape(dst));
+    AttnArgs a{};
+    a.q = static_cast<const float*>(q->data);
+    a.D = D;
+    a.S = 1;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.qnb1 = (int64_t)q->nb[1];
+    a.qnb2 = (int64_t)q->nb[2];
+    a.k = static_cast<const uint16_t*>(k_pool->data);
+    a.v = static_cast<const uint16_t*>(v_pool->data);
+    a.n_kv = rows;
+    a.knb1 = (int64_t)k_pool->nb[1];
+    a.knb2 = (int64_t)k_pool->nb[2];
+    a.vnb1 = (int64_t)v_pool->nb[1];
+    a.vnb2 = (int64_t)v_pool->nb[2];
+    a.mask = nullptr;
+    a.mnb1 = 0;
+    a.scale = scale;
+    a.max_bias = 0.0f;
+    a.softcap = 0.0f;
+    a.dst = static_cast<float*>(dst->data);
+    PagedKv pg{static_cast<const int32_t*>(seq_len->data), static_cast<const int32_t*>(page_table->data),
+               (int64_t)(page_table->nb[1] / 4), lp, (int)B};
+    return attention_paged(a, pg, max_len, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int gq_paged_step_inputs(const int32_t* pos, int64_t B, const gq_tensor* page_table, int64_t page_size,
+                         int64_t trash_row, int64_t* kv_idx, int32_t* seq_len, gq_stream_t stream) {
+    const int lp = page_log2(page_size);
+    if (!pos || !page_table || !kv_idx || B <= 0 || lp < 0)
+        return fail(GQ_ERR_INVALID, "paged_step_inputs: needs positions, a page table, kv_idx and a power-of-two page");
+    if (page_table->type != GQ_TYPE_I32 || page_table->ne[1] < B || page_table->nb[0] != 4 || page_table->nb[1] % 4 ||
+        page_table->nb[1] / 4 < (size_t)page_table->ne[0])
+        return fail(GQ_ERR_INVALID, "paged_step_inputs: page table must be I32 [max_pages, >= B]: " + shape(page_table));
+    return paged_step_inputs(pos, B, static_cast<const int32_t*>(page_table->data), (int64_t)(page_table->nb[1] / 4),
+                             lp, trash_row, kv_idx, seq_len, (hipStream_t)stream);
+}
+
+int gq_paged_advance(int32_t* pos, const int32_t* active, int64_t B, gq_stream_t stream) {
+    if (!pos || B < 0) return fail(GQ_ERR_INVALID, "paged_advance: null positions");
+    return paged_advance(pos, active, B, (hipStream_t)stream);
+}
+
+int gq_kv_pages_copy(gq_tensor* pool, gq_tensor* cache, const int32_t* pages, int64_t n_pages, int64_t page_size,
+                     int64_t r0, int64_t r1, int to_pool, gq_stream_t stream) {
+    const int lp = page_log2(page_size);
+    if (!pool || !cache || !pages || n_pages <= 0 || lp < 0)
+        return fail(GQ_ERR_INVALID, "kv_pages_copy: needs a pool, a cache, page ids and a power-of-two page");
+    if (pool->type != GQ_TYPE_F16 || cache->type != GQ_TYPE_F16 || pool->ne[0] != cache->ne[0] ||
+        pool->ne[2] != cache->ne[2] || pool->ne[3] != 1 || cache->ne[3] != 1 || pool->nb[0] != 2 ||
+        cache->nb[0] != 2 || (pool->ne[0] * 2) % 16 || pool->nb[1] % 16 || pool->nb[2] % 16 || cache->nb[1] % 16 ||
+        cache->nb[2] % 16 || (reinterpret_cast<uintptr_t>(pool->data) & 15) ||
+        (reinterpret_cast<uintptr_t>(cache->data) & 15))
+        return fail(GQ_ERR_INVALID, "kv_pages_copy: pool " + shape(pool) + " and cache " + shape(cache) +
+                                        " must be F16 [D, rows, H, 1] with 16-byte aligned rows");
+    if (r0 < 0 || r1 > cache->ne[1] || r1 > n_pages * page_size)
+        return fail(GQ_ERR_INVALID, "kv_pages_copy: row range outside the cache or the pages");
+    return kv_pages_copy(static_cast<uint8_t*>(pool->data), (int64_t)pool->nb[1], (int64_t)pool->nb[2], pool->ne[1],
+                         static_cast<uint8_t*>(cache->data), (int64_t)cache->nb[1], (int64_t)cache->nb[2], pages,
+                         n_pages, lp, r0, r1, pool->ne[2], pool->ne[0] * 2, to_pool, (hipStream_t)stream);
+}
+
 // ---- measurement aid ------------------------------------------------------
 
 int gq_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, gq_stream_t stream) {

@@ -136,10 +136,18 @@ __device__ __forceinline__ void h8_to_f(const uint4 w, float* f) {
 // are not read. Streams merge by shuffles inside the wave and through LDS across
 // the 4 waves; the result is the output (one split) or an fp32 partial
 // (O, max, sum) for k_attn_merge.
-template <int D, int NQ, int U>
+//
+// PAGED (batched decode over a paged KV pool): blockIdx.z is the sequence b, whose
+// query vectors are row b of q (the G heads of this kv head) and whose logical KV
+// rows [0, len_b) live in pages of P rows: logical row r is pool row
+// table[b][r / P] * P + r % P. A split never crosses a page (P % rps == 0), so one
+// table entry per workgroup locates all its rows; rows past len_b (and splits past
+// it, or with a negative page id) read nothing and weigh 0. Partials are indexed by
+// query vector b * G + u, so k_attn_merge finishes them as B * G query rows.
+template <int D, int NQ, int U, bool PAGED>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int64_t rps, int n_split, float m0,
                                                   float m1, uint32_t n_head_log2, int q_f16,
-                                                  float* __restrict__ part) {
+                                                  float* __restrict__ part, PagedKv pg) {
     constexpr int LPR = D / 8;       // lanes per row
     constexpr int RPI = 64 / LPR;    // rows per wave instruction
     constexpr int ROWS_IT = 4 * RPI;
@@ -150,13 +158,22 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
     const int grp = lane / LPR, d0 = (lane % LPR) * 8;
     const int split = blockIdx.x, hk = blockIdx.y;
     const int Hkv = (int)a.Hkv;
+    const int seq = PAGED ? (int)blockIdx.z : 0;
+    int64_t r_begin = (int64_t)split * rps, r_len = a.n_kv, prow0 = r_begin;
+    if constexpr (PAGED) {
+        r_len = pg.len[seq];
+        const int64_t pi = r_begin >> pg.log2p;
+        const int page = (r_begin < r_len && pi < pg.tstride) ? pg.table[seq * pg.tstride + pi] : -1;
+        if (page < 0) r_len = 0;  // nothing to read for this split
+        prow0 = ((int64_t)(page < 0 ? 0 : page) << pg.log2p) + (r_begin & ((1 << pg.log2p) - 1));
+    }
 
     float q[NQ][8], slope[NQ];
     const uint16_t* mrow[NQ];
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
         const int uu = u < nq ? u : 0;
-        const int64_t h = (int64_t)hk * G + uu % G, i = uu / G;
+        const int64_t h = (int64_t)hk * G + uu % G, i = seq + uu / G;
         const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + i * a.qnb1 +
                                                          h * a.qnb2) + d0;
 #pragma unroll
@@ -180,8 +197,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         for (int e = 0; e < 8; ++e) o[u][e] = 0.0f;
     }
 
-    const int64_t r_begin = (int64_t)split * rps;
-    const int64_t r_end = min<int64_t>(a.n_kv, r_begin + rps);
+    const int64_t r_end = min<int64_t>(r_len, r_begin + rps);
 
     // All U rows of this lane's stream (rows r0 + t * ROWS_IT) are requested at once,
     // together with their mask values: one memory round trip per workgroup. K/V rows
@@ -204,8 +220,9 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
     for (int t = 0; t < U; ++t) {
         const int64_t r = r0 + (int64_t)t * ROWS_IT;
         const bool in = r < r_end;
-        const uint32_t ko = in ? (uint32_t)(r * a.knb1 + d0 * 2) : 0x80000000u;
-        const uint32_t vo = in ? (uint32_t)(r * a.vnb1 + d0 * 2) : 0x80000000u;
+        const int64_t pr = prow0 + (r - r_begin);  // pool row (the row itself when not paged)
+        const uint32_t ko = in ? (uint32_t)(pr * a.knb1 + d0 * 2) : 0x80000000u;
+        const uint32_t vo = in ? (uint32_t)(pr * a.vnb1 + d0 * 2) : 0x80000000u;
         kw[t] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
         vw[t] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
 #pragma unroll
@@ -285,11 +302,12 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
                 acc += sO[w][u][d] * f;
             }
         }
-        const int64_t h = (int64_t)hk * G + u % G, i = u / G;
+        const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
         if (n_split == 1) {
             a.dst[(i * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
         } else {
-            float* pp = part + (((int64_t)split * Hkv + hk) * nq + u) * (D + 2);
+            const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;  // query vectors of all sequences
+            float* pp = part + (((int64_t)split * Hkv + hk) * nqt + (int64_t)seq * nq + u) * (D + 2);
             pp[2 + d] = acc;
             if (d == 0) pp[0] = mx, pp[1] = L;
         }
@@ -825,8 +843,8 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv);
         const int nq = (int)p.NQ, G = (int)p.G, ns = (int)p.n_split;
 #define GQ_DEC(DD, NN, UU)                                                                                       \
-    hipLaunchKernelGGL((k_attn_dec<DD, NN, UU>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
-                       n_head_log2, q_f16, part)
+    hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, false>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
+                       n_head_log2, q_f16, part, PagedKv{})
 #define GQ_DEC_U(DD, NN)                           \
     do {                                           \
         if (p.dec_u == 8) GQ_DEC(DD, NN, 8);       \
@@ -874,6 +892,83 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ,
                            (int)p.G, a.Hq, a.dst);
     return check_hip(hipGetLastError(), "flash_attn_ext merge launch");
+}
+
+namespace {
+
+struct PagedPlan {
+    int u;
+    int64_t rps, n_split;
+};
+
+// the largest rows-per-lane-stream U (8, 4, 2; at most 4 for more than 4 query vectors)
+// whose split (U x rows per iteration) divides the page and still gives >= 256 workgroups
+PagedPlan paged_plan(int64_t D, int64_t B, int64_t G, int64_t Hkv, int64_t max_len, int64_t page) {
+    const int64_t rows_it = 4 * (64 / (D / 8));
+    PagedPlan p{0, 0, 0};
+    for (int u = G > 4 ? 4 : 8; u >= 2; u >>= 1) {  // a smaller U replaces a larger one: more workgroups
+        const int64_t rps = u * rows_it;
+        if (page % rps) continue;
+        p = PagedPlan{u, rps, cdiv(max_len < 1 ? 1 : max_len, rps)};
+        if (B * Hkv * p.n_split >= DEC_TARGET_WG / 2 && p.n_split <= MAX_SPLIT) break;
+    }
+    return p;
+}
+
+}  // namespace
+
+size_t attn_paged_workspace_bytes(int64_t D, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t page) {
+    if (Hkv <= 0 || Hq % Hkv) return 0;
+    const PagedPlan p = paged_plan(D, B, Hq / Hkv, Hkv, max_len, page);
+    if (p.u == 0 || p.n_split <= 1) return 0;
+    return (size_t)p.n_split * Hkv * B * (Hq / Hkv) * (D + 2) * sizeof(float);
+}
+
+int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void* ws, size_t ws_bytes, hipStream_t s) {
+    const int64_t G = a.Hq / a.Hkv, page = (int64_t)1 << pg.log2p;
+    const PagedPlan p = paged_plan(a.D, pg.B, G, a.Hkv, max_len, page);
+    if (p.u == 0) return fail(GQ_ERR_INVALID, "flash_attn_paged: page size must be a multiple of 64 rows (128 for D = 64)");
+    if (p.n_split > MAX_SPLIT) return fail(GQ_ERR_INVALID, "flash_attn_paged: context too long for one launch");
+    const size_t need = attn_paged_workspace_bytes(a.D, pg.B, a.Hq, a.Hkv, max_len, page);
+    if (need > 0 && (ws == nullptr || ws_bytes < need))
+        return fail(GQ_ERR_WORKSPACE, "flash_attn_paged: workspace too small (need " + std::to_string(need) + " bytes)");
+    float* part = reinterpret_cast<float*>(ws);
+    const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)pg.B);
+    const int nq = (int)G, ns = (int)p.n_split;
+#define GQ_PDEC(DD, NN, UU)                                                                                        \
+    hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, true>), gd, dim3(256), 0, s, a, nq, nq, p.rps, ns, 1.0f, 1.0f, 1u, \
+                       1, part, pg)
+#define GQ_PDEC_U(DD, NN)                          \
+    do {                                           \
+        if (p.u == 8) GQ_PDEC(DD, NN, 8);          \
+        else if (p.u == 4) GQ_PDEC(DD, NN, 4);     \
+        else GQ_PDEC(DD, NN, 2);                   \
+    } while (0)
+    if (a.D == 128) {
+        if (nq == 1) GQ_PDEC_U(128, 1);
+        else if (nq == 2) GQ_PDEC_U(128, 2);
+        else if (nq <= 4) GQ_PDEC_U(128, 4);
+        else if (p.u == 4) GQ_PDEC(128, 8, 4);
+        else GQ_PDEC(128, 8, 2);
+    } else {
+        if (nq == 1) GQ_PDEC_U(64, 1);
+        else if (nq == 2) GQ_PDEC_U(64, 2);
+        else if (nq <= 4) GQ_PDEC_U(64, 4);
+        else if (p.u == 4) GQ_PDEC(64, 8, 4);
+        else GQ_PDEC(64, 8, 2);
+    }
+#undef GQ_PDEC_U
+#undef GQ_PDEC
+    int rc = check_hip(hipGetLastError(), "flash_attn_paged launch");
+    if (rc != GQ_OK || p.n_split == 1) return rc;
+    const dim3 g2((unsigned)(pg.B * G), (unsigned)a.Hkv);
+    if (a.D == 128)
+        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
+                           a.Hq, a.dst);
+    else
+        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
+                           a.Hq, a.dst);
+    return check_hip(hipGetLastError(), "flash_attn_paged merge launch");
 }
 
 }  // namespace gq

@@ -253,7 +253,9 @@ int gemm_bm(int64_t N, int64_t M) {
         if (v == 64 || v == 128) return v;
     }
     int dev = 0, ncu = 256;
-    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        ncu = 256;
     return cdiv(N, BN) * cdiv(M, 128) < ncu ? 64 : 128;
 }
 

@@ -96,6 +96,19 @@ struct AttnArgs {
 };
 size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv);
 int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
+// batched decode over a paged KV pool: sequence b has len[b] rows, logical row r at pool
+// row table[b * tstride + (r >> log2p)] << log2p | (r & (2^log2p - 1))
+struct PagedKv {
+    const int32_t* len;
+    const int32_t* table;
+    int64_t tstride;
+    int log2p;
+    int B;
+};
+// a.q: [B][Hq][D] rows (qnb1 = sequence stride, qnb2 = head stride), a.n_kv = pool rows,
+// a.dst [B][Hq][D]; max_len bounds every len[b] (sizes the grid)
+size_t attn_paged_workspace_bytes(int64_t D, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t page);
+int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void* ws, size_t ws_bytes, hipStream_t s);
 
 // softmax.hip
 struct SoftmaxArgs {
@@ -153,6 +166,12 @@ int argmax(const float* x, int64_t xnb1, int64_t n, int64_t nrows, int32_t* out,
 int kv_step_inputs(const int32_t* pos_dev, int64_t s, int32_t* pos_ids, int64_t* kv_idx, uint16_t* mask,
                    int64_t n_kv, int64_t mask_stride, hipStream_t st);
 int kv_advance(int32_t* pos_dev, int64_t s, hipStream_t st);
+int paged_step_inputs(const int32_t* pos, int64_t B, const int32_t* table, int64_t tstride, int log2p,
+                      int64_t trash_row, int64_t* kv_idx, int32_t* seq_len, hipStream_t st);
+int paged_advance(int32_t* pos, const int32_t* active, int64_t B, hipStream_t st);
+int kv_pages_copy(uint8_t* pool, int64_t pnb1, int64_t pnb2, int64_t prows, uint8_t* cache, int64_t cnb1, int64_t cnb2,
+                  const int32_t* pages, int64_t n_pages, int log2p, int64_t r0, int64_t r1, int64_t H,
+                  int64_t row_bytes, int to_pool, hipStream_t st);
 
 // probe.hip
 int read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t s);

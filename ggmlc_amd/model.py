@@ -64,6 +64,17 @@ LLAMA_7B = LlamaConfig("llama-7b-shape", 32, 4096, 32, 32, 128, 11008, 32000, op
 QWEN25_1_5B = LlamaConfig("qwen2.5-1.5b-shape", 28, 1536, 12, 2, 128, 8960, 151936, ops.Q8_0, tied_embeddings=True)
 
 
+class _Recorder:
+    """Collects (name, layer, copy) of op outputs when a trace list is given."""
+
+    def __init__(self, trace: list | None):
+        self.trace = trace
+
+    def __call__(self, name, li, t):
+        if self.trace is not None:
+            self.trace.append((name, li, t.detach().clone()))
+
+
 def pad_kv_len(n: int, max_ctx: int, n_pad: int = 256) -> int:
     """executor.cpp:58-64"""
     n = max(n, 1)
@@ -127,6 +138,82 @@ def random_weights(cfg: LlamaConfig, device, seed: int = 0, std: float = 0.02) -
             down=q(cfg.n_embd, cfg.n_ff),
         ))
     return ModelWeights(cfg, embed, lm_head, layers)
+
+
+def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, v_cache: list, attend, fused: bool,
+            rec, ws: ops.Workspace, out: torch.Tensor, r0: int) -> torch.Tensor:
+    """The layer stack of one step over s rows: embedding -> layers -> RMS_NORM -> lm_head
+    logits of rows [r0, s) into `out`. b holds the step's buffers, with pos_ids (int32 [s])
+    and kv_idx (int64 [s]) already filled: row i is rotated at pos_ids[i] and its K/V rows
+    are stored at row kv_idx[i] of k_cache[l] / v_cache[l] ([1, Hkv, rows, hd] fp16).
+    attend(l, q) returns the attention output [s, Hq, hd] of layer l for the rotated q
+    ([1, s, Hq, hd]); the caller picks what the rows attend to (one sequence's cache with
+    its causal mask, or each row its own sequence's pages)."""
+    c = w.cfg
+    qd, kvd = c.q_dim, c.kv_dim
+    if fused:  # the rope (cos, sin) table of this step's positions, shared by all layers
+        ops.rope_cache(b["pos_ids"], c.head_dim, c.rope_base, out=b["rope_cs"])
+    x = b["x"]
+    ops.get_rows(w.embed, ids, out=x)
+    # fused path: the residual ADD after O and after down is done by the next GEMV's
+    # prologue (x_next = x + proj, stored for the following ADD), alternating buffers
+    other = {id(b["x"]): b["x_alt"], id(b["x_alt"]): b["x"]}
+    pending = None  # proj still to be added to x
+    for li, L in enumerate(w.layers):
+        if fused:  # ADD + RMS_NORM + QKV + ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
+            nx = other[id(x)] if pending is not None else None
+            ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=ops.RopeKv(
+                c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"],
+                b["q"], k_cache[li], v_cache[li], cache=b["rope_cs"]))
+            x = nx if nx is not None else x
+            q = b["q"]
+        else:
+            rec("x_in", li, x)
+            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+            rec("h1", li, h)
+            qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
+            rec("qkv", li, qkv)
+            # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
+            qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
+            kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
+            vv = qkv[:, qd + kvd:].view(1, s, c.n_head_kv, c.head_dim)
+            if rec.trace is None:  # ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
+                q = ops.rope_kv_store(qv, kv, vv, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"], b["q"],
+                                      k_cache[li], v_cache[li])
+            else:
+                q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
+                k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
+                # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
+                ops.set_rows(k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
+                ops.set_rows(v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
+                rec("q", li, q), rec("k", li, k), rec("kc", li, k_cache[li]), rec("vc", li, v_cache[li])
+        attend(li, q)
+        rec("attn", li, b["attn"])
+        if fused:
+            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"])
+            nx = other[id(x)]
+            a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx)
+            x = nx
+            pending = ops.mul_mat_fused(L.down, a, out=b["proj"])
+        else:
+            o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
+            ops.add(x, o, out=x)
+            rec("x_mid", li, x)
+            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+            rec("h2", li, h)
+            gu = ops.mul_mat(L.gate_up, h, out=b["gu"], ws=ws)
+            rec("gu", li, gu)
+            a = ops.swiglu(gu, out=b["act"])
+            rec("act", li, a)
+            d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
+            ops.add(x, d, out=x)
+        rec("x_out", li, x)
+    if fused:
+        return ops.mul_mat_fused(w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps,
+                                 x_add=pending[r0:] if pending is not None else None)
+    h = ops.rms_norm(x[r0:], c.rms_eps, out=b["h"][:s - r0])
+    rec("hf", -1, h)
+    return ops.mul_mat(w.lm_head, h, out=out, ws=ws)
 
 
 class Decoder:
@@ -193,9 +280,7 @@ class Decoder:
         if fused is None:
             fused = s <= 4 and trace is None
 
-        def rec(name, li, t):
-            if trace is not None:
-                trace.append((name, li, t.detach().clone()))
+        rec = _Recorder(trace)
 
         if n_kv > self.max_ctx:
             raise ValueError("n_kv exceeds the KV cache")
@@ -203,67 +288,13 @@ class Decoder:
         self.ws.get(self._ws_need(s))
         mask = b["mask"][:, :n_kv]
         ops.kv_step_inputs(self.pos, s, b["pos_ids"], b["kv_idx"], mask)
-        if fused:  # the rope (cos, sin) table of this step's positions, shared by all layers
-            ops.rope_cache(b["pos_ids"], c.head_dim, c.rope_base, out=b["rope_cs"])
-        x = b["x"]
-        ops.get_rows(self.w.embed, ids, out=x)
         rec("pos", -1, self.pos)
         scale = 1.0 / math.sqrt(c.head_dim)
-        qd, kvd = c.q_dim, c.kv_dim
-        # fused path: the residual ADD after O and after down is done by the next GEMV's
-        # prologue (x_next = x + proj, stored for the following ADD), alternating buffers
-        other = {id(b["x"]): b["x_alt"], id(b["x_alt"]): b["x"]}
-        pending = None  # proj still to be added to x
-        for li, L in enumerate(self.w.layers):
-            if fused:  # ADD + RMS_NORM + QKV + ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
-                nx = other[id(x)] if pending is not None else None
-                ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=ops.RopeKv(
-                    c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"],
-                    b["q"], self.k_cache[li], self.v_cache[li], cache=b["rope_cs"]))
-                x = nx if nx is not None else x
-                q = b["q"]
-            else:
-                rec("x_in", li, x)
-                h = ops.rms_norm(x, c.rms_eps, out=b["h"])
-                rec("h1", li, h)
-                qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
-                rec("qkv", li, qkv)
-                # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
-                qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
-                kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
-                vv = qkv[:, qd + kvd:].view(1, s, c.n_head_kv, c.head_dim)
-                if trace is None:  # ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
-                    q = ops.rope_kv_store(qv, kv, vv, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"], b["q"],
-                                          self.k_cache[li], self.v_cache[li])
-                else:
-                    q = ops.rope_ext(qv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["q"])
-                    k = ops.rope_ext(kv, b["pos_ids"], c.head_dim, 2, c.rope_base, out=b["k"])
-                    # [1, s, H, hd] -> ggml src [hd, s, H, 1] for SET_ROWS
-                    ops.set_rows(self.k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
-                    ops.set_rows(self.v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
-                    rec("q", li, q), rec("k", li, k), rec("kc", li, self.k_cache[li]), rec("vc", li, self.v_cache[li])
-            ops.flash_attn_ext(q[0].permute(1, 0, 2), self.k_cache[li][0, :, :n_kv], self.v_cache[li][0, :, :n_kv],
-                               mask, scale, out=b["attn"], ws=ws)
-            rec("attn", li, b["attn"])
-            if fused:
-                o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"])
-                nx = other[id(x)]
-                a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx)
-                x = nx
-                pending = ops.mul_mat_fused(L.down, a, out=b["proj"])
-            else:
-                o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
-                ops.add(x, o, out=x)
-                rec("x_mid", li, x)
-                h = ops.rms_norm(x, c.rms_eps, out=b["h"])
-                rec("h2", li, h)
-                gu = ops.mul_mat(L.gate_up, h, out=b["gu"], ws=ws)
-                rec("gu", li, gu)
-                a = ops.swiglu(gu, out=b["act"])
-                rec("act", li, a)
-                d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
-                ops.add(x, d, out=x)
-            rec("x_out", li, x)
+
+        def attend(li, q):
+            return ops.flash_attn_ext(q[0].permute(1, 0, 2), self.k_cache[li][0, :, :n_kv],
+                                      self.v_cache[li][0, :, :n_kv], mask, scale, out=b["attn"], ws=ws)
+
         r0 = 0 if logits_all else s - 1  # first row that gets logits
         if logits_all:
             if "logits_all" not in b:
@@ -272,13 +303,7 @@ class Decoder:
             self.ws.get(ops.mul_mat_workspace_size(self.w.lm_head, s))
         else:
             out = b["logits"]
-        if fused:
-            logits = ops.mul_mat_fused(self.w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps,
-                                       x_add=pending[r0:] if pending is not None else None)
-        else:
-            h = ops.rms_norm(x[r0:], c.rms_eps, out=b["h"][:s - r0])
-            rec("hf", -1, h)
-            logits = ops.mul_mat(self.w.lm_head, h, out=out, ws=ws)
+        logits = forward(self.w, s, b, ids, self.k_cache, self.v_cache, attend, fused, rec, ws, out, r0)
         ops.argmax(logits[s - 1 - r0:], out=b["next"])
         rec("logits", -1, logits), rec("next", -1, b["next"])
         if advance:

@@ -240,6 +240,57 @@ def flash_attn_ext(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torc
     return out
 
 
+def flash_attn_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, page_table: torch.Tensor,
+                     seq_len: torch.Tensor, page_size: int, max_len: int, scale: float,
+                     out: torch.Tensor | None = None, ws: Workspace | None = None) -> torch.Tensor:
+    """Batched decode attention over a paged KV pool (gq_flash_attn_paged): q fp32
+    ``[Hq, B, D]`` (row b = the new token of sequence b), pools fp16 ``[Hkv, rows, D]``,
+    page_table int32 ``[>= B, max_pages]``, seq_len int32 ``[>= B]``. Returns fp32 ``[B, Hq, D]``."""
+    Hq, B, D = q.shape
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=q.device)
+    L = _lib.load()
+    qd, kd, vd, od = _desc(q), _desc(k_pool), _desc(v_pool), _desc(out)
+    need = L.gq_flash_attn_paged_workspace_size(qd, kd, max_len, page_size)
+    ptr, size = _ws(ws).get(need)
+    check(L.gq_flash_attn_paged(qd, kd, vd, _desc(page_table), _desc(seq_len), page_size, max_len, scale, od, ptr,
+                                size, _stream()))
+    return out
+
+
+def flash_attn_paged_workspace_size(D: int, B: int, Hq: int, Hkv: int, max_len: int, page_size: int) -> int:
+    L = _lib.load()
+    q = make_tensor(0, F32, [D, B, Hq, 1], [4, 4 * D, 4 * D * B, 4 * D * B * Hq])
+    k = make_tensor(0, F16, [D, page_size, Hkv, 1], [2, 2 * D, 2 * D * page_size, 2 * D * page_size * Hkv])
+    return L.gq_flash_attn_paged_workspace_size(q, k, max_len, page_size)
+
+
+def paged_step_inputs(pos: torch.Tensor, page_table: torch.Tensor, page_size: int, trash_row: int,
+                      kv_idx: torch.Tensor, seq_len: torch.Tensor | None = None, B: int | None = None) -> None:
+    """kv_idx[b] (int64) = pool row of position pos[b]; seq_len[b] (int32) = pos[b] + 1."""
+    B = pos.numel() if B is None else B
+    check(_lib.load().gq_paged_step_inputs(pos.data_ptr(), B, _desc(page_table), page_size, trash_row,
+                                           kv_idx.data_ptr(), seq_len.data_ptr() if seq_len is not None else None,
+                                           _stream()))
+
+
+def paged_advance(pos: torch.Tensor, active: torch.Tensor | None = None, B: int | None = None) -> None:
+    """pos[b] += 1 on the device where active[b] != 0 (all slots when active is None)."""
+    B = pos.numel() if B is None else B
+    check(_lib.load().gq_paged_advance(pos.data_ptr(), active.data_ptr() if active is not None else None, B,
+                                       _stream()))
+
+
+def kv_pages_copy(pool: torch.Tensor, cache: torch.Tensor, pages: torch.Tensor, page_size: int, r0: int, r1: int,
+                  to_pool: bool) -> None:
+    """Rows [r0, r1) of one sequence between a contiguous cache ``[H, ctx, D]`` and its
+    pages (int32 device ids) in a pool ``[H, rows, D]`` (both fp16)."""
+    if r1 <= r0:
+        return
+    check(_lib.load().gq_kv_pages_copy(_desc(pool), _desc(cache), pages.data_ptr(), pages.numel(), page_size, r0, r1,
+                                       1 if to_pool else 0, _stream()))
+
+
 def soft_max_ext(x: torch.Tensor, mask: torch.Tensor | None = None, scale: float = 1.0,
                  max_bias: float = 0.0, out: torch.Tensor | None = None) -> torch.Tensor:
     """ggml_soft_max_ext over the last dim of x (fp32, up to 4-d)."""

@@ -262,6 +262,52 @@ int gq_kv_step_inputs(const int32_t* pos, int64_t s, int32_t* pos_ids, int64_t* 
                       gq_stream_t stream);
 int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream);
 
+/* ---- paged KV: batched decode over a page pool ---------------------------------
+ * ggmlc's paged KV (runtime/src/executor.cpp:634-920, VMM windows of
+ * vmm_pool.cu) gives every batch slot its own KV rows; the continuous-batching
+ * scheduler (batch_scheduler.cpp:130-405) then decodes all active slots in one
+ * graph. Here a pool holds pages of `page_size` rows (a power of two >= 64,
+ * 128 for D = 64) per layer, F16 [D, rows, Hkv, 1]; a page table I32
+ * [max_pages, B] lists each sequence's pages in order, so logical row r of
+ * sequence b is pool row table[b][r / P] * P + r % P. Pages are shared between
+ * sequences by listing them in several rows of the table (prefix caching). */
+
+/* Batched decode attention: ggml_flash_attn_ext (ggml.c:5402-5437; CPU
+ * ops.cpp:9130-9264) of every sequence's one new token over that sequence's own
+ * rows, each with its own length (the reference shares one position across the
+ * batch, batch_scheduler.cpp:302-321; here every sequence keeps its own):
+ *   out[:, h, b] = softmax_{j < seq_len[b]}(scale * q[:, b, h] . k_b[:, j, h / G]) v_b[:, j, ...]
+ *   q        : F32 [D, B, Hq, 1]  (row b = sequence b; the query is rounded to fp16
+ *              like the CPU decode path)
+ *   k/v_pool : F16 [D, rows, Hkv, 1], one head of a pool below 2 GiB
+ *   page_table, seq_len : device I32 (a negative page id reads nothing)
+ *   max_len  : an upper bound of every seq_len[b] (sizes the launch)
+ *   dst      : F32 [D, Hq, B] contiguous.  D in {64, 128}, Hq / Hkv <= 8.
+ * Equal to the reference's decode step of sequence b with the causal mask of its
+ * position (columns past it weigh exactly 0). */
+size_t gq_flash_attn_paged_workspace_size(const gq_tensor* q, const gq_tensor* k_pool, int64_t max_len,
+                                          int64_t page_size);
+int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
+                        const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
+                        float scale, gq_tensor* dst, void* workspace, size_t workspace_bytes, gq_stream_t stream);
+
+/* Per-slot inputs of a batched decode step from device-resident positions pos[B]
+ * (the per-slot set_decode_pos of executor.cpp:1181-1276):
+ *   kv_idx[b] = the pool row position pos[b] is written to (trash_row when its page
+ *   is missing), seq_len[b] = pos[b] + 1 (0 when missing; seq_len may be NULL).
+ * gq_paged_advance adds 1 to pos[b] where active[b] != 0 (active NULL: every slot). */
+int gq_paged_step_inputs(const int32_t* pos, int64_t B, const gq_tensor* page_table, int64_t page_size,
+                         int64_t trash_row, int64_t* kv_idx, int32_t* seq_len, gq_stream_t stream);
+int gq_paged_advance(int32_t* pos, const int32_t* active, int64_t B, gq_stream_t stream);
+
+/* Rows [r0, r1) of one sequence between a contiguous F16 cache [D, ctx, H, 1] (row r)
+ * and its pages in a pool [D, rows, H, 1] (pages: device I32 [n_pages] page ids):
+ * to_pool = 1 stores computed rows into the pages, 0 loads shared pages into the
+ * cache — what mapping existing pages into a slot's window does in the reference
+ * (paged_kv_map_existing_pages / paged_kv_extract_page_handles, executor.cpp:838-920). */
+int gq_kv_pages_copy(gq_tensor* pool, gq_tensor* cache, const int32_t* pages, int64_t n_pages, int64_t page_size,
+                     int64_t r0, int64_t r1, int to_pool, gq_stream_t stream);
+
 /* ---- measurement aid ------------------------------------------------------
  * No counterpart in the reference. Reads `bytes` (16-byte aligned) once with
  * the coalesced 16-byte streaming loads the GEMV uses, so a benchmark can
