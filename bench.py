@@ -20,6 +20,11 @@ methodology, runtime/tools/ggmlc_bench.cpp:295-560).
               k_gemv_grp<Q4_0> over this command covers the same launch mix.
 * roofline_prefill_gemm = the 128 prefill GEMMs (M = 512) of one ubatch, same way.
 * gemv_c1_q8_0 = configs[0], the Q8_0 Linear 4096 -> 4096 GEMV (16 rotating copies).
+* c5_batched_decode = configs[4]: a Qwen2.5-1.5B-shape decoder (Q8_0, tied embeddings)
+              over the paged KV pool; 16 sequences with contexts uniform in [256, 4096],
+              half of them sharing a 512-token prefix (its pages computed once), then 64
+              batched decode steps at B = 1, 2, 4, 8, 16, every sequence at its own
+              position; tokens/s = B * steps / time (graph replays chained on the device).
 * cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, built from the
               reference sources) running the same decoder graph on the same weights
               with the host's cores: pp512 then decode tokens for a bounded sample.
@@ -56,6 +61,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="decode budget of the CPU sample")
     p.add_argument("--c1-launches", type=int, default=400)
+    p.add_argument("--c5-steps", type=int, default=64, help="timed batched decode steps per batch size")
+    p.add_argument("--no-c5", action="store_true", help="skip the configs[4] continuous-batching decode")
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch one token's decode GEMVs and a 256 MiB device copy, eagerly, 3 times each "
                         "(the workload of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs behind roofline.traffic)")
@@ -368,11 +375,89 @@ def main() -> int:
     }
     log(f"gemv {gemv_gbs:.0f} GB/s, gemm {gemm_tflops:.0f} TFLOP/s, c1 {c1_gbs:.0f} GB/s, read {read_gbs:.0f} GB/s")
 
+    if not args.no_c5:
+        del dec, pp_graphs, tg_graphs
+        torch.cuda.empty_cache()
+        log("configs[4]: batched paged decode")
+        result["c5_batched_decode"] = bench_c5(dev, args.c5_steps)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def bench_c5(dev, steps: int) -> dict:
+    """continuous-batching decode over the paged KV cache (see the module doc)."""
+    import numpy as np
+    import torch
+
+    from ggmlc_amd.model import QWEN25_1_5B, random_weights
+    from ggmlc_amd.paged import BatchDecoder
+
+    cfg, Bmax, P, PREFIX = QWEN25_1_5B, 16, 128, 512
+    w = random_weights(cfg, dev, seed=4242)
+    rng = np.random.default_rng(4242)
+    ctx = rng.integers(256, 4097, Bmax)
+    # the even sequences share the prefix, so their contexts are drawn above it
+    ctx[0::2] = np.where(ctx[0::2] > PREFIX, ctx[0::2], rng.integers(PREFIX + 1, 4097, Bmax // 2))
+    prefix = rng.integers(0, cfg.n_vocab, PREFIX).astype(np.int32)
+    prompts = []
+    for b in range(Bmax):
+        t = rng.integers(0, cfg.n_vocab, int(ctx[b])).astype(np.int32)
+        if b % 2 == 0:  # 50% of the sequences open with the shared prefix
+            t[:PREFIX] = prefix
+        prompts.append(t)
+    max_ctx = 4096 + 2 * steps + 8
+    bd = BatchDecoder(w, max_batch=Bmax, max_ctx=max_ctx, page_size=P)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    first = np.zeros(Bmax, np.int32)
+    for b in range(Bmax):
+        bd.kv.alloc_slot(b)
+        start = 0
+        if b % 2 == 0 and b > 0:  # the prefix pages of sequence 0, shared
+            bd.kv.map_existing_pages(b, 0, bd.kv.pages[0][:PREFIX // P])
+            start = PREFIX
+        bd.kv.ensure_tokens(b, len(prompts[b]) + 2 * steps + 4)
+        first[b] = int(torch.argmax(bd.prefill(b, prompts[b], start)))
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    n_prefill = int(sum(len(t) for t in prompts)) - (Bmax // 2 - 1) * PREFIX
+    kv_token = 2 * cfg.n_layer * cfg.n_head_kv * cfg.head_dim * 2  # bytes of K+V per cached token
+    out = {"model": f"{cfg.name} Q8_0, tied embeddings", "weight_bytes": w.decode_bytes,
+           "contexts": [int(c) for c in ctx], "shared_prefix": PREFIX, "page_tokens": P,
+           "prefill_tokens_computed": n_prefill, "prefill_s": round(prefill_s, 3), "steps": steps, "B": {}}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for B in (1, 2, 4, 8, 16):
+        b = bd._buffers(B)
+
+        def run(n):
+            for _ in range(n):
+                L = bd.ctx_bucket(int(bd.pos_host[:B].max()) + 1)
+                bd.capture(B, L).replay()
+                b["ids"].copy_(b["next"])
+                bd.pos_host[:B] += 1
+
+        for phase in ("warm", "timed"):  # the warm pass captures every graph the timed pass replays
+            for i in range(B):
+                bd.set_pos(i, len(prompts[i]))
+            b["ids"].copy_(torch.from_numpy(first[:B]).to(dev))
+            torch.cuda.synchronize()
+            if phase == "timed":
+                e0.record()
+            run(steps)
+            if phase == "timed":
+                e1.record()
+            torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        kv = sum(len(prompts[i]) + steps / 2 for i in range(B)) * kv_token
+        out["B"][str(B)] = {"tok_s": round(B * 1000.0 / ms, 1), "ms_per_step": round(ms, 4),
+                            "GBps_weights_plus_kv": round((w.decode_bytes + kv) / (ms * 1e-3) / 1e9, 1)}
+        log(f"  B={B}: {B * 1000.0 / ms:.0f} tok/s, {ms:.3f} ms/step")
+    del bd, w
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_probe_launches(bufs, e0, e1, reps: int = 5) -> float:

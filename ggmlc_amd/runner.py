@@ -278,6 +278,7 @@ class ModelRunner:
         self._decoder_cls = Decoder
         self.decoder = None
         self._kv = False
+        self.executor = PagedExecutor(self)
 
     # -- KV cache (runner.py:304-316) -------------------------------------------------
     def init_kv_cache(self, max_ctx: int = 2048) -> None:
@@ -368,6 +369,78 @@ class ModelRunner:
             torch.cuda.synchronize()
             out.append((time.perf_counter() - t0) * 1e3)
         return out
+
+
+class PagedExecutor:
+    """The paged-KV surface of the reference executor (`ModelExecutor.init_paged_kv_cache`,
+    `paged_kv_*`, `get_paged_active_vram_bytes`, `set_tokens_per_page`: executor.cpp:634-920,
+    python_bindings.cpp:196-201) over `paged.BatchDecoder`; what
+    `batching.ContinuousBatchScheduler(runner.executor, ...)` drives.
+
+    Pages hold `tokens_per_page` KV rows of every layer (default 128, a power of two >= 64)
+    in one pool sized at `init_paged_kv_cache` for max_batch sequences of max_ctx rows;
+    `configure_vmm_pool` is accepted for the reference's signature and changes nothing
+    (the pool is allocated once, there is no warm pool of mapped pages)."""
+
+    def __init__(self, runner: "ModelRunner"):
+        self._runner = runner
+        self._tpp = 128
+        self.batch = None
+
+    # -- setup ------------------------------------------------------------------------
+    def set_tokens_per_page(self, n: int) -> None:
+        if self.batch is not None:
+            raise RuntimeError("tokens_per_page must be set before init_paged_kv_cache")
+        if n < 64 or n & (n - 1):
+            raise ValueError("tokens_per_page must be a power of two >= 64")
+        self._tpp = int(n)
+
+    @property
+    def tokens_per_page(self) -> int:
+        return self._tpp
+
+    def get_tokens_per_page(self) -> int:
+        return self._tpp
+
+    def configure_vmm_pool(self, max_warm_pages: int = 0, prealloc_pages: int = 0) -> None:
+        pass
+
+    def init_paged_kv_cache(self, max_batch: int = 8, max_ctx: int = 2048) -> None:
+        from .paged import BatchDecoder
+
+        if self.batch is None:
+            self.batch = BatchDecoder(self._runner.weights, int(max_batch), int(max_ctx), page_size=self._tpp,
+                                      device=self._runner._dev)
+
+    def is_paged_kv_cache_enabled(self) -> bool:
+        return self.batch is not None
+
+    def paged_decoder(self, max_batch: int = 8):
+        """The batched decoder (created with max_batch slots of 2048 rows if not yet)."""
+        if self.batch is None:
+            self.init_paged_kv_cache(max_batch, 2048)
+        return self.batch
+
+    # -- slots ------------------------------------------------------------------------
+    def _kv(self):
+        if self.batch is None:
+            raise RuntimeError("init_paged_kv_cache first")
+        return self.batch.kv
+
+    def paged_kv_alloc_slot(self, slot_id: int, prefix_hash: str = "") -> None:
+        self._kv().alloc_slot(slot_id)
+
+    def paged_kv_free_slot(self, slot_id: int) -> None:
+        self._kv().free_slot(slot_id)
+
+    def paged_kv_ensure_tokens(self, slot_id: int, total_tokens: int) -> None:
+        self._kv().ensure_tokens(slot_id, int(total_tokens))
+
+    def is_paged_slot_allocated(self, slot_id: int) -> bool:
+        return self.batch is not None and self.batch.kv.active[slot_id]
+
+    def get_paged_active_vram_bytes(self) -> int:
+        return 0 if self.batch is None else self.batch.kv.active_bytes()
 
 
 def load(model_source: str | Path | bytes, n_threads: int = 1, device: str = "auto") -> ModelRunner:

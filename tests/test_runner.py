@@ -93,3 +93,45 @@ def test_runner_rejects_missing_or_bad_files(tmp_path):
     with pytest.raises(ValueError, match="GGUF"):
         R.load(b"not a gguf file at all.........................")
     assert R.get_available_devices()[0] == "cuda:0"
+
+
+def test_runner_executor_drives_the_scheduler(tmp_path):
+    """`ContinuousBatchScheduler(runner.executor, ...)` as the reference's tests call it
+    (tests/e2e/test_prefix_caching.py): tokens_per_page set before the paged cache, two
+    requests sharing a one-page prefix, the ids generated for each request checked
+    against the reference executor running the same file on that request alone."""
+    from ggmlc_amd import runner as R
+    from ggmlc_amd.batching import ContinuousBatchScheduler
+    from ggmlc_amd.llama_gguf import write_llama_gguf
+
+    c = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q8_0)
+    p = write_llama_gguf(tmp_path / "m.gguf", c, _weights(c), max_pos=1024)
+    run = R.load(p, device="gpu")
+    ex = run.executor
+    ex.set_tokens_per_page(128)
+    assert ex.tokens_per_page == 128 and not ex.is_paged_kv_cache_enabled()
+    ex.configure_vmm_pool(max_warm_pages=32, prealloc_pages=8)
+    ex.init_paged_kv_cache(4, 512)
+    sched = ContinuousBatchScheduler(ex, max_batch_size=4, eos_token_id=-1)
+    rng = np.random.default_rng(8)
+    shared = rng.integers(0, c.n_vocab, 128).tolist()
+    prompts = [shared + rng.integers(0, c.n_vocab, 9).tolist(), shared + rng.integers(0, c.n_vocab, 3).tolist()]
+    rids = [sched.add_request(prompts[0], max_new_tokens=5)]
+    sched.step()
+    rids.append(sched.add_request(prompts[1], max_new_tokens=5))
+    while sched.has_work():
+        sched.step()
+    assert sched.total_prefix_cache_hits == 1
+    assert ex.get_paged_active_vram_bytes() == ex.batch.kv.page_bytes  # the cached prefix page
+    tid_in, tid_out = run.inputs[0], run.outputs[0]
+    for rid, prompt in zip(rids, prompts):
+        r = sched.get_request(rid)
+        assert r.finished and len(r.generated_tokens) == 5
+        ref = O.RefRuntime(p, max_ctx=512, n_threads=8)
+        ref.run({tid_in: np.array([prompt], np.int32)}, {"s": len(prompt), "pos": 0})
+        want = ref.output(tid_out).reshape(len(prompt), c.n_vocab)[-1]
+        for j, tok in enumerate(r.generated_tokens):
+            top = float(want.max())
+            assert tok == int(np.argmax(want)) or top - float(want[tok]) <= 0.02 * float(want.std()), (rid, j)
+            ref.run({tid_in: np.array([[tok]], np.int32)}, {"s": 1, "pos": len(prompt) + j})
+            want = ref.output(tid_out).reshape(-1)
