@@ -64,6 +64,9 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("b_add", ctypes.POINTER(gq_tensor)),
         ("b_sum", ctypes.POINTER(gq_tensor)),
         ("rope_kv", ctypes.POINTER(gq_rope_kv_epilogue)),
+        ("b_swiglu", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -98,6 +101,7 @@ SIGNATURES = {
     "gq_argmax": (ctypes.c_int, [_P, _P, _vp]),
     "gq_kv_step_inputs": (ctypes.c_int, [_vp, _i64, _vp, _vp, _P, _vp]),
     "gq_kv_advance": (ctypes.c_int, [_vp, _i64, _vp]),
+    "gq_mul_mat_fused_workspace_size": (ctypes.c_size_t, [_P, _P, ctypes.POINTER(gq_mul_mat_fusion)]),
     "gq_flash_attn_paged_workspace_size": (ctypes.c_size_t, [_P, _P, _i64, _i64]),
     "gq_flash_attn_paged": (ctypes.c_int, [_P, _P, _P, _P, _P, _i64, _i64, _f32, _P, _vp, ctypes.c_size_t, _vp]),
     "gq_paged_step_inputs": (ctypes.c_int, [_vp, _i64, _P, _i64, _i64, _vp, _vp, _vp]),

@@ -57,7 +57,7 @@ int gemv_max_m() {
 struct MulMatPlan {
     int64_t K, N, M, x_stride, ldd;
     bool use_gemv;
-    size_t ws;
+    size_t ws, ws_act;
 };
 
 int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, MulMatPlan& p) {
@@ -88,9 +88,12 @@ int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, M
         p.ldd = (int64_t)(dst->nb[1] / 4);
     }
     p.use_gemv = p.M <= gemv_max_m();
-    // the GEMV quantizes the activation in LDS; the GEMM takes it as fp16 from the workspace
+    // the GEMV quantizes the activation in LDS; the GEMM takes it as fp16 from the workspace,
+    // followed by the split-K partials when its plan splits K
     const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 2;
-    p.ws = (raw + 255) & ~(size_t)255;
+    p.ws_act = (raw + 255) & ~(size_t)255;
+    p.ws = p.ws_act;
+    if (!p.use_gemv && p.M > 0) p.ws += (gemm_plan(N, K, p.M).part_bytes + 255) & ~(size_t)255;
     return GQ_OK;
 }
 
@@ -162,7 +165,8 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     uint16_t* A = static_cast<uint16_t*>(workspace);
     rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, p.K, s);
     if (rc) return rc;
-    return gemm(a->type, W, p.N, p.K, A, p.K, p.M, y, p.ldd, s);
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.ws_act);
+    return gemm(a->type, W, p.N, p.K, A, p.K, p.M, y, p.ldd, part, s);
 }
 
 // The rope + KV-store epilogue of gq_mul_mat_fused: the checks of gq_rope_kv_store
@@ -220,6 +224,74 @@ static int rope_kv_epilogue(const gq_rope_kv_epilogue& e, const MulMatPlan& p, c
     return GQ_OK;
 }
 
+// b as the product's input: with b_swiglu its rows hold 2K values and the input is
+// SWIGLU of their halves, so the plan sees the first half
+static int fused_plan(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f, MulMatPlan& p) {
+    if (!f || !a || !b) return fail(GQ_ERR_INVALID, "mul_mat_fused: null argument");
+    if (!f->b_swiglu) return plan_mul_mat(a, b, nullptr, p);
+    if (b->ne[0] != 2 * a->ne[0])
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_swiglu needs b rows of 2K values: " + shape(b));
+    gq_tensor h = *b;
+    h.ne[0] = a->ne[0];
+    return plan_mul_mat(a, &h, nullptr, p);
+}
+
+size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f) {
+    MulMatPlan p;
+    if (fused_plan(a, b, f, p) != GQ_OK || p.M <= GEMV_MAX_M) return 0;
+    return p.ws;
+}
+
+// the GEMM path (M > 4): the input-side fusions run in the activation prologue that
+// feeds the GEMM (act_prep), the output-side ones are not fused there
+static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
+                              const MulMatPlan& p, hipStream_t s) {
+    if (f->swiglu || f->add || f->rope_kv)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: output fusions (swiglu, add, rope_kv) need M <= 4, M = " +
+                                            std::to_string(p.M));
+    if (p.K > PREP_MAX_K) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: K above the prologue's limit");
+    if (f->b_swiglu && (f->rms_norm || f->b_add))
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_swiglu excludes rms_norm and b_add");
+    if (dst->type != GQ_TYPE_F32 || dst->ne[0] != p.N || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
+        dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [N, M, ...]: " + shape(dst));
+    ActPrep ap{static_cast<const float*>(b->data), p.x_stride, nullptr, 0, nullptr, 0, p.K,
+               f->rms_norm ? 1 : 0, f->b_swiglu ? 1 : 0, f->rms_eps};
+    if (f->b_add) {
+        const gq_tensor* r = f->b_add;
+        if (r->type != GQ_TYPE_F32 || r->ne[0] != p.K || r->ne[1] != b->ne[1] || r->ne[2] != b->ne[2] ||
+            r->ne[3] != b->ne[3] || r->nb[0] != 4 || r->nb[1] % 4 != 0 || !rows_uniform(r))
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: b_add must be F32 shaped like b: " + shape(r));
+        ap.d = static_cast<const float*>(r->data);
+        ap.ds = (int64_t)(r->nb[1] / 4);
+        if (f->b_sum) {
+            const gq_tensor* o = f->b_sum;
+            if (o->type != GQ_TYPE_F32 || o->ne[0] != p.K || o->ne[1] != b->ne[1] || o->ne[2] != b->ne[2] ||
+                o->ne[3] != b->ne[3] || o->nb[0] != 4 || o->nb[1] % 4 != 0 || !rows_uniform(o))
+                return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum must be F32 shaped like b: " + shape(o));
+            if (o->data == b->data || o->data == r->data)
+                return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum must not alias b or b_add");
+            ap.sum = static_cast<float*>(o->data);
+            ap.ss = (int64_t)(o->nb[1] / 4);
+        }
+    } else if (f->b_sum) {
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum needs b_add");
+    }
+    if (p.M == 0) return GQ_OK;
+    if (!f->workspace || f->workspace_bytes < p.ws)
+        return fail(GQ_ERR_WORKSPACE, "mul_mat_fused: workspace too small (need " + std::to_string(p.ws) + " bytes)");
+    if ((reinterpret_cast<uintptr_t>(f->workspace) & 255) != 0)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: workspace must be 256-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
+    uint16_t* A = static_cast<uint16_t*>(f->workspace);
+    int rc = act_prep(ap, p.M, A, p.K, s);
+    if (rc) return rc;
+    float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(f->workspace) + p.ws_act);
+    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, p.K, p.M,
+                static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), part, s);
+}
+
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                      gq_stream_t stream) {
     if (!f) return fail(GQ_ERR_INVALID, "mul_mat_fused: null fusion");
@@ -228,10 +300,10 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     if (f->rope_kv ? dst != nullptr : dst == nullptr)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be NULL with rope_kv and given otherwise");
     MulMatPlan p;
-    int rc = plan_mul_mat(a, b, nullptr, p);
+    int rc = fused_plan(a, b, f, p);
     if (rc) return rc;
-    if (p.M > GEMV_MAX_M)
-        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: only the GEMV path (M <= 4) is fused, M = " + std::to_string(p.M));
+    if (p.M > GEMV_MAX_M) return mul_mat_fused_gemm(a, b, dst, f, p, (hipStream_t)stream);
+    if (f->b_swiglu) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: b_swiglu needs M > 4 (use swiglu on the producer)");
     GemvFuse fz;
     if (f->rope_kv) {
         rc = rope_kv_epilogue(*f->rope_kv, p, b, fz);

@@ -136,6 +136,14 @@ __device__ __forceinline__ void rope_pair(float p, int j, float theta_scale, flo
     rope_rotate(c, s, x0, x1, y0, y1);
 }
 
+// SWIGLU of one element: silu(g) * u with ggml's silu(x) = x / (1 + exp(-x))
+// (ops.cpp:3246). k_swiglu, the GEMV's SWIGLU epilogue and the GEMM path's prologue
+// all use this, so they give the same bits.
+__device__ __forceinline__ float swiglu_f(float g, float u) {
+    const float sg = g / (1.0f + expf(-g));
+    return sg * u;
+}
+
 // y = x * rms_scale(...): scale = 1 / sqrt(mean(x^2) + eps), mean rounded to fp32
 __device__ __forceinline__ float rms_scale(double sumsq, int64_t n, float eps) {
     const float mean = (float)(sumsq / (double)n);

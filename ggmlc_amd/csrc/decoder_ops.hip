@@ -26,8 +26,7 @@ __global__ __launch_bounds__(256) void k_swiglu(const float* __restrict__ a, int
     const int64_t r = gid / nc, c = gid % nc;
     const float x = *reinterpret_cast<const float*>(at(a, r * anb1) + c * 4);
     const float g = *reinterpret_cast<const float*>(at(b, r * bnb1) + c * 4);
-    const float s = x / (1.0f + expf(-x));
-    *reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + r * ynb1 + c * 4) = s * g;
+    *reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(y) + r * ynb1 + c * 4) = swiglu_f(x, g);
 }
 
 // ---- RMS_NORM: y = x / sqrt(mean(x^2) + eps) per row (ops.cpp rms_norm_f32, sum in double)

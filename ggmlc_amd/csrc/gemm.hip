@@ -17,6 +17,8 @@
 // runs on the matrix cores. Quant blocks are loaded with one 16-bit and
 // 8 (Q8_0) or 4 (Q4_0) dword loads whose alignment is fixed per block, and
 // expanded with v_perm (0x64xx fp16 exponent trick) + packed fp16 sub/mul.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -125,11 +127,15 @@ __device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* o
 
 // BM = 128 or 64 tokens per workgroup (64 doubles the grid of small-N shapes); PF K
 // steps of global loads are in flight while a step runs on the matrix cores
+//
+// Split K (gridDim.z > 1, for grids with fewer tiles than CUs): workgroup z sums K steps
+// [z * spk, (z + 1) * spk) and writes its partial tile to part[z][M][N]; k_gemm_reduce
+// adds the partials in z order (deterministic).
 template <int QT, int BM, int PF>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                  int64_t row_bytes, const uint16_t* __restrict__ A,
                                                  int64_t lda, int64_t M, float* __restrict__ dst,
-                                                 int64_t ldd) {
+                                                 int64_t ldd, int spk, float* __restrict__ part) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int MI = BM / 64;        // 32-row MFMA tiles per wave along M
     constexpr int AQ = BM / 32;        // 16-byte activation pieces per thread per K step
@@ -143,7 +149,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     const int64_t n0 = (int64_t)blockIdx.x * BN;
     const int64_t m0 = (int64_t)blockIdx.y * BM;
     const int nb = (int)(K / QK);
-    const int nk = (int)cdiv(K, BK);
+    const int kt0 = (int)blockIdx.z * spk;
+    const int kt1 = min((int)cdiv(K, BK), kt0 + spk);  // this workgroup's K steps [kt0, kt1)
 
     // loader mapping: B: thread -> (weight row tid / 2, block tid % 2); A: thread ->
     // (token row, AQ consecutive 16-byte pieces of the row's 128-byte K step)
@@ -162,12 +169,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
 
     auto load = [&](int kt, int slot) {
         const int64_t k = (int64_t)kt * BK + apiece * 8;
-        av[slot] = am < M && k < K;
+        av[slot] = am < M && k < K && kt < kt1;
         const uint4* ap = reinterpret_cast<const uint4*>(av[slot] ? A + am * lda + k : A);
 #pragma unroll
         for (int i = 0; i < AQ; ++i) ra[slot][i] = ap[i];
         const int kb = kt * 2 + lhalf;
-        bv[slot] = bn < N && kb < nb;
+        bv[slot] = bn < N && kb < nb && kt < kt1;
         load_block_any<QT>(bv[slot] ? W + bn * row_bytes + (int64_t)kb * BB : W, rb[slot]);
     };
 
@@ -220,16 +227,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     };
 
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load(p, p);
-    int kt = 0;
-    for (; kt + PF <= nk; kt += PF) {
+    for (int p = 0; p < PF; ++p) load(kt0 + p, p);
+    int kt = kt0;
+    for (; kt + PF <= kt1; kt += PF) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) step(kt + p, p, std::true_type{});
     }
-    // tail: the last nk % PF steps consume their slots without refilling
+    // tail: the last (kt1 - kt0) % PF steps consume their slots without refilling
 #pragma unroll
     for (int p = 0; p < PF - 1; ++p)
-        if (kt + p < nk) step(kt + p, p, std::false_type{});
+        if (kt + p < kt1) step(kt + p, p, std::false_type{});
+    if (part) {  // split K: this workgroup's partial tile
+        dst = part + (int64_t)blockIdx.z * M * N;
+        ldd = N;
+    }
 
     // D[i][j]: lane holds column j = lane % 32, rows i = 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
@@ -246,44 +257,88 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
         }
 }
 
+// dst[m * ldd + n] = sum_z part[z][m][n], z in order
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int ks, int64_t M, int64_t N,
+                                                     float* __restrict__ dst, int64_t ldd) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= M * N) return;
+    const int64_t m = i / N, n = i - m * N;
+    float acc = part[i];
+    for (int z = 1; z < ks; ++z) acc += part[(int64_t)z * M * N + i];
+    dst[m * ldd + n] = acc;
+}
+
+int num_cus() {
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0, v = 256;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            v = 256;
+        ncu = v;
+    }
+    return ncu;
+}
+
 // 128-token tiles unless they leave CUs without a workgroup (small N): then 64
 int gemm_bm(int64_t N, int64_t M) {
     if (const char* e = getenv("GQ_GEMM_BM")) {  // tuning measurements
         const int v = atoi(e);
         if (v == 64 || v == 128) return v;
     }
-    int dev = 0, ncu = 256;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        ncu = 256;
-    return cdiv(N, BN) * cdiv(M, 128) < ncu ? 64 : 128;
+    return cdiv(N, BN) * cdiv(M, 128) < num_cus() ? 64 : 128;
 }
+
+}  // namespace
+
+GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M) {
+    GemmPlan p;
+    p.bm = gemm_bm(N, M);
+    const int64_t tiles = cdiv(N, BN) * cdiv(M, p.bm), nk = cdiv(K, BK);
+    // split K while the tiles leave CUs idle, keeping >= 4 K steps per split
+    int64_t ks = 1;
+    if (tiles < num_cus()) ks = std::min<int64_t>({cdiv(2 * num_cus(), tiles), nk / 4, 16});
+    if (const char* e = getenv("GQ_GEMM_KS")) ks = atoi(e);  // tuning measurements
+    if (ks < 1) ks = 1;
+    p.spk = (int)cdiv(nk, ks);
+    p.ks = (int)cdiv(nk, p.spk);  // no empty split
+    p.part_bytes = p.ks > 1 ? (size_t)p.ks * M * N * sizeof(float) : 0;
+    return p;
+}
+
+namespace {
 
 template <int QT>
 int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M, float* dst,
-           int64_t ldd, hipStream_t s) {
+           int64_t ldd, float* part, hipStream_t s) {
     const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
-    if (gemm_bm(N, M) == 64) {
-        const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 64));
+    const GemmPlan p = gemm_plan(N, K, M);
+    float* pp = p.ks > 1 ? part : nullptr;
+    if (p.bm == 64) {
+        const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 64), (unsigned)p.ks);
         hipLaunchKernelGGL((k_gemm<QT, 64, GEMM_PF_64>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
-                           ldd);
+                           ldd, p.spk, pp);
     } else {
-        const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 128));
+        const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 128), (unsigned)p.ks);
         hipLaunchKernelGGL((k_gemm<QT, 128, GEMM_PF_128>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
-                           ldd);
+                           ldd, p.spk, pp);
     }
-    return check_hip(hipGetLastError(), "gemm launch");
+    int rc = check_hip(hipGetLastError(), "gemm launch");
+    if (rc != GQ_OK || p.ks == 1) return rc;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, s, part, p.ks, M, N, dst, ldd);
+    return check_hip(hipGetLastError(), "gemm reduce launch");
 }
 
 }  // namespace
 
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
-         float* dst, int64_t ldd, hipStream_t s) {
+         float* dst, int64_t ldd, float* part, hipStream_t s) {
     if ((reinterpret_cast<uintptr_t>(W) & 3) != 0) return fail(GQ_ERR_INVALID, "gemm: weight not 4-byte aligned");
     if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0)
         return fail(GQ_ERR_INVALID, "gemm: activation tile misaligned");
-    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, s);
-    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, M, dst, ldd, s);
+    if (gemm_plan(N, K, M).ks > 1 && part == nullptr) return fail(GQ_ERR_WORKSPACE, "gemm: split K needs partials");
+    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, part, s);
+    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, M, dst, ldd, part, s);
 }
 
 }  // namespace gq

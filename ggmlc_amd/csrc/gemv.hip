@@ -130,12 +130,6 @@ __device__ __forceinline__ int64_t phys_row(const GemvFuse& fz, int64_t r) {
     return (r & ~fz.pair_lo) + ((r & fz.pair_lo) >> 1) + (r & 1) * fz.pair_h;
 }
 
-// silu(g) * u with the arithmetic of k_swiglu (x / (1 + expf(-x)) * g)
-__device__ __forceinline__ float swiglu1(float g, float u) {
-    const float sg = g / (1.0f + expf(-g));
-    return sg * u;
-}
-
 // (cos, sin) of every rotated pair of the M positions (tab[m * n_dims/2 + j]) and
 // the M cache rows (after the pairs), computed once per workgroup into LDS while
 // the first weight loads are in flight
@@ -252,7 +246,7 @@ template <int M>
 __device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, float* dst, int64_t ldd, int m,
                                      int64_t row, float v, float vp) {
     if (fz.glu) {
-        if ((row & 1) == 0) dst[(int64_t)m * ldd + (row >> 1)] = swiglu1(v, vp);
+        if ((row & 1) == 0) dst[(int64_t)m * ldd + (row >> 1)] = swiglu_f(v, vp);
         return;
     }
     if (fz.rope) {

@@ -8,6 +8,22 @@ namespace gq {
 // quantize.hip
 int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
                          hipStream_t s);
+// The GEMM path's fused activation prologue (quantize.hip): per row of x (row stride xs),
+// x + d (stored to sum when given) or SWIGLU of the row's halves (glu: x rows are 2K
+// wide), then RMS_NORM (rms), then fp16(d * q) of quantize_row_q8_0 into y.
+constexpr int64_t PREP_MAX_K = 16384;
+struct ActPrep {
+    const float* x;
+    int64_t xs;
+    const float* d;
+    int64_t ds;
+    float* sum;
+    int64_t ss;
+    int64_t K;
+    int rms, glu;
+    float eps;
+};
+int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStream_t s);
 int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
                       int64_t y_stride_elems, hipStream_t s);
 int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s);
@@ -60,9 +76,16 @@ struct GemvFuse {
 int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
          const GemvFuse& fz, hipStream_t s);
 
-// gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k], A fp16
-int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda,
-         int64_t M, float* dst, int64_t ldd, hipStream_t s);
+// gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k], A fp16; grids with
+// fewer tiles than CUs split K over ks workgroups whose partials (part, part_bytes) are summed
+// in order by a second kernel
+struct GemmPlan {
+    int bm, ks, spk;
+    size_t part_bytes;
+};
+GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M);
+int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
+         float* dst, int64_t ldd, float* part, hipStream_t s);
 
 // set_rows.hip
 struct SetRowsArgs {

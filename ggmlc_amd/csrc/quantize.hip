@@ -90,6 +90,97 @@ int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride
     return launch_quant<OUT_F16>(x, nrows, K, x_stride, y, y_stride_elems, s);
 }
 
+// ---- fused activation prologue of the GEMM path ----------------------------------
+// One workgroup per activation row: v = x (+ d, stored to `sum`), then RMS_NORM
+// (v * scale, the sum of squares in the order of k_rms_norm) or SWIGLU of the row's
+// halves (silu(x[c]) * x[K + c], the arithmetic of k_swiglu), then the fp16(d * q)
+// of quantize_row_q8_0 — the bits of ADD -> RMS_NORM -> quantize (or SWIGLU ->
+// quantize) run one by one. Thread t holds elements c * 2048 + 8t.. of every 2048-wide
+// chunk c in registers (K <= PREP_MAX_K).
+constexpr int PREP_CH = PREP_MAX_K / 2048;
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restrict__ y, int64_t y_stride) {
+    __shared__ double red[4];
+    const int64_t m = blockIdx.x;
+    const int nb = (int)(a.K / QK);
+    const float* xr = a.x + m * a.xs;
+    float v[PREP_CH][8];
+#pragma unroll
+    for (int c = 0; c < PREP_CH; ++c) {
+        const int t = c * 256 + (int)threadIdx.x;  // 8-element piece
+        const bool valid = (t >> 2) < nb;
+        if (c * 2048 >= a.K) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = 0.0f;
+            continue;
+        }
+        if (a.glu) {
+            float u[8];
+            load8<VEC>(xr + (int64_t)t * 8, valid, v[c]);
+            load8<VEC>(xr + a.K + (int64_t)t * 8, valid, u);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = swiglu_f(v[c][i], u[i]);
+        } else {
+            load8<VEC>(xr + (int64_t)t * 8, valid, v[c]);
+            if (a.d) {
+                float w[8];
+                load8<VEC>(a.d + m * a.ds + (int64_t)t * 8, valid, w);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + w[i];
+                if (a.sum && valid) {
+                    float* o = a.sum + m * a.ss + (int64_t)t * 8;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = v[c][i];
+                }
+            }
+        }
+    }
+    if (a.rms) {
+        double sq = 0.0;
+#pragma unroll
+        for (int c = 0; c < PREP_CH; ++c)
+            if (c * 2048 < a.K) sq = sumsq8(v[c], sq);
+        const float sc = rms_scale(block_sum_d(sq, red), a.K, a.eps);
+#pragma unroll
+        for (int c = 0; c < PREP_CH; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] * sc;
+    }
+#pragma unroll
+    for (int c = 0; c < PREP_CH; ++c) {
+        if (c * 2048 >= a.K) break;  // uniform: whole chunks past K
+        const int t = c * 256 + (int)threadIdx.x;
+        int q[8];
+        uint16_t dh;
+        int qsum;
+        quant8_block(v[c], q, dh, qsum);  // all lanes: pieces past K quantize zeros
+        if ((t >> 2) >= nb) continue;
+        const float df = h2f(dh);
+        uint16_t hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hv[i] = f2h((float)q[i] * df);
+        uint4 pk;
+        pk.x = hv[0] | ((uint32_t)hv[1] << 16);
+        pk.y = hv[2] | ((uint32_t)hv[3] << 16);
+        pk.z = hv[4] | ((uint32_t)hv[5] << 16);
+        pk.w = hv[6] | ((uint32_t)hv[7] << 16);
+        *reinterpret_cast<uint4*>(y + m * y_stride + (int64_t)t * 8) = pk;
+    }
+}
+
+int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStream_t s) {
+    if (M == 0) return GQ_OK;
+    if (a.K > PREP_MAX_K || a.K % QK) return fail(GQ_ERR_UNSUPPORTED, "act_prep: K too large");
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.xs % 4 == 0) &&
+                     (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) && a.K % 4 == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_act_prep<true>, dim3((unsigned)M), dim3(256), 0, s, a, y, y_stride);
+    else
+        hipLaunchKernelGGL(k_act_prep<false>, dim3((unsigned)M), dim3(256), 0, s, a, y, y_stride);
+    return check_hip(hipGetLastError(), "act_prep launch");
+}
+
 // ---- weight quantizers (quantize.py semantics) ------------------------------
 
 __global__ __launch_bounds__(256) void k_quant_w_q8_0(const float* __restrict__ x, uint8_t* __restrict__ y,

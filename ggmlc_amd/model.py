@@ -151,6 +151,9 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
     its causal mask, or each row its own sequence's pages)."""
     c = w.cfg
     qd, kvd = c.q_dim, c.kv_dim
+    # more than 4 rows without a trace: the GEMM path with ADD / RMS_NORM / SWIGLU fused
+    # into the prologue that quantizes each GEMM's activation (bit-identical as well)
+    pro = not fused and rec.trace is None and s > 4
     if fused:  # the rope (cos, sin) table of this step's positions, shared by all layers
         ops.rope_cache(b["pos_ids"], c.head_dim, c.rope_base, out=b["rope_cs"])
     x = b["x"]
@@ -168,11 +171,16 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             x = nx if nx is not None else x
             q = b["q"]
         else:
-            rec("x_in", li, x)
-            h = ops.rms_norm(x, c.rms_eps, out=b["h"])
-            rec("h1", li, h)
-            qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
-            rec("qkv", li, qkv)
+            if pro:  # ADD + RMS_NORM in the QKV GEMM's prologue
+                nx = other[id(x)] if pending is not None else None
+                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws)
+                x = nx if nx is not None else x
+            else:
+                rec("x_in", li, x)
+                h = ops.rms_norm(x, c.rms_eps, out=b["h"])
+                rec("h1", li, h)
+                qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
+                rec("qkv", li, qkv)
             # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
             qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
             kv = qkv[:, qd:qd + kvd].view(1, s, c.n_head_kv, c.head_dim)
@@ -195,6 +203,12 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx)
             x = nx
             pending = ops.mul_mat_fused(L.down, a, out=b["proj"])
+        elif pro:  # ADD + RMS_NORM before gate_up, SWIGLU before down, in their prologues
+            o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
+            nx = other[id(x)]
+            gu = ops.mul_mat_fused(L.gate_up, x, out=b["gu"], rms_eps=c.rms_eps, x_add=o, x_sum=nx, ws=ws)
+            x = nx
+            pending = ops.mul_mat_fused(L.down, gu, out=b["proj"], x_swiglu=True, ws=ws)
         else:
             o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
             ops.add(x, o, out=x)
@@ -208,9 +222,9 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
             ops.add(x, d, out=x)
         rec("x_out", li, x)
-    if fused:
+    if fused or pro:
         return ops.mul_mat_fused(w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps,
-                                 x_add=pending[r0:] if pending is not None else None)
+                                 x_add=pending[r0:] if pending is not None else None, ws=ws)
     h = ops.rms_norm(x[r0:], c.rms_eps, out=b["h"][:s - r0])
     rec("hf", -1, h)
     return ops.mul_mat(w.lm_head, h, out=out, ws=ws)

@@ -168,18 +168,22 @@ class RopeKv:
 
 def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
                   swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
-                  x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None) -> torch.Tensor | None:
-    """Decode MUL_MAT (x has at most 4 rows) fused with its graph neighbours, bit-identical
-    to the unfused ops: x_add -> x + x_add first (stored to x_sum when given); rms_eps ->
-    RMS_NORM; swiglu -> SWIGLU of the result's two halves (out [..., N/2]); add -> add +
-    result (add may be out); rope_kv -> the result's q/k/v rows go through
-    :func:`rope_kv_store` instead of being written (returns None)."""
+                  x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None, x_swiglu: bool = False,
+                  ws: Workspace | None = None) -> torch.Tensor | None:
+    """MUL_MAT fused with its graph neighbours, bit-identical to the unfused ops:
+    x_add -> x + x_add first (stored to x_sum when given); rms_eps -> RMS_NORM;
+    x_swiglu -> the input is SWIGLU of x's two halves (x [..., 2K]); swiglu -> SWIGLU of
+    the result's two halves (out [..., N/2]); add -> add + result (add may be out);
+    rope_kv -> the result's q/k/v rows go through :func:`rope_kv_store` instead of
+    being written (returns None). Up to 4 rows run as one GEMV launch; more rows take
+    the GEMM path (input-side fusions only, with the workspace ws)."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
     n_out = w.N // 2 if swiglu else w.N
     if out is None and rope_kv is None:
         out = torch.empty(x.shape[:-1] + (n_out,), dtype=torch.float32, device=x.device)
     f = _lib.gq_mul_mat_fusion()
+    f.b_swiglu = 1 if x_swiglu else 0
     keep = []  # descriptors the fusion struct points at
     if rope_kv is not None:
         r = rope_kv
@@ -206,7 +210,11 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     if xs is not None:
         f.b_sum = ctypes.pointer(xs)
     od = _desc(out) if out is not None else None
-    check(_lib.load().gq_mul_mat_fused(w.desc(), _desc(x), od, ctypes.byref(f), _stream()))
+    L, wd, xd = _lib.load(), w.desc(), _desc(x)
+    need = L.gq_mul_mat_fused_workspace_size(wd, xd, ctypes.byref(f))
+    if need:
+        f.workspace, f.workspace_bytes = _ws(ws).get(need)
+    check(L.gq_mul_mat_fused(wd, xd, od, ctypes.byref(f), _stream()))
     del keep
     return out
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define GQ_ABI_VERSION 1
+#define GQ_ABI_VERSION 2
 
 /* ggml type ids (third_party/ggml/include/ggml.h enum ggml_type; ggmlc
  * python/ggmlc/dialect/ggml/ops.py:39-108) */
@@ -102,9 +102,9 @@ size_t gq_mul_mat_workspace_size(const gq_tensor* a, const gq_tensor* b);
 int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* workspace,
                size_t workspace_bytes, gq_stream_t stream);
 
-/* Decode MUL_MAT fused with its neighbours in ggmlc's LLaMA graph (the node runs
+/* MUL_MAT fused with its neighbours in ggmlc's LLaMA graph (the node runs
  * executor.cpp:2034-2090 RMS_NORM, :2362-2447 MUL_MAT, GLU SWIGLU and ADD emit),
- * giving the bits of the unfused calls in one launch, applied in this order:
+ * giving the bits of the unfused calls, applied in this order:
  *   b_add:    b := b + b_add first (gq_add(b, b_add): the residual ADD feeding the
  *             next RMS_NORM); the sum is also stored to b_sum when it is non-null
  *             (b_sum must not alias b or b_add)
@@ -119,12 +119,18 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  *             and v copied into the caches at rows kv_idx (fp16). dst must be NULL.
  *             Modes 0 and 2; mode 2 needs n_dims == head_dim; head_dim a power of
  *             two (>= 4).
- * (swiglu, add and rope_kv exclude each other.) Only the GEMV path (M <= 4
- * activation rows) is fused; larger M, and rope_kv shapes outside the conditions
- * above, return GQ_ERR_UNSUPPORTED and the caller runs the ops unfused. No
- * workspace. The ggml CUDA backend fuses the same neighbours (ADD+RMS_NORM+MUL,
- * MUL_MAT+GLU, MUL_MAT+ADD, ROPE+SET_ROWS) for the same reason: decode steps are
- * launch-bound. */
+ * (swiglu, add and rope_kv exclude each other.) With M <= 4 activation rows (the
+ * GEMV path) everything runs in one launch and needs no workspace. With M > 4 (the
+ * GEMM path, K <= 16384) the input-side fusions run in the prologue that quantizes
+ * the GEMM's activation (two launches), plus
+ *   b_swiglu: the input is SWIGLU(b) of b's two halves (b ne0 = 2K: the gate|up
+ *             product feeding the down projection), excluding rms_norm and b_add;
+ * the output-side ones (swiglu, add, rope_kv), rope_kv shapes outside the conditions
+ * above and b_swiglu on the GEMV path return GQ_ERR_UNSUPPORTED and the caller runs
+ * those ops unfused. The GEMM path takes workspace / workspace_bytes
+ * (gq_mul_mat_fused_workspace_size). The ggml CUDA backend fuses the same neighbours
+ * (ADD+RMS_NORM+MUL, MUL_MAT+GLU, MUL_MAT+ADD, ROPE+SET_ROWS) for the same reason:
+ * these steps are launch-bound. */
 typedef struct gq_rope_kv_epilogue {
     int32_t n_head, n_head_kv, head_dim;
     const gq_tensor* pos;   /* I32 [>= M] */
@@ -147,7 +153,11 @@ typedef struct gq_mul_mat_fusion {
     const gq_tensor* b_add;
     gq_tensor* b_sum;
     const gq_rope_kv_epilogue* rope_kv;
+    int32_t b_swiglu;        /* the input is SWIGLU of b's rows: b ne0 = 2K (GEMM path only) */
+    void* workspace;         /* GEMM path: gq_mul_mat_fused_workspace_size bytes, 256-aligned */
+    size_t workspace_bytes;
 } gq_mul_mat_fusion;
+size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f);
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                      gq_stream_t stream);
 

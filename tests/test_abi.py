@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_struct_layout(lib):
-    assert lib.gq_abi_version() == 1
+    assert lib.gq_abi_version() == 2
     # gq_tensor: void* + 2 x int32 + 4 x int64 + 4 x size_t
     assert ctypes.sizeof(_lib.gq_tensor) == 8 + 8 + 32 + 32
 
@@ -97,8 +97,22 @@ def test_mul_mat_fused_rejects_without_device(lib):
     x5 = _t(_lib.F32, [4096, 5], [4, 16384])
     d5 = _t(_lib.F32, [64, 5], [4, 256])
     f = _lib.gq_mul_mat_fusion(1, 1e-5, 0, None)
-    assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(f), None) == -2  # M > 4: not the GEMV path
+    # M > 4: the GEMM path, whose prologue fusions need the workspace it reports
+    need = lib.gq_mul_mat_fused_workspace_size(w, x5, ctypes.byref(f))
+    assert need >= 5 * 4096 * 2
+    assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(f), None) == -3
+    # output-side fusions are GEMV-only
+    g5 = _lib.gq_mul_mat_fusion(0, 0.0, 1, None)
+    assert lib.gq_mul_mat_fused(w, x5, _t(_lib.F32, [32, 5], [4, 128]), ctypes.byref(g5), None) == -2
     assert b"M <= 4" in lib.gq_last_error()
+    # the SWIGLU input needs 2K-wide rows, and only exists on the GEMM path
+    s5 = _lib.gq_mul_mat_fusion()
+    s5.b_swiglu = 1
+    assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(s5), None) == -1
+    x1w = _t(_lib.F32, [8192, 1], [4, 32768])
+    assert lib.gq_mul_mat_fused(w, x1w, _t(_lib.F32, [64, 1], [4, 256]), ctypes.byref(s5), None) == -2
+    x5w = _t(_lib.F32, [8192, 5], [4, 32768])
+    assert lib.gq_mul_mat_fused_workspace_size(w, x5w, ctypes.byref(s5)) == need
     x = _t(_lib.F32, [4096, 1], [4, 16384])
     d64 = _t(_lib.F32, [64, 1], [4, 256])
     g = _lib.gq_mul_mat_fusion(0, 0.0, 1, None)

@@ -125,7 +125,8 @@ def test_mlp_c2_q4_0(M):
 
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("K,N,M", [(960, 1600, 1), (960, 5120, 3), (2560, 960, 1), (960, 960, 37),
-                                   (1536, 2048, 16), (8960, 1536, 1), (256, 130, 5), (32, 7, 2)])
+                                   (1536, 2048, 16), (8960, 1536, 1), (256, 130, 5), (32, 7, 2),
+                                   (8960, 1536, 16), (1536, 17920, 12)])
 def test_mul_mat_shapes(qtype, K, N, M):
     _check_mm(qtype, K, N, M, seed=K + N + M)
 
@@ -192,6 +193,46 @@ def test_mul_mat_fused_bit_identical_to_unfused(qtype, K, N, M, rms, glu, add, p
     assert torch.equal(got, want), (got - want).abs().max().item()
     if pre_add:
         assert torch.equal(x_sum, x_sum_want)
+
+
+@pytest.mark.parametrize("qtype,K,N,M,mode", [
+    (O.Q4_0, 4096, 12288, 37, "rms"),        # 7B QKV prefill rows: RMS_NORM in the prologue
+    (O.Q4_0, 4096, 22016, 64, "add_rms"),    # 7B gate_up after the residual ADD
+    (O.Q8_0, 1536, 2048, 16, "add_rms"),     # Qwen2.5-1.5B QKV at batch 16 (split K)
+    (O.Q8_0, 8960, 1536, 16, "swiglu"),      # Qwen2.5-1.5B down: SWIGLU of gate|up in front
+    (O.Q4_0, 11008, 4096, 9, "swiglu"),      # 7B down, 9 rows
+    (O.Q8_0, 960, 960, 5, "add_rms"),        # K = 960 (not a multiple of 64)
+    (O.Q4_0, 14336, 64, 6, "rms"),           # K near the prologue's limit
+])
+def test_mul_mat_fused_gemm_prologue_bit_identical(qtype, K, N, M, mode):
+    """More than 4 rows: ADD / RMS_NORM / SWIGLU fused into the prologue that quantizes
+    the GEMM's activation give exactly the bits of the ops run one by one."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    eps = 1e-5
+    if mode == "swiglu":
+        gu = torch.randn((M, 2 * K), generator=g, device=DEV) * 2.0
+        want = ops.mul_mat(w, ops.swiglu(gu))
+        got = ops.mul_mat_fused(w, gu, x_swiglu=True)
+    else:
+        x = torch.randn((M, K), generator=g, device=DEV) * 3.0
+        kw = dict(rms_eps=eps)
+        xin = x
+        if mode == "add_rms":
+            d = torch.randn((M, K), generator=g, device=DEV)
+            x_sum_want = ops.add(x, d)
+            xin = x_sum_want
+            x_sum = torch.full_like(x, float("nan"))
+            kw.update(x_add=d, x_sum=x_sum)
+        want = ops.mul_mat(w, ops.rms_norm(xin, eps))
+        got = ops.mul_mat_fused(w, x, **kw)
+        if mode == "add_rms":
+            torch.cuda.synchronize()
+            assert torch.equal(x_sum, x_sum_want)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape
+    assert torch.equal(got, want), (got - want).abs().max().item()
 
 
 @pytest.mark.parametrize("qtype,K,Hq,Hkv,hd,M,mode,n_dims", [

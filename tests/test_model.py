@@ -377,3 +377,32 @@ def test_fused_decode_steps_bit_identical(shape):
         assert torch.equal(la, lb), (s, (la - lb).abs().max().item())
         assert torch.equal(na, nb) and torch.equal(ra, rb)
         assert int(dec.pos[0]) == p0 + s
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", ["tiny_q4", "gqa6_q8"])
+def test_prefill_gemm_prologue_fusions_bit_identical(shape):
+    """A prefill step whose GEMMs take ADD / RMS_NORM / SWIGLU in their activation
+    prologues gives exactly the bits (logits of every row, KV rows) of the traced step
+    that runs those ops one by one (the op-by-op checks above pin that one)."""
+    import torch
+
+    from ggmlc_amd.model import LlamaConfig, pad_kv_len
+
+    if shape == "tiny_q4":
+        cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q4_0)
+    else:
+        cfg = LlamaConfig("tiny-gqa6", 2, 256, 12, 2, 128, 512, 512, O.Q8_0)
+    dec, _ = _gpu_model(cfg, 512, seed=13)
+    ids = torch.from_numpy(np.random.default_rng(6).integers(0, cfg.n_vocab, 70).astype(np.int32)).cuda()
+    outs = []
+    for trace in (None, []):
+        dec.reset(0)
+        dec.step(70, pad_kv_len(70, 512), ids=ids, trace=trace, logits_all=True)
+        logits = dec._buffers(70)["logits_all"].clone()
+        rows = torch.stack([torch.cat([kc[0, :, :70], vc[0, :, :70]]) for kc, vc in zip(dec.k_cache, dec.v_cache)])
+        outs.append((logits, rows))
+    torch.cuda.synchronize()
+    (la, ra), (lb, rb) = outs
+    assert torch.equal(la, lb), (la - lb).abs().max().item()
+    assert torch.equal(ra, rb)
