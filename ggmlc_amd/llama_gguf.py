@@ -53,6 +53,8 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
     pos = g.add_tensor("rope_arange", I32, [s], CONSTANT, role="constant")
     x = g.add_node("GET_ROWS", [embd, ids], act("inp_embd", [E, s, 1, 1]))
     nq = (Hq + 2 * Hkv) * hd
+    # RMS_NORM's eps as the PyTorch importer records it; the runtime's default needs none
+    eps = {} if float(cfg.rms_eps) == 1e-5 else {"eps": float(cfg.rms_eps)}
     for li in range(cfg.n_layer):
         p = f"blk.{li}."
         if fused_qkv:
@@ -63,7 +65,7 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
         w_o = g.add_tensor(p + "attn_output", wt("attn_output"), [Hq * hd, E], PARAMETER, role="parameter")
         w_gu = g.add_tensor(p + "ffn_gate_up", wt("ffn_gate_up"), [E, 2 * F], PARAMETER, role="parameter")
         w_d = g.add_tensor(p + "ffn_down", wt("ffn_down"), [F, E], PARAMETER, role="parameter")
-        h = g.add_node("RMS_NORM", [x], act(p + "attn_norm", [E, s]))
+        h = g.add_node("RMS_NORM", [x], act(p + "attn_norm", [E, s]), **eps)
         if fused_qkv:
             qkv = g.add_node("MUL_MAT", [w_qkv, h], act(p + "qkv", [nq, s]))
         heads = {}
@@ -85,12 +87,12 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
         a2 = g.add_node("RESHAPE", [a], act(p + "attn_2d", [Hq * hd, s]))
         o = g.add_node("MUL_MAT", [w_o, a2], act(p + "attn_out", [E, s]))
         x = g.add_node("ADD", [x, o], act(p + "ffn_inp", [E, s]))
-        h2 = g.add_node("RMS_NORM", [x], act(p + "ffn_norm", [E, s]))
+        h2 = g.add_node("RMS_NORM", [x], act(p + "ffn_norm", [E, s]), **eps)
         gu = g.add_node("MUL_MAT", [w_gu, h2], act(p + "ffn_gate_up_out", [2 * F, s]))
         sw = g.add_node("GLU", [gu], act(p + "ffn_act", [F, s]), op=GLU_SWIGLU)
         d = g.add_node("MUL_MAT", [w_d, sw], act(p + "ffn_out", [E, s]))
         x = g.add_node("ADD", [x, d], act(p + "l_out", [E, s]))
-    hf = g.add_node("RMS_NORM", [x], act("result_norm", [E, s]))
+    hf = g.add_node("RMS_NORM", [x], act("result_norm", [E, s]), **eps)
     w_lm = embd if cfg.tied_embeddings else g.add_tensor("output", wt("output"), [E, V], PARAMETER,
                                                           role="parameter")
     logits = g.add_tensor("logits", F32, [V, s], OUTPUT)
