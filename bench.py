@@ -63,6 +63,8 @@ def parse():
     p.add_argument("--c1-launches", type=int, default=400)
     p.add_argument("--c5-steps", type=int, default=64, help="timed batched decode steps per batch size")
     p.add_argument("--no-c5", action="store_true", help="skip the configs[4] continuous-batching decode")
+    p.add_argument("--c5-only", action="store_true", help="run only the configs[4] measurement (profiling)")
+    p.add_argument("--c5-batches", default="1,2,4,8,16", help="configs[4] batch sizes")
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch one token's decode GEMVs and a 256 MiB device copy, eagerly, 3 times each "
                         "(the workload of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs behind roofline.traffic)")
@@ -92,6 +94,10 @@ def main() -> int:
     torch.cuda.set_device(0)
     _lib.check(_lib.load().gq_init())
     dev = torch.device("cuda", 0)
+    batches = tuple(int(b) for b in args.c5_batches.split(","))
+    if args.c5_only:
+        print(json.dumps({"c5_batched_decode": bench_c5(dev, args.c5_steps, batches)}), flush=True)
+        return 0
     cfg = LLAMA_7B
     stream = torch.cuda.current_stream()
 
@@ -379,7 +385,7 @@ def main() -> int:
         del dec, pp_graphs, tg_graphs
         torch.cuda.empty_cache()
         log("configs[4]: batched paged decode")
-        result["c5_batched_decode"] = bench_c5(dev, args.c5_steps)
+        result["c5_batched_decode"] = bench_c5(dev, args.c5_steps, batches)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds)
@@ -387,7 +393,7 @@ def main() -> int:
     return 0
 
 
-def bench_c5(dev, steps: int) -> dict:
+def bench_c5(dev, steps: int, batches=(1, 2, 4, 8, 16)) -> dict:
     """continuous-batching decode over the paged KV cache (see the module doc)."""
     import numpy as np
     import torch
@@ -429,7 +435,7 @@ def bench_c5(dev, steps: int) -> dict:
            "contexts": [int(c) for c in ctx], "shared_prefix": PREFIX, "page_tokens": P,
            "prefill_tokens_computed": n_prefill, "prefill_s": round(prefill_s, 3), "steps": steps, "B": {}}
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for B in (1, 2, 4, 8, 16):
+    for B in batches:
         b = bd._buffers(B)
 
         def run(n):
