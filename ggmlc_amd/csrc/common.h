@@ -84,11 +84,56 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---- lane exchanges without LDS (DPP / permlane) ------------------------------------
+// Partner values inside quads of 4 lanes (quad_perm [1,0,3,2] = lane ^ 1 and
+// [2,3,0,1] = lane ^ 2), for 32-bit and 64-bit values.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float quad_xor1(float x) { return __uint_as_float(dpp_u<0xB1>(__float_as_uint(x))); }
+__device__ __forceinline__ float quad_xor2(float x) { return __uint_as_float(dpp_u<0x4E>(__float_as_uint(x))); }
+__device__ __forceinline__ int quad_xor1(int x) { return (int)dpp_u<0xB1>((uint32_t)x); }
+__device__ __forceinline__ int quad_xor2(int x) { return (int)dpp_u<0x4E>((uint32_t)x); }
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+    const uint64_t u = (uint64_t)__builtin_bit_cast(unsigned long long, x);
+    const uint64_t r = (uint64_t)dpp_u<CTRL>((uint32_t)u) | ((uint64_t)dpp_u<CTRL>((uint32_t)(u >> 32)) << 32);
+    return __builtin_bit_cast(double, (unsigned long long)r);
+}
+// sum of a double over the 64 lanes of a wave, every lane gets the total: quads
+// (lane ^ 1, lane ^ 2), half rows (row_half_mirror), rows of 16 (row_mirror), then
+// row pairs and wave halves through permlane16/32 swaps. Each step adds two values
+// that every lane of the pair holds, so all lanes end with the same bits.
+__device__ __forceinline__ double wave_sum_d(double s) {
+    s += dpp_d<0xB1>(s);
+    s += dpp_d<0x4E>(s);
+    s += dpp_d<0x141>(s);
+    s += dpp_d<0x140>(s);
+    {
+        const uint64_t u = (uint64_t)__builtin_bit_cast(unsigned long long, s);
+        const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)u, (uint32_t)u, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+        const double a = __builtin_bit_cast(double, (unsigned long long)((uint64_t)lo[0] | ((uint64_t)hi[0] << 32)));
+        const double b = __builtin_bit_cast(double, (unsigned long long)((uint64_t)lo[1] | ((uint64_t)hi[1] << 32)));
+        s = a + b;
+    }
+    {
+        const uint64_t u = (uint64_t)__builtin_bit_cast(unsigned long long, s);
+        const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)u, (uint32_t)u, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(u >> 32), (uint32_t)(u >> 32), false, false);
+        const double a = __builtin_bit_cast(double, (unsigned long long)((uint64_t)lo[0] | ((uint64_t)hi[0] << 32)));
+        const double b = __builtin_bit_cast(double, (unsigned long long)((uint64_t)lo[1] | ((uint64_t)hi[1] << 32)));
+        s = a + b;
+    }
+    return s;
+}
+
 // ---- RMS_NORM sum of squares in one fixed order ----------------------------------
 // Shared by k_rms_norm and the GEMV prologue, so RMS_NORM -> MUL_MAT fused gives the
 // bits of the two ops: lane t of a 256-lane block owns elements [2048 p + 8 t,
 // 2048 p + 8 t + 8) of pass p; each lane sums the fp32 squares in double in element
-// order (passes ascending), then the wave by xor shuffles, then the 4 waves in order
+// order (passes ascending), then the wave (wave_sum_d), then the 4 waves in order
 // (ggml sums in double too: ops.cpp rms_norm_f32, ggml_float).
 __device__ __forceinline__ double sumsq8(const float (&v)[8], double s) {
 #pragma clang fp contract(off)
@@ -102,8 +147,7 @@ __device__ __forceinline__ double sumsq8(const float (&v)[8], double s) {
 
 // all 256 lanes call it; red: 4 doubles of LDS (free again on return)
 __device__ __forceinline__ double block_sum_d(double s, double* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_sum_d(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
     const double r = red[0] + red[1] + red[2] + red[3];
@@ -163,8 +207,8 @@ __device__ __forceinline__ void quant8_block(const float (&v)[8], int (&q)[8], u
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, quad_xor1(amax));
+    amax = fmaxf(amax, quad_xor2(amax));
     const float d = amax / 127.0f;  // IEEE division, correctly rounded (no fast-math)
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     int s = 0;
@@ -176,8 +220,8 @@ __device__ __forceinline__ void quant8_block(const float (&v)[8], int (&q)[8], u
         q[i] = iv;
         s += iv;
     }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
+    s += quad_xor1(s);
+    s += quad_xor2(s);
     qsum = s;
     dh = f2h(d);
 }

@@ -168,11 +168,17 @@ __device__ __forceinline__ void rope_cache_loads(const GemvFuse& fz, RopeIn<M>& 
         in.cs[k] = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
     }
 }
-// the positions and cache rows (wave-uniform loads), read first thing
+// the cache rows and, when the (cos, sin) table is not cached, the positions
+// (wave-uniform loads), read first thing; nothing waits for them before the weight
+// loads are issued
 template <int M>
-__device__ __forceinline__ void rope_inputs(const GemvRope& r, RopeIn<M>& in) {
+__device__ __forceinline__ void rope_inputs(const GemvFuse& fz, RopeIn<M>& in) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) in.pos[m] = r.pos[m], in.row[m] = r.idx[m];
+    for (int m = 0; m < M; ++m) in.row[m] = fz.rp.idx[m];
+    if (!rope_cached(fz, M)) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) in.pos[m] = fz.rp.pos[m];
+    }
 }
 // (cos, sin) of every rotated pair of the M positions (tab[m * n_dims/2 + j]) and the
 // M cache rows (after the pairs) into LDS
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     // waited for while the weight loads stay in flight (vector loads complete in order)
     RopeIn<M> rin{};
     rope_cache_loads<M>(fz, rin);
-    if (fz.rope) rope_inputs<M>(fz.rp, rin);
+    if (fz.rope) rope_inputs<M>(fz, rin);
     float xr[XPMAX][8], ar[XAMAX][8];
     const bool xpre = M * XP <= XPMAX && (!act.d || M * XP <= XAMAX);
     if (xpre) {
@@ -371,8 +377,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         }
         if (++lj == S) lj = 0, ++lk;
     };
-#pragma unroll
-    for (int s = 0; s < PF; ++s) issue(pre[s]);
+    // the first step's loads go out before the activation prologue, the rest after it:
+    // a wave stalls at issue while the memory pipeline is full, and the prologue would
+    // wait behind loads it does not need (measured: 5-13% faster launches)
+    issue(pre[0]);
     __builtin_amdgcn_sched_barrier(0);
     if (fz.rope) rope_table<M>(fz, rin, rtab);  // while the loads are in flight
 
@@ -433,6 +441,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, G * 256, s_act, act_bytes, scale);
     }
     __syncthreads();  // quantized activation (and rope table) visible to all waves
+#pragma unroll
+    for (int s = 1; s < PF; ++s) issue(pre[s]);
 
     float acc[M];
 #pragma unroll
@@ -551,7 +561,7 @@ __global__ __launch_bounds__(256) void k_gemv_blk(const uint8_t* __restrict__ W,
     if (fz.rope) {
         RopeIn<M> rin{};
         rope_cache_loads<M>(fz, rin);
-        rope_inputs<M>(fz.rp, rin);
+        rope_inputs<M>(fz, rin);
         rope_table<M>(fz, rin, rtab);
     }
     __syncthreads();
