@@ -32,12 +32,40 @@ constexpr int DEC_MAX_NQ = 8;     // query vectors per kv head served by the dec
 constexpr int DEC_TARGET_WG = 512;
 constexpr int MAX_SPLIT = 1024;
 
+// Fused split merge of the decode kernel: the last workgroup to finish a (sequence,
+// kv head) merges that pair's split partials itself, so no second launch is needed.
+// Partials are written and read with agent-scope relaxed atomics (coherent across the
+// XCDs' L2s, no cache flushes) and each workgroup arrives on the pair's counter after
+// its own stores have completed. Every launch leaves the counters at zero (the last
+// arrival resets its counter), so decode launches on one device must not overlap
+// (they run on one stream).
+constexpr int ARRIVE_N = 4096;     // (sequence, kv head) pairs of one launch
+constexpr int FUSE_MAX_SPLIT = 16;  // splits merged from registers (one round trip)
+__device__ unsigned g_attn_arrive[ARRIVE_N];
+
+__device__ __forceinline__ void st_ag(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_ag(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct Plan {
     int64_t G, NQ, n_qt, n_chunks, cps, n_split;
     bool dec;               // k_attn_dec: one workgroup per (split, kv head), all NQ queries
     int64_t rows_per_split;  // dec only
     int dec_u;               // dec only: rows per lane stream
 };
+
+// the split merge runs inside the decode kernel when one thread per (query vector,
+// dim) can hold every split's partial in registers and the launch's (sequence, kv
+// head) pairs fit the counters;
+// GQ_ATTN_SEPARATE_MERGE=1 keeps the second launch (comparison runs)
+bool fuse_merge_ok(int64_t n_split, int64_t nq, int64_t D, int64_t pairs) {
+    const char* e = getenv("GQ_ATTN_SEPARATE_MERGE");  // read per call: tests switch it
+    const bool off = e && atoi(e) == 1;
+    return !off && n_split > 1 && n_split <= FUSE_MAX_SPLIT && nq * D <= 256 && pairs <= ARRIVE_N;
+}
 
 Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     Plan p;
@@ -147,7 +175,7 @@ __device__ __forceinline__ void h8_to_f(const uint4 w, float* f) {
 template <int D, int NQ, int U, bool PAGED>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int64_t rps, int n_split, float m0,
                                                   float m1, uint32_t n_head_log2, int q_f16,
-                                                  float* __restrict__ part, PagedKv pg) {
+                                                  float* __restrict__ part, PagedKv pg, int fuse) {
     constexpr int LPR = D / 8;       // lanes per row
     constexpr int RPI = 64 / LPR;    // rows per wave instruction
     constexpr int ROWS_IT = 4 * RPI;
@@ -214,26 +242,46 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
                                                  (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
     };
     const __amdgpu_buffer_rsrc_t krs = rsrc(a.k, a.knb2, a.knb1), vrs = rsrc(a.v, a.vnb2, a.vnb1);
+    // mask rows as buffers too (no mask: an empty resource, every value reads 0)
+    __amdgpu_buffer_rsrc_t mrs[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+        const uint64_t base = reinterpret_cast<uint64_t>(mrow[u]);
+        const uint32_t n = mrow[u] ? (uint32_t)(r_len * 2 > 0x7fffffff ? 0x7fffffff : r_len * 2) : 0u;
+        // readfirstlane returns int: both halves go through uint32_t so the low half is
+        // zero-extended when the address is put back together
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+        mrs[u] = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                                   (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
+    }
     u32x4 kw[U], vw[U];
-    float mk[U][NQ];
+    uint16_t mb[U][NQ];
+    bool rin[U];
 #pragma unroll
     for (int t = 0; t < U; ++t) {
         const int64_t r = r0 + (int64_t)t * ROWS_IT;
         const bool in = r < r_end;
+        rin[t] = in;
         const int64_t pr = prow0 + (r - r_begin);  // pool row (the row itself when not paged)
         const uint32_t ko = in ? (uint32_t)(pr * a.knb1 + d0 * 2) : 0x80000000u;
         const uint32_t vo = in ? (uint32_t)(pr * a.vnb1 + d0 * 2) : 0x80000000u;
         kw[t] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
         vw[t] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
 #pragma unroll
+        for (int u = 0; u < NQ; ++u)
+            mb[t][u] = __builtin_amdgcn_raw_buffer_load_b16(mrs[u], in ? (int)(r * 2) : (int)0x80000000, 0, 0);
+    }
+    // the mask values are converted only once every row's loads are in flight (a use
+    // right after its load would wait for all loads issued before it)
+    __builtin_amdgcn_sched_barrier(0);
+    float mk[U][NQ];
+#pragma unroll
+    for (int t = 0; t < U; ++t) {
+#pragma unroll
         for (int u = 0; u < NQ; ++u) {
-            float mv = 0.0f;
-            if (!in || u >= nq) mv = -INFINITY;
-            else if (mrow[u]) {
-                const float x = h2f(mrow[u][r]);
-                mv = x == -INFINITY ? -INFINITY : slope[u] * x;
-            }
-            mk[t][u] = mv;
+            const float x = h2f(mb[t][u]);
+            mk[t][u] = !rin[t] || u >= nq ? -INFINITY : (x == -INFINITY ? -INFINITY : slope[u] * x);
         }
     }
 #pragma unroll
@@ -308,10 +356,66 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         } else {
             const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;  // query vectors of all sequences
             float* pp = part + (((int64_t)split * Hkv + hk) * nqt + (int64_t)seq * nq + u) * (D + 2);
-            pp[2 + d] = acc;
-            if (d == 0) pp[0] = mx, pp[1] = L;
+            if (fuse) {
+                st_ag(pp + 2 + d, acc);
+                if (d == 0) st_ag(pp, mx), st_ag(pp + 1, L);
+            } else {
+                pp[2 + d] = acc;
+                if (d == 0) pp[0] = mx, pp[1] = L;
+            }
         }
     }
+    if (!fuse || n_split == 1) return;
+
+    // arrive once this workgroup's partial stores are complete; the last arrival merges
+    __shared__ int sLast;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        unsigned* ctr = &g_attn_arrive[seq * Hkv + hk];
+        const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == (unsigned)(n_split - 1);
+        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sLast = last;
+    }
+    __syncthreads();
+    if (!sLast) return;
+    // The reduction of k_attn_merge with the same operations in the same order, one
+    // thread per (query vector, dim) with every split's (m, l, o) requested at once:
+    // one memory round trip (n_split <= FUSE_MAX_SPLIT, nq <= 256 / D).
+    const int u = tid / D, d = tid % D;
+    if (u >= nq) return;
+    const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;
+    const int64_t stride = (int64_t)Hkv * nqt * (D + 2);
+    const float* base = part + ((int64_t)hk * nqt + (int64_t)seq * nq + u) * (D + 2);
+    float pm[FUSE_MAX_SPLIT], pl[FUSE_MAX_SPLIT], po[FUSE_MAX_SPLIT];
+#pragma unroll
+    for (int s2 = 0; s2 < FUSE_MAX_SPLIT; ++s2) {
+        if (s2 < n_split) {
+            pm[s2] = ld_ag(base + s2 * stride);
+            pl[s2] = ld_ag(base + s2 * stride + 1);
+            po[s2] = ld_ag(base + s2 * stride + 2 + d);
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s2 = 0; s2 < FUSE_MAX_SPLIT; ++s2) {
+        if (s2 < n_split) {
+            pm[s2] = pl[s2] == 0.0f ? -INFINITY : pm[s2];
+            mx = fmaxf(mx, pm[s2]);
+        }
+    }
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < FUSE_MAX_SPLIT; ++s2) {
+        if (s2 < n_split) {
+            const float w = pm[s2] == -INFINITY ? 0.0f : __expf(pm[s2] - mx);
+            L += pl[s2] * w;
+            acc += po[s2] * w;
+        }
+    }
+    const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
+    a.dst[(i * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
 }
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -839,12 +943,14 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     if (b.softcap != 0.0f) b.scale /= b.softcap;
     const int q_f16 = a.S < 64 ? 1 : 0;
     float* part = reinterpret_cast<float*>(ws);
+    const bool fused_merge = p.dec && fuse_merge_ok(p.n_split, p.NQ, a.D, a.Hkv);
     if (p.dec) {
         const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv);
         const int nq = (int)p.NQ, G = (int)p.G, ns = (int)p.n_split;
+        const int fuse = fused_merge ? 1 : 0;
 #define GQ_DEC(DD, NN, UU)                                                                                       \
     hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, false>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
-                       n_head_log2, q_f16, part, PagedKv{})
+                       n_head_log2, q_f16, part, PagedKv{}, fuse)
 #define GQ_DEC_U(DD, NN)                           \
     do {                                           \
         if (p.dec_u == 8) GQ_DEC(DD, NN, 8);       \
@@ -883,7 +989,7 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
                            (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
     }
     int rc = check_hip(hipGetLastError(), "flash_attn_ext launch");
-    if (rc != GQ_OK || p.n_split == 1) return rc;
+    if (rc != GQ_OK || p.n_split == 1 || fused_merge) return rc;
     const dim3 g2((unsigned)p.NQ, (unsigned)a.Hkv);
     if (a.D == 128)
         hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ,
@@ -935,9 +1041,11 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
     float* part = reinterpret_cast<float*>(ws);
     const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)pg.B);
     const int nq = (int)G, ns = (int)p.n_split;
+    const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);
+    const int fuse = fused_merge ? 1 : 0;
 #define GQ_PDEC(DD, NN, UU)                                                                                        \
     hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, true>), gd, dim3(256), 0, s, a, nq, nq, p.rps, ns, 1.0f, 1.0f, 1u, \
-                       1, part, pg)
+                       1, part, pg, fuse)
 #define GQ_PDEC_U(DD, NN)                          \
     do {                                           \
         if (p.u == 8) GQ_PDEC(DD, NN, 8);          \
@@ -960,7 +1068,7 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
 #undef GQ_PDEC_U
 #undef GQ_PDEC
     int rc = check_hip(hipGetLastError(), "flash_attn_paged launch");
-    if (rc != GQ_OK || p.n_split == 1) return rc;
+    if (rc != GQ_OK || p.n_split == 1 || fused_merge) return rc;
     const dim3 g2((unsigned)(pg.B * G), (unsigned)a.Hkv);
     if (a.D == 128)
         hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,

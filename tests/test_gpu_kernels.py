@@ -439,6 +439,35 @@ def test_flash_attn_decode_workspace_and_replays(Hq, Hkv, D, S, pos, ctx):
         assert torch.equal(again, clean[1])
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
+    (32, 32, 128, 1, 1100, 2048),   # 7B decode: 10 splits per kv head
+    (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, 34 splits
+    (15, 5, 64, 1, 700, 1024),      # SmolLM2 shape
+])
+def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx, monkeypatch):
+    """The decode kernel merges its split partials itself (the last workgroup of each
+    kv head, counted on a device counter); that gives the bits of the separate merge
+    launch (GQ_ATTN_SEPARATE_MERGE=1), call after call."""
+    rng = np.random.default_rng(Hq * D + S)
+    n_kv = O.pad_kv_len(pos + S, ctx)
+    kc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
+    vc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
+    mask = to_dev(O.causal_mask_f16(pos, S, n_kv)).view(torch.float16)
+    q = to_dev(rng.standard_normal((Hq, S, D)).astype(np.float32))
+    scale = 1.0 / np.sqrt(D)
+    monkeypatch.delenv("GQ_ATTN_SEPARATE_MERGE", raising=False)
+    fused = [ops.flash_attn_ext(q, kc, vc, mask, scale) for _ in range(4)]
+    monkeypatch.setenv("GQ_ATTN_SEPARATE_MERGE", "1")
+    sep = ops.flash_attn_ext(q, kc, vc, mask, scale)
+    monkeypatch.delenv("GQ_ATTN_SEPARATE_MERGE")
+    for f in fused:
+        assert torch.equal(f, sep)
+    exact = O.flash_attn_ext_f16(q.cpu().numpy(), kc.view(torch.int16).cpu().numpy().view(np.uint16),
+                                 vc.view(torch.int16).cpu().numpy().view(np.uint16), n_kv,
+                                 mask.view(torch.int16).cpu().numpy().view(np.uint16), mode=1)
+    assert mar(fused[0].cpu().numpy(), exact) < 1e-3
+
+
 def test_flash_attn_padding_and_gqa_invariants():
     rng = np.random.default_rng(21)
     Hq, Hkv, D, ctx, pos = 6, 2, 64, 1024, 300

@@ -17,6 +17,7 @@
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -116,6 +117,14 @@ def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
         assert _mar(out[b], ref[0]) < 2e-6, b
     print(f"paged attention max-abs-rel vs exact {worst:.2e}")
     assert worst < 1e-5
+    # the in-kernel split merge gives the bits of the separate merge launch
+    os.environ["GQ_ATTN_SEPARATE_MERGE"] = "1"
+    try:
+        sep = ops.flash_attn_paged(t(q), t(k_pool), t(v_pool), t(table), t(np.array(lens, np.int32)), P, max(lens),
+                                   scale).cpu().numpy()
+    finally:
+        del os.environ["GQ_ATTN_SEPARATE_MERGE"]
+    assert np.array_equal(sep, out, equal_nan=True)
 
 
 def test_paged_step_inputs_advance_and_copy():
