@@ -263,7 +263,7 @@ __device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, flo
     dst[(int64_t)m * ldd + row] = v;
 }
 
-template <int QT, int M, bool XVEC, int PF, int KS>
+template <int QT, int M, bool XVEC, int PF, int KS, int XPT>
 __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__ W, int64_t N,
                                                      int64_t row_bytes, int G, ActSrc act, float* dst,
                                                      int64_t ldd, GemvFuse fz) {
@@ -272,6 +272,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     constexpr int SEG = LPR * CPG;       // chunks of one row per step
     constexpr int XPMAX = 6;             // activation passes held in registers (K <= 12288 at M = 1)
     constexpr int XAMAX = 2;             // of which can carry a fused ADD operand
+    // XPT > 0: the launch has exactly XPT activation passes (M = 1), so the prologue's
+    // passes are straight-line code the compiler can interleave
+    static_assert(XPT == 0 || (M == 1 && XPT <= XPMAX), "exact pass count only for one row");
+    constexpr int XPN = XPT ? XPT : XPMAX;
     constexpr int RG = WAVES / KS;       // row groups (of RPW rows) per workgroup tile
     constexpr int ROWS = RG * RPW;       // rows per workgroup tile
     constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any matrix: load returns 0, no fetch
@@ -289,7 +293,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     const int rsub = lane / LPR;
     const int gsub = lane % LPR;
     const int nb = G * 8;
-    const int XP = (nb * 4 + 255) / 256;
+    const int XP = XPT ? XPT : (nb * 4 + 255) / 256;
 
     // wave -> (row group, K part); K parts are whole steps of LPR groups so every
     // step stays a full 64-group slice (a part may be empty: it then runs one
@@ -318,8 +322,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     const bool xpre = M * XP <= XPMAX && (!act.d || M * XP <= XAMAX);
     if (xpre) {
 #pragma unroll
-        for (int p = 0; p < XPMAX; ++p) {
-            if (p < M * XP) {
+        for (int p = 0; p < XPN; ++p) {
+            if (XPT || p < M * XP) {
                 const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
                 load8<XVEC>(act.x + (int64_t)m * act.xs + (int64_t)t * 8, (t >> 2) < nb, xr[p]);
                 if (p < XAMAX && act.d)
@@ -391,7 +395,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         if (act.d) {  // ADD fused in front: x + d, stored once for the nodes that read the sum
 #pragma unroll
             for (int p = 0; p < XAMAX; ++p) {
-                if (p < M * XP) {
+                if (p < XPN && (XPT || p < M * XP)) {
                     const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
 #pragma unroll
                     for (int i = 0; i < 8; ++i) xr[p][i] = xr[p][i] + ar[p][i];
@@ -404,14 +408,14 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             for (int m = 0; m < M; ++m) {
                 double sq = 0.0;
 #pragma unroll
-                for (int p = 0; p < XPMAX; ++p)
-                    if (p < M * XP && p / XP == m) sq = sumsq8(xr[p], sq);
+                for (int p = 0; p < XPN; ++p)
+                    if ((XPT || p < M * XP) && p / XP == m) sq = sumsq8(xr[p], sq);
                 scale[m] = rms_scale(block_sum_d(sq, red_d), (int64_t)G * 256, fz.eps);
             }
         }
 #pragma unroll
-        for (int p = 0; p < XPMAX; ++p) {
-            if (p < M * XP) {  // uniform across the workgroup
+        for (int p = 0; p < XPN; ++p) {
+            if (XPT || p < M * XP) {  // uniform across the workgroup
                 const int m = p / XP, t = (p - m * XP) * 256 + (int)threadIdx.x;
                 const int b = t >> 2, part = t & 3;
 #pragma unroll
@@ -658,12 +662,12 @@ int gemv_ks_override() {
     return v;
 }
 
-template <int QT, int M, bool XVEC, int PF, int KS>
+template <int QT, int M, bool XVEC, int PF, int KS, int XPT>
 int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s, size_t lds, int resident) {
     const int G = (int)(K / 256);
     const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
-    auto* fn = &k_gemv_grp<QT, M, XVEC, PF, KS>;
+    auto* fn = &k_gemv_grp<QT, M, XVEC, PF, KS, XPT>;
     static size_t allowed = 0;
     int rc = allow_big_lds(fn, allowed, lds);
     if (rc) return rc;
@@ -673,7 +677,7 @@ int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
     return check_hip(hipGetLastError(), "gemv launch");
 }
 
-template <int QT, int M, bool XVEC, int PF>
+template <int QT, int M, bool XVEC, int PF, int XPT>
 int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
     const int G = (int)(K / 256);
@@ -681,7 +685,7 @@ int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
     // residency is the same for every KS (same registers and LDS)
     int resident = 0;
-    int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1>, lds, resident);
+    int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1, XPT>, lds, resident);
     if (rc) return rc;
     // split K over the waves of a workgroup (whole steps per wave) only when
     // the row tiles leave most CUs without a workgroup (measured: splitting a
@@ -690,25 +694,43 @@ int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
     const int J = (G + LPR - 1) / LPR;
     const int ks_force = gemv_ks_override();
     if (ks_force == 1 || (ks_force == 2 && J >= 2) || (ks_force == 4 && J >= 2)) {
-        if (ks_force == 1) return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-        if (ks_force == 2) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-        return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+        if (ks_force == 1) return launch_grp_ks<QT, M, XVEC, PF, 1, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+        if (ks_force == 2) return launch_grp_ks<QT, M, XVEC, PF, 2, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+        return launch_grp_ks<QT, M, XVEC, PF, 4, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
     }
     if (4 * t1 >= resident || J < 2)
-        return launch_grp_ks<QT, M, XVEC, PF, 1>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-    if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-    return launch_grp_ks<QT, M, XVEC, PF, 4>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+        return launch_grp_ks<QT, M, XVEC, PF, 1, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+    if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
+    return launch_grp_ks<QT, M, XVEC, PF, 4, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
 }
 
 // Q4_0 keeps two steps of weight loads in flight per wave
+template <int QT, int M, bool XVEC, int XPT>
+int launch_grp_x(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
+                 float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
+    if constexpr (QT == GQ_TYPE_Q8_0) {
+        return launch_grp_pf<QT, M, XVEC, 1, XPT>(W, N, K, act, dst, ldd, fz, s);
+    } else {
+        return launch_grp_pf<QT, M, XVEC, 2, XPT>(W, N, K, act, dst, ldd, fz, s);
+    }
+}
+
+// one-row launches with 16-byte aligned activations get the instance with their exact
+// number of prologue passes (K = 1536, 2560-4096, 8960-10240, 10496-12288: the
+// configs' shapes); the rest the generic one
 template <int QT, int M, bool XVEC>
 int launch_grp(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s) {
-    if constexpr (QT == GQ_TYPE_Q8_0) {
-        return launch_grp_pf<QT, M, XVEC, 1>(W, N, K, act, dst, ldd, fz, s);
-    } else {
-        return launch_grp_pf<QT, M, XVEC, 2>(W, N, K, act, dst, ldd, fz, s);
+    if constexpr (M == 1 && XVEC) {
+        switch (cdiv(K / QK * 4, 256)) {
+            case 1: return launch_grp_x<QT, M, XVEC, 1>(W, N, K, act, dst, ldd, fz, s);
+            case 2: return launch_grp_x<QT, M, XVEC, 2>(W, N, K, act, dst, ldd, fz, s);
+            case 5: return launch_grp_x<QT, M, XVEC, 5>(W, N, K, act, dst, ldd, fz, s);
+            case 6: return launch_grp_x<QT, M, XVEC, 6>(W, N, K, act, dst, ldd, fz, s);
+            default: break;
+        }
     }
+    return launch_grp_x<QT, M, XVEC, 0>(W, N, K, act, dst, ldd, fz, s);
 }
 
 template <int QT, int M, bool XVEC>
