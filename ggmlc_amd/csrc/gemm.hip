@@ -280,12 +280,16 @@ int num_cus() {
     return ncu;
 }
 
-// 128-token tiles unless they leave CUs without a workgroup (small N): then 64
+// Tile height: 128 tokens for prompt-sized M on weights of >= 16 row tiles (the grid is
+// then filled by splitting K, below); otherwise 128 unless it leaves CUs without a
+// workgroup, then 64. (Measured at M = 512, Q4_0: 4096-row o and down projections run
+// 14% and 32% faster as 128-token tiles split 4 ways than as unsplit 64-token tiles.)
 int gemm_bm(int64_t N, int64_t M) {
     if (const char* e = getenv("GQ_GEMM_BM")) {  // tuning measurements
         const int v = atoi(e);
         if (v == 64 || v == 128) return v;
     }
+    if (M > 64 && cdiv(N, BN) >= 16) return 128;
     return cdiv(N, BN) * cdiv(M, 128) < num_cus() ? 64 : 128;
 }
 
