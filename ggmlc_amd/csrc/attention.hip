@@ -487,29 +487,33 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
     // staging: the block's 64 rows x D halves of K and of V in 16-byte pieces
     constexpr int PPR = D / 8;                 // pieces per row
     constexpr int NPC = BKV * PPR / 256;       // pieces per thread per matrix (2 or 4)
+    // thread -> piece column pc of NPC consecutive keys (each wave instruction reads
+    // 4 or 8 whole rows), so V is transposed with one NPC-key write per dim
+    const int ppc = tid % PPR, pr0 = NPC * (tid / PPR);
     u32x4 kreg[NPC], vreg[NPC];
     auto fetch = [&](int64_t c0) {
 #pragma unroll
         for (int u = 0; u < NPC; ++u) {
-            const int idx = tid + 256 * u, r = idx / PPR, pc = idx % PPR;
-            const int64_t row = c0 + r;
-            const uint32_t ko = row < a.n_kv ? (uint32_t)(row * a.knb1 + pc * 16) : 0x80000000u;
-            const uint32_t vo = row < a.n_kv ? (uint32_t)(row * a.vnb1 + pc * 16) : 0x80000000u;
+            const int64_t row = c0 + pr0 + u;
+            const uint32_t ko = row < a.n_kv ? (uint32_t)(row * a.knb1 + ppc * 16) : 0x80000000u;
+            const uint32_t vo = row < a.n_kv ? (uint32_t)(row * a.vnb1 + ppc * 16) : 0x80000000u;
             kreg[u] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
             vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
         }
     };
     auto park = [&]() {
 #pragma unroll
-        for (int u = 0; u < NPC; ++u) {
-            const int idx = tid + 256 * u, r = idx / PPR, pc = idx % PPR;
-            *reinterpret_cast<u32x4*>(&sK[r * LDK + pc * 8]) = kreg[u];
-            const uint32_t w4[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+        for (int u = 0; u < NPC; ++u) *reinterpret_cast<u32x4*>(&sK[(pr0 + u) * LDK + ppc * 8]) = kreg[u];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                uint16_t lo16 = (uint16_t)(w4[e] & 0xffff), hi16 = (uint16_t)(w4[e] >> 16);
-                __builtin_memcpy(&sVT[(pc * 8 + 2 * e) * LDV + r], &lo16, 2);
-                __builtin_memcpy(&sVT[(pc * 8 + 2 * e + 1) * LDV + r], &hi16, 2);
+        for (int e = 0; e < 8; ++e) {
+            uint32_t hv[NPC];
+#pragma unroll
+            for (int u = 0; u < NPC; ++u) hv[u] = (vreg[u][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            _Float16* dst = &sVT[(ppc * 8 + e) * LDV + pr0];
+            if constexpr (NPC == 4) {
+                *reinterpret_cast<uint2*>(dst) = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
+            } else {
+                *reinterpret_cast<uint32_t*>(dst) = hv[0] | (hv[1] << 16);
             }
         }
     };
