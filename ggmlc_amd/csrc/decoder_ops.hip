@@ -92,48 +92,70 @@ __global__ __launch_bounds__(256) void k_rope(const float* __restrict__ x, int64
     for (int64_t j = n_dims + threadIdx.x; j < ne0; j += blockDim.x) yr[j] = xr[j];
 }
 
-// ROPE(q), ROPE(k), SET_ROWS(k_cache, k), SET_ROWS(v_cache, v) in one launch: block
-// (token i, head h) with h < Hq a query head, then Hkv key heads, then Hkv value heads.
-__global__ __launch_bounds__(64) void k_rope_kv(RopeKvArgs a) {
+// ROPE(q), ROPE(k), SET_ROWS(k_cache, k), SET_ROWS(v_cache, v) in one launch: one
+// workgroup per token; the token's (cos, sin) pairs are computed once into LDS (the
+// rope_cs values every rotating kernel uses) and applied to all its q and k heads, then
+// its v heads are copied. Tokens whose cache row is out of range write no k or v and
+// count 2 * Hkv (one per head).
+__global__ __launch_bounds__(256) void k_rope_kv(RopeKvArgs a) {
+    extern __shared__ float2 s_cs[];
     const int64_t i = blockIdx.x;
-    const int64_t h = blockIdx.y;
     const float p = (float)a.pos[i];
     const int half = a.n_dims / 2;
-    if (h < a.Hq) {
-        const float* xr = reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1));
-        float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1);
-        for (int j = threadIdx.x; j < half; j += blockDim.x) {
-            const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
-            float y0, y1;
-            rope_pair(p, j, a.theta_scale, a.freq_scale, a.attn_factor, xr[i0], xr[i1], y0, y1);
+    for (int j = threadIdx.x; j < half; j += blockDim.x) {
+        float c, sn;
+        rope_cs(p, j, a.theta_scale, a.freq_scale, a.attn_factor, c, sn);
+        s_cs[j] = make_float2(c, sn);
+    }
+    __syncthreads();
+    const int64_t row = a.idx[i];
+    const bool bad = row < 0 || row >= a.rows;
+    if (bad && threadIdx.x == 0 && a.n_bad) atomicAdd(a.n_bad, (int)(2 * a.Hkv));
+    // rotated pairs: q heads, then (valid row) k heads
+    const int64_t nq = a.Hq * half, nk = bad ? 0 : a.Hkv * half;
+    for (int64_t e = threadIdx.x; e < nq + nk; e += blockDim.x) {
+        const bool isq = e < nq;
+        const int64_t ee = isq ? e : e - nq;
+        const int64_t h = ee / half;
+        const int j = (int)(ee - h * half);
+        const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
+        const float2 cs = s_cs[j];
+        float y0, y1;
+        if (isq) {
+            const float* xr = reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1));
+            float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1);
+            rope_rotate(cs.x, cs.y, xr[i0], xr[i1], y0, y1);
             yr[i0] = y0;
             yr[i1] = y1;
-        }
-        for (int64_t j = a.n_dims + threadIdx.x; j < a.hd; j += blockDim.x) yr[j] = xr[j];
-        return;
-    }
-    const bool is_k = h < a.Hq + a.Hkv;
-    const int64_t kh = is_k ? h - a.Hq : h - a.Hq - a.Hkv;
-    const int64_t row = a.idx[i];
-    if (row < 0 || row >= a.rows) {
-        if (threadIdx.x == 0 && a.n_bad) atomicAdd(a.n_bad, 1);
-        return;
-    }
-    if (is_k) {
-        const float* xr = reinterpret_cast<const float*>(at(a.k, i * a.knb2 + kh * a.knb1));
-        uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + kh * a.kcnb2);
-        for (int j = threadIdx.x; j < half; j += blockDim.x) {
-            const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
-            float y0, y1;
-            rope_pair(p, j, a.theta_scale, a.freq_scale, a.attn_factor, xr[i0], xr[i1], y0, y1);
+        } else {
+            const float* xr = reinterpret_cast<const float*>(at(a.k, i * a.knb2 + h * a.knb1));
+            uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + h * a.kcnb2);
+            rope_rotate(cs.x, cs.y, xr[i0], xr[i1], y0, y1);
             yr[i0] = f2h(y0);
             yr[i1] = f2h(y1);
         }
-        for (int64_t j = a.n_dims + threadIdx.x; j < a.hd; j += blockDim.x) yr[j] = f2h(xr[j]);
-    } else {
-        const float* xr = reinterpret_cast<const float*>(at(a.v, i * a.vnb2 + kh * a.vnb1));
-        uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.vc) + row * a.vcnb1 + kh * a.vcnb2);
-        for (int64_t j = threadIdx.x; j < a.hd; j += blockDim.x) yr[j] = f2h(xr[j]);
+    }
+    // dims past n_dims pass through (q fp32, k fp16)
+    const int64_t tail = a.hd - a.n_dims;
+    if (tail > 0) {
+        for (int64_t e = threadIdx.x; e < (a.Hq + (bad ? 0 : a.Hkv)) * tail; e += blockDim.x) {
+            const int64_t h = e / tail, d = a.n_dims + (e - h * tail);
+            if (h < a.Hq) {
+                const float* xr = reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1));
+                reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1)[d] = xr[d];
+            } else {
+                const int64_t kh = h - a.Hq;
+                const float* xr = reinterpret_cast<const float*>(at(a.k, i * a.knb2 + kh * a.knb1));
+                reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + kh * a.kcnb2)[d] =
+                    f2h(xr[d]);
+            }
+        }
+    }
+    if (bad) return;
+    for (int64_t e = threadIdx.x; e < a.Hkv * a.hd; e += blockDim.x) {
+        const int64_t h = e / a.hd, d = e - h * a.hd;
+        const float* xr = reinterpret_cast<const float*>(at(a.v, i * a.vnb2 + h * a.vnb1));
+        reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.vc) + row * a.vcnb1 + h * a.vcnb2)[d] = f2h(xr[d]);
     }
 }
 
@@ -278,7 +300,7 @@ int rope_kv(const RopeKvArgs& a, float freq_base, hipStream_t s) {
     if (a.s == 0) return GQ_OK;
     RopeKvArgs b = a;
     b.theta_scale = powf(freq_base, -2.0f / a.n_dims);
-    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)a.s, (unsigned)(a.Hq + 2 * a.Hkv)), dim3(64), 0, s, b);
+    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)a.s), dim3(256), (size_t)(a.n_dims / 2) * sizeof(float2), s, b);
     return check_hip(hipGetLastError(), "rope_kv launch");
 }
 
