@@ -99,18 +99,21 @@ int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride
 // chunk c in registers (K <= PREP_MAX_K).
 constexpr int PREP_CH = PREP_MAX_K / 2048;
 
-template <bool VEC>
+// CH > 0: the launch has exactly CH chunks (straight-line code the compiler can
+// interleave); CH = 0: up to PREP_CH chunks, the ones past K skipped
+template <bool VEC, int CH>
 __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restrict__ y, int64_t y_stride) {
+    constexpr int NC = CH ? CH : PREP_CH;
     __shared__ double red[4];
     const int64_t m = blockIdx.x;
     const int nb = (int)(a.K / QK);
     const float* xr = a.x + m * a.xs;
-    float v[PREP_CH][8];
+    float v[NC][8];
 #pragma unroll
-    for (int c = 0; c < PREP_CH; ++c) {
+    for (int c = 0; c < NC; ++c) {
         const int t = c * 256 + (int)threadIdx.x;  // 8-element piece
         const bool valid = (t >> 2) < nb;
-        if (c * 2048 >= a.K) {
+        if (!CH && c * 2048 >= a.K) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[c][i] = 0.0f;
             continue;
@@ -139,17 +142,17 @@ __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restric
     if (a.rms) {
         double sq = 0.0;
 #pragma unroll
-        for (int c = 0; c < PREP_CH; ++c)
-            if (c * 2048 < a.K) sq = sumsq8(v[c], sq);
+        for (int c = 0; c < NC; ++c)
+            if (CH || c * 2048 < a.K) sq = sumsq8(v[c], sq);
         const float sc = rms_scale(block_sum_d(sq, red), a.K, a.eps);
 #pragma unroll
-        for (int c = 0; c < PREP_CH; ++c)
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] * sc;
     }
 #pragma unroll
-    for (int c = 0; c < PREP_CH; ++c) {
-        if (c * 2048 >= a.K) break;  // uniform: whole chunks past K
+    for (int c = 0; c < NC; ++c) {
+        if (!CH && c * 2048 >= a.K) break;  // uniform: whole chunks past K
         const int t = c * 256 + (int)threadIdx.x;
         int q[8];
         uint16_t dh;
@@ -174,10 +177,18 @@ int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStre
     if (a.K > PREP_MAX_K || a.K % QK) return fail(GQ_ERR_UNSUPPORTED, "act_prep: K too large");
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.xs % 4 == 0) &&
                      (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) && a.K % 4 == 0;
-    if (vec)
-        hipLaunchKernelGGL(k_act_prep<true>, dim3((unsigned)M), dim3(256), 0, s, a, y, y_stride);
-    else
-        hipLaunchKernelGGL(k_act_prep<false>, dim3((unsigned)M), dim3(256), 0, s, a, y, y_stride);
+    const dim3 g((unsigned)M);
+    if (vec) {  // the configs' K: 960 and 1536 (1 chunk), 2560 and 4096 (2), 8960 (5), 11008 (6)
+        switch (cdiv(a.K, 2048)) {
+            case 1: hipLaunchKernelGGL((k_act_prep<true, 1>), g, dim3(256), 0, s, a, y, y_stride); break;
+            case 2: hipLaunchKernelGGL((k_act_prep<true, 2>), g, dim3(256), 0, s, a, y, y_stride); break;
+            case 5: hipLaunchKernelGGL((k_act_prep<true, 5>), g, dim3(256), 0, s, a, y, y_stride); break;
+            case 6: hipLaunchKernelGGL((k_act_prep<true, 6>), g, dim3(256), 0, s, a, y, y_stride); break;
+            default: hipLaunchKernelGGL((k_act_prep<true, 0>), g, dim3(256), 0, s, a, y, y_stride); break;
+        }
+    } else {
+        hipLaunchKernelGGL((k_act_prep<false, 0>), g, dim3(256), 0, s, a, y, y_stride);
+    }
     return check_hip(hipGetLastError(), "act_prep launch");
 }
 
