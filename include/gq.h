@@ -187,7 +187,9 @@ int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n
  *   dst  : F32 ne = [D, Hq, S, 1] contiguous (the op's permuted output)
  * D in {64, 128}. max_bias and logit_softcap follow ops.cpp:8532-8768. Query
  * rounding follows the CPU path taken for that S (fp16 for S < 64, fp32 for
- * S >= 64); accumulation is fp32. */
+ * S >= 64); accumulation is fp32. Decode launches (few query vectors per kv head)
+ * merge their KV splits inside the kernel through per-device arrival counters, so
+ * two of them must not run concurrently on one device (issue them on one stream). */
 size_t gq_flash_attn_ext_workspace_size(const gq_tensor* q, const gq_tensor* k);
 int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v,
                       const gq_tensor* mask, float scale, float max_bias, float logit_softcap,
@@ -294,7 +296,8 @@ int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream);
  *   max_len  : an upper bound of every seq_len[b] (sizes the launch)
  *   dst      : F32 [D, Hq, B] contiguous.  D in {64, 128}, Hq / Hkv <= 8.
  * Equal to the reference's decode step of sequence b with the causal mask of its
- * position (columns past it weigh exactly 0). */
+ * position (columns past it weigh exactly 0). Shares gq_flash_attn_ext's per-device
+ * split counters: no two decode attention launches concurrently on one device. */
 size_t gq_flash_attn_paged_workspace_size(const gq_tensor* q, const gq_tensor* k_pool, int64_t max_len,
                                           int64_t page_size);
 int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
