@@ -700,8 +700,11 @@ int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_te
     const int lp = page_log2(page_size);
     if (lp < 0) return fail(GQ_ERR_INVALID, "flash_attn_paged: page_size must be a power of two >= 64");
     if (D != 64 && D != 128) return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged: head dim must be 64 or 128");
-    if (Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > 8)
-        return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged: needs Hq a multiple of Hkv with at most 8 q heads per kv head");
+    // up to 8 q heads per kv head on any page size, up to 16 with pages of a multiple of 128 rows
+    // (the matrix-core kernel)
+    if (Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > (page_size % 128 == 0 ? 16 : 8))
+        return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged: needs Hq a multiple of Hkv with at most 8 q heads per kv head "
+                                        "(16 with pages of a multiple of 128 rows)");
     if (k_pool->ne[0] != D || v_pool->ne[0] != D || v_pool->ne[1] != rows || v_pool->ne[2] != Hkv ||
         q->ne[3] != 1 || k_pool->ne[3] != 1 || v_pool->ne[3] != 1 || B <= 0 || rows <= 0 || max_len <= 0)
         return fail(GQ_ERR_INVALID, "flash_attn_paged: shape mismatch q " + shape(q) + " k " + shape(k_pool) + " v " +

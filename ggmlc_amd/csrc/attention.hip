@@ -672,6 +672,196 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
         for (int r = 0; r < 4; ++r) op[16 * dt + 4 * g + r] = o[dt][r] * inv;
 }
 
+// Paged batched decode attention on the matrix cores for groups of 5..16 query heads
+// per kv head (v_mfma_f32_16x16x32_f16, operand layouts as in k_attn_mma). A workgroup
+// owns (split of 128 rows, kv head, sequence); wave w takes the split's keys 32 w .. +31:
+//   S^T (16 keys x 16 queries, two tiles) = K . Q^T with K read straight into the MFMA
+//   operand (16 bytes of one key row per lane) and Q rounded to fp16 (the decode path's
+//   rounding); s = S * scale, keys at or past the sequence's length weigh 0;
+//   O^T += V^T . P^T with P = p_hi + p_lo (fp32-level weights) and V transposed into the
+//   wave's LDS slice (one packed write of 8 or 4 keys per dim).
+// The 4 waves' (m, l, O) merge in LDS into the split's partial, which k_attn_merge
+// combines across splits. Rows past a sequence's length (and missing pages) are never
+// read: their loads use out-of-range offsets.
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_split, float* __restrict__ part,
+                                                      PagedKv pg) {
+    constexpr int KS = D / 32;         // k-steps of the QK product
+    constexpr int DT = D / 16;         // 16-dim tiles of O^T
+    constexpr int KW = 32;             // keys per wave
+    constexpr int LDV = KW + 8;        // halves per V^T row
+    constexpr int PPR = D / 8;         // 16-byte pieces per V row
+    constexpr int KPL = KW * PPR / 64; // V keys per lane (8 or 4)
+    constexpr int SV = D * LDV;        // halves of one wave's V^T slice
+    __shared__ __align__(16) _Float16 sVT[4 * SV];
+    __shared__ float sM[4][16], sL[4][16];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int split = blockIdx.x, hk = blockIdx.y, seq = blockIdx.z;
+    const int Hkv = (int)a.Hkv;
+    const int64_t r_begin = (int64_t)split * 128;
+    const int64_t len = pg.len[seq];
+    const int64_t pi = r_begin >> pg.log2p;
+    const int page = (r_begin < len && pi < pg.tstride) ? pg.table[seq * pg.tstride + pi] : -1;
+    const int64_t r_len = page < 0 ? 0 : len;  // logical rows below r_len are read
+    const int64_t prow0 = ((int64_t)(page < 0 ? 0 : page) << pg.log2p) + (r_begin & ((1 << pg.log2p) - 1));
+    const int64_t kb0 = r_begin + wave * KW;   // this wave's first key (logical row)
+
+    auto rsrc = [&](const void* p, int64_t nb2, int64_t nb1) {
+        const uint64_t base = reinterpret_cast<uint64_t>(p) + (uint64_t)(hk * nb2);
+        const int64_t bytes = a.n_kv * nb1;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+        const uint32_t n = (uint32_t)(bytes > 0x7fffffff ? 0x7fffffff : bytes);
+        return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                                 (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t krs = rsrc(a.k, a.knb2, a.knb1), vrs = rsrc(a.v, a.vnb2, a.vnb1);
+
+    // K operands of both key tiles and this lane's V pieces, all requested at once
+    u32x4 kw[2][KS];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int64_t r = kb0 + 16 * t + j;
+        const bool in = r < r_len;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const uint32_t off = in ? (uint32_t)((prow0 + r - r_begin) * a.knb1 + (32 * ks + 8 * g) * 2) : 0x80000000u;
+            kw[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)off, 0, 0);
+        }
+    }
+    const int pc = lane % PPR, kg = lane / PPR;
+    u32x4 vreg[KPL];
+#pragma unroll
+    for (int u = 0; u < KPL; ++u) {
+        const int64_t r = kb0 + kg * KPL + u;
+        const uint32_t off = r < r_len ? (uint32_t)((prow0 + r - r_begin) * a.vnb1 + pc * 16) : 0x80000000u;
+        vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)off, 0, 0);
+    }
+
+    // Q^T operand: query j (lanes past G hold zeros), dims 32 ks + 8 g .. +7, fp16
+    const bool qok = j < G;
+    half8_t qh[KS];
+    {
+        const int64_t h = (int64_t)hk * G + (qok ? j : 0);
+        const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + seq * a.qnb1 +
+                                                         h * a.qnb2);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qh[ks][e] = (_Float16)(qok ? qp[32 * ks + 8 * g + e] : 0.0f);
+    }
+
+    // V^T into this wave's slice: dim pc * 8 + e, keys kg * KPL .. + KPL - 1 in one write
+    _Float16* vt = sVT + wave * SV;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint32_t hv[KPL];
+#pragma unroll
+        for (int u = 0; u < KPL; ++u) hv[u] = (vreg[u][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        _Float16* dst = vt + (pc * 8 + e) * LDV + kg * KPL;
+        if constexpr (KPL == 8) {
+            *reinterpret_cast<uint4*>(dst) =
+                make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+        } else {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
+        }
+    }
+
+    // S^T tiles: keys 16 t + 4 g + r of this wave x query j
+    float sv[2][4];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        float4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            half8_t kf;
+            __builtin_memcpy(&kf, &kw[t][ks], 16);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], c, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool ok = qok && kb0 + 16 * t + 4 * g + r < r_len;
+            sv[t][r] = ok ? c[r] * a.scale : -INFINITY;
+            bmax = fmaxf(bmax, sv[t][r]);
+        }
+    }
+    {
+        const Pair p16 = xchg_16(bmax);
+        bmax = fmaxf(p16.a, p16.b);
+        const Pair p32 = xchg_32(bmax);
+        bmax = fmaxf(p32.a, p32.b);
+    }
+    const float m = bmax;
+    // P^T operand (keys 4 g .. +3, 16 + 4 g .. +3), p = p_hi + p_lo in fp16
+    half8_t pb, pl;
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float pv = m == -INFINITY ? 0.0f : __expf(sv[t][r] - m);
+            const _Float16 ph = (_Float16)pv;
+            psum += pv;
+            pb[4 * t + r] = ph;
+            pl[4 * t + r] = (_Float16)(pv - (float)ph);
+        }
+    {
+        const Pair p16 = xchg_16(psum);
+        psum = p16.a + p16.b;
+        const Pair p32 = xchg_32(psum);
+        psum = p32.a + p32.b;
+    }
+    wave_lds_sync();  // the wave's V^T slice is written
+    float4_t o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+        const _Float16* vr = vt + (16 * dt + j) * LDV + 4 * g;
+        half8_t vf;
+        __builtin_memcpy(&vf, vr, 8);
+        __builtin_memcpy(reinterpret_cast<_Float16*>(&vf) + 4, vr + 16, 8);
+        float4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pb, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, c, 0, 0, 0);
+        o[dt] = c;
+    }
+
+    // merge the 4 waves (the V^T slices are reused as sO[wave][dim][query])
+    __syncthreads();
+    float* sO = reinterpret_cast<float*>(sVT);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sO[(wave * D + 16 * dt + 4 * g + r) * 16 + j] = o[dt][r];
+    if (g == 0) sM[wave][j] = m, sL[wave][j] = psum;
+    __syncthreads();
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int u = idx / D, d = idx % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sM[w][u]);
+        float L = 0.0f, acc = 0.0f;
+        if (mx != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = sM[w][u] == -INFINITY ? 0.0f : __expf(sM[w][u] - mx);
+                L += sL[w][u] * f;
+                acc += sO[(w * D + d) * 16 + u] * f;
+            }
+        }
+        const int64_t h = (int64_t)hk * G + u;
+        if (n_split == 1) {
+            a.dst[(seq * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
+        } else {
+            float* pp = part + (((int64_t)split * Hkv + hk) * pg.B * G + (int64_t)seq * G + u) * (D + 2);
+            pp[2 + d] = acc;
+            if (d == 0) pp[0] = mx, pp[1] = L;
+        }
+    }
+}
+
 // GQ_ATTN_NO_MMA=1 keeps prefill attention on the VALU kernel (comparison runs)
 bool mma_disabled() {
     static int v = -1;
@@ -1007,15 +1197,25 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
 namespace {
 
 struct PagedPlan {
-    int u;
+    int u;  // rows per lane stream of k_attn_dec; -1: k_attn_dec_mma
     int64_t rps, n_split;
 };
+
+// groups of 5..16 query heads per kv head go to the matrix-core kernel (pages of a
+// multiple of 128 rows); GQ_ATTN_PAGED_VALU=1 keeps them on k_attn_dec (comparison runs)
+bool paged_mma(int64_t D, int64_t G, int64_t page) {
+    const char* e = getenv("GQ_ATTN_PAGED_VALU");
+    if (e && atoi(e) == 1 && G <= 8) return false;  // k_attn_dec serves at most 8
+    return (D == 64 || D == 128) && G > 4 && G <= 16 && page % 128 == 0;
+}
 
 // the largest rows-per-lane-stream U (8, 4, 2; at most 4 for more than 4 query vectors)
 // whose split (U x rows per iteration) divides the page and still gives >= 256 workgroups
 PagedPlan paged_plan(int64_t D, int64_t B, int64_t G, int64_t Hkv, int64_t max_len, int64_t page) {
     const int64_t rows_it = 4 * (64 / (D / 8));
     PagedPlan p{0, 0, 0};
+    if (paged_mma(D, G, page))  // matrix-core kernel: splits of 128 rows (u = 0 marks it)
+        return PagedPlan{-1, 128, cdiv(max_len < 1 ? 1 : max_len, 128)};
     for (int u = G > 4 ? 4 : 8; u >= 2; u >>= 1) {  // a smaller U replaces a larger one: more workgroups
         const int64_t rps = u * rows_it;
         if (page % rps) continue;
@@ -1045,6 +1245,22 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
     float* part = reinterpret_cast<float*>(ws);
     const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)pg.B);
     const int nq = (int)G, ns = (int)p.n_split;
+    if (p.u < 0) {
+        if (a.D == 128)
+            hipLaunchKernelGGL(k_attn_dec_mma<128>, gd, dim3(256), 0, s, a, nq, ns, part, pg);
+        else
+            hipLaunchKernelGGL(k_attn_dec_mma<64>, gd, dim3(256), 0, s, a, nq, ns, part, pg);
+        int rc = check_hip(hipGetLastError(), "flash_attn_paged (mfma) launch");
+        if (rc != GQ_OK || p.n_split == 1) return rc;
+        const dim3 g2((unsigned)(pg.B * G), (unsigned)a.Hkv);
+        if (a.D == 128)
+            hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
+                               a.Hq, a.dst);
+        else
+            hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
+                               a.Hq, a.dst);
+        return check_hip(hipGetLastError(), "flash_attn_paged merge launch");
+    }
     const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);
     const int fuse = fused_merge ? 1 : 0;
 #define GQ_PDEC(DD, NN, UU)                                                                                        \

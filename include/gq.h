@@ -294,7 +294,8 @@ int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream);
  *   k/v_pool : F16 [D, rows, Hkv, 1], one head of a pool below 2 GiB
  *   page_table, seq_len : device I32 (a negative page id reads nothing)
  *   max_len  : an upper bound of every seq_len[b] (sizes the launch)
- *   dst      : F32 [D, Hq, B] contiguous.  D in {64, 128}, Hq / Hkv <= 8.
+ *   dst      : F32 [D, Hq, B] contiguous.  D in {64, 128}, Hq / Hkv <= 8 (<= 16 when
+ *              page_size is a multiple of 128; groups of 5-16 run on the matrix cores).
  * Equal to the reference's decode step of sequence b with the causal mask of its
  * position (columns past it weigh exactly 0). Shares gq_flash_attn_ext's per-device
  * split counters: no two decode attention launches concurrently on one device. */

@@ -64,6 +64,8 @@ def _init():
     (64, 15, 5, 128, [300, 1, 129, 128, 255]),
     (128, 8, 8, 256, [20]),                      # one split: the output is written directly
     (64, 4, 4, 256, [1000, 999, 513, 17, 256, 2, 700, 64]),
+    (64, 32, 4, 128, [300, 1, 129, 0, 511]),     # 8 query heads per kv head (matrix-core kernel)
+    (128, 16, 1, 256, [1000, 257, 3]),           # 16 per kv head, 256-row pages
 ])
 def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
     import torch
