@@ -61,6 +61,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="decode budget of the CPU sample")
     p.add_argument("--c1-launches", type=int, default=400)
+    p.add_argument("--no-sweep", action="store_true", help="skip the Q8_0 decode GEMV size sweep")
     p.add_argument("--c5-steps", type=int, default=64, help="timed batched decode steps per batch size")
     p.add_argument("--no-c5", action="store_true", help="skip the configs[4] continuous-batching decode")
     p.add_argument("--c5-only", action="store_true", help="run only the configs[4] measurement (profiling)")
@@ -286,6 +287,7 @@ def main() -> int:
     c1_gbs = c1_bytes / (c1_ms * 1e-3) / 1e9
     c1_probe_ms = time_probe_launches([c1[i % 16].data for i in range(Lc)], e0, e1) / Lc
     del gq, c1
+    sweep = [] if args.no_sweep else gemv_sweep_q8_0(dev, ws, e0, e1)
 
     # ---- measured ceilings next to the datasheet peak: the streaming-read probe
     # (the GEMV's 16-byte nontemporal load pattern) and a device copy
@@ -375,6 +377,7 @@ def main() -> int:
             "read_probe_same_size_us": round(c1_probe_ms * 1e3, 3),
             "frac_of_same_size_read": round(c1_probe_ms / c1_ms, 4),
         },
+        "gemv_sweep_q8_0": sweep,
         "measured_read_GBps": round(read_gbs, 1),
         "measured_copy_GBps": round(copy_gbs, 1),
         "wall_s_timed": round(wall, 3),
@@ -464,6 +467,66 @@ def bench_c5(dev, steps: int, batches=(1, 2, 4, 8, 16)) -> dict:
     del bd, w
     torch.cuda.empty_cache()
     return out
+
+
+# (N, K) of the Q8_0 decode GEMV sweep: configs[0], the LLaMA-7B layer and lm_head
+# shapes, and the Qwen2.5-1.5B tied lm_head (248 MB, the largest single weight here)
+SWEEP_SHAPES = ((4096, 4096), (4096, 11008), (12288, 4096), (22016, 4096), (32000, 4096), (151936, 1536))
+
+
+def gemv_sweep_q8_0(dev, ws, e0, e1, launches: int = 96, reps: int = 3) -> list:
+    """Q8_0 GEMV (M = 1) over SWEEP_SHAPES: achieved GB/s (weight + x + y bytes per
+    launch) as a fraction of the HBM peak and of a streaming read of the same buffers.
+    Each shape rotates over enough weight copies (>= 512 MB together) that no launch
+    finds its weight in the 256 MB Infinity Cache; launches run back to back in one
+    graph, as the decode GEMVs of a token do."""
+    import torch
+
+    from ggmlc_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    rows = []
+    for N, K in SWEEP_SHAPES:
+        wbytes = N * (K // 32) * ops.BLOCK_BYTES[ops.Q8_0]
+        ncopy = max(2, min(16, -(-(512 << 20) // wbytes)))
+        ws_ = []
+        for _ in range(ncopy):
+            t = torch.randn((N, K), generator=g, device=dev) * 0.02
+            ws_.append(ops.quantize_weights(t, ops.Q8_0))
+            del t
+        x = torch.randn((1, K), generator=g, device=dev)
+        y = torch.empty((1, N), device=dev)
+
+        def loop():
+            for i in range(launches):
+                ops.mul_mat(ws_[i % ncopy], x, out=y, ws=ws)
+
+        loop()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            loop()
+        gr.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / (reps * launches)
+        nbytes = wbytes + 4 * K + 4 * N
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        probe_ms = time_probe_launches([ws_[i % ncopy].data for i in range(launches)], e0, e1) / launches
+        rows.append({
+            "N": N, "K": K, "bytes_per_launch": nbytes, "weight_copies": ncopy,
+            "us_per_launch": round(ms * 1e3, 3), "achieved_GBps": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "frac_of_same_size_read": round(probe_ms / ms, 4),
+        })
+        log(f"sweep q8_0 N={N} K={K}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+        del gr, ws_
+    return rows
 
 
 def time_probe_launches(bufs, e0, e1, reps: int = 5) -> float:
