@@ -11,14 +11,10 @@ __version__ = "0.1.0"
 
 
 def get_available_devices() -> list[str]:
-    """Devices this runtime can execute on (mirrors ggmlc runtime/runner.py:34-38).
+    """Devices this runtime can execute on (mirrors ggmlc runtime/runner.py:34-38 and
+    executor.cpp:184): the visible GPUs named as the reference names them, "cuda:N".
 
     Only GPUs are listed: the quantized path here has no CPU implementation."""
-    try:
-        import torch
+    from .runner import get_available_devices as _devs
 
-        if torch.cuda.is_available():
-            return [f"gpu:{i}" for i in range(torch.cuda.device_count())]
-    except Exception:  # pragma: no cover - torch import failure
-        pass
-    return []
+    return _devs()

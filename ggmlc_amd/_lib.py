@@ -16,6 +16,7 @@ F32, F16, Q4_0, Q8_0, I32, I64 = 0, 1, 2, 8, 26, 27
 BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
 
 GQ_OK = 0
+GQ_OPT_ATTN_SEPARATE_MERGE = 1
 _ERR_NAMES = {-1: "GQ_ERR_INVALID", -2: "GQ_ERR_UNSUPPORTED", -3: "GQ_ERR_WORKSPACE", -4: "GQ_ERR_DEVICE"}
 
 
@@ -80,6 +81,7 @@ SIGNATURES = {
     "gq_abi_version": (ctypes.c_int, []),
     "gq_last_error": (ctypes.c_char_p, []),
     "gq_init": (ctypes.c_int, []),
+    "gq_set_option": (ctypes.c_int, [ctypes.c_int, _i64]),
     "gq_quantize_row_q8_0": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "gq_quantize_weights": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _i64, _vp]),
     "gq_mul_mat_workspace_size": (ctypes.c_size_t, [_P, _P]),
@@ -89,6 +91,7 @@ SIGNATURES = {
     "gq_set_rows": (ctypes.c_int, [_P, _P, _P, _vp, _vp]),
     "gq_flash_attn_ext_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_flash_attn_ext": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_attn_reset_counters": (ctypes.c_int, [_vp]),
     "gq_soft_max": (ctypes.c_int, [_P, _P, _f32, _f32, _P, _vp]),
     "gq_swiglu": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _vp]),
     "gq_rms_norm": (ctypes.c_int, [_P, _f32, _P, _vp]),

@@ -2,6 +2,7 @@
 // validation against the ggml op contracts, workspace carving and dispatch to
 // the kernels. Validation failures return an error before anything is
 // launched, so a rejected call leaves all device state untouched.
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 
@@ -11,6 +12,9 @@
 namespace gq {
 
 static thread_local std::string g_err;
+static std::atomic<int> g_opt_separate_merge{0};
+
+bool option_attn_separate_merge() { return g_opt_separate_merge.load(std::memory_order_relaxed) != 0; }
 
 void set_error(const std::string& msg) { g_err = msg; }
 
@@ -40,18 +44,6 @@ std::string shape(const gq_tensor* t) {
 bool rows_uniform(const gq_tensor* t) {
     return (t->ne[2] == 1 || t->nb[2] == t->nb[1] * (size_t)t->ne[1]) &&
            (t->ne[3] == 1 || t->nb[3] == t->nb[2] * (size_t)t->ne[2]);
-}
-
-// GEMV up to this many activation rows, MFMA GEMM above
-int gemv_max_m() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("GQ_GEMV_MAX_M");
-        v = e ? atoi(e) : GEMV_MAX_M;
-        if (v < 0) v = 0;
-        if (v > GEMV_MAX_M) v = GEMV_MAX_M;
-    }
-    return v;
 }
 
 struct MulMatPlan {
@@ -87,7 +79,7 @@ int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, M
             return fail(GQ_ERR_INVALID, "mul_mat: dst rows must be uniformly strided: " + shape(dst));
         p.ldd = (int64_t)(dst->nb[1] / 4);
     }
-    p.use_gemv = p.M <= gemv_max_m();
+    p.use_gemv = p.M <= GEMV_MAX_M;  // GEMV up to this many activation rows, MFMA GEMM above
     // the GEMV quantizes the activation in LDS; the GEMM takes it as fp16 from the workspace,
     // followed by the split-K partials when its plan splits K
     const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 2;
@@ -118,6 +110,17 @@ int gq_init(void) {
     if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
         return fail(GQ_ERR_UNSUPPORTED, std::string("libgq is built for gfx950, device is ") + prop.gcnArchName);
     return GQ_OK;
+}
+
+int gq_set_option(int option, int64_t value) {
+    switch (option) {
+        case GQ_OPT_ATTN_SEPARATE_MERGE:
+            if (value != 0 && value != 1) return fail(GQ_ERR_INVALID, "set_option: value must be 0 or 1");
+            g_opt_separate_merge.store((int)value, std::memory_order_relaxed);
+            return GQ_OK;
+        default:
+            return fail(GQ_ERR_INVALID, "set_option: unknown option " + std::to_string(option));
+    }
 }
 
 int gq_quantize_row_q8_0(const float* x, void* y, int64_t k, gq_stream_t stream) {
@@ -404,9 +407,12 @@ size_t gq_flash_attn_ext_workspace_size(const gq_tensor* q, const gq_tensor* k) 
     return attn_workspace_bytes(q->ne[0], q->ne[1], q->ne[2], k->ne[2], k->ne[1]);
 }
 
-int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* mask, float scale,
-                      float max_bias, float logit_softcap, gq_tensor* dst, void* workspace, size_t workspace_bytes,
-                      gq_stream_t stream) {
+}  // extern "C"
+
+namespace {
+// validation of a flash_attn_ext call (the op contract of ggml.c:5402-5437) into kernel arguments
+int attn_args(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* mask, float scale,
+              float max_bias, float logit_softcap, gq_tensor* dst, AttnArgs& a) {
     if (!q || !k || !v || !dst) return fail(GQ_ERR_INVALID, "flash_attn_ext: null tensor");
     if (q->type != GQ_TYPE_F32 || k->type != GQ_TYPE_F16 || v->type != GQ_TYPE_F16 || dst->type != GQ_TYPE_F32)
         return fail(GQ_ERR_UNSUPPORTED, "flash_attn_ext: needs F32 q/dst and F16 k/v");
@@ -421,13 +427,15 @@ int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v
     if (dst->ne[0] != D || dst->ne[1] != Hq || dst->ne[2] != S || dst->nb[0] != 4 || dst->nb[1] != (size_t)D * 4 ||
         dst->nb[2] != (size_t)D * 4 * Hq)
         return fail(GQ_ERR_INVALID, "flash_attn_ext: dst must be contiguous F32 [D, Hq, S]: " + shape(dst));
+    // the kernels address one head's rows through a buffer resource of < 2 GiB
+    if ((double)n_kv * (double)k->nb[1] >= 2147418112.0 || (double)n_kv * (double)v->nb[1] >= 2147418112.0)
+        return fail(GQ_ERR_INVALID, "flash_attn_ext: one K/V head must span less than 2 GiB: k " + shape(k));
     if (mask) {
         if (mask->type != GQ_TYPE_F16 || mask->ne[0] < n_kv || mask->ne[1] < S || mask->nb[0] != 2 ||
             mask->ne[2] != 1 || mask->ne[3] != 1)
             return fail(GQ_ERR_INVALID, "flash_attn_ext: mask must be F16 [>= n_kv, >= S, 1, 1]: " + shape(mask));
     }
     if (max_bias > 0.0f && !mask) return fail(GQ_ERR_INVALID, "flash_attn_ext: max_bias needs a mask");
-    AttnArgs a;
     a.q = static_cast<const float*>(q->data);
     a.D = D;
     a.S = S;
@@ -448,8 +456,22 @@ int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v
     a.max_bias = max_bias;
     a.softcap = logit_softcap;
     a.dst = static_cast<float*>(dst->data);
+    return GQ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* mask, float scale,
+                      float max_bias, float logit_softcap, gq_tensor* dst, void* workspace, size_t workspace_bytes,
+                      gq_stream_t stream) {
+    AttnArgs a;
+    const int rc = attn_args(q, k, v, mask, scale, max_bias, logit_softcap, dst, a);
+    if (rc) return rc;
     return attention(a, workspace, workspace_bytes, (hipStream_t)stream);
 }
+
+int gq_attn_reset_counters(gq_stream_t stream) { return attn_reset_counters((hipStream_t)stream); }
 
 int gq_soft_max(const gq_tensor* a, const gq_tensor* mask, float scale, float max_bias, gq_tensor* dst,
                 gq_stream_t stream) {

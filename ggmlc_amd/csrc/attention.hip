@@ -59,12 +59,11 @@ struct Plan {
 
 // the split merge runs inside the decode kernel when one thread per (query vector,
 // dim) can hold every split's partial in registers and the launch's (sequence, kv
-// head) pairs fit the counters;
-// GQ_ATTN_SEPARATE_MERGE=1 keeps the second launch (comparison runs)
+// head) pairs fit the counters, unless GQ_OPT_ATTN_SEPARATE_MERGE asks for the
+// second launch (comparison runs; the results are the same bits)
 bool fuse_merge_ok(int64_t n_split, int64_t nq, int64_t D, int64_t pairs) {
-    const char* e = getenv("GQ_ATTN_SEPARATE_MERGE");  // read per call: tests switch it
-    const bool off = e && atoi(e) == 1;
-    return !off && n_split > 1 && n_split <= FUSE_MAX_SPLIT && nq * D <= 256 && pairs <= ARRIVE_N;
+    return !option_attn_separate_merge() && n_split > 1 && n_split <= FUSE_MAX_SPLIT && nq * D <= 256 &&
+           pairs <= ARRIVE_N;
 }
 
 Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
@@ -73,24 +72,23 @@ Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     p.NQ = p.G * S;
     p.n_qt = cdiv(p.NQ, QT);
     p.n_chunks = cdiv(n_kv, CH);
-    // (contexts past MAX_SPLIT splits of the largest rows-per-split take the tiled kernel)
-    p.dec = p.NQ <= DEC_MAX_NQ && (D == 64 || D == 128) && n_kv <= (int64_t)MAX_SPLIT * 8 * 4 * (64 / (D / 8));
+    p.dec = p.NQ <= DEC_MAX_NQ && (D == 64 || D == 128);
     if (p.dec) {
         // rows per split = U rows per lane stream x (4 waves x rows per wave instruction);
-        // the largest U (8, 4, 2) that still gives DEC_TARGET_WG / 2 workgroups
+        // the largest U (8, 4, 2; at most 4 for more than 4 query vectors) that still
+        // gives DEC_TARGET_WG / 2 workgroups
         const int64_t rows_it = 4 * (64 / (D / 8));
         const int umax = p.NQ > 4 ? 4 : 8;
         int u = umax;
         while (u > 2 && Hkv * cdiv(n_kv, u * rows_it) < DEC_TARGET_WG / 2) u >>= 1;
-        if (const char* e = getenv("GQ_ATTN_U")) {  // tuning measurements
-            const int f = atoi(e);
-            if (f == 2 || f == 4 || (f == 8 && umax == 8)) u = f;
-        }
         p.dec_u = u;
         p.rows_per_split = u * rows_it;
         p.n_split = cdiv(n_kv, p.rows_per_split);
         p.cps = 0;
-        return p;
+        // the merge holds one weight per split in LDS: longer contexts take the tiled kernel
+        if (p.n_split <= MAX_SPLIT) return p;
+        p.dec = false;
+        p.dec_u = 0;
     }
     const int64_t base = Hkv * p.n_qt;
     int64_t want = base >= TARGET_WG ? 1 : cdiv(TARGET_WG, base);
@@ -367,7 +365,19 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
     }
     if (!fuse || n_split == 1) return;
 
-    // arrive once this workgroup's partial stores are complete; the last arrival merges
+    // Arrive once this workgroup's partial stores are complete; the last arrival merges.
+    // What this relies on (gfx950, as on gfx942): agent-scope atomic stores and loads
+    // carry the sc1 bit, so they bypass the per-XCD L2 for coherence and are served by
+    // memory (through the Infinity Fabric / MALL), never by a stale L2 line of another
+    // XCD; s_waitcnt vmcnt(0) returns only after every such store has been acknowledged
+    // at that level; the counter's fetch_add is performed at the same level, so a
+    // workgroup that reads n_split - 1 from it runs after every other workgroup's
+    // partials are visible to sc1 loads. The loads below are atomic, so the compiler
+    // cannot hoist them above the __syncthreads that follows the arrival. The C++/HIP
+    // memory model would ask for a release fetch_add and an acquire fence instead;
+    // both write back / invalidate the whole XCD L2 on this target (measured: the merge
+    // took 38 us instead of ~2 us), so the protocol stays at the hardware level.
+    // gq_attn_reset_counters clears the counters after a launch that did not finish.
     __shared__ int sLast;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -862,20 +872,9 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
     }
 }
 
-// GQ_ATTN_NO_MMA=1 keeps prefill attention on the VALU kernel (comparison runs)
-bool mma_disabled() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("GQ_ATTN_NO_MMA");
-        v = e && atoi(e) ? 1 : 0;
-    }
-    return v == 1;
-}
-
 // the matrix-core prefill kernel: no ALiBi / softcap, 16-byte aligned K/V rows,
 // buffer offsets within 2 GiB
 bool mma_ok(const AttnArgs& a) {
-    if (mma_disabled()) return false;
     if (a.max_bias != 0.0f || a.softcap != 0.0f || (a.D != 64 && a.D != 128)) return false;
     if (a.knb1 % 16 || a.vnb1 % 16) return false;
     return a.n_kv * a.knb1 < 0x7fff0000LL && a.n_kv * a.vnb1 < 0x7fff0000LL;
@@ -1115,7 +1114,17 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
     dst[(i * Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
 }
 
+__global__ void k_attn_reset_counters() {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < ARRIVE_N) g_attn_arrive[i] = 0u;
+}
+
 }  // namespace
+
+int attn_reset_counters(hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_reset_counters, dim3(ARRIVE_N / 256), dim3(256), 0, s);
+    return check_hip(hipGetLastError(), "attn_reset_counters launch");
+}
 
 size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     if (Hkv <= 0 || Hq % Hkv) return 0;
@@ -1126,6 +1135,7 @@ size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64
 
 int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     const Plan p = make_plan(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
+    if (p.n_split > MAX_SPLIT) return fail(GQ_ERR_INVALID, "flash_attn_ext: context too long for one launch");
     const size_t need = attn_workspace_bytes(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
     if (need > 0 && (ws == nullptr || ws_bytes < need))
         return fail(GQ_ERR_WORKSPACE, "flash_attn_ext: workspace too small (need " + std::to_string(need) + " bytes)");
@@ -1202,10 +1212,8 @@ struct PagedPlan {
 };
 
 // groups of 5..16 query heads per kv head go to the matrix-core kernel (pages of a
-// multiple of 128 rows); GQ_ATTN_PAGED_VALU=1 keeps them on k_attn_dec (comparison runs)
+// multiple of 128 rows)
 bool paged_mma(int64_t D, int64_t G, int64_t page) {
-    const char* e = getenv("GQ_ATTN_PAGED_VALU");
-    if (e && atoi(e) == 1 && G <= 8) return false;  // k_attn_dec serves at most 8
     return (D == 64 || D == 128) && G > 4 && G <= 16 && page % 128 == 0;
 }
 

@@ -285,10 +285,6 @@ int num_cus() {
 // workgroup, then 64. (Measured at M = 512, Q4_0: 4096-row o and down projections run
 // 14% and 32% faster as 128-token tiles split 4 ways than as unsplit 64-token tiles.)
 int gemm_bm(int64_t N, int64_t M) {
-    if (const char* e = getenv("GQ_GEMM_BM")) {  // tuning measurements
-        const int v = atoi(e);
-        if (v == 64 || v == 128) return v;
-    }
     if (M > 64 && cdiv(N, BN) >= 16) return 128;
     return cdiv(N, BN) * cdiv(M, 128) < num_cus() ? 64 : 128;
 }
@@ -302,7 +298,6 @@ GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M) {
     // split K while the tiles leave CUs idle, keeping >= 4 K steps per split
     int64_t ks = 1;
     if (tiles < num_cus()) ks = std::min<int64_t>({cdiv(2 * num_cus(), tiles), nk / 4, 16});
-    if (const char* e = getenv("GQ_GEMM_KS")) ks = atoi(e);  // tuning measurements
     if (ks < 1) ks = 1;
     p.spk = (int)cdiv(nk, ks);
     p.ks = (int)cdiv(nk, p.spk);  // no empty split

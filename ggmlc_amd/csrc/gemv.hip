@@ -651,17 +651,6 @@ int resident_wgs(KFn* fn, size_t lds, int& out) {
     return GQ_OK;
 }
 
-// GQ_GEMV_KS=1|2|4 pins the split-K factor (tuning measurements); unset: heuristic
-int gemv_ks_override() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("GQ_GEMV_KS");
-        v = e ? atoi(e) : 0;
-        if (v != 1 && v != 2 && v != 4) v = 0;
-    }
-    return v;
-}
-
 template <int QT, int M, bool XVEC, int PF, int KS, int XPT>
 int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s, size_t lds, int resident) {
@@ -692,12 +681,6 @@ int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
     // 4096-row down projection is slower, a 1536-row one faster)
     const int64_t t1 = cdiv(N, WAVES * RPW);
     const int J = (G + LPR - 1) / LPR;
-    const int ks_force = gemv_ks_override();
-    if (ks_force == 1 || (ks_force == 2 && J >= 2) || (ks_force == 4 && J >= 2)) {
-        if (ks_force == 1) return launch_grp_ks<QT, M, XVEC, PF, 1, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-        if (ks_force == 2) return launch_grp_ks<QT, M, XVEC, PF, 2, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-        return launch_grp_ks<QT, M, XVEC, PF, 4, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
-    }
     if (4 * t1 >= resident || J < 2)
         return launch_grp_ks<QT, M, XVEC, PF, 1, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
     if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);

@@ -5,6 +5,9 @@
 
 namespace gq {
 
+// api.hip: process-wide switches set through gq_set_option
+bool option_attn_separate_merge();
+
 // quantize.hip
 int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
                          hipStream_t s);
@@ -119,6 +122,7 @@ struct AttnArgs {
 };
 size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv);
 int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
+int attn_reset_counters(hipStream_t s);
 // batched decode over a paged KV pool: sequence b has len[b] rows, logical row r at pool
 // row table[b * tstride + (r >> log2p)] << log2p | (r & (2^log2p - 1))
 struct PagedKv {

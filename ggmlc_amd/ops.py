@@ -79,11 +79,16 @@ def _desc(t: torch.Tensor, gtype: int | None = None):
 
 
 class Workspace:
-    """Grow-only device scratch buffer (256-byte aligned) shared by calls on one stream."""
+    """Grow-only device scratch buffer (256-byte aligned) shared by calls on one stream.
+
+    HIP graphs captured while a smaller buffer was current keep its raw address, so a
+    buffer replaced by a larger one is retired, not freed: it lives as long as the
+    workspace (and so as long as the decoder whose graphs may still replay it)."""
 
     def __init__(self, device=None):
         self.device = device
         self.buf = None
+        self.retired: list[torch.Tensor] = []
 
     def get(self, nbytes: int) -> tuple[int, int]:
         if nbytes == 0:
@@ -93,6 +98,8 @@ class Workspace:
                 # a graph captured earlier may still point at the current buffer
                 raise RuntimeError(f"Workspace: {nbytes} bytes needed during graph capture; size it first")
             dev = self.device or torch.device("cuda", torch.cuda.current_device())
+            if self.buf is not None:
+                self.retired.append(self.buf)
             self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         return self.buf.data_ptr(), self.buf.numel()
 
@@ -107,6 +114,19 @@ def _ws(ws: Workspace | None) -> Workspace:
     if dev not in _default_ws:
         _default_ws[dev] = Workspace(torch.device("cuda", dev))
     return _default_ws[dev]
+
+
+class separate_attn_merge:
+    """Context manager: decode attention merges its KV splits in a second launch
+    (gq_set_option GQ_OPT_ATTN_SEPARATE_MERGE) inside the block; same bits, for comparisons."""
+
+    def __enter__(self):
+        check(_lib.load().gq_set_option(_lib.GQ_OPT_ATTN_SEPARATE_MERGE, 1))
+        return self
+
+    def __exit__(self, *exc):
+        check(_lib.load().gq_set_option(_lib.GQ_OPT_ATTN_SEPARATE_MERGE, 0))
+        return False
 
 
 def quantize_row_q8_0(x: torch.Tensor) -> torch.Tensor:

@@ -239,8 +239,11 @@ class ModelRunner:
         dev = str(device)
         if dev in ("auto", "gpu", "cuda"):
             dev = "cuda:0"
+        elif dev.startswith("gpu:"):
+            dev = "cuda:" + dev[4:]
         if not dev.startswith("cuda"):
-            raise ValueError(f"device {device!r}: this runtime executes on the GPU only ('gpu', 'cuda[:N]', 'auto')")
+            raise ValueError(f"device {device!r}: this runtime executes on the GPU only ('gpu[:N]', 'cuda[:N]', "
+                             "'auto')")
         if not torch.cuda.is_available():
             raise RuntimeError("no GPU visible: this runtime has no CPU path")
         self.device = dev

@@ -69,6 +69,16 @@ const char* gq_last_error(void);
 /* Checks that a gfx950 device is current and loads the kernels. */
 int gq_init(void);
 
+/* Process-wide switches. No counterpart in the reference (ggml has no such call):
+ * they choose between launch plans that give the same bits, so a test or a
+ * measurement can compare them. Unknown options or values return GQ_ERR_INVALID.
+ *   GQ_OPT_ATTN_SEPARATE_MERGE (0 default / 1): decode attention merges its KV
+ *   splits in a second launch instead of inside the decode kernel. */
+enum gq_option {
+    GQ_OPT_ATTN_SEPARATE_MERGE = 1,
+};
+int gq_set_option(int option, int64_t value);
+
 /* ---- quantize_row_q8_0 -------------------------------------------------- */
 
 /* Replaces the x86 runtime quantizer the CPU backend runs on MUL_MAT's src1:
@@ -195,6 +205,13 @@ int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v
                       const gq_tensor* mask, float scale, float max_bias, float logit_softcap,
                       gq_tensor* dst, void* workspace, size_t workspace_bytes,
                       gq_stream_t stream);
+
+/* Zeroes the per-device arrival counters of the decode kernels' in-kernel split
+ * merge (a fill kernel on `stream`, safe inside graph capture). Every completed
+ * launch leaves them at zero; a caller whose decode attention launch did not run to
+ * completion (an aborted graph, an error between capture and replay) calls this on
+ * the device before its next decode attention. No counterpart in the reference. */
+int gq_attn_reset_counters(gq_stream_t stream);
 
 /* ---- SOFT_MAX ----------------------------------------------------------- */
 

@@ -155,6 +155,19 @@ def quantize_row_q8_0(x, impl: str = "oracle") -> np.ndarray:
     return y
 
 
+def quantize_row_q8_0_ref(x, impl: str = "oracle") -> np.ndarray:
+    """ggml's scalar reference quantizer quantize_row_q8_0_ref (ggml-quants.c:276-299):
+    d = amax/127, q = roundf(x * (1/d)) (halves away from zero, unlike the x86 path's
+    round-to-nearest-even). Not on the GPU path; kept as the textbook statement the x86
+    quantizer is compared with."""
+    x = _c(x, np.float32)
+    K = x.shape[-1]
+    y = np.empty(x.shape[:-1] + (K // 32 * 34,), np.uint8)
+    f = lib().or_quantize_row_q8_0_ref if impl == "oracle" else ref().ref_quantize_row_q8_0_ref
+    f(_ptr(x), _ptr(y), x.size)
+    return y
+
+
 def quantize_weights(w, wtype: int) -> np.ndarray:
     """ggmlc's Python weight quantizer semantics; w [N, K] -> uint8 [N, K/32*block]."""
     w = _c(w, np.float32)

@@ -122,9 +122,64 @@ def main() -> None:
     manifest["files"]["decoder ops"] = ("swiglu / rms_norm / rope_{neox,normal} / get_rows_{q8_0,q4_0} / argmax: "
                                         "one ggml node each on the CPU backend")
 
+    config_attention(manifest)
     (OUT / "MANIFEST.json").write_text(json.dumps(manifest, indent=1) + "\n")
     print("wrote", len(list(OUT.glob("*.npz"))), "fixtures")
 
 
+# decode attention at the BASELINE configs' shapes: (name, Hq, Hkv, hd, pos) with s = 1 and
+# n_kv = pad_kv_len(pos + 1); pos is the last decode position of each config's run
+CFG_ATTN = (
+    ("smollm2_gqa3", 15, 5, 64, 639),      # configs[2]: 512-token prompt + 128 steps -> n_kv 768
+    ("llama7b_mha", 32, 32, 128, 1279),    # configs[3]: 1024 + 128 (+ margin) -> n_kv 1280
+    ("qwen_gqa6_3k", 12, 2, 128, 3071),    # configs[4]: contexts up to 4096
+    ("qwen_gqa6_4k", 12, 2, 128, 4095),
+)
+CFG_THREADS = (1, 4, 16)
+
+
+def cfg_attn_inputs(seed: int, Hq: int, Hkv: int, hd: int, pos: int):
+    """Seeded inputs of a config-shape attention fixture (regenerated by the tests; the
+    fixture stores their sha256 so a different generator is caught)."""
+    rng = np.random.default_rng(seed)
+    n_kv = O.pad_kv_len(pos + 1, 1 << 20)
+    kc = f16(rng.standard_normal((Hkv, n_kv, hd)))
+    vc = f16(rng.standard_normal((Hkv, n_kv, hd)))
+    q = rng.standard_normal((Hq, 1, hd)).astype(np.float32)
+    mask = O.causal_mask_f16(pos, 1, n_kv)
+    return q, kc, vc, mask, n_kv
+
+
+def inputs_digest(*arrays) -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def config_attention(manifest: dict) -> None:
+    """ggml's decode attention at the configs' shapes, at 1, 4 and 16 threads: its
+    split-KV chunking (ops.cpp:9179-9209) and fp16 V accumulator make the output depend
+    on the thread count, and these fixtures record by how much."""
+    for i, (name, Hq, Hkv, hd, pos) in enumerate(CFG_ATTN):
+        seed = 777000 + i
+        q, kc, vc, mask, n_kv = cfg_attn_inputs(seed, Hq, Hkv, hd, pos)
+        outs = {f"out_t{t}": O.flash_attn_ext_f16(q, kc, vc, n_kv, mask, impl="ref", n_threads=t)
+                for t in CFG_THREADS}
+        np.savez_compressed(OUT / f"cfg_attn_{name}.npz", seed=np.int64(seed), Hq=np.int64(Hq), Hkv=np.int64(Hkv),
+                            hd=np.int64(hd), pos=np.int64(pos), n_kv=np.int64(n_kv),
+                            digest=np.array(inputs_digest(q, kc, vc, mask)), **outs)
+    manifest["files"]["cfg_attn_*"] = ("decode attention at the configs' shapes: inputs regenerated from `seed` "
+                                       "(cfg_attn_inputs, checked against `digest`), outputs of ggml_flash_attn_ext "
+                                       "at 1, 4 and 16 threads (out_t1, out_t4, out_t16)")
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["--config-attention"]:
+        man = json.loads((OUT / "MANIFEST.json").read_text())
+        config_attention(man)
+        (OUT / "MANIFEST.json").write_text(json.dumps(man, indent=1) + "\n")
+    else:
+        main()

@@ -171,3 +171,36 @@ def test_mul_mat_fused_rope_kv_validation(lib):
     assert call(epi(mode=1)) == -2
     f = _lib.gq_mul_mat_fusion(0, 0.0, 0, None, None, None, None)
     assert lib.gq_mul_mat_fused(w, x, None, ctypes.byref(f), None) == -1  # no epilogue: dst required
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,n_kv", [
+    (12, 2, 128, 1, 70000),    # GQA 6: 6 query vectors per kv head
+    (16, 2, 64, 1, 140000),    # GQA 8, D = 64
+    (12, 2, 128, 1, 4096),
+    (32, 32, 128, 1, 1280),
+])
+def test_attention_split_plan_bounded(lib, Hq, Hkv, D, S, n_kv):
+    """The decode plan never asks for more KV splits than the merge holds (1024): the
+    workspace is n_split * Hkv * (Hq / Hkv * S) * (D + 2) floats."""
+    q = _t(_lib.F32, [D, S, Hq, 1], [4, 4 * D, 4 * D * S, 4 * D * S * Hq])
+    k = _t(_lib.F16, [D, n_kv, Hkv, 1], [2, 2 * D, 2 * D * n_kv, 2 * D * n_kv * Hkv])
+    ws = lib.gq_flash_attn_ext_workspace_size(q, k)
+    per_split = Hkv * (Hq // Hkv) * S * (D + 2) * 4
+    assert ws % per_split == 0
+    assert 1 <= ws // per_split <= 1024
+
+
+def test_set_option_rejects_unknown(lib):
+    assert lib.gq_set_option(_lib.GQ_OPT_ATTN_SEPARATE_MERGE, 0) == 0
+    assert lib.gq_set_option(_lib.GQ_OPT_ATTN_SEPARATE_MERGE, 7) == -1
+    assert lib.gq_set_option(999, 1) == -1
+    assert b"unknown option" in lib.gq_last_error()
+
+
+def test_flash_attn_rejects_heads_past_2gib(lib):
+    D, n_kv, Hkv = 128, 1 << 20, 2
+    q = _t(_lib.F32, [D, 1, 2, 1], [4, 4 * D, 4 * D, 8 * D])
+    k = _t(_lib.F16, [D, n_kv, Hkv, 1], [2, 4096, 4096 * n_kv, 4096 * n_kv * Hkv])  # 4 GiB per head
+    d = _t(_lib.F32, [D, 2, 1, 1], [4, 4 * D, 8 * D, 8 * D])
+    assert lib.gq_flash_attn_ext(q, k, k, None, 1.0, 0.0, 0.0, d, None, 0, None) == -1
+    assert b"2 GiB" in lib.gq_last_error()

@@ -444,10 +444,10 @@ def test_flash_attn_decode_workspace_and_replays(Hq, Hkv, D, S, pos, ctx):
     (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, 34 splits
     (15, 5, 64, 1, 700, 1024),      # SmolLM2 shape
 ])
-def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx, monkeypatch):
+def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx):
     """The decode kernel merges its split partials itself (the last workgroup of each
     kv head, counted on a device counter); that gives the bits of the separate merge
-    launch (GQ_ATTN_SEPARATE_MERGE=1), call after call."""
+    launch (gq_set_option GQ_OPT_ATTN_SEPARATE_MERGE), call after call."""
     rng = np.random.default_rng(Hq * D + S)
     n_kv = O.pad_kv_len(pos + S, ctx)
     kc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
@@ -455,13 +455,15 @@ def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx, monkeypatch):
     mask = to_dev(O.causal_mask_f16(pos, S, n_kv)).view(torch.float16)
     q = to_dev(rng.standard_normal((Hq, S, D)).astype(np.float32))
     scale = 1.0 / np.sqrt(D)
-    monkeypatch.delenv("GQ_ATTN_SEPARATE_MERGE", raising=False)
     fused = [ops.flash_attn_ext(q, kc, vc, mask, scale) for _ in range(4)]
-    monkeypatch.setenv("GQ_ATTN_SEPARATE_MERGE", "1")
-    sep = ops.flash_attn_ext(q, kc, vc, mask, scale)
-    monkeypatch.delenv("GQ_ATTN_SEPARATE_MERGE")
+    with ops.separate_attn_merge():
+        sep = ops.flash_attn_ext(q, kc, vc, mask, scale)
     for f in fused:
         assert torch.equal(f, sep)
+    # clearing the arrival counters between launches (gq_attn_reset_counters) changes nothing
+    from ggmlc_amd import _lib
+    _lib.check(_lib.load().gq_attn_reset_counters(ops._stream()))
+    assert torch.equal(ops.flash_attn_ext(q, kc, vc, mask, scale), sep)
     exact = O.flash_attn_ext_f16(q.cpu().numpy(), kc.view(torch.int16).cpu().numpy().view(np.uint16),
                                  vc.view(torch.int16).cpu().numpy().view(np.uint16), n_kv,
                                  mask.view(torch.int16).cpu().numpy().view(np.uint16), mode=1)
@@ -505,3 +507,27 @@ def test_soft_max_alibi_vs_torch():
     z = x * 0.5 + slopes[:, None, None] * m.astype(np.float16).astype(np.float32)[None]
     z = np.exp(z - z.max(-1, keepdims=True))
     assert np.abs(y - z / z.sum(-1, keepdims=True)).max() < 1e-6
+
+
+@pytest.mark.parametrize("pos,s,max_ctx", [
+    (0, 1, 256), (0, 37, 512), (255, 1, 512), (256, 1, 512), (700, 4, 1024), (1023, 1, 2048), (100, 512, 2048),
+])
+def test_kv_step_inputs_bits(pos, s, max_ctx):
+    """gq_kv_step_inputs against the executor's host-side step inputs restated in the
+    oracle (executor.cpp:58-64 pad_kv_len, :136-148 fill_f16_causal_mask, :1181-1393
+    positions and KV row indices), bit for bit, with garbage in every output first."""
+    n_kv = O.pad_kv_len(pos + s, max_ctx)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    pos_ids = torch.full((s,), -7, dtype=torch.int32, device=DEV)
+    kv_idx = torch.full((s,), -7, dtype=torch.int64, device=DEV)
+    mask_full = torch.full((s, max_ctx), 12345, dtype=torch.int16, device=DEV)
+    mask = mask_full.view(torch.float16)[:, :n_kv]
+    ops.kv_step_inputs(p, s, pos_ids, kv_idx, mask)
+    want = O.causal_mask_f16(pos, s, n_kv)
+    assert np.array_equal(mask_full[:, :n_kv].cpu().numpy().view(np.uint16), want)
+    assert (mask_full[:, n_kv:] == 12345).all()  # the view's columns past n_kv are untouched
+    assert pos_ids.cpu().tolist() == list(range(pos, pos + s))
+    assert kv_idx.cpu().tolist() == list(range(pos, pos + s))
+    ops.kv_advance(p, s)
+    assert int(p.item()) == pos + s
+

@@ -406,3 +406,42 @@ def test_prefill_gemm_prologue_fusions_bit_identical(shape):
     (la, ra), (lb, rb) = outs
     assert torch.equal(la, lb), (la - lb).abs().max().item()
     assert torch.equal(ra, rb)
+
+
+@pytest.mark.gpu
+def test_graph_replay_after_workspace_growth():
+    """A decode graph captured while the workspace was small keeps its bits and writes
+    nothing outside its own buffers after a larger bucket replaced the workspace buffer:
+    the replaced buffer is retired, not freed, so tensors allocated afterwards (which the
+    caching allocator would otherwise place at the freed address) stay untouched."""
+    import torch
+
+    from ggmlc_amd import ops
+    from ggmlc_amd.model import LlamaConfig, pad_kv_len
+
+    cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q8_0)
+    dec, _ = _gpu_model(cfg, 512, seed=17)
+    prompt = torch.from_numpy(np.random.default_rng(8).integers(0, cfg.n_vocab, 40).astype(np.int32)).cuda()
+    dec.step(40, pad_kv_len(40, 512), ids=prompt)
+    p0, n_kv = int(dec.pos[0]), pad_kv_len(41, 512)
+    assert ops.flash_attn_workspace_size(cfg.head_dim, 1, cfg.n_head, cfg.n_head_kv, n_kv) > 0  # uses the buffer
+    ids1, _ = dec.decode_buffers()
+    ids1.fill_(5)
+    dec.reset(p0)
+    dec.step(1, n_kv)
+    want = dec._buffers(1)["logits"].clone()
+    dec.reset(p0)
+    g = dec.capture(1, n_kv)
+    old = dec.ws.buf
+    dec.ws.get(old.numel() * 4)  # what a larger bucket's step does
+    assert dec.ws.buf.data_ptr() != old.data_ptr() and dec.ws.retired[-1] is old
+    size = old.numel()
+    del old
+    junk = [torch.full((size,), 0x7F, dtype=torch.uint8, device="cuda") for _ in range(6)]
+    for _ in range(3):
+        dec.reset(p0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dec._buffers(1)["logits"], want)
+        for j in junk:
+            assert bool((j == 0x7F).all())

@@ -78,6 +78,32 @@ def test_quantize_q8_0_vs_reference_random():
         assert np.array_equal(O.quantize_row_q8_0(x), O.quantize_row_q8_0(x, impl="ref"))
 
 
+def test_quantize_q8_0_scalar_ref_closed_forms():
+    """ggml's scalar quantize_row_q8_0_ref rounds halves away from zero (roundf) and
+    scales by 1/d rather than 127/amax: a block whose x * id land on k + 0.5 tells it
+    from the x86 path."""
+    x = np.zeros((1, 64), np.float32)
+    x[0, 32] = 127.0                                    # d = 1, id = 1: q = roundf(x)
+    x[0, 33:64] = np.arange(31, dtype=np.float32) - 15.5
+    q = O.quantize_row_q8_0_ref(x).reshape(2, 34)
+    qs = q[:, 2:].view(np.int8)
+    assert q[0, :2].view(np.uint16)[0] == 0 and not qs[0].any()
+    want = np.trunc(np.arange(31, dtype=np.float64) - 15.5 + np.sign(np.arange(31) - 15.5) * 0.5)
+    assert qs[1, 0] == 127
+    assert np.array_equal(qs[1, 1:], want.astype(np.int8))
+    # the x86 quantizer rounds the same halves to even
+    assert not np.array_equal(O.quantize_row_q8_0(x)[0, 36:], q.reshape(-1)[36:])
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built")
+def test_quantize_q8_0_scalar_ref_vs_reference():
+    rng = np.random.default_rng(8)
+    for scale in (1e-4, 1.0, 50.0):
+        x = (rng.standard_normal((32, 2048)) * scale).astype(np.float32)
+        x[::3] = np.round(x[::3] * 4) / 4
+        assert np.array_equal(O.quantize_row_q8_0_ref(x), O.quantize_row_q8_0_ref(x, impl="ref"))
+
+
 # ------------------------------------------------------ weight quantizers ---
 
 def _np_quantize_q8_0(w):

@@ -120,12 +120,9 @@ def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
     print(f"paged attention max-abs-rel vs exact {worst:.2e}")
     assert worst < 1e-5
     # the in-kernel split merge gives the bits of the separate merge launch
-    os.environ["GQ_ATTN_SEPARATE_MERGE"] = "1"
-    try:
+    with ops.separate_attn_merge():
         sep = ops.flash_attn_paged(t(q), t(k_pool), t(v_pool), t(table), t(np.array(lens, np.int32)), P, max(lens),
                                    scale).cpu().numpy()
-    finally:
-        del os.environ["GQ_ATTN_SEPARATE_MERGE"]
     assert np.array_equal(sep, out, equal_nan=True)
 
 
