@@ -17,6 +17,7 @@ BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
 
 GQ_OK = 0
 GQ_OPT_ATTN_SEPARATE_MERGE = 1
+GQ_ATTN_SCRATCH_BYTES = 16 << 20  # gq_flash_attn_ext_noalloc's static scratch per device
 _ERR_NAMES = {-1: "GQ_ERR_INVALID", -2: "GQ_ERR_UNSUPPORTED", -3: "GQ_ERR_WORKSPACE", -4: "GQ_ERR_DEVICE"}
 
 
@@ -91,6 +92,7 @@ SIGNATURES = {
     "gq_set_rows": (ctypes.c_int, [_P, _P, _P, _vp, _vp]),
     "gq_flash_attn_ext_workspace_size": (ctypes.c_size_t, [_P, _P]),
     "gq_flash_attn_ext": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_flash_attn_ext_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _f32, _f32, _f32, _P, _vp]),
     "gq_attn_reset_counters": (ctypes.c_int, [_vp]),
     "gq_soft_max": (ctypes.c_int, [_P, _P, _f32, _f32, _P, _vp]),
     "gq_swiglu": (ctypes.c_int, [_P, _P, _P, ctypes.c_int, _vp]),

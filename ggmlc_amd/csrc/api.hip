@@ -109,7 +109,8 @@ int gq_init(void) {
     if (rc) return rc;
     if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
         return fail(GQ_ERR_UNSUPPORTED, std::string("libgq is built for gfx950, device is ") + prop.gcnArchName);
-    return GQ_OK;
+    // the device address of gq_flash_attn_ext_noalloc's static scratch on this device
+    return attn_scratch_init(nullptr);
 }
 
 int gq_set_option(int option, int64_t value) {
@@ -469,6 +470,14 @@ int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v
     const int rc = attn_args(q, k, v, mask, scale, max_bias, logit_softcap, dst, a);
     if (rc) return rc;
     return attention(a, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int gq_flash_attn_ext_noalloc(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const gq_tensor* mask,
+                              float scale, float max_bias, float logit_softcap, gq_tensor* dst, gq_stream_t stream) {
+    AttnArgs a;
+    const int rc = attn_args(q, k, v, mask, scale, max_bias, logit_softcap, dst, a);
+    if (rc) return rc;
+    return attention_noalloc(a, (hipStream_t)stream);
 }
 
 int gq_attn_reset_counters(gq_stream_t stream) { return attn_reset_counters((hipStream_t)stream); }

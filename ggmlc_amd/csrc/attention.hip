@@ -17,6 +17,8 @@
 // through LDS with an online softmax; when the KV range is split across
 // workgroups, unnormalised partials (O, max, sum) go to the workspace and a
 // second kernel merges them (the reduction of ops.cpp:9060-9128).
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -1305,6 +1307,51 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
         hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
                            a.Hq, a.dst);
     return check_hip(hipGetLastError(), "flash_attn_paged merge launch");
+}
+
+// ---- allocation-free decode attention -------------------------------------
+// gq_flash_attn_ext_noalloc takes its split partials from this file-scope device
+// array instead of a caller workspace. Each device that loads the library holds its
+// own copy (at its own address) until the process ends; in host code the name
+// `scratch` is only a host-side stand-in, so kernels get the device address looked up
+// once per device with hipGetSymbolAddress. Every partial a launch reads was written
+// by the same launch, so nothing is cleared between calls; calls that overlap on one
+// device race on it.
+namespace {
+static __device__ __align__(256) unsigned char scratch[ATTN_SCRATCH_BYTES];
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
+}  // namespace
+
+int attn_scratch_init(void** out) {
+    int dev = 0;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return fail(GQ_ERR_UNSUPPORTED, "attention scratch: device index too large");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(attention scratch)");
+        if (rc) return rc;
+        g_scratch_ptr[dev] = p;
+    }
+    if (out) *out = g_scratch_ptr[dev];
+    return GQ_OK;
+}
+
+int attention_noalloc(const AttnArgs& a, hipStream_t s) {
+    const size_t need = attn_workspace_bytes(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
+    if (need > ATTN_SCRATCH_BYTES)
+        return fail(GQ_ERR_WORKSPACE, "flash_attn_ext_noalloc: this shape needs " + std::to_string(need) +
+                                          " bytes of split partials, more than the " +
+                                          std::to_string(ATTN_SCRATCH_BYTES) + "-byte static scratch");
+    void* ptr = nullptr;
+    if (need > 0) {
+        const int rc = attn_scratch_init(&ptr);
+        if (rc) return rc;
+    }
+    return attention(a, ptr, need, s);
 }
 
 }  // namespace gq

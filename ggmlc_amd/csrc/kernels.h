@@ -123,6 +123,12 @@ struct AttnArgs {
 size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv);
 int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s);
 int attn_reset_counters(hipStream_t s);
+// the same launches with the split partials in a static per-device array of
+// ATTN_SCRATCH_BYTES (no workspace); attn_scratch_init looks its address up once per
+// device (the current one) and returns it
+constexpr size_t ATTN_SCRATCH_BYTES = (size_t)16 << 20;
+int attn_scratch_init(void** out);
+int attention_noalloc(const AttnArgs& a, hipStream_t s);
 // batched decode over a paged KV pool: sequence b has len[b] rows, logical row r at pool
 // row table[b * tstride + (r >> log2p)] << log2p | (r & (2^log2p - 1))
 struct PagedKv {

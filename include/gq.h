@@ -206,6 +206,20 @@ int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v
                       gq_tensor* dst, void* workspace, size_t workspace_bytes,
                       gq_stream_t stream);
 
+/* gq_flash_attn_ext without a workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same validation, kernels and bits as
+ * gq_flash_attn_ext; the KV-split partials go to a static device array of
+ * GQ_ATTN_SCRATCH_BYTES (16 MiB) that each device holds until the process ends
+ * (its address is looked up by gq_init, or by the first call on the device). A
+ * shape whose partials need more (gq_flash_attn_ext_workspace_size) returns
+ * GQ_ERR_WORKSPACE before anything launches. Calls share the array, so two calls
+ * that overlap on one device race: issue them on one stream. */
+#define GQ_ATTN_SCRATCH_BYTES ((size_t)16 << 20)
+int gq_flash_attn_ext_noalloc(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v,
+                              const gq_tensor* mask, float scale, float max_bias, float logit_softcap,
+                              gq_tensor* dst, gq_stream_t stream);
+
 /* Zeroes the per-device arrival counters of the decode kernels' in-kernel split
  * merge (a fill kernel on `stream`, safe inside graph capture). Every completed
  * launch leaves them at zero; a caller whose decode attention launch did not run to
