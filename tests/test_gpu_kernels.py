@@ -531,3 +531,37 @@ def test_kv_step_inputs_bits(pos, s, max_ctx):
     ops.kv_advance(p, s)
     assert int(p.item()) == pos + s
 
+
+def test_flash_attn_config_goldens(golden_dir):
+    """Decode attention at the configs' shapes (SmolLM2 GQA-3 n_kv 768, 7B MHA n_kv 1280,
+    Qwen2.5 GQA-6 n_kv 3072 and 4096) against ggml's own output at 1, 4 and 16 threads.
+    ggml's result moves with its thread count (split-KV chunks, fp16 V accumulator:
+    ops.cpp:8682-8696, 9179-9209); the GPU accumulates in fp32. Bars: within 1e-3 of the
+    exact softmax, and no farther from each reference output than the reference outputs
+    are from each other (its thread spread) or, where one reference output is farther from
+    the exact softmax than that spread, than the triangle bound through the exact result
+    (the reference's distance from it plus the GPU's); and within that distance + 1e-3."""
+    import sys
+
+    sys.path.insert(0, str(golden_dir))
+    from make_golden import CFG_THREADS, cfg_attn_inputs, inputs_digest
+
+    files = sorted(golden_dir.glob("cfg_attn_*.npz"))
+    assert len(files) == 4
+    for f in files:
+        g = np.load(f)
+        q, kc, vc, mask, n_kv = cfg_attn_inputs(int(g["seed"]), int(g["Hq"]), int(g["Hkv"]), int(g["hd"]),
+                                                int(g["pos"]))
+        assert inputs_digest(q, kc, vc, mask) == str(g["digest"]), f.name
+        got = _attn_dev(q, kc, vc, n_kv, mask)
+        exact = O.flash_attn_ext_f16(q, kc, vc, n_kv, mask, mode=1)
+        refs = {t: g[f"out_t{t}"] for t in CFG_THREADS}
+        spread = max(mar(refs[a], refs[b]) for a in CFG_THREADS for b in CFG_THREADS if a != b)
+        line = [f"{f.name}: vs exact {mar(got, exact):.2e}, spread {spread:.2e}"]
+        assert mar(got, exact) < 1e-3, f.name
+        for t, r in refs.items():
+            dev = mar(r, exact)
+            line.append(f"t{t} {mar(got, r):.2e} (ref vs exact {dev:.2e})")
+            assert mar(got, r) <= max(spread, dev + mar(got, exact)), (f.name, t)
+            assert mar(got, r) < dev + 1e-3, (f.name, t)
+        print(" | ".join(line))

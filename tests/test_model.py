@@ -179,10 +179,13 @@ def _gpu_model(cfg, max_ctx, seed):
     return dec, host
 
 
-def _check_trace(cfg, host, trace, s, n_kv, max_ctx):
-    """Recompute every traced op from the GPU's own inputs."""
+def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
+    """Recompute every traced op from the GPU's own inputs (of the given layers only, and
+    the output head, when layers is a collection of layer indices)."""
     t = cfg.qtype
-    T = {(n, li): v.cpu().numpy() for n, li, v in trace}
+    last = len(host[2]) - 1
+    keep = (lambda li: True) if layers is None else (lambda li: li in layers or li == -1)
+    T = {(n, li): v.cpu().numpy() for n, li, v in trace if keep(li) or (n == "x_out" and li == last)}
     p0 = int(T[("pos", -1)][0])
     pos = np.arange(p0, p0 + s)
     mask = O.causal_mask_f16(p0, s, n_kv)
@@ -195,14 +198,22 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx):
         assert m <= tol, (name, m)
 
     for li, (wqkv, wo, wgu, wd) in enumerate(host[2]):
+        if not keep(li):
+            continue
         g = lambda n: T[(n, li)]  # noqa: E731
         x_in = g("x_in")
         bar("rms_norm", g("h1"), _rms(x_in, cfg.rms_eps), 1e-5)
         bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1")), 1e-3)
         qkv = g("qkv")
-        bar("rope q", g("q")[0], _rope(qkv[:, :qd].reshape(s, cfg.n_head, cfg.head_dim), pos, cfg.rope_base), 1e-5)
-        bar("rope k", g("k")[0], _rope(qkv[:, qd:qd + kvd].reshape(s, cfg.n_head_kv, cfg.head_dim), pos,
-                                       cfg.rope_base), 1e-5)
+        qh = qkv[:, :qd].reshape(s, cfg.n_head, cfg.head_dim)
+        kh = qkv[:, qd:qd + kvd].reshape(s, cfg.n_head_kv, cfg.head_dim)
+        if O.ref_available():  # ggml's own ROPE (its angle recurrence): the GPU's bits
+            bar("rope q", g("q")[0], O.ref_rope(qh, pos.astype(np.int32), cfg.head_dim, 2, cfg.rope_base), 1e-6)
+            bar("rope k", g("k")[0], O.ref_rope(kh, pos.astype(np.int32), cfg.head_dim, 2, cfg.rope_base), 1e-6)
+        else:  # float64 rotation: ggml's float angle recurrence drifts with the position
+            tol = 1e-5 * max(1.0, float(pos.max()) / 256.0)
+            bar("rope q", g("q")[0], _rope(qh, pos, cfg.rope_base), tol)
+            bar("rope k", g("k")[0], _rope(kh, pos, cfg.rope_base), tol)
         # SET_ROWS: rows pos..pos+s-1 of the caches hold the F16 of this step's k and v, bit for bit
         kc, vc = g("kc").view(np.uint16), g("vc").view(np.uint16)
         k16 = O.set_rows_f32_f16(np.zeros((1, cfg.n_head_kv, max_ctx, cfg.head_dim), np.uint16),
