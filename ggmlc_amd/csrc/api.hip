@@ -80,9 +80,10 @@ int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, M
         p.ldd = (int64_t)(dst->nb[1] / 4);
     }
     p.use_gemv = p.M <= GEMV_MAX_M;  // GEMV up to this many activation rows, MFMA GEMM above
-    // the GEMV quantizes the activation in LDS; the GEMM takes it as fp16 from the workspace,
-    // followed by the split-K partials when its plan splits K
-    const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 2;
+    // the GEMV quantizes the activation in LDS; the GEMM takes it from the workspace as the
+    // exact fp16 pair hi + lo of d * q (rows of 2K halves), followed by the split-K partials
+    // when its plan splits K
+    const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 4;
     p.ws_act = (raw + 255) & ~(size_t)255;
     p.ws = p.ws_act;
     if (!p.use_gemv && p.M > 0) p.ws += (gemm_plan(N, K, p.M).part_bytes + 255) & ~(size_t)255;
@@ -167,10 +168,10 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     if (p.use_gemv) return gemv(a->type, W, p.N, p.K, ActSrc{x, p.x_stride, nullptr, 0, nullptr, 0}, p.M, y, p.ldd,
                                 GemvFuse{}, s);
     uint16_t* A = static_cast<uint16_t*>(workspace);
-    rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, p.K, s);
+    rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, 2 * p.K, s);
     if (rc) return rc;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.ws_act);
-    return gemm(a->type, W, p.N, p.K, A, p.K, p.M, y, p.ldd, part, s);
+    return gemm(a->type, W, p.N, p.K, A, 2 * p.K, p.M, y, p.ldd, part, s);
 }
 
 // The rope + KV-store epilogue of gq_mul_mat_fused: the checks of gq_rope_kv_store
@@ -289,10 +290,10 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
     uint16_t* A = static_cast<uint16_t*>(f->workspace);
-    int rc = act_prep(ap, p.M, A, p.K, s);
+    int rc = act_prep(ap, p.M, A, 2 * p.K, s);
     if (rc) return rc;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(f->workspace) + p.ws_act);
-    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, p.K, p.M,
+    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, 2 * p.K, p.M,
                 static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), part, s);
 }
 

@@ -226,6 +226,27 @@ __device__ __forceinline__ void quant8_block(const float (&v)[8], int (&q)[8], u
     dh = f2h(d);
 }
 
+// d * q of 8 quants of one block as an exact pair of fp16 vectors, hi + lo == d * q:
+// d (fp16, 11 significant bits) times |q| <= 128 has at most 18 significant bits and is
+// exact in fp32; hi = fp16_rne(d * q) and lo = d * q - hi (exact in fp32) has at most 7
+// significant bits on the grid of d's last bit, which fp16 holds exactly (d normal: that
+// grid is >= 2^-24; d subnormal: every product is a multiple of 2^-24). Packed two
+// halves per dword, element i in the low half of dword i / 2.
+__device__ __forceinline__ void split_dq8(const int (&q)[8], uint16_t dh, uint4& hi, uint4& lo) {
+    const float df = h2f(dh);
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float p0 = (float)q[2 * i] * df, p1 = (float)q[2 * i + 1] * df;
+        const uint16_t h0 = f2h(p0), h1 = f2h(p1);
+        const uint16_t l0 = f2h(p0 - h2f(h0)), l1 = f2h(p1 - h2f(h1));
+        h[i] = h0 | ((uint32_t)h1 << 16);
+        l[i] = l0 | ((uint32_t)l1 << 16);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
 // load the 8 floats of one lane's part of a block (16-byte loads when aligned)
 template <bool VEC>
 __device__ __forceinline__ void load8(const float* src, bool valid, float (&v)[8]) {

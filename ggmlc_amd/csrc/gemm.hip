@@ -1,22 +1,28 @@
-// Prefill GEMM for Q8_0 / Q4_0 weights on fp16 MFMA (gfx950 v_mfma_f32_32x32x16_f16).
+// Prefill GEMM for Q8_0 / Q4_0 weights with exact block products on fp16 MFMA
+// (gfx950 v_mfma_f32_32x32x16_f16).
 //
-// Semantics: ggml_mul_mat with src1 quantized to Q8_0 (llamafile tinyBLAS_Q0
-// path, ggml-cpu/llamafile/sgemm.cpp:3805-4113, entered at ggml-cpu.c:1366-1386)
-// computes sum_b d_w d_x isum_b. Here both operands are expanded to fp16
-// before the tensor-core product: A = fp16(d_x * q_x) is written by the
-// activation quantizer, B = fp16(d_w * q_w) is expanded tile by tile in LDS.
-// Each fp16 rounding is relative 2^-12 and independent, so the result stays
-// within ~3e-4 max-abs-rel of the exact block sum (checked against the oracle
-// at 1e-3). The alternative — int8 MFMA with an fp32 rescale of every 32x32
-// tile per 32-wide block — needs ~3 VALU ops per output per block and would
-// leave the int8 matrix cores idle most of the time.
+// Semantics: ggml_mul_mat with src1 quantized to Q8_0 (llamafile tinyBLAS_Q0 path,
+// ggml-cpu/llamafile/sgemm.cpp:3805-4113, entered at ggml-cpu.c:1366-1386):
+//   dst[m, n] = sum_b d_w[n, b] * d_x[m, b] * sum_{j<32} q_w[n, b, j] * q_x[m, b, j].
+// Every product is formed exactly, and only fp32 accumulation rounds (as on the CPU):
+// * the activation quantizer writes d_x * q_x as an exact fp16 pair hi + lo
+//   (split_dq8: 18 significant bits over two halves);
+// * weight quants are staged in LDS as raw fp16 integers (q, or nibble - 8);
+// * per quant block and 32x32 output tile, four MFMAs (hi and lo, two K16 halves)
+//   sum sum_j (hi + lo) * q_w, each product exact in fp32 (19 significant bits), into a
+//   block accumulator that starts at zero; then acc = fma(d_w, block, acc).
+// Against int8 MFMA (v_mfma_i32_32x32x32_i8), which yields the integer block sum in one
+// instruction but leaves both scales to VALU (int -> float, d_x * d_w, fma: 3 ops per
+// output per block, about 6x the int8 matrix time on CDNA4 without packed fp32), the
+// fp16 pair keeps the per-block VALU work to one fma per output and the kernel bound by
+// the matrix cores (4 x 32-cycle MFMAs against 16 fmas per lane per block tile).
 //
-// Tiling: 128 (tokens) x 128 (weight rows) per workgroup, K step 64 (two
-// quant blocks), 4 waves each owning a 64x64 sub-tile (2x2 MFMA 32x32 tiles).
-// Next K step's global loads are held in registers while the current step
-// runs on the matrix cores. Quant blocks are loaded with one 16-bit and
-// 8 (Q8_0) or 4 (Q4_0) dword loads whose alignment is fixed per block, and
-// expanded with v_perm (0x64xx fp16 exponent trick) + packed fp16 sub/mul.
+// Tiling: 128 weight rows x BM (128 or 64) tokens per workgroup, K step 64 (two quant
+// blocks), 4 waves each owning a BM/2 x 64 sub-tile (MI x 2 MFMA 32x32 tiles). The next
+// K steps' global loads are held in a register ring while the current step runs on the
+// matrix cores. Quant blocks are loaded with one 16-bit and 8 (Q8_0) or 4 (Q4_0) dword
+// loads whose alignment is fixed per block, and expanded with v_perm (0x64xx fp16
+// exponent trick) + a packed fp16 subtraction.
 #include <algorithm>
 
 #include "common.h"
@@ -31,23 +37,23 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int BN = 128, BK = 64, LDK = BK + 8;  // LDS row pitch in halves (144 B)
-constexpr int GEMM_PF_128 = 2, GEMM_PF_64 = 3;   // K steps of loads in flight per tile height
+constexpr int GEMM_PF_128 = 1, GEMM_PF_64 = 2;   // K steps of loads in flight per tile height
 
-__device__ __forceinline__ uint32_t h2_fma_bits(uint32_t pair, half2v bias, half2v d) {
+__device__ __forceinline__ uint32_t h2_sub_bits(uint32_t pair, half2v bias) {
     half2v h;
     __builtin_memcpy(&h, &pair, 4);
-    h = (h - bias) * d;
+    h = h - bias;  // integers below 2048: exact
     uint32_t r;
     __builtin_memcpy(&r, &h, 4);
     return r;
 }
 
-// 4 bytes (values 0..255 as unsigned) -> 4 fp16 of (byte - off) * d, as 2 dwords
-__device__ __forceinline__ void expand4(uint32_t u, half2v bias, half2v d, uint32_t& lo, uint32_t& hi) {
+// 4 bytes (values 0..255 as unsigned) -> 4 fp16 of (byte - off), as 2 dwords
+__device__ __forceinline__ void expand4(uint32_t u, half2v bias, uint32_t& lo, uint32_t& hi) {
     const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
     const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-    lo = h2_fma_bits(p01, bias, d);
-    hi = h2_fma_bits(p23, bias, d);
+    lo = h2_sub_bits(p01, bias);
+    hi = h2_sub_bits(p23, bias);
 }
 
 template <int QT>
@@ -56,25 +62,6 @@ struct BlockRegs {
     uint32_t u;  // the 16-bit piece
     bool even;   // block start is 4-byte aligned
 };
-
-template <int QT>
-__device__ __forceinline__ void load_block(const uint8_t* p, bool valid, BlockRegs<QT>& r) {
-    constexpr int NW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
-    constexpr int TAIL = QT == GQ_TYPE_Q8_0 ? 32 : 16;
-    if (!valid) {
-#pragma unroll
-        for (int i = 0; i < NW; ++i) r.dw[i] = 0;
-        r.u = 0;
-        r.even = false;
-        return;
-    }
-    r.even = (reinterpret_cast<uintptr_t>(p) & 3) == 0;
-    const uint32_t* dp = reinterpret_cast<const uint32_t*>(r.even ? p : p + 2);
-    const uint16_t* up = reinterpret_cast<const uint16_t*>(r.even ? p + TAIL : p);
-#pragma unroll
-    for (int i = 0; i < NW; ++i) r.dw[i] = dp[i];
-    r.u = *up;
-}
 
 // The block at p, loaded unconditionally (callers pass a valid block address; a
 // step past the matrix loads block 0 and is zeroed where it is used), so the loads of
@@ -91,9 +78,10 @@ __device__ __forceinline__ void load_block_any(const uint8_t* p, BlockRegs<QT>& 
     r.u = *up;
 }
 
-// expand one quant block into 32 fp16 (16 dwords)
+// one quant block as its 32 raw quants in fp16 (16 dwords: Q8_0 q, Q4_0 nibble - 8)
+// and its scale
 template <int QT>
-__device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* out) {
+__device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* out, float& d) {
     constexpr int NW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
     uint32_t q[NW];
     uint32_t hdr;
@@ -107,26 +95,24 @@ __device__ __forceinline__ void expand_block(const BlockRegs<QT>& r, uint32_t* o
 #pragma unroll
         for (int i = 0; i < NW; ++i) q[i] = r.dw[i];
     }
-    _Float16 dh;
-    const uint16_t hb = (uint16_t)hdr;
-    __builtin_memcpy(&dh, &hb, 2);
-    const half2v d = {dh, dh};
+    d = h2f((uint16_t)hdr);
     if (QT == GQ_TYPE_Q8_0) {
         const half2v bias = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
 #pragma unroll
-        for (int i = 0; i < 8; ++i) expand4(q[i] ^ 0x80808080u, bias, d, out[2 * i], out[2 * i + 1]);
+        for (int i = 0; i < 8; ++i) expand4(q[i] ^ 0x80808080u, bias, out[2 * i], out[2 * i + 1]);
     } else {
         const half2v bias = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            expand4(q[i] & 0x0f0f0f0fu, bias, d, out[2 * i], out[2 * i + 1]);
-            expand4((q[i] >> 4) & 0x0f0f0f0fu, bias, d, out[8 + 2 * i], out[8 + 2 * i + 1]);
+            expand4(q[i] & 0x0f0f0f0fu, bias, out[2 * i], out[2 * i + 1]);
+            expand4((q[i] >> 4) & 0x0f0f0f0fu, bias, out[8 + 2 * i], out[8 + 2 * i + 1]);
         }
     }
 }
 
 // BM = 128 or 64 tokens per workgroup (64 doubles the grid of small-N shapes); PF K
-// steps of global loads are in flight while a step runs on the matrix cores
+// steps of global loads are in flight while a step runs on the matrix cores. A holds
+// each token row as 2K halves: the hi parts of d_x * q_x, then the lo parts (lda >= 2K).
 //
 // Split K (gridDim.z > 1, for grids with fewer tiles than CUs): workgroup z sums K steps
 // [z * spk, (z + 1) * spk) and writes its partial tile to part[z][M][N]; k_gemm_reduce
@@ -138,9 +124,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
                                                  int64_t ldd, int spk, float* __restrict__ part) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int MI = BM / 64;        // 32-row MFMA tiles per wave along M
-    constexpr int AQ = BM / 32;        // 16-byte activation pieces per thread per K step
-    __shared__ __align__(16) uint16_t sA[BM * LDK];
+    constexpr int AQ = BM / 32;        // 16-byte activation pieces per thread per K step (each of hi, lo)
+    __shared__ __align__(16) uint16_t sAh[BM * LDK];
+    __shared__ __align__(16) uint16_t sAl[BM * LDK];
     __shared__ __align__(16) uint16_t sB[BN * LDK];
+    __shared__ float sD[2][BN];  // weight scales of the K step's two blocks, per weight row
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -153,7 +141,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     const int kt1 = min((int)cdiv(K, BK), kt0 + spk);  // this workgroup's K steps [kt0, kt1)
 
     // loader mapping: B: thread -> (weight row tid / 2, block tid % 2); A: thread ->
-    // (token row, AQ consecutive 16-byte pieces of the row's 128-byte K step)
+    // (token row, AQ consecutive 16-byte pieces of the row's 128-byte K step, hi and lo)
     const int lrow = tid >> 1;
     const int lhalf = tid & 1;
     const int arow = tid / (8 / AQ);
@@ -163,16 +151,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
 
     // register ring: PF K steps in flight; loads from clamped (always valid) addresses,
     // the validity travels with the slot and zeroes the data when it is parked in LDS
-    uint4 ra[PF][AQ];
+    uint4 rh[PF][AQ], rl[PF][AQ];
     BlockRegs<QT> rb[PF];
     bool av[PF], bv[PF];
 
     auto load = [&](int kt, int slot) {
         const int64_t k = (int64_t)kt * BK + apiece * 8;
         av[slot] = am < M && k < K && kt < kt1;
-        const uint4* ap = reinterpret_cast<const uint4*>(av[slot] ? A + am * lda + k : A);
+        const uint16_t* ap = av[slot] ? A + am * lda + k : A;
+        const uint4* aph = reinterpret_cast<const uint4*>(ap);
+        const uint4* apl = reinterpret_cast<const uint4*>(av[slot] ? ap + K : A);
 #pragma unroll
-        for (int i = 0; i < AQ; ++i) ra[slot][i] = ap[i];
+        for (int i = 0; i < AQ; ++i) rh[slot][i] = aph[i];
+#pragma unroll
+        for (int i = 0; i < AQ; ++i) rl[slot][i] = apl[i];
         const int kb = kt * 2 + lhalf;
         bv[slot] = bn < N && kb < nb && kt < kt1;
         load_block_any<QT>(bv[slot] ? W + bn * row_bytes + (int64_t)kb * BB : W, rb[slot]);
@@ -192,37 +184,62 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     auto step = [&](int kt, int slot, auto prefetch) {
         __syncthreads();  // the previous step's LDS tiles are fully read
         {
-            uint4* sa = reinterpret_cast<uint4*>(sA + arow * LDK + apiece * 8);
+            const int ao = arow * LDK + apiece * 8;
+            uint4* sah = reinterpret_cast<uint4*>(sAh + ao);
+            uint4* sal = reinterpret_cast<uint4*>(sAl + ao);
 #pragma unroll
-            for (int i = 0; i < AQ; ++i) sa[i] = av[slot] ? ra[slot][i] : make_uint4(0, 0, 0, 0);
+            for (int i = 0; i < AQ; ++i) {
+                sah[i] = av[slot] ? rh[slot][i] : make_uint4(0, 0, 0, 0);
+                sal[i] = av[slot] ? rl[slot][i] : make_uint4(0, 0, 0, 0);
+            }
             uint32_t e[16];
-            expand_block<QT>(rb[slot], e);
+            float d;
+            expand_block<QT>(rb[slot], e, d);
             uint4* sb = reinterpret_cast<uint4*>(sB + lrow * LDK + lhalf * 32);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 sb[i] = bv[slot] ? make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3])
                                  : make_uint4(0, 0, 0, 0);
+            sD[lhalf][lrow] = bv[slot] ? d : 0.0f;
         }
         __syncthreads();
         if constexpr (decltype(prefetch)::value) load(kt + PF, slot);
+        // MFMA operand layout (32x32x16 f16): lane l holds row l % 32 and the 8 K values
+        // 8 (l / 32) .. + 7 of the 16; D[i][j]: column j = l % 32, rows 8 (r / 4) +
+        // 4 (l / 32) + r % 4
 #pragma unroll
-        for (int k16 = 0; k16 < BK / 16; ++k16) {
-            half8 a[MI], b[2];
+        for (int kb = 0; kb < 2; ++kb) {  // the K step's two quant blocks
+            const float16v zero = {};
+            float16v blk[MI][2];
 #pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const uint16_t* pa = sA + (wm * (BM / 2) + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
-                a[i] = *reinterpret_cast<const half8*>(pa);
-            }
+            for (int h = 0; h < 2; ++h) {
+                const int kk = kb * 32 + h * 16 + 8 * (lane >> 5);
+                half8 ah[MI], al[MI], b[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint16_t* pb = sB + (wn * 64 + i * 32 + (lane & 31)) * LDK + k16 * 16 + 8 * (lane >> 5);
-                b[i] = *reinterpret_cast<const half8*>(pb);
-            }
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
+                for (int i = 0; i < MI; ++i) {
+                    const int ro = (wm * (BM / 2) + i * 32 + (lane & 31)) * LDK + kk;
+                    ah[i] = *reinterpret_cast<const half8*>(sAh + ro);
+                    al[i] = *reinterpret_cast<const half8*>(sAl + ro);
+                }
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                    b[j] = *reinterpret_cast<const half8*>(sB + (wn * 64 + j * 32 + (lane & 31)) * LDK + kk);
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], h ? blk[i][j] : zero, 0, 0, 0);
+                        blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], blk[i][j], 0, 0, 0);
+                    }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float dw = sD[kb][wn * 64 + j * 32 + (lane & 31)];
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(dw, blk[i][j][r], acc[i][j][r]);
+            }
         }
     };
 
@@ -333,7 +350,7 @@ int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t ld
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
          float* dst, int64_t ldd, float* part, hipStream_t s) {
     if ((reinterpret_cast<uintptr_t>(W) & 3) != 0) return fail(GQ_ERR_INVALID, "gemm: weight not 4-byte aligned");
-    if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0)
+    if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0 || lda < 2 * K)
         return fail(GQ_ERR_INVALID, "gemm: activation tile misaligned");
     if (gemm_plan(N, K, M).ks > 1 && part == nullptr) return fail(GQ_ERR_WORKSPACE, "gemm: split K needs partials");
     if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, part, s);

@@ -13,7 +13,9 @@ int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_str
                          hipStream_t s);
 // The GEMM path's fused activation prologue (quantize.hip): per row of x (row stride xs),
 // x + d (stored to sum when given) or SWIGLU of the row's halves (glu: x rows are 2K
-// wide), then RMS_NORM (rms), then fp16(d * q) of quantize_row_q8_0 into y.
+// wide), then RMS_NORM (rms), then d * q of quantize_row_q8_0 into y as the exact fp16
+// pair hi + lo (split_dq8): hi at y[m * y_stride + k], lo at y[m * y_stride + K + k]
+// (y_stride >= 2K). quantize_q8_0_f16 writes the same without the neighbours.
 constexpr int64_t PREP_MAX_K = 16384;
 struct ActPrep {
     const float* x;

@@ -50,17 +50,12 @@ __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             qp[i] = (uint16_t)((q[2 * i] & 0xff) | ((q[2 * i + 1] & 0xff) << 8));
-    } else {  // OUT_F16: fp16(d * q), the GEMM's A operand
-        const float df = h2f(dh);
-        uint16_t hv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hv[i] = f2h((float)q[i] * df);
-        uint4 pk;
-        pk.x = hv[0] | ((uint32_t)hv[1] << 16);
-        pk.y = hv[2] | ((uint32_t)hv[3] << 16);
-        pk.z = hv[4] | ((uint32_t)hv[5] << 16);
-        pk.w = hv[6] | ((uint32_t)hv[7] << 16);
-        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + m * y_stride + b * QK + part * 8) = pk;
+    } else {  // OUT_F16: the GEMM's A operand, d * q as fp16 hi (at k) + lo (at K + k) of the row
+        uint4 hi, lo;
+        split_dq8(q, dh, hi, lo);
+        uint16_t* row = reinterpret_cast<uint16_t*>(y) + m * y_stride + b * QK + part * 8;
+        *reinterpret_cast<uint4*>(row) = hi;
+        *reinterpret_cast<uint4*>(row + K) = lo;
     }
 }
 
@@ -95,7 +90,7 @@ int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride
 // (v * scale, the sum of squares in the order of k_rms_norm) or SWIGLU of the row's
 // halves (silu(x[c]) * x[K + c], the arithmetic of k_swiglu), then the fp16(d * q)
 // of quantize_row_q8_0 — the bits of ADD -> RMS_NORM -> quantize (or SWIGLU ->
-// quantize) run one by one. Thread t holds elements c * 2048 + 8t.. of every 2048-wide
+// quantize) run one by one — written as the exact fp16 pair hi (row[k]) + lo (row[K + k]). Thread t holds elements c * 2048 + 8t.. of every 2048-wide
 // chunk c in registers (K <= PREP_MAX_K).
 constexpr int PREP_CH = PREP_MAX_K / 2048;
 
@@ -159,16 +154,11 @@ __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restric
         int qsum;
         quant8_block(v[c], q, dh, qsum);  // all lanes: pieces past K quantize zeros
         if ((t >> 2) >= nb) continue;
-        const float df = h2f(dh);
-        uint16_t hv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hv[i] = f2h((float)q[i] * df);
-        uint4 pk;
-        pk.x = hv[0] | ((uint32_t)hv[1] << 16);
-        pk.y = hv[2] | ((uint32_t)hv[3] << 16);
-        pk.z = hv[4] | ((uint32_t)hv[5] << 16);
-        pk.w = hv[6] | ((uint32_t)hv[7] << 16);
-        *reinterpret_cast<uint4*>(y + m * y_stride + (int64_t)t * 8) = pk;
+        uint4 hi, lo;
+        split_dq8(q, dh, hi, lo);
+        uint16_t* row = y + m * y_stride + (int64_t)t * 8;
+        *reinterpret_cast<uint4*>(row) = hi;
+        *reinterpret_cast<uint4*>(row + a.K) = lo;
     }
 }
 

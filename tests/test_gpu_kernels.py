@@ -1,8 +1,9 @@
 """Parity of the HIP path (through the C ABI) with the oracle and the reference's
 golden vectors. Needs an MI355X.
 
-Bars (north star): quantize_row_q8_0 and set_rows bit-exact; mul_mat within
-max-abs-rel 1e-3 (max|d| / max|ref|); attention within 1e-3 of the exact
+Bars: quantize_row_q8_0 and set_rows bit-exact; mul_mat within max-abs-rel 1e-5
+(max|d| / max|ref|; the north star asks 1e-3: both paths form every block product
+exactly, so only fp32 accumulation order differs); attention within 1e-3 of the exact
 softmax, and within the reference's own deviation from it when compared to
 the reference (its decode path accumulates V in fp16).
 """
@@ -90,7 +91,7 @@ def test_mul_mat_golden(golden_dir):
         y = ops.mul_mat(w, to_dev(g["x"])).cpu().numpy()
         r = mar(y, g["y"])
         print(f.name, f"{r:.2e}")
-        assert r < 1e-3, (f.name, r)
+        assert r < 1e-5, (f.name, r)
 
 
 def _check_mm(qtype, K, N, M, rows_checked=256, seed=0):
@@ -106,7 +107,7 @@ def _check_mm(qtype, K, N, M, rows_checked=256, seed=0):
     want = O.mul_mat(wq_sel, qtype, K, x[msel])
     r = mar(y[np.ix_(msel, sel)], want)
     print(f"qtype={qtype} K={K} N={N} M={M}: max-abs-rel {r:.2e}")
-    assert r < 1e-3
+    assert r < 1e-5
     return r
 
 
@@ -141,7 +142,7 @@ def test_mul_mat_strided_rows():
     xt = to_dev(big)[:, :, :K]
     y = ops.mul_mat(qw, xt).cpu().numpy()
     want = O.mul_mat(qw.data.cpu().numpy(), O.Q8_0, K, big[:, :, :K].reshape(-1, K)).reshape(2, 3, N)
-    assert mar(y, want) < 1e-3
+    assert mar(y, want) < 1e-5
 
 
 @pytest.mark.parametrize("qtype,K,N,M,rms,glu,add", [

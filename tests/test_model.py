@@ -5,7 +5,7 @@ Two kinds of check:
 
 * op by op (teacher-forced): every op of every layer of a traced step is recomputed on
   the CPU from the inputs the GPU step actually used, to the per-op bars: Q8_0/Q4_0
-  MUL_MAT and FLASH_ATTN_EXT within max-abs-rel 1e-3, SET_ROWS bit-exact, the last
+  MUL_MAT within max-abs-rel 1e-5, FLASH_ATTN_EXT within 1e-3, SET_ROWS bit-exact, the last
   token's logits at cosine >= 0.99999. This pins the wiring of the graph (views, permutes,
   positions, masks, residuals) at the tolerance the ops are held to.
 * end to end: chunked prefill then greedy decode with the persistent KV cache, eager and
@@ -203,7 +203,7 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
         g = lambda n: T[(n, li)]  # noqa: E731
         x_in = g("x_in")
         bar("rms_norm", g("h1"), _rms(x_in, cfg.rms_eps), 1e-5)
-        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1")), 1e-3)
+        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1")), 1e-5)
         qkv = g("qkv")
         qh = qkv[:, :qd].reshape(s, cfg.n_head, cfg.head_dim)
         kh = qkv[:, qd:qd + kvd].reshape(s, cfg.n_head_kv, cfg.head_dim)
@@ -224,16 +224,16 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
         want = O.flash_attn_ext_f16(g("q")[0].transpose(1, 0, 2), kc[0], vc[0], n_kv, mask,
                                     1.0 / math.sqrt(cfg.head_dim), mode=1)
         bar("flash_attn_ext", g("attn"), want, 1e-3)
-        bar("mul_mat o + add", g("x_mid"), x_in + O.mul_mat(wo, t, qd, g("attn").reshape(s, qd)), 1e-3)
+        bar("mul_mat o + add", g("x_mid"), x_in + O.mul_mat(wo, t, qd, g("attn").reshape(s, qd)), 1e-5)
         bar("rms_norm", g("h2"), _rms(g("x_mid"), cfg.rms_eps), 1e-5)
-        bar("mul_mat gate_up", g("gu"), O.mul_mat(wgu, t, cfg.n_embd, g("h2")), 1e-3)
+        bar("mul_mat gate_up", g("gu"), O.mul_mat(wgu, t, cfg.n_embd, g("h2")), 1e-5)
         bar("swiglu", g("act"), _swiglu(g("gu"), cfg.n_ff), 1e-5)
-        bar("mul_mat down + add", g("x_out"), g("x_mid") + O.mul_mat(wd, t, cfg.n_ff, g("act")), 1e-3)
+        bar("mul_mat down + add", g("x_out"), g("x_mid") + O.mul_mat(wd, t, cfg.n_ff, g("act")), 1e-5)
     x_last = T[("x_out", len(host[2]) - 1)][s - 1:]
     bar("rms_norm", T[("hf", -1)], _rms(x_last, cfg.rms_eps), 1e-5)
     logits = T[("logits", -1)][0]
     want = O.mul_mat(host[1], t, cfg.n_embd, T[("hf", -1)])[0]
-    bar("mul_mat lm_head", logits, want, 1e-3)
+    bar("mul_mat lm_head", logits, want, 1e-5)
     assert _cos(logits, want) >= 0.99999
     assert int(T[("next", -1)][0]) == int(np.argmax(logits))
     return worst
