@@ -613,10 +613,10 @@ def cpu_baseline(w, cfg, seconds: float) -> dict:
     import numpy as np
 
     import oracle as O
+    from ggmlc_amd.model import host_weights
 
     cores = O.n_cpu_threads()
-    host = (w.embed.data.cpu().numpy(), w.lm_head.data.cpu().numpy(),
-            [tuple(m.data.cpu().numpy() for m in (L.qkv, L.o, L.gate_up, L.down)) for L in w.layers])
+    host = host_weights(w)
     prompt = np.random.default_rng(5).integers(0, cfg.n_vocab, UBATCH).astype(np.int32)
     if O.ref_available():
         rl = O.RefLlama(cfg, host, 1024, n_threads=cores)

@@ -69,6 +69,7 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("b_swiglu", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("bias", ctypes.POINTER(gq_tensor)),
     ]
 
 

@@ -19,10 +19,14 @@ restated for the decoders this package runs, with the same results:
 * RMS_NORM carries the module's eps as an attribute, as the PyTorch importer writes it
   (frontend/pytorch/importer.py:1041-1053), except the runtime's default 1e-5.
 
+* Linear biases stay fp32 and feed the MUL_MAT node's third input (dialect/ggml/
+  lowering.py:462-475), those of a fused group concatenated like its rows (the Qwen2
+  family's q/k/v biases).
+
 Supported: LlamaForCausalLM-shaped modules (model.embed_tokens, model.layers[i].
 {input_layernorm, self_attn.{q,k,v,o}_proj, post_attention_layernorm,
-mlp.{gate,up,down}_proj}, model.norm, lm_head) without biases and with the default
-rotary embedding (NEOX pairs over the whole head); anything else raises
+mlp.{gate,up,down}_proj}, model.norm, lm_head), Qwen2ForCausalLM included, with the
+default rotary embedding (NEOX pairs over the whole head); anything else raises
 NotImplementedError naming what does not fit.
 """
 
@@ -113,17 +117,31 @@ def compile_llama(model, path: str | Path, quantize: str = "q8_0", max_pos: int 
     cfg = llama_config_of(model, qt, name)
     body = model.model
     layers = []
+
+    def biases(lins, what):
+        """the fp32 biases of a fused group, concatenated like the rows (fusion.py:1347-1390)"""
+        bs = [getattr(lin, "bias", None) for lin in lins]
+        if all(b is None for b in bs):
+            return None
+        _need(all(b is not None for b in bs), f"{what}: biases on some projections of a fused group only")
+        return np.concatenate([_f32(b) for b in bs]).astype(np.float32)
+
     for li, L in enumerate(body.layers):
         at, mlp = L.self_attn, L.mlp
-        for lin in (at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj):
-            _need(getattr(lin, "bias", None) is None, f"layer {li}: Linear biases")
         g1, g2 = _f32(L.input_layernorm.weight), _f32(L.post_attention_layernorm.weight)
         qkv = np.concatenate([_f32(at.q_proj.weight), _f32(at.k_proj.weight), _f32(at.v_proj.weight)], axis=0)
         gu = np.concatenate([_f32(mlp.gate_proj.weight), _f32(mlp.up_proj.weight)], axis=0)
         _need(qkv.shape == (cfg.q_dim + 2 * cfg.kv_dim, cfg.n_embd), f"layer {li}: q/k/v shapes")
         _need(gu.shape == (2 * cfg.n_ff, cfg.n_embd), f"layer {li}: gate/up shapes")
+        # the RMS bake scales W's input columns only: a bias is added after the product
         layers.append((quantize_rows(qkv * g1[None, :], qt), quantize_rows(_f32(at.o_proj.weight), qt),
-                       quantize_rows(gu * g2[None, :], qt), quantize_rows(_f32(mlp.down_proj.weight), qt)))
+                       quantize_rows(gu * g2[None, :], qt), quantize_rows(_f32(mlp.down_proj.weight), qt),
+                       biases((at.q_proj, at.k_proj, at.v_proj), f"layer {li} q/k/v"),
+                       biases((at.o_proj,), f"layer {li} o"),
+                       biases((mlp.gate_proj, mlp.up_proj), f"layer {li} gate/up"),
+                       biases((mlp.down_proj,), f"layer {li} down")))
+    cfg.qkv_bias = layers[0][4] is not None if layers else False
+    _need(getattr(model.lm_head, "bias", None) is None, "an output head with a bias")
     emb = _f32(body.embed_tokens.weight)
     gf = _f32(body.norm.weight)
     embed_q = quantize_rows(emb, qt)

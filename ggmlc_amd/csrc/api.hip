@@ -229,6 +229,19 @@ static int rope_kv_epilogue(const gq_rope_kv_epilogue& e, const MulMatPlan& p, c
     return GQ_OK;
 }
 
+// the bias of MUL_MAT's bias ADD: F32 [N] (one row, broadcast over the activation rows)
+static int fused_bias(const gq_mul_mat_fusion* f, const MulMatPlan& p, const float** out) {
+    *out = nullptr;
+    if (!f->bias) return GQ_OK;
+    const gq_tensor* t = f->bias;
+    if (t->type != GQ_TYPE_F32 || t->ne[0] != p.N || t->ne[1] != 1 || t->ne[2] != 1 || t->ne[3] != 1 ||
+        t->nb[0] != 4 || !t->data)
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: bias must be F32 [N, 1, 1, 1] with N = " + std::to_string(p.N) +
+                                        ": " + shape(t));
+    *out = static_cast<const float*>(t->data);
+    return GQ_OK;
+}
+
 // b as the product's input: with b_swiglu its rows hold 2K values and the input is
 // SWIGLU of their halves, so the plan sees the first half
 static int fused_plan(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f, MulMatPlan& p) {
@@ -257,6 +270,8 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
     if (p.K > PREP_MAX_K) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: K above the prologue's limit");
     if (f->b_swiglu && (f->rms_norm || f->b_add))
         return fail(GQ_ERR_INVALID, "mul_mat_fused: b_swiglu excludes rms_norm and b_add");
+    const float* bias = nullptr;
+    if (int rc = fused_bias(f, p, &bias)) return rc;
     if (dst->type != GQ_TYPE_F32 || dst->ne[0] != p.N || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
         dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
         return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [N, M, ...]: " + shape(dst));
@@ -294,7 +309,7 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
     if (rc) return rc;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(f->workspace) + p.ws_act);
     return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, 2 * p.K, p.M,
-                static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), part, s);
+                static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), part, s, bias);
 }
 
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
@@ -310,6 +325,8 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     if (p.M > GEMV_MAX_M) return mul_mat_fused_gemm(a, b, dst, f, p, (hipStream_t)stream);
     if (f->b_swiglu) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: b_swiglu needs M > 4 (use swiglu on the producer)");
     GemvFuse fz;
+    rc = fused_bias(f, p, &fz.bias);
+    if (rc) return rc;
     if (f->rope_kv) {
         rc = rope_kv_epilogue(*f->rope_kv, p, b, fz);
         if (rc) return rc;

@@ -121,7 +121,8 @@ template <int QT, int BM, int PF>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                  int64_t row_bytes, const uint16_t* __restrict__ A,
                                                  int64_t lda, int64_t M, float* __restrict__ dst,
-                                                 int64_t ldd, int spk, float* __restrict__ part) {
+                                                 int64_t ldd, int spk, float* __restrict__ part,
+                                                 const float* __restrict__ bias) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int MI = BM / 64;        // 32-row MFMA tiles per wave along M
     constexpr int AQ = BM / 32;        // 16-byte activation pieces per thread per K step (each of hi, lo)
@@ -254,9 +255,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
 #pragma unroll
     for (int p = 0; p < PF - 1; ++p)
         if (kt + p < kt1) step(kt + p, p, std::false_type{});
-    if (part) {  // split K: this workgroup's partial tile
+    if (part) {  // split K: this workgroup's partial tile; the reduce adds the bias
         dst = part + (int64_t)blockIdx.z * M * N;
         ldd = N;
+        bias = nullptr;
     }
 
     // D[i][j]: lane holds column j = lane % 32, rows i = 8*(r/4) + 4*(lane/32) + r%4
@@ -266,23 +268,25 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
         for (int j = 0; j < 2; ++j) {
             const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
             if (n >= N) continue;
+            const float bn_ = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M) dst[m * ldd + n] = acc[i][j][r];
+                if (m < M) dst[m * ldd + n] = bias ? acc[i][j][r] + bn_ : acc[i][j][r];
             }
         }
 }
 
-// dst[m * ldd + n] = sum_z part[z][m][n], z in order
+// dst[m * ldd + n] = sum_z part[z][m][n], z in order (+ bias[n])
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int ks, int64_t M, int64_t N,
-                                                     float* __restrict__ dst, int64_t ldd) {
+                                                     float* __restrict__ dst, int64_t ldd,
+                                                     const float* __restrict__ bias) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= M * N) return;
     const int64_t m = i / N, n = i - m * N;
     float acc = part[i];
     for (int z = 1; z < ks; ++z) acc += part[(int64_t)z * M * N + i];
-    dst[m * ldd + n] = acc;
+    dst[m * ldd + n] = bias ? acc + bias[n] : acc;
 }
 
 int num_cus() {
@@ -326,35 +330,35 @@ namespace {
 
 template <int QT>
 int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M, float* dst,
-           int64_t ldd, float* part, hipStream_t s) {
+           int64_t ldd, float* part, hipStream_t s, const float* bias) {
     const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
     const GemmPlan p = gemm_plan(N, K, M);
     float* pp = p.ks > 1 ? part : nullptr;
     if (p.bm == 64) {
         const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 64), (unsigned)p.ks);
         hipLaunchKernelGGL((k_gemm<QT, 64, GEMM_PF_64>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
-                           ldd, p.spk, pp);
+                           ldd, p.spk, pp, bias);
     } else {
         const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 128), (unsigned)p.ks);
         hipLaunchKernelGGL((k_gemm<QT, 128, GEMM_PF_128>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
-                           ldd, p.spk, pp);
+                           ldd, p.spk, pp, bias);
     }
     int rc = check_hip(hipGetLastError(), "gemm launch");
     if (rc != GQ_OK || p.ks == 1) return rc;
-    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, s, part, p.ks, M, N, dst, ldd);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, s, part, p.ks, M, N, dst, ldd, bias);
     return check_hip(hipGetLastError(), "gemm reduce launch");
 }
 
 }  // namespace
 
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
-         float* dst, int64_t ldd, float* part, hipStream_t s) {
+         float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias) {
     if ((reinterpret_cast<uintptr_t>(W) & 3) != 0) return fail(GQ_ERR_INVALID, "gemm: weight not 4-byte aligned");
     if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0 || lda < 2 * K)
         return fail(GQ_ERR_INVALID, "gemm: activation tile misaligned");
     if (gemm_plan(N, K, M).ks > 1 && part == nullptr) return fail(GQ_ERR_WORKSPACE, "gemm: split K needs partials");
-    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, part, s);
-    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, M, dst, ldd, part, s);
+    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, part, s, bias);
+    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, M, dst, ldd, part, s, bias);
 }
 
 }  // namespace gq

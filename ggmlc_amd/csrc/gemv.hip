@@ -247,10 +247,15 @@ __device__ __forceinline__ void rope_emit(const GemvRope& r, const float2* tab, 
 
 // Write logical row `row` of activation m: plain, residual-added (res + v: the
 // operand order of ADD(x, MUL_MAT)), or, for the paired epilogues (SWIGLU, rope),
-// from the even row with its partner's value vp.
+// from the even row with its partner's value vp. A bias is added to the product first
+// (v + bias: the operand order of ADD(MUL_MAT, bias), executor.cpp:2436-2445).
 template <int M>
 __device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, float* dst, int64_t ldd, int m,
                                      int64_t row, float v, float vp) {
+    if (fz.bias) {
+        v = v + fz.bias[phys_row(fz, row)];
+        if (fz.glu | fz.rope) vp = vp + fz.bias[phys_row(fz, row ^ 1)];
+    }
     if (fz.glu) {
         if ((row & 1) == 0) dst[(int64_t)m * ldd + (row >> 1)] = swiglu_f(v, vp);
         return;

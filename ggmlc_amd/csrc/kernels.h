@@ -76,21 +76,22 @@ struct GemvFuse {
     int64_t pair_lo = 0, pair_h = 0;
     const float* res = nullptr;
     int64_t ldr = 0;
+    const float* bias = nullptr;  // [N] added to the product first (MUL_MAT's bias ADD)
     GemvRope rp{};
 };
 int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
          const GemvFuse& fz, hipStream_t s);
 
-// gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k], A fp16; grids with
-// fewer tiles than CUs split K over ks workgroups whose partials (part, part_bytes) are summed
-// in order by a second kernel
+// gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k] (+ bias[n]), A the
+// fp16 hi + lo rows of the activation prologue; grids with fewer tiles than CUs split K over
+// ks workgroups whose partials (part, part_bytes) are summed in order by a second kernel
 struct GemmPlan {
     int bm, ks, spk;
     size_t part_bytes;
 };
 GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M);
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
-         float* dst, int64_t ldd, float* part, hipStream_t s);
+         float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias = nullptr);
 
 // set_rows.hip
 struct SetRowsArgs {

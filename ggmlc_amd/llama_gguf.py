@@ -36,10 +36,15 @@ GLU_SWIGLU = 2  # enum ggml_glu_op
 ROPE_NEOX = 2
 
 
-def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_qkv: bool = True) -> Graph:
+def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_qkv: bool = True,
+                biases: frozenset = frozenset()) -> Graph:
     """The execution graph of `cfg` (a model.LlamaConfig); wtypes maps a weight name
     to its ggml type (default cfg.qtype). fused_qkv=False emits three projections
-    (attn_q, attn_k, attn_v) instead of the fused one and its VIEWs."""
+    (attn_q, attn_k, attn_v) instead of the fused one and its VIEWs. biases names the
+    projections ("qkv", "o", "gate_up", "down") whose MUL_MAT takes an F32 bias as its
+    third input, as ggmlc's lowering of a Linear with bias emits it
+    (dialect/ggml/lowering.py:462-475; fused q | k | v biases concatenated like the
+    weight rows, transforms/fusion.py:1347-1390)."""
     g = Graph(name=cfg.name, symbol_table=["s"])
     s = Dim.symbol("s")
     E, hd, Hq, Hkv, F, V = cfg.n_embd, cfg.head_dim, cfg.n_head, cfg.n_head_kv, cfg.n_ff, cfg.n_vocab
@@ -47,6 +52,9 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
 
     def act(name, ne):
         return g.add_tensor(name, F32, ne, ACTIVATION)
+
+    def bias(name, n, which):
+        return [g.add_tensor(name, F32, [n], PARAMETER, role="parameter")] if which in biases else []
 
     ids = g.add_tensor("input_ids", I32, [s, 1], INPUT)
     embd = g.add_tensor("tok_embd", wt("tok_embd"), [E, V], PARAMETER, role="parameter")
@@ -67,13 +75,14 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
         w_d = g.add_tensor(p + "ffn_down", wt("ffn_down"), [F, E], PARAMETER, role="parameter")
         h = g.add_node("RMS_NORM", [x], act(p + "attn_norm", [E, s]), **eps)
         if fused_qkv:
-            qkv = g.add_node("MUL_MAT", [w_qkv, h], act(p + "qkv", [nq, s]))
+            qkv = g.add_node("MUL_MAT", [w_qkv, h] + bias(p + "attn_qkv.bias", nq, "qkv"), act(p + "qkv", [nq, s]))
         heads = {}
         for nm, H, start in (("q", Hq, 0), ("k", Hkv, Hq * hd), ("v", Hkv, (Hq + Hkv) * hd)):
             if fused_qkv:
                 src = g.add_node("VIEW", [qkv], act(p + nm + "_view", [H * hd, s]), ggml_dim=0, start=start)
             else:
-                src = g.add_node("MUL_MAT", [w_sep[nm], h], act(p + nm + "_proj", [H * hd, s]))
+                src = g.add_node("MUL_MAT", [w_sep[nm], h] + bias(p + "attn_" + nm + ".bias", H * hd, "qkv"),
+                                 act(p + nm + "_proj", [H * hd, s]))
             heads[nm] = g.add_node("RESHAPE", [src], act(p + nm + "_3d", [hd, H, s]))
         for nm in ("q", "k"):
             heads[nm] = g.add_node("ROPE", [heads[nm], pos], act(p + nm + "_rope", [hd, Hq if nm == "q" else Hkv, s]),
@@ -85,12 +94,13 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
         a = g.add_node("FLASH_ATTN_EXT", [perm["q"], perm["k"], perm["v"]], act(p + "attn", [hd, Hq, s]),
                        scale=1.0 / math.sqrt(hd), fused_transpose=1, is_causal=1)
         a2 = g.add_node("RESHAPE", [a], act(p + "attn_2d", [Hq * hd, s]))
-        o = g.add_node("MUL_MAT", [w_o, a2], act(p + "attn_out", [E, s]))
+        o = g.add_node("MUL_MAT", [w_o, a2] + bias(p + "attn_output.bias", E, "o"), act(p + "attn_out", [E, s]))
         x = g.add_node("ADD", [x, o], act(p + "ffn_inp", [E, s]))
         h2 = g.add_node("RMS_NORM", [x], act(p + "ffn_norm", [E, s]), **eps)
-        gu = g.add_node("MUL_MAT", [w_gu, h2], act(p + "ffn_gate_up_out", [2 * F, s]))
+        gu = g.add_node("MUL_MAT", [w_gu, h2] + bias(p + "ffn_gate_up.bias", 2 * F, "gate_up"),
+                        act(p + "ffn_gate_up_out", [2 * F, s]))
         sw = g.add_node("GLU", [gu], act(p + "ffn_act", [F, s]), op=GLU_SWIGLU)
-        d = g.add_node("MUL_MAT", [w_d, sw], act(p + "ffn_out", [E, s]))
+        d = g.add_node("MUL_MAT", [w_d, sw] + bias(p + "ffn_down.bias", E, "down"), act(p + "ffn_out", [E, s]))
         x = g.add_node("ADD", [x, d], act(p + "l_out", [E, s]))
     hf = g.add_node("RMS_NORM", [x], act("result_norm", [E, s]), **eps)
     w_lm = embd if cfg.tied_embeddings else g.add_tensor("output", wt("output"), [E, V], PARAMETER,
@@ -104,9 +114,16 @@ def llama_graph(cfg, max_pos: int, wtypes: dict[str, int] | None = None, fused_q
 
 def write_llama_gguf(path: str | Path, cfg, weights, max_pos: int = 4096, fused_qkv: bool = True) -> Path:
     """Write cfg's decoder with host weights = (embed, lm_head, [(qkv, o, gate_up, down), ...])
-    (uint8 GGUF block rows, as model.ModelWeights holds them) to a .gguf file."""
+    (uint8 GGUF block rows, as model.ModelWeights holds them) to a .gguf file. A layer
+    tuple may carry the four projections' fp32 biases after them (None where absent;
+    model.host_weights), written as F32 tensors feeding the MUL_MATs' third input."""
     embed, lm_head, layers = weights
-    g = llama_graph(cfg, max_pos, fused_qkv=fused_qkv)
+    names = ("qkv", "o", "gate_up", "down")
+    biases = frozenset(nm for nm, b in zip(names, layers[0][4:8]) if b is not None) if layers else frozenset()
+    for L in layers:
+        if frozenset(nm for nm, b in zip(names, L[4:8]) if b is not None) != biases:
+            raise ValueError("every layer must carry the same projection biases")
+    g = llama_graph(cfg, max_pos, fused_qkv=fused_qkv, biases=biases)
     w = GGUFWriter()
     w.add_string("general.architecture", "ggmlc")
     w.add_string("general.name", g.name)
@@ -121,6 +138,13 @@ def write_llama_gguf(path: str | Path, cfg, weights, max_pos: int = 4096, fused_
         qkv = np.asarray(L[0])  # rows q | k | v: the separate projections are row slices
         data[f"blk.{li}.attn_q"], data[f"blk.{li}.attn_k"], data[f"blk.{li}.attn_v"] = \
             qkv[:qd], qkv[qd:qd + kvd], qkv[qd + kvd:]
+        for nm, b in zip(("attn_qkv", "attn_output", "ffn_gate_up", "ffn_down"), L[4:8]):
+            if b is not None:
+                data[f"blk.{li}.{nm}.bias"] = np.asarray(b, np.float32)
+        if L[4:5] and L[4] is not None:
+            bq = np.asarray(L[4], np.float32)
+            data[f"blk.{li}.attn_q.bias"], data[f"blk.{li}.attn_k.bias"], data[f"blk.{li}.attn_v.bias"] = \
+                bq[:qd], bq[qd:qd + kvd], bq[qd + kvd:]
     for tid in sorted(g.tensors):
         t = g.tensors[tid]
         if t.name not in data:
@@ -128,6 +152,8 @@ def write_llama_gguf(path: str | Path, cfg, weights, max_pos: int = 4096, fused_
         arr = np.ascontiguousarray(data[t.name])
         if t.name == "rope_arange":
             ne = [max_pos]
+        elif t.name.endswith(".bias"):
+            ne = [arr.size]
         else:
             ne = [d.evaluate({}) for d in t.ne[:2]]
         w.add_tensor(t.name, ne + [1] * (4 - len(ne)), t.type, arr.view(np.uint8).reshape(-1))

@@ -47,6 +47,7 @@ class LlamaConfig:
     tied_embeddings: bool = False
     rms_eps: float = 1e-5
     rope_base: float = 10000.0
+    qkv_bias: bool = False  # q/k/v projections carry biases (the Qwen2 family)
 
     @property
     def q_dim(self) -> int:
@@ -60,8 +61,9 @@ class LlamaConfig:
 # BASELINE.json configs[2] and configs[3]
 SMOLLM2_360M = LlamaConfig("smollm2-360m-shape", 32, 960, 15, 5, 64, 2560, 49152, ops.Q8_0, tied_embeddings=True)
 LLAMA_7B = LlamaConfig("llama-7b-shape", 32, 4096, 32, 32, 128, 11008, 32000, ops.Q4_0)
-# configs[4] (used for its shapes; continuous batching is not built)
-QWEN25_1_5B = LlamaConfig("qwen2.5-1.5b-shape", 28, 1536, 12, 2, 128, 8960, 151936, ops.Q8_0, tied_embeddings=True)
+# the Qwen2 architecture, q/k/v biases included
+QWEN25_1_5B = LlamaConfig("qwen2.5-1.5b-shape", 28, 1536, 12, 2, 128, 8960, 151936, ops.Q8_0, tied_embeddings=True,
+                          qkv_bias=True)
 
 
 class _Recorder:
@@ -89,6 +91,12 @@ class LayerWeights:
     o: ops.QWeight
     gate_up: ops.QWeight
     down: ops.QWeight
+    # the MUL_MAT nodes' bias inputs (fp32 [N] device tensors, e.g. Qwen2's q/k/v biases,
+    # concatenated q | k | v like the weight rows): ADD(MUL_MAT(W, x), bias)
+    qkv_b: torch.Tensor | None = None
+    o_b: torch.Tensor | None = None
+    gate_up_b: torch.Tensor | None = None
+    down_b: torch.Tensor | None = None
 
 
 @dataclass
@@ -114,10 +122,12 @@ class ModelWeights:
         return n
 
 
-def random_weights(cfg: LlamaConfig, device, seed: int = 0, std: float = 0.02) -> ModelWeights:
+def random_weights(cfg: LlamaConfig, device, seed: int = 0, std: float = 0.02, bias_std: float = 0.1) -> ModelWeights:
     """Random-init weights N(0, std) quantized on the device with ggmlc's quantizer
     (quantize.py semantics). RMSNorm weights are 1 at init, so the fused graph's
-    baked-in gamma leaves the Linear weights unchanged."""
+    baked-in gamma leaves the Linear weights unchanged. With cfg.qkv_bias the fused
+    q | k | v projection gets an fp32 bias N(0, bias_std) (the quantizer keeps 1-d
+    parameters in fp32)."""
     g = torch.Generator(device=device)
     g.manual_seed(seed)
 
@@ -136,8 +146,27 @@ def random_weights(cfg: LlamaConfig, device, seed: int = 0, std: float = 0.02) -
             o=q(cfg.n_embd, cfg.q_dim),
             gate_up=q(2 * cfg.n_ff, cfg.n_embd),
             down=q(cfg.n_embd, cfg.n_ff),
+            qkv_b=(torch.randn(cfg.q_dim + 2 * cfg.kv_dim, generator=g, device=device) * bias_std
+                   if cfg.qkv_bias else None),
         ))
     return ModelWeights(cfg, embed, lm_head, layers)
+
+
+def host_weights(w: ModelWeights) -> tuple:
+    """(embed, lm_head, [(qkv, o, gate_up, down, qkv_b, o_b, gate_up_b, down_b), ...]) on the
+    host: the GGUF block bytes (uint8) and the fp32 biases (None where absent)."""
+    def np_(t):
+        return None if t is None else t.cpu().numpy()
+
+    return (np_(w.embed.data), np_(w.lm_head.data),
+            [tuple(np_(m.data) for m in (L.qkv, L.o, L.gate_up, L.down)) +
+             tuple(np_(b) for b in (L.qkv_b, L.o_b, L.gate_up_b, L.down_b)) for L in w.layers])
+
+
+def _linear(wt: ops.QWeight, bias: torch.Tensor | None, x: torch.Tensor, out: torch.Tensor, ws) -> torch.Tensor:
+    """MUL_MAT(W, x) (+ bias: the node's ADD, executor.cpp:2436-2445) as separate ops"""
+    y = ops.mul_mat(wt, x, out=out, ws=ws)
+    return ops.add(y, bias, out=y) if bias is not None else y
 
 
 def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, v_cache: list, attend, fused: bool,
@@ -167,19 +196,20 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             nx = other[id(x)] if pending is not None else None
             ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=ops.RopeKv(
                 c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"],
-                b["q"], k_cache[li], v_cache[li], cache=b["rope_cs"]))
+                b["q"], k_cache[li], v_cache[li], cache=b["rope_cs"]), bias=L.qkv_b)
             x = nx if nx is not None else x
             q = b["q"]
         else:
             if pro:  # ADD + RMS_NORM in the QKV GEMM's prologue
                 nx = other[id(x)] if pending is not None else None
-                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws)
+                qkv = ops.mul_mat_fused(L.qkv, x, out=b["qkv"], rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws,
+                                        bias=L.qkv_b)
                 x = nx if nx is not None else x
             else:
                 rec("x_in", li, x)
                 h = ops.rms_norm(x, c.rms_eps, out=b["h"])
                 rec("h1", li, h)
-                qkv = ops.mul_mat(L.qkv, h, out=b["qkv"], ws=ws)
+                qkv = _linear(L.qkv, L.qkv_b, h, b["qkv"], ws)
                 rec("qkv", li, qkv)
             # views of the fused projection (ggml VIEW/RESHAPE, executor.cpp:75-113)
             qv = qkv[:, :qd].view(1, s, c.n_head, c.head_dim)
@@ -198,28 +228,30 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
         attend(li, q)
         rec("attn", li, b["attn"])
         if fused:
-            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"])
+            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], bias=L.o_b)
             nx = other[id(x)]
-            a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx)
+            a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx,
+                                  bias=L.gate_up_b)
             x = nx
-            pending = ops.mul_mat_fused(L.down, a, out=b["proj"])
+            pending = ops.mul_mat_fused(L.down, a, out=b["proj"], bias=L.down_b)
         elif pro:  # ADD + RMS_NORM before gate_up, SWIGLU before down, in their prologues
-            o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
+            o = _linear(L.o, L.o_b, b["attn"].view(s, qd), b["proj"], ws)
             nx = other[id(x)]
-            gu = ops.mul_mat_fused(L.gate_up, x, out=b["gu"], rms_eps=c.rms_eps, x_add=o, x_sum=nx, ws=ws)
+            gu = ops.mul_mat_fused(L.gate_up, x, out=b["gu"], rms_eps=c.rms_eps, x_add=o, x_sum=nx, ws=ws,
+                                   bias=L.gate_up_b)
             x = nx
-            pending = ops.mul_mat_fused(L.down, gu, out=b["proj"], x_swiglu=True, ws=ws)
+            pending = ops.mul_mat_fused(L.down, gu, out=b["proj"], x_swiglu=True, ws=ws, bias=L.down_b)
         else:
-            o = ops.mul_mat(L.o, b["attn"].view(s, qd), out=b["proj"], ws=ws)
+            o = _linear(L.o, L.o_b, b["attn"].view(s, qd), b["proj"], ws)
             ops.add(x, o, out=x)
             rec("x_mid", li, x)
             h = ops.rms_norm(x, c.rms_eps, out=b["h"])
             rec("h2", li, h)
-            gu = ops.mul_mat(L.gate_up, h, out=b["gu"], ws=ws)
+            gu = _linear(L.gate_up, L.gate_up_b, h, b["gu"], ws)
             rec("gu", li, gu)
             a = ops.swiglu(gu, out=b["act"])
             rec("act", li, a)
-            d = ops.mul_mat(L.down, a, out=b["proj"], ws=ws)
+            d = _linear(L.down, L.down_b, a, b["proj"], ws)
             ops.add(x, d, out=x)
         rec("x_out", li, x)
     if fused or pro:

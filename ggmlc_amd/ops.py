@@ -189,13 +189,14 @@ class RopeKv:
 def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
                   swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
                   x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None, x_swiglu: bool = False,
-                  ws: Workspace | None = None) -> torch.Tensor | None:
+                  ws: Workspace | None = None, bias: torch.Tensor | None = None) -> torch.Tensor | None:
     """MUL_MAT fused with its graph neighbours, bit-identical to the unfused ops:
     x_add -> x + x_add first (stored to x_sum when given); rms_eps -> RMS_NORM;
     x_swiglu -> the input is SWIGLU of x's two halves (x [..., 2K]); swiglu -> SWIGLU of
     the result's two halves (out [..., N/2]); add -> add + result (add may be out);
     rope_kv -> the result's q/k/v rows go through :func:`rope_kv_store` instead of
-    being written (returns None). Up to 4 rows run as one GEMV launch; more rows take
+    being written (returns None); bias (fp32 [N]) -> the product + bias before the
+    output-side fusions (MUL_MAT's bias ADD). Up to 4 rows run as one GEMV launch; more rows take
     the GEMM path (input-side fusions only, with the workspace ws)."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
@@ -229,6 +230,9 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     xs = _desc(x_sum) if x_sum is not None else None
     if xs is not None:
         f.b_sum = ctypes.pointer(xs)
+    bd = _desc(bias) if bias is not None else None
+    if bd is not None:
+        f.bias = ctypes.pointer(bd)
     od = _desc(out) if out is not None else None
     L, wd, xd = _lib.load(), w.desc(), _desc(x)
     need = L.gq_mul_mat_fused_workspace_size(wd, xd, ctypes.byref(f))

@@ -88,6 +88,20 @@ def match_llama(g: Graph, reader: GGUFReader) -> _Match:
         ne = reader.tensors[t.name].ne
         return t.name, t.type, int(ne[0]), int(ne[1])
 
+    def bias_of(node, n):
+        """the MUL_MAT node's bias input (executor.cpp:2436-2445): an F32 [n] tensor in the file"""
+        if len(node.inputs) < 3:
+            return None
+        if len(node.inputs) > 3:
+            _fail(node, "MUL_MAT with more than three inputs")
+        t = T[node.inputs[2]]
+        if t.type != 0 or t.name not in reader.tensors:
+            _fail(node, f"bias '{t.name}' must be an F32 tensor stored in the file")
+        ne = [int(v) for v in reader.tensors[t.name].ne if int(v) != 1] or [1]
+        if ne != [n]:
+            _fail(node, f"bias '{t.name}' must hold {n} values")
+        return t.name
+
     def rms_eps(node):
         if len(node.inputs) != 1:
             _fail(node, "RMS_NORM with a weight input (expected the weight baked into the next MUL_MAT)")
@@ -110,6 +124,8 @@ def match_llama(g: Graph, reader: GGUFReader) -> _Match:
             m.lm_head, m.lm_type, k, n = weight(mms[0].inputs[0], mms[0])
             if k != m.n_embd or n != m.n_vocab:
                 _fail(mms[0], "lm_head shape")
+            if len(mms[0].inputs) > 2:
+                _fail(mms[0], "an output head with a bias is not mapped")
             break
         L: dict[str, Any] = {}
         # q, k, v: RESHAPE [hd, H, s] of either VIEWs of one fused product or three products
@@ -152,11 +168,18 @@ def match_llama(g: Graph, reader: GGUFReader) -> _Match:
             _fail(srcs[2], "k and v head counts differ")
         if L["qkv"] is None:  # three products, concatenated in q | k | v order
             L["qkv"] = [weight(t[1].inputs[0], t[1]) for t in paths]
+            L["qkv_b"] = [bias_of(t[1], t[3] * hd) for t in paths]
+            if any(b is None for b in L["qkv_b"]):
+                if any(b is not None for b in L["qkv_b"]):
+                    _fail(srcs[0], "biases on some of q, k, v only")
+                L["qkv_b"] = None
         else:
             w0 = L["qkv"][0]
             if w0[3] != (n_head + 2 * n_head_kv) * hd or [t[1].attr_int("start") for t in paths] != \
                     [0, n_head * hd, (n_head + n_head_kv) * hd]:
                 _fail(srcs[0], "fused QKV rows are not q | k | v")
+            b0 = bias_of(mms[0], w0[3])
+            L["qkv_b"] = [b0] if b0 is not None else None
         rq, rk = paths[0][4], paths[1][4]
         for rn in (rq, rk):
             if rn.attr_int("mode", 2) != 2 or rn.attr_int("n_dims", hd) != hd:
@@ -174,6 +197,7 @@ def match_llama(g: Graph, reader: GGUFReader) -> _Match:
         a2 = only(cons.get(fa.outputs[0], []), "RESHAPE", "attention output reshape", fa)
         o = only(cons.get(a2.outputs[0], []), "MUL_MAT", "output projection", a2)
         L["o"] = weight(o.inputs[0], o)
+        L["o_b"] = bias_of(o, L["o"][3])
         add1 = only(cons.get(o.outputs[0], []), "ADD", "residual", o)
         if x not in add1.inputs:
             _fail(add1, "residual must add the layer input")
@@ -182,11 +206,13 @@ def match_llama(g: Graph, reader: GGUFReader) -> _Match:
         eps.append(rms_eps(norm2))
         gu = only(cons.get(norm2.outputs[0], []), "MUL_MAT", "gate|up projection", norm2)
         L["gate_up"] = weight(gu.inputs[0], gu)
+        L["gate_up_b"] = bias_of(gu, L["gate_up"][3])
         glu = only(cons.get(gu.outputs[0], []), "GLU", "SWIGLU", gu)
         if glu.attr_int("op", 2) != 2 or glu.attr_int("swapped", 0) != 0:
             _fail(glu, "only SWIGLU is mapped")
         dn = only(cons.get(glu.outputs[0], []), "MUL_MAT", "down projection", glu)
         L["down"] = weight(dn.inputs[0], dn)
+        L["down_b"] = bias_of(dn, L["down"][3])
         add2 = only(cons.get(dn.outputs[0], []), "ADD", "residual", dn)
         if x1 not in add2.inputs:
             _fail(add2, "residual must add the attention block's output")
@@ -257,7 +283,8 @@ class ModelRunner:
                                              for w in [L[k]]} | {w[1] for L in m.layers for w in L["qkv"]}
         self.cfg = LlamaConfig(self.name, len(m.layers), m.n_embd, m.n_head, m.n_head_kv, m.head_dim, m.n_ff,
                                m.n_vocab, m.embed_type if len(qt) == 1 else -1,
-                               tied_embeddings=m.lm_head == m.embed, rms_eps=m.rms_eps, rope_base=m.rope_base)
+                               tied_embeddings=m.lm_head == m.embed, rms_eps=m.rms_eps, rope_base=m.rope_base,
+                               qkv_bias=m.layers[0]["qkv_b"] is not None)
 
         cache: dict[str, ops.QWeight] = {}
 
@@ -273,8 +300,17 @@ class ModelRunner:
                 cache[key] = ops.QWeight(dev_t, types.pop(), names_types[0][2])
             return cache[key]
 
+        def upload_bias(names) -> torch.Tensor | None:
+            if not names:
+                return None
+            host = np.concatenate([np.asarray(reader.tensor_array(n), np.float32).reshape(-1) for n in names])
+            return torch.from_numpy(host).to(self._dev)
+
         layers = [LayerWeights(qkv=upload(L["qkv"]), o=upload([L["o"]]), gate_up=upload([L["gate_up"]]),
-                               down=upload([L["down"]])) for L in m.layers]
+                               down=upload([L["down"]]), qkv_b=upload_bias(L["qkv_b"]),
+                               o_b=upload_bias([L["o_b"]] if L["o_b"] else None),
+                               gate_up_b=upload_bias([L["gate_up_b"]] if L["gate_up_b"] else None),
+                               down_b=upload_bias([L["down_b"]] if L["down_b"] else None)) for L in m.layers]
         embed = upload([(m.embed, m.embed_type, m.n_embd)])
         lm = upload([(m.lm_head, m.lm_type, m.n_embd)])
         self.weights = ModelWeights(self.cfg, embed, lm, layers)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define GQ_ABI_VERSION 2
+#define GQ_ABI_VERSION 3
 
 /* ggml type ids (third_party/ggml/include/ggml.h enum ggml_type; ggmlc
  * python/ggmlc/dialect/ggml/ops.py:39-108) */
@@ -121,6 +121,9 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  *   rms_norm: b's rows are RMS-normalized (gq_rms_norm with rms_eps)
  *   swiglu:   dst = SWIGLU(MUL_MAT(a, b)) over the two halves of a's rows
  *             (gq_swiglu of the [N, M] result): dst ne0 = N / 2
+ *   bias:     MUL_MAT(a, b) + bias first, before the output-side fusions below (the
+ *             MUL_MAT node's bias input, executor.cpp:2436-2445: ggml_add of an F32
+ *             [N] row broadcast over the M rows); on both paths
  *   add:      dst = add + MUL_MAT(a, b) (gq_add); add may be dst itself
  *   rope_kv:  the rows of MUL_MAT(a, b) are a fused QKV projection,
  *             (n_head + 2 n_head_kv) heads of head_dim rows (q heads, k heads, v
@@ -166,6 +169,7 @@ typedef struct gq_mul_mat_fusion {
     int32_t b_swiglu;        /* the input is SWIGLU of b's rows: b ne0 = 2K (GEMM path only) */
     void* workspace;         /* GEMM path: gq_mul_mat_fused_workspace_size bytes, 256-aligned */
     size_t workspace_bytes;
+    const gq_tensor* bias;   /* F32 [N, 1, 1, 1] or NULL */
 } gq_mul_mat_fusion;
 size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f);
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,

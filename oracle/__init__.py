@@ -112,6 +112,7 @@ def ref():
         L.ref_llama_create.restype = _vp
         L.ref_llama_create.argtypes = [_vp, _i32, _f32, _f32, _vp, _vp, _vp, _vp]
         L.ref_llama_step.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32]
+        L.ref_llama_set_bias.argtypes = [_vp, _i64, _i32, _vp, _i64]
         L.ref_llama_free.argtypes = [_vp]
         L.ref_llama_free.restype = None
         L.ref_rt_last_error.restype = ctypes.c_char_p
@@ -370,12 +371,14 @@ class RefLlama:
 
     cfg needs n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, qtype,
     rms_eps, rope_base; weights = (embed, lm_head, [(qkv, o, gate_up, down), ...])
-    as uint8 GGUF block bytes."""
+    as uint8 GGUF block bytes. A layer tuple may carry four more entries, the fp32 biases
+    of the same projections (None where a projection has none): the MUL_MAT node's
+    bias ADD (executor.cpp:2436-2445)."""
 
     def __init__(self, cfg, weights, max_ctx: int, n_threads: int = 8):
         embed, lm_head, layers = weights
         self.cfg, self.max_ctx, self.n_threads = cfg, max_ctx, n_threads
-        self._w = [_c(embed, np.uint8), _c(lm_head, np.uint8)] + [_c(m, np.uint8) for L in layers for m in L]
+        self._w = [_c(embed, np.uint8), _c(lm_head, np.uint8)] + [_c(m, np.uint8) for L in layers for m in L[:4]]
         self.kc = [np.zeros((cfg.n_head_kv, max_ctx, cfg.head_dim), np.uint16) for _ in layers]
         self.vc = [np.zeros_like(k) for k in self.kc]
         dims = np.array([cfg.n_layer, cfg.n_embd, cfg.n_head, cfg.n_head_kv, cfg.head_dim, cfg.n_ff,
@@ -386,6 +389,15 @@ class RefLlama:
                                         _ptr(self._w[1]), lw, kv)
         if not self.h:
             raise RuntimeError("ref_llama_create failed")
+        self._b = []
+        for li, L in enumerate(layers):
+            for which, b in enumerate(L[4:8]):
+                if b is None:
+                    continue
+                b = _c(b, np.float32)
+                self._b.append(b)
+                if ref().ref_llama_set_bias(self.h, li, which, _ptr(b), b.size) != 0:
+                    raise RuntimeError("ref_llama_set_bias failed")
         self.pos = 0
 
     def step(self, ids):

@@ -314,7 +314,9 @@ int ref_argmax(const float* x, int64_t n, int64_t nrows, int32_t* out) {
 //   set_rows(Kc, k^T, idx); set_rows(Vc, v^T, idx)          (executor.cpp:2181-2184)
 //   a = flash_attn_ext(q^T, Kc[:n_kv], Vc[:n_kv], mask, 1/sqrt(hd))  (:2195-2197)
 //   x += mul_mat(Wo, a); x += mul_mat(Wdown, swiglu(mul_mat(Wgate_up, rms_norm(x))))
-// then rms_norm(x[s-1]) -> mul_mat(lm_head) -> argmax.
+// then rms_norm(x[s-1]) -> mul_mat(lm_head) -> argmax. A projection with a bias
+// (ref_llama_set_bias) is ggml_add(mul_mat(W, h), b), the executor's MUL_MAT with a third
+// input (executor.cpp:2436-2445).
 
 struct RefLlama {
     int64_t n_layer, n_embd, n_head, n_head_kv, hd, n_ff, n_vocab, max_ctx;
@@ -323,6 +325,7 @@ struct RefLlama {
     ggml_context* wctx = nullptr;
     ggml_tensor *embed = nullptr, *lm_head = nullptr;
     std::vector<ggml_tensor*> wqkv, wo, wgu, wd, kc, vc;
+    std::vector<ggml_tensor*> bias;  // [4 * layer + which] or null
     ggml_gallocr_t galloc = nullptr;
     std::vector<uint8_t> work;
 };
@@ -343,7 +346,7 @@ void* ref_llama_create(const int64_t* dims, int wtype, float eps, float rope_bas
     m->n_layer = dims[0], m->n_embd = dims[1], m->n_head = dims[2], m->n_head_kv = dims[3];
     m->hd = dims[4], m->n_ff = dims[5], m->n_vocab = dims[6], m->max_ctx = dims[7];
     m->wt = (ggml_type)wtype, m->eps = eps, m->base = rope_base;
-    ggml_init_params p = {ggml_tensor_overhead() * (size_t)(8 * m->n_layer + 8), nullptr, true};
+    ggml_init_params p = {ggml_tensor_overhead() * (size_t)(12 * m->n_layer + 8), nullptr, true};
     m->wctx = ggml_init(p);
     if (!m->wctx) {
         delete m;
@@ -363,8 +366,28 @@ void* ref_llama_create(const int64_t* dims, int wtype, float eps, float rope_bas
             (j ? m->vc : m->kc).push_back(c);
         }
     }
+    m->bias.assign(4 * m->n_layer, nullptr);
     m->galloc = ggml_gallocr_new(ggml_backend_cpu_buffer_type());
     return m;
+}
+
+// bias of layer l's projection `which` (0 qkv, 1 o, 2 gate_up, 3 down): F32 [N] in the
+// caller's memory, N = that projection's output rows. Returns 0 on success.
+int ref_llama_set_bias(void* h, int64_t l, int which, const float* b, int64_t n) {
+    RefLlama* m = (RefLlama*)h;
+    if (!m || l < 0 || l >= m->n_layer || which < 0 || which > 3) return -1;
+    const ggml_tensor* w = which == 0 ? m->wqkv[l] : which == 1 ? m->wo[l] : which == 2 ? m->wgu[l] : m->wd[l];
+    if (n != w->ne[1]) return -1;
+    ggml_tensor* t = ggml_new_tensor_1d(m->wctx, GGML_TYPE_F32, n);
+    t->data = const_cast<float*>(b);
+    m->bias[4 * l + which] = t;
+    return 0;
+}
+
+// the executor's MUL_MAT node: mul_mat(W, x), + bias when the node has one
+static ggml_tensor* linear(ggml_context* c, ggml_tensor* w, ggml_tensor* x, ggml_tensor* b) {
+    ggml_tensor* r = ggml_mul_mat(c, w, x);
+    return b ? ggml_add(c, r, b) : r;
 }
 
 // ids I32 [s]; mask F16 [s][n_kv] (row i = query pos+i); logits F32 [n_vocab] of the
@@ -392,7 +415,7 @@ int ref_llama_step(void* h, const int32_t* ids, int64_t s, int64_t pos, int64_t 
     const float scale = 1.0f / sqrtf((float)hd);
     for (int64_t l = 0; l < m->n_layer; ++l) {
         ggml_tensor* hn = ggml_rms_norm(c, x, m->eps);
-        ggml_tensor* qkv = ggml_mul_mat(c, m->wqkv[l], hn);  // [qd + 2 kvd, s]
+        ggml_tensor* qkv = linear(c, m->wqkv[l], hn, m->bias[4 * l]);  // [qd + 2 kvd, s]
         const size_t es = sizeof(float);
         ggml_tensor* q = ggml_view_3d(c, qkv, hd, H, s, hd * es, qkv->nb[1], 0);
         ggml_tensor* k = ggml_view_3d(c, qkv, hd, Hk, s, hd * es, qkv->nb[1], qd * es);
@@ -412,9 +435,9 @@ int ref_llama_step(void* h, const int32_t* ids, int64_t s, int64_t pos, int64_t 
                                       m->vc[l]->nb[3], 0);
         ggml_tensor* a = ggml_flash_attn_ext(c, ggml_permute(c, q, 0, 2, 1, 3), K, V, t_mask, scale, 0.0f, 0.0f);
         a = ggml_reshape_2d(c, a, qd, s);  // the op's output is [hd, H, s]
-        x = ggml_add(c, x, ggml_mul_mat(c, m->wo[l], a));
-        ggml_tensor* gu = ggml_mul_mat(c, m->wgu[l], ggml_rms_norm(c, x, m->eps));
-        x = ggml_add(c, x, ggml_mul_mat(c, m->wd[l], ggml_swiglu(c, gu)));
+        x = ggml_add(c, x, linear(c, m->wo[l], a, m->bias[4 * l + 1]));
+        ggml_tensor* gu = linear(c, m->wgu[l], ggml_rms_norm(c, x, m->eps), m->bias[4 * l + 2]);
+        x = ggml_add(c, x, linear(c, m->wd[l], ggml_swiglu(c, gu), m->bias[4 * l + 3]));
     }
     ggml_tensor* xl = ggml_view_2d(c, x, E, 1, x->nb[1], (size_t)(s - 1) * x->nb[1]);
     ggml_tensor* lo = ggml_mul_mat(c, m->lm_head, ggml_rms_norm(c, xl, m->eps));

@@ -39,7 +39,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_struct_layout(lib):
-    assert lib.gq_abi_version() == 2
+    assert lib.gq_abi_version() == 3
     # gq_tensor: void* + 2 x int32 + 4 x int64 + 4 x size_t
     assert ctypes.sizeof(_lib.gq_tensor) == 8 + 8 + 32 + 32
 

@@ -1,5 +1,6 @@
 """The compile path (ggmlc_amd.compile): PyTorch LLaMA-family module -> fused, baked,
-quantized .gguf.
+quantized .gguf (LlamaForCausalLM and Qwen2ForCausalLM, whose q/k/v biases ride on the
+fused QKV MUL_MAT's third input).
 
 * the host quantizer gives the bytes of the oracle's restatement of quantize.py
   (itself pinned by tests/test_oracle.py), ties and zero blocks included;
@@ -56,6 +57,50 @@ def _hf_llama(tied: bool, eps: float, seed: int = 0):
     return m
 
 
+def _hf_qwen2(tied: bool, seed: int = 0):
+    """A random-init transformers Qwen2ForCausalLM: the LLaMA layout plus q/k/v biases
+    (made non-zero here: the module initialises them to zero)."""
+    import torch
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=1024,
+                      rms_norm_eps=1e-6, rope_theta=1000000.0, tie_word_embeddings=tied)
+    torch.manual_seed(seed)
+    m = Qwen2ForCausalLM(cfg).eval()
+    with torch.no_grad():
+        for mod in m.modules():
+            if type(mod).__name__.endswith("RMSNorm"):
+                mod.weight.copy_(1.0 + 0.2 * torch.randn_like(mod.weight))
+        for L in m.model.layers:
+            for lin in (L.self_attn.q_proj, L.self_attn.k_proj, L.self_attn.v_proj):
+                lin.bias.copy_(0.5 * torch.randn_like(lin.bias))
+    return m
+
+
+def test_compiled_qwen2_biases(tmp_path):
+    """q/k/v biases land concatenated (q | k | v, fp32, unbaked) on the fused QKV MUL_MAT's
+    third input, and the runner's matcher reads them back."""
+    from ggmlc_amd.compile import compile_llama
+    from ggmlc_amd.gguf import GGUFReader
+    from ggmlc_amd.graph_spec import OPS, Graph
+    from ggmlc_amd.runner import match_llama
+
+    m = _hf_qwen2(tied=True)
+    p = compile_llama(m, tmp_path / "q.gguf", quantize="q8_0", max_pos=512)
+    r = GGUFReader(p)
+    g = Graph.from_json(r.metadata["ggmlc.graph_spec"])
+    mt = match_llama(g, r)
+    assert mt.rope_base == 1e6 and mt.layers[0]["o_b"] is None and mt.layers[0]["down_b"] is None
+    for li, L in enumerate(m.model.layers):
+        (name,) = mt.layers[li]["qkv_b"]
+        want = np.concatenate([lin.bias.detach().numpy() for lin in
+                               (L.self_attn.q_proj, L.self_attn.k_proj, L.self_attn.v_proj)])
+        assert np.array_equal(r.tensor_array(name), want.astype(np.float32))
+    mm3 = [n for n in g.nodes if n.opcode == OPS["MUL_MAT"] and len(n.inputs) == 3]
+    assert len(mm3) == 2  # one fused QKV product per layer
+
+
 def test_compiled_layout_and_bake(tmp_path):
     from ggmlc_amd.compile import compile_llama
     from ggmlc_amd.gguf import GGUFReader
@@ -85,13 +130,16 @@ def test_compiled_layout_and_bake(tmp_path):
 
 @pytest.mark.skipif(not O.ref_available(), reason="needs oracle/_ref")
 @pytest.mark.parametrize("quant,tied,eps,bar", [("q8_0", False, 1e-5, 0.999), ("q8_0", True, 1e-6, 0.999),
-                                                 ("q4_0", False, 1e-5, 0.95)])
+                                                 ("q4_0", False, 1e-5, 0.95), ("qwen2", True, 1e-6, 0.999)])
 def test_reference_runtime_runs_the_compiled_module(tmp_path, quant, tied, eps, bar):
     import torch
 
     from ggmlc_amd.compile import compile_llama
 
-    m = _hf_llama(tied=tied, eps=eps, seed=1)
+    if quant == "qwen2":  # q/k/v biases through the reference executor's bias ADD
+        m, quant = _hf_qwen2(tied=tied, seed=1), "q8_0"
+    else:
+        m = _hf_llama(tied=tied, eps=eps, seed=1)
     p = compile_llama(m, tmp_path / "m.gguf", quantize=quant, max_pos=512)
     ids = np.random.default_rng(2).integers(0, 512, 29).astype(np.int32)
     with torch.no_grad():
@@ -111,13 +159,14 @@ def test_reference_runtime_runs_the_compiled_module(tmp_path, quant, tied, eps, 
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not O.ref_available(), reason="needs oracle/_ref")
-def test_gpu_runner_runs_the_compiled_module(tmp_path):
+@pytest.mark.parametrize("family", ["llama", "qwen2"])
+def test_gpu_runner_runs_the_compiled_module(tmp_path, family):
     import torch
 
     from ggmlc_amd import runner as R
     from ggmlc_amd.compile import compile_llama
 
-    m = _hf_llama(tied=False, eps=1e-5, seed=3)
+    m = _hf_llama(tied=False, eps=1e-5, seed=3) if family == "llama" else _hf_qwen2(tied=True, seed=3)
     p = compile_llama(m, tmp_path / "m.gguf", quantize="q8_0", max_pos=512)
     ids = np.random.default_rng(4).integers(0, 512, 33).astype(np.int32)
     run = R.load(p, device="gpu")

@@ -154,14 +154,20 @@ def test_reference_loader_reads_our_file(tmp_path, fused_qkv):
 
 
 @needs_ref
-@pytest.mark.parametrize("qtype,tied,fused_qkv", [(O.Q8_0, False, True), (O.Q4_0, True, False)])
-def test_reference_runtime_runs_our_llama_file(tmp_path, qtype, tied, fused_qkv):
+@pytest.mark.parametrize("qtype,tied,fused_qkv,bias", [(O.Q8_0, False, True, False), (O.Q4_0, True, False, False),
+                                                       (O.Q8_0, True, True, True), (O.Q8_0, False, False, True)])
+def test_reference_runtime_runs_our_llama_file(tmp_path, qtype, tied, fused_qkv, bias):
     """The reference's own executor running our .gguf (prefill of 37 tokens, then
     decode steps with the KV cache, symbols s/pos) gives the bits of the reference
     ggml decoder graph (oracle.RefLlama) on the same weights: the file's graph is the
-    decoder."""
+    decoder, projection biases (q | k | v, and o / gate_up / down) included."""
     c = _tiny(qtype, tied)
     w = _weights(c)
+    if bias:
+        rng = np.random.default_rng(11)
+        nq, E, F = c.q_dim + 2 * c.kv_dim, c.n_embd, c.n_ff
+        w = (w[0], w[1], [tuple(L) + tuple((rng.standard_normal(n) * 0.3).astype(np.float32)
+                                            for n in (nq, E, 2 * F, E)) for L in w[2]])
     p = write_llama_gguf(tmp_path / "m.gguf", c, w, max_pos=1024, fused_qkv=fused_qkv)
     g = Graph.from_json(gguf.GGUFReader(p).metadata["ggmlc.graph_spec"])
     rt = O.RefRuntime(p, max_ctx=512, n_threads=8)

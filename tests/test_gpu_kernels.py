@@ -283,6 +283,64 @@ def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_d
     assert int(bad1.item()) == int(bad2.item()) == 2 * Hkv * n_bad_rows
 
 
+@pytest.mark.parametrize("qtype,K,N,M,epi", [
+    (O.Q8_0, 1536, 2048, 1, "plain"),       # Qwen2.5-1.5B QKV shape, decode
+    (O.Q8_0, 960, 1600, 3, "plain"),        # K = 960 (block-wise kernel), three rows
+    (O.Q4_0, 4096, 22016, 1, "swiglu"),     # bias on both halves before SWIGLU
+    (O.Q8_0, 2560, 960, 2, "add"),          # bias, then the residual ADD
+    (O.Q8_0, 1536, 2048, 16, "gemm"),       # batch 16: GEMM path, split K, bias in the reduce
+    (O.Q4_0, 4096, 12288, 37, "gemm"),      # prompt rows: GEMM path, bias in the tile store
+])
+def test_mul_mat_fused_bias_bit_identical(qtype, K, N, M, epi):
+    """MUL_MAT with its bias input (executor.cpp:2436-2445: ADD(MUL_MAT(W, x), b)) fused
+    into the GEMV epilogue or the GEMM store gives exactly the bits of MUL_MAT then ADD."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M + 1)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV) * 3.0
+    b = torch.randn(N, generator=g, device=DEV) * 0.5
+    y = ops.add(ops.mul_mat(w, ops.rms_norm(x, 1e-5)), b)
+    kw = dict(rms_eps=1e-5, bias=b)
+    if epi == "swiglu":
+        want, got = ops.swiglu(y), ops.mul_mat_fused(w, x, swiglu=True, **kw)
+    elif epi == "add":
+        r = torch.randn((M, N), generator=g, device=DEV)
+        want = ops.add(r, y)
+        got = r.clone()
+        ops.mul_mat_fused(w, x, out=got, add=got, **kw)
+    else:
+        want, got = y, ops.mul_mat_fused(w, x, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (got - want).abs().max().item()
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_mul_mat_fused_rope_kv_with_bias_bit_identical(M):
+    """Qwen2's q/k/v biases ahead of the rope + KV-store epilogue (the decode QKV launch)."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(77 + M)
+    K, Hq, Hkv, hd = 1536, 12, 2, 128
+    N = (Hq + 2 * Hkv) * hd
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, O.Q8_0)
+    x = torch.randn((M, K), generator=g, device=DEV) * 3.0
+    b = torch.randn(N, generator=g, device=DEV)
+    pos = torch.arange(300, 300 + M, dtype=torch.int32, device=DEV)
+    idx = pos.to(torch.int64)
+    kc1 = torch.zeros((1, Hkv, 512, hd), dtype=torch.float16, device=DEV)
+    vc1, kc2, vc2 = kc1.clone(), kc1.clone(), kc1.clone()
+    y = ops.add(ops.mul_mat(w, ops.rms_norm(x, 1e-5)), b)
+    q1 = torch.empty((1, M, Hq, hd), device=DEV)
+    ops.rope_kv_store(y[:, :Hq * hd].view(1, M, Hq, hd), y[:, Hq * hd:(Hq + Hkv) * hd].view(1, M, Hkv, hd),
+                      y[:, (Hq + Hkv) * hd:].view(1, M, Hkv, hd), pos, hd, 2, 1e6, idx, q1, kc1, vc1)
+    q2 = torch.full_like(q1, float("nan"))
+    ops.mul_mat_fused(w, x, rms_eps=1e-5, bias=b, rope_kv=ops.RopeKv(
+        Hq, Hkv, hd, pos, hd, 2, 1e6, idx, q2, kc2, vc2, cache=ops.rope_cache(pos, hd, 1e6)))
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+
+
 # --------------------------------------------------------------- set_rows ---
 
 def test_set_rows_golden(golden_dir):

@@ -89,8 +89,11 @@ class RefModel:
         mask = O.causal_mask_f16(self.pos, s, n_kv)
         x = self.embed[np.asarray(ids)].copy()
         qd, kvd = c.q_dim, c.kv_dim
-        for li, (wqkv, wo, wgu, wd) in enumerate(self.layers):
+        for li, Lw in enumerate(self.layers):
+            wqkv, wo, wgu, wd = Lw[:4]
             qkv = P(O.mul_mat(wqkv, t, c.n_embd, _rms(x, c.rms_eps)))
+            if len(Lw) > 4 and Lw[4] is not None:
+                qkv = qkv + Lw[4]
             q = _rope(qkv[:, :qd].reshape(s, c.n_head, c.head_dim), pos, c.rope_base)
             k = _rope(qkv[:, qd:qd + kvd].reshape(s, c.n_head_kv, c.head_dim), pos, c.rope_base)
             v = qkv[:, qd + kvd:].reshape(s, c.n_head_kv, c.head_dim)
@@ -169,13 +172,12 @@ def test_reference_graph_matches_restatement(qtype):
 def _gpu_model(cfg, max_ctx, seed):
     import torch
     from ggmlc_amd import _lib
-    from ggmlc_amd.model import Decoder, random_weights
+    from ggmlc_amd.model import Decoder, host_weights, random_weights
 
     _lib.check(_lib.load().gq_init())
     w = random_weights(cfg, torch.device("cuda"), seed=seed)
     dec = Decoder(w, max_ctx, torch.device("cuda"))
-    host = (w.embed.data.cpu().numpy(), w.lm_head.data.cpu().numpy(),
-            [tuple(m.data.cpu().numpy() for m in (L.qkv, L.o, L.gate_up, L.down)) for L in w.layers])
+    host = host_weights(w)
     return dec, host
 
 
@@ -197,13 +199,15 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
         worst[name] = max(worst.get(name, 0.0), m)
         assert m <= tol, (name, m)
 
-    for li, (wqkv, wo, wgu, wd) in enumerate(host[2]):
+    for li, Lw in enumerate(host[2]):
         if not keep(li):
             continue
+        wqkv, wo, wgu, wd = Lw[:4]
+        bq = Lw[4] if len(Lw) > 4 and Lw[4] is not None else np.float32(0.0)
         g = lambda n: T[(n, li)]  # noqa: E731
         x_in = g("x_in")
         bar("rms_norm", g("h1"), _rms(x_in, cfg.rms_eps), 1e-5)
-        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1")), 1e-5)
+        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1")) + bq, 1e-5)
         qkv = g("qkv")
         qh = qkv[:, :qd].reshape(s, cfg.n_head, cfg.head_dim)
         kh = qkv[:, qd:qd + kvd].reshape(s, cfg.n_head_kv, cfg.head_dim)
@@ -239,15 +243,23 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
     return worst
 
 
+def _tiny_qwen():
+    """A 2-layer model of the Qwen2 family's layout: GQA 6 over heads of 128, q/k/v biases,
+    rope base 1e6"""
+    from ggmlc_amd.model import LlamaConfig
+
+    return LlamaConfig("tiny-qwen", 2, 256, 12, 2, 128, 512, 512, O.Q8_0, rope_base=1e6, qkv_bias=True)
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0, "qwen"])
 def test_decoder_ops_teacher_forced(qtype):
     """Prefill (37 tokens: GEMM path) then two decode steps (GEMV path), each traced and
-    recomputed op by op on the CPU."""
+    recomputed op by op on the CPU (q/k/v biases included for the Qwen2 layout)."""
     import torch
     from ggmlc_amd.model import LlamaConfig, pad_kv_len
 
-    cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, qtype)
+    cfg = _tiny_qwen() if qtype == "qwen" else LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, qtype)
     max_ctx = 512
     dec, host = _gpu_model(cfg, max_ctx, seed=7)
     prompt = np.random.default_rng(3).integers(0, cfg.n_vocab, 37).astype(np.int32)
@@ -328,14 +340,14 @@ def _check_end_to_end(res, tokens, min_cos):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0, "qwen"])
 @pytest.mark.parametrize("graphs", [False, True])
 def test_tiny_decoder_end_to_end(qtype, graphs):
     """bar: cosine >= 0.9999 per step, within the measured floor of the quantized
     pipeline (cosine ~0.99995 under a 1e-6 perturbation at this shape)."""
     from ggmlc_amd.model import LlamaConfig
 
-    cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, qtype)
+    cfg = _tiny_qwen() if qtype == "qwen" else LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, qtype)
     res, tokens, pos = _run(cfg, prompt_len=37, n_new=6, max_ctx=512, graphs=graphs)
     _check_end_to_end(res, tokens, 0.9999)
     assert pos == 37 + 6
@@ -355,7 +367,7 @@ def test_smollm2_shape_two_layers():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", ["tiny_q8", "tiny_q4", "smollm2"])
+@pytest.mark.parametrize("shape", ["tiny_q8", "tiny_q4", "smollm2", "qwen"])
 def test_fused_decode_steps_bit_identical(shape):
     """Decode steps with RMS_NORM / ADD / SWIGLU fused into the GEMVs give exactly the
     bits of the unfused graph (logits, next token and the KV rows written), for 1 and 3
@@ -367,6 +379,8 @@ def test_fused_decode_steps_bit_identical(shape):
 
     if shape == "smollm2":
         cfg = replace(SMOLLM2_360M, n_layer=2, n_vocab=4096)
+    elif shape == "qwen":
+        cfg = _tiny_qwen()
     else:
         cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q8_0 if shape == "tiny_q8" else O.Q4_0)
     dec, _ = _gpu_model(cfg, 512, seed=11)
@@ -391,7 +405,7 @@ def test_fused_decode_steps_bit_identical(shape):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("shape", ["tiny_q4", "gqa6_q8"])
+@pytest.mark.parametrize("shape", ["tiny_q4", "gqa6_q8", "qwen"])
 def test_prefill_gemm_prologue_fusions_bit_identical(shape):
     """A prefill step whose GEMMs take ADD / RMS_NORM / SWIGLU in their activation
     prologues gives exactly the bits (logits of every row, KV rows) of the traced step
@@ -402,6 +416,8 @@ def test_prefill_gemm_prologue_fusions_bit_identical(shape):
 
     if shape == "tiny_q4":
         cfg = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q4_0)
+    elif shape == "qwen":
+        cfg = _tiny_qwen()
     else:
         cfg = LlamaConfig("tiny-gqa6", 2, 256, 12, 2, 128, 512, 512, O.Q8_0)
     dec, _ = _gpu_model(cfg, 512, seed=13)

@@ -167,12 +167,11 @@ def test_paged_step_inputs_advance_and_copy():
 
 def _model(cfg, seed=7):
     import torch
-    from ggmlc_amd.model import random_weights
+    from ggmlc_amd.model import host_weights, random_weights
 
     dev = _init()
     w = random_weights(cfg, dev, seed=seed)
-    host = (w.embed.data.cpu().numpy(), w.lm_head.data.cpu().numpy(),
-            [tuple(m.data.cpu().numpy() for m in (L.qkv, L.o, L.gate_up, L.down)) for L in w.layers])
+    host = host_weights(w)
     torch.cuda.synchronize()
     return w, host
 

@@ -36,7 +36,8 @@ def _weights(c, seed=7):
     return embed, embed if c.tied_embeddings else q(c.n_vocab, c.n_embd), layers
 
 
-@pytest.mark.parametrize("shape,fused_qkv", [("tiny_q8", True), ("tiny_q4", False), ("smollm2", True)])
+@pytest.mark.parametrize("shape,fused_qkv", [("tiny_q8", True), ("tiny_q4", False), ("smollm2", True),
+                                             ("qwen_bias", True), ("qwen_bias", False)])
 def test_runner_matches_reference_runtime(tmp_path, shape, fused_qkv):
     from dataclasses import replace
 
@@ -45,9 +46,16 @@ def test_runner_matches_reference_runtime(tmp_path, shape, fused_qkv):
 
     if shape == "smollm2":
         c, bar = replace(SMOLLM2_360M, n_layer=2, n_vocab=4096), 0.9995
+    elif shape == "qwen_bias":  # the Qwen2 layout: GQA 6, q/k/v biases, rope base 1e6
+        c, bar = LlamaConfig("tiny-qwen", 2, 256, 12, 2, 128, 512, 512, O.Q8_0, rope_base=1e6, qkv_bias=True), 0.9999
     else:
         c, bar = LlamaConfig("tiny", 2, 256, 4, 2, 64, 512, 512, O.Q8_0 if shape == "tiny_q8" else O.Q4_0), 0.9999
-    p = write_llama_gguf(tmp_path / "m.gguf", c, _weights(c), max_pos=1024, fused_qkv=fused_qkv)
+    w = _weights(c)
+    if c.qkv_bias:
+        rng = np.random.default_rng(12)
+        w = (w[0], w[1], [tuple(L) + ((rng.standard_normal(c.q_dim + 2 * c.kv_dim) * 0.3).astype(np.float32),
+                                      None, None, None) for L in w[2]])
+    p = write_llama_gguf(tmp_path / "m.gguf", c, w, max_pos=1024, fused_qkv=fused_qkv)
     with pytest.raises(ValueError, match="GPU only"):
         R.load(p, device="cpu")
     run = R.load(p, device="gpu")
