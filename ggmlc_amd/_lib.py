@@ -114,6 +114,27 @@ SIGNATURES = {
     "gq_paged_advance": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "gq_kv_pages_copy": (ctypes.c_int, [_P, _P, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
     "gq_probe_stream_read": (ctypes.c_int, [_vp, ctypes.c_size_t, _vp, _vp]),
+    "gq_exec_available_devices": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+    "gq_exec_create": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "gq_exec_free": (None, [_vp]),
+    "gq_exec_describe": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+    "gq_exec_inspect": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_size_t,
+                                       ctypes.POINTER(ctypes.c_size_t)]),
+    "gq_exec_prepare": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64), _i64]),
+    "gq_exec_set_input": (ctypes.c_int, [_vp, ctypes.c_uint32, _vp, ctypes.c_size_t]),
+    "gq_exec_set_input_by_name": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, ctypes.c_size_t]),
+    "gq_exec_run": (ctypes.c_int, [_vp]),
+    "gq_exec_synchronize": (ctypes.c_int, [_vp]),
+    "gq_exec_get_tensor_shape": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.POINTER(_i64)]),
+    "gq_exec_get_output": (ctypes.c_int, [_vp, ctypes.c_uint32, _vp, ctypes.c_size_t,
+                                          ctypes.POINTER(ctypes.c_size_t)]),
+    "gq_exec_init_kv_cache": (ctypes.c_int, [_vp, _i64]),
+    "gq_exec_reset_kv_cache": (ctypes.c_int, [_vp]),
+    "gq_exec_has_kv_cache": (ctypes.c_int, [_vp]),
+    "gq_exec_set_logits_last_only": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "gq_exec_logits_last_only": (ctypes.c_int, [_vp]),
+    "gq_exec_set_enable_graphs": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "gq_exec_position": (_i64, [_vp]),
 }
 
 _lib = None

@@ -39,10 +39,11 @@ _QUANT = {2, 8}  # Q4_0, Q8_0
 
 
 def get_available_devices() -> list[str]:
-    """Devices this runtime executes on (runner.py:34-38): the visible GPUs."""
-    import torch
+    """Devices this runtime executes on (runner.py:34-38; executor.cpp:184): the visible
+    GPUs, from libgq's executor."""
+    from .executor import get_available_devices as devs
 
-    return [f"cuda:{i}" for i in range(torch.cuda.device_count())]
+    return devs()
 
 
 class _Match:
@@ -233,23 +234,24 @@ def match_llama(g: Graph, reader: GGUFReader) -> _Match:
 
 
 class ModelRunner:
-    """ggmlc's ModelRunner (runner.py:48-316) on the MI355X path."""
+    """ggmlc's ModelRunner (runner.py:48-316) on the MI355X path: runs go through libgq's
+    executor handle (`executor.ModelExecutor`, the C ABI gq_exec_*: GGUF and graph parsing,
+    the decoder and its per-bucket HIP graphs in C++, no torch); `executor` also serves
+    the paged-KV surface the continuous-batching scheduler drives."""
 
     def __init__(self, model_source: str | Path | bytes, n_threads: int = 1, device: str = "auto"):
-        import torch
-
-        from . import _lib, ops
-        from .model import Decoder, LayerWeights, LlamaConfig, ModelWeights
+        from .executor import ModelExecutor
 
         if isinstance(model_source, (str, Path)):
             p = Path(model_source)
             if not p.exists():
                 raise FileNotFoundError(f"Model file not found: {p}")
-            reader = GGUFReader(p)
+            raw = p.read_bytes()
         elif isinstance(model_source, (bytes, bytearray, memoryview)):
-            reader = GGUFReader(model_source)
+            raw = bytes(model_source)
         else:
             raise TypeError(f"Expected file path or bytes, got {type(model_source)}")
+        reader = GGUFReader(raw)
         if "ggmlc.graph_spec" not in reader.metadata:
             raise ValueError("GGUF metadata missing 'ggmlc.graph_spec'")
         self.n_threads = n_threads
@@ -270,22 +272,45 @@ class ModelRunner:
         if not dev.startswith("cuda"):
             raise ValueError(f"device {device!r}: this runtime executes on the GPU only ('gpu[:N]', 'cuda[:N]', "
                              "'auto')")
-        if not torch.cuda.is_available():
-            raise RuntimeError("no GPU visible: this runtime has no CPU path")
-        self.device = dev
-        self._dev = torch.device(dev)
-        torch.cuda.set_device(self._dev)
-        _lib.check(_lib.load().gq_init())
-
         m = match_llama(self.graph, reader)
         self.match = m
+        self._reader = reader
         qt = {m.embed_type, m.lm_type} | {w[1] for L in m.layers for k in ("o", "gate_up", "down")
                                              for w in [L[k]]} | {w[1] for L in m.layers for w in L["qkv"]}
+        from .model import LlamaConfig
+
         self.cfg = LlamaConfig(self.name, len(m.layers), m.n_embd, m.n_head, m.n_head_kv, m.head_dim, m.n_ff,
                                m.n_vocab, m.embed_type if len(qt) == 1 else -1,
                                tied_embeddings=m.lm_head == m.embed, rms_eps=m.rms_eps, rope_base=m.rope_base,
                                qkv_bias=m.layers[0]["qkv_b"] is not None)
+        try:
+            native = ModelExecutor(raw, dev)
+        except RuntimeError as e:  # no GPU, or a device index past the visible ones
+            raise RuntimeError(f"no usable GPU for device {device!r}: {e}") from e
+        self.device = native.device
+        self._weights = None
+        self.executor = PagedExecutor(self, native)
 
+    @property
+    def weights(self):
+        """The model as device tensors for the batched decoder (built on first use)."""
+        if self._weights is None:
+            self._weights = self._build_weights()
+        return self._weights
+
+    @property
+    def _dev(self):
+        import torch
+
+        return torch.device(self.device)
+
+    def _build_weights(self):
+        import torch
+
+        from . import ops
+        from .model import LayerWeights, ModelWeights
+
+        m, reader = self.match, self._reader
         cache: dict[str, ops.QWeight] = {}
 
         def upload(names_types) -> ops.QWeight:
@@ -313,38 +338,24 @@ class ModelRunner:
                                down_b=upload_bias([L["down_b"]] if L["down_b"] else None)) for L in m.layers]
         embed = upload([(m.embed, m.embed_type, m.n_embd)])
         lm = upload([(m.lm_head, m.lm_type, m.n_embd)])
-        self.weights = ModelWeights(self.cfg, embed, lm, layers)
-        self._decoder_cls = Decoder
-        self.decoder = None
-        self._kv = False
-        self.executor = PagedExecutor(self)
+        return ModelWeights(self.cfg, embed, lm, layers)
 
     # -- KV cache (runner.py:304-316) -------------------------------------------------
     def init_kv_cache(self, max_ctx: int = 2048) -> None:
-        if self.decoder is not None and self._kv:
-            return
-        self.decoder = self._decoder_cls(self.weights, int(max_ctx), self._dev)
-        self._kv = True
+        self.executor.native.init_kv_cache(int(max_ctx))
 
     def reset_kv_cache(self) -> None:
-        if self.decoder is not None:
-            for k, v in zip(self.decoder.k_cache, self.decoder.v_cache):
-                k.zero_()
-                v.zero_()
-            self.decoder.reset(0)
+        self.executor.native.reset_kv_cache()
 
     def has_kv_cache(self) -> bool:
-        return self._kv
+        return self.executor.native.has_kv_cache()
 
     # -- run --------------------------------------------------------------------------
     def __call__(self, *args: np.ndarray, symbols: dict[str, int] | None = None, n_threads: int | None = None,
                  enable_arena_reuse: bool = True, **kwargs: np.ndarray):
-        """Token ids (positional or by input name) -> logits of every token, shaped
-        like the reference's get_outputs: [s, vocab] for a rank-2 input."""
-        import torch
-
-        from .model import pad_kv_len
-
+        """Token ids (positional or by input name) -> logits of every token (of the last
+        one with executor.set_logits_last_only(True)), shaped like the reference's
+        get_outputs: [s, vocab] for a rank-2 input."""
         if len(args) == 1 and isinstance(args[0], dict) and not kwargs:
             kwargs, args = args[0], ()
         if args:
@@ -363,49 +374,37 @@ class ModelRunner:
         syms = dict(symbols or {})
         if "s" in syms and int(syms["s"]) != s:
             raise ValueError(f"symbol s = {syms['s']} but {s} input ids")
-        if self._kv:
-            pos = int(syms.get("pos", int(self.decoder.pos[0])))
-        else:  # no KV cache: the whole sequence from position 0 in a scratch cache
-            pos = 0
-            self.decoder = self._decoder_cls(self.weights, pad_kv_len(s, 1 << 30), self._dev)
-        dec = self.decoder
-        if pos + s > dec.max_ctx:
-            raise ValueError(f"pos + s = {pos + s} exceeds the KV cache ({dec.max_ctx})")
-        dec.reset(pos)
-        buf = dec._buffers(s)["ids"]
-        buf.copy_(torch.from_numpy(flat).to(self._dev))
-        dec.step(s, pad_kv_len(pos + s, dec.max_ctx), logits_all=True)
-        logits = dec._buffers(s)["logits_all"].cpu().numpy()
-        if not self._kv:
-            self.decoder = None
-        self._last = logits
-        shape = [1, 1, s, self.cfg.n_vocab][-max(2, rank):]
-        return logits.reshape(shape)
+        ex = self.executor.native
+        syms["s"] = s
+        if not ex.has_kv_cache():
+            syms["pos"] = 0
+        ex.prepare(syms, enable_arena_reuse)
+        ex.set_input_by_id(self.inputs[0], flat)
+        ex.run()
+        logits = ex.get_output(self.outputs[0])
+        self._last = (logits, dict(syms))
+        rows = logits.shape[0]
+        return logits.reshape([1, 1, rows, self.cfg.n_vocab][-max(2, rank):])
 
     def get_outputs(self, input_ndim: int = 2):
-        s = self._last.shape[0]
-        return self._last.reshape([1, 1, s, self.cfg.n_vocab][-max(2, input_ndim):])
+        logits = self._last[0]
+        return logits.reshape([1, 1, logits.shape[0], self.cfg.n_vocab][-max(2, input_ndim):])
 
     def run_benchmark(self, runs: int = 5, n_threads: int | None = None) -> list[float]:
-        """Latency (ms) of the last call's step shape, replayed `runs` times."""
+        """Latency (ms) of the last call's step, replayed `runs` times at its position."""
         import time
 
-        import torch
-
-        from .model import pad_kv_len
-
-        dec = self.decoder
-        if dec is None or not hasattr(self, "_last"):
+        if not hasattr(self, "_last"):
             raise RuntimeError("call the runner once before benchmarking")
-        s = self._last.shape[0]
-        p0 = int(dec.pos[0]) - s
+        ex = self.executor.native
+        syms = self._last[1]
+        ids = np.zeros(int(syms["s"]), np.int32)
         out = []
         for _ in range(runs):
-            dec.reset(p0)
-            torch.cuda.synchronize()
+            ex.prepare(syms)
+            ex.set_input_by_id(self.inputs[0], ids)
             t0 = time.perf_counter()
-            dec.step(s, pad_kv_len(p0 + s, dec.max_ctx))
-            torch.cuda.synchronize()
+            ex.run()
             out.append((time.perf_counter() - t0) * 1e3)
         return out
 
@@ -421,10 +420,19 @@ class PagedExecutor:
     `configure_vmm_pool` is accepted for the reference's signature and changes nothing
     (the pool is allocated once, there is no warm pool of mapped pages)."""
 
-    def __init__(self, runner: "ModelRunner"):
+    def __init__(self, runner: "ModelRunner", native=None):
         self._runner = runner
+        self.native = native  # executor.ModelExecutor: the handle the runner's calls go through
         self._tpp = 128
         self.batch = None
+
+    def __getattr__(self, name):
+        # the reference executor's other methods (prepare, set_input_by_id, run,
+        # get_output_bytes, get_tensor_shape, set_logits_last_only, ...) are the native handle's
+        native = self.__dict__.get("native")
+        if native is None:
+            raise AttributeError(name)
+        return getattr(native, name)
 
     # -- setup ------------------------------------------------------------------------
     def set_tokens_per_page(self, n: int) -> None:

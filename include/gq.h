@@ -357,6 +357,62 @@ int gq_paged_advance(int32_t* pos, const int32_t* active, int64_t B, gq_stream_t
 int gq_kv_pages_copy(gq_tensor* pool, gq_tensor* cache, const int32_t* pages, int64_t n_pages, int64_t page_size,
                      int64_t r0, int64_t r1, int to_pool, gq_stream_t stream);
 
+/* ---- executor handle --------------------------------------------------------
+ * ggmlc's ModelExecutor (runtime/include/ggmlc/executor.h:25-289; the surface its
+ * Python binding exposes, runtime/bindings/python_bindings.cpp:137-216) for the graphs
+ * this library executes: a ggmlc .gguf (GGUF v3 whose `ggmlc.graph_spec` JSON is the
+ * execution graph, runtime/src/loader.cpp:77-443) whose graph is the LLaMA-family
+ * decoder layout ggmlc's compiler emits (embedding GET_ROWS; per layer RMS_NORM -> QKV
+ * MUL_MAT (fused with three VIEWs, or three products; optional F32 bias inputs) ->
+ * RESHAPE -> NEOX ROPE (q, k) -> PERMUTE -> FLASH_ATTN_EXT -> RESHAPE -> MUL_MAT -> ADD,
+ * RMS_NORM -> gate|up MUL_MAT -> GLU SWIGLU -> MUL_MAT -> ADD; RMS_NORM -> head MUL_MAT).
+ * A graph outside it is rejected with GQ_ERR_UNSUPPORTED naming the first node that
+ * does not fit. Weights are the file's bytes, uploaded once; each step runs the
+ * decoder on this library's kernels, replayed from one HIP graph per (s, n_kv, output
+ * rows) bucket after that bucket's first run. The handle owns its device memory and a
+ * stream of default priority. One handle per thread (not re-entrant), as in the reference.
+ *
+ *   device: "auto", "gpu", "cuda" (device 0), "gpu:N", "cuda:N"; anything else, or no
+ *   visible GPU, is an error (this runtime has no CPU path).
+ *   symbols: "s" (tokens this step, required) and "pos" (position of the first; default
+ *   the handle's running position with a KV cache, else 0).
+ *   The input is the graph's token-id tensor (I32 or I64, s values); the output its
+ *   logits, F32 [n_vocab, s] (rows = tokens), or [n_vocab, 1] with logits_last_only
+ *   (executor.cpp:2396-2410). Without init_kv_cache each run is a whole sequence from
+ *   position 0 in a scratch cache. n_kv follows pad_kv_len (executor.cpp:58-64). */
+typedef struct gq_exec gq_exec;
+/* ModelExecutor::get_available_devices (executor.cpp:184): JSON list of "cuda:N" for the
+ * visible GPUs (no CPU entry: this runtime has no CPU path). */
+int gq_exec_available_devices(char* buf, size_t buf_len, size_t* needed);
+int gq_exec_create(const void* gguf_bytes, size_t len, const char* device, gq_exec** out);
+void gq_exec_free(gq_exec* h);
+/* JSON: name, device, inputs, outputs, parameters, symbol_table, names {id: name},
+ * embed / lm_head / layers (the matched weights), config (hyper-parameters). The call
+ * writes at most buf_len bytes (NUL-terminated) and the full size + 1 to *needed. */
+int gq_exec_describe(gq_exec* h, char* buf, size_t buf_len, size_t* needed);
+/* The same description of a model without a device (parse and match only). */
+int gq_exec_inspect(const void* gguf_bytes, size_t len, char* buf, size_t buf_len, size_t* needed);
+int gq_exec_prepare(gq_exec* h, const char* const* sym_names, const int64_t* sym_values, int64_t n_syms);
+int gq_exec_set_input(gq_exec* h, uint32_t tensor_id, const void* data, size_t bytes);
+int gq_exec_set_input_by_name(gq_exec* h, const char* name, const void* data, size_t bytes);
+/* Runs the prepared step synchronously; the output is then held on the host. */
+int gq_exec_run(gq_exec* h);
+int gq_exec_synchronize(gq_exec* h);
+int gq_exec_get_tensor_shape(gq_exec* h, uint32_t tensor_id, int64_t ne[4]);
+/* Copies the output's bytes (F32, rows of n_vocab) to dst when dst_bytes suffices;
+ * *written (if non-NULL) receives the output's size either way. */
+int gq_exec_get_output(gq_exec* h, uint32_t tensor_id, void* dst, size_t dst_bytes, size_t* written);
+int gq_exec_init_kv_cache(gq_exec* h, int64_t max_ctx);
+int gq_exec_reset_kv_cache(gq_exec* h);
+int gq_exec_has_kv_cache(gq_exec* h);
+int gq_exec_set_logits_last_only(gq_exec* h, int enable);
+int gq_exec_logits_last_only(gq_exec* h);
+/* HIP graph replay of the step buckets (on by default; the reference's
+ * set_enable_cuda_graph). */
+int gq_exec_set_enable_graphs(gq_exec* h, int enable);
+/* The handle's running position (tokens written to the KV cache), -1 for NULL. */
+int64_t gq_exec_position(gq_exec* h);
+
 /* ---- measurement aid ------------------------------------------------------
  * No counterpart in the reference. Reads `bytes` (16-byte aligned) once with
  * the coalesced 16-byte streaming loads the GEMV uses, so a benchmark can

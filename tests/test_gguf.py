@@ -234,3 +234,73 @@ def test_matcher_rejects_other_graphs():
     with pytest.raises(NotImplementedError):
         match_llama(g2, r)
     assert OPS["FLASH_ATTN_EXT"] == 74 and OPS["GLU"] == 100  # ggml 0.20.2 enum ggml_op
+
+
+@pytest.mark.parametrize("fused_qkv,bias,tied", [(True, False, True), (False, False, False), (True, True, True),
+                                                 (False, True, False)])
+def test_native_executor_reads_the_file_like_the_python_reader(tmp_path, fused_qkv, bias, tied):
+    """libgq's executor parser (GGUF v3 + graph_spec JSON + the decoder matcher, C++,
+    gq_exec_inspect: no device) reports the graph surface, the matched weights and the
+    hyper-parameters the Python reader and matcher report for the same file."""
+    from ggmlc_amd.executor import inspect
+
+    c = LlamaConfig("m", 3, 960, 15, 5, 64, 2560, 1024, O.Q8_0, tied_embeddings=tied, rope_base=50000.0,
+                    rms_eps=1e-6)
+    rng = np.random.default_rng(5)
+
+    def q(n, k):
+        return O.quantize_weights((rng.standard_normal((n, k)) * 0.02).astype(np.float32), c.qtype)
+
+    nq = c.q_dim + 2 * c.kv_dim
+    layers = [(q(nq, c.n_embd), q(c.n_embd, c.q_dim), q(2 * c.n_ff, c.n_embd), q(c.n_embd, c.n_ff))
+              + (((rng.standard_normal(nq) * 0.1).astype(np.float32), None,
+                  (rng.standard_normal(2 * c.n_ff) * 0.1).astype(np.float32), None) if bias else ())
+              for _ in range(c.n_layer)]
+    emb = q(c.n_vocab, c.n_embd)
+    p = write_llama_gguf(tmp_path / "m.gguf", c, (emb, emb if tied else q(c.n_vocab, c.n_embd), layers),
+                         max_pos=256, fused_qkv=fused_qkv)
+    raw = p.read_bytes()
+    d = inspect(raw)
+    r = gguf.GGUFReader(p)
+    g = Graph.from_json(r.metadata["ggmlc.graph_spec"])
+    m = match_llama(g, r)
+    cfg = d["config"]
+    assert (cfg["n_layer"], cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"], cfg["head_dim"], cfg["n_ff"],
+            cfg["n_vocab"]) == (len(m.layers), m.n_embd, m.n_head, m.n_head_kv, m.head_dim, m.n_ff, m.n_vocab)
+    assert cfg["rope_base"] == m.rope_base and cfg["rms_eps"] == pytest.approx(m.rms_eps)
+    assert cfg["tied"] == (m.lm_head == m.embed) and cfg["qkv_bias"] == bias
+    assert d["inputs"] == g.inputs and d["outputs"] == g.outputs and d["symbol_table"] == g.symbol_table
+    assert d["embed"] == m.embed and d["lm_head"] == m.lm_head
+    for Ln, Lp in zip(d["layers"], m.layers):
+        assert Ln["qkv"]["names"] == [n for n, *_ in Lp["qkv"]]
+        assert Ln["qkv"]["bias"] == (list(Lp["qkv_b"]) if Lp["qkv_b"] else [])
+        assert Ln["gate_up"]["bias"] == ([Lp["gate_up_b"]] if Lp["gate_up_b"] else [])
+        assert Ln["down"]["names"] == [Lp["down"][0]] and Ln["o"]["bias"] == []
+        assert (Ln["qkv"]["K"], Ln["qkv"]["N"]) == (c.n_embd, nq)
+
+
+def test_native_executor_rejects_bad_files(tmp_path):
+    from ggmlc_amd import _lib
+    from ggmlc_amd.executor import inspect
+
+    c = _tiny()
+    p = write_llama_gguf(tmp_path / "m.gguf", c, _weights(c), max_pos=64)
+    raw = p.read_bytes()
+    with pytest.raises(_lib.GQError, match="magic"):
+        inspect(b"XXXX" + raw[4:])
+    with pytest.raises(_lib.GQError, match="truncated|past the end"):
+        inspect(raw[: len(raw) // 2])
+    # a graph the decoder layout does not cover is refused, naming the node
+    g = Graph.from_json(gguf.GGUFReader(p).metadata["ggmlc.graph_spec"])
+    for n in g.nodes:
+        if n.op == "ROPE":
+            n.attributes["mode"] = 0
+    w = gguf.GGUFWriter()
+    w.add_string("ggmlc.graph_spec", g.to_json())
+    rd = gguf.GGUFReader(p)
+    for name in rd.tensor_order:
+        t = rd.tensors[name]
+        w.add_tensor(name, list(t.ne) + [1] * (4 - len(t.ne)), t.ggml_type, bytes(rd.tensor_bytes(name)))
+    with pytest.raises(_lib.GQError, match="NEOX") as e:
+        inspect(w.to_bytes())
+    assert e.value.code == -2  # GQ_ERR_UNSUPPORTED
