@@ -12,22 +12,27 @@ methodology, runtime/tools/ggmlc_bench.cpp:295-560).
               32 layers -> lm_head -> argmax), replayed from the (1, n_kv) bucket's
               HIP graph whose input is its own previous output; value = tg tokens/s
               over exactly --steps tokens (tg128 by default).
-* roofline  = the decode GEMV (k_gemv_grp<Q4_0, M=1>), the dominant kernel: the
-              129 GEMV launches of one decode token (qkv, o, gate_up, down per layer,
-              lm_head) captured in one graph with the model's own weights and timed
-              with HIP events on the launch stream; achieved = their algorithmic bytes
-              (weights + fp32 x + fp32 y) / their time. rocprofv3's average for
-              k_gemv_grp<Q4_0> over this command covers the same launch mix.
+* roofline  = the decode GEMV, the dominant kernel of the step: the 129 fused GEMV
+              launches of one decode token exactly as the timed step issues them
+              (qkv with ADD + RMS_NORM + ROPE + SET_ROWS, o, gate_up with ADD +
+              RMS_NORM + SWIGLU, down, lm_head with ADD + RMS_NORM), same buffers and
+              weights, captured back to back in one graph and timed with HIP events on
+              the launch stream; achieved = their algorithmic bytes (weights + the fp32
+              activations read + the outputs written) / their time.
 * roofline_prefill_gemm = the 128 prefill GEMMs (M = 512) of one ubatch, same way.
 * gemv_c1_q8_0 = configs[0], the Q8_0 Linear 4096 -> 4096 GEMV (16 rotating copies).
+* mlp_c2_q4_0 = configs[1], the SwiGLU MLP block 4096 -> 11008 -> 4096 (Q4_0) at
+              M = 1, 8, 128, 512 tokens (4 rotating weight copies, 304 MB).
+* smollm2_c3 = configs[2], the SmolLM2-360M-shape decoder (Q8_0): pp512, then tg128.
 * c5_batched_decode = configs[4]: a Qwen2.5-1.5B-shape decoder (Q8_0, tied embeddings)
               over the paged KV pool; 16 sequences with contexts uniform in [256, 4096],
               half of them sharing a 512-token prefix (its pages computed once), then 64
               batched decode steps at B = 1, 2, 4, 8, 16, every sequence at its own
               position; tokens/s = B * steps / time (graph replays chained on the device).
 * cpu_baseline = the reference's own ggml CPU backend (oracle/_ref, built from the
-              reference sources) running the same decoder graph on the same weights
-              with the host's cores: pp512 then decode tokens for a bounded sample.
+              reference sources, AVX-512 build where the host has it) running the same
+              decoder graph on the same weights with the host's cores: pp512, then decode
+              tokens at the GPU's context (~1030), and a 1-thread decode sample.
 
 Weights (3.7 GB) far exceed the 256 MB Infinity Cache, so every decode token
 streams them from HBM. Inputs are resident before timing.
@@ -49,6 +54,7 @@ METRIC = "pp512 & tg128 tokens/sec (1 GPU, Q8_0/Q4_0); GEMV HBM GB/s as % of pea
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 UBATCH = 512
+CPU_SHARE = 16  # host cores one GPU's job may use on the GPU boxes
 
 
 def parse():
@@ -62,18 +68,55 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="decode budget of the CPU sample")
     p.add_argument("--c1-launches", type=int, default=400)
     p.add_argument("--no-sweep", action="store_true", help="skip the Q8_0 decode GEMV size sweep")
+    p.add_argument("--no-c2", action="store_true", help="skip the configs[1] MLP M-sweep")
+    p.add_argument("--no-c3", action="store_true", help="skip the configs[2] SmolLM2-360M decoder")
     p.add_argument("--c5-steps", type=int, default=64, help="timed batched decode steps per batch size")
     p.add_argument("--no-c5", action="store_true", help="skip the configs[4] continuous-batching decode")
     p.add_argument("--c5-only", action="store_true", help="run only the configs[4] measurement (profiling)")
     p.add_argument("--c5-batches", default="1,2,4,8,16", help="configs[4] batch sizes")
+    p.add_argument("--roofline-only", action="store_true",
+                   help="only the configs[3] decoder (pp, tg) and the step-GEMV roofline graph: the workload of "
+                        "the rocprofv3 --kernel-trace --stats summary behind roofline")
     p.add_argument("--traffic-probe", action="store_true",
-                   help="only launch one token's decode GEMVs and a 256 MiB device copy, eagerly, 3 times each "
-                        "(the workload of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs behind roofline.traffic)")
+                   help="only launch one token's fused decode GEMVs and a 256 MiB device copy, eagerly, 3 times "
+                        "each (the workload of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs behind "
+                        "roofline.traffic)")
+    p.add_argument("--gemm-probe", action="store_true",
+                   help="only launch one ubatch's 128 prefill GEMMs (M = 512) eagerly, 3 times (the workload of "
+                        "the rocprofv3 --pmc MFMA counter runs)")
     return p.parse_args()
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _ev():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True)
+
+
+def time_graph(fn, reps: int, warm: int = 1) -> float:
+    """ms per replay of a HIP graph of fn(), timed with events on the replay stream."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = _ev(), _ev()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del g
+    return e0.elapsed_time(e1) / reps
 
 
 def main() -> int:
@@ -86,11 +129,10 @@ def main() -> int:
         print("bench.py: --prompt must be a positive multiple of 512", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     from ggmlc_amd import _lib, ops
-    from ggmlc_amd.model import LLAMA_7B, Decoder, pad_kv_len, random_weights
+    from ggmlc_amd.model import LLAMA_7B, SMOLLM2_360M, random_weights
 
     torch.cuda.set_device(0)
     _lib.check(_lib.load().gq_init())
@@ -100,26 +142,161 @@ def main() -> int:
         print(json.dumps({"c5_batched_decode": bench_c5(dev, args.c5_steps, batches)}), flush=True)
         return 0
     cfg = LLAMA_7B
-    stream = torch.cuda.current_stream()
 
     log(f"building {cfg.name} Q4_0 weights on device")
     w = random_weights(cfg, dev, seed=1234)
     torch.cuda.synchronize()
     if args.traffic_probe:
-        return traffic_probe(w, cfg, dev)
-    n_ctx = args.prompt + args.warmup + args.steps
+        return traffic_probe(w, dev)
+    if args.gemm_probe:
+        return gemm_probe(w, dev)
+
+    r7, dec = bench_decoder(w, dev, args.prompt, args.steps, args.warmup, args.pp_reps)
+    ws = ops.Workspace(dev)
+    ws.get(1 << 20)
+
+    # ---- roofline: the fused GEMVs of the timed decode step, one graph, HIP events
+    run_gemvs, gemv_bytes = step_gemv_launches(dec)
+    R = 20
+    gemv_ms_token = time_graph(run_gemvs, R, warm=3)
+    n_gemv = len(gemv_bytes)
+    gemv_bytes_token = sum(gemv_bytes)
+    gemv_gbs = gemv_bytes_token / (gemv_ms_token * 1e-3) / 1e9
+    weights_token = w.decode_bytes
+    # the same launches as plain streaming reads of the same weight buffers: the
+    # ceiling a kernel that only reads its weights reaches at these per-launch sizes
+    probe_ms_token = time_probe_launches(step_weight_buffers(w))
+    log(f"step GEMVs: {gemv_ms_token * 1e3:.1f} us/token, {gemv_gbs:.0f} GB/s "
+        f"({gemv_gbs / HBM_PEAK_GBS:.1%}), same-size read {probe_ms_token * 1e3:.1f} us")
+    roofline = {
+        "kernel": "k_gemv_grp<Q4_0, M=1> fused: the 129 GEMV launches of one timed decode step (qkv + "
+                  "ADD/RMS_NORM/ROPE/SET_ROWS, o, gate_up + ADD/RMS_NORM/SWIGLU, down x 32; lm_head + ADD/RMS_NORM)",
+        "bound": "hbm",
+        "achieved": round(gemv_gbs, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+        "traffic": load_traffic("k_gemv_grp<Q4_0, M=1> fused step mix"),
+        "bytes_per_launch": round(gemv_bytes_token / n_gemv),
+        "weight_bytes_per_launch": round(weights_token / n_gemv),
+        "us_per_launch": round(gemv_ms_token * 1e3 / n_gemv, 3),
+        "launches_per_token": n_gemv,
+        "gemv_ms_per_token": round(gemv_ms_token, 4),
+        "gemv_share_of_step": round(gemv_ms_token / r7["ms_per_token"], 4),
+        "read_probe_same_launches_ms": round(probe_ms_token, 4),
+        "frac_of_same_size_read": round(probe_ms_token / gemv_ms_token, 4),
+    }
+    if args.roofline_only:
+        print(json.dumps({"configs[3]": r7, "roofline": roofline}), flush=True)
+        return 0
+
+    # ---- prefill GEMM rate: the 128 GEMMs of one ubatch (M = 512)
+    gemm_ubatch, gemm_flops = prefill_gemms(w, dev, ws)
+    gemm_ms = time_graph(gemm_ubatch, 3)
+    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    del gemm_ubatch
+    log(f"prefill GEMMs: {gemm_ms:.3f} ms/ubatch, {gemm_tflops:.0f} TFLOP/s")
+
+    c1 = bench_c1(dev, ws, args.c1_launches)
+    sweep = [] if args.no_sweep else gemv_sweep_q8_0(dev, ws)
+    read_gbs, copy_gbs = measured_ceilings(dev)
+
+    result = {
+        "metric": METRIC,
+        "value": r7["tg_tok_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r7["ms_per_token"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights x q8_0 activations: int8 dot4 with exact int32 block sums (decode); exact "
+                 "fp16 hi+lo block products on f16 MFMA (prefill); f32 accumulate; f16 KV",
+        "data": "synthetic (random-init weights N(0,0.02) -> Q4_0; uniform-random prompt ids)",
+        "config": {
+            "workload": f"configs[3] {cfg.name} decoder, Q4_0, batch 1: pp{args.prompt} (ubatch 512) then "
+                        f"greedy decode; value = tg{args.steps} tokens/s",
+            "global_batch": 1,
+            "seq_len": args.prompt,
+            "parallelism": "single GPU",
+            "weight_bytes": w.nbytes,
+        },
+        "tg_tok_s": r7["tg_tok_s"],
+        "pp512_tok_s": r7["pp512_tok_s"],
+        f"pp{args.prompt}_tok_s": r7[f"pp{args.prompt}_tok_s"],
+        "decode_weight_GBps": r7["decode_weight_GBps"],
+        "decode_weight_plus_kv_GBps": r7["decode_weight_plus_kv_GBps"],
+        "roofline": roofline,
+        "roofline_prefill_gemm": {
+            "kernel": "k_gemm<Q4_0>: the 128 GEMMs of one 512-token ubatch (activation quantize excluded); "
+                      "each exact block product takes two f16 MFMAs (hi, lo) per 32 K",
+            "bound": "mfma",
+            "achieved": round(gemm_tflops, 1),
+            "peak": FP16_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
+            "mfma_tflops_issued": round(2 * gemm_tflops, 1),
+            "ms_per_ubatch": round(gemm_ms, 3),
+        },
+        "gemv_c1_q8_0": c1,
+        "gemv_sweep_q8_0": sweep,
+        "measured_read_GBps": round(read_gbs, 1),
+        "measured_copy_GBps": round(copy_gbs, 1),
+        "wall_s_timed": r7["wall_s_timed"],
+    }
+
+    del dec, run_gemvs
+    torch.cuda.empty_cache()
+    if not args.no_c2:
+        log("configs[1]: SwiGLU MLP block, M sweep")
+        result["mlp_c2_q4_0"] = bench_c2(dev, ws)
+    if not args.no_c3:
+        log("configs[2]: SmolLM2-360M-shape decoder")
+        w3 = random_weights(SMOLLM2_360M, dev, seed=360)
+        r3, d3 = bench_decoder(w3, dev, 512, 128, 2, args.pp_reps)
+        run3, bytes3 = step_gemv_launches(d3)
+        ms3 = time_graph(run3, 20, warm=3)
+        r3["step_gemvs"] = {"launches": len(bytes3), "us_per_launch": round(ms3 * 1e3 / len(bytes3), 3),
+                            "achieved_GBps": round(sum(bytes3) / (ms3 * 1e-3) / 1e9, 1),
+                            "ms_per_token": round(ms3, 4)}
+        r3["published_context"] = {"pp512_tok_s": 9900, "tg32_tok_s": 160.6,
+                                   "hardware": "NVIDIA RTX 4050 Laptop (reference README.md:243, "
+                                               "docs/benchmarks/ggmlc_vs_llama_cpp.md:121,150)"}
+        result["smollm2_c3"] = r3
+        del d3, w3, run3
+        torch.cuda.empty_cache()
+    if not args.no_c5:
+        log("configs[4]: batched paged decode")
+        result["c5_batched_decode"] = bench_c5(dev, args.c5_steps, batches)
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds, ctx=args.prompt)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def bench_decoder(w, dev, prompt_len: int, steps: int, warmup: int, pp_reps: int):
+    """pp (per 512-token ubatch graph) and tg (graph replays chained on the device) of
+    one decoder at batch 1; returns (figures, the Decoder)."""
+    import numpy as np
+    import torch
+
+    from ggmlc_amd.model import Decoder, pad_kv_len
+
+    cfg = w.cfg
+    n_ctx = prompt_len + warmup + steps
     max_ctx = pad_kv_len(n_ctx, 1 << 30)
     dec = Decoder(w, max_ctx, dev)
-    log(f"weights {w.nbytes / 1e9:.3f} GB, KV cache {2 * cfg.n_layer * cfg.kv_dim * max_ctx * 2 / 1e9:.3f} GB "
-        f"(max_ctx {max_ctx})")
-
-    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    log(f"{cfg.name}: weights {w.nbytes / 1e9:.3f} GB, KV cache "
+        f"{2 * cfg.n_layer * cfg.kv_dim * max_ctx * 2 / 1e9:.3f} GB (max_ctx {max_ctx})")
 
     # ---- prefill graphs: one per ubatch bucket, reading its slice of the prompt
     gen = torch.Generator(device=dev)
     gen.manual_seed(99)
-    prompt = torch.randint(0, cfg.n_vocab, (args.prompt,), generator=gen, device=dev, dtype=torch.int32)
-    n_ub = args.prompt // UBATCH
+    prompt = torch.randint(0, cfg.n_vocab, (prompt_len,), generator=gen, device=dev, dtype=torch.int32)
+    n_ub = prompt_len // UBATCH
     pp_graphs = []
     for u in range(n_ub):
         dec.reset(u * UBATCH)
@@ -131,10 +308,10 @@ def main() -> int:
     # overwrites it with the new token, so replays generate without host work
     _, next1 = dec.decode_buffers()
     tg_graphs = {}
-    for i in range(args.warmup + args.steps):
-        n_kv = pad_kv_len(args.prompt + i + 1, max_ctx)
+    for i in range(warmup + steps):
+        n_kv = pad_kv_len(prompt_len + i + 1, max_ctx)
         if n_kv not in tg_graphs:
-            dec.reset(args.prompt + i)
+            dec.reset(prompt_len + i)
             tg_graphs[n_kv] = dec.capture(1, n_kv, ids=next1)
     torch.cuda.synchronize()
 
@@ -143,14 +320,13 @@ def main() -> int:
         for g in pp_graphs:
             g.replay()
 
-    # ---- pp: time each ubatch (pp512 = the first, ppN = all)
-    log(f"prefill: {n_ub} ubatch(es) of {UBATCH}, {args.pp_reps} reps")
+    log(f"prefill: {n_ub} ubatch(es) of {UBATCH}, {pp_reps} reps")
     prefill()
     torch.cuda.synchronize()
     t_first, t_all = [], []
-    for _ in range(args.pp_reps):
+    for _ in range(pp_reps):
         dec.reset(0)
-        es = [ev() for _ in range(n_ub + 1)]
+        es = [_ev() for _ in range(n_ub + 1)]
         es[0].record()
         for u, g in enumerate(pp_graphs):
             g.replay()
@@ -159,73 +335,120 @@ def main() -> int:
         t_first.append(es[0].elapsed_time(es[1]))
         t_all.append(es[0].elapsed_time(es[-1]))
     pp512_tok_s = UBATCH * 1000.0 / float(np.median(t_first))
-    ppN_tok_s = args.prompt * 1000.0 / float(np.median(t_all))
-    log(f"pp512 {pp512_tok_s:.0f} tok/s, pp{args.prompt} {ppN_tok_s:.0f} tok/s")
+    ppN_tok_s = prompt_len * 1000.0 / float(np.median(t_all))
+    log(f"pp512 {pp512_tok_s:.0f} tok/s, pp{prompt_len} {ppN_tok_s:.0f} tok/s")
 
     # ---- tg: the prompt's KV is in the cache (last prefill rep); decode from its token
     prefill()
     next1.copy_(b_pp["next"])
     torch.cuda.synchronize()
-    if int(dec.pos[0]) != args.prompt:
+    if int(dec.pos[0]) != prompt_len:
         raise RuntimeError("device position after prefill is wrong")
-    tokens = []
-    pos = args.prompt
-    for i in range(args.warmup):
+    pos = prompt_len
+    for i in range(warmup):
         tg_graphs[pad_kv_len(pos + 1, max_ctx)].replay()
         pos += 1
     torch.cuda.synchronize()
-    log(f"decode: {args.warmup} warmup + {args.steps} timed tokens (graph replay)")
-    e0, e1 = ev(), ev()
+    log(f"decode: {warmup} warmup + {steps} timed tokens (graph replay)")
+    e0, e1 = _ev(), _ev()
     t0 = time.perf_counter()
     e0.record()
-    for i in range(args.steps):
+    for i in range(steps):
         tg_graphs[pad_kv_len(pos + 1, max_ctx)].replay()
         pos += 1
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_step = e0.elapsed_time(e1) / args.steps
+    ms_step = e0.elapsed_time(e1) / steps
     tg_tok_s = 1000.0 / ms_step
     logits = dec._buffers(1)["logits"]
     if int(dec.pos[0]) != pos or not bool(torch.isfinite(logits).all()):
         raise RuntimeError("decode produced a wrong position or non-finite logits")
-    tokens.append(int(next1[0]))
-    kv_bytes_last = 2 * cfg.n_layer * cfg.kv_dim * 2 * pos  # valid K+V rows read by the last token
+    # valid K+V rows read by the tokens, on average over the timed ones
+    kv_bytes = 2 * cfg.n_layer * cfg.kv_dim * 2 * (pos - steps / 2)
     log(f"tg {tg_tok_s:.1f} tok/s ({ms_step:.3f} ms/token)")
+    out = {
+        "model": f"{cfg.name}, {'Q4_0' if cfg.qtype == 2 else 'Q8_0'}, batch 1",
+        "pp512_tok_s": round(pp512_tok_s, 1),
+        f"pp{prompt_len}_tok_s": round(ppN_tok_s, 1),
+        "tg_tok_s": round(tg_tok_s, 2),
+        "tg_steps": steps,
+        "ms_per_token": round(ms_step, 5),
+        "decode_context": [prompt_len + warmup + 1, pos],
+        "decode_weight_GBps": round(w.decode_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "decode_weight_plus_kv_GBps": round((w.decode_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9, 1),
+        "wall_s_timed": round(wall, 3),
+    }
+    del pp_graphs, tg_graphs
+    dec.graphs.clear()
+    return out, dec
 
-    # ---- roofline: the 129 decode GEMVs of one token, one graph, HIP events
-    mats, outs = decode_gemvs(w, cfg, dev, gen)
-    ws = ops.Workspace(dev)
-    ws.get(1 << 20)
 
-    def gemv_token():
-        for (m, x), o in zip(mats, outs):
-            ops.mul_mat(m, x, out=o, ws=ws)
+def step_gemv_launches(dec):
+    """The fused GEMV launches of one decode step of `dec` (model.forward's fused path
+    at s = 1, on the s = 1 bucket's buffers, KV cache and weights), without the other
+    kernels of the step; returns (issue(), algorithmic bytes of each launch)."""
+    from ggmlc_amd import ops
 
-    gemv_token()
-    torch.cuda.synchronize()
-    gg = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gg):
-        gemv_token()
-    for _ in range(3):
-        gg.replay()
-    torch.cuda.synchronize()
-    R = 20
-    e0.record()
-    for _ in range(R):
-        gg.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    gemv_ms_token = e0.elapsed_time(e1) / R
-    gemv_bytes_token = sum(m.nbytes + m.K * 4 + m.N * 4 for m, _ in mats)
-    n_gemv = len(mats)
-    gemv_gbs = gemv_bytes_token / (gemv_ms_token * 1e-3) / 1e9
-    del gg
-    # the same launches as plain streaming reads of the same weight buffers: the
-    # ceiling a kernel that only reads its weights reaches at these per-launch sizes
-    probe_ms_token = time_probe_launches([m.data for m, _ in mats], e0, e1)
+    w, c, b = dec.w, dec.cfg, dec._buffers(1)
+    qd, kvd = c.q_dim, c.kv_dim
+    f32 = 4
 
-    # ---- prefill GEMM rate: the 128 GEMMs of one ubatch (M = 512)
+    def rope_kv(li):
+        return ops.RopeKv(c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base,
+                          b["kv_idx"], b["q"], dec.k_cache[li], dec.v_cache[li], cache=b["rope_cs"])
+
+    def bias(t):
+        return 0 if t is None else t.numel() * f32
+
+    nbytes = []
+    for li, L in enumerate(w.layers):
+        x_io = c.n_embd * f32 * (3 if li else 1)  # x (+ the pending residual, + the new x)
+        nbytes.append(L.qkv.nbytes + x_io + bias(L.qkv_b) + qd * f32 + 2 * kvd * 2)
+        nbytes.append(L.o.nbytes + qd * f32 + c.n_embd * f32 + bias(L.o_b))
+        nbytes.append(L.gate_up.nbytes + 3 * c.n_embd * f32 + c.n_ff * f32 + bias(L.gate_up_b))
+        nbytes.append(L.down.nbytes + c.n_ff * f32 + c.n_embd * f32 + bias(L.down_b))
+    nbytes.append(w.lm_head.nbytes + 2 * c.n_embd * f32 + c.n_vocab * f32)
+
+    def issue():
+        x = b["x"]
+        other = {id(b["x"]): b["x_alt"], id(b["x_alt"]): b["x"]}
+        pending = None
+        for li, L in enumerate(w.layers):
+            nx = other[id(x)] if pending is not None else None
+            ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=rope_kv(li),
+                              bias=L.qkv_b)
+            x = nx if nx is not None else x
+            o = ops.mul_mat_fused(L.o, b["attn"].view(1, qd), out=b["proj"], bias=L.o_b)
+            nx = other[id(x)]
+            a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx,
+                                  bias=L.gate_up_b)
+            x = nx
+            pending = ops.mul_mat_fused(L.down, a, out=b["proj"], bias=L.down_b)
+        ops.mul_mat_fused(w.lm_head, x, out=b["logits"], rms_eps=c.rms_eps, x_add=pending)
+
+    return issue, nbytes
+
+
+def step_weight_buffers(w) -> list:
+    """The weight buffers of one decode step, in launch order."""
+    bufs = []
+    for L in w.layers:
+        bufs += [L.qkv.data, L.o.data, L.gate_up.data, L.down.data]
+    bufs.append(w.lm_head.data)
+    return bufs
+
+
+def prefill_gemms(w, dev, ws):
+    """The 128 GEMMs of one 512-token ubatch (fp32 N(0,1) activations); returns
+    (issue(), flops)."""
+    import torch
+
+    from ggmlc_amd import ops
+
+    cfg = w.cfg
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
     xs = {k: torch.randn((UBATCH, k), generator=gen, device=dev) for k in (cfg.n_embd, cfg.q_dim, cfg.n_ff)}
     gmats = []
     for L in w.layers:
@@ -233,73 +456,127 @@ def main() -> int:
     gout = {n: torch.empty((UBATCH, n), device=dev) for n in {m.N for m, _ in gmats}}
     ws.get(max(ops.mul_mat_workspace_size(m, UBATCH) for m, _ in gmats))
 
-    def gemm_ubatch():
+    def issue():
         for m, x in gmats:
             ops.mul_mat(m, x, out=gout[m.N], ws=ws)
 
-    gemm_ubatch()
-    torch.cuda.synchronize()
-    gm = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gm):
-        gemm_ubatch()
-    gm.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(3):
-        gm.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    gemm_ms = e0.elapsed_time(e1) / 3
-    gemm_flops = sum(2.0 * UBATCH * m.N * m.K for m, _ in gmats)
-    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
-    del gm, gout, xs
+    return issue, sum(2.0 * UBATCH * m.N * m.K for m, _ in gmats)
 
-    # ---- Linear 4096 -> 4096, Q8_0, M = 1 (17.8 MB per launch)
-    gc1 = torch.Generator(device=dev)
-    gc1.manual_seed(7)
+
+def bench_c1(dev, ws, launches: int) -> dict:
+    """Linear 4096 -> 4096, Q8_0, M = 1 (17.8 MB per launch), 16 rotating
+    weight copies (285 MB > the 256 MB Infinity Cache)."""
+    import torch
+
+    from ggmlc_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
     c1 = []
-    for _ in range(16):  # 16 x 17.8 MB = 285 MB > Infinity Cache
-        t = torch.randn((4096, 4096), generator=gc1, device=dev) * 0.02
+    for _ in range(16):
+        t = torch.randn((4096, 4096), generator=g, device=dev) * 0.02
         c1.append(ops.quantize_weights(t, ops.Q8_0))
         del t
-    x1 = torch.randn((1, 4096), generator=gc1, device=dev)
+    x1 = torch.randn((1, 4096), generator=g, device=dev)
     out1 = torch.empty((1, 4096), device=dev)
-    Lc = args.c1_launches
 
-    def c1_loop():
-        for i in range(Lc):
+    def loop():
+        for i in range(launches):
             ops.mul_mat(c1[i % 16], x1, out=out1, ws=ws)
 
-    c1_loop()
-    torch.cuda.synchronize()
-    gq = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gq):
-        c1_loop()
-    gq.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(3):
-        gq.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    c1_ms = e0.elapsed_time(e1) / (3 * Lc)
-    c1_bytes = c1[0].nbytes + 4096 * 4 + 4096 * 4
-    c1_gbs = c1_bytes / (c1_ms * 1e-3) / 1e9
-    c1_probe_ms = time_probe_launches([c1[i % 16].data for i in range(Lc)], e0, e1) / Lc
-    del gq, c1
-    sweep = [] if args.no_sweep else gemv_sweep_q8_0(dev, ws, e0, e1)
+    ms = time_graph(loop, 3) / launches
+    nbytes = c1[0].nbytes + 4096 * 4 + 4096 * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    probe_ms = time_probe_launches([c1[i % 16].data for i in range(launches)]) / launches
+    log(f"configs[0] Q8_0 GEMV: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    return {
+        "kernel": "k_gemv_grp<Q8_0, M=1> (configs[0] Linear 4096->4096)",
+        "achieved_GBps": round(gbs, 1),
+        "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "us_per_launch": round(ms * 1e3, 3),
+        "bytes_per_launch": nbytes,
+        "read_probe_same_size_us": round(probe_ms * 1e3, 3),
+        "frac_of_same_size_read": round(probe_ms / ms, 4),
+    }
 
-    # ---- measured ceilings next to the datasheet peak: the streaming-read probe
-    # (the GEMV's 16-byte nontemporal load pattern) and a device copy
+
+def bench_c2(dev, ws, Ms=(1, 8, 128, 512), copies: int = 4, blocks: int = 16) -> dict:
+    """the SwiGLU MLP block (gate/up 4096 -> 11008 as one fused 4096 ->
+    22016 MUL_MAT, SWIGLU, down 11008 -> 4096), Q4_0, at M tokens; `copies` weight sets
+    rotate so every block streams its weights from HBM. Up to 4 rows: gate_up GEMV with
+    SWIGLU in its epilogue, then the down GEMV; more rows: the gate_up GEMM, then the
+    down GEMM with SWIGLU in its activation prologue."""
+    import torch
+
+    from ggmlc_amd import ops
+
+    H, F = 4096, 11008
+    g = torch.Generator(device=dev)
+    g.manual_seed(1101)
+    sets = []
+    for _ in range(copies):
+        t = torch.randn((2 * F, H), generator=g, device=dev) * 0.02
+        gu = ops.quantize_weights(t, ops.Q4_0)
+        t = torch.randn((H, F), generator=g, device=dev) * 0.02
+        dn = ops.quantize_weights(t, ops.Q4_0)
+        del t
+        sets.append((gu, dn))
+    wbytes = sets[0][0].nbytes + sets[0][1].nbytes
+    out = {"shape": "gate/up 4096->11008 (fused 4096->22016), SWIGLU, down 11008->4096, Q4_0",
+           "weight_bytes": wbytes, "weight_copies": copies, "M": {}}
+    for M in Ms:
+        x = torch.randn((M, H), generator=g, device=dev)
+        act = torch.empty((M, F), device=dev)
+        gu_out = torch.empty((M, 2 * F), device=dev)
+        y = torch.empty((M, H), device=dev)
+        ws.get(max(ops.mul_mat_workspace_size(m, M) for s in sets for m in s))
+
+        def block(gu, dn):
+            if M <= 4:
+                a = ops.mul_mat_fused(gu, x, out=act, swiglu=True)
+                ops.mul_mat(dn, a, out=y, ws=ws)
+            else:
+                ops.mul_mat(gu, x, out=gu_out, ws=ws)
+                ops.mul_mat_fused(dn, gu_out, out=y, x_swiglu=True, ws=ws)
+
+        def loop():
+            for i in range(blocks):
+                block(*sets[i % copies])
+
+        ms = time_graph(loop, 5 if M <= 128 else 3) / blocks
+        flops = 2.0 * M * (2 * F * H + H * F)
+        nbytes = wbytes + 4 * M * (H + F + H)
+        row = {"path": "GEMV" if M <= 4 else "GEMM", "us_per_block": round(ms * 1e3, 3),
+               "tok_s": round(M * 1000.0 / ms, 1), "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+               "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
+               "frac_of_f16_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / FP16_MFMA_PEAK_TFLOPS, 4)}
+        out["M"][str(M)] = row
+        log(f"  M={M}: {ms * 1e3:.1f} us/block, {row['achieved_GBps']} GB/s, {row['achieved_TFLOPs']} TFLOP/s")
+        del x, act, gu_out, y
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
+def measured_ceilings(dev) -> tuple[float, float]:
+    """Streaming-read probe (the GEMV's 16-byte nontemporal load pattern) and device
+    copy GB/s over 1 GiB: measured ceilings next to the datasheet peak."""
+    import torch
+
+    from ggmlc_amd import _lib
+
     big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     Lib = _lib.load()
+    stream = torch.cuda.current_stream()
 
     def probe():
         _lib.check(Lib.gq_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(), stream.cuda_stream))
 
     probe(), probe()
     torch.cuda.synchronize()
+    e0, e1 = _ev(), _ev()
     e0.record()
     for _ in range(10):
         probe()
@@ -316,84 +593,8 @@ def main() -> int:
     torch.cuda.synchronize()
     copy_gbs = 2 * big.numel() * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
     del big, big2
-
-    decode_bytes = w.decode_bytes
-    result = {
-        "metric": METRIC,
-        "value": round(tg_tok_s, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4_0 weights x q8_0 activations, int8 dot, f32 accum (prefill: f16 MFMA); f16 KV",
-        "data": "synthetic (random-init weights N(0,0.02) -> Q4_0; uniform-random prompt ids)",
-        "config": {
-            "workload": f"configs[3] {cfg.name} decoder, Q4_0, batch 1: pp{args.prompt} (ubatch 512) then "
-                        f"greedy decode; value = tg{args.steps} tokens/s",
-            "global_batch": 1,
-            "seq_len": args.prompt,
-            "parallelism": "single GPU",
-            "weight_bytes": w.nbytes,
-        },
-        "tg_tok_s": round(tg_tok_s, 2),
-        "pp512_tok_s": round(pp512_tok_s, 1),
-        f"pp{args.prompt}_tok_s": round(ppN_tok_s, 1),
-        "decode_weight_GBps": round(decode_bytes / (ms_step * 1e-3) / 1e9, 1),
-        "decode_weight_plus_kv_GBps": round((decode_bytes + kv_bytes_last) / (ms_step * 1e-3) / 1e9, 1),
-        "roofline": {
-            "kernel": "k_gemv_grp<Q4_0, M=1>: the 129 decode GEMVs of one token (qkv, o, gate_up, down x 32, lm_head)",
-            "bound": "hbm",
-            "achieved": round(gemv_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-            "traffic": load_traffic("k_gemv_grp<Q4_0, M=1> decode mix"),
-            "bytes_per_launch": round(gemv_bytes_token / n_gemv),
-            "us_per_launch": round(gemv_ms_token * 1e3 / n_gemv, 3),
-            "launches_per_token": n_gemv,
-            "gemv_ms_per_token": round(gemv_ms_token, 4),
-            "read_probe_same_launches_ms": round(probe_ms_token, 4),
-            "frac_of_same_size_read": round(probe_ms_token / gemv_ms_token, 4),
-        },
-        "roofline_prefill_gemm": {
-            "kernel": "k_gemm<Q4_0>: the 128 GEMMs of one 512-token ubatch (activation quantize excluded)",
-            "bound": "mfma",
-            "achieved": round(gemm_tflops, 1),
-            "peak": FP16_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(gemm_tflops / FP16_MFMA_PEAK_TFLOPS, 4),
-            "ms_per_ubatch": round(gemm_ms, 3),
-        },
-        "gemv_c1_q8_0": {
-            "kernel": "k_gemv_grp<Q8_0, M=1> (configs[0] Linear 4096->4096)",
-            "achieved_GBps": round(c1_gbs, 1),
-            "frac_of_peak": round(c1_gbs / HBM_PEAK_GBS, 4),
-            "us_per_launch": round(c1_ms * 1e3, 3),
-            "bytes_per_launch": c1_bytes,
-            "read_probe_same_size_us": round(c1_probe_ms * 1e3, 3),
-            "frac_of_same_size_read": round(c1_probe_ms / c1_ms, 4),
-        },
-        "gemv_sweep_q8_0": sweep,
-        "measured_read_GBps": round(read_gbs, 1),
-        "measured_copy_GBps": round(copy_gbs, 1),
-        "wall_s_timed": round(wall, 3),
-    }
-    log(f"gemv {gemv_gbs:.0f} GB/s, gemm {gemm_tflops:.0f} TFLOP/s, c1 {c1_gbs:.0f} GB/s, read {read_gbs:.0f} GB/s")
-
-    if not args.no_c5:
-        del dec, pp_graphs, tg_graphs
-        torch.cuda.empty_cache()
-        log("configs[4]: batched paged decode")
-        result["c5_batched_decode"] = bench_c5(dev, args.c5_steps, batches)
-    if not args.no_cpu:
-        log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds)
-    print(json.dumps(result), flush=True)
-    return 0
+    torch.cuda.empty_cache()
+    return read_gbs, copy_gbs
 
 
 def bench_c5(dev, steps: int, batches=(1, 2, 4, 8, 16)) -> dict:
@@ -437,7 +638,7 @@ def bench_c5(dev, steps: int, batches=(1, 2, 4, 8, 16)) -> dict:
     out = {"model": f"{cfg.name} Q8_0, tied embeddings", "weight_bytes": w.decode_bytes,
            "contexts": [int(c) for c in ctx], "shared_prefix": PREFIX, "page_tokens": P,
            "prefill_tokens_computed": n_prefill, "prefill_s": round(prefill_s, 3), "steps": steps, "B": {}}
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0, e1 = _ev(), _ev()
     for B in batches:
         b = bd._buffers(B)
 
@@ -470,16 +671,18 @@ def bench_c5(dev, steps: int, batches=(1, 2, 4, 8, 16)) -> dict:
 
 
 # (N, K) of the Q8_0 decode GEMV sweep: configs[0], the LLaMA-7B layer and lm_head
-# shapes, and the Qwen2.5-1.5B tied lm_head (248 MB, the largest single weight here)
-SWEEP_SHAPES = ((4096, 4096), (4096, 11008), (12288, 4096), (22016, 4096), (32000, 4096), (151936, 1536))
+# shapes, the SmolLM2-360M K = 960 projections and tied head, and the Qwen2.5-1.5B tied
+# lm_head (248 MB, the largest single weight here)
+SWEEP_SHAPES = ((4096, 4096), (4096, 11008), (12288, 4096), (22016, 4096), (32000, 4096),
+                (1600, 960), (5120, 960), (960, 2560), (49152, 960), (151936, 1536))
 
 
-def gemv_sweep_q8_0(dev, ws, e0, e1, launches: int = 96, reps: int = 3) -> list:
+def gemv_sweep_q8_0(dev, ws, min_launches: int = 96, reps: int = 3) -> list:
     """Q8_0 GEMV (M = 1) over SWEEP_SHAPES: achieved GB/s (weight + x + y bytes per
     launch) as a fraction of the HBM peak and of a streaming read of the same buffers.
-    Each shape rotates over enough weight copies (>= 512 MB together) that no launch
-    finds its weight in the 256 MB Infinity Cache; launches run back to back in one
-    graph, as the decode GEMVs of a token do."""
+    Each shape rotates over enough weight copies (>= 512 MB together, each read once per
+    replay) that no launch finds its weight in the 256 MB Infinity Cache; launches run
+    back to back in one graph, as the decode GEMVs of a token do."""
     import torch
 
     from ggmlc_amd import ops
@@ -489,7 +692,8 @@ def gemv_sweep_q8_0(dev, ws, e0, e1, launches: int = 96, reps: int = 3) -> list:
     rows = []
     for N, K in SWEEP_SHAPES:
         wbytes = N * (K // 32) * ops.BLOCK_BYTES[ops.Q8_0]
-        ncopy = max(2, min(16, -(-(512 << 20) // wbytes)))
+        ncopy = max(2, min(400, -(-(512 << 20) // wbytes)))
+        launches = max(min_launches, ncopy)
         ws_ = []
         for _ in range(ncopy):
             t = torch.randn((N, K), generator=g, device=dev) * 0.02
@@ -502,22 +706,10 @@ def gemv_sweep_q8_0(dev, ws, e0, e1, launches: int = 96, reps: int = 3) -> list:
             for i in range(launches):
                 ops.mul_mat(ws_[i % ncopy], x, out=y, ws=ws)
 
-        loop()
-        torch.cuda.synchronize()
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            loop()
-        gr.replay()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
-            gr.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / (reps * launches)
+        ms = time_graph(loop, reps) / launches
         nbytes = wbytes + 4 * K + 4 * N
         gbs = nbytes / (ms * 1e-3) / 1e9
-        probe_ms = time_probe_launches([ws_[i % ncopy].data for i in range(launches)], e0, e1) / launches
+        probe_ms = time_probe_launches([ws_[i % ncopy].data for i in range(launches)]) / launches
         rows.append({
             "N": N, "K": K, "bytes_per_launch": nbytes, "weight_copies": ncopy,
             "us_per_launch": round(ms * 1e3, 3), "achieved_GBps": round(gbs, 1),
@@ -525,11 +717,11 @@ def gemv_sweep_q8_0(dev, ws, e0, e1, launches: int = 96, reps: int = 3) -> list:
             "frac_of_same_size_read": round(probe_ms / ms, 4),
         })
         log(f"sweep q8_0 N={N} K={K}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
-        del gr, ws_
+        del ws_
     return rows
 
 
-def time_probe_launches(bufs, e0, e1, reps: int = 5) -> float:
+def time_probe_launches(bufs, reps: int = 5) -> float:
     """ms for one pass of streaming-read probes, one launch per buffer (each read once,
     whole), captured in a graph and timed like the GEMV graphs."""
     import torch
@@ -544,56 +736,46 @@ def time_probe_launches(bufs, e0, e1, reps: int = 5) -> float:
         for b in bufs:
             _lib.check(Lib.gq_probe_stream_read(b.data_ptr(), b.numel() // 16 * 16, sink.data_ptr(), st))
 
-    run()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        run()
-    g.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(reps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    return time_graph(run, reps)
 
 
-def decode_gemvs(w, cfg, dev, gen):
-    """The 129 decode GEMVs of one token (qkv, o, gate_up, down per layer; lm_head)
-    with activations of the right widths."""
+def traffic_probe(w, dev) -> int:
+    """Eager launches for the PMC runs (per-dispatch counters do not survive graph
+    replay under the profiler): 3 x one decode step's fused GEMVs, then 3 x a 256 MiB
+    device copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters (256 MiB each way)."""
     import torch
 
-    x_h = torch.randn((1, cfg.n_embd), generator=gen, device=dev)
-    x_f = torch.randn((1, cfg.n_ff), generator=gen, device=dev)
-    mats = []
-    for L in w.layers:
-        mats += [(L.qkv, x_h), (L.o, x_h), (L.gate_up, x_h), (L.down, x_f)]
-    mats.append((w.lm_head, x_h))
-    outs = [torch.empty((1, m.N), device=dev) for m, _ in mats]
-    return mats, outs
+    from ggmlc_amd.model import Decoder
+
+    dec = Decoder(w, 256, dev)
+    b = dec._buffers(1)
+    b["x"].normal_(), b["x_alt"].normal_(), b["attn"].normal_()
+    b["pos_ids"].fill_(100), b["kv_idx"].fill_(100)
+    issue, nbytes = step_gemv_launches(dec)
+    for _ in range(3):
+        issue()
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    c = torch.empty_like(a)
+    for _ in range(3):
+        c.copy_(a)
+    torch.cuda.synchronize()
+    log(f"traffic probe: {3 * len(nbytes)} fused GEMV launches ({sum(nbytes) / len(nbytes):.0f} algorithmic "
+        f"bytes per launch), 3 copies of {a.numel()} bytes")
+    return 0
 
 
-def traffic_probe(w, cfg, dev) -> int:
-    """Eager launches for the PMC runs (per-dispatch counters do not survive graph
-    replay under the profiler): 3 x the decode GEMV mix, then 3 x a 256 MiB device copy
-    whose FETCH_SIZE / WRITE_SIZE calibrate the counters (256 MiB each way)."""
+def gemm_probe(w, dev) -> int:
+    """Eager launches for the MFMA counter runs: 3 x one ubatch's 128 prefill GEMMs."""
     import torch
 
     from ggmlc_amd import ops
 
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(5)
-    mats, outs = decode_gemvs(w, cfg, dev, gen)
+    ws = ops.Workspace(dev)
+    issue, flops = prefill_gemms(w, dev, ws)
     for _ in range(3):
-        for (m, x), o in zip(mats, outs):
-            ops.mul_mat(m, x, out=o)
-    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-    b = torch.empty_like(a)
-    for _ in range(3):
-        b.copy_(a)
+        issue()
     torch.cuda.synchronize()
-    log(f"traffic probe: {3 * len(mats)} GEMV launches, 3 copies of {a.numel()} bytes")
+    log(f"gemm probe: 3 x 128 GEMMs, {flops / 1e12:.3f} TFLOP per ubatch")
     return 0
 
 
@@ -607,36 +789,70 @@ def load_traffic(kernel: str) -> float | None:
     return None if d is None else float(d["hbm_bytes_per_launch"])
 
 
-def cpu_baseline(w, cfg, seconds: float) -> dict:
+def cpu_identity() -> dict:
+    """Host CPU model and the ISA extensions ggml's x86 kernels use."""
+    model, flags = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni", "avx512_bf16",
+                       "avx_vnni", "amx_int8", "amx_bf16") if f in flags]
+    return {"cpu_model": model, "isa": isa}
+
+
+def cpu_baseline(w, cfg, seconds: float, ctx: int = 1024) -> dict:
     """The reference ggml CPU backend running the same decoder on the same weights:
-    pp512 (one ubatch from position 0), then greedy decode tokens for ~`seconds`."""
+    pp512 (one ubatch from position 0), then greedy decode tokens at the GPU's decode
+    context for ~`seconds` on CPU_SHARE threads, then a few at 1 thread. The cache rows
+    between 512 and `ctx` are not computed on the CPU (it would cost minutes): they hold
+    zeros, and a decode token at position ctx reads them all the same (the work of
+    attention depends on n_kv, not on the values)."""
     import numpy as np
 
     import oracle as O
-    from ggmlc_amd.model import host_weights
+    from ggmlc_amd.model import host_weights, pad_kv_len
 
-    cores = O.n_cpu_threads()
+    cores = min(CPU_SHARE, O.n_cpu_threads())
+    ident = cpu_identity()
     host = host_weights(w)
     prompt = np.random.default_rng(5).integers(0, cfg.n_vocab, UBATCH).astype(np.int32)
     if O.ref_available():
-        rl = O.RefLlama(cfg, host, 1024, n_threads=cores)
+        variant = "v4" if O.ref_v4_usable() else "v3"
+        max_ctx = pad_kv_len(ctx + 64, 1 << 30)
+        rl = O.RefLlama(cfg, host, max_ctx, n_threads=cores, variant=variant)
         t0 = time.perf_counter()
         _, tok = rl.step(prompt)
         pp_s = time.perf_counter() - t0
+        rl.pos = ctx
         rl.step([tok])  # first decode token untimed
         n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds and rl.pos < 1024:
+        while time.perf_counter() - t0 < seconds and rl.pos < ctx + 48:
             _, tok = rl.step([tok])
             n += 1
         dt = (time.perf_counter() - t0) / n
+        rl.n_threads = 1
+        n1, t0 = 0, time.perf_counter()
+        while (n1 < 2 or time.perf_counter() - t0 < seconds / 3) and rl.pos < ctx + 60:
+            _, tok = rl.step([tok])
+            n1 += 1
+        dt1 = (time.perf_counter() - t0) / n1
         del rl
+        isa = "x86-64-v4 + AVX-512 VNNI" if variant == "v4" else "x86-64-v3 (AVX2 + FMA + F16C)"
         return {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": cores, "kind": "reference",
-                "sample": f"ggml CPU backend ({cores} threads) on the same {cfg.name} Q4_0 weights: one 512-token "
-                          f"prefill ubatch, then {n} timed greedy decode tokens at context ~{UBATCH}",
-                "ms_per_step": round(dt * 1e3, 2), "pp512_tok_s": round(UBATCH / pp_s, 2)}
+                "sample": f"ggml CPU backend built from the reference sources for {isa} ({cores} threads) on the "
+                          f"same {cfg.name} Q4_0 weights: one 512-token prefill ubatch, then {n} timed greedy "
+                          f"decode tokens at context {ctx + 1}..{ctx + 1 + n}; then {n1} tokens at 1 thread",
+                "ms_per_step": round(dt * 1e3, 2), "pp512_tok_s": round(UBATCH / pp_s, 2),
+                "one_thread_tok_s": round(1.0 / dt1, 4), "one_thread_ms_per_step": round(dt1 * 1e3, 1),
+                "build": f"oracle/_ref{'/v4' if variant == 'v4' else ''}/libggmlref.so ({isa})", **ident}
     # no reference build: the C restatement's MUL_MATs of one decode token (the bulk of its work)
     x = np.random.default_rng(6).standard_normal((1, cfg.n_ff)).astype(np.float32)
-    mats = [(m, cfg.n_embd if i != 3 else cfg.n_ff) for L in host[2] for i, m in enumerate(L)]
+    mats = [(m, cfg.n_embd if i != 3 else cfg.n_ff) for L in host[2] for i, m in enumerate(L[:4])]
     mats.append((host[1], cfg.n_embd))
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds and n < 20:
@@ -646,7 +862,7 @@ def cpu_baseline(w, cfg, seconds: float) -> dict:
     dt = (time.perf_counter() - t0) / n
     return {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{n} decode tokens' MUL_MATs (the {len(mats)} GEMVs) through the C restatement",
-            "ms_per_step": round(dt * 1e3, 2)}
+            "ms_per_step": round(dt * 1e3, 2), **ident}
 
 
 if __name__ == "__main__":

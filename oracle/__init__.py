@@ -24,6 +24,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 ORACLE_SO = HERE / "liboracle.so"
 REF_SO = HERE / "_ref" / "libggmlref.so"
+REF_V4_SO = HERE / "_ref" / "v4" / "libggmlref.so"
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -81,56 +82,87 @@ def ref_available() -> bool:
     return REF_SO.exists()
 
 
-def ref():
-    """The compiled reference ggml CPU backend (raises if it was not built)."""
+def ref(variant: str = "v3"):
+    """The compiled reference ggml CPU backend (raises if it was not built). variant
+    "v3" is the x86-64-v3 build the tests use; "v4" the AVX-512 + VNNI build of the same
+    sources (oracle/Makefile ref-v4), for timing on hosts that support it."""
     global _ref
+    if variant == "v4":
+        return _load_ref(REF_V4_SO, "v4")
     if _ref is None:
-        if not REF_SO.exists():
-            raise FileNotFoundError(f"{REF_SO} not built (needs /root/reference)")
-        L = ctypes.CDLL(str(REF_SO))
-        L.ref_ggml_version.restype = ctypes.c_char_p
-        for n in ("ref_quantize_row_q8_0", "ref_quantize_row_q8_0_ref"):
-            getattr(L, n).argtypes = [_vp, _vp, _i64]
-            getattr(L, n).restype = None
-        L.ref_mul_mat.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32]
-        L.ref_set_rows_f32_f16.argtypes = [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32]
-        L.ref_flash_attn_ext_f16.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
-                                             _vp, _f32, _vp, _i32]
-        L.ref_soft_max_f32.argtypes = [_vp, _i64, _i64, _vp, _f32, _vp, _i32]
-        L.ref_mm_create.restype = _vp
-        L.ref_mm_create.argtypes = [_i32, _vp, _i64, _i64, _i64]
-        L.ref_mlp_create.restype = _vp
-        L.ref_mlp_create.argtypes = [_i32, _vp, _vp, _i64, _i64, _i64]
-        L.ref_graph_run.argtypes = [_vp, _vp, _vp, _i32]
-        L.ref_graph_free.argtypes = [_vp]
-        L.ref_graph_free.restype = None
-        L.ref_swiglu.argtypes = [_vp, _i64, _i64, _vp]
-        L.ref_rms_norm.argtypes = [_vp, _i64, _i64, _f32, _vp]
-        L.ref_rope.argtypes = [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _f32, _vp]
-        L.ref_get_rows.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp]
-        L.ref_argmax.argtypes = [_vp, _i64, _i64, _vp]
-        L.ref_llama_create.restype = _vp
-        L.ref_llama_create.argtypes = [_vp, _i32, _f32, _f32, _vp, _vp, _vp, _vp]
-        L.ref_llama_step.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32]
-        L.ref_llama_set_bias.argtypes = [_vp, _i64, _i32, _vp, _i64]
-        L.ref_llama_free.argtypes = [_vp]
-        L.ref_llama_free.restype = None
-        L.ref_rt_last_error.restype = ctypes.c_char_p
-        L.ref_rt_load.restype = _vp
-        L.ref_rt_load.argtypes = [ctypes.c_char_p]
-        L.ref_rt_free.argtypes = [_vp]
-        L.ref_rt_free.restype = None
-        L.ref_rt_describe.restype = _i64
-        L.ref_rt_describe.argtypes = [_vp, ctypes.c_char_p, _i64]
-        L.ref_rt_init_kv.argtypes = [_vp, _i64]
-        L.ref_rt_reset_kv.argtypes = [_vp]
-        L.ref_rt_run.argtypes = [_vp, ctypes.POINTER(ctypes.c_char_p), _vp, _i32, _vp, ctypes.POINTER(_vp), _vp,
-                                 _i32, _i32]
-        L.ref_rt_output.restype = _i64
-        L.ref_rt_output.argtypes = [_vp, ctypes.c_uint32, _vp, _vp, _i64]
-        L.ref_init()
-        _ref = L
+        _ref = _load_ref(REF_SO, "v3")
     return _ref
+
+
+_ref_v4 = None
+
+
+def ref_v4_usable() -> bool:
+    """The AVX-512 build exists and this host's CPU has the instructions it uses."""
+    if not REF_V4_SO.exists():
+        return False
+    try:
+        flags = set()
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("flags"):
+                flags = set(line.split(":", 1)[1].split())
+                break
+    except OSError:
+        return False
+    return {"avx512f", "avx512bw", "avx512dq", "avx512vl", "avx512cd", "avx512_vnni"} <= flags
+
+
+def _load_ref(path, variant):
+    global _ref_v4
+    if variant == "v4" and _ref_v4 is not None:
+        return _ref_v4
+    if not path.exists():
+        raise FileNotFoundError(f"{path} not built (needs /root/reference)")
+    L = ctypes.CDLL(str(path))
+    L.ref_ggml_version.restype = ctypes.c_char_p
+    for n in ("ref_quantize_row_q8_0", "ref_quantize_row_q8_0_ref"):
+        getattr(L, n).argtypes = [_vp, _vp, _i64]
+        getattr(L, n).restype = None
+    L.ref_mul_mat.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp, _i32]
+    L.ref_set_rows_f32_f16.argtypes = [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i32]
+    L.ref_flash_attn_ext_f16.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
+                                         _vp, _f32, _vp, _i32]
+    L.ref_soft_max_f32.argtypes = [_vp, _i64, _i64, _vp, _f32, _vp, _i32]
+    L.ref_mm_create.restype = _vp
+    L.ref_mm_create.argtypes = [_i32, _vp, _i64, _i64, _i64]
+    L.ref_mlp_create.restype = _vp
+    L.ref_mlp_create.argtypes = [_i32, _vp, _vp, _i64, _i64, _i64]
+    L.ref_graph_run.argtypes = [_vp, _vp, _vp, _i32]
+    L.ref_graph_free.argtypes = [_vp]
+    L.ref_graph_free.restype = None
+    L.ref_swiglu.argtypes = [_vp, _i64, _i64, _vp]
+    L.ref_rms_norm.argtypes = [_vp, _i64, _i64, _f32, _vp]
+    L.ref_rope.argtypes = [_vp, _i64, _i64, _i64, _vp, _i32, _i32, _f32, _vp]
+    L.ref_get_rows.argtypes = [_i32, _vp, _i64, _i64, _vp, _i64, _vp]
+    L.ref_argmax.argtypes = [_vp, _i64, _i64, _vp]
+    L.ref_llama_create.restype = _vp
+    L.ref_llama_create.argtypes = [_vp, _i32, _f32, _f32, _vp, _vp, _vp, _vp]
+    L.ref_llama_step.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i32]
+    L.ref_llama_set_bias.argtypes = [_vp, _i64, _i32, _vp, _i64]
+    L.ref_llama_free.argtypes = [_vp]
+    L.ref_llama_free.restype = None
+    L.ref_rt_last_error.restype = ctypes.c_char_p
+    L.ref_rt_load.restype = _vp
+    L.ref_rt_load.argtypes = [ctypes.c_char_p]
+    L.ref_rt_free.argtypes = [_vp]
+    L.ref_rt_free.restype = None
+    L.ref_rt_describe.restype = _i64
+    L.ref_rt_describe.argtypes = [_vp, ctypes.c_char_p, _i64]
+    L.ref_rt_init_kv.argtypes = [_vp, _i64]
+    L.ref_rt_reset_kv.argtypes = [_vp]
+    L.ref_rt_run.argtypes = [_vp, ctypes.POINTER(ctypes.c_char_p), _vp, _i32, _vp, ctypes.POINTER(_vp), _vp,
+                             _i32, _i32]
+    L.ref_rt_output.restype = _i64
+    L.ref_rt_output.argtypes = [_vp, ctypes.c_uint32, _vp, _vp, _i64]
+    L.ref_init()
+    if variant == "v4":
+        _ref_v4 = L
+    return L
 
 
 # ----------------------------------------------------------------- numpy API
@@ -375,8 +407,9 @@ class RefLlama:
     of the same projections (None where a projection has none): the MUL_MAT node's
     bias ADD (executor.cpp:2436-2445)."""
 
-    def __init__(self, cfg, weights, max_ctx: int, n_threads: int = 8):
+    def __init__(self, cfg, weights, max_ctx: int, n_threads: int = 8, variant: str = "v3"):
         embed, lm_head, layers = weights
+        self._R = ref(variant)
         self.cfg, self.max_ctx, self.n_threads = cfg, max_ctx, n_threads
         self._w = [_c(embed, np.uint8), _c(lm_head, np.uint8)] + [_c(m, np.uint8) for L in layers for m in L[:4]]
         self.kc = [np.zeros((cfg.n_head_kv, max_ctx, cfg.head_dim), np.uint16) for _ in layers]
@@ -385,7 +418,7 @@ class RefLlama:
                          cfg.n_vocab, max_ctx], np.int64)
         lw = (_vp * (4 * len(layers)))(*[a.ctypes.data for a in self._w[2:]])
         kv = (_vp * (2 * len(layers)))(*[a.ctypes.data for pair in zip(self.kc, self.vc) for a in pair])
-        self.h = ref().ref_llama_create(_ptr(dims), cfg.qtype, cfg.rms_eps, cfg.rope_base, _ptr(self._w[0]),
+        self.h = self._R.ref_llama_create(_ptr(dims), cfg.qtype, cfg.rms_eps, cfg.rope_base, _ptr(self._w[0]),
                                         _ptr(self._w[1]), lw, kv)
         if not self.h:
             raise RuntimeError("ref_llama_create failed")
@@ -396,7 +429,7 @@ class RefLlama:
                     continue
                 b = _c(b, np.float32)
                 self._b.append(b)
-                if ref().ref_llama_set_bias(self.h, li, which, _ptr(b), b.size) != 0:
+                if self._R.ref_llama_set_bias(self.h, li, which, _ptr(b), b.size) != 0:
                     raise RuntimeError("ref_llama_set_bias failed")
         self.pos = 0
 
@@ -408,7 +441,7 @@ class RefLlama:
         mask = causal_mask_f16(self.pos, s, n_kv)
         logits = np.empty(self.cfg.n_vocab, np.float32)
         nxt = np.zeros(1, np.int32)
-        if ref().ref_llama_step(self.h, _ptr(ids), s, self.pos, n_kv, _ptr(mask), _ptr(logits), _ptr(nxt),
+        if self._R.ref_llama_step(self.h, _ptr(ids), s, self.pos, n_kv, _ptr(mask), _ptr(logits), _ptr(nxt),
                                 self.n_threads) != 0:
             raise RuntimeError("ref_llama_step failed")
         self.pos += s
@@ -416,7 +449,7 @@ class RefLlama:
 
     def __del__(self):
         if getattr(self, "h", None):
-            ref().ref_llama_free(self.h)
+            self._R.ref_llama_free(self.h)
             self.h = None
 
 

@@ -304,3 +304,27 @@ def test_native_executor_rejects_bad_files(tmp_path):
     with pytest.raises(_lib.GQError, match="NEOX") as e:
         inspect(w.to_bytes())
     assert e.value.code == -2  # GQ_ERR_UNSUPPORTED
+
+
+@needs_ref
+@pytest.mark.skipif(not O.ref_v4_usable(), reason="AVX-512 reference build absent or host lacks AVX-512 VNNI")
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+def test_reference_avx512_build_agrees_with_v3_build(qtype):
+    """The AVX-512 build of the reference (bench.py's CPU baseline on hosts that have
+    the instructions) computes the decoder of the x86-64-v3 build. The int block sums
+    are exact in both; the fp32 accumulation of ggml's 16-lane AVX-512 paths is ordered
+    differently from its 8-lane AVX2 ones for Q4_0 (Q8_0 gives the same bits), which a
+    random-init model amplifies to a few 1e-5 in the logits' cosine, the order of the
+    reference's own prefill-vs-token-by-token spread at this depth."""
+    c = _tiny(qtype, False)
+    w = _weights(c)
+    toks = np.random.default_rng(8).integers(0, c.n_vocab, 29).astype(np.int32)
+    a, b = O.RefLlama(c, w, 256, n_threads=4), O.RefLlama(c, w, 256, n_threads=4, variant="v4")
+    la, na = a.step(toks)
+    lb, _ = b.step(toks)
+    for _ in range(3):
+        cos = float(la @ lb / np.linalg.norm(la) / np.linalg.norm(lb))
+        assert cos > 0.9999 and np.abs(la - lb).max() <= 3e-2 * np.abs(la).max(), cos
+        t = np.array([na], np.int32)  # both decode the v3 build's token
+        la, na = a.step(t)
+        lb, _ = b.step(t)
