@@ -63,19 +63,32 @@ struct BlockRegs {
     bool even;   // block start is 4-byte aligned
 };
 
-// The block at p, loaded unconditionally (callers pass a valid block address; a
-// step past the matrix loads block 0 and is zeroed where it is used), so the loads of
-// the register ring stay in order for the compiler's memory-counter waits.
+constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any resource: reads 0, no fetch
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+    const uint64_t base = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    const uint32_t n = bytes <= 0 ? 0u : (bytes > 0x7fffffff ? 0x7fffffffu : (uint32_t)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+                                             (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
+}
+
+// The block at byte offset off of a 4-byte aligned resource, or zeros (scale 0) when not
+// `valid`: raw buffer loads, a fixed number per block, so the loads of the register ring
+// stay in order for the compiler's memory-counter waits and nothing has to be zeroed
+// where the block is used (rows past the resource read 0 as well).
 template <int QT>
-__device__ __forceinline__ void load_block_any(const uint8_t* p, BlockRegs<QT>& r) {
+__device__ __forceinline__ void load_block_rs(__amdgpu_buffer_rsrc_t rs, uint32_t off, bool valid,
+                                              BlockRegs<QT>& r) {
     constexpr int NW = QT == GQ_TYPE_Q8_0 ? 8 : 4;
-    constexpr int TAIL = QT == GQ_TYPE_Q8_0 ? 32 : 16;
-    r.even = (reinterpret_cast<uintptr_t>(p) & 3) == 0;
-    const uint32_t* dp = reinterpret_cast<const uint32_t*>(r.even ? p : p + 2);
-    const uint16_t* up = reinterpret_cast<const uint16_t*>(r.even ? p + TAIL : p);
+    constexpr uint32_t TAIL = QT == GQ_TYPE_Q8_0 ? 32 : 16;
+    r.even = (off & 3) == 0;
+    const uint32_t doff = valid ? (r.even ? off : off + 2) : OOB;
+    const uint32_t uoff = valid ? (r.even ? off + TAIL : off) : OOB;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) r.dw[i] = dp[i];
-    r.u = *up;
+    for (int i = 0; i < NW; ++i) r.dw[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(doff + 4 * i), 0, 0);
+    r.u = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)uoff, 0, 0);
 }
 
 // one quant block as its 32 raw quants in fp16 (16 dwords: Q8_0 q, Q4_0 nibble - 8)
@@ -147,28 +160,33 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     const int lhalf = tid & 1;
     const int arow = tid / (8 / AQ);
     const int apiece = (tid % (8 / AQ)) * AQ;
-    const int64_t am = m0 + arow;
-    const int64_t bn = n0 + lrow;
 
-    // register ring: PF K steps in flight; loads from clamped (always valid) addresses,
-    // the validity travels with the slot and zeroes the data when it is parked in LDS
+    // register ring: PF K steps in flight, raw buffer loads over this workgroup's rows of A
+    // and W (rows past M / N, K past the matrix and steps past this split read zeros)
     uint4 rh[PF][AQ], rl[PF][AQ];
     BlockRegs<QT> rb[PF];
-    bool av[PF], bv[PF];
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(A + m0 * lda, min<int64_t>(M - m0, BM) * lda * 2);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W + n0 * row_bytes, min<int64_t>(N - n0, BN) * row_bytes);
+    const uint32_t arow_off = (uint32_t)(arow * lda * 2);
+    const uint32_t wrow_off = (uint32_t)(lrow * row_bytes);
 
     auto load = [&](int kt, int slot) {
         const int64_t k = (int64_t)kt * BK + apiece * 8;
-        av[slot] = am < M && k < K && kt < kt1;
-        const uint16_t* ap = av[slot] ? A + am * lda + k : A;
-        const uint4* aph = reinterpret_cast<const uint4*>(ap);
-        const uint4* apl = reinterpret_cast<const uint4*>(av[slot] ? ap + K : A);
+        const bool av = k < K && kt < kt1;
+        const uint32_t ao = av ? arow_off + (uint32_t)k * 2 : OOB;
+        const uint32_t lo = av ? ao + (uint32_t)K * 2 : OOB;
 #pragma unroll
-        for (int i = 0; i < AQ; ++i) rh[slot][i] = aph[i];
+        for (int i = 0; i < AQ; ++i) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(ao + 16 * i), 0, 0);
+            rh[slot][i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
 #pragma unroll
-        for (int i = 0; i < AQ; ++i) rl[slot][i] = apl[i];
+        for (int i = 0; i < AQ; ++i) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(lo + 16 * i), 0, 0);
+            rl[slot][i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
         const int kb = kt * 2 + lhalf;
-        bv[slot] = bn < N && kb < nb && kt < kt1;
-        load_block_any<QT>(bv[slot] ? W + bn * row_bytes + (int64_t)kb * BB : W, rb[slot]);
+        load_block_rs<QT>(wrs, wrow_off + (uint32_t)kb * BB, kb < nb && kt < kt1, rb[slot]);
     };
 
     float16v acc[MI][2];
@@ -190,18 +208,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
             uint4* sal = reinterpret_cast<uint4*>(sAl + ao);
 #pragma unroll
             for (int i = 0; i < AQ; ++i) {
-                sah[i] = av[slot] ? rh[slot][i] : make_uint4(0, 0, 0, 0);
-                sal[i] = av[slot] ? rl[slot][i] : make_uint4(0, 0, 0, 0);
+                sah[i] = rh[slot][i];
+                sal[i] = rl[slot][i];
             }
             uint32_t e[16];
             float d;
-            expand_block<QT>(rb[slot], e, d);
+            expand_block<QT>(rb[slot], e, d);  // a zero block: scale 0, quants -8 (Q4_0) or 0
             uint4* sb = reinterpret_cast<uint4*>(sB + lrow * LDK + lhalf * 32);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                sb[i] = bv[slot] ? make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3])
-                                 : make_uint4(0, 0, 0, 0);
-            sD[lhalf][lrow] = bv[slot] ? d : 0.0f;
+            for (int i = 0; i < 4; ++i) sb[i] = make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3]);
+            sD[lhalf][lrow] = d;
         }
         __syncthreads();
         if constexpr (decltype(prefetch)::value) load(kt + PF, slot);

@@ -161,7 +161,7 @@ __device__ __forceinline__ void rope_cache_loads(const GemvFuse& fz, RopeIn<M>& 
         0x00020000);
 #pragma unroll
     for (int k = 0; k < RC; ++k) {
-        const int idx = (int)threadIdx.x + k * 256;
+        const int idx = (int)threadIdx.x + k * (int)blockDim.x;  // the entries rope_table stores
         const int m = use ? idx / np : 0, j = idx - m * np;
         const uint32_t off = use && idx < M * np ? (uint32_t)(m * fz.rp.cache_nb1 + j * 8) : 0x80000000u;
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)off, 0, 0);
