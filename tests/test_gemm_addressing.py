@@ -1,0 +1,147 @@
+"""Host model of the prefill GEMM's addressing (csrc/gemm.hip k_gemm): every global load
+offset, LDS address and store index that a launch generates, for the shapes the GPU tests
+and the configs run, checked against the buffer resources, the LDS allocation and the
+output extents on the CPU.
+
+It restates the kernel's index formulas (loader mapping, the PF-deep register ring and its
+K-step sequence, the LDS tile layout, MFMA operand reads, epilogue) and the host plan
+(gemm_plan: tile height and K splits), so a change to either is checked here before it
+reaches a GPU.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+QK = 32
+BN, BK, LDK = 128, 64, 72
+OOB = 0x80000000
+BLOCK = {8: 34, 2: 18}  # Q8_0, Q4_0 block bytes
+
+
+def cdiv(a, b):
+    return -(-a // b)
+
+
+def gemm_plan(N, K, M, ncu=256):
+    """gemm.hip gemm_bm + gemm_plan"""
+    if M > 64 and cdiv(N, BN) >= 16:
+        bm = 128
+    else:
+        bm = 64 if cdiv(N, BN) * cdiv(M, 128) < ncu else 128
+    tiles, nk = cdiv(N, BN) * cdiv(M, bm), cdiv(K, BK)
+    ks = 1
+    if tiles < ncu:
+        ks = min(cdiv(2 * ncu, tiles), nk // 4, 16)
+    ks = max(ks, 1)
+    spk = cdiv(nk, ks)
+    return bm, cdiv(nk, spk), spk
+
+
+PF = {128: 1, 64: 2}  # gemm.hip GEMM_PF_128, GEMM_PF_64: K steps of loads in flight
+
+
+def lds_bytes(bm):
+    """sAh, sAl (BM x LDK halves), sB (BN x LDK halves), sD[2][BN] floats"""
+    return (2 * bm * LDK + BN * LDK) * 2 + 2 * BN * 4
+
+
+def check_launch(qt, N, K, M):
+    bm, ks, spk = gemm_plan(N, K, M)
+    bb = BLOCK[qt]
+    row_bytes = (K // QK) * bb
+    lda = 2 * K
+    nb = K // QK
+    aq = bm // 32
+    mi = bm // 64
+    sb = lds_bytes(bm)
+    assert sb <= 64 * 1024  # static LDS of one workgroup
+    tid = np.arange(256)
+    lane, wave = tid & 63, tid >> 6
+    wm, wn = wave >> 1, wave & 1
+    lrow, lhalf = tid >> 1, tid & 1
+    arow = tid // (8 // aq)
+    apiece = (tid % (8 // aq)) * aq
+    assert arow.max() < bm and (apiece + aq - 1).max() < 8
+    a_bytes = M * lda * 2  # the activation workspace: M rows of lda halves
+    # every offset grows with the tile index, so the first and last tiles of each grid
+    # dimension bound the rest (every K step of every split is checked for them)
+    for bx in sorted({0, cdiv(N, BN) - 1}):
+        n0 = bx * BN
+        w_base = n0 * row_bytes
+        w_rec = min(N - n0, BN) * row_bytes
+        assert w_base + w_rec <= N * row_bytes  # the weight resource stays inside W
+        for by in sorted({0, cdiv(M, bm) - 1}):
+            m0 = by * bm
+            a_base = m0 * lda * 2
+            a_rec = min(M - m0, bm) * lda * 2
+            assert a_base + a_rec <= a_bytes and a_rec < 2**31 and w_rec < 2**31
+            arow_off = arow * lda * 2
+            wrow_off = lrow * row_bytes
+            for bz in range(ks):
+                kt0 = bz * spk
+                kt1 = min(cdiv(K, BK), kt0 + spk)
+                assert kt0 < kt1  # no empty split
+                # every step the ring loads: kt0 .. kt1 + PF - 1 (prologue and refills)
+                for kt in range(kt0, kt1 + PF[bm]):
+                    k = kt * BK + apiece * 8
+                    av = (k < K) & (kt < kt1)
+                    ao = np.where(av, arow_off + k * 2, OOB)
+                    lo = np.where(av, ao + K * 2, OOB)
+                    for i in range(aq):
+                        for off in (ao + 16 * i, lo + 16 * i):
+                            ok = off >= OOB
+                            inb = off + 16 <= a_rec
+                            assert np.all(ok | inb | (arow + m0 >= M)), (qt, N, K, M, kt)
+                            # an in-range read stays inside its own row's hi / lo halves
+                            rowok = (off - arow_off) + 16 <= lda * 2
+                            assert np.all(ok | rowok)
+                    kb = kt * 2 + lhalf
+                    valid = (kb < nb) & (kt < kt1)
+                    off = wrow_off + kb * bb
+                    even = (off & 3) == 0
+                    doff = np.where(valid, np.where(even, off, off + 2), OOB)
+                    uoff = np.where(valid, np.where(even, off + (32 if qt == 8 else 16), off), OOB)
+                    nw = 8 if qt == 8 else 4
+                    for o, width in [(doff + 4 * (nw - 1), 4), (uoff, 2)]:
+                        ok = o >= OOB
+                        assert np.all(ok | (o + width <= w_rec) | (lrow + n0 >= N))
+                        # the block read stays inside its row
+                        assert np.all(ok | (o + width - wrow_off <= row_bytes))
+                    assert np.all(~valid | (doff % 4 == 0))
+    # LDS: tile writes and MFMA operand reads (halves within a tile, then bytes)
+    for i in range(aq):
+        ah = (arow * LDK + apiece * 8 + 8 * i) * 2
+        assert (ah + 16).max() <= bm * LDK * 2
+    sbw = (lrow * LDK + lhalf * 32 + 8 * 3) * 2 + 16
+    assert sbw.max() <= BN * LDK * 2
+    sd = (lhalf * BN + lrow) * 4 + 4
+    assert sd.max() <= 2 * BN * 4
+    for kb in range(2):
+        for h in range(2):
+            kk = kb * 32 + h * 16 + 8 * (lane >> 5)
+            for i in range(mi):
+                ro = (wm * (bm // 2) + i * 32 + (lane & 31)) * LDK + kk
+                assert (ro + 8).max() * 2 <= bm * LDK * 2
+            for j in range(2):
+                rb = (wn * 64 + j * 32 + (lane & 31)) * LDK + kk
+                assert (rb + 8).max() * 2 <= BN * LDK * 2
+        dwi = kb * BN + wn * 64 + 32 + (lane & 31)
+        assert dwi.max() < 2 * BN
+    # epilogue rows / columns are guarded by m < M, n < N; partial tiles by z < ks
+    return bm, ks
+
+
+SHAPES = [
+    (2, 64, 1024, 5),      # the shape a pipelined variant once faulted on
+    (2, 12288, 4096, 512), (2, 4096, 4096, 512), (2, 22016, 4096, 512), (2, 4096, 11008, 512),
+    (2, 32000, 4096, 37), (8, 1600, 960, 512), (8, 5120, 960, 512), (8, 960, 2560, 512),
+    (8, 2048, 1536, 16), (8, 17920, 1536, 8), (8, 1536, 8960, 16), (8, 151936, 1536, 7),
+    (2, 4096, 4096, 5), (2, 4096, 4096, 129), (8, 256, 512, 70), (2, 96, 64, 3),
+]
+
+
+@pytest.mark.parametrize("qt,N,K,M", SHAPES)
+def test_gemm_addresses_in_bounds(qt, N, K, M):
+    check_launch(qt, N, K, M)
