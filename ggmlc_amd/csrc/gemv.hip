@@ -25,6 +25,7 @@
 // Fallback (any K % 32 == 0): one lane per block with 16-bit loads, activation
 // quantized into LDS the same way.
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 #include "common.h"
@@ -268,7 +269,7 @@ __device__ __forceinline__ void emit(const GemvFuse& fz, const float2* rtab, flo
     dst[(int64_t)m * ldd + row] = v;
 }
 
-template <int QT, int M, bool XVEC, int PF, int KS, int XPT>
+template <int QT, int M, bool XVEC, int PF, int KS, int XPT, int PRE>
 __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__ W, int64_t N,
                                                      int64_t row_bytes, int G, ActSrc act, float* dst,
                                                      int64_t ldd, GemvFuse fz) {
@@ -359,7 +360,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
     uint4 pre[PF][CPG];
     // load cursor: tile k, step j (wave-uniform)
     int lk = 0, lj = 0;
-    auto issue = [&](uint4(&buf)[CPG]) {
+    // chunks [LO, HI) of the step at the load cursor; the cursor moves on when ADV (a step may
+    // be issued in two parts, both for the same cursor position)
+    auto issue_rng = [&](uint4(&buf)[CPG], auto lo_c, auto hi_c, bool adv) {
+        constexpr int LO = decltype(lo_c)::value, HI = decltype(hi_c)::value;
         const int64_t row0 = ((int64_t)blockIdx.x + (int64_t)lk * gridDim.x) * ROWS + rg * RPW;
         const int64_t prow = phys_row(fz, row0);
         const int gfirst = g_begin + lj * LPR;
@@ -376,6 +380,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         const bool tail = lj == S - 1 && ngr_tail < LPR;
 #pragma unroll
         for (int c = 0; c < CPG; ++c) {
+            if (c < LO || c >= HI) continue;  // resolved at compile time
             uint32_t vo = voff[c];
             if (tail) {  // chunks of groups past the K range
                 const int ci = lane + 64 * c, within = ci - (ci / SEG) * SEG;
@@ -384,12 +389,17 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vo, 0, 2 /* nt */);
             buf[c] = make_uint4(v.x, v.y, v.z, v.w);
         }
-        if (++lj == S) lj = 0, ++lk;
+        if (adv && ++lj == S) lj = 0, ++lk;
     };
-    // the first step's loads go out before the activation prologue, the rest after it:
-    // a wave stalls at issue while the memory pipeline is full, and the prologue would
-    // wait behind loads it does not need (measured: 5-13% faster launches)
-    issue(pre[0]);
+    using C0 = std::integral_constant<int, 0>;
+    using CP = std::integral_constant<int, CPG>;
+    auto issue = [&](uint4(&buf)[CPG]) { issue_rng(buf, C0{}, CP{}, true); };
+    // the first step's loads (its first PRE chunks when PRE < CPG) go out before the
+    // activation prologue, the rest after it: a CU serves its waves' memory requests in
+    // order, so an activation load issued behind many weight loads holds the prologue
+    // (measured: 5-13% faster launches; the partial first step for grids of a tile or more
+    // per resident workgroup: 7B qkv, gate_up and lm_head 4-12% faster)
+    issue_rng(pre[0], C0{}, std::integral_constant<int, PRE>{}, false);
     __builtin_amdgcn_sched_barrier(0);
     if (fz.rope) rope_table<M>(fz, rin, rtab);  // while the loads are in flight
 
@@ -450,6 +460,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_grp(const uint8_t* __restrict__
         quantize_rows_to_act<XVEC, M>(act, blockIdx.x == 0, M, G * 256, s_act, act_bytes, scale);
     }
     __syncthreads();  // quantized activation (and rope table) visible to all waves
+    issue_rng(pre[0], std::integral_constant<int, PRE>{}, CP{}, true);  // nothing when PRE == CPG
 #pragma unroll
     for (int s = 1; s < PF; ++s) issue(pre[s]);
 
@@ -656,12 +667,12 @@ int resident_wgs(KFn* fn, size_t lds, int& out) {
     return GQ_OK;
 }
 
-template <int QT, int M, bool XVEC, int PF, int KS, int XPT>
+template <int QT, int M, bool XVEC, int PF, int KS, int XPT, int PRE = QTraits<QT>::CPG>
 int launch_grp_ks(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
                   float* dst, int64_t ldd, const GemvFuse& fz, hipStream_t s, size_t lds, int resident) {
     const int G = (int)(K / 256);
     const int64_t row_bytes = (K / QK) * QTraits<QT>::BB;
-    auto* fn = &k_gemv_grp<QT, M, XVEC, PF, KS, XPT>;
+    auto* fn = &k_gemv_grp<QT, M, XVEC, PF, KS, XPT, PRE>;
     static size_t allowed = 0;
     int rc = allow_big_lds(fn, allowed, lds);
     if (rc) return rc;
@@ -679,13 +690,20 @@ int launch_grp_pf(const uint8_t* W, int64_t N, int64_t K, const ActSrc& act,
     if (lds > LDS_MAX) return fail(GQ_ERR_UNSUPPORTED, "gemv: activation too large for LDS");
     // residency is the same for every KS (same registers and LDS)
     int resident = 0;
-    int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1, XPT>, lds, resident);
+    int rc = resident_wgs(&k_gemv_grp<QT, M, XVEC, PF, 1, XPT, QTraits<QT>::CPG>, lds, resident);
     if (rc) return rc;
     // split K over the waves of a workgroup (whole steps per wave) only when
     // the row tiles leave most CUs without a workgroup (measured: splitting a
     // 4096-row down projection is slower, a 1536-row one faster)
     const int64_t t1 = cdiv(N, WAVES * RPW);
     const int J = (G + LPR - 1) / LPR;
+    // one row, a tile or more per resident workgroup: only part of the first step goes out
+    // before the activation prologue (4 of 9 chunks for Q4_0, 8 of 17 for Q8_0)
+    if constexpr (M == 1) {
+        if (t1 >= resident)
+            return launch_grp_ks<QT, M, XVEC, PF, 1, XPT, QT == GQ_TYPE_Q8_0 ? 8 : 4>(W, N, K, act, dst, ldd, fz, s,
+                                                                                       lds, resident);
+    }
     if (4 * t1 >= resident || J < 2)
         return launch_grp_ks<QT, M, XVEC, PF, 1, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
     if (J < 3) return launch_grp_ks<QT, M, XVEC, PF, 2, XPT>(W, N, K, act, dst, ldd, fz, s, lds, resident);
