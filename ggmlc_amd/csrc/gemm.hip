@@ -24,6 +24,7 @@
 // loads whose alignment is fixed per block, and expanded with v_perm (0x64xx fp16
 // exponent trick) + a packed fp16 subtraction.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "kernels.h"
@@ -38,6 +39,9 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int BN = 128, BK = 64, LDK = BK + 8;  // LDS row pitch in halves (144 B)
 constexpr int GEMM_PF_128 = 1, GEMM_PF_64 = 2;   // K steps of loads in flight per tile height
+#ifndef GEMM_PF_WS
+#define GEMM_PF_WS 2  // K steps in the producers' register ring (specialised 128-token kernel)
+#endif
 
 __device__ __forceinline__ uint32_t h2_sub_bits(uint32_t pair, half2v bias) {
     half2v h;
@@ -293,6 +297,231 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
         }
 }
 
+// 128-token tiles with specialised waves: 8 waves per workgroup, one workgroup per CU.
+// Waves 4-7 (producers) hold the register ring of global loads, park K step kt + 1 in
+// one of two LDS stages and expand its weight blocks, while waves 0-3 (consumers) run
+// step kt on the matrix cores from the other stage; one barrier per K step hands the
+// stages over. A SIMD then holds one wave of each kind, so the staging work (raw loads,
+// weight expansion, LDS writes) overlaps the MFMA phase instead of alternating with it.
+// Same tile, operand layout, block products and fma order as k_gemm: same bits.
+// The producers stage every step of [kt0, kt1] (kt1 itself reads zeros and is never
+// used) and always refill the ring, so their memory-counter waits stay exact.
+template <int QT>
+constexpr int ws_stage_bytes() {
+    return (2 * 128 + BN) * LDK * 2 + 2 * BN * 4;  // sAh, sAl (128 x LDK halves), sB, sD
+}
+
+template <int QT, int PF>
+__global__ __launch_bounds__(512, 1) void k_gemm_ws(const uint8_t* __restrict__ W, int64_t N, int64_t K,
+                                                    int64_t row_bytes, const uint16_t* __restrict__ A,
+                                                    int64_t lda, int64_t M, float* __restrict__ dst,
+                                                    int64_t ldd, int spk, float* __restrict__ part,
+                                                    const float* __restrict__ bias) {
+    constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
+    constexpr int BM = 128, MI = 2, AQ = 4;
+    constexpr int TILE_H = BM * LDK;  // halves of one of sAh / sAl
+    constexpr int STAGE = ws_stage_bytes<QT>();
+    extern __shared__ __align__(16) uint8_t gsm[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: role branches are scalar
+    const int64_t n0 = (int64_t)blockIdx.x * BN;
+    const int64_t m0 = (int64_t)blockIdx.y * BM;
+    const int nb = (int)(K / QK);
+    const int kt0 = (int)blockIdx.z * spk;
+    const int kt1 = min((int)cdiv(K, BK), kt0 + spk);  // this workgroup's K steps [kt0, kt1)
+
+    if (wave >= 4) {
+        // producers: thread p -> B: (weight row p / 2, block p % 2); A: (token row p / 2,
+        // 16-byte pieces 4 (p % 2) .. + 3 of the row's 128-byte K step, hi and lo)
+        const int p = tid - 256;
+        const int lrow = p >> 1, lhalf = p & 1;
+        const int arow = p >> 1, apiece = (p & 1) * AQ;
+        uint4 rh[PF][AQ], rl[PF][AQ];
+        BlockRegs<QT> rb[PF];
+        const __amdgpu_buffer_rsrc_t ars = make_rsrc(A + m0 * lda, min<int64_t>(M - m0, BM) * lda * 2);
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W + n0 * row_bytes, min<int64_t>(N - n0, BN) * row_bytes);
+        const uint32_t arow_off = (uint32_t)(arow * lda * 2);
+        const uint32_t wrow_off = (uint32_t)(lrow * row_bytes);
+        auto load = [&](int kt, int slot) {
+            const int64_t k = (int64_t)kt * BK + apiece * 8;
+            const bool av = k < K && kt < kt1;
+            const uint32_t ao = av ? arow_off + (uint32_t)k * 2 : OOB;
+            const uint32_t lo = av ? ao + (uint32_t)K * 2 : OOB;
+#pragma unroll
+            for (int i = 0; i < AQ; ++i) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(ao + 16 * i), 0, 0);
+                rh[slot][i] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+#pragma unroll
+            for (int i = 0; i < AQ; ++i) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)(lo + 16 * i), 0, 0);
+                rl[slot][i] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+            const int kb = kt * 2 + lhalf;
+            load_block_rs<QT>(wrs, wrow_off + (uint32_t)kb * BB, kb < nb && kt < kt1, rb[slot]);
+        };
+        // park ring slot `slot` in LDS stage `buf`
+        auto park = [&](int slot, int buf) {
+            uint16_t* sAh = reinterpret_cast<uint16_t*>(gsm + buf * STAGE);
+            uint16_t* sAl = sAh + TILE_H;
+            uint16_t* sB = sAl + TILE_H;
+            float* sD = reinterpret_cast<float*>(sB + BN * LDK);
+            const int ao = arow * LDK + apiece * 8;
+            uint4* sah = reinterpret_cast<uint4*>(sAh + ao);
+            uint4* sal = reinterpret_cast<uint4*>(sAl + ao);
+#pragma unroll
+            for (int i = 0; i < AQ; ++i) {
+                sah[i] = rh[slot][i];
+                sal[i] = rl[slot][i];
+            }
+            uint32_t e[16];
+            float d;
+            expand_block<QT>(rb[slot], e, d);  // a zero block: scale 0, quants -8 (Q4_0) or 0
+            uint4* sb = reinterpret_cast<uint4*>(sB + lrow * LDK + lhalf * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sb[i] = make_uint4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3]);
+            sD[lhalf * BN + lrow] = d;
+        };
+#pragma unroll
+        for (int s = 0; s < PF; ++s) load(kt0 + s, s);
+        park(0, 0);
+        load(kt0 + PF, 0);
+        __syncthreads();
+        // iteration kt parks step kt + 1 (ring slot (kt + 1 - kt0) % PF) while the
+        // consumers run step kt
+        auto iter = [&](int kt, int slot) {
+            park(slot, (kt + 1 - kt0) & 1);
+            load(kt + 1 + PF, slot);
+            __syncthreads();
+        };
+        int kt = kt0;
+        for (; kt + PF <= kt1; kt += PF) {
+#pragma unroll
+            for (int s = 0; s < PF; ++s) iter(kt + s, (s + 1) % PF);
+        }
+#pragma unroll
+        for (int s = 0; s < PF - 1; ++s)
+            if (kt + s < kt1) iter(kt + s, (s + 1) % PF);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's last (unused) loads
+        return;
+    }
+
+    // consumers: wave (wm, wn) owns rows wm * 64 .. + 63 of the token tile and weight rows
+    // wn * 64 .. + 63
+    const int wm = wave >> 1, wn = wave & 1;
+    float16v acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    // A K step is 8 tile-blocks (block kb, tile (i, j)), each four dependent MFMAs (hi, lo of
+    // two K16 halves) into a block sum. The tiles run in pairs (i, 0), (i, 1) with the two
+    // chains interleaved (a dependent MFMA waits for its predecessor's result), and the 32
+    // scale fmas of the previous pair run while this pair's 8 MFMAs execute. Each tile keeps
+    // its MFMA order and its block order of fmas, so the bits are those of k_gemm.
+    // Operand fragments are read one quant block ahead: block 1 of stage kt while block 0
+    // runs; after the barrier (stage kt read, stage kt + 1 parked) block 0 of stage kt + 1
+    // while block 1 of kt runs.
+    const float16v zero = {};
+    float16v pend[2] = {zero, zero};  // the pending pair: tiles (1, 0), (1, 1) at a block boundary
+    float pdw[2] = {0.0f, 0.0f};      // acc starts at +0, so the first (empty) pending fmas leave it
+    struct Frag {
+        half8 a[2][MI], l[2][MI], b[2][2];  // [K16 half][i or j]
+        float dw[2];
+    };
+    auto read_block = [&](int stage, int kb, Frag& f) {
+        const uint16_t* sAh = reinterpret_cast<const uint16_t*>(gsm + stage * STAGE);
+        const uint16_t* sAl = sAh + TILE_H;
+        const uint16_t* sB = sAl + TILE_H;
+        const float* sD = reinterpret_cast<const float*>(sB + BN * LDK);
+        // MFMA operand layout (32x32x16 f16): lane l holds row l % 32 and the 8 K values
+        // 8 (l / 32) .. + 7 of the 16; D[i][j]: column j = l % 32, rows 8 (r / 4) +
+        // 4 (l / 32) + r % 4
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int kk = kb * 32 + h * 16 + 8 * (lane >> 5);
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int ro = (wm * (BM / 2) + i * 32 + (lane & 31)) * LDK + kk;
+                f.a[h][i] = *reinterpret_cast<const half8*>(sAh + ro);
+                f.l[h][i] = *reinterpret_cast<const half8*>(sAl + ro);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                f.b[h][j] = *reinterpret_cast<const half8*>(sB + (wn * 64 + j * 32 + (lane & 31)) * LDK + kk);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) f.dw[j] = sD[kb * BN + wn * 64 + j * 32 + (lane & 31)];
+    };
+    auto run_block = [&](const Frag& f) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            float16v blk[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    blk[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[h][i], f.b[h][j], h ? blk[j] : zero, 0, 0, 0);
+                    blk[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.l[h][i], f.b[h][j], blk[j], 0, 0, 0);
+                }
+            const int pi = i == 0 ? 1 : 0;  // the pending pair's row of tiles
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[pi][j][r] = __builtin_fmaf(pdw[j], pend[j][r], acc[pi][j][r]);
+                pend[j] = blk[j];
+                pdw[j] = f.dw[j];
+            }
+        }
+        // one MFMA and four scale fmas at a time
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+    };
+    Frag f0, f1;
+    __syncthreads();  // stage 0 parked
+    read_block(0, 0, f0);
+    for (int kt = kt0; kt < kt1; ++kt) {
+        const int stage = (kt - kt0) & 1;
+        read_block(stage, 1, f1);
+        __builtin_amdgcn_sched_barrier(0);  // the reads go out before the block's MFMAs
+        run_block(f0);
+        __builtin_amdgcn_sched_barrier(0);  // the barrier (and its wait for the reads) after them
+        __syncthreads();  // stage kt read; stage kt + 1 parked
+        read_block(stage ^ 1, 0, f0);
+        __builtin_amdgcn_sched_barrier(0);
+        run_block(f1);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[1][j][r] = __builtin_fmaf(pdw[j], pend[j][r], acc[1][j][r]);
+    if (part) {  // split K: this workgroup's partial tile; the reduce adds the bias
+        dst = part + (int64_t)blockIdx.z * M * N;
+        ldd = N;
+        bias = nullptr;
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= N) continue;
+            const float bn_ = bias ? bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < M) dst[m * ldd + n] = bias ? acc[i][j][r] + bn_ : acc[i][j][r];
+            }
+        }
+}
+
 // dst[m * ldd + n] = sum_z part[z][m][n], z in order (+ bias[n])
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int ks, int64_t M, int64_t N,
                                                      float* __restrict__ dst, int64_t ldd,
@@ -332,9 +561,11 @@ GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M) {
     GemmPlan p;
     p.bm = gemm_bm(N, M);
     const int64_t tiles = cdiv(N, BN) * cdiv(M, p.bm), nk = cdiv(K, BK);
-    // split K while the tiles leave CUs idle, keeping >= 4 K steps per split
+    // split K while the tiles leave CUs idle, keeping >= 4 K steps per split: up to one
+    // workgroup per CU for 128-token tiles (k_gemm_ws holds a CU), two for 64-token tiles
+    const int64_t per_cu = p.bm == 128 ? 1 : 2;
     int64_t ks = 1;
-    if (tiles < num_cus()) ks = std::min<int64_t>({cdiv(2 * num_cus(), tiles), nk / 4, 16});
+    if (tiles < num_cus()) ks = std::min<int64_t>({cdiv(per_cu * num_cus(), tiles), nk / 4, 16});
     if (ks < 1) ks = 1;
     p.spk = (int)cdiv(nk, ks);
     p.ks = (int)cdiv(nk, p.spk);  // no empty split
@@ -355,9 +586,18 @@ int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t ld
         hipLaunchKernelGGL((k_gemm<QT, 64, GEMM_PF_64>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
                            ldd, p.spk, pp, bias);
     } else {
+        constexpr size_t lds = 2 * (size_t)ws_stage_bytes<QT>();  // 112,640 B: two stages
+        static_assert(lds <= 160 * 1024, "two stages fit the workgroup's LDS");
+        auto* fn = &k_gemm_ws<QT, GEMM_PF_WS>;
+        static std::once_flag once;
+        static hipError_t attr = hipSuccess;
+        std::call_once(once, [&] {
+            attr = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+        });
+        if (attr != hipSuccess) return check_hip(attr, "gemm: set LDS attribute");
         const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 128), (unsigned)p.ks);
-        hipLaunchKernelGGL((k_gemm<QT, 128, GEMM_PF_128>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
-                           ldd, p.spk, pp, bias);
+        hipLaunchKernelGGL(fn, grid, dim3(512), lds, s, W, N, K, row_bytes, A, lda, M, dst, ldd, p.spk, pp, bias);
     }
     int rc = check_hip(hipGetLastError(), "gemm launch");
     if (rc != GQ_OK || p.ks == 1) return rc;

@@ -31,20 +31,27 @@ def gemm_plan(N, K, M, ncu=256):
     else:
         bm = 64 if cdiv(N, BN) * cdiv(M, 128) < ncu else 128
     tiles, nk = cdiv(N, BN) * cdiv(M, bm), cdiv(K, BK)
+    per_cu = 1 if bm == 128 else 2
     ks = 1
     if tiles < ncu:
-        ks = min(cdiv(2 * ncu, tiles), nk // 4, 16)
+        ks = min(cdiv(per_cu * ncu, tiles), nk // 4, 16)
     ks = max(ks, 1)
     spk = cdiv(nk, ks)
     return bm, cdiv(nk, spk), spk
 
 
-PF = {128: 1, 64: 2}  # gemm.hip GEMM_PF_128, GEMM_PF_64: K steps of loads in flight
+PF = {128: 2, 64: 2}  # gemm.hip GEMM_PF_WS (k_gemm_ws), GEMM_PF_64 (k_gemm): K steps of loads in flight
+LDS_MAX = 160 * 1024  # LDS of one workgroup on gfx950
 
 
 def lds_bytes(bm):
-    """sAh, sAl (BM x LDK halves), sB (BN x LDK halves), sD[2][BN] floats"""
+    """one stage: sAh, sAl (BM x LDK halves), sB (BN x LDK halves), sD[2][BN] floats"""
     return (2 * bm * LDK + BN * LDK) * 2 + 2 * BN * 4
+
+
+def stages(bm):
+    """k_gemm_ws (128-token tiles) double-buffers its stage in dynamic LDS; k_gemm (64) has one"""
+    return 2 if bm == 128 else 1
 
 
 def check_launch(qt, N, K, M):
@@ -56,7 +63,11 @@ def check_launch(qt, N, K, M):
     aq = bm // 32
     mi = bm // 64
     sb = lds_bytes(bm)
-    assert sb <= 64 * 1024  # static LDS of one workgroup
+    if stages(bm) == 1:
+        assert sb <= 64 * 1024  # static LDS of one workgroup
+    else:
+        assert stages(bm) * sb <= LDS_MAX and sb % 16 == 0  # stage 1 starts 16-byte aligned
+    # loader threads: all 256 threads of k_gemm, the 256 producer threads (waves 4-7) of k_gemm_ws
     tid = np.arange(256)
     lane, wave = tid & 63, tid >> 6
     wm, wn = wave >> 1, wave & 1
@@ -83,8 +94,8 @@ def check_launch(qt, N, K, M):
                 kt0 = bz * spk
                 kt1 = min(cdiv(K, BK), kt0 + spk)
                 assert kt0 < kt1  # no empty split
-                # every step the ring loads: kt0 .. kt1 + PF - 1 (prologue and refills)
-                for kt in range(kt0, kt1 + PF[bm]):
+                # every step the ring loads: kt0 .. kt1 + PF (prologue and refills)
+                for kt in range(kt0, kt1 + PF[bm] + 1):
                     k = kt * BK + apiece * 8
                     av = (k < K) & (kt < kt1)
                     ao = np.where(av, arow_off + k * 2, OOB)
@@ -110,7 +121,12 @@ def check_launch(qt, N, K, M):
                         # the block read stays inside its row
                         assert np.all(ok | (o + width - wrow_off <= row_bytes))
                     assert np.all(~valid | (doff % 4 == 0))
-    # LDS: tile writes and MFMA operand reads (halves within a tile, then bytes)
+    # LDS: tile writes and MFMA operand reads (halves within a tile, then bytes); with two
+    # stages every address below is also taken at + sb, which stays inside 2 * sb
+    if stages(bm) == 2:
+        # parity of the stage parked by iteration kt and the one read in it never coincide
+        for r in range(40):
+            assert ((r + 1) & 1) != (r & 1)
     for i in range(aq):
         ah = (arow * LDK + apiece * 8 + 8 * i) * 2
         assert (ah + 16).max() <= bm * LDK * 2
@@ -145,3 +161,56 @@ SHAPES = [
 @pytest.mark.parametrize("qt,N,K,M", SHAPES)
 def test_gemm_addresses_in_bounds(qt, N, K, M):
     check_launch(qt, N, K, M)
+
+
+def ws_schedule(kt0, kt1, pf):
+    """k_gemm_ws's loop structure restated: the producers' ring loads and parks and the
+    consumers' reads, per barrier interval. Returns (producer barriers, consumer barriers,
+    intervals), each interval a dict of the step parked (and its stage) and the step read."""
+    ring = {}
+    intervals = [{"park": None, "read": None}]
+    for s in range(pf):  # prologue loads
+        ring[s] = kt0 + s
+    intervals[0]["park"] = (ring[0], 0)
+    ring[0] = kt0 + pf
+    pbar = 1
+
+    def iter_(kt, slot):
+        nonlocal pbar
+        intervals.append({"park": (ring[slot], (kt + 1 - kt0) & 1), "read": None})
+        assert ring[slot] == kt + 1  # the slot holds the step being parked
+        ring[slot] = kt + 1 + pf
+        pbar += 1
+
+    kt = kt0
+    while kt + pf <= kt1:
+        for s in range(pf):
+            iter_(kt + s, (s + 1) % pf)
+        kt += pf
+    for s in range(pf - 1):
+        if kt + s < kt1:
+            iter_(kt + s, (s + 1) % pf)
+    cbar = 1
+    for kt in range(kt0, kt1):
+        intervals[cbar]["read"] = (kt, (kt - kt0) & 1)
+        cbar += 1
+    return pbar, cbar, intervals
+
+
+@pytest.mark.parametrize("pf", [1, 2, 3, 4])
+def test_gemm_ws_schedule(pf):
+    for kt0 in (0, 3, 16):
+        for n in range(1, 40):
+            kt1 = kt0 + n
+            pbar, cbar, iv = ws_schedule(kt0, kt1, pf)
+            assert pbar == cbar == n + 1  # both roles pass the same barriers
+            parked = {}
+            for i, d in enumerate(iv):
+                if d["read"] is not None:
+                    step, buf = d["read"]
+                    assert parked[buf] == step  # parked in an earlier interval, not overwritten since
+                    assert d["park"][1] != buf  # the stage being parked is not the one being read
+                if d["park"] is not None:
+                    parked[d["park"][1]] = d["park"][0]
+            reads = [d["read"][0] for d in iv if d["read"] is not None]
+            assert reads == list(range(kt0, kt1))
