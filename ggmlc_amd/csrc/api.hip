@@ -6,6 +6,8 @@
 #include <cmath>
 #include <cstdio>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -49,6 +51,7 @@ bool rows_uniform(const gq_tensor* t) {
 struct MulMatPlan {
     int64_t K, N, M, x_stride, ldd;
     bool use_gemv;
+    bool use_i8;  // 5..16 rows on int8 MFMA (gemm_i8) when the weight is 16-byte aligned
     size_t ws, ws_act;
 };
 
@@ -83,10 +86,14 @@ int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, M
     // the GEMV quantizes the activation in LDS; the GEMM takes it from the workspace as the
     // exact fp16 pair hi + lo of d * q (rows of 2K halves), followed by the split-K partials
     // when its plan splits K
+    p.use_i8 = !p.use_gemv && p.M <= GEMM_I8_MAX_M && K % GEMM_I8_K_ALIGN == 0 && K <= PREP_MAX_K;
     const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 4;
     p.ws_act = (raw + 255) & ~(size_t)255;
     p.ws = p.ws_act;
     if (!p.use_gemv && p.M > 0) p.ws += (gemm_plan(N, K, p.M).part_bytes + 255) & ~(size_t)255;
+    // the int8 path's activation layout; the GEMM path's size is kept for weights that are
+    // not 16-byte aligned (known only at the call), which take the GEMM
+    if (p.use_i8) p.ws = std::max(p.ws, (gemm_i8_act_bytes(K) + 255) & ~(size_t)255);
     return GQ_OK;
 }
 
@@ -167,6 +174,12 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
     const uint8_t* W = static_cast<const uint8_t*>(a->data);
     if (p.use_gemv) return gemv(a->type, W, p.N, p.K, ActSrc{x, p.x_stride, nullptr, 0, nullptr, 0}, p.M, y, p.ldd,
                                 GemvFuse{}, s);
+    if (p.use_i8 && (reinterpret_cast<uintptr_t>(W) & 15) == 0) {
+        uint8_t* act = static_cast<uint8_t*>(workspace);
+        rc = act_prep_i8(ActPrep{x, p.x_stride, nullptr, 0, nullptr, 0, p.K, 0, 0, 0.0f}, p.M, act, s);
+        if (rc) return rc;
+        return gemm_i8(a->type, W, p.N, p.K, act, p.M, y, p.ldd, s);
+    }
     uint16_t* A = static_cast<uint16_t*>(workspace);
     rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, 2 * p.K, s);
     if (rc) return rc;
@@ -304,6 +317,13 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
         return fail(GQ_ERR_INVALID, "mul_mat_fused: workspace must be 256-byte aligned");
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
+    if (p.use_i8 && (reinterpret_cast<uintptr_t>(a->data) & 15) == 0) {
+        uint8_t* act = static_cast<uint8_t*>(f->workspace);
+        int rc = act_prep_i8(ap, p.M, act, s);
+        if (rc) return rc;
+        return gemm_i8(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M,
+                       static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), s, bias);
+    }
     uint16_t* A = static_cast<uint16_t*>(f->workspace);
     int rc = act_prep(ap, p.M, A, 2 * p.K, s);
     if (rc) return rc;

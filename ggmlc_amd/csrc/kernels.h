@@ -29,6 +29,11 @@ struct ActPrep {
     float eps;
 };
 int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStream_t s);
+// The same prologue for gemm_i8 (M <= 16): the quants of quantize_row_q8_0 as int8 in
+// the i8 layout, per block b: y[b * 512 + m * 32 + j] the quants of row m, then
+// y[nb * 512 + (b * 16 + m) * 4] the scale (f32) and y[nb * 576 + (b * 16 + m) * 4] the
+// block sum (i32); gemm_i8_act_bytes(K) bytes
+int act_prep_i8(const ActPrep& a, int64_t M, uint8_t* y, hipStream_t s);
 int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
                       int64_t y_stride_elems, hipStream_t s);
 int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s);
@@ -92,6 +97,20 @@ struct GemmPlan {
 GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M);
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
          float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias = nullptr);
+
+// gemm_i8.hip — dst[m * ldd + n] for 1 <= M <= GEMM_I8_MAX_M activation rows on int8
+// MFMA, for K % 256 == 0 and 16-byte aligned weights, from act_prep_i8's layout; 16-row
+// tiles, the 4 waves of a workgroup splitting K into ks parts for narrow weights
+constexpr int GEMM_I8_MAX_M = 16;
+constexpr int64_t GEMM_I8_K_ALIGN = 256;
+inline size_t gemm_i8_act_bytes(int64_t K) { return (size_t)(K / 32) * 640; }
+struct GemmI8Plan {
+    int ks;
+    int64_t wgs;
+};
+GemmI8Plan gemm_i8_plan(int64_t N, int64_t K);
+int gemm_i8(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst,
+            int64_t ldd, hipStream_t s, const float* bias = nullptr);
 
 // set_rows.hip
 struct SetRowsArgs {

@@ -95,8 +95,9 @@ int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride
 constexpr int PREP_CH = PREP_MAX_K / 2048;
 
 // CH > 0: the launch has exactly CH chunks (straight-line code the compiler can
-// interleave); CH = 0: up to PREP_CH chunks, the ones past K skipped
-template <bool VEC, int CH>
+// interleave); CH = 0: up to PREP_CH chunks, the ones past K skipped. I8: the int8 layout
+// of gemm_i8 (quants, scale, block sum per (block, row)) instead of the fp16 pair.
+template <bool VEC, int CH, bool I8 = false>
 __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restrict__ y, int64_t y_stride) {
     constexpr int NC = CH ? CH : PREP_CH;
     __shared__ double red[4];
@@ -154,12 +155,49 @@ __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restric
         int qsum;
         quant8_block(v[c], q, dh, qsum);  // all lanes: pieces past K quantize zeros
         if ((t >> 2) >= nb) continue;
+        if constexpr (I8) {
+            uint8_t* yb = reinterpret_cast<uint8_t*>(y);
+            const int64_t e = (int64_t)(t >> 2) * 16 + m;  // (block, row)
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w0 |= (uint32_t)(q[i] & 0xff) << (8 * i);
+                w1 |= (uint32_t)(q[4 + i] & 0xff) << (8 * i);
+            }
+            *reinterpret_cast<uint2*>(yb + e * 32 + (t & 3) * 8) = make_uint2(w0, w1);
+            if ((t & 3) == 0) {
+                *reinterpret_cast<float*>(yb + (int64_t)nb * 512 + e * 4) = h2f(dh);
+                *reinterpret_cast<int*>(yb + (int64_t)nb * 576 + e * 4) = qsum;
+            }
+            continue;
+        }
         uint4 hi, lo;
         split_dq8(q, dh, hi, lo);
         uint16_t* row = y + m * y_stride + (int64_t)t * 8;
         *reinterpret_cast<uint4*>(row) = hi;
         *reinterpret_cast<uint4*>(row + a.K) = lo;
     }
+}
+
+int act_prep_i8(const ActPrep& a, int64_t M, uint8_t* y, hipStream_t s) {
+    if (M == 0) return GQ_OK;
+    if (M > GEMM_I8_MAX_M || a.K > PREP_MAX_K || a.K % QK) return fail(GQ_ERR_UNSUPPORTED, "act_prep_i8: shape");
+    const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.xs % 4 == 0) &&
+                     (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) && a.K % 4 == 0;
+    uint16_t* yy = reinterpret_cast<uint16_t*>(y);
+    const dim3 g((unsigned)M);
+    if (vec) {
+        switch (cdiv(a.K, 2048)) {
+            case 1: hipLaunchKernelGGL((k_act_prep<true, 1, true>), g, dim3(256), 0, s, a, yy, 0); break;
+            case 2: hipLaunchKernelGGL((k_act_prep<true, 2, true>), g, dim3(256), 0, s, a, yy, 0); break;
+            case 5: hipLaunchKernelGGL((k_act_prep<true, 5, true>), g, dim3(256), 0, s, a, yy, 0); break;
+            case 6: hipLaunchKernelGGL((k_act_prep<true, 6, true>), g, dim3(256), 0, s, a, yy, 0); break;
+            default: hipLaunchKernelGGL((k_act_prep<true, 0, true>), g, dim3(256), 0, s, a, yy, 0); break;
+        }
+    } else {
+        hipLaunchKernelGGL((k_act_prep<false, 0, true>), g, dim3(256), 0, s, a, yy, 0);
+    }
+    return check_hip(hipGetLastError(), "act_prep_i8 launch");
 }
 
 int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStream_t s) {

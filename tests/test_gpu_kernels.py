@@ -127,7 +127,9 @@ def test_mlp_c2_q4_0(M):
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("K,N,M", [(960, 1600, 1), (960, 5120, 3), (2560, 960, 1), (960, 960, 37),
                                    (1536, 2048, 16), (8960, 1536, 1), (256, 130, 5), (32, 7, 2),
-                                   (8960, 1536, 16), (1536, 17920, 12)])
+                                   (8960, 1536, 16), (1536, 17920, 12),
+                                   # 5..16 rows on int8 MFMA: row tails, K split in 1, 2 and 4 parts
+                                   (2048, 100, 9), (4096, 33, 13), (11008, 300, 16), (4096, 16500, 6)])
 def test_mul_mat_shapes(qtype, K, N, M):
     _check_mm(qtype, K, N, M, seed=K + N + M)
 
@@ -288,7 +290,8 @@ def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_d
     (O.Q8_0, 960, 1600, 3, "plain"),        # K = 960 (block-wise kernel), three rows
     (O.Q4_0, 4096, 22016, 1, "swiglu"),     # bias on both halves before SWIGLU
     (O.Q8_0, 2560, 960, 2, "add"),          # bias, then the residual ADD
-    (O.Q8_0, 1536, 2048, 16, "gemm"),       # batch 16: GEMM path, split K, bias in the reduce
+    (O.Q8_0, 1536, 2048, 16, "gemm"),       # batch 16: int8 MFMA path, K in 4 parts, bias in the store
+    (O.Q4_0, 4096, 4096, 5, "gemm"),        # 5 rows: int8 MFMA path
     (O.Q4_0, 4096, 12288, 37, "gemm"),      # prompt rows: GEMM path, bias in the tile store
 ])
 def test_mul_mat_fused_bias_bit_identical(qtype, K, N, M, epi):
