@@ -28,9 +28,9 @@ def plan(N, K):
     """gemm_i8.hip gemm_i8_plan"""
     tiles, nsteps = cdiv(N, 16), K // (QK * NBS)
     ks = 1
-    if tiles < 512 and nsteps >= 8:
+    if tiles < 512 and nsteps >= 4:
         ks = 4
-    elif tiles < 1024 and nsteps >= 4:
+    elif tiles < 4096 and nsteps >= 4:
         ks = 2
     return ks, cdiv(tiles, 4 // ks)
 
