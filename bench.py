@@ -213,7 +213,8 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_0 weights x q8_0 activations: int8 dot4 with exact int32 block sums (decode); exact "
-                 "fp16 hi+lo block products on f16 MFMA (prefill); f32 accumulate; f16 KV",
+                 "fp16 hi+lo block products on f16 MFMA (prefill); exact int32 block sums on int8 MFMA "
+                 "(5..16 rows); f32 accumulate; f16 KV",
         "data": "synthetic (random-init weights N(0,0.02) -> Q4_0; uniform-random prompt ids)",
         "config": {
             "workload": f"configs[3] {cfg.name} decoder, Q4_0, batch 1: pp{args.prompt} (ubatch 512) then "
@@ -230,7 +231,7 @@ def main() -> int:
         "decode_weight_plus_kv_GBps": r7["decode_weight_plus_kv_GBps"],
         "roofline": roofline,
         "roofline_prefill_gemm": {
-            "kernel": "k_gemm<Q4_0>: the 128 GEMMs of one 512-token ubatch (activation quantize excluded); "
+            "kernel": "k_gemm_ws<Q4_0>: the 128 GEMMs of one 512-token ubatch (activation quantize excluded); "
                       "each exact block product takes two f16 MFMAs (hi, lo) per 32 K",
             "bound": "mfma",
             "achieved": round(gemm_tflops, 1),
@@ -546,7 +547,8 @@ def bench_c2(dev, ws, Ms=(1, 8, 128, 512), copies: int = 4, blocks: int = 16) ->
         ms = time_graph(loop, 5 if M <= 128 else 3) / blocks
         flops = 2.0 * M * (2 * F * H + H * F)
         nbytes = wbytes + 4 * M * (H + F + H)
-        row = {"path": "GEMV" if M <= 4 else "GEMM", "us_per_block": round(ms * 1e3, 3),
+        path = "GEMV (v_dot4)" if M <= 4 else ("int8 MFMA GEMM" if M <= 16 else "fp16 MFMA GEMM (exact hi + lo products)")
+        row = {"path": path, "us_per_block": round(ms * 1e3, 3),
                "tok_s": round(M * 1000.0 / ms, 1), "achieved_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2),
