@@ -83,6 +83,18 @@ Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
         const int umax = p.NQ > 4 ? 4 : 8;
         int u = umax;
         while (u > 2 && Hkv * cdiv(n_kv, u * rows_it) < DEC_TARGET_WG / 2) u >>= 1;
+        // one query vector per kv head (MHA decode), 128-dim: 160- or 192-row splits when
+        // they need fewer rounds of workgroups over the CUs (rounds x rows per split), so a
+        // 32-head launch at n_kv = 1280 is one workgroup per CU (measured: tg128 +0.65%)
+        if (p.NQ == 1 && D == 128 && u == 8) {
+            const int64_t ncu = 256;
+            int64_t best = cdiv(Hkv * cdiv(n_kv, 8 * rows_it), ncu) * 8;
+            for (int c : {10, 12}) {
+                const int64_t ns = cdiv(n_kv, c * rows_it);
+                const int64_t cost = cdiv(Hkv * ns, ncu) * c;
+                if (ns <= FUSE_MAX_SPLIT && cost < best) best = cost, u = c;
+            }
+        }
         p.dec_u = u;
         p.rows_per_split = u * rows_it;
         p.n_split = cdiv(n_kv, p.rows_per_split);
@@ -714,6 +726,7 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
     const int Hkv = (int)a.Hkv;
     const int64_t r_begin = (int64_t)split * 128;
     const int64_t len = pg.len[seq];
+    if (r_begin >= len) return;  // past this sequence: k_attn_merge reads no partial for it
     const int64_t pi = r_begin >> pg.log2p;
     const int page = (r_begin < len && pi < pg.tstride) ? pg.table[seq * pg.tstride + pi] : -1;
     const int64_t r_len = page < 0 ? 0 : len;  // logical rows below r_len are read
@@ -1079,14 +1092,19 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps
 // Merge of split partials (ops.cpp:9060-9128): weights w_s = exp(m_s - max) are
 // computed once in LDS, then each thread sums its dimension over the splits with
 // independent loads.
+// With `len` (paged batches), query vector qv belongs to sequence qv / G and only its
+// first cdiv(len, rps) splits hold partials (the splits past a sequence's length are not
+// computed); without it every split does.
 template <int D>
 __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part, int n_split, int Hkv, int NQ,
-                                                  int G, int64_t Hq, float* __restrict__ dst) {
+                                                  int G, int64_t Hq, float* __restrict__ dst,
+                                                  const int32_t* __restrict__ len = nullptr, int rps = 1) {
     __shared__ float sW[MAX_SPLIT];
     __shared__ float sRed[D / 64 > 0 ? D / 64 : 1];
     const int qv = blockIdx.x;
     const int hk = blockIdx.y;
     const int d = threadIdx.x;
+    if (len) n_split = min(n_split, (int)cdiv(max(len[qv / G], 0), rps));
     const int64_t stride = (int64_t)Hkv * NQ * (D + 2);
     const float* base = part + ((int64_t)hk * NQ + qv) * (D + 2);
     float mx = -INFINITY;
@@ -1164,7 +1182,9 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         else GQ_DEC(DD, NN, 2);                    \
     } while (0)
         if (a.D == 128) {
-            if (nq == 1) GQ_DEC_U(128, 1);
+            if (nq == 1 && p.dec_u == 12) GQ_DEC(128, 1, 12);
+            else if (nq == 1 && p.dec_u == 10) GQ_DEC(128, 1, 10);
+            else if (nq == 1) GQ_DEC_U(128, 1);
             else if (nq == 2) GQ_DEC_U(128, 2);
             else if (nq <= 4) GQ_DEC_U(128, 4);
             else if (p.dec_u == 4) GQ_DEC(128, 8, 4);  // u <= 4 for more than 4 query vectors
@@ -1265,10 +1285,10 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
         const dim3 g2((unsigned)(pg.B * G), (unsigned)a.Hkv);
         if (a.D == 128)
             hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
-                               a.Hq, a.dst);
+                               a.Hq, a.dst, pg.len, 128);
         else
             hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
-                               a.Hq, a.dst);
+                               a.Hq, a.dst, pg.len, 128);
         return check_hip(hipGetLastError(), "flash_attn_paged merge launch");
     }
     const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);

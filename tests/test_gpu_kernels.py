@@ -409,7 +409,9 @@ def test_flash_attn_golden(golden_dir):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
-    (32, 32, 128, 1, 1100, 2048),   # config 4 decode (MHA)
+    (32, 32, 128, 1, 1100, 2048),   # config 4 decode (MHA): n_kv 1280, 160-row splits
+    (32, 32, 128, 1, 1400, 2048),   # n_kv 1536: 192-row splits
+    (32, 32, 128, 1, 900, 2048),    # n_kv 1024: 128-row splits
     (15, 5, 64, 1, 600, 1024),      # config 3 decode (GQA 3)
     (12, 2, 128, 1, 4000, 4352),    # config 5 decode, long context (GQA 6)
     (15, 5, 64, 4, 300, 1024),      # small chunk
@@ -457,7 +459,7 @@ def test_flash_attn_banded_mask_prefill(D, G, masked):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
-    (32, 32, 128, 1, 1100, 2048),   # 7B decode: 10 splits per kv head
+    (32, 32, 128, 1, 1100, 2048),   # 7B decode: 8 splits of 160 rows per kv head
     (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, many splits
 ])
 def test_flash_attn_decode_workspace_and_replays(Hq, Hkv, D, S, pos, ctx):
@@ -502,7 +504,7 @@ def test_flash_attn_decode_workspace_and_replays(Hq, Hkv, D, S, pos, ctx):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
-    (32, 32, 128, 1, 1100, 2048),   # 7B decode: 10 splits per kv head
+    (32, 32, 128, 1, 1100, 2048),   # 7B decode: 8 splits of 160 rows per kv head
     (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, 34 splits
     (15, 5, 64, 1, 700, 1024),      # SmolLM2 shape
 ])
