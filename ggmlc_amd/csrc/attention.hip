@@ -707,6 +707,44 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
 // The 4 waves' (m, l, O) merge in LDS into the split's partial, which k_attn_merge
 // combines across splits. Rows past a sequence's length (and missing pages) are never
 // read: their loads use out-of-range offsets.
+//
+// The launch is a 1-D grid over a work list of (sequence, kv head, split) items that every
+// wave rebuilds from the sequence lengths: workgroup i takes item i, so the splits that
+// hold rows come first in dispatch order and the workgroups past the list's end (the
+// grid is sized for max_len) exit last. (A (split, kv head, sequence) grid left resident
+// slots to the empty splits of short sequences and ran working ones in a second round
+// behind them: 2 x the time at 16 sequences of 2048 rows under max_len 4096.)
+// Item i is kv head i % Hkv of split number i / Hkv in the list of every sequence's
+// min(cdiv(len, 128), n_split) splits in sequence order; false past the list's end.
+__device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int Hkv, int64_t i, int& seq, int& hk,
+                                           int& split) {
+    const int lane = threadIdx.x & 63;
+    const int64_t c = i / Hkv;
+    hk = (int)(i - c * Hkv);
+    int64_t base = 0;  // splits of the sequences before this chunk of 64
+    for (int b0 = 0; b0 < pg.B; b0 += 64) {
+        const int b = b0 + lane;
+        const int len = b < pg.B ? pg.len[b] : 0;
+        const int n = len > 0 ? (int)min<int64_t>(cdiv(len, 128), n_split) : 0;
+        int x = n;  // inclusive prefix sum over the chunk's lanes
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        const int tot = __shfl(x, 63, 64);
+        if (c < base + tot) {
+            // the sequences whose prefix ends at or before c precede the item's sequence
+            const int k = __popcll(__ballot(base + x <= c));
+            seq = b0 + k;
+            split = (int)(c - base - __shfl(x - n, k, 64));
+            return true;
+        }
+        base += tot;
+    }
+    return false;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_split, float* __restrict__ part,
                                                       PagedKv pg) {
@@ -722,11 +760,13 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
-    const int split = blockIdx.x, hk = blockIdx.y, seq = blockIdx.z;
     const int Hkv = (int)a.Hkv;
+    int seq_, hk_, split_;
+    if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_)) return;  // past the list
+    const int seq = __builtin_amdgcn_readfirstlane(seq_), hk = __builtin_amdgcn_readfirstlane(hk_),
+              split = __builtin_amdgcn_readfirstlane(split_);
     const int64_t r_begin = (int64_t)split * 128;
     const int64_t len = pg.len[seq];
-    if (r_begin >= len) return;  // past this sequence: k_attn_merge reads no partial for it
     const int64_t pi = r_begin >> pg.log2p;
     const int page = (r_begin < len && pi < pg.tstride) ? pg.table[seq * pg.tstride + pi] : -1;
     const int64_t r_len = page < 0 ? 0 : len;  // logical rows below r_len are read
@@ -1139,6 +1179,17 @@ __global__ void k_attn_reset_counters() {
     if (i < ARRIVE_N) g_attn_arrive[i] = 0u;
 }
 
+// the split merge (len, rps: the paged launches' per-sequence split counts)
+int launch_merge(int64_t D, const float* part, int ns, int Hkv, int NQ, int G, int64_t Hq, float* dst,
+                 const int32_t* len, int rps, hipStream_t s) {
+    const dim3 g2((unsigned)NQ, (unsigned)Hkv);
+    if (D == 128)
+        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps);
+    else
+        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps);
+    return check_hip(hipGetLastError(), "attention merge launch");
+}
+
 }  // namespace
 
 int attn_reset_counters(hipStream_t s) {
@@ -1216,14 +1267,7 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     }
     int rc = check_hip(hipGetLastError(), "flash_attn_ext launch");
     if (rc != GQ_OK || p.n_split == 1 || fused_merge) return rc;
-    const dim3 g2((unsigned)p.NQ, (unsigned)a.Hkv);
-    if (a.D == 128)
-        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ,
-                           (int)p.G, a.Hq, a.dst);
-    else
-        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ,
-                           (int)p.G, a.Hq, a.dst);
-    return check_hip(hipGetLastError(), "flash_attn_ext merge launch");
+    return launch_merge(a.D, part, (int)p.n_split, (int)a.Hkv, (int)p.NQ, (int)p.G, a.Hq, a.dst, nullptr, 1, s);
 }
 
 namespace {
@@ -1276,20 +1320,14 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
     const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)pg.B);
     const int nq = (int)G, ns = (int)p.n_split;
     if (p.u < 0) {
+        const dim3 g1((unsigned)(p.n_split * a.Hkv * pg.B));  // one workgroup per possible item
         if (a.D == 128)
-            hipLaunchKernelGGL(k_attn_dec_mma<128>, gd, dim3(256), 0, s, a, nq, ns, part, pg);
+            hipLaunchKernelGGL(k_attn_dec_mma<128>, g1, dim3(256), 0, s, a, nq, ns, part, pg);
         else
-            hipLaunchKernelGGL(k_attn_dec_mma<64>, gd, dim3(256), 0, s, a, nq, ns, part, pg);
+            hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, nq, ns, part, pg);
         int rc = check_hip(hipGetLastError(), "flash_attn_paged (mfma) launch");
         if (rc != GQ_OK || p.n_split == 1) return rc;
-        const dim3 g2((unsigned)(pg.B * G), (unsigned)a.Hkv);
-        if (a.D == 128)
-            hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
-                               a.Hq, a.dst, pg.len, 128);
-        else
-            hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
-                               a.Hq, a.dst, pg.len, 128);
-        return check_hip(hipGetLastError(), "flash_attn_paged merge launch");
+        return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, pg.len, 128, s);
     }
     const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);
     const int fuse = fused_merge ? 1 : 0;
@@ -1319,14 +1357,7 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
 #undef GQ_PDEC
     int rc = check_hip(hipGetLastError(), "flash_attn_paged launch");
     if (rc != GQ_OK || p.n_split == 1 || fused_merge) return rc;
-    const dim3 g2((unsigned)(pg.B * G), (unsigned)a.Hkv);
-    if (a.D == 128)
-        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
-                           a.Hq, a.dst);
-    else
-        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G,
-                           a.Hq, a.dst);
-    return check_hip(hipGetLastError(), "flash_attn_paged merge launch");
+    return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, nullptr, 1, s);
 }
 
 // ---- allocation-free decode attention -------------------------------------

@@ -95,3 +95,59 @@ def test_radix_lru_eviction_respects_references():
     assert t.total_nodes == 1 and t.evict_lru(1) == []
     t.insert_prefix([8, 8], 0, [4])
     assert t.reset() == [4] and t.total_cached_pages == 0
+
+
+# ---- work list of the matrix-core paged attention kernel (k_attn_dec_mma) ---------
+# Host model of paged_item (csrc/attention.hip): each wave takes the sequence lengths
+# in chunks of 64 lanes, forms the inclusive prefix sum of every sequence's
+# min(cdiv(len, 128), n_split) splits, and locates split number c = i // Hkv with a
+# ballot of the lanes whose prefix ends at or before c.
+def _paged_item(lens, n_split, hkv, i):
+    c, hk = divmod(i, hkv)
+    base = 0
+    for b0 in range(0, len(lens), 64):
+        n = [0] * 64
+        for lane in range(64):
+            b = b0 + lane
+            ln = lens[b] if b < len(lens) else 0
+            n[lane] = min(-(-ln // 128), n_split) if ln > 0 else 0
+        x, acc = [], 0
+        for lane in range(64):
+            acc += n[lane]
+            x.append(acc)
+        tot = x[63]
+        if c < base + tot:
+            k = sum(1 for lane in range(64) if base + x[lane] <= c)
+            assert k < 64 and b0 + k < len(lens) and n[k] > 0
+            return b0 + k, hk, c - base - (x[k] - n[k])
+        base += tot
+    return None
+
+
+@pytest.mark.parametrize("lens,max_len,hkv", [
+    ([2079, 3260, 3543, 2835, 652, 1167, 2993, 945, 3521, 1587, 2105, 840, 763, 1452, 3882, 1174], 4096, 2),
+    ([2048] * 16, 4096, 2),
+    ([0, 1, 127, 128, 129, 0, 5000, -3], 4096, 1),  # empty, partial, exact, past max_len, negative
+    ([(i * 37) % 900 for i in range(130)], 1024, 3),  # three chunks of 64 lanes
+    ([0] * 5, 256, 2),
+])
+def test_paged_mma_work_list(lens, max_len, hkv):
+    """Every (sequence, kv head, split below the sequence's length and the grid's split
+    count) is exactly one item, items come first in the grid and the rest report the end."""
+    n_split = -(-max_len // 128)
+    grid = n_split * hkv * len(lens)
+    want = {(b, h, sp) for b, ln in enumerate(lens) if ln > 0
+            for sp in range(min(-(-ln // 128), n_split)) for h in range(hkv)}
+    got, ended = [], False
+    for i in range(grid):
+        it = _paged_item(lens, n_split, hkv, i)
+        if it is None:
+            ended = True
+            continue
+        assert not ended, "an item after the end of the list"
+        got.append(it)
+    assert len(got) == len(set(got)) == len(want)
+    assert set(got) == want
+    # the kernel reads rows [split * 128, min(len, split * 128 + 128)): inside the sequence
+    for b, _, sp in got:
+        assert sp * 128 < lens[b] and sp < n_split
