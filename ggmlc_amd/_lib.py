@@ -70,6 +70,8 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("bias", ctypes.POINTER(gq_tensor)),
+        ("out_q8", ctypes.c_void_p),
+        ("b_q8", ctypes.c_void_p),
     ]
 
 
@@ -110,6 +112,9 @@ SIGNATURES = {
     "gq_mul_mat_fused_workspace_size": (ctypes.c_size_t, [_P, _P, ctypes.POINTER(gq_mul_mat_fusion)]),
     "gq_flash_attn_paged_workspace_size": (ctypes.c_size_t, [_P, _P, _i64, _i64]),
     "gq_flash_attn_paged": (ctypes.c_int, [_P, _P, _P, _P, _P, _i64, _i64, _f32, _P, _vp, ctypes.c_size_t, _vp]),
+    "gq_flash_attn_paged_q8": (ctypes.c_int, [_P, _P, _P, _P, _P, _i64, _i64, _f32, _P, _vp, _vp, ctypes.c_size_t,
+                                              _vp]),
+    "gq_q8_rows_bytes": (ctypes.c_size_t, [_i64]),
     "gq_paged_step_inputs": (ctypes.c_int, [_vp, _i64, _P, _i64, _i64, _vp, _vp, _vp]),
     "gq_paged_advance": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "gq_kv_pages_copy": (ctypes.c_int, [_P, _P, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),

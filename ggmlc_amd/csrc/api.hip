@@ -267,6 +267,8 @@ static int fused_plan(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_f
     return plan_mul_mat(a, &h, nullptr, p);
 }
 
+size_t gq_q8_rows_bytes(int64_t K) { return K > 0 && K % QK == 0 ? gemm_i8_act_bytes(K) : 0; }
+
 size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f) {
     MulMatPlan p;
     if (fused_plan(a, b, f, p) != GQ_OK || p.M <= GEMV_MAX_M) return 0;
@@ -274,20 +276,50 @@ size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, c
 }
 
 // the GEMM path (M > 4): the input-side fusions run in the activation prologue that
-// feeds the GEMM (act_prep), the output-side ones are not fused there
+// feeds the GEMM (act_prep); on the int8 path SWIGLU (with the next product's quantized
+// rows) and ROPE + SET_ROWS also run as the product's epilogue, and b may come already
+// quantized (b_q8)
 static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                               const MulMatPlan& p, hipStream_t s) {
-    if (f->swiglu || f->add || f->rope_kv)
-        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: output fusions (swiglu, add, rope_kv) need M <= 4, M = " +
-                                            std::to_string(p.M));
+    const bool i8 = p.use_i8 && (reinterpret_cast<uintptr_t>(a->data) & 15) == 0;
+    if (f->add) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: add needs M <= 4, M = " + std::to_string(p.M));
+    if ((f->swiglu || f->rope_kv) && !i8)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: swiglu / rope_kv need M <= 4 or the int8 path (M <= 16, "
+                                        "K % 256 == 0, 16-byte aligned weights), M = " + std::to_string(p.M));
+    if (f->out_q8 && !(i8 && f->swiglu))
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: out_q8 needs swiglu on the int8 path");
+    if (f->b_q8 && !i8) return fail(GQ_ERR_INVALID, "mul_mat_fused: b_q8 needs the int8 path");
+    if (f->b_q8 && (f->rms_norm || f->b_add || f->b_swiglu || f->b_sum))
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_q8 excludes the input-side fusions");
     if (p.K > PREP_MAX_K) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: K above the prologue's limit");
     if (f->b_swiglu && (f->rms_norm || f->b_add))
         return fail(GQ_ERR_INVALID, "mul_mat_fused: b_swiglu excludes rms_norm and b_add");
     const float* bias = nullptr;
     if (int rc = fused_bias(f, p, &bias)) return rc;
-    if (dst->type != GQ_TYPE_F32 || dst->ne[0] != p.N || dst->ne[1] != b->ne[1] || dst->ne[2] != b->ne[2] ||
-        dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 || !rows_uniform(dst))
-        return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [N, M, ...]: " + shape(dst));
+    I8Epi epi;
+    if (f->rope_kv) {
+        GemvFuse fz;
+        if (int rc = rope_kv_epilogue(*f->rope_kv, p, b, fz)) return rc;
+        epi.rope = 1;
+        epi.rp = fz.rp;
+        epi.pair_lo = fz.pair_lo;
+        epi.pair_h = fz.pair_h;
+    } else if (f->swiglu) {
+        if (p.N % 2) return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu needs an even row count: " + shape(a));
+        epi.glu = 1;
+        epi.pair_lo = ~(int64_t)0;
+        epi.pair_h = p.N / 2;
+        epi.q8 = static_cast<uint8_t*>(f->out_q8);
+    }
+    const int64_t n_out = f->swiglu ? p.N / 2 : p.N;
+    const bool no_dst = f->rope_kv || (f->out_q8 && !dst);
+    if (!no_dst && (!dst || dst->type != GQ_TYPE_F32 || dst->ne[0] != n_out || dst->ne[1] != b->ne[1] ||
+                    dst->ne[2] != b->ne[2] || dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 ||
+                    !rows_uniform(dst)))
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [" + std::to_string(n_out) + ", M, ...]: " +
+                                        (dst ? shape(dst) : std::string("NULL")));
+    float* dp = dst && !f->rope_kv ? static_cast<float*>(dst->data) : nullptr;
+    const int64_t ldd = dp ? (int64_t)(dst->nb[1] / 4) : 0;
     ActPrep ap{static_cast<const float*>(b->data), p.x_stride, nullptr, 0, nullptr, 0, p.K,
                f->rms_norm ? 1 : 0, f->b_swiglu ? 1 : 0, f->rms_eps};
     if (f->b_add) {
@@ -311,25 +343,32 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
         return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum needs b_add");
     }
     if (p.M == 0) return GQ_OK;
+    if (i8) {
+        const uint8_t* act = static_cast<const uint8_t*>(f->b_q8);
+        if (!act) {
+            if (!f->workspace || f->workspace_bytes < p.ws)
+                return fail(GQ_ERR_WORKSPACE,
+                            "mul_mat_fused: workspace too small (need " + std::to_string(p.ws) + " bytes)");
+            if ((reinterpret_cast<uintptr_t>(f->workspace) & 255) != 0)
+                return fail(GQ_ERR_INVALID, "mul_mat_fused: workspace must be 256-byte aligned");
+            uint8_t* w = static_cast<uint8_t*>(f->workspace);
+            if (int rc = act_prep_i8(ap, p.M, w, s)) return rc;
+            act = w;
+        }
+        return gemm_i8(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M, dp, ldd, s, bias,
+                       (epi.rope || epi.glu) ? &epi : nullptr);
+    }
     if (!f->workspace || f->workspace_bytes < p.ws)
         return fail(GQ_ERR_WORKSPACE, "mul_mat_fused: workspace too small (need " + std::to_string(p.ws) + " bytes)");
     if ((reinterpret_cast<uintptr_t>(f->workspace) & 255) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: workspace must be 256-byte aligned");
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
-    if (p.use_i8 && (reinterpret_cast<uintptr_t>(a->data) & 15) == 0) {
-        uint8_t* act = static_cast<uint8_t*>(f->workspace);
-        int rc = act_prep_i8(ap, p.M, act, s);
-        if (rc) return rc;
-        return gemm_i8(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M,
-                       static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), s, bias);
-    }
     uint16_t* A = static_cast<uint16_t*>(f->workspace);
     int rc = act_prep(ap, p.M, A, 2 * p.K, s);
     if (rc) return rc;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(f->workspace) + p.ws_act);
-    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, 2 * p.K, p.M,
-                static_cast<float*>(dst->data), (int64_t)(dst->nb[1] / 4), part, s, bias);
+    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, 2 * p.K, p.M, dp, ldd, part, s, bias);
 }
 
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
@@ -337,13 +376,15 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     if (!f) return fail(GQ_ERR_INVALID, "mul_mat_fused: null fusion");
     if ((f->swiglu != 0) + (f->add != nullptr) + (f->rope_kv != nullptr) > 1)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: swiglu, add and rope_kv are exclusive");
-    if (f->rope_kv ? dst != nullptr : dst == nullptr)
+    if (f->rope_kv ? dst != nullptr : (dst == nullptr && !f->out_q8))
         return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be NULL with rope_kv and given otherwise");
     MulMatPlan p;
     int rc = fused_plan(a, b, f, p);
     if (rc) return rc;
     if (p.M > GEMV_MAX_M) return mul_mat_fused_gemm(a, b, dst, f, p, (hipStream_t)stream);
     if (f->b_swiglu) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: b_swiglu needs M > 4 (use swiglu on the producer)");
+    if (f->out_q8 || f->b_q8)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: out_q8 / b_q8 need the int8 path (5..16 rows)");
     GemvFuse fz;
     rc = fused_bias(f, p, &fz.bias);
     if (rc) return rc;
@@ -757,9 +798,10 @@ size_t gq_flash_attn_paged_workspace_size(const gq_tensor* q, const gq_tensor* k
     return attn_paged_workspace_bytes(q->ne[0], q->ne[1], q->ne[2], k_pool->ne[2], max_len, page_size);
 }
 
-int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
-                        const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
-                        float scale, gq_tensor* dst, void* workspace, size_t workspace_bytes, gq_stream_t stream) {
+static int flash_attn_paged_impl(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
+                                 const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size,
+                                 int64_t max_len, float scale, gq_tensor* dst, uint8_t* out_q8, void* workspace,
+                                 size_t workspace_bytes, gq_stream_t stream) {
     if (!q || !k_pool || !v_pool || !page_table || !seq_len || !dst)
         return fail(GQ_ERR_INVALID, "flash_attn_paged: null tensor");
     if (q->type != GQ_TYPE_F32 || k_pool->type != GQ_TYPE_F16 || v_pool->type != GQ_TYPE_F16 ||
@@ -817,7 +859,30 @@ int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_te
     a.dst = static_cast<float*>(dst->data);
     PagedKv pg{static_cast<const int32_t*>(seq_len->data), static_cast<const int32_t*>(page_table->data),
                (int64_t)(page_table->nb[1] / 4), lp, (int)B};
-    return attention_paged(a, pg, max_len, workspace, workspace_bytes, (hipStream_t)stream);
+    if (out_q8) {
+        if (!attention_paged_q8_ok(D, B, Hq, Hkv, max_len, page_size))
+            return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged_q8: needs B <= 16, 5..16 q heads per kv head on pages "
+                                            "of a multiple of 128 rows and max_len > 128");
+        if ((reinterpret_cast<uintptr_t>(out_q8) & 15) != 0)
+            return fail(GQ_ERR_INVALID, "flash_attn_paged_q8: out_q8 must be 16-byte aligned");
+    }
+    return attention_paged(a, pg, max_len, workspace, workspace_bytes, (hipStream_t)stream, out_q8);
+}
+
+int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
+                        const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
+                        float scale, gq_tensor* dst, void* workspace, size_t workspace_bytes, gq_stream_t stream) {
+    return flash_attn_paged_impl(q, k_pool, v_pool, page_table, seq_len, page_size, max_len, scale, dst, nullptr,
+                                 workspace, workspace_bytes, stream);
+}
+
+int gq_flash_attn_paged_q8(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
+                           const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
+                           float scale, gq_tensor* dst, void* out_q8, void* workspace, size_t workspace_bytes,
+                           gq_stream_t stream) {
+    if (!out_q8) return fail(GQ_ERR_INVALID, "flash_attn_paged_q8: null out_q8");
+    return flash_attn_paged_impl(q, k_pool, v_pool, page_table, seq_len, page_size, max_len, scale, dst,
+                                 static_cast<uint8_t*>(out_q8), workspace, workspace_bytes, stream);
 }
 
 int gq_paged_step_inputs(const int32_t* pos, int64_t B, const gq_tensor* page_table, int64_t page_size,

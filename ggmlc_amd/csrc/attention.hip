@@ -1135,10 +1135,16 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps
 // With `len` (paged batches), query vector qv belongs to sequence qv / G and only its
 // first cdiv(len, rps) splits hold partials (the splits past a sequence's length are not
 // computed); without it every split does.
+// With q8 (batched decode, NQ / G <= 16 sequences), the output rows are also written
+// quantized for the output projection: row i (Hq * D values) in quant blocks of 32
+// dims, each inside one half wave (the amax and block sum by xor shuffles), with
+// quantize_row_q8_0's rule as quant8_block, into the int8 activation layout of
+// act_prep_i8 (quants at (j * 16 + i) * 32, scale and block sum after all the quants).
 template <int D>
 __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part, int n_split, int Hkv, int NQ,
                                                   int G, int64_t Hq, float* __restrict__ dst,
-                                                  const int32_t* __restrict__ len = nullptr, int rps = 1) {
+                                                  const int32_t* __restrict__ len = nullptr, int rps = 1,
+                                                  uint8_t* __restrict__ q8 = nullptr) {
     __shared__ float sW[MAX_SPLIT];
     __shared__ float sRed[D / 64 > 0 ? D / 64 : 1];
     const int qv = blockIdx.x;
@@ -1171,7 +1177,26 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
     }
     const int64_t h = (int64_t)hk * G + qv % G;
     const int64_t i = qv / G;
-    dst[(i * Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
+    const float o = L == 0.0f ? 0.0f : acc / L;
+    dst[(i * Hq + h) * D + d] = o;
+    if (!q8) return;
+    float amax = fabsf(o);
+#pragma unroll
+    for (int k = 1; k < 32; k <<= 1) amax = fmaxf(amax, __shfl_xor(amax, k, 64));
+    const float dq = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    int q = (int)__builtin_rintf(o * id);
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    int qs = q;
+#pragma unroll
+    for (int k = 1; k < 32; k <<= 1) qs += __shfl_xor(qs, k, 64);
+    const int64_t nbq = Hq * D / 32;                  // quant blocks of a row
+    const int64_t e = ((h * D + d) / 32) * 16 + i;  // (block, row)
+    q8[e * 32 + (d & 31)] = (uint8_t)(q & 0xff);
+    if ((d & 31) == 0) {
+        *reinterpret_cast<float*>(q8 + nbq * 512 + e * 4) = h2f(f2h(dq));
+        *reinterpret_cast<int*>(q8 + nbq * 576 + e * 4) = qs;
+    }
 }
 
 __global__ void k_attn_reset_counters() {
@@ -1179,14 +1204,15 @@ __global__ void k_attn_reset_counters() {
     if (i < ARRIVE_N) g_attn_arrive[i] = 0u;
 }
 
-// the split merge (len, rps: the paged launches' per-sequence split counts)
+// the split merge (len, rps: the paged launches' per-sequence split counts; q8: the
+// quantized output rows)
 int launch_merge(int64_t D, const float* part, int ns, int Hkv, int NQ, int G, int64_t Hq, float* dst,
-                 const int32_t* len, int rps, hipStream_t s) {
+                 const int32_t* len, int rps, hipStream_t s, uint8_t* q8 = nullptr) {
     const dim3 g2((unsigned)NQ, (unsigned)Hkv);
     if (D == 128)
-        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps);
+        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8);
     else
-        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps);
+        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8);
     return check_hip(hipGetLastError(), "attention merge launch");
 }
 
@@ -1301,6 +1327,12 @@ PagedPlan paged_plan(int64_t D, int64_t B, int64_t G, int64_t Hkv, int64_t max_l
 
 }  // namespace
 
+bool attention_paged_q8_ok(int64_t D, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t page) {
+    if (Hkv <= 0 || Hq % Hkv || B > GEMM_I8_MAX_M) return false;
+    const PagedPlan p = paged_plan(D, B, Hq / Hkv, Hkv, max_len, page);
+    return p.u < 0 && p.n_split > 1;
+}
+
 size_t attn_paged_workspace_bytes(int64_t D, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t page) {
     if (Hkv <= 0 || Hq % Hkv) return 0;
     const PagedPlan p = paged_plan(D, B, Hq / Hkv, Hkv, max_len, page);
@@ -1308,7 +1340,8 @@ size_t attn_paged_workspace_bytes(int64_t D, int64_t B, int64_t Hq, int64_t Hkv,
     return (size_t)p.n_split * Hkv * B * (Hq / Hkv) * (D + 2) * sizeof(float);
 }
 
-int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void* ws, size_t ws_bytes, hipStream_t s) {
+int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void* ws, size_t ws_bytes, hipStream_t s,
+                    uint8_t* q8) {
     const int64_t G = a.Hq / a.Hkv, page = (int64_t)1 << pg.log2p;
     const PagedPlan p = paged_plan(a.D, pg.B, G, a.Hkv, max_len, page);
     if (p.u == 0) return fail(GQ_ERR_INVALID, "flash_attn_paged: page size must be a multiple of 64 rows (128 for D = 64)");
@@ -1327,7 +1360,7 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
             hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, nq, ns, part, pg);
         int rc = check_hip(hipGetLastError(), "flash_attn_paged (mfma) launch");
         if (rc != GQ_OK || p.n_split == 1) return rc;
-        return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, pg.len, 128, s);
+        return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, pg.len, 128, s, q8);
     }
     const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);
     const int fuse = fused_merge ? 1 : 0;

@@ -26,7 +26,10 @@
 #include <algorithm>
 
 #include "common.h"
+#include "epilogue.h"
 #include "kernels.h"
+
+#pragma clang fp contract(off)
 
 namespace gq {
 
@@ -47,11 +50,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t by
                                              (int)__builtin_amdgcn_readfirstlane(n), 0x00020000);
 }
 
-template <int QT, int KS>
+// Epilogues (template EPI, the I8Epi fusions): plain (+ bias), ROPE + SET_ROWS of a fused
+// QKV product, SWIGLU, SWIGLU + the next product's quantized rows. The paired ones read
+// logical rows (pair_row): lane l's 4 rows 4 (l / 16) .. + 3 are two whole pairs.
+enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_GLU = 2, EPI_GLU_Q8 = 3 };
+
+// ORD (KS == 1): the wave sums its K steps in the order of an ORD-part split (part k's
+// steps into their own sum, the parts added in part order), so a launch that needs whole
+// tiles per workgroup gives the bits of the plan's split launch of the same product.
+template <int QT, int KS, int EPI, int ORD = 1>
 __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                     int64_t row_bytes, const uint8_t* __restrict__ act, int64_t M,
                                                     float* __restrict__ dst, int64_t ldd,
-                                                    const float* __restrict__ bias) {
+                                                    const float* __restrict__ bias, I8Epi epi) {
+    static_assert(EPI != EPI_GLU_Q8 || KS == 1, "the quantized SWIGLU rows need 4 whole tiles per workgroup");
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int RB = NBS * BB;           // bytes of a row per step: 272 / 144
     constexpr int CPR = RB / 16;           // 16-byte chunks of a row per step: 17 / 9
@@ -71,10 +83,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
     const int sp = (nsteps + KS - 1) / KS;
     const int s0 = min(nsteps, kp * sp), s1 = min(nsteps, s0 + sp);
 
-    // the tile's rows of W (rows past N, or a whole tile past N, read 0 without a fetch)
+    // the tile's rows of W (rows past N, or a whole tile past N, read 0 without a fetch);
+    // paired epilogues: logical row n0 + r is physical row pair_row(n0 + r), the smallest
+    // of them pair_row(n0) (N % 16 == 0: tiles are whole)
+    constexpr bool PAIRED = EPI != EPI_PLAIN;
     const int64_t rows = N - n0;
-    const __amdgpu_buffer_rsrc_t wrs =
-        rsrc(W + (rows > 0 ? n0 : 0) * row_bytes, rows > 0 ? std::min<int64_t>(rows, 16) * row_bytes : 0);
+    const int64_t pbase = PAIRED && rows > 0 ? pair_row(epi.pair_lo, epi.pair_h, n0) : (rows > 0 ? n0 : 0);
+    const int64_t wbytes = rows <= 0 ? 0 : (PAIRED ? (N - pbase) * row_bytes : std::min<int64_t>(rows, 16) * row_bytes);
+    const __amdgpu_buffer_rsrc_t wrs = rsrc(W + pbase * row_bytes, wbytes);
     // activation workspace: quants [nb][16][32] int8, scales [nb][16] f32, block sums [nb][16] i32
     const __amdgpu_buffer_rsrc_t qrs = rsrc(act, (int64_t)nb * 512);
     const __amdgpu_buffer_rsrc_t drs = rsrc(act + (int64_t)nb * 512, (int64_t)nb * 64);
@@ -87,7 +103,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
     for (int i = 0; i < LPL; ++i) {
         const int c = lane + 64 * i;
         cval[i] = c < CPW;
-        coff[i] = cval[i] ? (uint32_t)((c / CPR) * row_bytes + (c % CPR) * 16) : 0u;
+        const int64_t prow = PAIRED ? pair_row(epi.pair_lo, epi.pair_h, n0 + c / CPR) - pbase : c / CPR;
+        coff[i] = cval[i] ? (uint32_t)(prow * row_bytes + (c % CPR) * 16) : 0u;
     }
 
     uint4 wb[2][LPL];
@@ -163,16 +180,54 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
         issue_a(s + 2, slot);
     };
 
+    static_assert(ORD == 1 || KS == 1, "the emulated split is for one-part launches");
+    float part[ORD][4];
+#pragma unroll
+    for (int k = 0; k < ORD; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[k][r] = 0.0f;
+    const int spo = (nsteps + ORD - 1) / ORD;  // steps per part of the emulated split
+    auto fold = [&](int st) {  // entering step st: the previous part's sum is complete
+        if constexpr (ORD > 1) {
+#pragma unroll
+            for (int k = 1; k < ORD; ++k)
+                if (st == k * spo) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) part[k - 1][r] = acc[r], acc[r] = 0.0f;
+                }
+        }
+    };
+
     issue_w(s0, 0);
     issue_a(s0, 0);
     issue_w(s0 + 1, 1);
     issue_a(s0 + 1, 1);
     int s = s0;
     for (; s + 1 < s1; s += 2) {
+        fold(s);
         body(s, 0);
+        fold(s + 1);
         body(s + 1, 1);
     }
-    if (s < s1) body(s, 0);
+    if (s < s1) {
+        fold(s);
+        body(s, 0);
+    }
+    if constexpr (ORD > 1) {  // the last part's sum, then the parts in order (empty ones 0)
+        const int kl = (s1 - 1) / spo;
+#pragma unroll
+        for (int k = 0; k < ORD; ++k)
+            if (k == kl) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) part[k][r] = acc[r];
+            }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            acc[r] = part[0][r];
+#pragma unroll
+            for (int k = 1; k < ORD; ++k) acc[r] += part[k][r];
+        }
+    }
 
     if constexpr (KS > 1) {
 #pragma unroll
@@ -185,27 +240,133 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
             for (int r = 0; r < 4; ++r) acc[r] += s_red[wave + k][lane][r];
     }
     const int64_t m = lr;  // activation row
-    if (m >= M) return;
+    if constexpr (EPI == EPI_PLAIN) {
+        if (m >= M) return;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t n = n0 + 4 * g + r;
-        if (n < N) dst[m * ldd + n] = bias ? acc[r] + bias[n] : acc[r];
+        for (int r = 0; r < 4; ++r) {
+            const int64_t n = n0 + 4 * g + r;
+            if (n < N) dst[m * ldd + n] = bias ? acc[r] + bias[n] : acc[r];
+        }
+    } else {
+        // the lane's two pairs: logical rows (row, row + 1), row = n0 + 4 g + 2 p; the bias is
+        // added to the product first, at the physical rows (v + bias: ADD(MUL_MAT, bias))
+        float v[2], vp[2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int64_t row = n0 + 4 * g + 2 * p;
+            v[p] = acc[2 * p];
+            vp[p] = acc[2 * p + 1];
+            if (bias && n0 < N) {
+                v[p] = v[p] + bias[pair_row(epi.pair_lo, epi.pair_h, row)];
+                vp[p] = vp[p] + bias[pair_row(epi.pair_lo, epi.pair_h, row + 1)];
+            }
+        }
+        if constexpr (EPI == EPI_ROPE) {
+            if (m >= M || n0 >= N) return;
+            const GemvRope& r = epi.rp;
+            const int64_t kv = r.idx[m];
+            auto cs = [&](int c) {
+                if (r.cache) return *reinterpret_cast<const float2*>(reinterpret_cast<const uint8_t*>(r.cache) +
+                                                                     m * r.cache_nb1 + (int64_t)c * 8);
+                float co, si;
+                rope_cs((float)r.pos[m], c, r.theta_scale, r.freq_scale, r.attn_factor, co, si);
+                return make_float2(co, si);
+            };
+#pragma unroll
+            for (int p = 0; p < 2; ++p) rope_store(r, (int)m, kv, n0 + 4 * g + 2 * p, v[p], vp[p], cs);
+        } else {
+            float u[2];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) u[p] = swiglu_f(v[p], vp[p]);
+            if (dst && m < M && n0 < N) {
+#pragma unroll
+                for (int p = 0; p < 2; ++p) dst[m * ldd + (n0 >> 1) + 2 * g + p] = u[p];
+            }
+            if constexpr (EPI == EPI_GLU_Q8) {
+                // one quant block per workgroup: SWIGLU outputs 32 b .. + 31 (b = blockIdx.x)
+                // of every activation row, 8 per wave, 2 per lane (rows of the same m sit in
+                // lanes lr, lr + 16, lr + 32, lr + 48 of each wave); quantize_row_q8_0's rule
+                // on the block max and the exact integer block sum, as quant8_block
+                __shared__ float s_amax[4][16];
+                __shared__ int s_isum[4][16];
+                float a = fmaxf(fabsf(u[0]), fabsf(u[1]));
+                a = fmaxf(a, __shfl_xor(a, 16, 64));
+                a = fmaxf(a, __shfl_xor(a, 32, 64));
+                if (g == 0) s_amax[wave][lr] = a;
+                __syncthreads();
+                float amax = s_amax[0][lr];
+#pragma unroll
+                for (int w = 1; w < 4; ++w) amax = fmaxf(amax, s_amax[w][lr]);
+                const float d = amax / 127.0f;
+                const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+                int q[2];
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const int iv = (int)__builtin_rintf(u[p] * id);
+                    q[p] = iv > 127 ? 127 : (iv < -128 ? -128 : iv);
+                }
+                int is = q[0] + q[1];
+                is += __shfl_xor(is, 16, 64);
+                is += __shfl_xor(is, 32, 64);
+                if (g == 0) s_isum[wave][lr] = is;
+                __syncthreads();
+                if (m >= M || n0 >= N) return;
+                const int64_t nbq = N / 64;  // blocks of the quantized rows (K = N / 2)
+                const int64_t e = (int64_t)blockIdx.x * 16 + m;  // (block, activation row)
+                *reinterpret_cast<uint16_t*>(epi.q8 + e * 32 + 8 * wave + 2 * g) =
+                    (uint16_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8));
+                if (wave == 0 && g == 0) {
+                    int isum = s_isum[0][lr];
+#pragma unroll
+                    for (int w = 1; w < 4; ++w) isum += s_isum[w][lr];
+                    *reinterpret_cast<float*>(epi.q8 + nbq * 512 + e * 4) = h2f(f2h(d));
+                    *reinterpret_cast<int*>(epi.q8 + nbq * 576 + e * 4) = isum;
+                }
+            }
+        }
     }
+}
+
+template <int QT, int EPI>
+int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst, int64_t ldd,
+               hipStream_t s, const float* bias, const I8Epi& e) {
+    const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
+    const GemmI8Plan p = gemm_i8_plan(N, K);
+    if constexpr (EPI == EPI_GLU_Q8) {  // one quant block (64 logical rows) per workgroup,
+        // summed in the order of the plan's split (the bits of the unfused product)
+        const dim3 g((unsigned)(N / 64));
+        if (p.ks == 4)
+            hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, 4>), g, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd,
+                               bias, e);
+        else if (p.ks == 2)
+            hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, 2>), g, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd,
+                               bias, e);
+        else
+            hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, 1>), g, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd,
+                               bias, e);
+        return check_hip(hipGetLastError(), "gemm_i8 launch");
+    }
+    const dim3 grid((unsigned)p.wgs);
+    if (p.ks == 4)
+        hipLaunchKernelGGL((k_gemm_i8<QT, 4, EPI == EPI_GLU_Q8 ? EPI_GLU : EPI>), grid, dim3(256), 0, s, W, N, K,
+                           row_bytes, act, M, dst, ldd, bias, e);
+    else if (p.ks == 2)
+        hipLaunchKernelGGL((k_gemm_i8<QT, 2, EPI == EPI_GLU_Q8 ? EPI_GLU : EPI>), grid, dim3(256), 0, s, W, N, K,
+                           row_bytes, act, M, dst, ldd, bias, e);
+    else
+        hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI>), grid, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd,
+                           bias, e);
+    return check_hip(hipGetLastError(), "gemm_i8 launch");
 }
 
 template <int QT>
 int launch(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst, int64_t ldd,
-           hipStream_t s, const float* bias) {
-    const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
-    const GemmI8Plan p = gemm_i8_plan(N, K);
-    const dim3 grid((unsigned)p.wgs);
-    if (p.ks == 4)
-        hipLaunchKernelGGL((k_gemm_i8<QT, 4>), grid, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd, bias);
-    else if (p.ks == 2)
-        hipLaunchKernelGGL((k_gemm_i8<QT, 2>), grid, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd, bias);
-    else
-        hipLaunchKernelGGL((k_gemm_i8<QT, 1>), grid, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd, bias);
-    return check_hip(hipGetLastError(), "gemm_i8 launch");
+           hipStream_t s, const float* bias, const I8Epi* e) {
+    const I8Epi none{};
+    if (!e || (!e->rope && !e->glu)) return launch_epi<QT, EPI_PLAIN>(W, N, K, act, M, dst, ldd, s, bias, none);
+    if (e->rope) return launch_epi<QT, EPI_ROPE>(W, N, K, act, M, dst, ldd, s, bias, *e);
+    if (e->q8) return launch_epi<QT, EPI_GLU_Q8>(W, N, K, act, M, dst, ldd, s, bias, *e);
+    return launch_epi<QT, EPI_GLU>(W, N, K, act, M, dst, ldd, s, bias, *e);
 }
 
 }  // namespace
@@ -224,13 +385,23 @@ GemmI8Plan gemm_i8_plan(int64_t N, int64_t K) {
 }
 
 int gemm_i8(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst,
-            int64_t ldd, hipStream_t s, const float* bias) {
+            int64_t ldd, hipStream_t s, const float* bias, const I8Epi* epi) {
     if (K % GEMM_I8_K_ALIGN != 0 || M < 1 || M > GEMM_I8_MAX_M)
         return fail(GQ_ERR_INVALID, "gemm_i8: needs K % 256 == 0 and 1 <= M <= 16");
     if ((reinterpret_cast<uintptr_t>(W) & 15) != 0 || (reinterpret_cast<uintptr_t>(act) & 15) != 0)
         return fail(GQ_ERR_INVALID, "gemm_i8: weight and activation must be 16-byte aligned");
-    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, act, M, dst, ldd, s, bias);
-    return launch<GQ_TYPE_Q4_0>(W, N, K, act, M, dst, ldd, s, bias);
+    if (epi && (epi->rope || epi->glu)) {
+        const int64_t row_bytes = (K / QK) * (type == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
+        if (N % (epi->glu && epi->q8 ? 64 : 16) != 0)
+            return fail(GQ_ERR_UNSUPPORTED, "gemm_i8: paired epilogues need N % 16 == 0 (64 with quantized rows)");
+        if (N * row_bytes > 0x7fffffffLL) return fail(GQ_ERR_UNSUPPORTED, "gemm_i8: paired epilogues need < 2 GiB weights");
+        if (epi->rope && epi->pair_lo != 0 && (epi->pair_lo + 1) % 16 != 0)
+            return fail(GQ_ERR_UNSUPPORTED, "gemm_i8: NEOX rope epilogue needs head_dim % 16 == 0");
+        if (epi->q8 && (reinterpret_cast<uintptr_t>(epi->q8) & 15) != 0)
+            return fail(GQ_ERR_INVALID, "gemm_i8: quantized rows must be 16-byte aligned");
+    }
+    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, act, M, dst, ldd, s, bias, epi);
+    return launch<GQ_TYPE_Q4_0>(W, N, K, act, M, dst, ldd, s, bias, epi);
 }
 
 }  // namespace gq

@@ -29,6 +29,7 @@
 #include <unordered_map>
 
 #include "common.h"
+#include "epilogue.h"
 #include "kernels.h"
 
 #pragma clang fp contract(off)
@@ -123,12 +124,10 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Physical weight row of logical row r. Paired epilogues (SWIGLU, rope) need the two
-// rows of a pair in one wave (rows of a wave are 4 consecutive logical rows), so
-// logical rows 2c, 2c+1 of a pair block read the physical rows of the pair.
+// Physical weight row of logical row r (pair_row: rows of a wave are 4 consecutive logical
+// rows, so both rows of a SWIGLU / rope pair land in one wave)
 __device__ __forceinline__ int64_t phys_row(const GemvFuse& fz, int64_t r) {
-    if (fz.pair_lo == 0) return r;
-    return (r & ~fz.pair_lo) + ((r & fz.pair_lo) >> 1) + (r & 1) * fz.pair_h;
+    return pair_row(fz.pair_lo, fz.pair_h, r);
 }
 
 // (cos, sin) of every rotated pair of the M positions (tab[m * n_dims/2 + j]) and
@@ -210,40 +209,12 @@ __device__ __forceinline__ void rope_table(const GemvFuse& fz, const RopeIn<M>& 
     }
 }
 
-// Rope epilogue of a fused QKV product, from the even logical row of a pair (v0, v1:
-// the pair's two dims i0, i1 of head `head`): the work of k_rope_kv for those dims
-// with the same arithmetic (q rotated into qo; k rotated, v copied, both rounded
-// to fp16 into cache row idx[m]; bad rows counted once per token and kv head).
+// Rope epilogue from the LDS table: (cos, sin) of row m's pairs and its cache row
 template <int M>
 __device__ __forceinline__ void rope_emit(const GemvRope& r, const float2* tab, int m, int64_t row, float v0,
                                           float v1) {
-    const int64_t head = row >> r.hd_log2;
-    const int c = (int)((row & (r.hd - 1)) >> 1);
-    const int i0 = r.neox ? c : 2 * c;
-    const int i1 = r.neox ? c + (int)(r.hd >> 1) : 2 * c + 1;
-    float y0 = v0, y1 = v1;
-    if (head < r.Hq + r.Hkv && 2 * c < r.n_dims) {
-        const float2 cs = tab[m * (r.n_dims >> 1) + c];
-        rope_rotate(cs.x, cs.y, v0, v1, y0, y1);
-    }
-    if (head < r.Hq) {
-        float* q = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(r.qo) + m * r.qonb2 + head * r.qonb1);
-        q[i0] = y0;
-        q[i1] = y1;
-        return;
-    }
     const int64_t kv = reinterpret_cast<const int64_t*>(tab + M * (r.n_dims >> 1))[m];
-    if (kv < 0 || kv >= r.rows) {
-        if (c == 0 && r.n_bad) atomicAdd(r.n_bad, 1);
-        return;
-    }
-    const bool is_k = head < r.Hq + r.Hkv;
-    uint16_t* y = is_k ? reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(r.kc) + kv * r.kcnb1 +
-                                                      (head - r.Hq) * r.kcnb2)
-                       : reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(r.vc) + kv * r.vcnb1 +
-                                                      (head - r.Hq - r.Hkv) * r.vcnb2);
-    y[i0] = f2h(y0);
-    y[i1] = f2h(y1);
+    rope_store(r, m, kv, row, v0, v1, [&](int c) { return tab[m * (r.n_dims >> 1) + c]; });
 }
 
 // Write logical row `row` of activation m: plain, residual-added (res + v: the

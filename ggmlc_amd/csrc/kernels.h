@@ -109,8 +109,19 @@ struct GemmI8Plan {
     int64_t wgs;
 };
 GemmI8Plan gemm_i8_plan(int64_t N, int64_t K);
+// Output-side fusions of gemm_i8 (the GEMV's, on the same logical row pairs: pair_row):
+//   rope: ROPE + SET_ROWS of a fused QKV product (rp; dst unused), N % 16 == 0;
+//   glu: SWIGLU of the pairs (gate row c, up row c + N/2) into dst[m * ldd + c] (dst may be
+//     null), N % 64 == 0; with q8, also those rows quantized (quantize_row_q8_0) into q8 in
+//     act_prep_i8's layout for K = N/2 — what the next product's prologue would write.
+struct I8Epi {
+    int rope = 0, glu = 0;
+    int64_t pair_lo = 0, pair_h = 0;
+    GemvRope rp{};
+    uint8_t* q8 = nullptr;
+};
 int gemm_i8(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst,
-            int64_t ldd, hipStream_t s, const float* bias = nullptr);
+            int64_t ldd, hipStream_t s, const float* bias = nullptr, const I8Epi* epi = nullptr);
 
 // set_rows.hip
 struct SetRowsArgs {
@@ -163,7 +174,12 @@ struct PagedKv {
 // a.q: [B][Hq][D] rows (qnb1 = sequence stride, qnb2 = head stride), a.n_kv = pool rows,
 // a.dst [B][Hq][D]; max_len bounds every len[b] (sizes the grid)
 size_t attn_paged_workspace_bytes(int64_t D, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t page);
-int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void* ws, size_t ws_bytes, hipStream_t s);
+// q8: with the matrix-core kernel and a split merge (B <= 16), the output rows also
+// quantized in act_prep_i8's layout (K = Hq * D) by the merge; ignored otherwise
+int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void* ws, size_t ws_bytes, hipStream_t s,
+                    uint8_t* q8 = nullptr);
+// whether attention_paged with q8 writes it: the matrix-core kernel with a split merge
+bool attention_paged_q8_ok(int64_t D, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t page);
 
 // softmax.hip
 struct SoftmaxArgs {

@@ -169,21 +169,44 @@ def _linear(wt: ops.QWeight, bias: torch.Tensor | None, x: torch.Tensor, out: to
     return ops.add(y, bias, out=y) if bias is not None else y
 
 
+def q8_chain_ok(w: ModelWeights) -> bool:
+    """Whether every product of a layer can take the int8 path with the quantized-row
+    handoffs (K % 256 == 0, 16-byte aligned weights, gate|up rows % 64, QKV rows % 16,
+    a power-of-two head_dim >= 16): see forward's q8 mode."""
+    c = w.cfg
+    hd = c.head_dim
+    if hd < 16 or hd & (hd - 1):
+        return False
+    for L in w.layers:
+        for wt in (L.qkv, L.o, L.gate_up, L.down):
+            if wt.K % 256 or wt.data.data_ptr() % 16:
+                return False
+        if L.gate_up.N % 64 or L.qkv.N % 16:
+            return False
+    return True
+
+
 def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, v_cache: list, attend, fused: bool,
-            rec, ws: ops.Workspace, out: torch.Tensor, r0: int) -> torch.Tensor:
+            rec, ws: ops.Workspace, out: torch.Tensor, r0: int, q8: bool = False) -> torch.Tensor:
     """The layer stack of one step over s rows: embedding -> layers -> RMS_NORM -> lm_head
     logits of rows [r0, s) into `out`. b holds the step's buffers, with pos_ids (int32 [s])
     and kv_idx (int64 [s]) already filled: row i is rotated at pos_ids[i] and its K/V rows
     are stored at row kv_idx[i] of k_cache[l] / v_cache[l] ([1, Hkv, rows, hd] fp16).
     attend(l, q) returns the attention output [s, Hq, hd] of layer l for the rotated q
     ([1, s, Hq, hd]); the caller picks what the rows attend to (one sequence's cache with
-    its causal mask, or each row its own sequence's pages)."""
+    its causal mask, or each row its own sequence's pages).
+    q8 (5..16 rows, q8_chain_ok, attend(l, q, out_q8) writing the rows quantized): the
+    int8 path with ROPE + SET_ROWS in the QKV product's epilogue, the attention's split
+    merge quantizing the o projection's input, and gate_up's epilogue writing SWIGLU's
+    rows quantized for down — the quantize steps of the unfused ops moved into their
+    producers (bit-identical), 3 launches fewer per layer."""
     c = w.cfg
     qd, kvd = c.q_dim, c.kv_dim
     # more than 4 rows without a trace: the GEMM path with ADD / RMS_NORM / SWIGLU fused
     # into the prologue that quantizes each GEMM's activation (bit-identical as well)
     pro = not fused and rec.trace is None and s > 4
-    if fused:  # the rope (cos, sin) table of this step's positions, shared by all layers
+    q8 = q8 and pro and s <= 16
+    if fused or q8:  # the rope (cos, sin) table of this step's positions, shared by all layers
         ops.rope_cache(b["pos_ids"], c.head_dim, c.rope_base, out=b["rope_cs"])
     x = b["x"]
     ops.get_rows(w.embed, ids, out=x)
@@ -197,6 +220,14 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, rope_kv=ops.RopeKv(
                 c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2, c.rope_base, b["kv_idx"],
                 b["q"], k_cache[li], v_cache[li], cache=b["rope_cs"]), bias=L.qkv_b)
+            x = nx if nx is not None else x
+            q = b["q"]
+        elif q8:  # ADD + RMS_NORM in the prologue, ROPE + SET_ROWS in the epilogue
+            nx = other[id(x)] if pending is not None else None
+            ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws, bias=L.qkv_b,
+                              rope_kv=ops.RopeKv(c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2,
+                                                 c.rope_base, b["kv_idx"], b["q"], k_cache[li], v_cache[li],
+                                                 cache=b["rope_cs"]))
             x = nx if nx is not None else x
             q = b["q"]
         else:
@@ -225,9 +256,19 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
                 ops.set_rows(k_cache[li], k.permute(0, 2, 1, 3), b["kv_idx"])
                 ops.set_rows(v_cache[li], vv.permute(0, 2, 1, 3), b["kv_idx"])
                 rec("q", li, q), rec("k", li, k), rec("kc", li, k_cache[li]), rec("vc", li, v_cache[li])
-        attend(li, q)
+        if q8:
+            attend(li, q, b["q8_o"])
+        else:
+            attend(li, q)
         rec("attn", li, b["attn"])
-        if fused:
+        if q8:  # o from the merge's quantized rows; SWIGLU's rows quantized for down
+            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], x_q8=b["q8_o"], ws=ws, bias=L.o_b)
+            nx = other[id(x)]
+            ops.mul_mat_fused(L.gate_up, x, rms_eps=c.rms_eps, x_add=o, x_sum=nx, swiglu=True, out_q8=b["q8_d"],
+                              no_out=True, ws=ws, bias=L.gate_up_b)
+            x = nx
+            pending = ops.mul_mat_fused(L.down, b["act"], out=b["proj"], x_q8=b["q8_d"], ws=ws, bias=L.down_b)
+        elif fused:
             o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], bias=L.o_b)
             nx = other[id(x)]
             a = ops.mul_mat_fused(L.gate_up, x, out=b["act"], rms_eps=c.rms_eps, swiglu=True, x_add=o, x_sum=nx,

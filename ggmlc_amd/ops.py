@@ -189,7 +189,8 @@ class RopeKv:
 def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, rms_eps: float | None = None,
                   swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
                   x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None, x_swiglu: bool = False,
-                  ws: Workspace | None = None, bias: torch.Tensor | None = None) -> torch.Tensor | None:
+                  ws: Workspace | None = None, bias: torch.Tensor | None = None, out_q8: torch.Tensor | None = None,
+                  x_q8: torch.Tensor | None = None, no_out: bool = False) -> torch.Tensor | None:
     """MUL_MAT fused with its graph neighbours, bit-identical to the unfused ops:
     x_add -> x + x_add first (stored to x_sum when given); rms_eps -> RMS_NORM;
     x_swiglu -> the input is SWIGLU of x's two halves (x [..., 2K]); swiglu -> SWIGLU of
@@ -197,14 +198,21 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     rope_kv -> the result's q/k/v rows go through :func:`rope_kv_store` instead of
     being written (returns None); bias (fp32 [N]) -> the product + bias before the
     output-side fusions (MUL_MAT's bias ADD). Up to 4 rows run as one GEMV launch; more rows take
-    the GEMM path (input-side fusions only, with the workspace ws)."""
+    the GEMM path (input-side fusions, with the workspace ws); on its int8 path (5..16 rows,
+    K % 256 == 0) also swiglu and rope_kv, plus out_q8 (uint8 [q8_rows_bytes(N / 2)]: with
+    swiglu, the result rows quantized for the next product; no_out: only those) and x_q8
+    (x's rows already quantized, e.g. another product's out_q8: x gives the shape only)."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
     n_out = w.N // 2 if swiglu else w.N
-    if out is None and rope_kv is None:
+    if out is None and rope_kv is None and not no_out:
         out = torch.empty(x.shape[:-1] + (n_out,), dtype=torch.float32, device=x.device)
     f = _lib.gq_mul_mat_fusion()
     f.b_swiglu = 1 if x_swiglu else 0
+    if out_q8 is not None:
+        f.out_q8 = out_q8.data_ptr()
+    if x_q8 is not None:
+        f.b_q8 = x_q8.data_ptr()
     keep = []  # descriptors the fusion struct points at
     if rope_kv is not None:
         r = rope_kv
@@ -233,7 +241,7 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     bd = _desc(bias) if bias is not None else None
     if bd is not None:
         f.bias = ctypes.pointer(bd)
-    od = _desc(out) if out is not None else None
+    od = _desc(out) if out is not None and not no_out else None
     L, wd, xd = _lib.load(), w.desc(), _desc(x)
     need = L.gq_mul_mat_fused_workspace_size(wd, xd, ctypes.byref(f))
     if need:
@@ -274,10 +282,13 @@ def flash_attn_ext(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: torc
 
 def flash_attn_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, page_table: torch.Tensor,
                      seq_len: torch.Tensor, page_size: int, max_len: int, scale: float,
-                     out: torch.Tensor | None = None, ws: Workspace | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, ws: Workspace | None = None,
+                     out_q8: torch.Tensor | None = None) -> torch.Tensor:
     """Batched decode attention over a paged KV pool (gq_flash_attn_paged): q fp32
     ``[Hq, B, D]`` (row b = the new token of sequence b), pools fp16 ``[Hkv, rows, D]``,
-    page_table int32 ``[>= B, max_pages]``, seq_len int32 ``[>= B]``. Returns fp32 ``[B, Hq, D]``."""
+    page_table int32 ``[>= B, max_pages]``, seq_len int32 ``[>= B]``. Returns fp32 ``[B, Hq, D]``.
+    out_q8 (uint8 [q8_rows_bytes(Hq * D)]): also the rows quantized for the output
+    projection (gq_flash_attn_paged_q8; see :func:`paged_q8_ok`)."""
     Hq, B, D = q.shape
     if out is None:
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=q.device)
@@ -285,9 +296,27 @@ def flash_attn_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     qd, kd, vd, od = _desc(q), _desc(k_pool), _desc(v_pool), _desc(out)
     need = L.gq_flash_attn_paged_workspace_size(qd, kd, max_len, page_size)
     ptr, size = _ws(ws).get(need)
-    check(L.gq_flash_attn_paged(qd, kd, vd, _desc(page_table), _desc(seq_len), page_size, max_len, scale, od, ptr,
-                                size, _stream()))
+    if out_q8 is not None:
+        check(L.gq_flash_attn_paged_q8(qd, kd, vd, _desc(page_table), _desc(seq_len), page_size, max_len, scale, od,
+                                       out_q8.data_ptr(), ptr, size, _stream()))
+    else:
+        check(L.gq_flash_attn_paged(qd, kd, vd, _desc(page_table), _desc(seq_len), page_size, max_len, scale, od,
+                                    ptr, size, _stream()))
     return out
+
+
+def q8_rows_bytes(K: int) -> int:
+    """Bytes of up to 16 activation rows of K values quantized for the int8 path
+    (gq_q8_rows_bytes)."""
+    return int(_lib.load().gq_q8_rows_bytes(K))
+
+
+def paged_q8_ok(D: int, B: int, Hq: int, Hkv: int, max_len: int, page_size: int) -> bool:
+    """Whether :func:`flash_attn_paged` can write out_q8 for this launch: B <= 16, 5..16 q
+    heads per kv head, pages of a multiple of 128 rows, max_len > 128 (the library rejects
+    the rest with GQ_ERR_UNSUPPORTED)."""
+    G = Hq // Hkv if Hkv and Hq % Hkv == 0 else 0
+    return (D in (64, 128) and 1 <= B <= 16 and 4 < G <= 16 and page_size % 128 == 0 and max_len > 128)
 
 
 def flash_attn_paged_workspace_size(D: int, B: int, Hq: int, Hkv: int, max_len: int, page_size: int) -> int:

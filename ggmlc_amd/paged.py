@@ -30,7 +30,7 @@ import numpy as np
 import torch
 
 from . import ops
-from .model import Decoder, ModelWeights, _Recorder, forward, pad_kv_len
+from .model import Decoder, ModelWeights, _Recorder, forward, pad_kv_len, q8_chain_ok
 
 FNV_OFFSET = 0xCBF29CE484222325
 FNV_PRIME = 0x100000001B3
@@ -336,6 +336,8 @@ class BatchDecoder:
         self.ws = ops.Workspace(self.dev)
         self._bufs: dict[int, dict[str, torch.Tensor]] = {}
         self.graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
+        self._q8_chain: bool | None = None  # q8_chain_ok(w), computed on the first step
+        self.use_q8 = True  # the int8 path's quantized-row handoffs when they apply (forward's q8)
 
     # -- prefill ----------------------------------------------------------------
     def prefill(self, slot: int, tokens, start: int = 0) -> torch.Tensor:
@@ -397,6 +399,9 @@ class BatchDecoder:
                 "kv_idx": torch.zeros(B, dtype=torch.int64, device=d),
                 "seq_len": torch.zeros(B, dtype=torch.int32, device=d),
                 "rope_cs": torch.zeros((B, c.head_dim), dtype=torch.float32, device=d),
+                # the int8 path's quantized rows: the o projection's input, down's input
+                "q8_o": torch.zeros(ops.q8_rows_bytes(c.q_dim), dtype=torch.uint8, device=d),
+                "q8_d": torch.zeros(ops.q8_rows_bytes(c.n_ff), dtype=torch.uint8, device=d),
             }
         return self._bufs[B]
 
@@ -417,17 +422,21 @@ class BatchDecoder:
             raise ValueError("max_len exceeds the slots' context")
         ws.get(self._ws_need(B, max_len))
         fused = B <= 4 and trace is None
+        if self._q8_chain is None:
+            self._q8_chain = q8_chain_ok(self.w)
+        q8 = (self.use_q8 and not fused and trace is None and 4 < B <= 16 and self._q8_chain and
+              ops.paged_q8_ok(c.head_dim, B, c.n_head, c.n_head_kv, max_len, self.P))
         b["pos_ids"] = self.pos[:B]
         ops.paged_step_inputs(self.pos, self.kv.table, self.P, self.kv.trash_row, b["kv_idx"], b["seq_len"], B=B)
         scale = 1.0 / math.sqrt(c.head_dim)
         table = self.kv.table[:B]
 
-        def attend(li, q):
+        def attend(li, q, out_q8=None):
             return ops.flash_attn_paged(q[0].permute(1, 0, 2), self.kv.k[li][0], self.kv.v[li][0], table,
-                                        b["seq_len"], self.P, max_len, scale, out=b["attn"], ws=ws)
+                                        b["seq_len"], self.P, max_len, scale, out=b["attn"], ws=ws, out_q8=out_q8)
 
         logits = forward(self.w, B, b, b["ids"], self.kv.k, self.kv.v, attend, fused, _Recorder(trace), ws,
-                         b["logits"], 0)
+                         b["logits"], 0, q8=q8)
         ops.argmax(logits, out=b["next"])
         ops.paged_advance(self.pos, B=B)
         return b["next"]

@@ -138,9 +138,18 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  * the GEMM's activation (two launches), plus
  *   b_swiglu: the input is SWIGLU(b) of b's two halves (b ne0 = 2K: the gate|up
  *             product feeding the down projection), excluding rms_norm and b_add;
- * the output-side ones (swiglu, add, rope_kv), rope_kv shapes outside the conditions
- * above and b_swiglu on the GEMV path return GQ_ERR_UNSUPPORTED and the caller runs
- * those ops unfused. The GEMM path takes workspace / workspace_bytes
+ * on the int8 path (5..16 rows, K % 256 == 0, 16-byte aligned weights) swiglu and
+ * rope_kv also run as the product's epilogue (N % 16 == 0) and
+ *   out_q8:   with swiglu, the SWIGLU rows are also written quantized for the next
+ *             product (quantize_row_q8_0, the gq_q8_rows layout below for K = N / 2;
+ *             N % 64 == 0); dst may then be NULL
+ *   b_q8:     b's rows are already quantized in the gq_q8_rows layout (a producer's
+ *             out_q8 or gq_flash_attn_paged_q8): no prologue; b gives the shape only,
+ *             and the input-side fusions are excluded;
+ * add with M > 4, the other output-side fusions off the int8 path, rope_kv shapes
+ * outside the conditions above and b_swiglu on the GEMV path return
+ * GQ_ERR_UNSUPPORTED and the caller runs those ops unfused. The GEMM path takes
+ * workspace / workspace_bytes
  * (gq_mul_mat_fused_workspace_size). The ggml CUDA backend fuses the same neighbours
  * (ADD+RMS_NORM+MUL, MUL_MAT+GLU, MUL_MAT+ADD, ROPE+SET_ROWS) for the same reason:
  * these steps are launch-bound. */
@@ -170,7 +179,17 @@ typedef struct gq_mul_mat_fusion {
     void* workspace;         /* GEMM path: gq_mul_mat_fused_workspace_size bytes, 256-aligned */
     size_t workspace_bytes;
     const gq_tensor* bias;   /* F32 [N, 1, 1, 1] or NULL */
+    void* out_q8;            /* int8 path with swiglu: the quantized SWIGLU rows, or NULL */
+    const void* b_q8;        /* int8 path: b's rows already quantized, or NULL */
 } gq_mul_mat_fusion;
+/* The quantized activation rows of the int8 path (up to 16 rows m of K values, K % 32
+ * == 0; no counterpart in the reference, which quantizes src1 inside each MUL_MAT):
+ * per quant block j of K, the 32 int8 quants of row m at byte (j * 16 + m) * 32, its
+ * scale (fp32 value of the fp16 d) at K / 32 * 512 + (j * 16 + m) * 4 and its block sum
+ * (int32) at K / 32 * 576 + (j * 16 + m) * 4 — the blocks of gq_quantize_row_q8_0
+ * rearranged; gq_q8_rows_bytes(K) bytes, 16-byte aligned.
+ * Rows past M are not written. */
+size_t gq_q8_rows_bytes(int64_t K);
 size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f);
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                      gq_stream_t stream);
@@ -339,6 +358,16 @@ size_t gq_flash_attn_paged_workspace_size(const gq_tensor* q, const gq_tensor* k
 int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
                         const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
                         float scale, gq_tensor* dst, void* workspace, size_t workspace_bytes, gq_stream_t stream);
+/* gq_flash_attn_paged that also writes dst's B rows (Hq * D values each) quantized for
+ * the output projection into out_q8 (the gq_q8_rows layout, K = Hq * D): the prologue of
+ * that projection's MUL_MAT done by the split merge, so the projection can take them
+ * through gq_mul_mat_fusion.b_q8. No counterpart in the reference (one fewer launch per
+ * layer for the batched decode). B <= 16, 5..16 query heads per kv head (the
+ * matrix-core kernel), max_len > 128 (a split merge runs). */
+int gq_flash_attn_paged_q8(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
+                           const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
+                           float scale, gq_tensor* dst, void* out_q8, void* workspace, size_t workspace_bytes,
+                           gq_stream_t stream);
 
 /* Per-slot inputs of a batched decode step from device-resident positions pos[B]
  * (the per-slot set_decode_pos of executor.cpp:1181-1276):

@@ -101,10 +101,28 @@ def test_mul_mat_fused_rejects_without_device(lib):
     need = lib.gq_mul_mat_fused_workspace_size(w, x5, ctypes.byref(f))
     assert need >= 5 * 4096 * 2
     assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(f), None) == -3
-    # output-side fusions are GEMV-only
+    # output-side fusions: the GEMV (M <= 4) and the int8 path (M <= 16, K % 256 == 0,
+    # 16-byte aligned weights: here it needs the workspace of its prologue), not beyond
     g5 = _lib.gq_mul_mat_fusion(0, 0.0, 1, None)
-    assert lib.gq_mul_mat_fused(w, x5, _t(_lib.F32, [32, 5], [4, 128]), ctypes.byref(g5), None) == -2
+    assert lib.gq_mul_mat_fused(w, x5, _t(_lib.F32, [32, 5], [4, 128]), ctypes.byref(g5), None) == -3
+    x17 = _t(_lib.F32, [4096, 17], [4, 16384])
+    assert lib.gq_mul_mat_fused(w, x17, _t(_lib.F32, [32, 17], [4, 128]), ctypes.byref(g5), None) == -2
     assert b"M <= 4" in lib.gq_last_error()
+    # quantized rows in and out: the int8 path only, out_q8 with swiglu, b_q8 without
+    # the input-side fusions
+    q = _lib.gq_mul_mat_fusion()
+    q.out_q8 = 0x1000
+    assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(q), None) == -1
+    q.swiglu = 1
+    assert lib.gq_mul_mat_fused(w, x17, _t(_lib.F32, [32, 17], [4, 128]), ctypes.byref(q), None) == -2
+    bq = _lib.gq_mul_mat_fusion()
+    bq.b_q8, bq.rms_norm, bq.rms_eps = 0x1000, 1, 1e-5
+    assert lib.gq_mul_mat_fused(w, x5, d5, ctypes.byref(bq), None) == -1
+    assert b"b_q8" in lib.gq_last_error()
+    x1 = _t(_lib.F32, [4096, 1], [4, 16384])
+    bq.rms_norm = 0
+    assert lib.gq_mul_mat_fused(w, x1, _t(_lib.F32, [64, 1], [4, 256]), ctypes.byref(bq), None) == -2
+    assert lib.gq_q8_rows_bytes(4096) == 4096 // 32 * 640 and lib.gq_q8_rows_bytes(100) == 0
     # the SWIGLU input needs 2K-wide rows, and only exists on the GEMM path
     s5 = _lib.gq_mul_mat_fusion()
     s5.b_swiglu = 1

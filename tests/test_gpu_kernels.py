@@ -243,12 +243,17 @@ def test_mul_mat_fused_gemm_prologue_bit_identical(qtype, K, N, M, mode):
     (O.Q8_0, 1536, 12, 2, 128, 3, 2, 128),    # Qwen2.5-1.5B QKV (GQA 6), three tokens
     (O.Q8_0, 960, 15, 5, 64, 2, 2, 64),       # SmolLM2 QKV: K = 960, block-wise kernel
     (O.Q4_0, 1024, 4, 2, 128, 4, 0, 96),      # normal rope, partial n_dims, four tokens
+    (O.Q8_0, 1536, 12, 2, 128, 16, 2, 128),   # batch 16: the int8 MFMA GEMM's epilogue, K in parts
+    (O.Q4_0, 1024, 8, 2, 64, 7, 2, 64),       # int8 path, 64-dim NEOX heads, 7 tokens
+    (O.Q4_0, 4096, 32, 32, 128, 5, 0, 128),   # int8 path, normal rope (adjacent pairs), 7B MHA
+    (O.Q8_0, 2048, 4, 2, 128, 9, 0, 96),      # int8 path, normal rope with partial n_dims
 ])
 @pytest.mark.parametrize("cached", [False, True])
 def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_dims, cached):
-    """The QKV GEMV with the rope + KV-store epilogue gives exactly the bits of
-    RMS_NORM -> MUL_MAT -> gq_rope_kv_store (pinned by the decoder-op tests): q_out,
-    both caches (untouched rows included) and the count of out-of-range rows."""
+    """The QKV product with the rope + KV-store epilogue (the GEMV for up to 4 tokens, the
+    int8 MFMA GEMM for 5..16) gives exactly the bits of RMS_NORM -> MUL_MAT ->
+    gq_rope_kv_store (pinned by the decoder-op tests): q_out, both caches (untouched rows
+    included) and the count of out-of-range rows."""
     g = torch.Generator(device=DEV)
     g.manual_seed(K + Hq + M)
     N = (Hq + 2 * Hkv) * hd
@@ -256,7 +261,7 @@ def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_d
     x = torch.randn((M, K), generator=g, device=DEV) * 3.0
     d = torch.randn((M, K), generator=g, device=DEV)
     pos = torch.arange(700, 700 + M, dtype=torch.int32, device=DEV)
-    idx = torch.tensor([5, 63, -1, 64][:M], dtype=torch.int64, device=DEV)
+    idx = torch.tensor(([5, 63, -1, 64] + list(range(6, 60, 4)))[:M], dtype=torch.int64, device=DEV)
     kc1 = torch.randn((1, Hkv, 64, hd), generator=g, device=DEV).half()
     vc1 = torch.randn((1, Hkv, 64, hd), generator=g, device=DEV).half()
     kc2, vc2 = kc1.clone(), vc1.clone()
@@ -293,6 +298,8 @@ def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_d
     (O.Q8_0, 1536, 2048, 16, "gemm"),       # batch 16: int8 MFMA path, K in 4 parts, bias in the store
     (O.Q4_0, 4096, 4096, 5, "gemm"),        # 5 rows: int8 MFMA path
     (O.Q4_0, 4096, 12288, 37, "gemm"),      # prompt rows: GEMM path, bias in the tile store
+    (O.Q8_0, 1536, 17920, 16, "swiglu"),    # batch 16: SWIGLU in the int8 GEMM's epilogue
+    (O.Q4_0, 4096, 22016, 6, "swiglu"),     # 6 rows, Q4_0
 ])
 def test_mul_mat_fused_bias_bit_identical(qtype, K, N, M, epi):
     """MUL_MAT with its bias input (executor.cpp:2436-2445: ADD(MUL_MAT(W, x), b)) fused
@@ -317,7 +324,7 @@ def test_mul_mat_fused_bias_bit_identical(qtype, K, N, M, epi):
     assert torch.equal(got, want), (got - want).abs().max().item()
 
 
-@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("M", [1, 3, 16])
 def test_mul_mat_fused_rope_kv_with_bias_bit_identical(M):
     """Qwen2's q/k/v biases ahead of the rope + KV-store epilogue (the decode QKV launch)."""
     g = torch.Generator(device=DEV)
@@ -342,6 +349,34 @@ def test_mul_mat_fused_rope_kv_with_bias_bit_identical(M):
     assert torch.equal(q1, q2)
     assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
     assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+
+
+@pytest.mark.parametrize("qtype,K,F,M", [
+    (O.Q8_0, 1536, 8960, 16),   # Qwen2.5-1.5B gate_up -> down at batch 16
+    (O.Q8_0, 1536, 8960, 5),
+    (O.Q4_0, 4096, 11008, 9),   # 7B MLP, 9 rows
+])
+def test_swiglu_quantized_rows_feed_down_bit_identical(qtype, K, F, M):
+    """gate_up with SWIGLU in the int8 GEMM's epilogue also writes its rows quantized
+    (out_q8); the down projection reading them (x_q8) gives exactly the bits of
+    MUL_MAT(down, SWIGLU(MUL_MAT(gate_up, RMS_NORM(x)))) run one by one, with and without
+    the fp32 SWIGLU rows written."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + F + M)
+    wgu = ops.quantize_weights(torch.randn((2 * F, K), generator=g, device=DEV) * 0.02, qtype)
+    wd = ops.quantize_weights(torch.randn((K, F), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV) * 3.0
+    bd = torch.randn(K, generator=g, device=DEV) * 0.1
+    act = ops.swiglu(ops.mul_mat(wgu, ops.rms_norm(x, 1e-5)))
+    want = ops.add(ops.mul_mat(wd, act), bd)
+    for no_out in (False, True):
+        q8 = torch.full((ops.q8_rows_bytes(F),), 0x55, dtype=torch.uint8, device=DEV)
+        a = ops.mul_mat_fused(wgu, x, rms_eps=1e-5, swiglu=True, out_q8=q8, no_out=no_out)
+        got = ops.mul_mat_fused(wd, act, x_q8=q8, bias=bd)
+        torch.cuda.synchronize()
+        if not no_out:
+            assert torch.equal(a, act)
+        assert torch.equal(got, want), (got - want).abs().max().item()
 
 
 # --------------------------------------------------------------- set_rows ---

@@ -126,6 +126,51 @@ def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
     assert np.array_equal(sep, out, equal_nan=True)
 
 
+@pytest.mark.parametrize("D,Hq,Hkv,lens,qtype", [
+    (128, 12, 2, [2079, 3260, 1, 0, 652, 1167, 300, 945, 129, 128, 2105, 840, 763, 1452, 3882, 1174], O.Q8_0),
+    (128, 12, 2, [700, 5, 1300, 257, 64, 900], O.Q8_0),
+    (64, 32, 4, [500, 1, 129, 1000, 384], O.Q4_0),   # 8 q heads per kv head, K = 2048
+])
+def test_flash_attn_paged_q8_feeds_o_projection(D, Hq, Hkv, lens, qtype):
+    """gq_flash_attn_paged_q8 writes the same fp32 rows as gq_flash_attn_paged and, from
+    the split merge, those rows quantized for the output projection: the projection
+    reading them (gq_mul_mat_fusion.b_q8) gives exactly the bits of MUL_MAT on the fp32
+    rows (the int8 path's own prologue)."""
+    import torch
+    from ggmlc_amd import ops
+
+    dev = _init()
+    rng = np.random.default_rng(D + Hq + len(lens))
+    P, B = 128, len(lens)
+    npg = [-(-n // P) for n in lens]
+    max_len = max(lens)
+    n_pages = 1 + sum(npg)
+    table = np.full((B, -(-max_len // P)), -1, np.int32)
+    perm = rng.permutation(np.arange(1, n_pages))
+    used = 0
+    for b, n in enumerate(npg):
+        table[b, :n] = perm[used:used + n]
+        used += n
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    k_pool = t(rng.standard_normal((Hkv, n_pages * P, D)).astype(np.float16))
+    v_pool = t(rng.standard_normal((Hkv, n_pages * P, D)).astype(np.float16))
+    q = t(rng.standard_normal((Hq, B, D)).astype(np.float32))
+    tb, sl = t(table), t(np.array(lens, np.int32))
+    scale = 1.0 / math.sqrt(D)
+    assert ops.paged_q8_ok(D, B, Hq, Hkv, max_len, P)
+    want = ops.flash_attn_paged(q, k_pool, v_pool, tb, sl, P, max_len, scale)
+    q8 = torch.full((ops.q8_rows_bytes(Hq * D),), 0x55, dtype=torch.uint8, device=dev)
+    got = ops.flash_attn_paged(q, k_pool, v_pool, tb, sl, P, max_len, scale, out_q8=q8)
+    g = torch.Generator(device=dev)
+    g.manual_seed(B)
+    w = ops.quantize_weights(torch.randn((1536, Hq * D), generator=g, device=dev) * 0.02, qtype)
+    y_want = ops.mul_mat(w, want.view(B, Hq * D))
+    y_got = ops.mul_mat_fused(w, got.view(B, Hq * D), x_q8=q8)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(y_got, y_want), (y_got - y_want).abs().max().item()
+
+
 def test_paged_step_inputs_advance_and_copy():
     import torch
     from ggmlc_amd import ops
@@ -229,6 +274,41 @@ def test_batch_decoder_matches_reference_per_sequence(qtype, B, graphs):
         print(f"step {i}: min cos {min(cs):.7f}")
         tokens = nxt
     assert bd.pos_host[:B].tolist() == [n + n_new for n in lens]
+
+
+@pytest.mark.parametrize("qtype,B", [(O.Q8_0, 8), (O.Q4_0, 5), (O.Q8_0, 16)])
+def test_batch_decoder_q8_chain_bit_identical(qtype, B):
+    """The batched decode step with the quantized-row handoffs (rope in the QKV epilogue,
+    the merge quantizing o's input, gate_up quantizing down's input) gives exactly the
+    logits of the same step through the separate prologue and rope launches."""
+    import torch
+    from ggmlc_amd.paged import BatchDecoder
+
+    cfg = _gqa_cfg(qtype)
+    w, _ = _model(cfg)
+    P, max_ctx = 128, 1024
+    rng = np.random.default_rng(11)
+    lens = [int(n) for n in rng.integers(1, 700, B)]
+    prompts = [rng.integers(0, cfg.n_vocab, n).astype(np.int32) for n in lens]
+    decs = []
+    for use_q8 in (False, True):
+        bd = BatchDecoder(w, max_batch=B, max_ctx=max_ctx, page_size=P)
+        bd.use_q8 = use_q8
+        for b in range(B):
+            bd.kv.alloc_slot(b)
+            bd.kv.ensure_tokens(b, lens[b] + 3)
+            bd.prefill(b, prompts[b])
+        decs.append(bd)
+    tokens = rng.integers(0, cfg.n_vocab, B).astype(np.int32)
+    for i in range(3):
+        outs = []
+        for bd in decs:
+            outs.append(bd.decode(B, tokens, use_graph=i > 0))
+        l0, l1 = (bd._buffers(B)["logits"] for bd in decs)
+        torch.cuda.synchronize()
+        assert torch.equal(l0, l1), (i, (l0 - l1).abs().max().item())
+        assert np.array_equal(outs[0], outs[1])
+        tokens = outs[0]
 
 
 def _near_argmax(tok, ref_logits, dev_frac=0.02):
