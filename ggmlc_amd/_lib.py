@@ -72,6 +72,7 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("bias", ctypes.POINTER(gq_tensor)),
         ("out_q8", ctypes.c_void_p),
         ("b_q8", ctypes.c_void_p),
+        ("int8", ctypes.c_int32),
     ]
 
 

@@ -256,22 +256,36 @@ static int fused_bias(const gq_mul_mat_fusion* f, const MulMatPlan& p, const flo
 }
 
 // b as the product's input: with b_swiglu its rows hold 2K values and the input is
-// SWIGLU of their halves, so the plan sees the first half
+// SWIGLU of their halves, so the plan sees the first half; int8 takes the int8 path for
+// 1..16 rows (also 1..4, where the GEMV is the default)
 static int fused_plan(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f, MulMatPlan& p) {
     if (!f || !a || !b) return fail(GQ_ERR_INVALID, "mul_mat_fused: null argument");
-    if (!f->b_swiglu) return plan_mul_mat(a, b, nullptr, p);
-    if (b->ne[0] != 2 * a->ne[0])
-        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_swiglu needs b rows of 2K values: " + shape(b));
-    gq_tensor h = *b;
-    h.ne[0] = a->ne[0];
-    return plan_mul_mat(a, &h, nullptr, p);
+    int rc;
+    if (!f->b_swiglu) {
+        rc = plan_mul_mat(a, b, nullptr, p);
+    } else {
+        if (b->ne[0] != 2 * a->ne[0])
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: b_swiglu needs b rows of 2K values: " + shape(b));
+        gq_tensor h = *b;
+        h.ne[0] = a->ne[0];
+        rc = plan_mul_mat(a, &h, nullptr, p);
+    }
+    if (rc || !f->int8) return rc;
+    if (p.M > GEMM_I8_MAX_M || p.K % GEMM_I8_K_ALIGN || p.K > PREP_MAX_K ||
+        (reinterpret_cast<uintptr_t>(a->data) & 15) != 0)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: int8 needs at most 16 rows, K % 256 == 0 (K <= 16384) and "
+                                        "16-byte aligned weights");
+    p.use_gemv = false;
+    p.use_i8 = true;
+    p.ws = (gemm_i8_act_bytes(p.K) + 255) & ~(size_t)255;
+    return GQ_OK;
 }
 
 size_t gq_q8_rows_bytes(int64_t K) { return K > 0 && K % QK == 0 ? gemm_i8_act_bytes(K) : 0; }
 
 size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f) {
     MulMatPlan p;
-    if (fused_plan(a, b, f, p) != GQ_OK || p.M <= GEMV_MAX_M) return 0;
+    if (fused_plan(a, b, f, p) != GQ_OK || p.use_gemv) return 0;
     return p.ws;
 }
 
@@ -282,7 +296,9 @@ size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, c
 static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,
                               const MulMatPlan& p, hipStream_t s) {
     const bool i8 = p.use_i8 && (reinterpret_cast<uintptr_t>(a->data) & 15) == 0;
-    if (f->add) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: add needs M <= 4, M = " + std::to_string(p.M));
+    if (f->add)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: add needs the GEMV path (M <= 4, no int8), M = " +
+                                            std::to_string(p.M));
     if ((f->swiglu || f->rope_kv) && !i8)
         return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: swiglu / rope_kv need M <= 4 or the int8 path (M <= 16, "
                                         "K % 256 == 0, 16-byte aligned weights), M = " + std::to_string(p.M));
@@ -381,7 +397,7 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     MulMatPlan p;
     int rc = fused_plan(a, b, f, p);
     if (rc) return rc;
-    if (p.M > GEMV_MAX_M) return mul_mat_fused_gemm(a, b, dst, f, p, (hipStream_t)stream);
+    if (!p.use_gemv) return mul_mat_fused_gemm(a, b, dst, f, p, (hipStream_t)stream);
     if (f->b_swiglu) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: b_swiglu needs M > 4 (use swiglu on the producer)");
     if (f->out_q8 || f->b_q8)
         return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: out_q8 / b_q8 need the int8 path (5..16 rows)");

@@ -195,17 +195,18 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
     attend(l, q) returns the attention output [s, Hq, hd] of layer l for the rotated q
     ([1, s, Hq, hd]); the caller picks what the rows attend to (one sequence's cache with
     its causal mask, or each row its own sequence's pages).
-    q8 (5..16 rows, q8_chain_ok, attend(l, q, out_q8) writing the rows quantized): the
-    int8 path with ROPE + SET_ROWS in the QKV product's epilogue, the attention's split
-    merge quantizing the o projection's input, and gate_up's epilogue writing SWIGLU's
-    rows quantized for down — the quantize steps of the unfused ops moved into their
-    producers (bit-identical), 3 launches fewer per layer."""
+    q8 (up to 16 rows, not fused, q8_chain_ok, attend(l, q, out_q8) writing the rows
+    quantized): every product on the int8 path, with ROPE + SET_ROWS in the QKV product's
+    epilogue, the attention's split merge quantizing the o projection's input, and
+    gate_up's epilogue writing SWIGLU's rows quantized for down — the quantize steps of
+    the unfused ops moved into their producers (bit-identical), 3 launches fewer per
+    layer."""
     c = w.cfg
     qd, kvd = c.q_dim, c.kv_dim
     # more than 4 rows without a trace: the GEMM path with ADD / RMS_NORM / SWIGLU fused
     # into the prologue that quantizes each GEMM's activation (bit-identical as well)
-    pro = not fused and rec.trace is None and s > 4
-    q8 = q8 and pro and s <= 16
+    q8 = q8 and not fused and rec.trace is None and s <= 16
+    pro = not fused and rec.trace is None and (s > 4 or q8)
     if fused or q8:  # the rope (cos, sin) table of this step's positions, shared by all layers
         ops.rope_cache(b["pos_ids"], c.head_dim, c.rope_base, out=b["rope_cs"])
     x = b["x"]
@@ -224,7 +225,7 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             q = b["q"]
         elif q8:  # ADD + RMS_NORM in the prologue, ROPE + SET_ROWS in the epilogue
             nx = other[id(x)] if pending is not None else None
-            ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws, bias=L.qkv_b,
+            ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws, bias=L.qkv_b, int8=True,
                               rope_kv=ops.RopeKv(c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2,
                                                  c.rope_base, b["kv_idx"], b["q"], k_cache[li], v_cache[li],
                                                  cache=b["rope_cs"]))
@@ -262,12 +263,14 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             attend(li, q)
         rec("attn", li, b["attn"])
         if q8:  # o from the merge's quantized rows; SWIGLU's rows quantized for down
-            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], x_q8=b["q8_o"], ws=ws, bias=L.o_b)
+            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], x_q8=b["q8_o"], ws=ws, bias=L.o_b,
+                                  int8=True)
             nx = other[id(x)]
             ops.mul_mat_fused(L.gate_up, x, rms_eps=c.rms_eps, x_add=o, x_sum=nx, swiglu=True, out_q8=b["q8_d"],
-                              no_out=True, ws=ws, bias=L.gate_up_b)
+                              no_out=True, ws=ws, bias=L.gate_up_b, int8=True)
             x = nx
-            pending = ops.mul_mat_fused(L.down, b["act"], out=b["proj"], x_q8=b["q8_d"], ws=ws, bias=L.down_b)
+            pending = ops.mul_mat_fused(L.down, b["act"], out=b["proj"], x_q8=b["q8_d"], ws=ws, bias=L.down_b,
+                                        int8=True)
         elif fused:
             o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], bias=L.o_b)
             nx = other[id(x)]
@@ -297,7 +300,8 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
         rec("x_out", li, x)
     if fused or pro:
         return ops.mul_mat_fused(w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps,
-                                 x_add=pending[r0:] if pending is not None else None, ws=ws)
+                                 x_add=pending[r0:] if pending is not None else None, ws=ws,
+                                 int8=q8 and w.lm_head.K % 256 == 0 and w.lm_head.data.data_ptr() % 16 == 0)
     h = ops.rms_norm(x[r0:], c.rms_eps, out=b["h"][:s - r0])
     rec("hf", -1, h)
     return ops.mul_mat(w.lm_head, h, out=out, ws=ws)

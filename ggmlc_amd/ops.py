@@ -190,7 +190,7 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
                   swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
                   x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None, x_swiglu: bool = False,
                   ws: Workspace | None = None, bias: torch.Tensor | None = None, out_q8: torch.Tensor | None = None,
-                  x_q8: torch.Tensor | None = None, no_out: bool = False) -> torch.Tensor | None:
+                  x_q8: torch.Tensor | None = None, no_out: bool = False, int8: bool = False) -> torch.Tensor | None:
     """MUL_MAT fused with its graph neighbours, bit-identical to the unfused ops:
     x_add -> x + x_add first (stored to x_sum when given); rms_eps -> RMS_NORM;
     x_swiglu -> the input is SWIGLU of x's two halves (x [..., 2K]); swiglu -> SWIGLU of
@@ -201,7 +201,8 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     the GEMM path (input-side fusions, with the workspace ws); on its int8 path (5..16 rows,
     K % 256 == 0) also swiglu and rope_kv, plus out_q8 (uint8 [q8_rows_bytes(N / 2)]: with
     swiglu, the result rows quantized for the next product; no_out: only those) and x_q8
-    (x's rows already quantized, e.g. another product's out_q8: x gives the shape only)."""
+    (x's rows already quantized, e.g. another product's out_q8: x gives the shape only);
+    int8 -> the int8 path also for 1..4 rows."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
     n_out = w.N // 2 if swiglu else w.N
@@ -213,6 +214,7 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
         f.out_q8 = out_q8.data_ptr()
     if x_q8 is not None:
         f.b_q8 = x_q8.data_ptr()
+    f.int8 = 1 if int8 else 0
     keep = []  # descriptors the fusion struct points at
     if rope_kv is not None:
         r = rope_kv

@@ -421,11 +421,13 @@ class BatchDecoder:
         if max_len > self.max_ctx:
             raise ValueError("max_len exceeds the slots' context")
         ws.get(self._ws_need(B, max_len))
-        fused = B <= 4 and trace is None
         if self._q8_chain is None:
             self._q8_chain = q8_chain_ok(self.w)
-        q8 = (self.use_q8 and not fused and trace is None and 4 < B <= 16 and self._q8_chain and
+        # 3..16 slots: the int8 chain with the quantized-row handoffs where it applies
+        # (1 and 2 rows keep the fused GEMV)
+        q8 = (self.use_q8 and trace is None and 2 < B <= 16 and self._q8_chain and
               ops.paged_q8_ok(c.head_dim, B, c.n_head, c.n_head_kv, max_len, self.P))
+        fused = B <= 4 and trace is None and not q8
         b["pos_ids"] = self.pos[:B]
         ops.paged_step_inputs(self.pos, self.kv.table, self.P, self.kv.trash_row, b["kv_idx"], b["seq_len"], B=B)
         scale = 1.0 / math.sqrt(c.head_dim)

@@ -146,6 +146,8 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  *   b_q8:     b's rows are already quantized in the gq_q8_rows layout (a producer's
  *             out_q8 or gq_flash_attn_paged_q8): no prologue; b gives the shape only,
  *             and the input-side fusions are excluded;
+ *   int8:     the int8 path also for 1..4 rows (where the GEMV is the default), so a
+ *             small batch can use the handoffs above;
  * add with M > 4, the other output-side fusions off the int8 path, rope_kv shapes
  * outside the conditions above and b_swiglu on the GEMV path return
  * GQ_ERR_UNSUPPORTED and the caller runs those ops unfused. The GEMM path takes
@@ -181,6 +183,7 @@ typedef struct gq_mul_mat_fusion {
     const gq_tensor* bias;   /* F32 [N, 1, 1, 1] or NULL */
     void* out_q8;            /* int8 path with swiglu: the quantized SWIGLU rows, or NULL */
     const void* b_q8;        /* int8 path: b's rows already quantized, or NULL */
+    int32_t int8;            /* 1: the int8 path for 1..16 rows, also 1..4 (GQ_ERR_UNSUPPORTED off it) */
 } gq_mul_mat_fusion;
 /* The quantized activation rows of the int8 path (up to 16 rows m of K values, K % 32
  * == 0; no counterpart in the reference, which quantizes src1 inside each MUL_MAT):

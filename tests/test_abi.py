@@ -123,6 +123,14 @@ def test_mul_mat_fused_rejects_without_device(lib):
     bq.rms_norm = 0
     assert lib.gq_mul_mat_fused(w, x1, _t(_lib.F32, [64, 1], [4, 256]), ctypes.byref(bq), None) == -2
     assert lib.gq_q8_rows_bytes(4096) == 4096 // 32 * 640 and lib.gq_q8_rows_bytes(100) == 0
+    # int8: the int8 path for 1..16 rows (here its workspace is missing), nothing beyond
+    i8 = _lib.gq_mul_mat_fusion()
+    i8.int8 = 1
+    assert lib.gq_mul_mat_fused_workspace_size(w, x1, ctypes.byref(i8)) == 4096 // 32 * 640
+    assert lib.gq_mul_mat_fused(w, x1, _t(_lib.F32, [64, 1], [4, 256]), ctypes.byref(i8), None) == -3
+    assert lib.gq_mul_mat_fused(w, x17, _t(_lib.F32, [64, 17], [4, 256]), ctypes.byref(i8), None) == -2
+    wu = _lib.make_tensor(0x1004, _lib.Q4_0, [4096, 64], [18, 2304])  # not 16-byte aligned
+    assert lib.gq_mul_mat_fused(wu, x1, _t(_lib.F32, [64, 1], [4, 256]), ctypes.byref(i8), None) == -2
     # the SWIGLU input needs 2K-wide rows, and only exists on the GEMM path
     s5 = _lib.gq_mul_mat_fusion()
     s5.b_swiglu = 1

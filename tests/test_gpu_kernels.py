@@ -379,6 +379,25 @@ def test_swiglu_quantized_rows_feed_down_bit_identical(qtype, K, F, M):
         assert torch.equal(got, want), (got - want).abs().max().item()
 
 
+@pytest.mark.parametrize("qtype,K,N", [(O.Q8_0, 1536, 2048), (O.Q4_0, 4096, 4096)])
+@pytest.mark.parametrize("M", [1, 3, 4])
+def test_int8_path_for_few_rows_matches_rows_of_a_batch(qtype, K, N, M):
+    """int8 = 1 puts 1..4 rows on the int8 MFMA path (default: the GEMV): every row is
+    computed on its own, so its bits equal the same row of a 16-row product (which is
+    pinned against the oracle), with ADD + RMS_NORM in the prologue and the bias."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((16, K), generator=g, device=DEV) * 3.0
+    d = torch.randn((16, K), generator=g, device=DEV)
+    b = torch.randn(N, generator=g, device=DEV) * 0.1
+    want = ops.mul_mat_fused(w, x, rms_eps=1e-5, x_add=d, x_sum=torch.empty_like(x), bias=b)
+    got = ops.mul_mat_fused(w, x[:M].contiguous(), rms_eps=1e-5, x_add=d[:M].contiguous(),
+                            x_sum=torch.empty((M, K), device=DEV), bias=b, int8=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want[:M]), (got - want[:M]).abs().max().item()
+
+
 # --------------------------------------------------------------- set_rows ---
 
 def test_set_rows_golden(golden_dir):

@@ -230,16 +230,20 @@ def _gqa_cfg(qtype):
 
 @pytest.mark.skipif(not O.ref_available(), reason="needs oracle/_ref")
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
-@pytest.mark.parametrize("B,graphs", [(3, True), (6, False), (6, True)])
-def test_batch_decoder_matches_reference_per_sequence(qtype, B, graphs):
-    """B <= 4 runs the fused GEMV layer stack, B > 4 the GEMM one; sequence 3 reuses
-    sequence 1's first page (its prefix) and computes only its suffix."""
+@pytest.mark.parametrize("B,graphs,q8", [(3, True, True), (3, True, False), (6, False, True), (6, True, True),
+                                         (6, True, False)])
+def test_batch_decoder_matches_reference_per_sequence(qtype, B, graphs, q8):
+    """q8: 3..16 slots run the int8 chain with the quantized-row handoffs; without it 3
+    slots run the fused GEMV layer stack and 6 the GEMM one with separate prologue and
+    rope launches. Sequence 3 reuses sequence 1's first page (its prefix) and computes
+    only its suffix."""
     from ggmlc_amd.paged import BatchDecoder
 
     cfg = _gqa_cfg(qtype)
     w, host = _model(cfg)
     P, max_ctx, n_new = 128, 1024, 4
     bd = BatchDecoder(w, max_batch=8, max_ctx=max_ctx, page_size=P)
+    bd.use_q8 = q8
     rng = np.random.default_rng(5)
     lens = [37, 133, 300, 140, 260, 64][:B]
     prompts = [rng.integers(0, cfg.n_vocab, n).astype(np.int32) for n in lens]
