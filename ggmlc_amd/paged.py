@@ -423,9 +423,9 @@ class BatchDecoder:
         ws.get(self._ws_need(B, max_len))
         if self._q8_chain is None:
             self._q8_chain = q8_chain_ok(self.w)
-        # 3..16 slots: the int8 chain with the quantized-row handoffs where it applies
-        # (1 and 2 rows keep the fused GEMV)
-        q8 = (self.use_q8 and trace is None and 2 < B <= 16 and self._q8_chain and
+        # 2..16 slots: the int8 chain with the quantized-row handoffs where it applies
+        # (one row keeps the fused GEMV)
+        q8 = (self.use_q8 and trace is None and 1 < B <= 16 and self._q8_chain and
               ops.paged_q8_ok(c.head_dim, B, c.n_head, c.n_head_kv, max_len, self.P))
         fused = B <= 4 and trace is None and not q8
         b["pos_ids"] = self.pos[:B]
