@@ -25,18 +25,18 @@ def cdiv(a, b):
 
 
 def plan(N, K):
-    """gemm_i8.hip gemm_i8_plan"""
+    """gemm_i8.hip gemm_i8_plan: (K parts, waves per workgroup, workgroups)"""
     tiles, nsteps = cdiv(N, 16), K // (QK * NBS)
-    ks = 1
+    ks, waves = 1, 4
     if tiles < 512 and nsteps >= 4:
         ks = 4
     elif tiles < 4096 and nsteps >= 4:
         ks = 2
-    return ks, cdiv(tiles, 4 // ks)
+    return ks, waves, cdiv(tiles, waves // ks)
 
 
-def wave_range(bx, wave, ks, nsteps):
-    tile = bx * (4 // ks) + wave // ks
+def wave_range(bx, wave, ks, nsteps, waves=4):
+    tile = bx * (waves // ks) + wave // ks
     kp = wave % ks
     sp = cdiv(nsteps, ks)
     s0 = min(nsteps, kp * sp)
@@ -53,7 +53,7 @@ def check_addresses(qt, N, K, M):
     nsteps = nb // NBS
     row_bytes = nb * bb
     assert K % 256 == 0 and rb % 16 == 0 and row_bytes == nsteps * rb and row_bytes % 16 == 0
-    ks, wgs = plan(N, K)
+    ks, waves, wgs = plan(N, K)
     lane = np.arange(64)
     g, lr = lane >> 4, lane & 15
     stage_bytes = 16 * rb
@@ -61,8 +61,8 @@ def check_addresses(qt, N, K, M):
     # grow with the tile), plus one in the middle
     seen_parts = {}
     for bx in sorted({0, wgs // 2, wgs - 1}):
-        for wave in range(4):
-            tile, kp, s0, s1 = wave_range(bx, wave, ks, nsteps)
+        for wave in range(waves):
+            tile, kp, s0, s1 = wave_range(bx, wave, ks, nsteps, waves)
             seen_parts.setdefault(tile, []).append((kp, s0, s1))
             n0 = tile * 16
             rows = N - n0
@@ -108,7 +108,7 @@ def check_addresses(qt, N, K, M):
         if len(parts) == ks:
             steps = sorted(s for _, s0, s1 in parts for s in range(s0, s1))
             assert steps == list(range(nsteps))
-    return ks, wgs
+    return ks, waves, wgs
 
 
 SHAPES = [
@@ -178,7 +178,7 @@ def emulate(qt, N, K, M, wraw, act):
     nb = K // QK
     nsteps = nb // NBS
     row_bytes = nb * bb
-    ks, wgs = plan(N, K)
+    ks, waves, wgs = plan(N, K)
     flat = wraw.reshape(-1)
     qv = act[:nb * 512].reshape(nb, 16, 32).view(np.int8)
     dv = act[nb * 512:nb * 576].view(np.float32).reshape(nb, 16)
@@ -190,8 +190,8 @@ def emulate(qt, N, K, M, wraw, act):
     out = np.zeros((M, N), np.float32)
     for bx in range(wgs):
         parts = {}
-        for wave in range(4):
-            tile, kp, s0, s1 = wave_range(bx, wave, ks, nsteps)
+        for wave in range(waves):
+            tile, kp, s0, s1 = wave_range(bx, wave, ks, nsteps, waves)
             n0 = tile * 16
             acc = np.zeros((64, 4), np.float32)
             for s in range(s0, s1):
@@ -253,3 +253,116 @@ def test_gemm_i8_emulated_data_path_matches_block_formula(qt, N, K, M):
     isum = np.einsum("nbj,mbj->mnb", wvals, qx.astype(np.int64))
     ref = (isum * dw.astype(np.float64)[None, :, :] * dx.astype(np.float64)[:, None, :]).sum(-1)
     np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-6 * np.abs(ref).max())
+
+
+# ---- paired epilogues (rope, SWIGLU) and the quantized SWIGLU rows ----------------------
+
+def pair_row(lo, h, r):
+    """epilogue.h pair_row: logical row r -> physical row"""
+    if lo == 0:
+        return r
+    return (r & ~lo) + ((r & lo) >> 1) + (r & 1) * h
+
+
+@pytest.mark.parametrize("N,K,qt,lo,h", [
+    (17920, 1536, 8, ~0, 8960),          # Qwen2.5-1.5B gate|up: SWIGLU pairs (c, c + N/2)
+    (22016, 4096, 2, ~0, 11008),         # 7B gate|up
+    (2048, 1536, 8, 127, 64),            # Qwen2.5-1.5B QKV: NEOX pairs of 128-dim heads
+    (12288, 4096, 2, 127, 64),           # 7B QKV
+    (1024, 1024, 2, 63, 32),             # 64-dim heads
+    (1024, 2048, 8, 0, 0),               # normal rope: adjacent pairs, the identity
+])
+def test_paired_weight_rows_in_bounds(N, K, qt, lo, h):
+    """k_gemm_i8 with a paired epilogue: tile n0's resource starts at physical row
+    pbase = pair_row(n0) and spans (N - pbase) rows; every chunk offset stays inside it,
+    the logical -> physical map is a bijection of [0, N), and a lane's rows 4g .. 4g + 3 are
+    two whole pairs (even logical row and its partner)."""
+    bb = BLOCK[qt]
+    row_bytes = K // QK * bb
+    rb = NBS * bb
+    cpr = rb // 16
+    assert N % 16 == 0
+    phys = [pair_row(lo, h, r) for r in range(N)]
+    assert sorted(phys) == list(range(N))
+    for n0 in range(0, N, 16):
+        pbase = pair_row(lo, h, n0)
+        wbytes = (N - pbase) * row_bytes
+        assert wbytes < 2**31
+        rows = [pair_row(lo, h, n0 + r) for r in range(16)]
+        assert min(rows) == pbase
+        for c in range(16 * cpr):
+            off = (rows[c // cpr] - pbase) * row_bytes + (c % cpr) * 16 + (K // 256 - 1) * rb
+            assert 0 <= off and off + 16 <= wbytes
+        for g in range(4):  # the lane's two pairs
+            for p in range(2):
+                row = n0 + 4 * g + 2 * p
+                if lo == ~0:
+                    assert phys[row + 1] == phys[row] + h
+                elif lo:
+                    assert phys[row + 1] == phys[row] + h and phys[row] // (lo + 1) == phys[row + 1] // (lo + 1)
+
+
+@pytest.mark.parametrize("N,M", [(17920, 16), (17920, 5), (22016, 9), (1024, 16)])
+def test_quantized_swiglu_rows_in_bounds(N, M):
+    """EPI_GLU_Q8: workgroup b writes quant block b of every row m < M: 2 quant bytes per
+    lane at (b * 16 + m) * 32 + 8 wave + 2 g, the scale and block sum after all quants,
+    inside gq_q8_rows_bytes(N / 2); the blocks of all workgroups tile the layout."""
+    Kq = N // 2
+    nbq = Kq // 32
+    size = nbq * 640
+    assert N % 64 == 0 and N // 64 == nbq
+    seen = set()
+    for b in range(N // 64):
+        for m in range(M):
+            e = b * 16 + m
+            for wave in range(4):
+                for g in range(4):
+                    o = e * 32 + 8 * wave + 2 * g
+                    assert o % 2 == 0 and o + 2 <= nbq * 512
+                    seen.update((o, o + 1))
+            assert nbq * 512 + e * 4 + 4 <= nbq * 576 and nbq * 576 + e * 4 + 4 <= size
+    assert len(seen) == (N // 64) * M * 32
+
+
+@pytest.mark.parametrize("nsteps,ord_", [(6, 2), (6, 4), (35, 4), (3, 4), (5, 2), (16, 8)])
+def test_emulated_split_order_equals_the_split(nsteps, ord_):
+    """ORD: one wave walking every step, folding its sum at the part boundaries k * sp and
+    adding the parts in order (empty ones 0), gives the float32 bits of the ord_-part
+    launch, whose waves sum their own steps and are then added in part order."""
+    rng = np.random.default_rng(nsteps * 10 + ord_)
+    contrib = (rng.standard_normal((nsteps, 8)) * 10.0 ** rng.integers(-3, 3, (nsteps, 8))).astype(np.float32)
+    sp = cdiv(nsteps, ord_)
+    # the split launch
+    parts = []
+    for k in range(ord_):
+        s0, s1 = min(nsteps, k * sp), min(nsteps, k * sp + sp)
+        acc = np.zeros(8, np.float32)
+        for s in range(s0, s1):
+            acc = np.float32(acc + contrib[s])
+        parts.append(acc)
+    want = parts[0]
+    for k in range(1, ord_):
+        want = np.float32(want + parts[k])
+    # the one-wave emulation (k_gemm_i8's fold)
+    part = [np.zeros(8, np.float32) for _ in range(ord_)]
+    acc = np.zeros(8, np.float32)
+    for s in range(nsteps):
+        for k in range(1, ord_):
+            if s == k * sp:
+                part[k - 1], acc = acc, np.zeros(8, np.float32)
+        acc = np.float32(acc + contrib[s])
+    part[(nsteps - 1) // sp] = acc
+    got = part[0]
+    for k in range(1, ord_):
+        got = np.float32(got + part[k])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_plan_of_the_configs():
+    """the launch shapes of the configs' batched-decode products"""
+    assert plan(2048, 1536) == (4, 4, 128)       # Qwen2.5-1.5B qkv
+    assert plan(1536, 1536) == (4, 4, 96)        # o
+    assert plan(17920, 1536) == (2, 4, 560)      # gate|up
+    assert plan(1536, 8960) == (4, 4, 96)        # down
+    assert plan(151936, 1536) == (1, 4, 2374)    # tied head
+    assert plan(4096, 11008) == (4, 4, 256)      # 7B down
