@@ -513,7 +513,8 @@ int attn_args(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v, const 
     if (q->type != GQ_TYPE_F32 || k->type != GQ_TYPE_F16 || v->type != GQ_TYPE_F16 || dst->type != GQ_TYPE_F32)
         return fail(GQ_ERR_UNSUPPORTED, "flash_attn_ext: needs F32 q/dst and F16 k/v");
     const int64_t D = q->ne[0], S = q->ne[1], Hq = q->ne[2], n_kv = k->ne[1], Hkv = k->ne[2];
-    if (D != 64 && D != 128) return fail(GQ_ERR_UNSUPPORTED, "flash_attn_ext: head dim must be 64 or 128");
+    if (D < 8 || D > 256 || D % 8)
+        return fail(GQ_ERR_UNSUPPORTED, "flash_attn_ext: head dim must be a multiple of 8 up to 256");
     if (k->ne[0] != D || v->ne[0] != D || v->ne[1] != n_kv || v->ne[2] != Hkv || Hkv <= 0 || Hq % Hkv != 0 ||
         q->ne[3] != 1 || k->ne[3] != 1 || v->ne[3] != 1 || n_kv <= 0 || S <= 0)
         return fail(GQ_ERR_INVALID, "flash_attn_ext: shape mismatch q " + shape(q) + " k " + shape(k) + " v " + shape(v));

@@ -68,18 +68,22 @@ bool fuse_merge_ok(int64_t n_split, int64_t nq, int64_t D, int64_t pairs) {
            pairs <= ARRIVE_N;
 }
 
+// the kernels' head-dim width: 64, 128 or 256 (other head dims, multiples of 8, are padded:
+// their loads past the head read 0 and nothing past it is stored)
+int64_t attn_width(int64_t D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
+
 Plan make_plan(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     Plan p;
     p.G = Hq / Hkv;
     p.NQ = p.G * S;
     p.n_qt = cdiv(p.NQ, QT);
     p.n_chunks = cdiv(n_kv, CH);
-    p.dec = p.NQ <= DEC_MAX_NQ && (D == 64 || D == 128);
+    p.dec = p.NQ <= DEC_MAX_NQ;
     if (p.dec) {
         // rows per split = U rows per lane stream x (4 waves x rows per wave instruction);
         // the largest U (8, 4, 2; at most 4 for more than 4 query vectors) that still
         // gives DEC_TARGET_WG / 2 workgroups
-        const int64_t rows_it = 4 * (64 / (D / 8));
+        const int64_t rows_it = 4 * (64 / (attn_width(D) / 8));
         const int umax = p.NQ > 4 ? 4 : 8;
         int u = umax;
         while (u > 2 && Hkv * cdiv(n_kv, u * rows_it) < DEC_TARGET_WG / 2) u >>= 1;
@@ -119,13 +123,16 @@ __device__ __forceinline__ float dpp_f(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
-// sum over aligned groups of W lanes (W = 8 or 16) with DPP; every lane gets its group's total
+// sum over aligned groups of W lanes (W = 8, 16 or 32) with DPP (and a permlane swap of
+// the 16-lane totals for 32); every lane gets its group's total
+__device__ __forceinline__ float add_16(float x);
 template <int W>
 __device__ __forceinline__ float lanes_sum(float v) {
     v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
     v += dpp_f<0x141>(v);  // row_half_mirror: 8-lane totals
-    if constexpr (W == 16) v += dpp_f<0x140>(v);  // row_mirror: 16-lane totals
+    if constexpr (W >= 16) v += dpp_f<0x140>(v);  // row_mirror: 16-lane totals
+    if constexpr (W == 32) v = add_16(v);         // 32-lane totals
     return v;
 }
 
@@ -141,6 +148,10 @@ __device__ __forceinline__ Pair xchg_16(float x) {
 __device__ __forceinline__ Pair xchg_32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float add_16(float x) {  // x + the value of lane ^ 16 (same bits in both)
+    const Pair p = xchg_16(x);
+    return p.a + p.b;
 }
 
 // online-softmax states (m, l, o[8]) of two lanes merged into both
@@ -218,7 +229,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
                                                          h * a.qnb2) + d0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            q[u][e] = qp[e];  // q rows need only 4-byte alignment
+            q[u][e] = d0 < a.D ? qp[e] : 0.0f;  // q rows need only 4-byte alignment; dims past a.D: 0
             if (q_f16) q[u][e] = (float)(_Float16)q[u][e];
             q[u][e] *= a.scale;  // folded: (q*scale).k, the order ggml's tiled path uses is irrelevant at 1e-6
         }
@@ -276,8 +287,9 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         const bool in = r < r_end;
         rin[t] = in;
         const int64_t pr = prow0 + (r - r_begin);  // pool row (the row itself when not paged)
-        const uint32_t ko = in ? (uint32_t)(pr * a.knb1 + d0 * 2) : 0x80000000u;
-        const uint32_t vo = in ? (uint32_t)(pr * a.vnb1 + d0 * 2) : 0x80000000u;
+        const bool dim_in = d0 < a.D;  // head dims padded to the template's D read 0
+        const uint32_t ko = in && dim_in ? (uint32_t)(pr * a.knb1 + d0 * 2) : 0x80000000u;
+        const uint32_t vo = in && dim_in ? (uint32_t)(pr * a.vnb1 + d0 * 2) : 0x80000000u;
         kw[t] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
         vw[t] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
 #pragma unroll
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
         if constexpr (LPR == 8) merge_pair(m[u], l[u], o[u], xchg_row8);
-        merge_pair(m[u], l[u], o[u], xchg_16);
+        if constexpr (LPR <= 16) merge_pair(m[u], l[u], o[u], xchg_16);
         merge_pair(m[u], l[u], o[u], xchg_32);
     }
     if (grp == 0) {
@@ -364,7 +376,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         }
         const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
         if (n_split == 1) {
-            a.dst[(i * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
+            if (d < a.D) a.dst[(i * a.Hq + h) * a.D + d] = L == 0.0f ? 0.0f : acc / L;
         } else {
             const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;  // query vectors of all sequences
             float* pp = part + (((int64_t)split * Hkv + hk) * nqt + (int64_t)seq * nq + u) * (D + 2);
@@ -439,7 +451,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         }
     }
     const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
-    a.dst[(i * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
+    if (d < a.D) a.dst[(i * a.Hq + h) * a.D + d] = L == 0.0f ? 0.0f : acc / L;
 }
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -957,7 +969,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps
         const int qq = idx / D, d = idx % D;
         const int qv = qt * QT + qq;
         float val = 0.0f;
-        if (qv < NQ) {
+        if (qv < NQ && d < a.D) {  // head dims padded to the template's D: 0
             const int64_t h = (int64_t)hk * G + qv % G;
             const int64_t i = qv / G;
             val = *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + i * a.qnb1 +
@@ -999,7 +1011,7 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps
         for (int idx = tid; idx < CH * PPR; idx += 256) {
             const int r = idx / PPR, pc = idx % PPR;
             uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-            if (r < rows) {
+            if (r < rows && pc * 8 < a.D) {
                 kv = *reinterpret_cast<const uint4*>(kbase + (c0 + r) * a.knb1 + pc * 16);
                 vv = *reinterpret_cast<const uint4*>(vbase + (c0 + r) * a.vnb1 + pc * 16);
             }
@@ -1114,9 +1126,11 @@ __global__ __launch_bounds__(256) void k_attn(AttnArgs a, int G, int NQ, int cps
         if (n_split == 1) {
             const float L = sL[qq];
             const float inv = L == 0.0f ? 0.0f : 1.0f / L;
-            float* op = a.dst + (i * a.Hq + h) * D + od;
-            op[0] = o[u][0] * inv;
-            op[1] = o[u][1] * inv;
+            if (od < a.D) {  // a.D % 8 == 0: both dims or neither
+                float* op = a.dst + (i * a.Hq + h) * a.D + od;
+                op[0] = o[u][0] * inv;
+                op[1] = o[u][1] * inv;
+            }
         } else {
             float* pp = part + (((int64_t)split * Hkv + hk) * NQ + qv) * (D + 2);
             pp[2 + od] = o[u][0];
@@ -1144,7 +1158,7 @@ template <int D>
 __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part, int n_split, int Hkv, int NQ,
                                                   int G, int64_t Hq, float* __restrict__ dst,
                                                   const int32_t* __restrict__ len = nullptr, int rps = 1,
-                                                  uint8_t* __restrict__ q8 = nullptr) {
+                                                  uint8_t* __restrict__ q8 = nullptr, int Dr = D) {
     __shared__ float sW[MAX_SPLIT];
     __shared__ float sRed[D / 64 > 0 ? D / 64 : 1];
     const int qv = blockIdx.x;
@@ -1178,7 +1192,7 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
     const int64_t h = (int64_t)hk * G + qv % G;
     const int64_t i = qv / G;
     const float o = L == 0.0f ? 0.0f : acc / L;
-    dst[(i * Hq + h) * D + d] = o;
+    if (d < Dr) dst[(i * Hq + h) * Dr + d] = o;  // Dr: the head dim, D its padded width
     if (!q8) return;
     float amax = fabsf(o);
 #pragma unroll
@@ -1190,8 +1204,8 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
     int qs = q;
 #pragma unroll
     for (int k = 1; k < 32; k <<= 1) qs += __shfl_xor(qs, k, 64);
-    const int64_t nbq = Hq * D / 32;                  // quant blocks of a row
-    const int64_t e = ((h * D + d) / 32) * 16 + i;  // (block, row)
+    const int64_t nbq = Hq * Dr / 32;                  // quant blocks of a row
+    const int64_t e = ((h * Dr + d) / 32) * 16 + i;  // (block, row)
     q8[e * 32 + (d & 31)] = (uint8_t)(q & 0xff);
     if ((d & 31) == 0) {
         *reinterpret_cast<float*>(q8 + nbq * 512 + e * 4) = h2f(f2h(dq));
@@ -1205,14 +1219,17 @@ __global__ void k_attn_reset_counters() {
 }
 
 // the split merge (len, rps: the paged launches' per-sequence split counts; q8: the
-// quantized output rows)
+// quantized output rows); D: the head dim, padded to 64, 128 or 256 for the partials
 int launch_merge(int64_t D, const float* part, int ns, int Hkv, int NQ, int G, int64_t Hq, float* dst,
                  const int32_t* len, int rps, hipStream_t s, uint8_t* q8 = nullptr) {
     const dim3 g2((unsigned)NQ, (unsigned)Hkv);
-    if (D == 128)
-        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8);
+    const int Dr = (int)D;
+    if (D > 128)
+        hipLaunchKernelGGL(k_attn_merge<256>, g2, dim3(256), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8, Dr);
+    else if (D > 64)
+        hipLaunchKernelGGL(k_attn_merge<128>, g2, dim3(128), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8, Dr);
     else
-        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8);
+        hipLaunchKernelGGL(k_attn_merge<64>, g2, dim3(64), 0, s, part, ns, Hkv, NQ, G, Hq, dst, len, rps, q8, Dr);
     return check_hip(hipGetLastError(), "attention merge launch");
 }
 
@@ -1227,7 +1244,7 @@ size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64
     if (Hkv <= 0 || Hq % Hkv) return 0;
     const Plan p = make_plan(D, S, Hq, Hkv, n_kv);
     if (p.n_split <= 1) return 0;
-    return (size_t)p.n_split * Hkv * p.NQ * (D + 2) * sizeof(float);
+    return (size_t)p.n_split * Hkv * p.NQ * (attn_width(D) + 2) * sizeof(float);
 }
 
 int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
@@ -1244,7 +1261,8 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     if (b.softcap != 0.0f) b.scale /= b.softcap;
     const int q_f16 = a.S < 64 ? 1 : 0;
     float* part = reinterpret_cast<float*>(ws);
-    const bool fused_merge = p.dec && fuse_merge_ok(p.n_split, p.NQ, a.D, a.Hkv);
+    const int64_t W = attn_width(a.D);
+    const bool fused_merge = p.dec && fuse_merge_ok(p.n_split, p.NQ, W, a.Hkv);
     if (p.dec) {
         const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv);
         const int nq = (int)p.NQ, G = (int)p.G, ns = (int)p.n_split;
@@ -1258,7 +1276,13 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         else if (p.dec_u == 4) GQ_DEC(DD, NN, 4);  \
         else GQ_DEC(DD, NN, 2);                    \
     } while (0)
-        if (a.D == 128) {
+        if (W == 256) {
+            if (nq == 1) GQ_DEC_U(256, 1);
+            else if (nq == 2) GQ_DEC_U(256, 2);
+            else if (nq <= 4) GQ_DEC_U(256, 4);
+            else if (p.dec_u == 4) GQ_DEC(256, 8, 4);
+            else GQ_DEC(256, 8, 2);
+        } else if (W == 128) {
             if (nq == 1 && p.dec_u == 12) GQ_DEC(128, 1, 12);
             else if (nq == 1 && p.dec_u == 10) GQ_DEC(128, 1, 10);
             else if (nq == 1) GQ_DEC_U(128, 1);
@@ -1284,7 +1308,10 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         return check_hip(hipGetLastError(), "flash_attn_ext (mfma) launch");
     } else {
     const dim3 grid((unsigned)p.n_split, (unsigned)a.Hkv, (unsigned)p.n_qt);
-    if (a.D == 128)
+    if (W == 256)
+        hipLaunchKernelGGL(k_attn<256>, grid, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, (int)p.cps, (int)p.n_chunks,
+                           (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
+    else if (W == 128)
         hipLaunchKernelGGL(k_attn<128>, grid, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, (int)p.cps, (int)p.n_chunks,
                            (int)p.n_split, m0, m1, n_head_log2, q_f16, part);
     else

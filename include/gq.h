@@ -221,7 +221,11 @@ int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n
  *   k, v : F16 ne = [D, n_kv, Hkv, 1] (any row/head strides, nb[0] = 2)
  *   mask : F16 ne = [n_kv, >= S, 1, 1] or NULL
  *   dst  : F32 ne = [D, Hq, S, 1] contiguous (the op's permuted output)
- * D in {64, 128}. max_bias and logit_softcap follow ops.cpp:8532-8768. Query
+ * D a multiple of 8 up to 256: the head dims ggmlc's executor sends to flash attention
+ * (40, 64, 72, 80, 96, 112, 128, 192, 256; executor.cpp:2306-2309) and the ones it runs
+ * through its soft_max fallback; 64 and 128 take the matrix-core prefill kernel, the
+ * others the VALU kernels padded to 64, 128 or 256 dims (the padded dims read 0 and are
+ * not stored). max_bias and logit_softcap follow ops.cpp:8532-8768. Query
  * rounding follows the CPU path taken for that S (fp16 for S < 64, fp32 for
  * S >= 64); accumulation is fp32. Decode launches (few query vectors per kv head)
  * merge their KV splits inside the kernel through per-device arrival counters, so

@@ -77,10 +77,16 @@ def test_other_entry_points_validate_on_host(lib):
     src = _t(_lib.F32, [64, 3, 2, 1], [4, 256, 768, 1536])
     idx_bad = _t(_lib.I64, [4, 1, 1, 1], [8, 32, 32, 32])
     assert lib.gq_set_rows(cache, src, idx_bad, None, None) == -1
+    # head dims: multiples of 8 up to 256 (a 100-dim head is rejected; a 96-dim one passes
+    # validation and then needs its split workspace)
+    q = _t(_lib.F32, [100, 1, 4, 1], [4, 400, 400, 1600])
+    k = _t(_lib.F16, [100, 256, 2, 1], [2, 208, 53248, 106496])
+    d = _t(_lib.F32, [100, 4, 1, 1], [4, 400, 1600, 1600])
+    assert lib.gq_flash_attn_ext(q, k, k, None, 0.1, 0.0, 0.0, d, None, 0, None) == -2
     q = _t(_lib.F32, [96, 1, 4, 1], [4, 384, 384, 1536])
     k = _t(_lib.F16, [96, 256, 2, 1], [2, 192, 49152, 98304])
     d = _t(_lib.F32, [96, 4, 1, 1], [4, 384, 1536, 1536])
-    assert lib.gq_flash_attn_ext(q, k, k, None, 0.1, 0.0, 0.0, d, None, 0, None) == -2
+    assert lib.gq_flash_attn_ext(q, k, k, None, 0.1, 0.0, 0.0, d, None, 0, None) == -3
     x = _t(_lib.F32, [10, 3, 1, 1], [4, 40, 120, 120])
     y = _t(_lib.F32, [10, 4, 1, 1], [4, 40, 160, 160])
     assert lib.gq_soft_max(x, None, 1.0, 0.0, y, None) == -1

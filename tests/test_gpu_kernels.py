@@ -490,6 +490,33 @@ def test_flash_attn_vs_exact(Hq, Hkv, D, S, pos, ctx):
     assert r < 1e-3
 
 
+@pytest.mark.parametrize("D", [40, 72, 80, 96, 112, 192, 256, 8])
+@pytest.mark.parametrize("Hq,Hkv,S,pos,ctx", [
+    (8, 8, 1, 1100, 2048),    # decode, MHA, splits merged inside the kernel
+    (12, 2, 1, 3000, 4096),   # decode, GQA 6 (8 query slots), many splits: separate merge
+    (4, 2, 3, 200, 512),      # three query rows per kv head pair
+    (4, 1, 37, 450, 1024),    # prefill rows: the tiled kernel
+    (6, 2, 1, 20, 64),        # one split
+])
+def test_flash_attn_other_head_dims_vs_exact(D, Hq, Hkv, S, pos, ctx):
+    """Head dims other than 64 and 128 (the rest of the set ggmlc's executor sends to
+    flash attention, executor.cpp:2306-2309, and one it sends to its soft_max fallback)
+    run on the VALU kernels padded to 64, 128 or 256 dims: against the exact softmax at
+    the bar of the 64/128 cases, with every dst row written at the real head stride."""
+    rng = np.random.default_rng(D * 7 + Hq * S + pos)
+    n_kv = O.pad_kv_len(pos + S, ctx)
+    q = rng.standard_normal((Hq, S, D)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, ctx, D)))
+    vc = f16(rng.standard_normal((Hkv, ctx, D)))
+    mask = O.causal_mask_f16(pos, S, n_kv)
+    got = _attn_dev(q, kc, vc, n_kv, mask)
+    exact = O.flash_attn_ext_f16(q, kc, vc, n_kv, mask, mode=1)
+    assert got.shape == exact.shape and np.isfinite(got).all()
+    r = mar(got, exact)
+    print(f"Hq={Hq} Hkv={Hkv} D={D} S={S} n_kv={n_kv}: vs exact {r:.2e}")
+    assert r < 1e-3
+
+
 @pytest.mark.parametrize("D,G,masked", [(128, 1, 0xF800), (64, 4, 0xF800), (128, 2, 0xFC00)])
 def test_flash_attn_banded_mask_prefill(D, G, masked):
     """Prefill (matrix-core path) under a band mask: query row i sees keys
