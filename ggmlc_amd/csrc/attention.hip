@@ -727,9 +727,10 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
 // slots to the empty splits of short sequences and ran working ones in a second round
 // behind them: 2 x the time at 16 sequences of 2048 rows under max_len 4096.)
 // Item i is kv head i % Hkv of split number i / Hkv in the list of every sequence's
-// min(cdiv(len, 128), n_split) splits in sequence order; false past the list's end.
+// min(cdiv(len, 128), n_split) splits in sequence order (slen: that sequence's length);
+// false past the list's end.
 __device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int Hkv, int64_t i, int& seq, int& hk,
-                                           int& split) {
+                                           int& split, int& slen) {
     const int lane = threadIdx.x & 63;
     const int64_t c = i / Hkv;
     hk = (int)(i - c * Hkv);
@@ -750,6 +751,7 @@ __device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int H
             const int k = __popcll(__ballot(base + x <= c));
             seq = b0 + k;
             split = (int)(c - base - __shfl(x - n, k, 64));
+            slen = __shfl(len, k, 64);
             return true;
         }
         base += tot;
@@ -759,7 +761,7 @@ __device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int H
 
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_split, float* __restrict__ part,
-                                                      PagedKv pg) {
+                                                      PagedKv pg, int q16) {
     constexpr int KS = D / 32;         // k-steps of the QK product
     constexpr int DT = D / 16;         // 16-dim tiles of O^T
     constexpr int KW = 32;             // keys per wave
@@ -773,12 +775,12 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
     const int Hkv = (int)a.Hkv;
-    int seq_, hk_, split_;
-    if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_)) return;  // past the list
+    int seq_, hk_, split_, len_;
+    if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_, len_)) return;  // past the list
     const int seq = __builtin_amdgcn_readfirstlane(seq_), hk = __builtin_amdgcn_readfirstlane(hk_),
               split = __builtin_amdgcn_readfirstlane(split_);
     const int64_t r_begin = (int64_t)split * 128;
-    const int64_t len = pg.len[seq];
+    const int64_t len = __builtin_amdgcn_readfirstlane(len_);
     const int64_t pi = r_begin >> pg.log2p;
     const int page = (r_begin < len && pi < pg.tstride) ? pg.table[seq * pg.tstride + pi] : -1;
     const int64_t r_len = page < 0 ? 0 : len;  // logical rows below r_len are read
@@ -824,10 +826,21 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
         const int64_t h = (int64_t)hk * G + (qok ? j : 0);
         const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + seq * a.qnb1 +
                                                          h * a.qnb2);
+        if (q16) {  // 16-byte aligned q rows: two 16-byte loads per 8 dims
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+            for (int ks = 0; ks < KS; ++ks) {
+                const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * ks + 8 * g);
+                const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * ks + 8 * g + 4);
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) qh[ks][e] = (_Float16)(qok ? qp[32 * ks + 8 * g + e] : 0.0f);
+                for (int e = 0; e < 8; ++e) qh[ks][e] = (_Float16)(qok ? xv[e] : 0.0f);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qh[ks][e] = (_Float16)(qok ? qp[32 * ks + 8 * g + e] : 0.0f);
+        }
     }
 
     // V^T into this wave's slice: dim pc * 8 + e, keys kg * KPL .. + KPL - 1 in one write
@@ -1381,10 +1394,11 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
     const int nq = (int)G, ns = (int)p.n_split;
     if (p.u < 0) {
         const dim3 g1((unsigned)(p.n_split * a.Hkv * pg.B));  // one workgroup per possible item
+        const int q16 = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
         if (a.D == 128)
-            hipLaunchKernelGGL(k_attn_dec_mma<128>, g1, dim3(256), 0, s, a, nq, ns, part, pg);
+            hipLaunchKernelGGL(k_attn_dec_mma<128>, g1, dim3(256), 0, s, a, nq, ns, part, pg, q16);
         else
-            hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, nq, ns, part, pg);
+            hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, nq, ns, part, pg, q16);
         int rc = check_hip(hipGetLastError(), "flash_attn_paged (mfma) launch");
         if (rc != GQ_OK || p.n_split == 1) return rc;
         return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, pg.len, 128, s, q8);
