@@ -195,9 +195,11 @@ __device__ __forceinline__ void h8_to_f(const uint4 w, float* f) {
 // table entry per workgroup locates all its rows; rows past len_b (and splits past
 // it, or with a negative page id) read nothing and weigh 0. Partials are indexed by
 // query vector b * G + u, so k_attn_merge finishes them as B * G query rows.
+// qmode: bit 0 rounds the query to fp16 (the CPU decode path), bit 1 says its rows are
+// 16-byte aligned (two 16-byte loads per lane instead of eight 4-byte ones).
 template <int D, int NQ, int U, bool PAGED>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int64_t rps, int n_split, float m0,
-                                                  float m1, uint32_t n_head_log2, int q_f16,
+                                                  float m1, uint32_t n_head_log2, int qmode,
                                                   float* __restrict__ part, PagedKv pg, int fuse) {
     constexpr int LPR = D / 8;       // lanes per row
     constexpr int RPI = 64 / LPR;    // rows per wave instruction
@@ -227,10 +229,18 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         const int64_t h = (int64_t)hk * G + uu % G, i = seq + uu / G;
         const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(a.q) + i * a.qnb1 +
                                                          h * a.qnb2) + d0;
+        if ((qmode & 2) && d0 < a.D) {  // 16-byte aligned q rows: two 16-byte loads
+            const float4 x0 = *reinterpret_cast<const float4*>(qp);
+            const float4 x1 = *reinterpret_cast<const float4*>(qp + 4);
+            q[u][0] = x0.x, q[u][1] = x0.y, q[u][2] = x0.z, q[u][3] = x0.w;
+            q[u][4] = x1.x, q[u][5] = x1.y, q[u][6] = x1.z, q[u][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q[u][e] = d0 < a.D ? qp[e] : 0.0f;  // dims past a.D: 0
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            q[u][e] = d0 < a.D ? qp[e] : 0.0f;  // q rows need only 4-byte alignment; dims past a.D: 0
-            if (q_f16) q[u][e] = (float)(_Float16)q[u][e];
+            if (qmode & 1) q[u][e] = (float)(_Float16)q[u][e];
             q[u][e] *= a.scale;  // folded: (q*scale).k, the order ggml's tiled path uses is irrelevant at 1e-6
         }
         slope[u] = 1.0f;
@@ -1273,6 +1283,7 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     AttnArgs b = a;
     if (b.softcap != 0.0f) b.scale /= b.softcap;
     const int q_f16 = a.S < 64 ? 1 : 0;
+    const int q_al = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
     float* part = reinterpret_cast<float*>(ws);
     const int64_t W = attn_width(a.D);
     const bool fused_merge = p.dec && fuse_merge_ok(p.n_split, p.NQ, W, a.Hkv);
@@ -1282,7 +1293,7 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
         const int fuse = fused_merge ? 1 : 0;
 #define GQ_DEC(DD, NN, UU)                                                                                       \
     hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, false>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
-                       n_head_log2, q_f16, part, PagedKv{}, fuse)
+                       n_head_log2, q_f16 | (q_al << 1), part, PagedKv{}, fuse)
 #define GQ_DEC_U(DD, NN)                           \
     do {                                           \
         if (p.dec_u == 8) GQ_DEC(DD, NN, 8);       \
@@ -1404,10 +1415,11 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
         return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, pg.len, 128, s, q8);
     }
     const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);
+    const int q_al = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
     const int fuse = fused_merge ? 1 : 0;
 #define GQ_PDEC(DD, NN, UU)                                                                                        \
     hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, true>), gd, dim3(256), 0, s, a, nq, nq, p.rps, ns, 1.0f, 1.0f, 1u, \
-                       1, part, pg, fuse)
+                       1 | (q_al << 1), part, pg, fuse)
 #define GQ_PDEC_U(DD, NN)                          \
     do {                                           \
         if (p.u == 8) GQ_PDEC(DD, NN, 8);          \
