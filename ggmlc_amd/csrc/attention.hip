@@ -1182,7 +1182,7 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
                                                   int G, int64_t Hq, float* __restrict__ dst,
                                                   const int32_t* __restrict__ len = nullptr, int rps = 1,
                                                   uint8_t* __restrict__ q8 = nullptr, int Dr = D) {
-    __shared__ float sW[MAX_SPLIT];
+    __shared__ float sW[MAX_SPLIT], sL[MAX_SPLIT];
     __shared__ float sRed[D / 64 > 0 ? D / 64 : 1];
     const int qv = blockIdx.x;
     const int hk = blockIdx.y;
@@ -1195,8 +1195,23 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
         const float ms = base[s * stride], ls = base[s * stride + 1];
         const float mv = ls == 0.0f ? -INFINITY : ms;
         sW[s] = mv;
+        sL[s] = ls;
         mx = fmaxf(mx, mv);
     }
+    // up to MERGE_REG splits: every split's o is requested right behind the (m, l) loads,
+    // before the max is known, so the partials arrive in one memory round trip. The loads
+    // are unconditional (splits past n_split reread the last one) and the sums below skip
+    // those splits by selects, in the same order as the loop.
+    constexpr int MERGE_REG = 32;
+    const bool in_reg = n_split <= MERGE_REG;
+    float po[MERGE_REG];
+    __builtin_amdgcn_sched_barrier(0);
+    if (in_reg) {
+        const int last = max(n_split - 1, 0);
+#pragma unroll
+        for (int s = 0; s < MERGE_REG; ++s) po[s] = base[min(s, last) * stride + 2 + d];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     mx = xor_max<64>(mx);
     if ((d & 63) == 0) sRed[d >> 6] = mx;
     __syncthreads();
@@ -1206,11 +1221,22 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
     for (int s = d; s < n_split; s += D) sW[s] = sW[s] == -INFINITY ? 0.0f : __expf(sW[s] - mx);
     __syncthreads();
     float L = 0.0f, acc = 0.0f;
+    if (in_reg) {
+#pragma unroll
+        for (int s = 0; s < MERGE_REG; ++s) {
+            const bool on = s < n_split;  // entries past n_split are read, never used
+            const float w = sW[s], ls = sL[s];
+            const float L1 = L + ls * w, a1 = acc + po[s] * w;
+            L = on ? L1 : L;
+            acc = on ? a1 : acc;
+        }
+    } else {
 #pragma unroll 8
-    for (int s = 0; s < n_split; ++s) {
-        const float w = sW[s];
-        L += base[s * stride + 1] * w;
-        acc += base[s * stride + 2 + d] * w;
+        for (int s = 0; s < n_split; ++s) {
+            const float w = sW[s];
+            L += base[s * stride + 1] * w;
+            acc += base[s * stride + 2 + d] * w;
+        }
     }
     const int64_t h = (int64_t)hk * G + qv % G;
     const int64_t i = qv / G;
