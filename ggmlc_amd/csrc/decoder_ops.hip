@@ -213,6 +213,11 @@ __global__ __launch_bounds__(256) void k_get_rows(const uint8_t* __restrict__ a,
 }
 
 // ---- ARGMAX per row (first index of the maximum, ggml_vec_argmax_f32)
+// VEC (16-byte aligned rows, n % 4 == 0): 8 float4 loads in flight per lane per pass
+// (32768 values per pass: 5 passes for a 151936-entry vocabulary); otherwise 4 scalar
+// loads. Each lane walks its indices in increasing order (the first maximum wins) and
+// ties between lanes go to the smaller index.
+template <bool VEC>
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t xnb1, int64_t n,
                                                  int32_t* __restrict__ out) {
     __shared__ float sv[16];
@@ -221,17 +226,37 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     const float* xr = reinterpret_cast<const float*>(at(x, r * xnb1));
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    // each lane walks its indices in increasing order (first maximum wins), four loads in flight
-    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 4 * 1024) {
-        float v[4];
+    if constexpr (VEC) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        const int64_t n4 = n / 4;
+        for (int64_t c0 = threadIdx.x; c0 < n4; c0 += 8 * 1024) {
+            float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = i0 + u * 1024 < n ? xr[i0 + u * 1024] : -INFINITY;
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (v[u] > best) {
-                best = v[u];
-                bi = (int)(i0 + u * 1024);
+            for (int u = 0; u < 8; ++u) {
+                const int64_t c = c0 + u * 1024;
+                v[u] = c < n4 ? x4[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
             }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = (int)(4 * (c0 + u * 1024));
+                if (v[u].x > best) best = v[u].x, bi = i;
+                if (v[u].y > best) best = v[u].y, bi = i + 1;
+                if (v[u].z > best) best = v[u].z, bi = i + 2;
+                if (v[u].w > best) best = v[u].w, bi = i + 3;
+            }
+        }
+    } else {
+        for (int64_t i0 = threadIdx.x; i0 < n; i0 += 4 * 1024) {
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = i0 + u * 1024 < n ? xr[i0 + u * 1024] : -INFINITY;
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (v[u] > best) {
+                    best = v[u];
+                    bi = (int)(i0 + u * 1024);
+                }
+        }
     }
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(best, o, 64);
@@ -324,7 +349,11 @@ int get_rows(const uint8_t* a, int atype, int64_t ne0, int64_t anb1, int64_t aro
 
 int argmax(const float* x, int64_t xnb1, int64_t n, int64_t nrows, int32_t* out, hipStream_t s) {
     if (nrows == 0) return GQ_OK;
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned)nrows), dim3(1024), 0, s, x, xnb1, n, out);
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && xnb1 % 16 == 0 && n % 4 == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_argmax<true>, dim3((unsigned)nrows), dim3(1024), 0, s, x, xnb1, n, out);
+    else
+        hipLaunchKernelGGL(k_argmax<false>, dim3((unsigned)nrows), dim3(1024), 0, s, x, xnb1, n, out);
     return check_hip(hipGetLastError(), "argmax launch");
 }
 

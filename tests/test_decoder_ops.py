@@ -144,6 +144,39 @@ def test_argmax_add_gpu(golden_dir, dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n,pad", [(151936, 0), (32000, 0), (49152, 1), (4099, 0), (5, 0)])
+def test_argmax_first_maximum(dev, n, pad):
+    """ggml_vec_argmax_f32: the first index of the maximum; -inf rows give 0. Ties are planted
+    inside one 4-value chunk, across lanes and across passes of the 16-byte path (n % 4 == 0
+    with 16-byte rows), and on the scalar path (n % 4 != 0, or rows padded by one float so
+    they are not 16-byte aligned)."""
+    from ggmlc_amd import ops
+
+    rng = np.random.default_rng(n + pad)
+    rows = 7
+    x = rng.standard_normal((rows, n + pad)).astype(np.float32)
+    top = np.float32(9.5)
+    plants = [
+        [n - 1],                              # the last entry
+        [3, 2],                               # inside one chunk: 2 comes first
+        [5 * 4 + 1, 4 * 1024 * 4 + 1],        # two lanes' chunks
+        [min(n - 1, 40000), min(n - 1, 33000 * 4 % n)],  # far apart: different passes
+        [0],
+    ]
+    for r, idx in enumerate(plants):
+        for i in idx:
+            if i < n:
+                x[r, i] = top
+    x[5, :n] = -np.inf
+    x[6, :n] = np.float32(-3.0)  # all equal: index 0
+    xt = _t(x, dev)[:, :n]
+    got = ops.argmax(xt).cpu().numpy()
+    want = np.array([0 if np.all(x[r, :n] == -np.inf) else int(np.argmax(x[r, :n])) for r in range(rows)],
+                    np.int32)
+    assert np.array_equal(got, want), (got, want)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("mode,n_dims,Hq,Hkv,hd,s", [(2, 128, 32, 32, 128, 1), (2, 64, 15, 5, 64, 7),
                                                      (0, 96, 4, 2, 128, 3)])
 def test_rope_kv_store_bit_identical(dev, mode, n_dims, Hq, Hkv, hd, s):
