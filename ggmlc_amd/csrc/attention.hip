@@ -1230,12 +1230,21 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
             L = on ? L1 : L;
             acc = on ? a1 : acc;
         }
-    } else {
-#pragma unroll 8
-        for (int s = 0; s < n_split; ++s) {
-            const float w = sW[s];
-            L += base[s * stride + 1] * w;
-            acc += base[s * stride + 2 + d] * w;
+    } else {  // chunks of MERGE_REG splits, each chunk's loads at once, the same order
+        const int last = n_split - 1;
+        for (int s0 = 0; s0 < n_split; s0 += MERGE_REG) {
+#pragma unroll
+            for (int s = 0; s < MERGE_REG; ++s) po[s] = base[min(s0 + s, last) * stride + 2 + d];
+#pragma unroll
+            for (int s = 0; s < MERGE_REG; ++s) {
+                const int k = s0 + s;
+                const bool on = k < n_split;  // entries past n_split are read, never used
+                const int kk = min(k, MAX_SPLIT - 1);
+                const float w = sW[kk], ls = sL[kk];
+                const float L1 = L + ls * w, a1 = acc + po[s] * w;
+                L = on ? L1 : L;
+                acc = on ? a1 : acc;
+            }
         }
     }
     const int64_t h = (int64_t)hk * G + qv % G;
