@@ -169,6 +169,17 @@ def test_flash_attn_paged_q8_feeds_o_projection(D, Hq, Hkv, lens, qtype):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(y_got, y_want), (y_got - y_want).abs().max().item()
+    # every row is written, those of sequences of length 0 included (zeros, quantized as
+    # zeros), and a second call gives the same bits; quantized rows past B are written by
+    # neither call, so both buffers start from the same bytes
+    q8a = torch.full_like(q8, 0x5A)
+    first = ops.flash_attn_paged(q, k_pool, v_pool, tb, sl, P, max_len, scale, out_q8=q8a)
+    q8b = torch.full_like(q8, 0x5A)
+    again = torch.full_like(first, float("nan"))
+    ops.flash_attn_paged(q, k_pool, v_pool, tb, sl, P, max_len, scale, out=again, out_q8=q8b)
+    torch.cuda.synchronize()
+    assert torch.equal(again, first)
+    assert torch.equal(q8b, q8a)
 
 
 def test_paged_step_inputs_advance_and_copy():
