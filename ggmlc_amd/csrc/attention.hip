@@ -786,13 +786,21 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
     const int j = lane & 15, g = lane >> 4;
     const int Hkv = (int)a.Hkv;
     int seq_, hk_, split_, len_;
-    if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_, len_)) return;  // past the list
+    if (pg.len) {
+        if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_, len_)) return;  // past the list
+    } else {  // one contiguous sequence of a.n_kv rows (no table: page i is rows 128 i ..)
+        seq_ = 0;
+        hk_ = (int)(blockIdx.x % (unsigned)Hkv);
+        split_ = (int)(blockIdx.x / (unsigned)Hkv);
+        len_ = (int)a.n_kv;
+        if (split_ >= n_split) return;
+    }
     const int seq = __builtin_amdgcn_readfirstlane(seq_), hk = __builtin_amdgcn_readfirstlane(hk_),
               split = __builtin_amdgcn_readfirstlane(split_);
     const int64_t r_begin = (int64_t)split * 128;
     const int64_t len = __builtin_amdgcn_readfirstlane(len_);
     const int64_t pi = r_begin >> pg.log2p;
-    const int page = (r_begin < len && pi < pg.tstride) ? pg.table[seq * pg.tstride + pi] : -1;
+    const int page = (r_begin < len && pi < pg.tstride) ? (pg.table ? pg.table[seq * pg.tstride + pi] : (int)pi) : -1;
     const int64_t r_len = page < 0 ? 0 : len;  // logical rows below r_len are read
     const int64_t prow0 = ((int64_t)(page < 0 ? 0 : page) << pg.log2p) + (r_begin & ((1 << pg.log2p) - 1));
     const int64_t kb0 = r_begin + wave * KW;   // this wave's first key (logical row)
@@ -827,6 +835,21 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
         const int64_t r = kb0 + kg * KPL + u;
         const uint32_t off = r < r_len ? (uint32_t)((prow0 + r - r_begin) * a.vnb1 + pc * 16) : 0x80000000u;
         vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)off, 0, 0);
+    }
+
+    // the KQ mask of a contiguous decode (one query row, 8-byte aligned): this lane's keys
+    // 16 t + 4 g .. + 3 in one 8-byte load per t (keys past n_kv read 0 and are not used)
+    u32x2 mk[2] = {{0u, 0u}, {0u, 0u}};
+    if (a.mask) {
+        const uint64_t mb = reinterpret_cast<uint64_t>(a.mask);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)mb);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(mb >> 32));
+        const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+            (int)__builtin_amdgcn_readfirstlane((uint32_t)(a.n_kv * 2)), 0x00020000);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            mk[t] = __builtin_amdgcn_raw_buffer_load_b64(mrs, (int)((kb0 + 16 * t + 4 * g) * 2), 0, 0);
     }
 
     // Q^T operand: query j (lanes past G hold zeros), dims 32 ks + 8 g .. +7, fp16
@@ -884,7 +907,12 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const bool ok = qok && kb0 + 16 * t + 4 * g + r < r_len;
-            sv[t][r] = ok ? c[r] * a.scale : -INFINITY;
+            if (a.mask) {  // s = scale * q.k + mask, as the prefill kernel
+                const float mv = h2f((uint16_t)(mk[t][r >> 1] >> (16 * (r & 1))));
+                sv[t][r] = ok && mv != -INFINITY ? c[r] * a.scale + mv : -INFINITY;
+            } else {
+                sv[t][r] = ok ? c[r] * a.scale : -INFINITY;
+            }
             bmax = fmaxf(bmax, sv[t][r]);
         }
     }
@@ -1298,14 +1326,55 @@ int attn_reset_counters(hipStream_t s) {
     return check_hip(hipGetLastError(), "attn_reset_counters launch");
 }
 
+// the shapes a contiguous decode may run on k_attn_dec_mma (the strides and alignments
+// decide at the call, contig_mma_ok)
+bool contig_mma_shape(int64_t D, int64_t S, int64_t Hq, int64_t Hkv) {
+    if (S != 1 || Hkv <= 0 || Hq % Hkv) return false;
+    const int64_t G = Hq / Hkv;
+    return (D == 64 || D == 128) && G > 4 && G <= 16;
+}
+
+// one query row of 5..16 query heads per kv head on the matrix cores (the paged kernel with
+// 128-row pages that are the cache's own rows): head dim 64 or 128, no ALiBi or softcap,
+// 16-byte K/V rows, an 8-byte aligned mask row, buffer offsets within 2 GiB
+bool contig_mma_ok(const AttnArgs& a) {
+    if (!contig_mma_shape(a.D, a.S, a.Hq, a.Hkv) || a.max_bias != 0.0f || a.softcap != 0.0f) return false;
+    if (a.knb1 % 16 || a.vnb1 % 16 || (a.mask && (reinterpret_cast<uintptr_t>(a.mask) & 7))) return false;
+    if (a.n_kv < 1 || a.n_kv * a.knb1 >= 0x7fff0000LL || a.n_kv * a.vnb1 >= 0x7fff0000LL) return false;
+    return cdiv(a.n_kv, 128) <= MAX_SPLIT;
+}
+
 size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64_t n_kv) {
     if (Hkv <= 0 || Hq % Hkv) return 0;
     const Plan p = make_plan(D, S, Hq, Hkv, n_kv);
-    if (p.n_split <= 1) return 0;
-    return (size_t)p.n_split * Hkv * p.NQ * (attn_width(D) + 2) * sizeof(float);
+    size_t need = p.n_split <= 1 ? 0 : (size_t)p.n_split * Hkv * p.NQ * (attn_width(D) + 2) * sizeof(float);
+    if (contig_mma_shape(D, S, Hq, Hkv) && n_kv > 128) {  // its splits of 128 rows
+        const size_t mma = (size_t)cdiv(n_kv, 128) * Hkv * (Hq / Hkv) * (D + 2) * sizeof(float);
+        need = need > mma ? need : mma;
+    }
+    return need;
+}
+
+int attention_contig_mma(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+    const int64_t G = a.Hq / a.Hkv, ns = cdiv(a.n_kv, 128);
+    const size_t need = attn_workspace_bytes(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
+    if (ns > 1 && (ws == nullptr || ws_bytes < need))
+        return fail(GQ_ERR_WORKSPACE, "flash_attn_ext: workspace too small (need " + std::to_string(need) + " bytes)");
+    float* part = reinterpret_cast<float*>(ws);
+    const PagedKv pg{nullptr, nullptr, ns, 7, 1};
+    const int q16 = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
+    const dim3 g1((unsigned)(ns * a.Hkv));
+    if (a.D == 128)
+        hipLaunchKernelGGL(k_attn_dec_mma<128>, g1, dim3(256), 0, s, a, (int)G, (int)ns, part, pg, q16);
+    else
+        hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, (int)G, (int)ns, part, pg, q16);
+    const int rc = check_hip(hipGetLastError(), "flash_attn_ext (mfma decode) launch");
+    if (rc != GQ_OK || ns == 1) return rc;
+    return launch_merge(a.D, part, (int)ns, (int)a.Hkv, (int)G, (int)G, a.Hq, a.dst, nullptr, 1, s);
 }
 
 int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
+    if (contig_mma_ok(a)) return attention_contig_mma(a, ws, ws_bytes, s);
     const Plan p = make_plan(a.D, a.S, a.Hq, a.Hkv, a.n_kv);
     if (p.n_split > MAX_SPLIT) return fail(GQ_ERR_INVALID, "flash_attn_ext: context too long for one launch");
     const size_t need = attn_workspace_bytes(a.D, a.S, a.Hq, a.Hkv, a.n_kv);

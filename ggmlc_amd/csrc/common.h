@@ -50,6 +50,7 @@ __device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
 __device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // 16-byte streaming load (nontemporal hint: data is used once)
 __device__ __forceinline__ uint4 ld_nt16(const void* p) {

@@ -36,7 +36,6 @@ namespace gq {
 namespace {
 
 typedef int int4v __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int NBS = 8;  // quant blocks per step
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any resource: reads 0, no fetch

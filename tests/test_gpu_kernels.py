@@ -615,6 +615,43 @@ def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx):
     assert mar(fused[0].cpu().numpy(), exact) < 1e-3
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,n_kv", [(12, 2, 128, 1000), (24, 4, 64, 700), (16, 1, 128, 130),
+                                            (10, 2, 128, 3000)])
+def test_flash_attn_decode_many_heads_per_kv_masked_vs_exact(Hq, Hkv, D, n_kv):
+    """One query row with 5..16 query heads per kv head (the matrix-core decode kernel over
+    the contiguous cache, the KQ mask added to the scores) against the exact softmax in
+    float64: -inf holes, a fully masked 256-row span, -32768 entries, n_kv not a multiple of
+    128 and a cache longer than the view."""
+    rng = np.random.default_rng(Hq * D + n_kv)
+    ctx = n_kv + 64
+    kc = f16(rng.standard_normal((Hkv, ctx, D)))
+    vc = f16(rng.standard_normal((Hkv, ctx, D)))
+    q = rng.standard_normal((Hq, 1, D)).astype(np.float32)
+    mask = np.zeros(n_kv, np.float32)
+    mask[rng.random(n_kv) < 0.1] = -np.inf
+    if n_kv > 400:
+        mask[128:384] = -np.inf
+    mask[rng.random(n_kv) < 0.05] = -32768.0
+    mask[0] = 0.0
+    scale = 1.0 / np.sqrt(D)
+    kd = to_dev(kc).view(torch.float16)[:, :n_kv]
+    vd = to_dev(vc).view(torch.float16)[:, :n_kv]
+    md = to_dev(f16(mask).reshape(1, n_kv)).view(torch.float16)
+    out = ops.flash_attn_ext(to_dev(q), kd, vd, md, scale).cpu().numpy()[0]
+    q16 = q[:, 0].astype(np.float16).astype(np.float64)
+    K = kc.view(np.float16)[:, :n_kv].astype(np.float64)
+    V = vc.view(np.float16)[:, :n_kv].astype(np.float64)
+    m64 = f16(mask).view(np.float16).astype(np.float64)
+    want = np.zeros((Hq, D))
+    for h in range(Hq):
+        s = K[h // (Hq // Hkv)] @ q16[h] * scale + m64
+        p = np.exp(s - s.max())
+        want[h] = p @ V[h // (Hq // Hkv)] / p.sum()
+    r = mar(out, want)
+    print(f"Hq={Hq} Hkv={Hkv} D={D} n_kv={n_kv}: vs exact {r:.2e}")
+    assert r < 2e-5
+
+
 def test_flash_attn_padding_and_gqa_invariants():
     rng = np.random.default_rng(21)
     Hq, Hkv, D, ctx, pos = 6, 2, 64, 1024, 300
