@@ -1348,7 +1348,7 @@ size_t attn_workspace_bytes(int64_t D, int64_t S, int64_t Hq, int64_t Hkv, int64
     if (Hkv <= 0 || Hq % Hkv) return 0;
     const Plan p = make_plan(D, S, Hq, Hkv, n_kv);
     size_t need = p.n_split <= 1 ? 0 : (size_t)p.n_split * Hkv * p.NQ * (attn_width(D) + 2) * sizeof(float);
-    if (contig_mma_shape(D, S, Hq, Hkv) && n_kv > 128) {  // its splits of 128 rows
+    if (contig_mma_shape(D, S, Hq, Hkv) && n_kv > 128 && cdiv(n_kv, 128) <= MAX_SPLIT) {  // 128-row splits
         const size_t mma = (size_t)cdiv(n_kv, 128) * Hkv * (Hq / Hkv) * (D + 2) * sizeof(float);
         need = need > mma ? need : mma;
     }
