@@ -1331,10 +1331,10 @@ int attn_reset_counters(hipStream_t s) {
 bool contig_mma_shape(int64_t D, int64_t S, int64_t Hq, int64_t Hkv) {
     if (S != 1 || Hkv <= 0 || Hq % Hkv) return false;
     const int64_t G = Hq / Hkv;
-    return (D == 64 || D == 128) && G > 4 && G <= 16;
+    return (D == 64 || D == 128) && G > 1 && G <= 16;
 }
 
-// one query row of 5..16 query heads per kv head on the matrix cores (the paged kernel with
+// one query row of 2..16 query heads per kv head on the matrix cores (the paged kernel with
 // 128-row pages that are the cache's own rows): head dim 64 or 128, no ALiBi or softcap,
 // 16-byte K/V rows, an 8-byte aligned mask row, buffer offsets within 2 GiB
 bool contig_mma_ok(const AttnArgs& a) {

@@ -225,7 +225,7 @@ int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n
  * (40, 64, 72, 80, 96, 112, 128, 192, 256; executor.cpp:2306-2309) and the ones it runs
  * through its soft_max fallback; 64 and 128 take the matrix-core prefill kernel, the
  * others the VALU kernels padded to 64, 128 or 256 dims (the padded dims read 0 and are
- * not stored). One query row with 5..16 query heads per kv head (head dim 64 or 128, no
+ * not stored). One query row with 2..16 query heads per kv head (head dim 64 or 128, no
  * ALiBi or softcap, 16-byte K/V rows, an 8-byte aligned mask) decodes on the matrix
  * cores in 128-row splits. max_bias and logit_softcap follow ops.cpp:8532-8768. Query
  * rounding follows the CPU path taken for that S (fp16 for S < 64, fp32 for

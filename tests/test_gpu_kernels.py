@@ -616,9 +616,9 @@ def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,n_kv", [(12, 2, 128, 1000), (24, 4, 64, 700), (16, 1, 128, 130),
-                                            (10, 2, 128, 3000)])
+                                            (10, 2, 128, 3000), (15, 5, 64, 700), (16, 8, 128, 1300)])
 def test_flash_attn_decode_many_heads_per_kv_masked_vs_exact(Hq, Hkv, D, n_kv):
-    """One query row with 5..16 query heads per kv head (the matrix-core decode kernel over
+    """One query row with 2..16 query heads per kv head (the matrix-core decode kernel over
     the contiguous cache, the KQ mask added to the scores) against the exact softmax in
     float64: -inf holes, a fully masked 256-row span, -32768 entries, n_kv not a multiple of
     128 and a cache longer than the view."""
