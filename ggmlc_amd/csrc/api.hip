@@ -878,7 +878,7 @@ static int flash_attn_paged_impl(const gq_tensor* q, const gq_tensor* k_pool, co
                (int64_t)(page_table->nb[1] / 4), lp, (int)B};
     if (out_q8) {
         if (!attention_paged_q8_ok(D, B, Hq, Hkv, max_len, page_size))
-            return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged_q8: needs B <= 16, 5..16 q heads per kv head on pages "
+            return fail(GQ_ERR_UNSUPPORTED, "flash_attn_paged_q8: needs B <= 16, 2..16 q heads per kv head on pages "
                                             "of a multiple of 128 rows and max_len > 128");
         if ((reinterpret_cast<uintptr_t>(out_q8) & 15) != 0)
             return fail(GQ_ERR_INVALID, "flash_attn_paged_q8: out_q8 must be 16-byte aligned");

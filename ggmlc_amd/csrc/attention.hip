@@ -718,7 +718,7 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
         for (int r = 0; r < 4; ++r) op[16 * dt + 4 * g + r] = o[dt][r] * inv;
 }
 
-// Paged batched decode attention on the matrix cores for groups of 5..16 query heads
+// Paged batched decode attention on the matrix cores for groups of 2..16 query heads
 // per kv head (v_mfma_f32_16x16x32_f16, operand layouts as in k_attn_mma). A workgroup
 // owns (split of 128 rows, kv head, sequence); wave w takes the split's keys 32 w .. +31:
 //   S^T (16 keys x 16 queries, two tiles) = K . Q^T with K read straight into the MFMA
@@ -1458,10 +1458,10 @@ struct PagedPlan {
     int64_t rps, n_split;
 };
 
-// groups of 5..16 query heads per kv head go to the matrix-core kernel (pages of a
-// multiple of 128 rows)
+// groups of 2..16 query heads per kv head go to the matrix-core kernel (pages of a
+// multiple of 128 rows); one query head per kv head stays on the VALU kernel
 bool paged_mma(int64_t D, int64_t G, int64_t page) {
-    return (D == 64 || D == 128) && G > 4 && G <= 16 && page % 128 == 0;
+    return (D == 64 || D == 128) && G > 1 && G <= 16 && page % 128 == 0;
 }
 
 // the largest rows-per-lane-stream U (8, 4, 2; at most 4 for more than 4 query vectors)

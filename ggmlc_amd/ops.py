@@ -314,11 +314,11 @@ def q8_rows_bytes(K: int) -> int:
 
 
 def paged_q8_ok(D: int, B: int, Hq: int, Hkv: int, max_len: int, page_size: int) -> bool:
-    """Whether :func:`flash_attn_paged` can write out_q8 for this launch: B <= 16, 5..16 q
+    """Whether :func:`flash_attn_paged` can write out_q8 for this launch: B <= 16, 2..16 q
     heads per kv head, pages of a multiple of 128 rows, max_len > 128 (the library rejects
     the rest with GQ_ERR_UNSUPPORTED)."""
     G = Hq // Hkv if Hkv and Hq % Hkv == 0 else 0
-    return (D in (64, 128) and 1 <= B <= 16 and 4 < G <= 16 and page_size % 128 == 0 and max_len > 128)
+    return (D in (64, 128) and 1 <= B <= 16 and 1 < G <= 16 and page_size % 128 == 0 and max_len > 128)
 
 
 def flash_attn_paged_workspace_size(D: int, B: int, Hq: int, Hkv: int, max_len: int, page_size: int) -> int:

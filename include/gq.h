@@ -358,7 +358,7 @@ int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream);
  *   page_table, seq_len : device I32 (a negative page id reads nothing)
  *   max_len  : an upper bound of every seq_len[b] (sizes the launch)
  *   dst      : F32 [D, Hq, B] contiguous.  D in {64, 128}, Hq / Hkv <= 8 (<= 16 when
- *              page_size is a multiple of 128; groups of 5-16 run on the matrix cores).
+ *              page_size is a multiple of 128; groups of 2-16 run on the matrix cores).
  * Equal to the reference's decode step of sequence b with the causal mask of its
  * position (columns past it weigh exactly 0). Shares gq_flash_attn_ext's per-device
  * split counters: no two decode attention launches concurrently on one device. */
@@ -371,7 +371,7 @@ int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_te
  * the output projection into out_q8 (the gq_q8_rows layout, K = Hq * D): the prologue of
  * that projection's MUL_MAT done by the split merge, so the projection can take them
  * through gq_mul_mat_fusion.b_q8. No counterpart in the reference (one fewer launch per
- * layer for the batched decode). B <= 16, 5..16 query heads per kv head (the
+ * layer for the batched decode). B <= 16, 2..16 query heads per kv head (the
  * matrix-core kernel), max_len > 128 (a split merge runs). */
 int gq_flash_attn_paged_q8(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
                            const gq_tensor* page_table, const gq_tensor* seq_len, int64_t page_size, int64_t max_len,
