@@ -53,6 +53,7 @@ struct MulMatPlan {
     bool use_gemv;
     bool use_i8;  // 5..16 rows on int8 MFMA (gemm_i8) when the weight is 16-byte aligned
     size_t ws, ws_act;
+    size_t ws_rs;  // offset of the GEMM's activation row scales (M floats) in the workspace
 };
 
 int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, MulMatPlan& p) {
@@ -84,11 +85,12 @@ int plan_mul_mat(const gq_tensor* a, const gq_tensor* b, const gq_tensor* dst, M
     }
     p.use_gemv = p.M <= GEMV_MAX_M;  // GEMV up to this many activation rows, MFMA GEMM above
     // the GEMV quantizes the activation in LDS; the GEMM takes it from the workspace as the
-    // exact fp16 pair hi + lo of d * q (rows of 2K halves), followed by the split-K partials
-    // when its plan splits K
+    // exact fp16 pair hi + lo of d * q / r (rows of 2K halves), then the row scales r (M
+    // floats), followed by the split-K partials when its plan splits K
     p.use_i8 = !p.use_gemv && p.M <= GEMM_I8_MAX_M && K % GEMM_I8_K_ALIGN == 0 && K <= PREP_MAX_K;
     const size_t raw = p.use_gemv ? 0 : (size_t)p.M * K * 4;
-    p.ws_act = (raw + 255) & ~(size_t)255;
+    p.ws_rs = (raw + 255) & ~(size_t)255;
+    p.ws_act = p.ws_rs + (p.use_gemv ? 0 : (((size_t)p.M * 4 + 255) & ~(size_t)255));
     p.ws = p.ws_act;
     if (!p.use_gemv && p.M > 0) p.ws += (gemm_plan(N, K, p.M).part_bytes + 255) & ~(size_t)255;
     // the int8 path's activation layout; the GEMM path's size is kept for weights that are
@@ -181,10 +183,14 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
         return gemm_i8(a->type, W, p.N, p.K, act, p.M, y, p.ldd, s);
     }
     uint16_t* A = static_cast<uint16_t*>(workspace);
-    rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, 2 * p.K, s);
+    float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.ws_rs);
+    if (p.K <= PREP_MAX_K)  // one launch: the row in registers, its scale from the quantized blocks
+        rc = act_prep(ActPrep{x, p.x_stride, nullptr, 0, nullptr, 0, p.K, 0, 0, 0.0f}, p.M, A, 2 * p.K, rs, s);
+    else
+        rc = quantize_q8_0_f16(x, p.M, p.K, p.x_stride, A, 2 * p.K, rs, s);
     if (rc) return rc;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + p.ws_act);
-    return gemm(a->type, W, p.N, p.K, A, 2 * p.K, p.M, y, p.ldd, part, s);
+    return gemm(a->type, W, p.N, p.K, A, 2 * p.K, rs, p.M, y, p.ldd, part, s);
 }
 
 // The rope + KV-store epilogue of gq_mul_mat_fused: the checks of gq_rope_kv_store
@@ -381,10 +387,12 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
     if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0)
         return fail(GQ_ERR_INVALID, "mul_mat_fused: weight data must be 4-byte aligned");
     uint16_t* A = static_cast<uint16_t*>(f->workspace);
-    int rc = act_prep(ap, p.M, A, 2 * p.K, s);
+    float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(f->workspace) + p.ws_rs);
+    int rc = act_prep(ap, p.M, A, 2 * p.K, rs, s);
     if (rc) return rc;
     float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(f->workspace) + p.ws_act);
-    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, 2 * p.K, p.M, dp, ldd, part, s, bias);
+    return gemm(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, A, 2 * p.K, rs, p.M, dp, ldd, part, s,
+                bias);
 }
 
 int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, const gq_mul_mat_fusion* f,

@@ -227,14 +227,36 @@ __device__ __forceinline__ void quant8_block(const float (&v)[8], int (&q)[8], u
     dh = f2h(d);
 }
 
-// d * q of 8 quants of one block as an exact pair of fp16 vectors, hi + lo == d * q:
-// d (fp16, 11 significant bits) times |q| <= 128 has at most 18 significant bits and is
-// exact in fp32; hi = fp16_rne(d * q) and lo = d * q - hi (exact in fp32) has at most 7
-// significant bits on the grid of d's last bit, which fp16 holds exactly (d normal: that
-// grid is >= 2^-24; d subnormal: every product is a multiple of 2^-24). Packed two
-// halves per dword, element i in the low half of dword i / 2.
-__device__ __forceinline__ void split_dq8(const int (&q)[8], uint16_t dh, uint4& hi, uint4& lo) {
-    const float df = h2f(dh);
+// The row scale of the GEMM's fp16 activation pairs: the smallest power of two
+// r = 2^e (0 <= e <= 8) with 127 * dmax / r <= 65504, dmax the largest block scale of the
+// row (|q| <= 127, so every d * q / r of the row then has a finite fp16 hi part). r = 1
+// for every row whose scales stay below 65504 / 127 = 515.8 (amax below ~65500), which
+// leaves those rows' pairs as they were. A non-finite dmax (amax / 127 past the fp16
+// range: ggml's own scale is then inf) keeps the loop bounded and the products inf.
+__device__ __forceinline__ float row_pow2(float dmax) {
+    float t = 127.0f * dmax;  // exact: 11 x 7 significant bits
+    float r = 1.0f;
+#pragma unroll 1
+    for (int e = 0; e < 8 && t > 65504.0f; ++e) {
+        t *= 0.5f;
+        r *= 2.0f;
+    }
+    return r;
+}
+
+// d * q / r of 8 quants of one block as an exact pair of fp16 vectors, hi + lo == d * q / r
+// (r = 2^e from row_pow2, inv = 1 / r): d (fp16, 11 significant bits) times |q| <= 127 has
+// at most 18 significant bits and is exact in fp32, and so is its power-of-two multiple;
+// hi = fp16_rne(d * q / r) (finite: |d * q / r| <= 65504) and lo = d * q / r - hi (exact in
+// fp32) has at most 7 significant bits on the grid of (d / r)'s last bit, which fp16 holds
+// exactly while that grid is >= 2^-24: always for r = 1 (d normal: the grid is >= 2^-24;
+// d subnormal: every product is a multiple of 2^-24), and for r = 2^e > 1 for every block
+// with d >= 2^(e - 14), which includes every block within a factor 2^22 of the row's
+// largest scale (that one is above 2^(e + 8)). Smaller blocks of such a row round lo to
+// the 2^-24 grid, an error below 2^-40 of the row's largest product. Packed two halves
+// per dword, element i in the low half of dword i / 2.
+__device__ __forceinline__ void split_dq8(const int (&q)[8], uint16_t dh, float inv, uint4& hi, uint4& lo) {
+    const float df = h2f(dh) * inv;  // exact: inv is a power of two, d / r stays a normal fp32
     uint32_t h[4], l[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
                                                  int64_t row_bytes, const uint16_t* __restrict__ A,
                                                  int64_t lda, int64_t M, float* __restrict__ dst,
                                                  int64_t ldd, int spk, float* __restrict__ part,
-                                                 const float* __restrict__ bias) {
+                                                 const float* __restrict__ bias, const float* __restrict__ rs) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int MI = BM / 64;        // 32-row MFMA tiles per wave along M
     constexpr int AQ = BM / 32;        // 16-byte activation pieces per thread per K step (each of hi, lo)
@@ -283,7 +283,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
 
     // D[i][j]: lane holds column j = lane % 32, rows i = 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MI; ++i) {
+        // the activation rows' power-of-two scales (exact products; 1 for almost every row)
+        float rsm[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            rsm[r] = m < M ? rs[m] : 1.0f;
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
@@ -292,9 +299,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M) dst[m * ldd + n] = bias ? acc[i][j][r] + bn_ : acc[i][j][r];
+                const float v = acc[i][j][r] * rsm[r];
+                if (m < M) dst[m * ldd + n] = bias ? v + bn_ : v;
             }
         }
+    }
 }
 
 // 128-token tiles with specialised waves: 8 waves per workgroup, one workgroup per CU.
@@ -316,7 +325,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_ws(const uint8_t* __restrict__ 
                                                     int64_t row_bytes, const uint16_t* __restrict__ A,
                                                     int64_t lda, int64_t M, float* __restrict__ dst,
                                                     int64_t ldd, int spk, float* __restrict__ part,
-                                                    const float* __restrict__ bias) {
+                                                    const float* __restrict__ bias, const float* __restrict__ rs) {
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int BM = 128, MI = 2, AQ = 4;
     constexpr int TILE_H = BM * LDK;  // halves of one of sAh / sAl
@@ -508,7 +517,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_ws(const uint8_t* __restrict__ 
         bias = nullptr;
     }
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MI; ++i) {
+        // the activation rows' power-of-two scales (exact products; 1 for almost every row)
+        float rsm[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            rsm[r] = m < M ? rs[m] : 1.0f;
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
@@ -517,9 +533,11 @@ __global__ __launch_bounds__(512, 1) void k_gemm_ws(const uint8_t* __restrict__ 
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < M) dst[m * ldd + n] = bias ? acc[i][j][r] + bn_ : acc[i][j][r];
+                const float v = acc[i][j][r] * rsm[r];
+                if (m < M) dst[m * ldd + n] = bias ? v + bn_ : v;
             }
         }
+    }
 }
 
 // dst[m * ldd + n] = sum_z part[z][m][n], z in order (+ bias[n])
@@ -576,15 +594,15 @@ GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M) {
 namespace {
 
 template <int QT>
-int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M, float* dst,
-           int64_t ldd, float* part, hipStream_t s, const float* bias) {
+int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const float* rs, int64_t M,
+           float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias) {
     const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
     const GemmPlan p = gemm_plan(N, K, M);
     float* pp = p.ks > 1 ? part : nullptr;
     if (p.bm == 64) {
         const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 64), (unsigned)p.ks);
         hipLaunchKernelGGL((k_gemm<QT, 64, GEMM_PF_64>), grid, dim3(256), 0, s, W, N, K, row_bytes, A, lda, M, dst,
-                           ldd, p.spk, pp, bias);
+                           ldd, p.spk, pp, bias, rs);
     } else {
         constexpr size_t lds = 2 * (size_t)ws_stage_bytes<QT>();  // 112,640 B: two stages
         static_assert(lds <= 160 * 1024, "two stages fit the workgroup's LDS");
@@ -597,7 +615,7 @@ int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t ld
         });
         if (attr != hipSuccess) return check_hip(attr, "gemm: set LDS attribute");
         const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 128), (unsigned)p.ks);
-        hipLaunchKernelGGL(fn, grid, dim3(512), lds, s, W, N, K, row_bytes, A, lda, M, dst, ldd, p.spk, pp, bias);
+        hipLaunchKernelGGL(fn, grid, dim3(512), lds, s, W, N, K, row_bytes, A, lda, M, dst, ldd, p.spk, pp, bias, rs);
     }
     int rc = check_hip(hipGetLastError(), "gemm launch");
     if (rc != GQ_OK || p.ks == 1) return rc;
@@ -607,14 +625,15 @@ int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t ld
 
 }  // namespace
 
-int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
-         float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias) {
+int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const float* rs,
+         int64_t M, float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias) {
+    if (!rs) return fail(GQ_ERR_INVALID, "gemm: null row scales");
     if ((reinterpret_cast<uintptr_t>(W) & 3) != 0) return fail(GQ_ERR_INVALID, "gemm: weight not 4-byte aligned");
     if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0 || lda < 2 * K)
         return fail(GQ_ERR_INVALID, "gemm: activation tile misaligned");
     if (gemm_plan(N, K, M).ks > 1 && part == nullptr) return fail(GQ_ERR_WORKSPACE, "gemm: split K needs partials");
-    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, M, dst, ldd, part, s, bias);
-    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, M, dst, ldd, part, s, bias);
+    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, rs, M, dst, ldd, part, s, bias);
+    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, rs, M, dst, ldd, part, s, bias);
 }
 
 }  // namespace gq

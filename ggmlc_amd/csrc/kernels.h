@@ -14,8 +14,11 @@ int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_str
 // The GEMM path's fused activation prologue (quantize.hip): per row of x (row stride xs),
 // x + d (stored to sum when given) or SWIGLU of the row's halves (glu: x rows are 2K
 // wide), then RMS_NORM (rms), then d * q of quantize_row_q8_0 into y as the exact fp16
-// pair hi + lo (split_dq8): hi at y[m * y_stride + k], lo at y[m * y_stride + K + k]
-// (y_stride >= 2K). quantize_q8_0_f16 writes the same without the neighbours.
+// pair hi + lo of d * q / rs[m] (split_dq8): hi at y[m * y_stride + k], lo at
+// y[m * y_stride + K + k] (y_stride >= 2K), rs[m] the row's power-of-two scale that keeps
+// hi finite (row_pow2; 1 unless the row's amax passes ~65500), which the GEMM multiplies
+// back. quantize_q8_0_f16 writes the same without the neighbours (two launches: the row
+// scales, then the blocks).
 constexpr int64_t PREP_MAX_K = 16384;
 struct ActPrep {
     const float* x;
@@ -28,14 +31,14 @@ struct ActPrep {
     int rms, glu;
     float eps;
 };
-int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStream_t s);
+int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, float* rs, hipStream_t s);
 // The same prologue for gemm_i8 (M <= 16): the quants of quantize_row_q8_0 as int8 in
 // the i8 layout, per block b: y[b * 512 + m * 32 + j] the quants of row m, then
 // y[nb * 512 + (b * 16 + m) * 4] the scale (f32) and y[nb * 576 + (b * 16 + m) * 4] the
 // block sum (i32); gemm_i8_act_bytes(K) bytes
 int act_prep_i8(const ActPrep& a, int64_t M, uint8_t* y, hipStream_t s);
 int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
-                      int64_t y_stride_elems, hipStream_t s);
+                      int64_t y_stride_elems, float* rs, hipStream_t s);
 int quantize_weights(int type, const float* x, void* y, int64_t n, hipStream_t s);
 
 // gemv.hip — dst[m * ldd + n] for m < M (M <= GEMV_MAX_M); x fp32 rows (stride x_stride),
@@ -87,16 +90,17 @@ struct GemvFuse {
 int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, int64_t M, float* dst, int64_t ldd,
          const GemvFuse& fz, hipStream_t s);
 
-// gemm.hip — dst[m * ldd + n] = sum_k A[m * lda + k] * dequant(W)[n, k] (+ bias[n]), A the
-// fp16 hi + lo rows of the activation prologue; grids with fewer tiles than CUs split K over
-// ks workgroups whose partials (part, part_bytes) are summed in order by a second kernel
+// gemm.hip — dst[m * ldd + n] = rs[m] * sum_k A[m * lda + k] * dequant(W)[n, k] (+ bias[n]),
+// A the fp16 hi + lo rows of the activation prologue and rs its row scales; grids with fewer
+// tiles than CUs split K over ks workgroups whose partials (part, part_bytes) are summed in
+// order by a second kernel
 struct GemmPlan {
     int bm, ks, spk;
     size_t part_bytes;
 };
 GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M);
-int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, int64_t M,
-         float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias = nullptr);
+int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const float* rs,
+         int64_t M, float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias = nullptr);
 
 // gemm_i8.hip — dst[m * ldd + n] for 1 <= M <= GEMM_I8_MAX_M activation rows on int8
 // MFMA, for K % 256 == 0 and 16-byte aligned weights, from act_prep_i8's layout; 16-row

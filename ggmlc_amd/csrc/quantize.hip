@@ -26,7 +26,8 @@ enum ActOut { OUT_BLOCKS = 0, OUT_F16 = 2 };
 template <int MODE, bool VEC>
 __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ x, int64_t nrows,
                                                       int64_t K, int64_t x_stride,
-                                                      uint8_t* __restrict__ y, int64_t y_stride) {
+                                                      uint8_t* __restrict__ y, int64_t y_stride,
+                                                      const float* __restrict__ rs) {
     const int64_t nb = K / QK;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gid >> 2;
@@ -50,28 +51,44 @@ __global__ __launch_bounds__(256) void k_quantize_act(const float* __restrict__ 
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             qp[i] = (uint16_t)((q[2 * i] & 0xff) | ((q[2 * i + 1] & 0xff) << 8));
-    } else {  // OUT_F16: the GEMM's A operand, d * q as fp16 hi (at k) + lo (at K + k) of the row
+    } else {  // OUT_F16: the GEMM's A operand, d * q / r as fp16 hi (at k) + lo (at K + k) of the row
         uint4 hi, lo;
-        split_dq8(q, dh, hi, lo);
+        split_dq8(q, dh, 1.0f / rs[m], hi, lo);  // r a power of two: 1 / r exact
         uint16_t* row = reinterpret_cast<uint16_t*>(y) + m * y_stride + b * QK + part * 8;
         *reinterpret_cast<uint4*>(row) = hi;
         *reinterpret_cast<uint4*>(row + K) = lo;
     }
 }
 
+// The row scales r of the fp16 pairs (row_pow2) for rows quantized block by block: one
+// workgroup per row takes max|x| over the row; fp16(max / 127) is the row's largest block
+// scale, since the division and the rounding are monotone.
+__global__ __launch_bounds__(256) void k_row_scale(const float* __restrict__ x, int64_t K, int64_t x_stride,
+                                                   float* __restrict__ rs) {
+    __shared__ float red[4];
+    const float* xr = x + (int64_t)blockIdx.x * x_stride;
+    float amax = 0.0f;
+    for (int64_t k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(xr[k]));
+    amax = xor_max<64>(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        rs[blockIdx.x] = row_pow2(h2f(f2h(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])) / 127.0f)));
+}
+
 template <int MODE>
 static int launch_quant(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,
-                        int64_t y_stride, hipStream_t s) {
+                        int64_t y_stride, hipStream_t s, const float* rs = nullptr) {
     const int64_t threads = nrows * (K / QK) * 4;
     if (threads == 0) return GQ_OK;
     const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (x_stride % 4 == 0);
     const dim3 grid((unsigned)cdiv(threads, 256));
     if (vec)
         hipLaunchKernelGGL((k_quantize_act<MODE, true>), grid, dim3(256), 0, s, x, nrows, K, x_stride,
-                           (uint8_t*)y, y_stride);
+                           (uint8_t*)y, y_stride, rs);
     else
         hipLaunchKernelGGL((k_quantize_act<MODE, false>), grid, dim3(256), 0, s, x, nrows, K, x_stride,
-                           (uint8_t*)y, y_stride);
+                           (uint8_t*)y, y_stride, rs);
     return check_hip(hipGetLastError(), "quantize launch");
 }
 
@@ -81,8 +98,11 @@ int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_str
 }
 
 int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride, uint16_t* y,
-                      int64_t y_stride_elems, hipStream_t s) {
-    return launch_quant<OUT_F16>(x, nrows, K, x_stride, y, y_stride_elems, s);
+                      int64_t y_stride_elems, float* rs, hipStream_t s) {
+    if (nrows == 0 || K == 0) return GQ_OK;
+    hipLaunchKernelGGL(k_row_scale, dim3((unsigned)nrows), dim3(256), 0, s, x, K, x_stride, rs);
+    if (int rc = check_hip(hipGetLastError(), "row scale launch")) return rc;
+    return launch_quant<OUT_F16>(x, nrows, K, x_stride, y, y_stride_elems, s, rs);
 }
 
 // ---- fused activation prologue of the GEMM path ----------------------------------
@@ -90,17 +110,21 @@ int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride
 // (v * scale, the sum of squares in the order of k_rms_norm) or SWIGLU of the row's
 // halves (silu(x[c]) * x[K + c], the arithmetic of k_swiglu), then the fp16(d * q)
 // of quantize_row_q8_0 — the bits of ADD -> RMS_NORM -> quantize (or SWIGLU ->
-// quantize) run one by one — written as the exact fp16 pair hi (row[k]) + lo (row[K + k]). Thread t holds elements c * 2048 + 8t.. of every 2048-wide
-// chunk c in registers (K <= PREP_MAX_K).
+// quantize) run one by one — written as the exact fp16 pair hi (row[k]) + lo (row[K + k])
+// of d * q / r, with the row scale r (row_pow2 of the row's largest block scale: 1 below
+// amax ~65500) stored to rs[m] for the GEMM's epilogue. Thread t holds elements
+// c * 2048 + 8t.. of every 2048-wide chunk c in registers (K <= PREP_MAX_K).
 constexpr int PREP_CH = PREP_MAX_K / 2048;
 
 // CH > 0: the launch has exactly CH chunks (straight-line code the compiler can
 // interleave); CH = 0: up to PREP_CH chunks, the ones past K skipped. I8: the int8 layout
 // of gemm_i8 (quants, scale, block sum per (block, row)) instead of the fp16 pair.
 template <bool VEC, int CH, bool I8 = false>
-__global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restrict__ y, int64_t y_stride) {
+__global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restrict__ y, int64_t y_stride,
+                                                  float* __restrict__ rs) {
     constexpr int NC = CH ? CH : PREP_CH;
     __shared__ double red[4];
+    __shared__ float redf[4];
     const int64_t m = blockIdx.x;
     const int nb = (int)(a.K / QK);
     const float* xr = a.x + m * a.xs;
@@ -146,16 +170,16 @@ __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restric
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] * sc;
     }
+    if constexpr (I8) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        if (!CH && c * 2048 >= a.K) break;  // uniform: whole chunks past K
-        const int t = c * 256 + (int)threadIdx.x;
-        int q[8];
-        uint16_t dh;
-        int qsum;
-        quant8_block(v[c], q, dh, qsum);  // all lanes: pieces past K quantize zeros
-        if ((t >> 2) >= nb) continue;
-        if constexpr (I8) {
+        for (int c = 0; c < NC; ++c) {
+            if (!CH && c * 2048 >= a.K) break;  // uniform: whole chunks past K
+            const int t = c * 256 + (int)threadIdx.x;
+            int q[8];
+            uint16_t dh;
+            int qsum;
+            quant8_block(v[c], q, dh, qsum);  // all lanes: pieces past K quantize zeros
+            if ((t >> 2) >= nb) continue;
             uint8_t* yb = reinterpret_cast<uint8_t*>(y);
             const int64_t e = (int64_t)(t >> 2) * 16 + m;  // (block, row)
             uint32_t w0 = 0, w1 = 0;
@@ -169,13 +193,42 @@ __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restric
                 *reinterpret_cast<float*>(yb + (int64_t)nb * 512 + e * 4) = h2f(dh);
                 *reinterpret_cast<int*>(yb + (int64_t)nb * 576 + e * 4) = qsum;
             }
-            continue;
         }
-        uint4 hi, lo;
-        split_dq8(q, dh, hi, lo);
-        uint16_t* row = y + m * y_stride + (int64_t)t * 8;
-        *reinterpret_cast<uint4*>(row) = hi;
-        *reinterpret_cast<uint4*>(row + a.K) = lo;
+    } else {
+        // quantize every chunk first: the row's largest block scale sets r before any
+        // pair is formed (pieces past K quantize zeros and are never stored)
+        int q[NC][8];
+        uint16_t dh[NC];
+        float dmax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (!CH && c * 2048 >= a.K) {  // uniform: whole chunks past K
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q[c][i] = 0;
+                dh[c] = 0;
+                continue;
+            }
+            int qsum;
+            quant8_block(v[c], q[c], dh[c], qsum);
+            dmax = fmaxf(dmax, h2f(dh[c]));
+        }
+        dmax = xor_max<64>(dmax);
+        if ((threadIdx.x & 63) == 0) redf[threadIdx.x >> 6] = dmax;
+        __syncthreads();
+        const float r = row_pow2(fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3])));
+        if (threadIdx.x == 0) rs[m] = r;
+        const float inv = 1.0f / r;  // exact: a power of two
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (!CH && c * 2048 >= a.K) break;
+            const int t = c * 256 + (int)threadIdx.x;
+            if ((t >> 2) >= nb) continue;
+            uint4 hi, lo;
+            split_dq8(q[c], dh[c], inv, hi, lo);
+            uint16_t* row = y + m * y_stride + (int64_t)t * 8;
+            *reinterpret_cast<uint4*>(row) = hi;
+            *reinterpret_cast<uint4*>(row + a.K) = lo;
+        }
     }
 }
 
@@ -188,19 +241,19 @@ int act_prep_i8(const ActPrep& a, int64_t M, uint8_t* y, hipStream_t s) {
     const dim3 g((unsigned)M);
     if (vec) {
         switch (cdiv(a.K, 2048)) {
-            case 1: hipLaunchKernelGGL((k_act_prep<true, 1, true>), g, dim3(256), 0, s, a, yy, 0); break;
-            case 2: hipLaunchKernelGGL((k_act_prep<true, 2, true>), g, dim3(256), 0, s, a, yy, 0); break;
-            case 5: hipLaunchKernelGGL((k_act_prep<true, 5, true>), g, dim3(256), 0, s, a, yy, 0); break;
-            case 6: hipLaunchKernelGGL((k_act_prep<true, 6, true>), g, dim3(256), 0, s, a, yy, 0); break;
-            default: hipLaunchKernelGGL((k_act_prep<true, 0, true>), g, dim3(256), 0, s, a, yy, 0); break;
+            case 1: hipLaunchKernelGGL((k_act_prep<true, 1, true>), g, dim3(256), 0, s, a, yy, 0, nullptr); break;
+            case 2: hipLaunchKernelGGL((k_act_prep<true, 2, true>), g, dim3(256), 0, s, a, yy, 0, nullptr); break;
+            case 5: hipLaunchKernelGGL((k_act_prep<true, 5, true>), g, dim3(256), 0, s, a, yy, 0, nullptr); break;
+            case 6: hipLaunchKernelGGL((k_act_prep<true, 6, true>), g, dim3(256), 0, s, a, yy, 0, nullptr); break;
+            default: hipLaunchKernelGGL((k_act_prep<true, 0, true>), g, dim3(256), 0, s, a, yy, 0, nullptr); break;
         }
     } else {
-        hipLaunchKernelGGL((k_act_prep<false, 0, true>), g, dim3(256), 0, s, a, yy, 0);
+        hipLaunchKernelGGL((k_act_prep<false, 0, true>), g, dim3(256), 0, s, a, yy, 0, nullptr);
     }
     return check_hip(hipGetLastError(), "act_prep_i8 launch");
 }
 
-int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStream_t s) {
+int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, float* rs, hipStream_t s) {
     if (M == 0) return GQ_OK;
     if (a.K > PREP_MAX_K || a.K % QK) return fail(GQ_ERR_UNSUPPORTED, "act_prep: K too large");
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.xs % 4 == 0) &&
@@ -208,14 +261,14 @@ int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, hipStre
     const dim3 g((unsigned)M);
     if (vec) {  // the configs' K: 960 and 1536 (1 chunk), 2560 and 4096 (2), 8960 (5), 11008 (6)
         switch (cdiv(a.K, 2048)) {
-            case 1: hipLaunchKernelGGL((k_act_prep<true, 1>), g, dim3(256), 0, s, a, y, y_stride); break;
-            case 2: hipLaunchKernelGGL((k_act_prep<true, 2>), g, dim3(256), 0, s, a, y, y_stride); break;
-            case 5: hipLaunchKernelGGL((k_act_prep<true, 5>), g, dim3(256), 0, s, a, y, y_stride); break;
-            case 6: hipLaunchKernelGGL((k_act_prep<true, 6>), g, dim3(256), 0, s, a, y, y_stride); break;
-            default: hipLaunchKernelGGL((k_act_prep<true, 0>), g, dim3(256), 0, s, a, y, y_stride); break;
+            case 1: hipLaunchKernelGGL((k_act_prep<true, 1>), g, dim3(256), 0, s, a, y, y_stride, rs); break;
+            case 2: hipLaunchKernelGGL((k_act_prep<true, 2>), g, dim3(256), 0, s, a, y, y_stride, rs); break;
+            case 5: hipLaunchKernelGGL((k_act_prep<true, 5>), g, dim3(256), 0, s, a, y, y_stride, rs); break;
+            case 6: hipLaunchKernelGGL((k_act_prep<true, 6>), g, dim3(256), 0, s, a, y, y_stride, rs); break;
+            default: hipLaunchKernelGGL((k_act_prep<true, 0>), g, dim3(256), 0, s, a, y, y_stride, rs); break;
         }
     } else {
-        hipLaunchKernelGGL((k_act_prep<false, 0>), g, dim3(256), 0, s, a, y, y_stride);
+        hipLaunchKernelGGL((k_act_prep<false, 0>), g, dim3(256), 0, s, a, y, y_stride, rs);
     }
     return check_hip(hipGetLastError(), "act_prep launch");
 }

@@ -145,8 +145,38 @@ def check_launch(qt, N, K, M):
                 assert (rb + 8).max() * 2 <= BN * LDK * 2
         dwi = kb * BN + wn * 64 + 32 + (lane & 31)
         assert dwi.max() < 2 * BN
-    # epilogue rows / columns are guarded by m < M, n < N; partial tiles by z < ks
+    # epilogue rows / columns are guarded by m < M, n < N (the row scales rs[m] are read for
+    # m < M only); partial tiles by z < ks
+    m = np.arange(M)
+    assert np.all(m * 4 + 4 <= M * 4)
     return bm, ks
+
+
+def workspace_layout(N, K, M):
+    """api.hip plan_mul_mat for the fp16 GEMM path: the hi + lo rows (M x 2K halves), the
+    row scales (M floats) and the split-K partials, each 256-byte aligned"""
+    r256 = lambda b: (b + 255) & ~255  # noqa: E731
+    ws_rs = r256(M * K * 4)
+    ws_act = ws_rs + r256(M * 4)
+    bm, ks, spk = gemm_plan(N, K, M)
+    part = ks * M * N * 4 if ks > 1 else 0
+    return ws_rs, ws_act, ws_act + r256(part)
+
+
+@pytest.mark.parametrize("qt,N,K,M", [(2, 4096, 4096, 512), (2, 96, 11008, 17), (8, 1600, 960, 37), (2, 96, 17408, 17)])
+def test_gemm_workspace_regions_disjoint(qt, N, K, M):
+    ws_rs, ws_act, total = workspace_layout(N, K, M)
+    assert M * 2 * K * 2 <= ws_rs  # the activation rows end before the row scales
+    assert ws_rs + M * 4 <= ws_act  # the row scales end before the partials
+    assert ws_rs % 256 == 0 and ws_act % 256 == 0
+    # the library sizes the workspace the same way (no device: 256 CUs assumed, as here)
+    from ggmlc_amd import _lib
+
+    lib = _lib.load()
+    bb = BLOCK[qt]
+    w = _lib.make_tensor(0x1000, _lib.Q8_0 if qt == 8 else _lib.Q4_0, [K, N], [bb, K // QK * bb])
+    x = _lib.make_tensor(0x1000, _lib.F32, [K, M], [4, 4 * K])
+    assert lib.gq_mul_mat_workspace_size(w, x) == total
 
 
 SHAPES = [

@@ -134,6 +134,77 @@ def test_mul_mat_shapes(qtype, K, N, M):
     _check_mm(qtype, K, N, M, seed=K + N + M)
 
 
+def _big_rows(M, K, seed):
+    """Activations whose blocks reach past the fp16 range of d * q on some rows: a block at
+    amax 3e4 (no row scale needed), 7e4 and 1e6 (row scales 2 and 32), 8e6 (128: the largest
+    finite fp16 block scale is 65504), a row whose other blocks sit 1e-3 low (wide range
+    inside one row) and ordinary N(0, 1) rows."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    nb = K // 32
+    for m, amax in zip(range(M), (3e4, 7e4, 1e6, 8e6, 1e6, 7e4)):
+        b = int(rng.integers(nb))
+        blk = x[m, 32 * b:32 * b + 32]
+        x[m, 32 * b:32 * b + 32] = blk / np.abs(blk).max() * np.float32(amax)
+    if M > 4:
+        x[4] *= np.float32(1e-3)
+        b = int(rng.integers(nb))
+        x[4, 32 * b:32 * b + 32] = np.linspace(-1e6, 1e6, 32, dtype=np.float32)
+    return x
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("K,N,M", [(4096, 1024, 17), (4096, 1024, 128), (11008, 1024, 512), (11008, 96, 17),
+                                   (4096, 300, 3), (4096, 300, 9),
+                                   (17408, 96, 17)])  # K past the one-launch prologue: two-pass row scales
+def test_mul_mat_large_activations(qtype, K, N, M):
+    """Activation blocks with amax up to 8e6 (where d * q leaves the fp16 range) on every
+    path: the GEMV (M <= 4), int8 MFMA (5..16) and the fp16 MFMA GEMM (row scales, split K at
+    N = 96), within 1e-5 of the oracle and finite."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M)
+    qw = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = _big_rows(M, K, K + M)
+    y = ops.mul_mat(qw, to_dev(x)).cpu().numpy()
+    assert np.isfinite(y).all()
+    want = O.mul_mat(qw.data.cpu().numpy(), qtype, K, x)
+    for m in range(min(M, 6)):  # each large row at the bar on its own
+        r = mar(y[m], want[m])
+        assert r < 1e-5, (m, r)
+    r = mar(y, want)
+    print(f"qtype={qtype} K={K} N={N} M={M}: max-abs-rel {r:.2e}")
+    assert r < 1e-5
+
+
+@pytest.mark.parametrize("K,N,M", [(4096, 1024, 17), (11008, 512, 128)])
+def test_mul_mat_fused_large_activations(K, N, M):
+    """The GEMM's fused prologues with inputs past the fp16 range of d * q: ADD (x + d of two
+    large rows) and SWIGLU (silu(g) * u up to ~1e6) give the bits of the separate ops, which
+    are within 1e-5 of the oracle."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, O.Q4_0)
+    x = to_dev(_big_rows(M, K, 1))
+    d = to_dev(_big_rows(M, K, 2) * np.float32(0.03))  # sums below 127 * 65504 wherever the blocks meet
+    got = ops.mul_mat_fused(w, x, x_add=d, x_sum=torch.empty_like(x))
+    s = ops.add(x, d)
+    want = ops.mul_mat(w, s)
+    assert torch.equal(got, want)
+    r = mar(want.cpu().numpy(), O.mul_mat(w.data.cpu().numpy(), O.Q4_0, K, s.cpu().numpy()))
+    assert r < 1e-5, r
+    gate = to_dev(np.random.default_rng(3).standard_normal((M, K)).astype(np.float32) * np.float32(3))
+    up = to_dev(_big_rows(M, K, 4) * np.float32(0.05))  # |silu(g) * u| up to ~5e6 < 127 * 65504
+    gu = torch.cat([gate, up], dim=1).contiguous()
+    got = ops.mul_mat_fused(w, gu, x_swiglu=True)
+    sw = ops.swiglu(gate, up)
+    assert float(sw.abs().max()) > 7e4
+    want = ops.mul_mat(w, sw)
+    assert torch.equal(got, want)
+    r = mar(want.cpu().numpy(), O.mul_mat(w.data.cpu().numpy(), O.Q4_0, K, sw.cpu().numpy()))
+    assert r < 1e-5, r
+    assert torch.isfinite(got).all()
+
+
 def test_mul_mat_strided_rows():
     """src1 with a row stride wider than K (a view) and batch dims."""
     K, N = 512, 96
