@@ -32,7 +32,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from test_model import _check_trace, _cos, _gpu_model, _mar
+from test_model import _check_trace, _cos, _gpu_model, _mar, _rms, _swiglu
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not O.ref_available(), reason="needs oracle/_ref")]
 
@@ -142,6 +142,52 @@ def test_llama7b_full_depth():
     rows = _end_to_end(cfg, dec, host, prompt, 4, max_ctx)
     for i, (c_gpu, c_ref, _) in enumerate(rows):
         assert c_gpu >= _spread_bar(c_ref), (i, c_gpu, c_ref)
+
+
+def test_llama7b_pp1024_decode_teacher_forced():
+    """configs[3] at its real positions: the second 512-token ubatch of the pp1024 prompt (pos
+    512, n_kv 1024) and a decode step at context 1100 (n_kv 1280), every op recomputed from
+    the GPU's own inputs at the op bars (MUL_MAT 1e-5, attention 1e-3 of exact, SET_ROWS
+    bit-exact, logits cosine 0.99999): layers 0 and 31 of the ubatch, every layer of the
+    decode step. The traced steps run the ops one by one; the same steps run fused (the
+    GEMM prologues, the fused decode GEMVs, and the decode step's graph replay) from the
+    same state give the traced steps' logits bit for bit."""
+    import torch
+
+    from ggmlc_amd.model import LLAMA_7B, pad_kv_len
+
+    cfg, max_ctx = LLAMA_7B, 1280
+    dec, host = _gpu_model(cfg, max_ctx, seed=33)
+    prompt = np.random.default_rng(34).integers(0, cfg.n_vocab, 1024).astype(np.int32)
+    b = dec._buffers(512)
+    b["ids"].copy_(torch.from_numpy(prompt[:512]))
+    dec.step(512, 512)  # first ubatch, as the bench runs it
+    b["ids"].copy_(torch.from_numpy(prompt[512:]))
+    trace = []
+    dec.step(512, 1024, trace=trace, advance=False)
+    traced = b["logits"].clone()
+    dec.step(512, 1024)  # the fused prologues from the same position
+    assert torch.equal(b["logits"], traced)
+    worst = _check_trace(cfg, host, trace, 512, 1024, max_ctx, layers=(0, cfg.n_layer - 1), n_threads=16)
+    del trace
+    # greedy decode (fused GEMVs) up to position 1099, then the traced step at context 1100
+    b1 = dec._buffers(1)
+    b1["ids"].copy_(b["next"])
+    for p in range(1024, 1099):
+        dec.step(1, pad_kv_len(p + 1, max_ctx), ids=b1["ids"])
+        b1["ids"].copy_(b1["next"])
+    assert int(dec.pos[0]) == 1099
+    trace = []
+    dec.step(1, 1280, ids=b1["ids"], trace=trace, advance=False)
+    traced = b1["logits"].clone()
+    dec.step(1, 1280, ids=b1["ids"], advance=False)  # the fused GEMVs
+    assert torch.equal(b1["logits"], traced)
+    dec.capture(1, 1280).replay()  # the step graph the bench replays
+    torch.cuda.synchronize()
+    assert torch.equal(b1["logits"], traced) and int(dec.pos[0]) == 1100
+    for k, v in _check_trace(cfg, host, trace, 1, 1280, max_ctx, n_threads=16).items():
+        worst[k] = max(worst.get(k, 0.0), v)
+    print({k: f"{v:.1e}" for k, v in worst.items()})
 
 
 @pytest.mark.parametrize("name,N,K,qtype,Ms", [
@@ -279,3 +325,126 @@ def test_qwen_batch_decoder_b4_full_depth():
             assert _greedy_ok(int(nxt[b]), w_full, logits[b]), (i, b)
         tokens = nxt
     assert bd.pos_host[:B].tolist() == [n + n_new for n in lens]
+
+
+def _check_paged_trace(cfg, host, trace, pos, table, P, logits, n_threads=16):
+    """Recompute every op of a traced batched decode step from the GPU's own inputs: row b
+    runs at position pos[b], its K/V rows live in the pool at table[b][r // P] * P + r % P,
+    and it attends to its rows [0, pos[b]] (the op bars of _check_trace)."""
+    t, nt = cfg.qtype, n_threads
+    B = len(pos)
+    T = {(n, li): v.cpu().numpy() for n, li, v in trace}
+    qd, kvd, hd = cfg.q_dim, cfg.kv_dim, cfg.head_dim
+    rows = [np.array([table[b][r // P] * P + r % P for r in range(pos[b] + 1)]) for b in range(B)]
+    worst = {}
+
+    def bar(name, got, want, tol):
+        m = _mar(got, want)
+        worst[name] = max(worst.get(name, 0.0), m)
+        assert m <= tol, (name, m)
+
+    for li, Lw in enumerate(host[2]):
+        wqkv, wo, wgu, wd = Lw[:4]
+        bq = Lw[4] if len(Lw) > 4 and Lw[4] is not None else np.float32(0.0)
+        g = lambda n: T[(n, li)]  # noqa: E731
+        x_in = g("x_in")
+        bar("rms_norm", g("h1"), _rms(x_in, cfg.rms_eps), 1e-5)
+        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1"), n_threads=nt) + bq, 1e-5)
+        qkv = g("qkv")
+        qh = qkv[:, :qd].reshape(B, cfg.n_head, hd)
+        kh = qkv[:, qd:qd + kvd].reshape(B, cfg.n_head_kv, hd)
+        bar("rope q", g("q")[0], O.ref_rope(qh, pos.astype(np.int32), hd, 2, cfg.rope_base), 1e-6)
+        bar("rope k", g("k")[0], O.ref_rope(kh, pos.astype(np.int32), hd, 2, cfg.rope_base), 1e-6)
+        kc, vc = g("kc")[0].view(np.uint16), g("vc")[0].view(np.uint16)  # [Hkv, pool rows, hd]
+        vh = qkv[:, qd + kvd:].reshape(B, cfg.n_head_kv, hd)
+        for b in range(B):  # SET_ROWS: row pos[b] of sequence b's pages holds the F16 of its k and v
+            r = rows[b][-1]
+            assert np.array_equal(kc[:, r], g("k")[0][b].astype(np.float16).view(np.uint16)), (li, b)
+            assert np.array_equal(vc[:, r], vh[b].astype(np.float16).view(np.uint16)), (li, b)
+            n = len(rows[b])
+            want = O.flash_attn_ext_f16(g("q")[0][b][:, None], kc[:, rows[b]], vc[:, rows[b]], n, None,
+                                        1.0 / math.sqrt(hd), mode=1)
+            bar("flash_attn paged", g("attn")[b], want[0], 1e-3)
+        bar("mul_mat o + add", g("x_mid"), x_in + O.mul_mat(wo, t, qd, g("attn").reshape(B, qd), n_threads=nt), 1e-5)
+        bar("rms_norm", g("h2"), _rms(g("x_mid"), cfg.rms_eps), 1e-5)
+        bar("mul_mat gate_up", g("gu"), O.mul_mat(wgu, t, cfg.n_embd, g("h2"), n_threads=nt), 1e-5)
+        bar("swiglu", g("act"), _swiglu(g("gu"), cfg.n_ff), 1e-5)
+        bar("mul_mat down + add", g("x_out"), g("x_mid") + O.mul_mat(wd, t, cfg.n_ff, g("act"), n_threads=nt), 1e-5)
+    x_last = T[("x_out", len(host[2]) - 1)]
+    bar("rms_norm", T[("hf", -1)], _rms(x_last, cfg.rms_eps), 1e-5)
+    want = O.mul_mat(host[1], t, cfg.n_embd, T[("hf", -1)], n_threads=nt)
+    bar("mul_mat lm_head", logits, want, 1e-5)
+    for b in range(B):
+        assert _cos(logits[b], want[b]) >= NORTH_STAR_COS, b
+    return worst
+
+
+def test_qwen_b16_int8_chain_teacher_forced():
+    """configs[4]'s batched decode step at B = 16 and full depth (28 layers): contexts
+    uniform in [256, 4096], the even sequences opening with one shared 512-token prefix
+    (its 4 pages listed by all 8). The step is traced op by op (the int8 MFMA products
+    with separate prologues) and every op recomputed from the GPU's own inputs at the op
+    bars; the same step on the int8 chain the bench times (quantized-row handoffs, ROPE +
+    SET_ROWS and SWIGLU epilogues, the merge writing the o projection's rows), eager and
+    from its graph, from the same state, gives the traced logits and KV pools bit for bit."""
+    import torch
+
+    from ggmlc_amd import ops
+    from ggmlc_amd.model import QWEN25_1_5B
+    from ggmlc_amd.paged import BatchDecoder
+
+    cfg = QWEN25_1_5B
+    dec, host = _gpu_model(cfg, 256, seed=43)
+    w = dec.w
+    del dec
+    P, B, PREFIX = 128, 16, 512
+    rng = np.random.default_rng(44)
+    ctx = rng.integers(256, 4097, B)
+    ctx[0::2] = np.where(ctx[0::2] > PREFIX, ctx[0::2], rng.integers(PREFIX + 1, 4097, B // 2))
+    prefix = rng.integers(0, cfg.n_vocab, PREFIX).astype(np.int32)
+    bd = BatchDecoder(w, max_batch=B, max_ctx=4096 + 8, page_size=P)
+    tokens = np.zeros(B, np.int32)
+    for b in range(B):
+        t = rng.integers(0, cfg.n_vocab, int(ctx[b])).astype(np.int32)
+        start = 0
+        bd.kv.alloc_slot(b)
+        if b % 2 == 0:
+            t[:PREFIX] = prefix
+            if b > 0:
+                bd.kv.map_existing_pages(b, 0, bd.kv.pages[0][:PREFIX // P])
+                start = PREFIX
+        bd.kv.ensure_tokens(b, len(t) + 2)
+        tokens[b] = int(torch.argmax(bd.prefill(b, t, start)))
+    bd.kv.sync()
+    pos = bd.pos_host[:B].copy()
+    assert pos.tolist() == ctx.tolist()
+    L = bd.ctx_bucket(int(pos.max()) + 1)
+    assert bd._q8_chain is not False and ops.paged_q8_ok(cfg.head_dim, B, cfg.n_head, cfg.n_head_kv, L, P)
+    bb = bd._buffers(B)
+
+    def rewind():
+        for i in range(B):
+            bd.set_pos(i, int(pos[i]))
+        bb["ids"].copy_(torch.from_numpy(tokens).cuda())
+
+    rewind()
+    trace = []
+    bd.step(B, L, trace=trace)
+    torch.cuda.synchronize()
+    traced = bb["logits"].clone()
+    kpool = [k.clone() for k in bd.kv.k]
+    vpool = [v.clone() for v in bd.kv.v]
+    for run in ("eager", "graph"):  # the int8 chain from the same state
+        rewind()
+        if run == "eager":
+            bd.step(B, L)
+        else:
+            bd.capture(B, L).replay()
+        torch.cuda.synchronize()
+        assert bd._q8_chain
+        assert torch.equal(bb["logits"], traced), run
+        assert all(torch.equal(a, b_) for a, b_ in zip(kpool, bd.kv.k)), run
+        assert all(torch.equal(a, b_) for a, b_ in zip(vpool, bd.kv.v)), run
+    del kpool, vpool
+    worst = _check_paged_trace(cfg, host, trace, pos, bd.kv.table_host, P, traced.cpu().numpy())
+    print(f"contexts {pos.min()}-{pos.max()}:", {k: f"{v:.1e}" for k, v in worst.items()})

@@ -181,10 +181,12 @@ def _gpu_model(cfg, max_ctx, seed):
     return dec, host
 
 
-def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
+def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None, n_threads=8):
     """Recompute every traced op from the GPU's own inputs (of the given layers only, and
-    the output head, when layers is a collection of layer indices)."""
+    the output head, when layers is a collection of layer indices); n_threads: the oracle's
+    threads for the products and the attention."""
     t = cfg.qtype
+    nt = n_threads
     last = len(host[2]) - 1
     keep = (lambda li: True) if layers is None else (lambda li: li in layers or li == -1)
     T = {(n, li): v.cpu().numpy() for n, li, v in trace if keep(li) or (n == "x_out" and li == last)}
@@ -207,7 +209,7 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
         g = lambda n: T[(n, li)]  # noqa: E731
         x_in = g("x_in")
         bar("rms_norm", g("h1"), _rms(x_in, cfg.rms_eps), 1e-5)
-        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1")) + bq, 1e-5)
+        bar("mul_mat qkv", g("qkv"), O.mul_mat(wqkv, t, cfg.n_embd, g("h1"), n_threads=nt) + bq, 1e-5)
         qkv = g("qkv")
         qh = qkv[:, :qd].reshape(s, cfg.n_head, cfg.head_dim)
         kh = qkv[:, qd:qd + kvd].reshape(s, cfg.n_head_kv, cfg.head_dim)
@@ -226,17 +228,17 @@ def _check_trace(cfg, host, trace, s, n_kv, max_ctx, layers=None):
         v16 = O.set_rows_f32_f16(np.zeros_like(k16), v.transpose(1, 0, 2)[None], pos)
         assert np.array_equal(kc[:, :, pos], k16[:, :, pos]) and np.array_equal(vc[:, :, pos], v16[:, :, pos])
         want = O.flash_attn_ext_f16(g("q")[0].transpose(1, 0, 2), kc[0], vc[0], n_kv, mask,
-                                    1.0 / math.sqrt(cfg.head_dim), mode=1)
+                                    1.0 / math.sqrt(cfg.head_dim), mode=1, n_threads=nt)
         bar("flash_attn_ext", g("attn"), want, 1e-3)
-        bar("mul_mat o + add", g("x_mid"), x_in + O.mul_mat(wo, t, qd, g("attn").reshape(s, qd)), 1e-5)
+        bar("mul_mat o + add", g("x_mid"), x_in + O.mul_mat(wo, t, qd, g("attn").reshape(s, qd), n_threads=nt), 1e-5)
         bar("rms_norm", g("h2"), _rms(g("x_mid"), cfg.rms_eps), 1e-5)
-        bar("mul_mat gate_up", g("gu"), O.mul_mat(wgu, t, cfg.n_embd, g("h2")), 1e-5)
+        bar("mul_mat gate_up", g("gu"), O.mul_mat(wgu, t, cfg.n_embd, g("h2"), n_threads=nt), 1e-5)
         bar("swiglu", g("act"), _swiglu(g("gu"), cfg.n_ff), 1e-5)
-        bar("mul_mat down + add", g("x_out"), g("x_mid") + O.mul_mat(wd, t, cfg.n_ff, g("act")), 1e-5)
+        bar("mul_mat down + add", g("x_out"), g("x_mid") + O.mul_mat(wd, t, cfg.n_ff, g("act"), n_threads=nt), 1e-5)
     x_last = T[("x_out", len(host[2]) - 1)][s - 1:]
     bar("rms_norm", T[("hf", -1)], _rms(x_last, cfg.rms_eps), 1e-5)
     logits = T[("logits", -1)][0]
-    want = O.mul_mat(host[1], t, cfg.n_embd, T[("hf", -1)])[0]
+    want = O.mul_mat(host[1], t, cfg.n_embd, T[("hf", -1)], n_threads=nt)[0]
     bar("mul_mat lm_head", logits, want, 1e-5)
     assert _cos(logits, want) >= 0.99999
     assert int(T[("next", -1)][0]) == int(np.argmax(logits))
