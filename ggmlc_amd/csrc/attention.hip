@@ -38,12 +38,32 @@ constexpr int MAX_SPLIT = 1024;
 // kv head) merges that pair's split partials itself, so no second launch is needed.
 // Partials are written and read with agent-scope relaxed atomics (coherent across the
 // XCDs' L2s, no cache flushes) and each workgroup arrives on the pair's counter after
-// its own stores have completed. Every launch leaves the counters at zero (the last
-// arrival resets its counter), so decode launches on one device must not overlap
-// (they run on one stream).
+// its own stores have completed. A launch needs its counters at zero and leaves them at
+// zero (the last arrival resets its counter). The counters are not in the caller's
+// workspace: that holds whatever the previous op left there, and clearing it would cost
+// a launch. Instead each stream gets a set of its own (ARRIVE_SETS sets, assigned on a
+// stream's first fused launch; launches on one stream never overlap), so launches on
+// different streams cannot collide; a stream past the last set takes the separate merge
+// launch. Launches captured in a graph keep their stream's set, so two graphs captured
+// on one stream must not be replayed concurrently.
 constexpr int ARRIVE_N = 4096;     // (sequence, kv head) pairs of one launch
+constexpr int ARRIVE_SETS = 16;    // streams with counters of their own
 constexpr int FUSE_MAX_SPLIT = 16;  // splits merged from registers (one round trip)
-__device__ unsigned g_attn_arrive[ARRIVE_N];
+__device__ unsigned g_attn_arrive[ARRIVE_SETS * ARRIVE_N];
+
+// the counter set of a stream (its first fused launch assigns one), or -1 when every set
+// is taken
+int arrive_set(hipStream_t s) {
+    static std::mutex mu;
+    static hipStream_t owner[ARRIVE_SETS];
+    static int used = 0;
+    std::lock_guard<std::mutex> lk(mu);
+    for (int i = 0; i < used; ++i)
+        if (owner[i] == s) return i;
+    if (used == ARRIVE_SETS) return -1;
+    owner[used] = s;
+    return used++;
+}
 
 __device__ __forceinline__ void st_ag(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -201,6 +221,7 @@ template <int D, int NQ, int U, bool PAGED>
 __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int64_t rps, int n_split, float m0,
                                                   float m1, uint32_t n_head_log2, int qmode,
                                                   float* __restrict__ part, PagedKv pg, int fuse) {
+    // fuse: 0 separate merge, else 1 + the stream's counter set (arrive_set)
     constexpr int LPR = D / 8;       // lanes per row
     constexpr int RPI = 64 / LPR;    // rows per wave instruction
     constexpr int ROWS_IT = 4 * RPI;
@@ -418,7 +439,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-        unsigned* ctr = &g_attn_arrive[seq * Hkv + hk];
+        unsigned* ctr = &g_attn_arrive[(fuse - 1) * ARRIVE_N + seq * Hkv + hk];
         const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int last = old == (unsigned)(n_split - 1);
         if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -740,7 +761,7 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
 // min(cdiv(len, 128), n_split) splits in sequence order (slen: that sequence's length);
 // false past the list's end.
 __device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int Hkv, int64_t i, int& seq, int& hk,
-                                           int& split, int& slen) {
+                                           int& split, int& slen, int64_t& n_items) {
     const int lane = threadIdx.x & 63;
     const int64_t c = i / Hkv;
     hk = (int)(i - c * Hkv);
@@ -766,6 +787,7 @@ __device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int H
         }
         base += tot;
     }
+    n_items = base * Hkv;
     return false;
 }
 
@@ -787,7 +809,18 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
     const int Hkv = (int)a.Hkv;
     int seq_, hk_, split_, len_;
     if (pg.len) {
-        if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_, len_)) return;  // past the list
+        int64_t n_items = 0;
+        if (!paged_item(pg, n_split, Hkv, blockIdx.x, seq_, hk_, split_, len_, n_items)) {  // past the list
+            // with one split the outputs are written here, not by the merge: the first
+            // workgroup past the list (there is one per kv head of each sequence without
+            // rows) writes zeros for those sequences, as the merge would
+            if (n_split == 1 && (int64_t)blockIdx.x == n_items) {
+                const int64_t per = a.Hq * D;
+                for (int64_t idx = tid; idx < (int64_t)pg.B * per; idx += 256)
+                    if (pg.len[idx / per] <= 0) a.dst[idx] = 0.0f;
+            }
+            return;
+        }
     } else {  // one contiguous sequence of a.n_kv rows (no table: page i is rows 128 i ..)
         seq_ = 0;
         hk_ = (int)(blockIdx.x % (unsigned)Hkv);
@@ -1301,7 +1334,7 @@ __global__ __launch_bounds__(D) void k_attn_merge(const float* __restrict__ part
 
 __global__ void k_attn_reset_counters() {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < ARRIVE_N) g_attn_arrive[i] = 0u;
+    if (i < ARRIVE_SETS * ARRIVE_N) g_attn_arrive[i] = 0u;
 }
 
 // the split merge (len, rps: the paged launches' per-sequence split counts; q8: the
@@ -1322,7 +1355,7 @@ int launch_merge(int64_t D, const float* part, int ns, int Hkv, int NQ, int G, i
 }  // namespace
 
 int attn_reset_counters(hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_reset_counters, dim3(ARRIVE_N / 256), dim3(256), 0, s);
+    hipLaunchKernelGGL(k_attn_reset_counters, dim3(ARRIVE_SETS * ARRIVE_N / 256), dim3(256), 0, s);
     return check_hip(hipGetLastError(), "attn_reset_counters launch");
 }
 
@@ -1340,6 +1373,9 @@ bool contig_mma_shape(int64_t D, int64_t S, int64_t Hq, int64_t Hkv) {
 bool contig_mma_ok(const AttnArgs& a) {
     if (!contig_mma_shape(a.D, a.S, a.Hq, a.Hkv) || a.max_bias != 0.0f || a.softcap != 0.0f) return false;
     if (a.knb1 % 16 || a.vnb1 % 16 || (a.mask && (reinterpret_cast<uintptr_t>(a.mask) & 7))) return false;
+    // the mask is read 4 keys per 8-byte load, bounded at n_kv keys: a multiple of 4 keeps
+    // every key's load inside the bound (other lengths take k_attn_dec)
+    if (a.mask && a.n_kv % 4) return false;
     if (a.n_kv < 1 || a.n_kv * a.knb1 >= 0x7fff0000LL || a.n_kv * a.vnb1 >= 0x7fff0000LL) return false;
     return cdiv(a.n_kv, 128) <= MAX_SPLIT;
 }
@@ -1390,11 +1426,12 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
     const int q_al = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
     float* part = reinterpret_cast<float*>(ws);
     const int64_t W = attn_width(a.D);
-    const bool fused_merge = p.dec && fuse_merge_ok(p.n_split, p.NQ, W, a.Hkv);
+    const int set = p.dec && fuse_merge_ok(p.n_split, p.NQ, W, a.Hkv) ? arrive_set(s) : -1;
+    const bool fused_merge = set >= 0;
     if (p.dec) {
         const dim3 gd((unsigned)p.n_split, (unsigned)a.Hkv);
         const int nq = (int)p.NQ, G = (int)p.G, ns = (int)p.n_split;
-        const int fuse = fused_merge ? 1 : 0;
+        const int fuse = set + 1;
 #define GQ_DEC(DD, NN, UU)                                                                                       \
     hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, false>), gd, dim3(256), 0, s, b, G, nq, p.rows_per_split, ns, m0, m1, \
                        n_head_log2, q_f16 | (q_al << 1), part, PagedKv{}, fuse)
@@ -1518,9 +1555,10 @@ int attention_paged(const AttnArgs& a, const PagedKv& pg, int64_t max_len, void*
         if (rc != GQ_OK || p.n_split == 1) return rc;
         return launch_merge(a.D, part, ns, (int)a.Hkv, (int)(pg.B * G), (int)G, a.Hq, a.dst, pg.len, 128, s, q8);
     }
-    const bool fused_merge = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B);
+    const int set = fuse_merge_ok(p.n_split, G, a.D, a.Hkv * pg.B) ? arrive_set(s) : -1;
+    const bool fused_merge = set >= 0;
     const int q_al = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
-    const int fuse = fused_merge ? 1 : 0;
+    const int fuse = set + 1;
 #define GQ_PDEC(DD, NN, UU)                                                                                        \
     hipLaunchKernelGGL((k_attn_dec<DD, NN, UU, true>), gd, dim3(256), 0, s, a, nq, nq, p.rps, ns, 1.0f, 1.0f, 1u, \
                        1 | (q_al << 1), part, pg, fuse)

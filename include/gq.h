@@ -226,12 +226,15 @@ int gq_set_rows(gq_tensor* a, const gq_tensor* b, const gq_tensor* c, int32_t* n
  * through its soft_max fallback; 64 and 128 take the matrix-core prefill kernel, the
  * others the VALU kernels padded to 64, 128 or 256 dims (the padded dims read 0 and are
  * not stored). One query row with 2..16 query heads per kv head (head dim 64 or 128, no
- * ALiBi or softcap, 16-byte K/V rows, an 8-byte aligned mask) decodes on the matrix
- * cores in 128-row splits. max_bias and logit_softcap follow ops.cpp:8532-8768. Query
- * rounding follows the CPU path taken for that S (fp16 for S < 64, fp32 for
- * S >= 64); accumulation is fp32. Decode launches (few query vectors per kv head)
- * merge their KV splits inside the kernel through per-device arrival counters, so
- * two of them must not run concurrently on one device (issue them on one stream). */
+ * ALiBi or softcap, 16-byte K/V rows, an 8-byte aligned mask and n_kv % 4 == 0 when a
+ * mask is given) decodes on the matrix cores in 128-row splits. max_bias and
+ * logit_softcap follow ops.cpp:8532-8768. Query rounding follows the CPU path taken for
+ * that S (fp16 for S < 64, fp32 for S >= 64); accumulation is fp32. Decode launches
+ * (few query vectors per kv head) merge their KV splits inside the kernel through
+ * arrival counters that belong to the launch's stream (16 streams per process have
+ * their own; launches on further streams merge in a second launch), so calls on
+ * different streams may overlap; graphs captured on one stream must not be replayed
+ * concurrently. */
 size_t gq_flash_attn_ext_workspace_size(const gq_tensor* q, const gq_tensor* k);
 int gq_flash_attn_ext(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v,
                       const gq_tensor* mask, float scale, float max_bias, float logit_softcap,
@@ -252,11 +255,12 @@ int gq_flash_attn_ext_noalloc(const gq_tensor* q, const gq_tensor* k, const gq_t
                               const gq_tensor* mask, float scale, float max_bias, float logit_softcap,
                               gq_tensor* dst, gq_stream_t stream);
 
-/* Zeroes the per-device arrival counters of the decode kernels' in-kernel split
- * merge (a fill kernel on `stream`, safe inside graph capture). Every completed
- * launch leaves them at zero; a caller whose decode attention launch did not run to
- * completion (an aborted graph, an error between capture and replay) calls this on
- * the device before its next decode attention. No counterpart in the reference. */
+/* Zeroes the arrival counters of the decode kernels' in-kernel split merge (every
+ * stream's set on the current device; a fill kernel on `stream`, safe inside graph
+ * capture). Every completed launch leaves them at zero; a caller whose decode attention
+ * launch did not run to completion (an aborted graph, an error between capture and
+ * replay) calls this on the device, with no decode attention in flight, before its next
+ * decode attention. No counterpart in the reference. */
 int gq_attn_reset_counters(gq_stream_t stream);
 
 /* ---- SOFT_MAX ----------------------------------------------------------- */

@@ -660,7 +660,7 @@ def test_flash_attn_decode_workspace_and_replays(Hq, Hkv, D, S, pos, ctx):
     (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, 34 splits
     (15, 5, 64, 1, 700, 1024),      # SmolLM2 shape
 ])
-def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx):
+def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx):  # noqa: PLR0913
     """The decode kernel merges its split partials itself (the last workgroup of each
     kv head, counted on a device counter); that gives the bits of the separate merge
     launch (gq_set_option GQ_OPT_ATTN_SEPARATE_MERGE), call after call."""
@@ -687,12 +687,16 @@ def test_flash_attn_fused_merge_bits(Hq, Hkv, D, S, pos, ctx):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,n_kv", [(12, 2, 128, 1000), (24, 4, 64, 700), (16, 1, 128, 130),
-                                            (10, 2, 128, 3000), (15, 5, 64, 700), (16, 8, 128, 1300)])
+                                            (10, 2, 128, 3000), (15, 5, 64, 700), (16, 8, 128, 1300),
+                                            # odd lengths: the VALU kernel (the matrix-core one
+                                            # reads the mask 4 keys per load)
+                                            (12, 2, 128, 131), (6, 2, 64, 1001), (8, 4, 128, 1001),
+                                            (15, 5, 64, 131), (10, 2, 128, 1002)])
 def test_flash_attn_decode_many_heads_per_kv_masked_vs_exact(Hq, Hkv, D, n_kv):
     """One query row with 2..16 query heads per kv head (the matrix-core decode kernel over
     the contiguous cache, the KQ mask added to the scores) against the exact softmax in
     float64: -inf holes, a fully masked 256-row span, -32768 entries, n_kv not a multiple of
-    128 and a cache longer than the view."""
+    128 and a cache longer than the view; a -inf on the last key (the mask's last element)."""
     rng = np.random.default_rng(Hq * D + n_kv)
     ctx = n_kv + 64
     kc = f16(rng.standard_normal((Hkv, ctx, D)))
@@ -704,6 +708,7 @@ def test_flash_attn_decode_many_heads_per_kv_masked_vs_exact(Hq, Hkv, D, n_kv):
         mask[128:384] = -np.inf
     mask[rng.random(n_kv) < 0.05] = -32768.0
     mask[0] = 0.0
+    mask[n_kv - 1] = -np.inf
     scale = 1.0 / np.sqrt(D)
     kd = to_dev(kc).view(torch.float16)[:, :n_kv]
     vd = to_dev(vc).view(torch.float16)[:, :n_kv]
@@ -818,3 +823,33 @@ def test_flash_attn_config_goldens(golden_dir):
             assert mar(got, r) <= max(spread, dev + mar(got, exact)), (f.name, t)
             assert mar(got, r) < dev + 1e-3, (f.name, t)
         print(" | ".join(line))
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,pos,ctx", [(32, 32, 128, 1100, 2048), (15, 5, 64, 700, 1024)])
+def test_flash_attn_decode_on_two_streams(Hq, Hkv, D, pos, ctx):
+    """Decode attention issued on two streams at once, each with its own workspace (the
+    in-kernel split merge counts arrivals per stream): every output has the bits of the
+    same call run alone."""
+    rng = np.random.default_rng(Hq + D)
+    n_kv = O.pad_kv_len(pos + 1, ctx)
+    mask = to_dev(O.causal_mask_f16(pos, 1, n_kv)).view(torch.float16)
+    scale = 1.0 / np.sqrt(D)
+    inputs = []
+    for _ in range(2):
+        kc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
+        vc = to_dev(f16(rng.standard_normal((Hkv, ctx, D)))).view(torch.float16)[:, :n_kv]
+        inputs.append((to_dev(rng.standard_normal((Hq, 1, D)).astype(np.float32)), kc, vc))
+    alone = [ops.flash_attn_ext(q, k, v, mask, scale) for q, k, v in inputs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wss = [ops.Workspace(torch.device(DEV)), ops.Workspace(torch.device(DEV))]
+    outs = [[], []]
+    for _ in range(24):
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                q, k, v = inputs[i]
+                outs[i].append(ops.flash_attn_ext(q, k, v, mask, scale, ws=wss[i]))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for o in outs[i]:
+            assert torch.equal(o, alone[i]), i

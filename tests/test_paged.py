@@ -66,6 +66,16 @@ def _init():
     (64, 4, 4, 256, [1000, 999, 513, 17, 256, 2, 700, 64]),
     (64, 32, 4, 128, [300, 1, 129, 0, 511]),     # 8 query heads per kv head (matrix-core kernel)
     (128, 16, 1, 256, [1000, 257, 3]),           # 16 per kv head, 256-row pages
+    # 2..4 query heads per kv head on the matrix-core kernel
+    (128, 12, 4, 128, [700, 1, 1300, 0, 129]),   # G = 3, the 12/4 x 128 shape
+    (128, 16, 8, 256, [513, 900, 2, 256]),       # G = 2
+    (64, 8, 4, 128, [300, 128, 0, 77]),          # G = 2, 64-dim heads
+    (128, 16, 4, 128, [40, 17, 128, 99]),        # G = 4
+    # one split (max_len <= 128): outputs written by the kernel itself, a sequence of
+    # length 0 among them (zeros), into a NaN-filled output
+    (128, 12, 4, 128, [100, 0, 128, 1]),         # G = 3
+    (64, 8, 4, 128, [0, 64, 0]),                 # G = 2
+    (128, 8, 2, 128, [3, 0]),                    # G = 4
 ])
 def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
     import torch
@@ -104,8 +114,9 @@ def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
     q = rng.standard_normal((Hq, B, D)).astype(np.float32)
     scale = 1.0 / math.sqrt(D)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    out = torch.full((B, Hq, D), float("nan"), dtype=torch.float32, device=dev)
     out = ops.flash_attn_paged(t(q), t(k_pool), t(v_pool), t(table), t(np.array(lens, np.int32)), P, max(lens),
-                               scale).cpu().numpy()
+                               scale, out=out).cpu().numpy()
     q16 = q.astype(np.float16).astype(np.float32)
     worst = 0.0
     for b, n in enumerate(lens):
@@ -130,6 +141,8 @@ def test_flash_attn_paged_vs_exact(D, Hq, Hkv, P, lens):
     (128, 12, 2, [2079, 3260, 1, 0, 652, 1167, 300, 945, 129, 128, 2105, 840, 763, 1452, 3882, 1174], O.Q8_0),
     (128, 12, 2, [700, 5, 1300, 257, 64, 900], O.Q8_0),
     (64, 32, 4, [500, 1, 129, 1000, 384], O.Q4_0),   # 8 q heads per kv head, K = 2048
+    (128, 12, 4, [700, 0, 1300, 129, 3], O.Q8_0),    # 3 q heads per kv head, K = 1536
+    (128, 16, 8, [900, 256, 5, 700, 130], O.Q4_0),   # 2 per kv head, K = 2048
 ])
 def test_flash_attn_paged_q8_feeds_o_projection(D, Hq, Hkv, lens, qtype):
     """gq_flash_attn_paged_q8 writes the same fp32 rows as gq_flash_attn_paged and, from

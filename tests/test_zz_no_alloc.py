@@ -1,7 +1,8 @@
 """gq_flash_attn_ext_noalloc (the allocation-free decode attention: split partials in a
 static per-device array) against gq_flash_attn_ext with a caller workspace, through the
 C ABI: the same bits, on calls in a row whose second one is smaller than the first, and
-across the three launch plans that use partials (in-kernel merge, separate merge, tiled).
+across the launch plans that use partials (the matrix-core decode with its merge launch,
+the VALU decode with its merge in the kernel or in a separate launch, the tiled kernel).
 """
 
 from __future__ import annotations
@@ -53,7 +54,8 @@ def _init():
 
 # (Hq, Hkv, D, S, pos, ctx): each case is run after the one before it, larger first
 CASES = [
-    (12, 2, 128, 1, 4000, 4352),   # GQA 6 decode: 64 splits, separate merge
+    (12, 2, 128, 1, 4000, 4352),   # GQA 6 decode: the matrix-core route, 32 splits of 128 rows
+    (8, 8, 64, 1, 8000, 8192),     # MHA decode (VALU kernel): 32 splits, the separate merge launch
     (32, 32, 128, 1, 1100, 2048),  # 7B decode: 9 splits merged in the kernel
     (32, 32, 128, 16, 300, 1024),  # 16 rows: the tiled kernel with partials
     (15, 5, 64, 1, 200, 512),      # SmolLM2 decode, smallest
