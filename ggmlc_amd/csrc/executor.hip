@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdint>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -472,6 +473,9 @@ struct Gguf {
         need(sz);
         pos += sz;
     }
+    // bytes of a tensor of ne elements (ne already checked: non-negative, a product that
+    // fits int64), refusing sizes that do not fit a size_t; 0 for types this loader
+    // does not know
     static uint64_t type_nbytes(int type, const int64_t* ne) {
         int64_t blk = 1, bs = 0;
         switch (type) {
@@ -486,9 +490,10 @@ struct Gguf {
             default: return 0;
         }
         if (ne[0] % blk) raise(GQ_ERR_INVALID, "GGUF: rows of partial blocks");
-        uint64_t n = (uint64_t)(ne[0] / blk) * bs;
-        for (int i = 1; i < 4; ++i) n *= (uint64_t)ne[i];
-        return n;
+        uint64_t n = (uint64_t)(ne[0] / blk);
+        for (int i = 1; i < 4; ++i) n *= (uint64_t)ne[i];  // <= the element count: no wrap
+        if (n > (uint64_t)SIZE_MAX / (uint64_t)bs) raise(GQ_ERR_INVALID, "GGUF: tensor byte size overflows");
+        return n * (uint64_t)bs;
     }
 
     void parse() {
@@ -516,7 +521,17 @@ struct Gguf {
             ti.name = rstr();
             const uint32_t nd = rd<uint32_t>();
             if (nd > 4) raise(GQ_ERR_INVALID, "GGUF: more than 4 dimensions");
-            for (uint32_t d = 0; d < nd; ++d) ti.ne[d] = (int64_t)rd<uint64_t>();
+            for (uint32_t d = 0; d < nd; ++d) {
+                ti.ne[d] = (int64_t)rd<uint64_t>();
+                if (ti.ne[d] < 0) raise(GQ_ERR_INVALID, "GGUF: negative dimension in tensor " + ti.name);
+            }
+            // the element count must be an int64 (ggml_nelements)
+            int64_t nel = 1;
+            for (int d = 0; d < 4; ++d) {
+                if (ti.ne[d] != 0 && nel > INT64_MAX / ti.ne[d])
+                    raise(GQ_ERR_INVALID, "GGUF: element count of tensor " + ti.name + " overflows");
+                nel *= ti.ne[d];
+            }
             ti.type = (int)rd<uint32_t>();
             ti.offset = rd<uint64_t>();
             ti.nbytes = type_nbytes(ti.type, ti.ne);
@@ -524,10 +539,12 @@ struct Gguf {
             tensors[ti.name] = ti;
         }
         data_start = (pos + alignment - 1) / alignment * alignment;
+        // every comparison below is free of wrap-around: data = bytes after data_start
+        const uint64_t data = data_start <= buf.size() ? buf.size() - data_start : 0;
         for (const auto& kv : tensors) {
             const GgufTensor& ti = kv.second;
             if (ti.offset % alignment) raise(GQ_ERR_INVALID, "GGUF: unaligned tensor " + ti.name);
-            if (data_start + ti.offset + ti.nbytes > buf.size())
+            if (ti.offset > data || ti.nbytes > data - ti.offset)
                 raise(GQ_ERR_INVALID, "GGUF: tensor " + ti.name + " runs past the end of the file");
         }
     }

@@ -306,6 +306,44 @@ def test_native_executor_rejects_bad_files(tmp_path):
     assert e.value.code == -2  # GQ_ERR_UNSUPPORTED
 
 
+def _one_tensor_gguf(ne, ggml_type=8, offset=0, data=b""):
+    """A GGUF v3 file holding one tensor info with the raw dims ne (u64 each)."""
+    import struct
+
+    name = b"w"
+    head = b"GGUF" + struct.pack("<IQQ", 3, 1, 0)
+    info = struct.pack("<Q", len(name)) + name + struct.pack("<I", len(ne))
+    info += b"".join(struct.pack("<Q", d & (2**64 - 1)) for d in ne)
+    info += struct.pack("<IQ", ggml_type, offset)
+    raw = head + info
+    return raw + b"\0" * (-len(raw) % 32) + data
+
+
+@pytest.mark.parametrize("ne,what", [
+    ([32, -1], "negative dimension"),
+    ([-32, 4], "negative dimension"),
+    ([2**40, 2**40], "element count"),                # 2^80 elements
+    ([32, 2**31, 2**31, 4], "element count"),          # 2^69
+    ([2**62, 4], "element count"),
+    ([32, 2**59], "element count"),                   # 2^64 elements
+    ([32, 2**56], "past the end"),                    # 2.4e18 bytes: no wrap, far past the file
+    ([64, 1], "past the end"),                        # two blocks declared, one present
+    ([2**61, 2, 1, 1, 28], "byte size"),              # F64: 2^62 elements of 8 bytes, past 2^64
+])
+def test_native_gguf_rejects_bad_dimensions(ne, what):
+    """gq_exec's GGUF reader refuses negative dims, element counts past int64 and byte sizes
+    that wrap (the reference's gguf.cpp:682-735 refuses the same), before any size is
+    used; a tensor whose bytes run past the file is refused with overflow-free checks."""
+    from ggmlc_amd import _lib
+    from ggmlc_amd.executor import inspect
+
+    ggml_type = 8  # Q8_0, or the fifth entry
+    if len(ne) == 5:
+        ne, ggml_type = ne[:4], ne[4]
+    with pytest.raises(_lib.GQError, match=what):
+        inspect(_one_tensor_gguf(ne, ggml_type, data=b"\x01" * 34))
+
+
 @needs_ref
 @pytest.mark.skipif(not O.ref_v4_usable(), reason="AVX-512 reference build absent or host lacks AVX-512 VNNI")
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_0])
