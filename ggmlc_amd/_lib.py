@@ -57,6 +57,20 @@ class gq_rope_kv_epilogue(ctypes.Structure):
     ]
 
 
+class gq_exec_profile(ctypes.Structure):
+    _fields_ = [
+        ("prepare_ms", ctypes.c_double),
+        ("set_decode_pos_ms", ctypes.c_double),
+        ("set_chunk_pos_ms", ctypes.c_double),
+        ("mask_fill_ms", ctypes.c_double),
+        ("run_ms", ctypes.c_double),
+        ("n_prepare", ctypes.c_int32),
+        ("n_set_decode_pos", ctypes.c_int32),
+        ("n_set_chunk_pos", ctypes.c_int32),
+        ("n_run", ctypes.c_int32),
+    ]
+
+
 class gq_mul_mat_fusion(ctypes.Structure):
     _fields_ = [
         ("rms_norm", ctypes.c_int32),
@@ -141,6 +155,28 @@ SIGNATURES = {
     "gq_exec_logits_last_only": (ctypes.c_int, [_vp]),
     "gq_exec_set_enable_graphs": (ctypes.c_int, [_vp, ctypes.c_int]),
     "gq_exec_position": (_i64, [_vp]),
+    "gq_exec_set_tokens_per_page": (ctypes.c_int, [_vp, _i64]),
+    "gq_exec_get_tokens_per_page": (_i64, [_vp]),
+    "gq_exec_init_paged_kv_cache": (ctypes.c_int, [_vp, _i64, _i64]),
+    "gq_exec_is_paged_kv_cache_enabled": (ctypes.c_int, [_vp]),
+    "gq_exec_paged_kv_alloc_slot": (ctypes.c_int, [_vp, _i64]),
+    "gq_exec_paged_kv_free_slot": (ctypes.c_int, [_vp, _i64]),
+    "gq_exec_is_paged_slot_allocated": (ctypes.c_int, [_vp, _i64]),
+    "gq_exec_paged_kv_ensure_tokens": (ctypes.c_int, [_vp, _i64, _i64]),
+    "gq_exec_paged_kv_map_existing_pages": (ctypes.c_int, [_vp, _i64, _i64, ctypes.POINTER(ctypes.c_int32), _i64]),
+    "gq_exec_paged_kv_extract_page": (ctypes.c_int, [_vp, _i64, _i64, ctypes.POINTER(ctypes.c_int32)]),
+    "gq_exec_paged_page_retain": (ctypes.c_int, [_vp, ctypes.c_int32]),
+    "gq_exec_paged_page_release": (ctypes.c_int, [_vp, ctypes.c_int32]),
+    "gq_exec_get_paged_active_vram_bytes": (ctypes.c_size_t, [_vp]),
+    "gq_exec_paged_slot_position": (ctypes.c_int, [_vp, _i64, ctypes.POINTER(_i64)]),
+    "gq_exec_paged_set_slot_position": (ctypes.c_int, [_vp, _i64, _i64]),
+    "gq_exec_set_enable_profile": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "gq_exec_reset_profile": (ctypes.c_int, [_vp]),
+    "gq_exec_get_profile": (ctypes.c_int, [_vp, ctypes.POINTER(gq_exec_profile)]),
+    "gq_exec_runtime_graph_summary": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_size_t,
+                                                     ctypes.POINTER(ctypes.c_size_t)]),
+    "gq_exec_runtime_mul_mat_shape_summary": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_size_t,
+                                                             ctypes.POINTER(ctypes.c_size_t)]),
 }
 
 _lib = None

@@ -7,6 +7,7 @@
 // their concrete shapes, the persistent KV cache (init/reset/has), logits_last_only.
 // Host code only; no torch. Every launch goes through the validated gq_* entry points.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdint>
@@ -838,9 +839,13 @@ struct QW {  // a device-resident block-quantized weight
     }
 };
 
-int64_t pad_kv_len(int64_t n, int64_t max_ctx) {  // executor.cpp:58-64 with n_pad = 256
+// the batched decode's attention launches are sized for max_len rounded up to this many rows
+constexpr int64_t PAGED_BUCKET = 512;
+
+int64_t pad_kv_len(int64_t n, int64_t max_ctx, int64_t n_pad) {  // executor.cpp:58-64
     n = std::max<int64_t>(n, 1);
-    return std::min(std::max<int64_t>(256, (n + 255) / 256 * 256), max_ctx);
+    if (n_pad <= 1) return std::min(n, max_ctx);
+    return std::min(std::max<int64_t>(n_pad, (n + n_pad - 1) / n_pad * n_pad), max_ctx);
 }
 
 // the graph's surface and the matched decoder as JSON (gq_exec_describe / gq_exec_inspect)
@@ -945,12 +950,57 @@ struct Executor {
         float* rope_cs;
         uint16_t* mask;
         int64_t rows_cap;  // logits rows allocated
+        int32_t* seq_len;       // paged decode: each row's rows to attend
+        uint8_t *q8_o, *q8_d;   // int8 path: the o and down projections' quantized input rows
     };
     std::map<int64_t, Bufs> bufs;
-    std::map<std::tuple<int64_t, int64_t, int64_t>, hipGraphExec_t> graphs;
+    std::map<std::tuple<int64_t, int64_t, int64_t>, std::pair<hipGraphExec_t, int64_t>> graphs;  // and its node count
     std::vector<hipGraph_t> graph_defs;
     std::vector<float> out_host;  // the last run's logits, [rows][vocab]
     int64_t out_rows = 0;
+    // the n_kv bucket pad: GGMLC_KV_PAD when init_kv_cache runs (executor.cpp:501-503), else 256
+    int64_t kv_n_pad = 256;
+
+    // -- paged KV (executor.cpp:634-920) -------------------------------------------------
+    // Per layer one K and one V pool, F16 [Hkv][n_pages * P][hd]: page p is rows
+    // [p P, (p + 1) P) of every layer's pools, so one page id names a token range in all
+    // layers. Slot tables list each slot's pages (device I32 [max_batch][max_pages], -1:
+    // none); page 0 takes the KV writes of batch rows whose slot has no page. Pages are
+    // reference counted: a slot holds one reference per listed page, and callers that
+    // keep pages beyond their slot (a prefix cache) take their own. A slot's prompt is
+    // computed on the contiguous cache (the single-sequence step and its graphs), with
+    // the slot's earlier rows copied in and the computed rows copied out to its pages;
+    // a batched decode step runs every slot of [0, b) at its own position.
+    struct Paged {
+        bool on = false;
+        int64_t P = 128, max_batch = 0, max_ctx = 0, max_pages = 0, n_pages = 0;
+        uint16_t* pool = nullptr;
+        int32_t* table = nullptr;
+        std::vector<int32_t> table_host;
+        std::vector<std::vector<int32_t>> pages;
+        std::vector<char> active, dirty;
+        std::vector<int32_t> refs;
+        std::vector<int32_t> free_pages;  // popped from the back: lowest ids first
+        int32_t* pos = nullptr;           // device: each slot's next position
+        std::vector<int32_t> pos_host;
+        int32_t* list = nullptr;          // device: one slot's page ids (row copies)
+        std::vector<int32_t> list_host;
+        int contig_slot = -1;             // the slot whose rows [0, contig_rows) the contiguous cache holds
+        int64_t contig_rows = 0;
+    } pg;
+    int slot = -1;       // prepared paged step: >= 0 a prompt step of that slot, -1 a batched decode
+    int64_t nb = 1;      // prepared paged step: batch rows (symbol b)
+    bool paged_step = false;
+    std::map<std::tuple<int64_t, int64_t>, std::pair<hipGraphExec_t, int64_t>> paged_graphs;  // (b, max_len)
+
+    // -- profiling (set_enable_profile / get_profile / runtime_graph_summary /
+    // runtime_mul_mat_shape_summary, executor.h:101-118) -----------------------------------
+    bool profile_on = false;
+    double prof_prepare_ms = 0.0, prof_run_ms = 0.0;
+    int64_t prof_n_prepare = 0, prof_n_run = 0;
+    std::map<std::string, int64_t> op_hist, mm_shapes, fa_shapes;  // launches of the last issued step
+    int64_t last_nodes = -1;  // kernel nodes of the graph the last run replayed (-1: eager)
+    void count(const std::string& op) { ++op_hist[op]; }
 
     int64_t E() const { return m.n_embd; }
     int64_t nq() const { return (m.n_head + 2 * m.n_head_kv) * m.hd; }
@@ -1013,6 +1063,7 @@ struct Executor {
     void init_kv(int64_t ctx) {
         if (ctx <= 0) raise(GQ_ERR_INVALID, "init_kv_cache: max_ctx must be positive");
         if (kv_on) return;
+        if (const char* env = std::getenv("GGMLC_KV_PAD")) kv_n_pad = std::max<int64_t>(1, std::atoll(env));
         drop_graphs();
         const size_t bytes = 2 * layers.size() * (size_t)m.n_head_kv * ctx * m.hd * 2;
         kv = static_cast<uint16_t*>(dmalloc(bytes));
@@ -1027,13 +1078,181 @@ struct Executor {
                "hipMemsetAsync");
         hip_ok(hipMemsetAsync(pos_dev, 0, 4, stream), "hipMemsetAsync");
         hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        pg.contig_slot = -1;  // the contiguous cache no longer holds a slot's rows
     }
     uint16_t* kc(size_t l) const { return kv + (2 * l) * (size_t)m.n_head_kv * max_ctx * m.hd; }
     uint16_t* vc(size_t l) const { return kv + (2 * l + 1) * (size_t)m.n_head_kv * max_ctx * m.hd; }
+    size_t pool_elems() const { return (size_t)m.n_head_kv * pg.n_pages * pg.P * m.hd; }
+    uint16_t* kp(size_t l) const { return pg.pool + (2 * l) * pool_elems(); }
+    uint16_t* vp(size_t l) const { return pg.pool + (2 * l + 1) * pool_elems(); }
+
+    void set_tokens_per_page(int64_t n) {
+        if (pg.on) raise(GQ_ERR_INVALID, "set_tokens_per_page: the paged cache is already initialised");
+        // the attention kernels take pages of a power of two >= 64 rows (>= 128 for 64-dim heads)
+        if (n < 64 || (n & (n - 1)) || (m.hd == 64 && n < 128))
+            raise(GQ_ERR_INVALID, "tokens_per_page must be a power of two >= 64 (>= 128 for head_dim 64)");
+        pg.P = n;
+    }
+
+    void init_paged(int64_t max_batch, int64_t ctx) {
+        if (pg.on) return;  // executor.cpp:635
+        if (max_batch <= 0 || max_batch > 256) raise(GQ_ERR_INVALID, "init_paged_kv_cache: max_batch must be 1..256");
+        if (ctx <= 0) raise(GQ_ERR_INVALID, "init_paged_kv_cache: max_ctx must be positive");
+        if (kv_on && max_ctx < ctx)
+            raise(GQ_ERR_INVALID, "init_paged_kv_cache: max_ctx above the contiguous cache's (" +
+                                      std::to_string(max_ctx) + ")");
+        if (!kv_on) init_kv(ctx);  // the prompt steps' contiguous cache
+        Paged& p = pg;
+        p.max_batch = max_batch, p.max_ctx = ctx;
+        p.max_pages = (ctx + p.P - 1) / p.P;
+        p.n_pages = max_batch * p.max_pages + 1;
+        if ((int64_t)p.n_pages * p.P * m.hd * 2 >= ((int64_t)1 << 31))
+            raise(GQ_ERR_UNSUPPORTED, "init_paged_kv_cache: one head of a pool must stay below 2 GiB");
+        drop_graphs();
+        p.pool = static_cast<uint16_t*>(dmalloc(2 * layers.size() * pool_elems() * 2));
+        hip_ok(hipMemsetAsync(p.pool, 0, 2 * layers.size() * pool_elems() * 2, stream), "hipMemsetAsync");
+        p.table = static_cast<int32_t*>(dmalloc((size_t)max_batch * p.max_pages * 4));
+        hip_ok(hipMemsetAsync(p.table, 0xff, (size_t)max_batch * p.max_pages * 4, stream), "hipMemsetAsync");
+        p.pos = static_cast<int32_t*>(dmalloc((size_t)max_batch * 4));
+        hip_ok(hipMemsetAsync(p.pos, 0, (size_t)max_batch * 4, stream), "hipMemsetAsync");
+        p.list = static_cast<int32_t*>(dmalloc((size_t)p.max_pages * 4));
+        p.table_host.assign((size_t)max_batch * p.max_pages, -1);
+        p.pages.assign((size_t)max_batch, {});
+        p.active.assign((size_t)max_batch, 0);
+        p.dirty.assign((size_t)max_batch, 0);
+        p.pos_host.assign((size_t)max_batch, 0);
+        p.list_host.assign((size_t)p.max_pages, -1);
+        p.refs.assign((size_t)p.n_pages, 0);
+        p.refs[0] = 1;  // the trash page is never handed out
+        p.free_pages.clear();
+        for (int64_t i = p.n_pages - 1; i >= 1; --i) p.free_pages.push_back((int32_t)i);
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        p.on = true;
+    }
+    void need_paged() const {
+        if (!pg.on) raise(GQ_ERR_INVALID, "init_paged_kv_cache first");
+    }
+    void check_slot(int64_t sl) const {
+        need_paged();
+        if (sl < 0 || sl >= pg.max_batch)
+            raise(GQ_ERR_INVALID, "slot " + std::to_string(sl) + " outside [0, " + std::to_string(pg.max_batch) + ")");
+    }
+    void set_slot_pos(int64_t sl, int64_t p) {
+        pg.pos_host[(size_t)sl] = (int32_t)p;
+        hip_ok(hipMemcpyAsync(pg.pos + sl, &pg.pos_host[(size_t)sl], 4, hipMemcpyHostToDevice, stream), "pos upload");
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");  // the host value may change next
+    }
+    void set_row(int64_t sl) {
+        int32_t* row = &pg.table_host[(size_t)sl * pg.max_pages];
+        std::fill(row, row + pg.max_pages, -1);
+        std::copy(pg.pages[(size_t)sl].begin(), pg.pages[(size_t)sl].end(), row);
+        pg.dirty[(size_t)sl] = 1;
+    }
+    void sync_tables() {
+        bool any = false;
+        for (int64_t sl = 0; sl < pg.max_batch; ++sl) {
+            if (!pg.dirty[(size_t)sl]) continue;
+            hip_ok(hipMemcpyAsync(pg.table + sl * pg.max_pages, &pg.table_host[(size_t)sl * pg.max_pages],
+                                  (size_t)pg.max_pages * 4, hipMemcpyHostToDevice, stream),
+                   "page table upload");
+            pg.dirty[(size_t)sl] = 0;
+            any = true;
+        }
+        if (any) hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    }
+    void release_page(int32_t id) {
+        if (id <= 0 || id >= pg.n_pages || pg.refs[(size_t)id] <= 0)
+            raise(GQ_ERR_INVALID, "page " + std::to_string(id) + " is not in use");
+        if (--pg.refs[(size_t)id] == 0) pg.free_pages.push_back(id);
+    }
+    void retain_page(int32_t id) {
+        if (id <= 0 || id >= pg.n_pages || pg.refs[(size_t)id] <= 0)
+            raise(GQ_ERR_INVALID, "page " + std::to_string(id) + " is not in use");
+        ++pg.refs[(size_t)id];
+    }
+    void alloc_slot(int64_t sl) {  // executor.cpp:738-765
+        check_slot(sl);
+        if (pg.active[(size_t)sl]) free_slot(sl);
+        pg.active[(size_t)sl] = 1;
+        set_slot_pos(sl, 0);
+    }
+    void free_slot(int64_t sl) {  // executor.cpp:767-803
+        check_slot(sl);
+        for (int32_t id : pg.pages[(size_t)sl]) release_page(id);
+        pg.pages[(size_t)sl].clear();
+        pg.active[(size_t)sl] = 0;
+        set_row(sl);
+        if (pg.contig_slot == sl) pg.contig_slot = -1;
+    }
+    void ensure_tokens(int64_t sl, int64_t total) {  // executor.cpp:812-851
+        check_slot(sl);
+        if (!pg.active[(size_t)sl]) raise(GQ_ERR_INVALID, "slot " + std::to_string(sl) + " is not allocated");
+        if (total < 0 || total > pg.max_ctx)
+            raise(GQ_ERR_INVALID, std::to_string(total) + " tokens exceed the slots' max_ctx (" +
+                                      std::to_string(pg.max_ctx) + ")");
+        auto& pl = pg.pages[(size_t)sl];
+        const size_t need = (size_t)((total + pg.P - 1) / pg.P);
+        if (pl.size() >= need) return;
+        if (pg.free_pages.size() < need - pl.size())
+            raise(GQ_ERR_WORKSPACE, "the page pool has " + std::to_string(pg.free_pages.size()) + " free pages, " +
+                                        std::to_string(need - pl.size()) + " needed");
+        while (pl.size() < need) {
+            const int32_t id = pg.free_pages.back();
+            pg.free_pages.pop_back();
+            pg.refs[(size_t)id] = 1;
+            pl.push_back(id);
+        }
+        set_row(sl);
+    }
+    void map_pages(int64_t sl, int64_t start, const int32_t* ids, int64_t n) {  // executor.cpp:853-897
+        check_slot(sl);
+        if (!pg.active[(size_t)sl]) raise(GQ_ERR_INVALID, "slot " + std::to_string(sl) + " is not allocated");
+        auto& pl = pg.pages[(size_t)sl];
+        if (start != (int64_t)pl.size()) raise(GQ_ERR_INVALID, "shared pages must continue the slot's page list");
+        if (n < 0 || (n && !ids) || (int64_t)pl.size() + n > pg.max_pages)
+            raise(GQ_ERR_INVALID, "map_existing_pages: bad page list");
+        for (int64_t i = 0; i < n; ++i) retain_page(ids[i]);  // validates every id first
+        for (int64_t i = 0; i < n; ++i) pl.push_back(ids[i]);
+        set_row(sl);
+        if (pg.contig_slot == sl) pg.contig_slot = -1;
+    }
+    int32_t page_of(int64_t sl, int64_t idx) const {  // executor.cpp:899-920
+        check_slot(sl);
+        const auto& pl = pg.pages[(size_t)sl];
+        if (idx < 0 || idx >= (int64_t)pl.size())
+            raise(GQ_ERR_INVALID, "slot " + std::to_string(sl) + " has no page " + std::to_string(idx));
+        return pl[(size_t)idx];
+    }
+    size_t active_bytes() const {
+        if (!pg.on) return 0;
+        int64_t used = 0;
+        for (int64_t i = 1; i < pg.n_pages; ++i) used += pg.refs[(size_t)i] > 0;
+        return (size_t)used * 2 * layers.size() * m.n_head_kv * pg.P * m.hd * 2;
+    }
+    // rows [r0, r1) of slot sl between its pages and the contiguous cache, every layer
+    void copy_rows(int64_t sl, int64_t r0, int64_t r1, int to_pool) {
+        if (r1 <= r0) return;
+        const auto& pl = pg.pages[(size_t)sl];
+        std::fill(pg.list_host.begin(), pg.list_host.end(), -1);
+        std::copy(pl.begin(), pl.end(), pg.list_host.begin());
+        hip_ok(hipMemcpyAsync(pg.list, pg.list_host.data(), (size_t)pg.max_pages * 4, hipMemcpyHostToDevice, stream),
+               "page list upload");
+        const int64_t rows = pg.n_pages * pg.P, hd = m.hd, Hkv = m.n_head_kv;
+        for (size_t l = 0; l < layers.size(); ++l) {
+            for (int kvi = 0; kvi < 2; ++kvi) {
+                gq_tensor pool = desc(kvi ? vp(l) : kp(l), GQ_TYPE_F16, hd, rows, Hkv);
+                gq_tensor cache = desc(kvi ? vc(l) : kc(l), GQ_TYPE_F16, hd, max_ctx, Hkv);
+                gq_ok(gq_kv_pages_copy(&pool, &cache, pg.list, (int64_t)pl.size(), pg.P, r0, r1, to_pool, stream));
+            }
+        }
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");  // the page list may change next
+    }
 
     void drop_graphs() {
-        for (auto& kvp : graphs) (void)hipGraphExecDestroy(kvp.second);
+        for (auto& kvp : graphs) (void)hipGraphExecDestroy(kvp.second.first);
         graphs.clear();
+        for (auto& kvp : paged_graphs) (void)hipGraphExecDestroy(kvp.second.first);
+        paged_graphs.clear();
         for (hipGraph_t g : graph_defs) (void)hipGraphDestroy(g);
         graph_defs.clear();
     }
@@ -1043,7 +1262,8 @@ struct Executor {
             Bufs& b = kvp.second;
             for (void* p : {(void*)b.ids, (void*)b.x, (void*)b.x_alt, (void*)b.h, (void*)b.qkv, (void*)b.q,
                             (void*)b.attn, (void*)b.proj, (void*)b.gu, (void*)b.act, (void*)b.logits, (void*)b.next,
-                            (void*)b.pos_ids, (void*)b.kv_idx, (void*)b.rope_cs, (void*)b.mask})
+                            (void*)b.pos_ids, (void*)b.kv_idx, (void*)b.rope_cs, (void*)b.mask, (void*)b.seq_len,
+                            (void*)b.q8_o, (void*)b.q8_d})
                 dfree(p);
         }
         bufs.clear();
@@ -1071,6 +1291,9 @@ struct Executor {
         b.kv_idx = static_cast<int64_t*>(dmalloc((size_t)n * 8));
         b.rope_cs = static_cast<float*>(dmalloc((size_t)n * m.hd * 4));
         b.mask = static_cast<uint16_t*>(dmalloc((size_t)n * max_ctx * 2));
+        b.seq_len = static_cast<int32_t*>(dmalloc((size_t)n * 4));
+        b.q8_o = static_cast<uint8_t*>(dmalloc(gq_q8_rows_bytes(qd())));
+        b.q8_d = static_cast<uint8_t*>(dmalloc(gq_q8_rows_bytes(m.n_ff)));
         return bufs.emplace(n, b).first->second;
     }
 
@@ -1091,11 +1314,19 @@ struct Executor {
         const Layer& L = layers[0];
         for (const QW* w : {&L.qkv, &L.o, &L.gate_up, &L.down}) mm(*w, n);
         mm(lm_head, rows);
-        for (int64_t nk = 256; nk < max_ctx + 256; nk += 256) {
+        const int64_t step = std::max<int64_t>(kv_n_pad, 1);
+        for (int64_t nk = step; nk < max_ctx + step; nk += step) {  // every n_kv bucket
             const int64_t nkv = std::min(nk, max_ctx);
             gq_tensor q = desc(nullptr, GQ_TYPE_F32, m.hd, n, m.n_head);
             gq_tensor k = desc(nullptr, GQ_TYPE_F16, m.hd, nkv, m.n_head_kv);
             need = std::max(need, gq_flash_attn_ext_workspace_size(&q, &k));
+        }
+        if (pg.on && n <= pg.max_batch) {  // the batched decode's paged attention
+            for (int64_t ml = PAGED_BUCKET; ml < pg.max_ctx + PAGED_BUCKET; ml += PAGED_BUCKET) {
+                gq_tensor q = desc(nullptr, GQ_TYPE_F32, m.hd, n, m.n_head, m.n_head * m.hd, m.hd);
+                gq_tensor k = desc(nullptr, GQ_TYPE_F16, m.hd, pg.n_pages * pg.P, m.n_head_kv);
+                need = std::max(need, gq_flash_attn_paged_workspace_size(&q, &k, std::min(ml, pg.max_ctx), pg.P));
+            }
         }
         if (need <= ws_bytes) return;
         if (ws) retired_ws.push_back(ws);
@@ -1106,6 +1337,18 @@ struct Executor {
     // -- one step: embedding -> layers -> RMS_NORM -> head on rows [r0, n) -> argmax ----
     void mm_fused(const QW& w, const float* x, int64_t xK, int64_t rows, float* dst, int64_t dN,
                   gq_mul_mat_fusion& f) {
+        std::string op = "MUL_MAT";
+        if (f.b_add) op = "ADD+" + op;
+        if (f.rms_norm) op = "RMS_NORM+" + op;
+        if (f.b_swiglu) op = "SWIGLU+" + op;
+        if (f.b_q8) op = "Q8_ROWS+" + op;
+        if (f.rope_kv) op += "+ROPE+SET_ROWS";
+        if (f.swiglu) op += "+SWIGLU";
+        if (f.out_q8) op += "+Q8_ROWS";
+        if (w.bias) op += "+ADD(bias)";
+        count(op);
+        ++mm_shapes[std::string(w.type == GQ_TYPE_Q8_0 ? "q8_0" : "q4_0") + " K=" + std::to_string(w.K) + " N=" +
+                    std::to_string(w.N) + " M=" + std::to_string(rows) + (f.int8 ? " int8" : "")];
         gq_tensor a = w.d();
         gq_tensor b = desc(x, GQ_TYPE_F32, xK, rows);
         gq_tensor d = desc(dst, GQ_TYPE_F32, dN, rows);
@@ -1118,21 +1361,24 @@ struct Executor {
 
     void forward(int64_t n, int64_t n_kv, int64_t r0) {
         Bufs& b = buffers(n);
+        op_hist.clear(), mm_shapes.clear(), fa_shapes.clear();
         const bool fused = n <= 4;  // one GEMV launch per projection with its graph neighbours
         const int64_t e = E(), hd = m.hd, Hq = m.n_head, Hkv = m.n_head_kv, F = m.n_ff, QD = qd(), NQ = nq();
         {
             gq_tensor mk = desc(b.mask, GQ_TYPE_F16, n_kv, n, 1, max_ctx);
             gq_ok(gq_kv_step_inputs(pos_dev, n, b.pos_ids, b.kv_idx, &mk, stream));
+            count("KV_STEP_INPUTS");
         }
         gq_tensor pos_t = desc(b.pos_ids, GQ_TYPE_I32, n);
         gq_tensor idx_t = desc(b.kv_idx, GQ_TYPE_I64, n);
         gq_tensor rcs = desc(b.rope_cs, GQ_TYPE_F32, hd, n);
-        if (fused) gq_ok(gq_rope_cache(&pos_t, (int)hd, m.rope_base, 1.0f, 1.0f, &rcs, stream));
+        if (fused) gq_ok(gq_rope_cache(&pos_t, (int)hd, m.rope_base, 1.0f, 1.0f, &rcs, stream)), count("ROPE_CACHE");
         {
             gq_tensor tab = embed.d();
             gq_tensor ids = desc(b.ids, GQ_TYPE_I32, n);
             gq_tensor xo = desc(b.x, GQ_TYPE_F32, e, n);
             gq_ok(gq_get_rows(&tab, &ids, &xo, stream));
+            count("GET_ROWS");
         }
         float* x = b.x;
         auto other = [&](float* p) { return p == b.x ? b.x_alt : b.x; };
@@ -1165,9 +1411,13 @@ struct Executor {
                 gq_tensor vv = desc(b.qkv + QD + Hkv * hd, GQ_TYPE_F32, hd, Hkv, n, hd, NQ);
                 gq_ok(gq_rope_kv_store(&qv, &kv_, &vv, &pos_t, (int)hd, 2, m.rope_base, 1.0f, 1.0f, &idx_t, &qo,
                                        &kcache, &vcache, nullptr, stream));
+                count("ROPE+SET_ROWS");
             }
             if (nx) x = nx;
             {  // FLASH_ATTN_EXT over the padded view [0, n_kv) of the cache
+                count("FLASH_ATTN_EXT");
+                ++fa_shapes["D=" + std::to_string(hd) + " Hq=" + std::to_string(Hq) + " Hkv=" + std::to_string(Hkv) +
+                            " S=" + std::to_string(n) + " n_kv=" + std::to_string(n_kv)];
                 gq_tensor q = desc(b.q, GQ_TYPE_F32, hd, n, Hq, Hq * hd, hd);
                 gq_tensor kview = desc(kc(l), GQ_TYPE_F16, hd, n_kv, Hkv, hd, max_ctx * hd);
                 gq_tensor vview = desc(vc(l), GQ_TYPE_F16, hd, n_kv, Hkv, hd, max_ctx * hd);
@@ -1210,66 +1460,220 @@ struct Executor {
         gq_tensor nt = desc(b.next, GQ_TYPE_I32, 1);
         gq_ok(gq_argmax(&last, &nt, stream));
         gq_ok(gq_kv_advance(pos_dev, n, stream));
+        count("ARGMAX"), count("KV_ADVANCE");
+    }
+
+    // whether every product of a layer takes the int8 path with the quantized-row handoffs
+    // (model.q8_chain_ok): K % 256 == 0, 16-byte aligned weights, gate|up rows % 64, QKV
+    // rows % 16, a power-of-two head_dim >= 16
+    bool q8_chain_ok() const {
+        if (m.hd < 16 || (m.hd & (m.hd - 1))) return false;
+        for (const Layer& L : layers) {
+            for (const QW* w : {&L.qkv, &L.o, &L.gate_up, &L.down})
+                if (w->K % 256 || reinterpret_cast<uintptr_t>(w->data) % 16) return false;
+            if (L.gate_up.N % 64 || L.qkv.N % 16) return false;
+        }
+        return true;
+    }
+
+    // One decode token for slots [0, B) over the paged pools (paged.BatchDecoder.step):
+    // row i runs the token ids[i] at position pg.pos[i], writes its K/V row into slot i's
+    // pages (page 0 when the slot has none) and attends to its rows [0, pos[i]]; every
+    // position then advances by one. 2..16 rows take the int8 chain where it applies (ROPE
+    // + SET_ROWS and SWIGLU in the products' epilogues, the split merge writing the o
+    // projection's quantized rows); up to 4 rows otherwise the fused GEMVs; the logits of
+    // every row.
+    void forward_paged(int64_t B, int64_t max_len) {
+        Bufs& b = buffers(B);
+        op_hist.clear(), mm_shapes.clear(), fa_shapes.clear();
+        const int64_t e = E(), hd = m.hd, Hq = m.n_head, Hkv = m.n_head_kv, F = m.n_ff, QD = qd(), NQ = nq();
+        const int64_t rows = pg.n_pages * pg.P;
+        const bool q8 = B > 1 && B <= 16 && q8_chain_ok() && Hq % Hkv == 0 && Hq / Hkv > 1 && Hq / Hkv <= 16 &&
+                        pg.P % 128 == 0 && max_len > 128;
+        const bool fused = !q8 && B <= 4;
+        gq_tensor tab_t = desc(pg.table, GQ_TYPE_I32, pg.max_pages, B);
+        gq_ok(gq_paged_step_inputs(pg.pos, B, &tab_t, pg.P, 0, b.kv_idx, b.seq_len, stream));
+        count("PAGED_STEP_INPUTS");
+        gq_tensor pos_t = desc(pg.pos, GQ_TYPE_I32, B);
+        gq_tensor idx_t = desc(b.kv_idx, GQ_TYPE_I64, B);
+        gq_tensor len_t = desc(b.seq_len, GQ_TYPE_I32, B);
+        gq_tensor rcs = desc(b.rope_cs, GQ_TYPE_F32, hd, B);
+        if (fused || q8) gq_ok(gq_rope_cache(&pos_t, (int)hd, m.rope_base, 1.0f, 1.0f, &rcs, stream)), count("ROPE_CACHE");
+        {
+            gq_tensor tab = embed.d();
+            gq_tensor ids = desc(b.ids, GQ_TYPE_I32, B);
+            gq_tensor xo = desc(b.x, GQ_TYPE_F32, e, B);
+            gq_ok(gq_get_rows(&tab, &ids, &xo, stream));
+            count("GET_ROWS");
+        }
+        float* x = b.x;
+        auto other = [&](float* p) { return p == b.x ? b.x_alt : b.x; };
+        float* pending = nullptr;
+        const float scale = 1.0f / std::sqrt((float)hd);
+        for (size_t l = 0; l < layers.size(); ++l) {
+            const Layer& L = layers[l];
+            gq_tensor kpool = desc(kp(l), GQ_TYPE_F16, hd, rows, Hkv);
+            gq_tensor vpool = desc(vp(l), GQ_TYPE_F16, hd, rows, Hkv);
+            gq_tensor pend = desc(pending, GQ_TYPE_F32, e, B);
+            float* nx = pending ? other(x) : nullptr;
+            gq_tensor nxt = desc(nx, GQ_TYPE_F32, e, B);
+            gq_mul_mat_fusion f{};
+            f.rms_norm = 1, f.rms_eps = m.rms_eps;
+            if (pending) f.b_add = &pend, f.b_sum = &nxt;
+            gq_tensor qo = desc(b.q, GQ_TYPE_F32, hd, Hq, B);
+            if (fused || q8) {  // ADD + RMS_NORM + QKV (+ bias) + ROPE x2 + SET_ROWS x2
+                gq_rope_kv_epilogue ep{};
+                ep.n_head = (int32_t)Hq, ep.n_head_kv = (int32_t)Hkv, ep.head_dim = (int32_t)hd;
+                ep.pos = &pos_t, ep.n_dims = (int32_t)hd, ep.mode = 2;
+                ep.freq_base = m.rope_base, ep.freq_scale = 1.0f, ep.attn_factor = 1.0f;
+                ep.kv_idx = &idx_t, ep.q_out = &qo, ep.k_cache = &kpool, ep.v_cache = &vpool;
+                ep.rope_cache = &rcs;
+                f.rope_kv = &ep;
+                f.int8 = q8 ? 1 : 0;
+                mm_fused(L.qkv, x, e, B, nullptr, NQ, f);
+            } else {  // ADD + RMS_NORM in the QKV GEMM's prologue, then ROPE + SET_ROWS in one launch
+                mm_fused(L.qkv, x, e, B, b.qkv, NQ, f);
+                gq_tensor qv = desc(b.qkv, GQ_TYPE_F32, hd, Hq, B, hd, NQ);
+                gq_tensor kv_ = desc(b.qkv + QD, GQ_TYPE_F32, hd, Hkv, B, hd, NQ);
+                gq_tensor vv = desc(b.qkv + QD + Hkv * hd, GQ_TYPE_F32, hd, Hkv, B, hd, NQ);
+                gq_ok(gq_rope_kv_store(&qv, &kv_, &vv, &pos_t, (int)hd, 2, m.rope_base, 1.0f, 1.0f, &idx_t, &qo,
+                                       &kpool, &vpool, nullptr, stream));
+                count("ROPE+SET_ROWS");
+            }
+            if (nx) x = nx;
+            {  // every row over its own slot's rows
+                gq_tensor q = desc(b.q, GQ_TYPE_F32, hd, B, Hq, Hq * hd, hd);
+                gq_tensor out = desc(b.attn, GQ_TYPE_F32, hd, Hq, B);
+                if (q8)
+                    gq_ok(gq_flash_attn_paged_q8(&q, &kpool, &vpool, &tab_t, &len_t, pg.P, max_len, scale, &out,
+                                                 b.q8_o, ws, ws_bytes, stream));
+                else
+                    gq_ok(gq_flash_attn_paged(&q, &kpool, &vpool, &tab_t, &len_t, pg.P, max_len, scale, &out, ws,
+                                              ws_bytes, stream));
+                count(q8 ? "FLASH_ATTN_PAGED+Q8_ROWS" : "FLASH_ATTN_PAGED");
+                ++fa_shapes["paged D=" + std::to_string(hd) + " Hq=" + std::to_string(Hq) + " Hkv=" +
+                            std::to_string(Hkv) + " B=" + std::to_string(B) + " max_len=" + std::to_string(max_len)];
+            }
+            float* x2 = other(x);
+            gq_tensor o_t = desc(b.proj, GQ_TYPE_F32, e, B);
+            gq_tensor x2_t = desc(x2, GQ_TYPE_F32, e, B);
+            {
+                gq_mul_mat_fusion fo{};
+                if (q8) fo.b_q8 = b.q8_o, fo.int8 = 1;
+                mm_fused(L.o, b.attn, QD, B, b.proj, e, fo);
+            }
+            if (q8) {  // ADD + RMS_NORM + gate|up + SWIGLU writing down's quantized rows, then down
+                gq_mul_mat_fusion fg{};
+                fg.rms_norm = 1, fg.rms_eps = m.rms_eps, fg.swiglu = 1, fg.b_add = &o_t, fg.b_sum = &x2_t;
+                fg.out_q8 = b.q8_d, fg.int8 = 1;
+                mm_fused(L.gate_up, x, e, B, nullptr, F, fg);
+                x = x2;
+                gq_mul_mat_fusion fd{};
+                fd.b_q8 = b.q8_d, fd.int8 = 1;
+                mm_fused(L.down, b.act, F, B, b.proj, e, fd);
+            } else if (fused) {
+                gq_mul_mat_fusion fg{};
+                fg.rms_norm = 1, fg.rms_eps = m.rms_eps, fg.swiglu = 1, fg.b_add = &o_t, fg.b_sum = &x2_t;
+                mm_fused(L.gate_up, x, e, B, b.act, F, fg);
+                x = x2;
+                gq_mul_mat_fusion fd{};
+                mm_fused(L.down, b.act, F, B, b.proj, e, fd);
+            } else {
+                gq_mul_mat_fusion fg{};
+                fg.rms_norm = 1, fg.rms_eps = m.rms_eps, fg.b_add = &o_t, fg.b_sum = &x2_t;
+                mm_fused(L.gate_up, x, e, B, b.gu, 2 * F, fg);
+                x = x2;
+                gq_mul_mat_fusion fd{};
+                fd.b_swiglu = 1;
+                mm_fused(L.down, b.gu, 2 * F, B, b.proj, e, fd);
+            }
+            pending = b.proj;
+        }
+        gq_tensor pend = desc(pending, GQ_TYPE_F32, e, B);
+        gq_mul_mat_fusion fh{};
+        fh.rms_norm = 1, fh.rms_eps = m.rms_eps, fh.b_add = &pend;
+        fh.int8 = q8 && lm_head.K % 256 == 0 && reinterpret_cast<uintptr_t>(lm_head.data) % 16 == 0 ? 1 : 0;
+        mm_fused(lm_head, x, e, B, b.logits, m.n_vocab, fh);
+        gq_ok(gq_paged_advance(pg.pos, nullptr, B, stream));
+        count("PAGED_ADVANCE");
+    }
+
+    // a step's graph: replayed when its bucket has one; otherwise issued eagerly (which also
+    // fills the kernels' per-shape attribute and occupancy caches) and, with graphs on,
+    // captured afterwards without executing, for the bucket's next run
+    template <typename Map, typename Key, typename Fwd>
+    void launch_step(Map& cache, const Key& key, bool graphs_ok, Fwd fwd) {
+        auto it = cache.find(key);
+        if (graphs_ok && it != cache.end()) {
+            hip_ok(hipGraphLaunch(it->second.first, stream), "hipGraphLaunch");
+            last_nodes = it->second.second;
+            return;
+        }
+        fwd();
+        last_nodes = -1;
+        if (!graphs_ok) return;
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        hipGraph_t g = nullptr;
+        hip_ok(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+            fwd();
+        } catch (...) {
+            (void)hipStreamEndCapture(stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        hip_ok(hipStreamEndCapture(stream, &g), "hipStreamEndCapture");
+        hipGraphExec_t ge = nullptr;
+        const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        if (ie != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            hip_ok(ie, "hipGraphInstantiate");
+        }
+        size_t nodes = 0;
+        (void)hipGraphGetNodes(g, nullptr, &nodes);
+        graph_defs.push_back(g);
+        cache.emplace(key, std::make_pair(ge, (int64_t)nodes));
+    }
+
+    void check_ids(int64_t n) const {
+        if ((int64_t)ids_host.size() != n) raise(GQ_ERR_INVALID, "run: input ids not set");
+        for (int32_t id : ids_host)
+            if (id < 0 || id >= m.n_vocab) raise(GQ_ERR_INVALID, "token id " + std::to_string(id) + " outside the vocabulary");
+    }
+
+    // s tokens at position p on the contiguous cache; the logits to the host
+    void step_contig(int64_t p, int64_t n, bool scratch) {
+        const int64_t n_kv = pad_kv_len(p + n, max_ctx, kv_n_pad);
+        const int64_t r0 = logits_last_only ? n - 1 : 0;
+        Bufs& b = buffers(n);
+        size_workspace(n, n - r0);
+        hip_ok(hipMemcpyAsync(b.ids, ids_host.data(), (size_t)n * 4, hipMemcpyHostToDevice, stream), "ids upload");
+        pos_host = (int32_t)p;
+        hip_ok(hipMemcpyAsync(pos_dev, &pos_host, 4, hipMemcpyHostToDevice, stream), "pos upload");
+        launch_step(graphs, std::make_tuple(n, n_kv, r0), use_graphs && !scratch, [&] { forward(n, n_kv, r0); });
+        out_rows = n - r0;
+        out_host.resize((size_t)out_rows * m.n_vocab);
+        hip_ok(hipMemcpyAsync(out_host.data(), b.logits, out_host.size() * 4, hipMemcpyDeviceToHost, stream),
+               "logits download");
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
     }
 
     void run() {
         if (!prepared) raise(GQ_ERR_INVALID, "run: call prepare first");
-        if ((int64_t)ids_host.size() != s) raise(GQ_ERR_INVALID, "run: input ids not set");
+        if (paged_step) return slot >= 0 ? run_prompt_slot() : run_batch();
+        check_ids(s);
         bool scratch = false;
         if (!kv_on) {  // no persistent cache: the whole sequence from position 0 in a scratch cache
             if (pos != 0) raise(GQ_ERR_INVALID, "run: pos > 0 needs init_kv_cache");
-            init_kv(pad_kv_len(s, INT64_MAX));
+            init_kv(pad_kv_len(s, INT64_MAX, kv_n_pad));
             scratch = true;
         }
         if (pos + s > max_ctx)
             raise(GQ_ERR_INVALID, "pos + s = " + std::to_string(pos + s) + " exceeds the KV cache (" +
                                       std::to_string(max_ctx) + ")");
-        for (int32_t id : ids_host)
-            if (id < 0 || id >= m.n_vocab) raise(GQ_ERR_INVALID, "token id " + std::to_string(id) + " outside the vocabulary");
-        const int64_t n_kv = pad_kv_len(pos + s, max_ctx);
-        const int64_t r0 = logits_last_only ? s - 1 : 0;
-        Bufs& b = buffers(s);
-        size_workspace(s, s - r0);
-        hip_ok(hipMemcpyAsync(b.ids, ids_host.data(), (size_t)s * 4, hipMemcpyHostToDevice, stream), "ids upload");
-        pos_host = (int32_t)pos;
-        hip_ok(hipMemcpyAsync(pos_dev, &pos_host, 4, hipMemcpyHostToDevice, stream), "pos upload");
-        const auto key = std::make_tuple(s, n_kv, r0);
-        auto it = graphs.find(key);
-        if (use_graphs && !scratch && it != graphs.end()) {
-            hip_ok(hipGraphLaunch(it->second, stream), "hipGraphLaunch");
-        } else {
-            // the bucket's first run executes eagerly (it also fills the kernels' per-shape
-            // attribute and occupancy caches); its graph is captured afterwards, without
-            // executing, and replayed from the next run of this bucket on
-            forward(s, n_kv, r0);
-            if (use_graphs && !scratch) {
-                hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
-                hipGraph_t g = nullptr;
-                hip_ok(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-                try {
-                    forward(s, n_kv, r0);
-                } catch (...) {
-                    (void)hipStreamEndCapture(stream, &g);
-                    if (g) (void)hipGraphDestroy(g);
-                    throw;
-                }
-                hip_ok(hipStreamEndCapture(stream, &g), "hipStreamEndCapture");
-                hipGraphExec_t ge = nullptr;
-                const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-                if (ie != hipSuccess) {
-                    (void)hipGraphDestroy(g);
-                    hip_ok(ie, "hipGraphInstantiate");
-                }
-                graph_defs.push_back(g);
-                graphs.emplace(key, ge);
-            }
-        }
-        out_rows = s - r0;
-        out_host.resize((size_t)out_rows * m.n_vocab);
-        hip_ok(hipMemcpyAsync(out_host.data(), b.logits, out_host.size() * 4, hipMemcpyDeviceToHost, stream),
-               "logits download");
-        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        step_contig(pos, s, scratch);
         pos += s;
+        if (pg.on) pg.contig_slot = -1;  // the contiguous cache no longer holds a slot's rows
         if (scratch) {  // the scratch cache lives for this call only
             bufs_free();
             dfree(kv);
@@ -1279,7 +1683,57 @@ struct Executor {
         }
     }
 
-    std::map<std::string, int64_t> env() const { return {{"s", s}, {"pos", pos}}; }
+    // a prompt step of one slot: rows [pos, pos + s) computed on the contiguous cache, after
+    // its rows [0, pos) are there (copied from its pages unless the previous prompt step of
+    // this slot left them), then stored into its pages; the slot continues at pos + s
+    void run_prompt_slot() {
+        check_ids(s);
+        const auto& pl = pg.pages[(size_t)slot];
+        if (!pg.active[(size_t)slot]) raise(GQ_ERR_INVALID, "slot " + std::to_string(slot) + " is not allocated");
+        if (pos + s > (int64_t)pl.size() * pg.P)
+            raise(GQ_ERR_INVALID, "slot " + std::to_string(slot) + " holds " + std::to_string(pl.size() * pg.P) +
+                                      " rows, pos + s = " + std::to_string(pos + s) + " (paged_kv_ensure_tokens first)");
+        sync_tables();
+        if (pg.contig_slot != slot || pg.contig_rows < pos) copy_rows(slot, 0, pos, 0);
+        pg.contig_slot = -1;  // until the rows below are in place
+        step_contig(pos, s, false);
+        copy_rows(slot, pos, pos + s, 1);
+        pg.contig_slot = slot, pg.contig_rows = pos + s;
+        set_slot_pos(slot, pos + s);
+    }
+
+    // one decode token for every slot of [0, nb), each at its own position
+    void run_batch() {
+        check_ids(nb);
+        int64_t longest = 1;
+        for (int64_t i = 0; i < nb; ++i) {
+            if (!pg.active[(size_t)i]) continue;  // its row writes the trash page, attends to nothing
+            const int64_t p = pg.pos_host[(size_t)i];
+            if (p + 1 > (int64_t)pg.pages[(size_t)i].size() * pg.P)
+                raise(GQ_ERR_INVALID, "slot " + std::to_string(i) + " has no row for position " + std::to_string(p) +
+                                          " (paged_kv_ensure_tokens first)");
+            longest = std::max(longest, p + 1);
+        }
+        const int64_t max_len = std::min(pg.max_ctx, (longest + PAGED_BUCKET - 1) / PAGED_BUCKET * PAGED_BUCKET);
+        sync_tables();
+        Bufs& b = buffers(nb);
+        size_workspace(nb, nb);
+        hip_ok(hipMemcpyAsync(b.ids, ids_host.data(), (size_t)nb * 4, hipMemcpyHostToDevice, stream), "ids upload");
+        launch_step(paged_graphs, std::make_tuple(nb, max_len), use_graphs, [&] { forward_paged(nb, max_len); });
+        out_rows = nb;
+        out_host.resize((size_t)nb * m.n_vocab);
+        hip_ok(hipMemcpyAsync(out_host.data(), b.logits, out_host.size() * 4, hipMemcpyDeviceToHost, stream),
+               "logits download");
+        hip_ok(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        for (int64_t i = 0; i < nb; ++i) ++pg.pos_host[(size_t)i];
+        pg.contig_slot = -1;
+    }
+
+    std::map<std::string, int64_t> env() const {
+        std::map<std::string, int64_t> en{{"s", s}, {"pos", pos}};
+        if (paged_step) en["b"] = nb, en["slot"] = slot < 0 ? 0 : slot;
+        return en;
+    }
 
     void shape(uint32_t tid, int64_t ne[4]) const {
         const GTensor& t = graph.t(tid);
@@ -1416,26 +1870,66 @@ int gq_exec_inspect(const void* gguf_bytes, size_t len, char* buf, size_t buf_le
 }
 
 int gq_exec_prepare(gq_exec* h, const char* const* names, const int64_t* values, int64_t n) {
-    return guarded(h ? &h->ex : nullptr, "exec_prepare", [&] {
+    const auto t0 = std::chrono::steady_clock::now();
+    const int rc = guarded(h ? &h->ex : nullptr, "exec_prepare", [&] {
         Executor& e = h->ex;
-        int64_t s = -1, pos = e.kv_on ? e.pos : 0;
+        int64_t s = -1, pos = -1, b = -1, slot = -1;
         for (int64_t i = 0; i < n; ++i) {
             if (!names || !names[i]) raise(GQ_ERR_INVALID, "null symbol name");
             const std::string k = names[i];
             if (k == "s") s = values[i];
             else if (k == "pos") pos = values[i];
+            else if (k == "b") b = values[i];
+            else if (k == "slot") slot = values[i];
             else if (std::find(e.graph.symbols.begin(), e.graph.symbols.end(), k) == e.graph.symbols.end())
                 raise(GQ_ERR_INVALID, "unknown symbol " + k);
         }
         if (s <= 0) raise(GQ_ERR_INVALID, "symbol s must be given and positive");
-        if (pos < 0) raise(GQ_ERR_INVALID, "symbol pos must not be negative");
-        if (e.kv_on && pos + s > e.max_ctx)
-            raise(GQ_ERR_INVALID, "pos + s = " + std::to_string(pos + s) + " exceeds the KV cache (" +
-                                      std::to_string(e.max_ctx) + ")");
-        e.s = s, e.pos = pos, e.prepared = true;
+        if (b == 0 || b < -1) raise(GQ_ERR_INVALID, "symbol b must be positive");
+        if (slot < -1) raise(GQ_ERR_INVALID, "symbol slot must not be negative");
+        if (pos < -1) raise(GQ_ERR_INVALID, "symbol pos must not be negative");
+        bool paged = false;
+        if (e.pg.on && (slot >= 0 || b >= 1)) {
+            // the reference scheduler's protocol (batch_scheduler.cpp:190-194, 318-321): a prompt
+            // step names its slot (b = 1); a decode step gives b (s = 1) and runs slots [0, b)
+            paged = true;
+            if (slot >= 0) {
+                e.check_slot(slot);
+                if (b > 1) raise(GQ_ERR_INVALID, "a prompt step of one slot needs b = 1");
+                if (pos < 0) pos = e.pg.pos_host[(size_t)slot];
+                if (pos + s > e.pg.max_ctx)
+                    raise(GQ_ERR_INVALID, "pos + s = " + std::to_string(pos + s) + " exceeds the slots' max_ctx (" +
+                                              std::to_string(e.pg.max_ctx) + ")");
+            } else {
+                if (s != 1) raise(GQ_ERR_INVALID, "a batched step decodes one token per slot: s must be 1");
+                if (b > e.pg.max_batch)
+                    raise(GQ_ERR_INVALID, "b = " + std::to_string(b) + " exceeds max_batch (" +
+                                              std::to_string(e.pg.max_batch) + ")");
+                // each slot decodes at its own position; pos (the scheduler passes the
+                // largest) only has to cover them
+                for (int64_t i = 0; i < b && pos >= 0; ++i)
+                    if (e.pg.active[(size_t)i] && e.pg.pos_host[(size_t)i] > pos)
+                        raise(GQ_ERR_INVALID, "pos = " + std::to_string(pos) + " is below slot " + std::to_string(i) +
+                                                  "'s position " + std::to_string(e.pg.pos_host[(size_t)i]));
+            }
+        } else {
+            if ((b > 1 || slot > 0))
+                raise(GQ_ERR_INVALID, "symbols b > 1 and slot > 0 need init_paged_kv_cache");
+            if (pos < 0) pos = e.kv_on ? e.pos : 0;
+            if (e.kv_on && pos + s > e.max_ctx)
+                raise(GQ_ERR_INVALID, "pos + s = " + std::to_string(pos + s) + " exceeds the KV cache (" +
+                                          std::to_string(e.max_ctx) + ")");
+        }
+        e.s = s, e.pos = pos < 0 ? 0 : pos, e.prepared = true;
+        e.paged_step = paged, e.slot = paged ? (int)slot : -1, e.nb = paged && slot < 0 ? (b < 0 ? 1 : b) : 1;
         e.ids_host.clear();
         e.out_rows = 0;
     });
+    if (rc == GQ_OK && h->ex.profile_on) {
+        h->ex.prof_prepare_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        ++h->ex.prof_n_prepare;
+    }
+    return rc;
 }
 
 int gq_exec_set_input(gq_exec* h, uint32_t tensor_id, const void* data, size_t bytes) {
@@ -1445,11 +1939,12 @@ int gq_exec_set_input(gq_exec* h, uint32_t tensor_id, const void* data, size_t b
         if (tensor_id != e.m.input_tid) raise(GQ_ERR_INVALID, "tensor " + std::to_string(tensor_id) + " is not the graph input");
         const int type = e.graph.t(tensor_id).type;
         const size_t es = type == GQ_TYPE_I64 ? 8 : 4;
-        if (!data || bytes != (size_t)e.s * es)
+        const int64_t n_ids = e.s * e.nb;  // s token ids (b x 1 in a batched decode step)
+        if (!data || bytes != (size_t)n_ids * es)
             raise(GQ_ERR_INVALID, "input holds " + std::to_string(bytes) + " bytes, expected " +
-                                      std::to_string((size_t)e.s * es) + " (s token ids)");
-        e.ids_host.resize((size_t)e.s);
-        for (int64_t i = 0; i < e.s; ++i) {
+                                      std::to_string((size_t)n_ids * es) + " (s x b token ids)");
+        e.ids_host.resize((size_t)n_ids);
+        for (int64_t i = 0; i < n_ids; ++i) {
             int64_t v;
             if (es == 8) memcpy(&v, static_cast<const uint8_t*>(data) + 8 * i, 8);
             else {
@@ -1476,7 +1971,13 @@ int gq_exec_set_input_by_name(gq_exec* h, const char* name, const void* data, si
 }
 
 int gq_exec_run(gq_exec* h) {
-    return guarded(h ? &h->ex : nullptr, "exec_run", [&] { h->ex.run(); });
+    const auto t0 = std::chrono::steady_clock::now();
+    const int rc = guarded(h ? &h->ex : nullptr, "exec_run", [&] { h->ex.run(); });
+    if (rc == GQ_OK && h->ex.profile_on) {
+        h->ex.prof_run_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        ++h->ex.prof_n_run;
+    }
+    return rc;
 }
 
 int gq_exec_synchronize(gq_exec* h) {
@@ -1532,5 +2033,147 @@ int gq_exec_set_enable_graphs(gq_exec* h, int enable) {
 }
 
 int64_t gq_exec_position(gq_exec* h) { return h ? h->ex.pos : -1; }
+
+// ---- paged KV (executor.h:73-93) ----------------------------------------------------
+int gq_exec_set_tokens_per_page(gq_exec* h, int64_t n) {
+    return guarded(h ? &h->ex : nullptr, "exec_set_tokens_per_page", [&] { h->ex.set_tokens_per_page(n); });
+}
+
+int64_t gq_exec_get_tokens_per_page(gq_exec* h) { return h ? h->ex.pg.P : -1; }
+
+int gq_exec_init_paged_kv_cache(gq_exec* h, int64_t max_batch, int64_t max_ctx) {
+    return guarded(h ? &h->ex : nullptr, "exec_init_paged_kv_cache", [&] { h->ex.init_paged(max_batch, max_ctx); });
+}
+
+int gq_exec_is_paged_kv_cache_enabled(gq_exec* h) { return h && h->ex.pg.on ? 1 : 0; }
+
+int gq_exec_paged_kv_alloc_slot(gq_exec* h, int64_t slot) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_kv_alloc_slot", [&] { h->ex.alloc_slot(slot); });
+}
+
+int gq_exec_paged_kv_free_slot(gq_exec* h, int64_t slot) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_kv_free_slot", [&] { h->ex.free_slot(slot); });
+}
+
+int gq_exec_is_paged_slot_allocated(gq_exec* h, int64_t slot) {
+    if (!h || !h->ex.pg.on || slot < 0 || slot >= h->ex.pg.max_batch) return 0;
+    return h->ex.pg.active[(size_t)slot] ? 1 : 0;
+}
+
+int gq_exec_paged_kv_ensure_tokens(gq_exec* h, int64_t slot, int64_t total_tokens) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_kv_ensure_tokens",
+                   [&] { h->ex.ensure_tokens(slot, total_tokens); });
+}
+
+int gq_exec_paged_kv_map_existing_pages(gq_exec* h, int64_t slot, int64_t start_page, const int32_t* pages,
+                                        int64_t n_pages) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_kv_map_existing_pages",
+                   [&] { h->ex.map_pages(slot, start_page, pages, n_pages); });
+}
+
+int gq_exec_paged_kv_extract_page(gq_exec* h, int64_t slot, int64_t page_idx, int32_t* page) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_kv_extract_page", [&] {
+        if (!page) raise(GQ_ERR_INVALID, "null page");
+        *page = h->ex.page_of(slot, page_idx);
+    });
+}
+
+int gq_exec_paged_page_retain(gq_exec* h, int32_t page) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_page_retain", [&] {
+        h->ex.need_paged();
+        h->ex.retain_page(page);
+    });
+}
+
+int gq_exec_paged_page_release(gq_exec* h, int32_t page) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_page_release", [&] {
+        h->ex.need_paged();
+        h->ex.release_page(page);
+    });
+}
+
+size_t gq_exec_get_paged_active_vram_bytes(gq_exec* h) { return h ? h->ex.active_bytes() : 0; }
+
+int gq_exec_paged_slot_position(gq_exec* h, int64_t slot, int64_t* pos) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_slot_position", [&] {
+        h->ex.check_slot(slot);
+        if (!pos) raise(GQ_ERR_INVALID, "null pos");
+        *pos = h->ex.pg.pos_host[(size_t)slot];
+    });
+}
+
+int gq_exec_paged_set_slot_position(gq_exec* h, int64_t slot, int64_t pos) {
+    return guarded(h ? &h->ex : nullptr, "exec_paged_set_slot_position", [&] {
+        Executor& e = h->ex;
+        e.check_slot(slot);
+        if (pos < 0 || pos > e.pg.max_ctx) raise(GQ_ERR_INVALID, "position outside [0, max_ctx]");
+        e.set_slot_pos(slot, pos);
+        if (e.pg.contig_slot == slot) e.pg.contig_rows = std::min(e.pg.contig_rows, pos);
+    });
+}
+
+// ---- profiling (executor.h:101-118) --------------------------------------------------
+int gq_exec_set_enable_profile(gq_exec* h, int enable) {
+    return guarded(h ? &h->ex : nullptr, "exec_set_enable_profile", [&] { h->ex.profile_on = enable != 0; });
+}
+
+int gq_exec_reset_profile(gq_exec* h) {
+    return guarded(h ? &h->ex : nullptr, "exec_reset_profile", [&] {
+        Executor& e = h->ex;
+        e.prof_prepare_ms = e.prof_run_ms = 0.0;
+        e.prof_n_prepare = e.prof_n_run = 0;
+    });
+}
+
+int gq_exec_get_profile(gq_exec* h, gq_exec_profile* out) {
+    return guarded(h ? &h->ex : nullptr, "exec_get_profile", [&] {
+        if (!out) raise(GQ_ERR_INVALID, "null profile");
+        const Executor& e = h->ex;
+        *out = gq_exec_profile{};
+        out->prepare_ms = e.prof_prepare_ms, out->run_ms = e.prof_run_ms;
+        out->n_prepare = e.prof_n_prepare, out->n_run = e.prof_n_run;
+    });
+}
+
+int gq_exec_runtime_graph_summary(gq_exec* h, char* buf, size_t len, size_t* needed) {
+    std::string j;
+    const int rc = guarded(h ? &h->ex : nullptr, "exec_runtime_graph_summary", [&] {
+        const Executor& e = h->ex;
+        int64_t n = 0, n_mm = 0, n_fa = 0, n_set = 0;
+        std::string ops;
+        for (const auto& kv : e.op_hist) {
+            n += kv.second;
+            if (kv.first.find("MUL_MAT") != std::string::npos) n_mm += kv.second;
+            if (kv.first.find("FLASH_ATTN") != std::string::npos) n_fa += kv.second;
+            if (kv.first.find("SET_ROWS") != std::string::npos) n_set += kv.second;
+            ops += (ops.empty() ? "\"" : ",\"") + kv.first + "\":" + std::to_string(kv.second);
+        }
+        j = "{\"n_nodes\":" + std::to_string(n) + ",\"n_kernel_nodes\":" +
+            std::to_string(e.last_nodes >= 0 ? e.last_nodes : n) + ",\"n_mul_mat\":" + std::to_string(n_mm) +
+            ",\"n_flash_attn\":" + std::to_string(n_fa) + ",\"n_set_rows\":" + std::to_string(n_set) +
+            ",\"kv_n_pad\":" + std::to_string(e.kv_n_pad) + ",\"graphs_captured\":" +
+            std::to_string(e.graphs.size() + e.paged_graphs.size()) + ",\"last_run_replayed\":" +
+            (e.last_nodes >= 0 ? "true" : "false") + ",\"paged_kv\":" + (e.pg.on ? "true" : "false") +
+            ",\"ops\":{" + ops + "}}";
+    });
+    return rc ? rc : copy_out(j, buf, len, needed);
+}
+
+int gq_exec_runtime_mul_mat_shape_summary(gq_exec* h, char* buf, size_t len, size_t* needed) {
+    std::string j;
+    const int rc = guarded(h ? &h->ex : nullptr, "exec_runtime_mul_mat_shape_summary", [&] {
+        auto list = [](const std::map<std::string, int64_t>& m) {
+            std::vector<std::pair<std::string, int64_t>> v(m.begin(), m.end());
+            std::stable_sort(v.begin(), v.end(), [](const auto& a, const auto& b) { return a.second > b.second; });
+            std::string o = "[";
+            for (size_t i = 0; i < v.size(); ++i)
+                o += std::string(i ? "," : "") + "{\"n\":" + std::to_string(v[i].second) + ",\"shape\":\"" +
+                     v[i].first + "\"}";
+            return o + "]";
+        };
+        j = "{\"mul_mat\":" + list(h->ex.mm_shapes) + ",\"flash_attn\":" + list(h->ex.fa_shapes) + "}";
+    });
+    return rc ? rc : copy_out(j, buf, len, needed);
+}
 
 }  // extern "C"

@@ -13,9 +13,11 @@ Errors raise ggmlc_amd.GQError (a RuntimeError), and a rejected call leaves the
 executor usable, as the reference's std::runtime_error / std::invalid_argument do.
 
 The paged-KV methods of the reference executor (`init_paged_kv_cache`, `paged_kv_*`,
-`set_tokens_per_page`, executor.cpp:634-920) are served by `runner.PagedExecutor` over
-`paged.BatchDecoder` on the same weights; `ModelRunner.executor` is that object, and
-it forwards every other method to this handle.
+`set_tokens_per_page`, `get_paged_active_vram_bytes`, executor.cpp:634-920) are native
+here too: with the paged cache on, `prepare({"s": n, "slot": i, "pos": p})` is a prompt
+step of slot i and `prepare({"b": B, "s": 1})` one decode token for slots [0, B), each at
+its own position — the protocol of the reference's C++ scheduler
+(batch_scheduler.cpp:190-194, 318-321). Page handles are int32 page ids.
 """
 
 from __future__ import annotations
@@ -155,6 +157,83 @@ class ModelExecutor:
     @property
     def position(self) -> int:
         return int(self._L.gq_exec_position(self._h))
+
+    # -- paged KV (executor.h:73-93) ---------------------------------------------------
+    def set_tokens_per_page(self, n: int) -> None:
+        check(self._L.gq_exec_set_tokens_per_page(self._h, int(n)))
+
+    def get_tokens_per_page(self) -> int:
+        return int(self._L.gq_exec_get_tokens_per_page(self._h))
+
+    def init_paged_kv_cache(self, max_batch: int = 8, max_ctx: int = 2048) -> None:
+        check(self._L.gq_exec_init_paged_kv_cache(self._h, int(max_batch), int(max_ctx)))
+
+    def is_paged_kv_cache_enabled(self) -> bool:
+        return bool(self._L.gq_exec_is_paged_kv_cache_enabled(self._h))
+
+    def paged_kv_alloc_slot(self, slot_id: int, prefix_hash: str = "") -> None:
+        check(self._L.gq_exec_paged_kv_alloc_slot(self._h, int(slot_id)))
+
+    def paged_kv_free_slot(self, slot_id: int) -> None:
+        check(self._L.gq_exec_paged_kv_free_slot(self._h, int(slot_id)))
+
+    def is_paged_slot_allocated(self, slot_id: int) -> bool:
+        return bool(self._L.gq_exec_is_paged_slot_allocated(self._h, int(slot_id)))
+
+    def paged_kv_ensure_tokens(self, slot_id: int, total_tokens: int) -> None:
+        check(self._L.gq_exec_paged_kv_ensure_tokens(self._h, int(slot_id), int(total_tokens)))
+
+    def paged_kv_map_existing_pages(self, slot_id: int, start_page_idx: int, pages) -> None:
+        ids = np.ascontiguousarray(np.asarray(pages, np.int32))
+        ptr = ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+        check(self._L.gq_exec_paged_kv_map_existing_pages(self._h, int(slot_id), int(start_page_idx), ptr, ids.size))
+
+    def paged_kv_extract_page_handles(self, slot_id: int, page_idx: int) -> int:
+        page = ctypes.c_int32(0)
+        check(self._L.gq_exec_paged_kv_extract_page(self._h, int(slot_id), int(page_idx), ctypes.byref(page)))
+        return int(page.value)
+
+    def paged_page_retain(self, page: int) -> None:
+        check(self._L.gq_exec_paged_page_retain(self._h, int(page)))
+
+    def paged_page_release(self, page: int) -> None:
+        check(self._L.gq_exec_paged_page_release(self._h, int(page)))
+
+    def get_paged_active_vram_bytes(self) -> int:
+        return int(self._L.gq_exec_get_paged_active_vram_bytes(self._h))
+
+    def paged_slot_position(self, slot_id: int) -> int:
+        p = ctypes.c_int64(0)
+        check(self._L.gq_exec_paged_slot_position(self._h, int(slot_id), ctypes.byref(p)))
+        return int(p.value)
+
+    def paged_set_slot_position(self, slot_id: int, pos: int) -> None:
+        check(self._L.gq_exec_paged_set_slot_position(self._h, int(slot_id), int(pos)))
+
+    # -- profiling (executor.h:101-118) ----------------------------------------------
+    def set_enable_profile(self, enable: bool) -> None:
+        check(self._L.gq_exec_set_enable_profile(self._h, 1 if enable else 0))
+
+    def reset_profile(self) -> None:
+        check(self._L.gq_exec_reset_profile(self._h))
+
+    def get_profile(self) -> dict:
+        p = _lib.gq_exec_profile()
+        check(self._L.gq_exec_get_profile(self._h, ctypes.byref(p)))
+        return {name: getattr(p, name) for name, _ in p._fields_}
+
+    def _json(self, fn) -> dict:
+        need = ctypes.c_size_t(0)
+        check(fn(self._h, None, 0, ctypes.byref(need)))
+        out = ctypes.create_string_buffer(need.value)
+        check(fn(self._h, out, need.value, None))
+        return json.loads(out.value.decode())
+
+    def runtime_graph_summary(self) -> dict:
+        return self._json(self._L.gq_exec_runtime_graph_summary)
+
+    def runtime_mul_mat_shape_summary(self) -> dict:
+        return self._json(self._L.gq_exec_runtime_mul_mat_shape_summary)
 
 
 __all__ = ["ModelExecutor", "inspect", "available", "get_available_devices", "GQError"]

@@ -364,8 +364,8 @@ int gq_kv_advance(int32_t* pos, int64_t s, gq_stream_t stream);
  *   dst      : F32 [D, Hq, B] contiguous.  D in {64, 128}, Hq / Hkv <= 8 (<= 16 when
  *              page_size is a multiple of 128; groups of 2-16 run on the matrix cores).
  * Equal to the reference's decode step of sequence b with the causal mask of its
- * position (columns past it weigh exactly 0). Shares gq_flash_attn_ext's per-device
- * split counters: no two decode attention launches concurrently on one device. */
+ * position (columns past it weigh exactly 0). Its in-kernel split merge counts
+ * arrivals per stream, like gq_flash_attn_ext's. */
 size_t gq_flash_attn_paged_workspace_size(const gq_tensor* q, const gq_tensor* k_pool, int64_t max_len,
                                           int64_t page_size);
 int gq_flash_attn_paged(const gq_tensor* q, const gq_tensor* k_pool, const gq_tensor* v_pool,
@@ -421,7 +421,8 @@ int gq_kv_pages_copy(gq_tensor* pool, gq_tensor* cache, const int32_t* pages, in
  *   The input is the graph's token-id tensor (I32 or I64, s values); the output its
  *   logits, F32 [n_vocab, s] (rows = tokens), or [n_vocab, 1] with logits_last_only
  *   (executor.cpp:2396-2410). Without init_kv_cache each run is a whole sequence from
- *   position 0 in a scratch cache. n_kv follows pad_kv_len (executor.cpp:58-64). */
+ *   position 0 in a scratch cache. n_kv follows pad_kv_len (executor.cpp:58-64) with the
+ *   pad GGMLC_KV_PAD gives when the cache is initialised (default 256, executor.cpp:501-503). */
 typedef struct gq_exec gq_exec;
 /* ModelExecutor::get_available_devices (executor.cpp:184): JSON list of "cuda:N" for the
  * visible GPUs (no CPU entry: this runtime has no CPU path). */
@@ -454,6 +455,79 @@ int gq_exec_logits_last_only(gq_exec* h);
 int gq_exec_set_enable_graphs(gq_exec* h, int enable);
 /* The handle's running position (tokens written to the KV cache), -1 for NULL. */
 int64_t gq_exec_position(gq_exec* h);
+
+/* ---- paged KV cache and batched decode (ModelExecutor::init_paged_kv_cache,
+ * paged_kv_*, get_paged_active_vram_bytes, set/get_tokens_per_page: executor.h:73-93,
+ * executor.cpp:634-920) ------------------------------------------------------------
+ * Per layer one K and one V page pool sized for max_batch slots of max_ctx rows; a page
+ * holds tokens_per_page rows of every layer (default 128; a power of two >= 64, >= 128
+ * for head_dim 64, set before init) and is named by one int32 id for all layers (the
+ * reference's per-layer VMM handles, executor.cpp:838-920). Pages are reference counted:
+ * a slot holds one reference per page it lists (ensure_tokens allocates, map_existing_pages
+ * shares, free_slot releases); a caller that keeps pages beyond their slot (a prefix cache)
+ * retains them (gq_exec_paged_page_retain) and releases them later.
+ * With the paged cache on, gq_exec_prepare takes the reference scheduler's symbols
+ * (batch_scheduler.cpp:190-194, 318-321):
+ *   {s, slot[, pos][, b = 1]}: a prompt step of that slot, s tokens at pos (default: the
+ *     slot's position), computed on the contiguous cache (its graphs) and stored into the
+ *     slot's pages; the slot then continues at pos + s. Output: the logits of the step.
+ *   {b, s = 1[, pos]}: one decode token for every slot of [0, b) (input: b token ids),
+ *     each slot at its own position (the reference runs the batch at the largest, pos;
+ *     here pos only has to cover every allocated slot's position), the slots' positions
+ *     then advance by one. Slots without pages write a trash page and attend to nothing.
+ *     Output: F32 [n_vocab, b], row i the logits of slot i. One HIP graph per (b, context
+ *     bucket of 512 rows); 2..16 rows run the int8 product chain.
+ * Every slot must hold rows for the positions it runs (paged_kv_ensure_tokens). */
+int gq_exec_set_tokens_per_page(gq_exec* h, int64_t tokens_per_page);
+int64_t gq_exec_get_tokens_per_page(gq_exec* h);
+/* Allocates the pools (and the contiguous cache of max_ctx rows when init_kv_cache has
+ * not run); a second call changes nothing (executor.cpp:635). */
+int gq_exec_init_paged_kv_cache(gq_exec* h, int64_t max_batch, int64_t max_ctx);
+int gq_exec_is_paged_kv_cache_enabled(gq_exec* h);
+/* Marks the slot in use at position 0 with no pages (an allocated slot is freed first). */
+int gq_exec_paged_kv_alloc_slot(gq_exec* h, int64_t slot);
+int gq_exec_paged_kv_free_slot(gq_exec* h, int64_t slot);
+int gq_exec_is_paged_slot_allocated(gq_exec* h, int64_t slot);
+/* Gives the slot pages for rows [0, total_tokens); GQ_ERR_WORKSPACE when the pool is out
+ * of free pages. */
+int gq_exec_paged_kv_ensure_tokens(gq_exec* h, int64_t slot, int64_t total_tokens);
+/* Appends existing pages (ids from gq_exec_paged_kv_extract_page) as the slot's pages
+ * start_page.. (start_page must equal the slot's page count), one reference each. */
+int gq_exec_paged_kv_map_existing_pages(gq_exec* h, int64_t slot, int64_t start_page, const int32_t* pages,
+                                        int64_t n_pages);
+/* The id of the slot's page page_idx (paged_kv_extract_page_handles). */
+int gq_exec_paged_kv_extract_page(gq_exec* h, int64_t slot, int64_t page_idx, int32_t* page);
+int gq_exec_paged_page_retain(gq_exec* h, int32_t page);
+int gq_exec_paged_page_release(gq_exec* h, int32_t page);
+/* Device bytes of the pages in use (every layer, K and V). */
+size_t gq_exec_get_paged_active_vram_bytes(gq_exec* h);
+/* A slot's position (its next row), and setting it (rewinding a slot). No counterpart in
+ * the reference, whose scheduler tracks positions outside the executor. */
+int gq_exec_paged_slot_position(gq_exec* h, int64_t slot, int64_t* pos);
+int gq_exec_paged_set_slot_position(gq_exec* h, int64_t slot, int64_t pos);
+
+/* ---- profiling (ModelExecutor::set_enable_profile, reset_profile, get_profile,
+ * runtime_graph_summary, runtime_mul_mat_shape_summary: executor.h:101-118,
+ * executor.cpp:3184-3459) -----------------------------------------------------------
+ * With profiling on, prepare and run add their host wall time (run: the whole step,
+ * graph replay and the logits' download included). The set_*_pos and mask fields stay 0:
+ * positions, row indices and the causal mask are computed on the device inside the step. */
+typedef struct gq_exec_profile {
+    double prepare_ms, set_decode_pos_ms, set_chunk_pos_ms, mask_fill_ms, run_ms;
+    int32_t n_prepare, n_set_decode_pos, n_set_chunk_pos, n_run;
+} gq_exec_profile;
+int gq_exec_set_enable_profile(gq_exec* h, int enable);
+int gq_exec_reset_profile(gq_exec* h);
+int gq_exec_get_profile(gq_exec* h, gq_exec_profile* out);
+/* JSON of the last issued step: n_nodes (launches), n_kernel_nodes (the replayed graph's
+ * nodes, else the launches), n_mul_mat, n_flash_attn, n_set_rows (launches that contain
+ * them: fused launches count once each), kv_n_pad, graphs_captured, last_run_replayed,
+ * paged_kv and ops {launch: count} (a launch named by the ops it runs, e.g.
+ * "RMS_NORM+ADD+MUL_MAT+ROPE+SET_ROWS"). Same output convention as gq_exec_describe. */
+int gq_exec_runtime_graph_summary(gq_exec* h, char* buf, size_t buf_len, size_t* needed);
+/* JSON {mul_mat: [{n, shape}], flash_attn: [{n, shape}]}: the products' (type, K, N, M)
+ * and the attention launches' shapes of the last issued step, most frequent first. */
+int gq_exec_runtime_mul_mat_shape_summary(gq_exec* h, char* buf, size_t buf_len, size_t* needed);
 
 /* ---- measurement aid ------------------------------------------------------
  * No counterpart in the reference. Reads `bytes` (16-byte aligned) once with

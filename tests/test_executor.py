@@ -152,3 +152,146 @@ def test_executor_rejected_calls_leave_it_usable(tmp_path):
     ex.run()
     out = ex.get_output(ex.outputs[0])
     assert out.shape == (2, c.n_vocab) and np.isfinite(out).all()
+
+
+def _check_spread(got, single, r16, r1, what):
+    """the batched GPU step against the reference (R16) within twice the larger of the
+    reference's thread spread and the single-sequence path's distance from it, and
+    against the single-sequence path"""
+    c_ref, c_single = _cos(r1, r16), _cos(single, r16)
+    bar = min(0.9999, 1.0 - 2.0 * max(1.0 - c_ref, 1.0 - c_single))
+    c = _cos(got, r16)
+    print(what, f"cos(gpu, R16) {c:.7f}  cos(R1, R16) {c_ref:.7f}  cos(single, R16) {c_single:.7f}  "
+          f"cos(gpu, single) {_cos(got, single):.7f}")
+    assert c >= bar, (what, c, bar)
+    assert _cos(got, single) >= 0.999999, (what, _cos(got, single))
+
+
+def _ref_step(pair, single, tid_in, tid_out, tok, pos):
+    """the next decode step of one sequence: its single-sequence executor, R16, R1"""
+    outs = [_run(single, [tok], pos)[0]]
+    for r in pair:
+        r.run({tid_in: np.array([[tok]], np.int32)}, {"s": 1, "pos": pos})
+        outs.append(r.output(tid_out).reshape(-1))
+    return outs
+
+
+def _slot_step(ex, slot, ids, pos):
+    ex.prepare({"b": 1, "s": len(ids), "pos": pos, "slot": slot})
+    ex.set_input_by_id(ex.inputs[0], np.asarray(ids, np.int32))
+    ex.run()
+    return ex.get_output(ex.outputs[0])[-1].copy()
+
+
+@pytest.mark.parametrize("kind", ["qwen", "tiny"])
+def test_executor_paged_batched_decode_matches_reference(tmp_path, kind):
+    """configs[4]'s serving path through gq_exec_* only (no torch): the paged cache, slots
+    prefilled through prompt steps (one in two chunks, one opening with another slot's two
+    prefix pages mapped in), then batched decode steps of 4 slots (the int8 chain, graph
+    replays from the second step) and of 1 slot (the fused GEMVs), each slot at its own
+    position; every slot against ggmlc's own runtime run on that sequence alone at the
+    bar its own deviations set, and against this executor's single-sequence path (pinned
+    against the reference above) running each sequence alone on the contiguous cache;
+    a freed slot inside the batch, page accounting and rejected calls.
+
+    ggml's decode attention accumulates V in an fp16 buffer, an error that grows with the
+    context (the single-sequence path agrees with it to ~1e-4 at these 2-layer shapes
+    once contexts pass a few hundred rows), so the bar against R16 (the reference at 16
+    threads) is 1 - cos(gpu, R16) <= 2 max(1 - cos(R1, R16), 1 - cos(single, R16)), capped
+    at 0.9999, R1 the reference at 1 thread; against the single-sequence path, cos >=
+    0.999999 (the same arithmetic: exact block products, fp32 attention)."""
+    from ggmlc_amd import GQError
+    from ggmlc_amd.executor import ModelExecutor
+
+    c, p = _model(tmp_path, kind)
+    ex = ModelExecutor(p.read_bytes(), "gpu")
+    assert not ex.is_paged_kv_cache_enabled() and ex.get_tokens_per_page() == 128
+    ex.init_paged_kv_cache(max_batch=8, max_ctx=1024)
+    assert ex.is_paged_kv_cache_enabled() and ex.get_paged_active_vram_bytes() == 0
+    tid_in, tid_out = ex.inputs[0], ex.outputs[0]
+    rng = np.random.default_rng(9)
+    lens, n_new, B = [300, 129, 420, 200], 4, 4
+    prompts = [rng.integers(0, c.n_vocab, n).astype(np.int32) for n in lens]
+    prompts[2][:256] = prompts[0][:256]  # slot 2 reuses slot 0's first two pages
+    refs, singles, toks = [], [], np.zeros(B, np.int32)
+    for b in range(B):
+        ex.paged_kv_alloc_slot(b)
+        start = 0
+        if b == 2:
+            shared = [ex.paged_kv_extract_page_handles(0, i) for i in range(2)]
+            ex.paged_kv_map_existing_pages(2, 0, shared)
+            start = 256
+        ex.paged_kv_ensure_tokens(b, lens[b] + n_new + 1)
+        if b == 0:  # two chunks: the second continues on the rows the first left
+            _slot_step(ex, 0, prompts[0][:128], 0)
+            got = _slot_step(ex, 0, prompts[0][128:], 128)
+        else:
+            got = _slot_step(ex, b, prompts[b][start:], start)
+        assert ex.paged_slot_position(b) == lens[b]
+        pair = [O.RefRuntime(p, max_ctx=1024, n_threads=nt) for nt in (16, 1)]
+        for r in pair:
+            r.run({tid_in: prompts[b][None, :]}, {"s": lens[b], "pos": 0})
+        single = ModelExecutor(p.read_bytes(), "gpu")
+        single.init_kv_cache(1024)
+        one = _run(single, prompts[b], 0)[-1]
+        _check_spread(got, one, *[r.output(tid_out).reshape(lens[b], c.n_vocab)[-1] for r in pair], ("prompt", b))
+        refs.append(pair)
+        singles.append(single)
+        toks[b] = int(np.argmax(got))
+    per_page = 2 * c.n_layer * c.n_head_kv * 128 * c.head_dim * 2
+    n_pages = sum(-(-(n + n_new + 1) // 128) for n in lens) - 2  # slot 2 shares two
+    assert ex.get_paged_active_vram_bytes() == n_pages * per_page
+    for i in range(n_new):
+        ex.prepare({"b": B, "s": 1, "pos": max(lens) + i})
+        ex.set_input_by_id(tid_in, toks)
+        ex.run()
+        out = ex.get_output(tid_out)
+        assert out.shape == (B, c.n_vocab) and ex.get_tensor_shape(tid_out)[:2] == [c.n_vocab, B]
+        summ = ex.runtime_graph_summary()
+        assert summ["last_run_replayed"] == (i > 0) and summ["paged_kv"]
+        assert summ["n_flash_attn"] == c.n_layer
+        for b in range(B):
+            _check_spread(out[b], *_ref_step(refs[b], singles[b], tid_in, tid_out, toks[b], lens[b] + i), (i, b))
+        toks = out.argmax(axis=1).astype(np.int32)
+    assert [ex.paged_slot_position(b) for b in range(B)] == [n + n_new for n in lens]
+    # slot 1 leaves: its row in the next step writes the trash page and its logits are
+    # unused; the other slots are unaffected; then one slot alone (the fused GEMVs)
+    ex.paged_kv_free_slot(1)
+    assert ex.get_paged_active_vram_bytes() == (n_pages - 2) * per_page
+    ex.prepare({"b": B, "s": 1})
+    ex.set_input_by_id(tid_in, toks)
+    ex.run()
+    out = ex.get_output(tid_out)
+    for b in (0, 2, 3):
+        _check_spread(out[b], *_ref_step(refs[b], singles[b], tid_in, tid_out, toks[b], lens[b] + n_new), ("freed", b))
+    tok0 = int(np.argmax(out[0]))
+    ex.prepare({"b": 1, "s": 1})
+    ex.set_input_by_id(tid_in, np.array([tok0], np.int32))
+    ex.run()
+    _check_spread(ex.get_output(tid_out)[0], *_ref_step(refs[0], singles[0], tid_in, tid_out, tok0, lens[0] + n_new + 1),
+                  "b=1")
+    shapes = ex.runtime_mul_mat_shape_summary()
+    assert shapes["mul_mat"] and shapes["flash_attn"][0]["n"] == c.n_layer
+    # rejected calls leave the handle usable
+    with pytest.raises(GQError, match="max_batch"):
+        ex.prepare({"b": 9, "s": 1})
+    ex.paged_kv_alloc_slot(5)  # allocated, no pages yet
+    ex.prepare({"b": 6, "s": 1})
+    ex.set_input_by_id(tid_in, np.ones(6, np.int32))
+    with pytest.raises(GQError, match="ensure_tokens"):
+        ex.run()
+    with pytest.raises(GQError, match="not allocated"):
+        ex.paged_kv_ensure_tokens(1, 10)
+    with pytest.raises(GQError, match="slot"):
+        ex.paged_kv_alloc_slot(8)
+    with pytest.raises(GQError, match="not in use"):
+        ex.paged_page_release(100000)
+    ex.paged_kv_free_slot(5)
+    ex.run()  # the prepared step, now with slots 1, 4 and 5 idle
+    assert np.isfinite(ex.get_output(tid_out)[[0, 2, 3]]).all()
+    ex.set_enable_profile(True)
+    ex.prepare({"b": 1, "s": 1})
+    ex.set_input_by_id(tid_in, np.array([1], np.int32))
+    ex.run()
+    prof = ex.get_profile()
+    assert prof["n_run"] == 1 and prof["n_prepare"] == 1 and prof["run_ms"] > 0
