@@ -177,6 +177,9 @@ def main() -> int:
         "unit": "GB/s",
         "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
         "traffic": load_traffic("k_gemv_grp<Q4_0, M=1> fused step mix"),
+        "traffic_source": "not measured in this run: HBM bytes per launch from two rocprofv3 --pmc passes "
+                          "(FETCH_SIZE, WRITE_SIZE, scaled by a 256 MiB copy) over an eager replay of the same "
+                          "129 launches (bench.py --traffic-probe), profiles/gemv_traffic.json",
         "bytes_per_launch": round(gemv_bytes_token / n_gemv),
         "weight_bytes_per_launch": round(weights_token / n_gemv),
         "us_per_launch": round(gemv_ms_token * 1e3 / n_gemv, 3),
@@ -570,11 +573,11 @@ def measured_ceilings(dev) -> tuple[float, float]:
 
     big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
-    Lib = _lib.load()
+    Lib = _probe_lib()
     stream = torch.cuda.current_stream()
 
     def probe():
-        _lib.check(Lib.gq_probe_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(), stream.cuda_stream))
+        _probe_check(Lib.gqbench_stream_read(big.data_ptr(), big.numel(), sink.data_ptr(), stream.cuda_stream))
 
     probe(), probe()
     torch.cuda.synchronize()
@@ -723,20 +726,42 @@ def gemv_sweep_q8_0(dev, ws, min_launches: int = 96, reps: int = 3) -> list:
     return rows
 
 
+_PROBE = None
+
+
+def _probe_lib():
+    """libgqbench.so: the streaming-read probe (a measurement aid outside libgq's ABI)."""
+    global _PROBE
+    if _PROBE is None:
+        import ctypes
+
+        path = ROOT / "ggmlc_amd" / "libgqbench.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built; run `python -m ggmlc_amd.build`")
+        lib = ctypes.CDLL(str(path))
+        lib.gqbench_stream_read.restype = ctypes.c_int
+        lib.gqbench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+        _PROBE = lib
+    return _PROBE
+
+
+def _probe_check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"streaming-read probe: HIP error {rc}")
+
+
 def time_probe_launches(bufs, reps: int = 5) -> float:
     """ms for one pass of streaming-read probes, one launch per buffer (each read once,
     whole), captured in a graph and timed like the GEMV graphs."""
     import torch
 
-    from ggmlc_amd import _lib
-
-    Lib = _lib.load()
+    Lib = _probe_lib()
     sink = torch.zeros(4, dtype=torch.int32, device=bufs[0].device)
 
     def run():
         st = torch.cuda.current_stream().cuda_stream  # the capture stream inside the graph
         for b in bufs:
-            _lib.check(Lib.gq_probe_stream_read(b.data_ptr(), b.numel() // 16 * 16, sink.data_ptr(), st))
+            _probe_check(Lib.gqbench_stream_read(b.data_ptr(), b.numel() // 16 * 16, sink.data_ptr(), st))
 
     return time_graph(run, reps)
 
@@ -792,8 +817,11 @@ def load_traffic(kernel: str) -> float | None:
 
 
 def cpu_identity() -> dict:
-    """Host CPU model and the ISA extensions ggml's x86 kernels use."""
-    model, flags = "unknown", set()
+    """Host CPU model (lscpu's "Model name", else /proc/cpuinfo's), its family / model /
+    stepping, sockets and cores, and the ISA extensions ggml's x86 kernels use."""
+    import subprocess
+
+    model, flags, extra = "unknown", set(), {}
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name") and model == "unknown":
@@ -802,9 +830,21 @@ def cpu_identity() -> dict:
                 flags = set(line.split(":", 1)[1].split())
     except OSError:
         pass
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "Model name" and v:
+                model = v
+            elif k in ("CPU family", "Model", "Stepping", "Socket(s)", "Core(s) per socket", "Thread(s) per core",
+                       "Vendor ID", "BIOS Model name"):
+                extra[k] = v
+    except (OSError, subprocess.SubprocessError):
+        pass
     isa = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni", "avx512_bf16",
                        "avx_vnni", "amx_int8", "amx_bf16") if f in flags]
-    return {"cpu_model": model, "isa": isa}
+    return {"cpu_model": model, "cpu_lscpu": extra, "isa": isa}
 
 
 def cpu_baseline(w, cfg, seconds: float, ctx: int = 1024) -> dict:

@@ -133,7 +133,6 @@ SIGNATURES = {
     "gq_paged_step_inputs": (ctypes.c_int, [_vp, _i64, _P, _i64, _i64, _vp, _vp, _vp]),
     "gq_paged_advance": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "gq_kv_pages_copy": (ctypes.c_int, [_P, _P, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, _vp]),
-    "gq_probe_stream_read": (ctypes.c_int, [_vp, ctypes.c_size_t, _vp, _vp]),
     "gq_exec_available_devices": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
     "gq_exec_create": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "gq_exec_free": (None, [_vp]),

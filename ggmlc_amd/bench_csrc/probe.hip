@@ -1,13 +1,12 @@
-// Streaming-read probe: reads a buffer once with coalesced 16-byte nontemporal
-// loads (the access pattern of the GEMV weight stream) so a benchmark can state
-// the HBM read bandwidth this device actually sustains next to the datasheet
-// peak. Measurement aid only; it has no counterpart among ggml's operators.
+// Streaming-read probe of the benchmark (libgqbench.so, loaded by bench.py only; not
+// part of libgq's ABI): reads a buffer once with coalesced 16-byte nontemporal loads
+// (the access pattern of the GEMV weight stream) so a benchmark can state the HBM read
+// bandwidth this device actually sustains next to the datasheet peak.
 #include "common.h"
-#include "kernels.h"
-
-namespace gq {
 
 namespace {
+
+using gq::ld_nt16;
 
 __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p, int64_t n16,
                                                     uint32_t* __restrict__ sink) {
@@ -30,16 +29,15 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p,
 
 }  // namespace
 
-int read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t s) {
+// Reads `bytes` (16-byte aligned) of p once; sink: a device uint32 that is (practically)
+// never written. Returns 0, or a HIP error code.
+extern "C" int gqbench_stream_read(const void* p, size_t bytes, uint32_t* sink, hipStream_t s) {
     int dev = 0, ncu = 0;
-    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
-    if (rc) return rc;
-    rc = check_hip(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
-    if (rc) return rc;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return (int)e;
     const int64_t n16 = (int64_t)(bytes / 16);
     hipLaunchKernelGGL(k_read_probe, dim3((unsigned)(ncu * 8)), dim3(256), 0, s, reinterpret_cast<const uint4*>(p),
                        n16, sink);
-    return check_hip(hipGetLastError(), "read probe launch");
+    return (int)hipGetLastError();
 }
-
-}  // namespace gq

@@ -1,7 +1,9 @@
 """Build libgq.so (HIP, gfx950) in-tree: ``python -m ggmlc_amd.build``.
 
 Every .hip file under csrc/ is compiled by hipcc to an object in
-ggmlc_amd/_build/ (parallel), then linked into ggmlc_amd/libgq.so.
+ggmlc_amd/_build/ (parallel), then linked into ggmlc_amd/libgq.so. The benchmark's
+measurement aids under bench_csrc/ (the streaming-read probe) are linked into their
+own ggmlc_amd/libgqbench.so, outside libgq's ABI.
 """
 
 from __future__ import annotations
@@ -18,6 +20,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libgq.so"
+BENCH_CSRC = PKG / "bench_csrc"
+BENCH_LIB = PKG / "libgqbench.so"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -37,7 +41,7 @@ FLAGS = [
 
 
 def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
+    obj = BUILD / (src.parent.name + "_" + src.stem + ".o")
     cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -50,20 +54,26 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    BUILD.mkdir(exist_ok=True)
-    srcs = sorted(CSRC.glob("*.hip"))
-    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = True) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+    bench_srcs = sorted(BENCH_CSRC.glob("*.hip"))
+    jobs = min(len(srcs) + len(bench_srcs), int(os.environ.get("MAX_JOBS", "8")))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, srcs + bench_srcs))
+    _link(objs[:len(srcs)], LIB)
+    _link(objs[len(srcs):], BENCH_LIB)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources, {BENCH_LIB} from {len(bench_srcs)}")
     return LIB
 
 

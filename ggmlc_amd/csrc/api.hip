@@ -946,12 +946,4 @@ int gq_kv_pages_copy(gq_tensor* pool, gq_tensor* cache, const int32_t* pages, in
                          n_pages, lp, r0, r1, pool->ne[2], pool->ne[0] * 2, to_pool, (hipStream_t)stream);
 }
 
-// ---- measurement aid ------------------------------------------------------
-
-int gq_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, gq_stream_t stream) {
-    if (!p || !sink || bytes < 16 || (reinterpret_cast<uintptr_t>(p) & 15))
-        return fail(GQ_ERR_INVALID, "probe_stream_read: needs a 16-byte aligned buffer and a sink");
-    return read_probe(p, bytes, sink, (hipStream_t)stream);
-}
-
 }  // extern "C"

@@ -248,7 +248,5 @@ int kv_pages_copy(uint8_t* pool, int64_t pnb1, int64_t pnb2, int64_t prows, uint
                   const int32_t* pages, int64_t n_pages, int log2p, int64_t r0, int64_t r1, int64_t H,
                   int64_t row_bytes, int to_pool, hipStream_t st);
 
-// probe.hip
-int read_probe(const void* p, size_t bytes, uint32_t* sink, hipStream_t s);
 
 }  // namespace gq

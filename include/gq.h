@@ -529,13 +529,6 @@ int gq_exec_runtime_graph_summary(gq_exec* h, char* buf, size_t buf_len, size_t*
  * and the attention launches' shapes of the last issued step, most frequent first. */
 int gq_exec_runtime_mul_mat_shape_summary(gq_exec* h, char* buf, size_t buf_len, size_t* needed);
 
-/* ---- measurement aid ------------------------------------------------------
- * No counterpart in the reference. Reads `bytes` (16-byte aligned) once with
- * the coalesced 16-byte streaming loads the GEMV uses, so a benchmark can
- * report the read bandwidth the device sustains beside the datasheet peak.
- * `sink` is a device uint32 that is (practically) never written. */
-int gq_probe_stream_read(const void* p, size_t bytes, uint32_t* sink, gq_stream_t stream);
-
 #ifdef __cplusplus
 }
 #endif
