@@ -72,6 +72,40 @@ __device__ __forceinline__ float ld_ag(const float* p) {
     return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Arrive once this workgroup's partial stores are complete; true in the last arrival of
+// the pair (which also resets the pair's counter to zero). Every thread of the workgroup
+// calls it.
+// What this relies on (gfx950, as on gfx942): agent-scope atomic stores and loads carry
+// the sc1 bit, so they bypass the per-XCD L2 for coherence and are served by memory
+// (through the Infinity Fabric / MALL), never by a stale L2 line of another XCD;
+// s_waitcnt vmcnt(0) returns only after every such store has been acknowledged at that
+// level; the counter's fetch_add is performed at the same level, so a workgroup that
+// reads n_split - 1 from it runs after every other workgroup's partials are visible to
+// sc1 loads. The loads of the merge are atomic, so the compiler cannot hoist them above
+// the __syncthreads that follows the arrival. The C++/HIP memory model would ask for a
+// release fetch_add and an acquire fence instead; both write back / invalidate the whole
+// XCD L2 on this target (measured: the merge took 38 us instead of ~2 us), so the
+// protocol stays at the hardware level. gq_attn_reset_counters clears the counters
+// after a launch that did not finish.
+__device__ __forceinline__ bool arrive_last(unsigned* ctr, int n_split) {
+    __shared__ int sLast;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == (unsigned)(n_split - 1);
+        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sLast = last;
+    }
+    __syncthreads();
+    return sLast != 0;
+}
+
+// The reduction of k_attn_merge for one (query vector, dim d) with the same operations in
+// the same order, every split's (m, l, o) requested at once: one memory round trip
+// (n_split <= FUSE_MAX_SPLIT). base: split 0's partial row; stride: floats between splits.
+__device__ __forceinline__ float merge_splits_ag(const float* base, int64_t stride, int n_split, int d);
+
 struct Plan {
     int64_t G, NQ, n_qt, n_chunks, cps, n_split;
     bool dec;               // k_attn_dec: one workgroup per (split, kv head), all NQ queries
@@ -421,40 +455,17 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         }
     }
     if (!fuse || n_split == 1) return;
-
-    // Arrive once this workgroup's partial stores are complete; the last arrival merges.
-    // What this relies on (gfx950, as on gfx942): agent-scope atomic stores and loads
-    // carry the sc1 bit, so they bypass the per-XCD L2 for coherence and are served by
-    // memory (through the Infinity Fabric / MALL), never by a stale L2 line of another
-    // XCD; s_waitcnt vmcnt(0) returns only after every such store has been acknowledged
-    // at that level; the counter's fetch_add is performed at the same level, so a
-    // workgroup that reads n_split - 1 from it runs after every other workgroup's
-    // partials are visible to sc1 loads. The loads below are atomic, so the compiler
-    // cannot hoist them above the __syncthreads that follows the arrival. The C++/HIP
-    // memory model would ask for a release fetch_add and an acquire fence instead;
-    // both write back / invalidate the whole XCD L2 on this target (measured: the merge
-    // took 38 us instead of ~2 us), so the protocol stays at the hardware level.
-    // gq_attn_reset_counters clears the counters after a launch that did not finish.
-    __shared__ int sLast;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        unsigned* ctr = &g_attn_arrive[(fuse - 1) * ARRIVE_N + seq * Hkv + hk];
-        const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == (unsigned)(n_split - 1);
-        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sLast = last;
-    }
-    __syncthreads();
-    if (!sLast) return;
-    // The reduction of k_attn_merge with the same operations in the same order, one
-    // thread per (query vector, dim) with every split's (m, l, o) requested at once:
-    // one memory round trip (n_split <= FUSE_MAX_SPLIT, nq <= 256 / D).
-    const int u = tid / D, d = tid % D;
+    if (!arrive_last(&g_attn_arrive[(fuse - 1) * ARRIVE_N + seq * Hkv + hk], n_split)) return;
+    const int u = tid / D, d = tid % D;  // one thread per (query vector, dim): nq <= 256 / D
     if (u >= nq) return;
     const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;
-    const int64_t stride = (int64_t)Hkv * nqt * (D + 2);
-    const float* base = part + ((int64_t)hk * nqt + (int64_t)seq * nq + u) * (D + 2);
+    const float mo = merge_splits_ag(part + ((int64_t)hk * nqt + (int64_t)seq * nq + u) * (D + 2),
+                                     (int64_t)Hkv * nqt * (D + 2), n_split, d);
+    const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
+    if (d < a.D) a.dst[(i * a.Hq + h) * a.D + d] = mo;
+}
+
+__device__ __forceinline__ float merge_splits_ag(const float* base, int64_t stride, int n_split, int d) {
     float pm[FUSE_MAX_SPLIT], pl[FUSE_MAX_SPLIT], po[FUSE_MAX_SPLIT];
 #pragma unroll
     for (int s2 = 0; s2 < FUSE_MAX_SPLIT; ++s2) {
@@ -481,8 +492,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
             acc += po[s2] * w;
         }
     }
-    const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
-    if (d < a.D) a.dst[(i * a.Hq + h) * a.D + d] = L == 0.0f ? 0.0f : acc / L;
+    return L == 0.0f ? 0.0f : acc / L;
 }
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -791,9 +801,12 @@ __device__ __forceinline__ bool paged_item(const PagedKv& pg, int n_split, int H
     return false;
 }
 
+// fuse (contiguous route only): 0 the merge runs in k_attn_merge, else 1 + the stream's
+// counter set: the last workgroup of each kv head merges (G * D <= 256, n_split <=
+// FUSE_MAX_SPLIT), as in k_attn_dec
 template <int D>
 __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_split, float* __restrict__ part,
-                                                      PagedKv pg, int q16) {
+                                                      PagedKv pg, int q16, int fuse = 0) {
     constexpr int KS = D / 32;         // k-steps of the QK product
     constexpr int DT = D / 16;         // 16-dim tiles of O^T
     constexpr int KW = 32;             // keys per wave
@@ -1017,10 +1030,21 @@ __global__ __launch_bounds__(256) void k_attn_dec_mma(AttnArgs a, int G, int n_s
             a.dst[(seq * a.Hq + h) * D + d] = L == 0.0f ? 0.0f : acc / L;
         } else {
             float* pp = part + (((int64_t)split * Hkv + hk) * pg.B * G + (int64_t)seq * G + u) * (D + 2);
-            pp[2 + d] = acc;
-            if (d == 0) pp[0] = mx, pp[1] = L;
+            if (fuse) {
+                st_ag(pp + 2 + d, acc);
+                if (d == 0) st_ag(pp, mx), st_ag(pp + 1, L);
+            } else {
+                pp[2 + d] = acc;
+                if (d == 0) pp[0] = mx, pp[1] = L;
+            }
         }
     }
+    if (!fuse || n_split == 1) return;
+    if (!arrive_last(&g_attn_arrive[(fuse - 1) * ARRIVE_N + hk], n_split)) return;
+    const int u = tid / D, d = tid % D;
+    if (u >= G) return;
+    const float mo = merge_splits_ag(part + ((int64_t)hk * G + u) * (D + 2), (int64_t)Hkv * G * (D + 2), n_split, d);
+    a.dst[((int64_t)hk * G + u) * D + d] = mo;
 }
 
 // the matrix-core prefill kernel: no ALiBi / softcap, 16-byte aligned K/V rows,
@@ -1400,12 +1424,15 @@ int attention_contig_mma(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream
     const PagedKv pg{nullptr, nullptr, ns, 7, 1};
     const int q16 = (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 && a.qnb1 % 16 == 0 && a.qnb2 % 16 == 0;
     const dim3 g1((unsigned)(ns * a.Hkv));
+    // the last workgroup of each kv head merges when one thread per (query head, dim) fits
+    // the workgroup (SmolLM2: 3 x 64); larger groups keep the merge launch
+    const int set = fuse_merge_ok(ns, G, a.D, a.Hkv) ? arrive_set(s) : -1;
     if (a.D == 128)
-        hipLaunchKernelGGL(k_attn_dec_mma<128>, g1, dim3(256), 0, s, a, (int)G, (int)ns, part, pg, q16);
+        hipLaunchKernelGGL(k_attn_dec_mma<128>, g1, dim3(256), 0, s, a, (int)G, (int)ns, part, pg, q16, set + 1);
     else
-        hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, (int)G, (int)ns, part, pg, q16);
+        hipLaunchKernelGGL(k_attn_dec_mma<64>, g1, dim3(256), 0, s, a, (int)G, (int)ns, part, pg, q16, set + 1);
     const int rc = check_hip(hipGetLastError(), "flash_attn_ext (mfma decode) launch");
-    if (rc != GQ_OK || ns == 1) return rc;
+    if (rc != GQ_OK || ns == 1 || set >= 0) return rc;
     return launch_merge(a.D, part, (int)ns, (int)a.Hkv, (int)G, (int)G, a.Hq, a.dst, nullptr, 1, s);
 }
 
