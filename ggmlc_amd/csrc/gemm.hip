@@ -147,6 +147,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
     __shared__ __align__(16) uint16_t sAl[BM * LDK];
     __shared__ __align__(16) uint16_t sB[BN * LDK];
     __shared__ float sD[2][BN];  // weight scales of the K step's two blocks, per weight row
+    __shared__ float sRS[BM];    // the tile's activation row scales (read by the epilogue)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -192,6 +193,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
         const int kb = kt * 2 + lhalf;
         load_block_rs<QT>(wrs, wrow_off + (uint32_t)kb * BB, kb < nb && kt < kt1, rb[slot]);
     };
+
+    // the row scales go to LDS with the first step's tiles (the K loop's barriers publish
+    // them), so the epilogue needs no memory round trip of its own
+    if (tid < BM) sRS[tid] = m0 + tid < M ? rs[m0 + tid] : 1.0f;
 
     float16v acc[MI][2];
 #pragma unroll
@@ -287,10 +292,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ W, 
         // the activation rows' power-of-two scales (exact products; 1 for almost every row)
         float rsm[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            rsm[r] = m < M ? rs[m] : 1.0f;
-        }
+        for (int r = 0; r < 16; ++r) rsm[r] = sRS[wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
@@ -341,10 +343,12 @@ __global__ __launch_bounds__(512, 1) void k_gemm_ws(const uint8_t* __restrict__ 
     const int kt0 = (int)blockIdx.z * spk;
     const int kt1 = min((int)cdiv(K, BK), kt0 + spk);  // this workgroup's K steps [kt0, kt1)
 
+    __shared__ float sRS[BM];  // the tile's activation row scales (read by the consumers' epilogue)
     if (wave >= 4) {
         // producers: thread p -> B: (weight row p / 2, block p % 2); A: (token row p / 2,
         // 16-byte pieces 4 (p % 2) .. + 3 of the row's 128-byte K step, hi and lo)
         const int p = tid - 256;
+        if (p < BM) sRS[p] = m0 + p < M ? rs[m0 + p] : 1.0f;  // published by the first barrier
         const int lrow = p >> 1, lhalf = p & 1;
         const int arow = p >> 1, apiece = (p & 1) * AQ;
         uint4 rh[PF][AQ], rl[PF][AQ];
@@ -521,10 +525,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_ws(const uint8_t* __restrict__ 
         // the activation rows' power-of-two scales (exact products; 1 for almost every row)
         float rsm[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            rsm[r] = m < M ? rs[m] : 1.0f;
-        }
+        for (int r = 0; r < 16; ++r) rsm[r] = sRS[wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int64_t n = n0 + wn * 64 + j * 32 + (lane & 31);
@@ -578,16 +579,36 @@ int gemm_bm(int64_t N, int64_t M) {
 GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M) {
     GemmPlan p;
     p.bm = gemm_bm(N, M);
-    const int64_t tiles = cdiv(N, BN) * cdiv(M, p.bm), nk = cdiv(K, BK);
+    const int64_t ncu = num_cus();
+    const int64_t n_tiles = cdiv(N, BN), m_tiles = cdiv(M, p.bm), tiles = n_tiles * m_tiles, nk = cdiv(K, BK);
     // split K while the tiles leave CUs idle, keeping >= 4 K steps per split: up to one
     // workgroup per CU for 128-token tiles (k_gemm_ws holds a CU), two for 64-token tiles
     const int64_t per_cu = p.bm == 128 ? 1 : 2;
     int64_t ks = 1;
-    if (tiles < num_cus()) ks = std::min<int64_t>({cdiv(per_cu * num_cus(), tiles), nk / 4, 16});
+    if (tiles < ncu) ks = std::min<int64_t>({cdiv(per_cu * ncu, tiles), nk / 4, 16});
     if (ks < 1) ks = 1;
     p.spk = (int)cdiv(nk, ks);
     p.ks = (int)cdiv(nk, p.spk);  // no empty split
     p.part_bytes = p.ks > 1 ? (size_t)p.ks * M * N * sizeof(float) : 0;
+    p.n_head = N, p.ks_tail = 0, p.spk_tail = 0;
+    // 128-token tiles over more than one round of CUs: when the last round would be at most
+    // half full, its weight rows (whole columns of tiles: a round is ncu / m_tiles columns)
+    // run as a second launch with K split so that it fills the CUs (7B qkv at M = 512: 384
+    // tiles = 256 + 128, the 128 split 2 ways)
+    if (p.bm == 128 && tiles > ncu && ncu % m_tiles == 0) {
+        const int64_t per_round = ncu / m_tiles;  // tile columns per round
+        const int64_t head = tiles / ncu * per_round;
+        const int64_t tail_tiles = (n_tiles - head) * m_tiles;
+        if (tail_tiles > 0 && 2 * tail_tiles <= ncu) {
+            const int64_t kt = std::min<int64_t>({ncu / tail_tiles, nk / 4, 4});
+            if (kt >= 2) {
+                p.n_head = head * BN;
+                p.spk_tail = (int)cdiv(nk, kt);
+                p.ks_tail = (int)cdiv(nk, p.spk_tail);
+                p.part_bytes = (size_t)p.ks_tail * M * (N - p.n_head) * sizeof(float);
+            }
+        }
+    }
     return p;
 }
 
@@ -595,9 +616,8 @@ namespace {
 
 template <int QT>
 int launch(const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const float* rs, int64_t M,
-           float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias) {
+           float* dst, int64_t ldd, float* part, hipStream_t s, const float* bias, const GemmPlan& p) {
     const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
-    const GemmPlan p = gemm_plan(N, K, M);
     float* pp = p.ks > 1 ? part : nullptr;
     if (p.bm == 64) {
         const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, 64), (unsigned)p.ks);
@@ -631,9 +651,22 @@ int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, in
     if ((reinterpret_cast<uintptr_t>(W) & 3) != 0) return fail(GQ_ERR_INVALID, "gemm: weight not 4-byte aligned");
     if ((reinterpret_cast<uintptr_t>(A) & 15) != 0 || lda % 8 != 0 || lda < 2 * K)
         return fail(GQ_ERR_INVALID, "gemm: activation tile misaligned");
-    if (gemm_plan(N, K, M).ks > 1 && part == nullptr) return fail(GQ_ERR_WORKSPACE, "gemm: split K needs partials");
-    if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, A, lda, rs, M, dst, ldd, part, s, bias);
-    return launch<GQ_TYPE_Q4_0>(W, N, K, A, lda, rs, M, dst, ldd, part, s, bias);
+    const GemmPlan p = gemm_plan(N, K, M);
+    if ((p.ks > 1 || p.ks_tail > 1) && part == nullptr) return fail(GQ_ERR_WORKSPACE, "gemm: split K needs partials");
+    auto run = [&](const uint8_t* Wp, int64_t n, float* d, const float* b, const GemmPlan& q) {
+        return type == GQ_TYPE_Q8_0 ? launch<GQ_TYPE_Q8_0>(Wp, n, K, A, lda, rs, M, d, ldd, part, s, b, q)
+                                    : launch<GQ_TYPE_Q4_0>(Wp, n, K, A, lda, rs, M, d, ldd, part, s, b, q);
+    };
+    if (p.ks_tail == 0) return run(W, N, dst, bias, p);
+    // the whole rounds of tiles, then the tail's weight rows with K split (their own launch,
+    // partials and reduce): the same per-tile arithmetic, the tail's sums in split order
+    const int64_t row_bytes = (K / QK) * (type == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
+    GemmPlan head = p;
+    head.ks = 1, head.spk = (int)cdiv(K, BK);
+    if (int rc = run(W, p.n_head, dst, bias, head)) return rc;
+    GemmPlan tail = p;
+    tail.ks = p.ks_tail, tail.spk = p.spk_tail;
+    return run(W + p.n_head * row_bytes, N - p.n_head, dst + p.n_head, bias ? bias + p.n_head : nullptr, tail);
 }
 
 }  // namespace gq

@@ -97,6 +97,11 @@ int gemv(int type, const uint8_t* W, int64_t N, int64_t K, const ActSrc& act, in
 struct GemmPlan {
     int bm, ks, spk;
     size_t part_bytes;
+    // a last round of 128-token tiles that would leave at least half the CUs idle: the
+    // weight rows from n_head on run as a second launch with K split ks_tail ways
+    // (0: no tail launch)
+    int64_t n_head;
+    int ks_tail, spk_tail;
 };
 GemmPlan gemm_plan(int64_t N, int64_t K, int64_t M);
 int gemm(int type, const uint8_t* W, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const float* rs,

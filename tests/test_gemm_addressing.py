@@ -40,6 +40,36 @@ def gemm_plan(N, K, M, ncu=256):
     return bm, cdiv(nk, spk), spk
 
 
+def gemm_tail(N, K, M, ncu=256):
+    """gemm.hip gemm_plan's tail round: (n_head, ks_tail, spk_tail), or None. When the last
+    round of 128-token tiles would be at most half full, the weight rows from n_head on run
+    as a second launch with K split."""
+    bm = gemm_plan(N, K, M, ncu)[0]
+    n_tiles, m_tiles, nk = cdiv(N, BN), cdiv(M, bm), cdiv(K, BK)
+    tiles = n_tiles * m_tiles
+    if bm != 128 or tiles <= ncu or ncu % m_tiles:
+        return None
+    head = tiles // ncu * (ncu // m_tiles)
+    tail_tiles = (n_tiles - head) * m_tiles
+    if tail_tiles <= 0 or 2 * tail_tiles > ncu:
+        return None
+    kt = min(ncu // tail_tiles, nk // 4, 4)
+    if kt < 2:
+        return None
+    spk = cdiv(nk, kt)
+    return head * BN, cdiv(nk, spk), spk
+
+
+def launches(N, K, M, ncu=256):
+    """the launches of one GEMM: (weight rows, bm, ks, spk), the head first"""
+    bm, ks, spk = gemm_plan(N, K, M, ncu)
+    t = gemm_tail(N, K, M, ncu)
+    if t is None:
+        return [(N, bm, ks, spk)]
+    n_head, kt, spkt = t
+    return [(n_head, bm, 1, cdiv(K, BK)), (N - n_head, bm, kt, spkt)]
+
+
 PF = {128: 2, 64: 2}  # gemm.hip GEMM_PF_WS (k_gemm_ws), GEMM_PF_64 (k_gemm): K steps of loads in flight
 LDS_MAX = 160 * 1024  # LDS of one workgroup on gfx950
 
@@ -54,8 +84,8 @@ def stages(bm):
     return 2 if bm == 128 else 1
 
 
-def check_launch(qt, N, K, M):
-    bm, ks, spk = gemm_plan(N, K, M)
+def check_launch(qt, N, K, M, plan=None):
+    bm, ks, spk = plan if plan is not None else gemm_plan(N, K, M)
     bb = BLOCK[qt]
     row_bytes = (K // QK) * bb
     lda = 2 * K
@@ -160,10 +190,14 @@ def workspace_layout(N, K, M):
     ws_act = ws_rs + r256(M * 4)
     bm, ks, spk = gemm_plan(N, K, M)
     part = ks * M * N * 4 if ks > 1 else 0
+    t = gemm_tail(N, K, M)
+    if t is not None:
+        part = t[1] * M * (N - t[0]) * 4
     return ws_rs, ws_act, ws_act + r256(part)
 
 
-@pytest.mark.parametrize("qt,N,K,M", [(2, 4096, 4096, 512), (2, 96, 11008, 17), (8, 1600, 960, 37), (2, 96, 17408, 17)])
+@pytest.mark.parametrize("qt,N,K,M", [(2, 4096, 4096, 512), (2, 96, 11008, 17), (8, 1600, 960, 37), (2, 96, 17408, 17),
+                                     (2, 12288, 4096, 512)])
 def test_gemm_workspace_regions_disjoint(qt, N, K, M):
     ws_rs, ws_act, total = workspace_layout(N, K, M)
     assert M * 2 * K * 2 <= ws_rs  # the activation rows end before the row scales
@@ -190,7 +224,20 @@ SHAPES = [
 
 @pytest.mark.parametrize("qt,N,K,M", SHAPES)
 def test_gemm_addresses_in_bounds(qt, N, K, M):
-    check_launch(qt, N, K, M)
+    # each launch of the GEMM addresses its own weight rows (the tail launch: from n_head,
+    # with the output and bias offset the same way) over the same activation
+    for n, bm, ks, spk in launches(N, K, M):
+        check_launch(qt, n, K, M, (bm, ks, spk))
+
+
+def test_gemm_tail_round_plans():
+    """7B qkv at M = 512: 384 tiles = 256 + 128; the 128 (32 tile columns x 4 token tiles)
+    run with K split 2 ways; gate_up's last round (176 of 256) stays whole"""
+    assert launches(12288, 4096, 512) == [(8192, 128, 1, 64), (4096, 128, 2, 32)]
+    assert gemm_tail(22016, 4096, 512) is None
+    assert gemm_tail(4096, 4096, 512) is None  # 128 tiles: one round, K split as before
+    for n, bm, ks, spk in launches(12288, 4096, 512):
+        assert n % BN == 0 and ks * spk >= cdiv(4096, BK)
 
 
 def ws_schedule(kt0, kt1, pf):

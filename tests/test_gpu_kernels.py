@@ -129,7 +129,10 @@ def test_mlp_c2_q4_0(M):
                                    (1536, 2048, 16), (8960, 1536, 1), (256, 130, 5), (32, 7, 2),
                                    (8960, 1536, 16), (1536, 17920, 12),
                                    # 5..16 rows on int8 MFMA: row tails, K split in 1, 2 and 4 parts
-                                   (2048, 100, 9), (4096, 33, 13), (11008, 300, 16), (4096, 16500, 6)])
+                                   (2048, 100, 9), (4096, 33, 13), (11008, 300, 16), (4096, 16500, 6),
+                                   # a last round of tiles run as its own launch with K split
+                                   # (7B qkv at 512 tokens: 2 ways; Qwen2.5 gate|up: 4 ways)
+                                   (4096, 12288, 512), (1536, 17920, 512)])
 def test_mul_mat_shapes(qtype, K, N, M):
     _check_mm(qtype, K, N, M, seed=K + N + M)
 
@@ -371,6 +374,7 @@ def test_mul_mat_fused_rope_kv_bit_identical(qtype, K, Hq, Hkv, hd, M, mode, n_d
     (O.Q4_0, 4096, 12288, 37, "gemm"),      # prompt rows: GEMM path, bias in the tile store
     (O.Q8_0, 1536, 17920, 16, "swiglu"),    # batch 16: SWIGLU in the int8 GEMM's epilogue
     (O.Q4_0, 4096, 22016, 6, "swiglu"),     # 6 rows, Q4_0
+    (O.Q8_0, 4096, 12288, 512, "gemm"),     # the last round's rows as a split-K launch: bias offset with them
 ])
 def test_mul_mat_fused_bias_bit_identical(qtype, K, N, M, epi):
     """MUL_MAT with its bias input (executor.cpp:2436-2445: ADD(MUL_MAT(W, x), b)) fused
