@@ -73,6 +73,7 @@ def parse():
     p.add_argument("--c5-steps", type=int, default=64, help="timed batched decode steps per batch size")
     p.add_argument("--no-c5", action="store_true", help="skip the configs[4] continuous-batching decode")
     p.add_argument("--c5-only", action="store_true", help="run only the configs[4] measurement (profiling)")
+    p.add_argument("--c3-only", action="store_true", help="run only the configs[2] measurement (profiling)")
     p.add_argument("--c5-batches", default="1,2,4,8,16", help="configs[4] batch sizes")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the configs[3] decoder (pp, tg) and the step-GEMV roofline graph: the workload of "
@@ -81,6 +82,13 @@ def parse():
                    help="only launch one token's fused decode GEMVs and a 256 MiB device copy, eagerly, 3 times "
                         "each (the workload of the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs behind "
                         "roofline.traffic)")
+    p.add_argument("--attn-probe", action="store_true",
+                   help="only launch the configs[3] decode attention at its tg context over 16 K/V copies "
+                        "(cold in the Infinity Cache), eagerly, 3 rounds, then a 256 MiB device copy 3 times "
+                        "(the workload of the rocprofv3 --pmc runs behind the decode attention summary)")
+    p.add_argument("--attn-stamps", action="store_true",
+                   help="with --attn-probe: run the same launches through libgqbench's timestamped build of "
+                        "the attention and print the per-wave event times")
     p.add_argument("--gemm-probe", action="store_true",
                    help="only launch one ubatch's 128 prefill GEMMs (M = 512) eagerly, 3 times (the workload of "
                         "the rocprofv3 --pmc MFMA counter runs)")
@@ -132,7 +140,7 @@ def main() -> int:
     import torch
 
     from ggmlc_amd import _lib, ops
-    from ggmlc_amd.model import LLAMA_7B, SMOLLM2_360M, random_weights
+    from ggmlc_amd.model import LLAMA_7B, random_weights
 
     torch.cuda.set_device(0)
     _lib.check(_lib.load().gq_init())
@@ -140,6 +148,11 @@ def main() -> int:
     batches = tuple(int(b) for b in args.c5_batches.split(","))
     if args.c5_only:
         print(json.dumps({"c5_batched_decode": bench_c5(dev, args.c5_steps, batches)}), flush=True)
+        return 0
+    if args.attn_probe:
+        return attn_probe(dev, args.attn_stamps)
+    if args.c3_only:
+        print(json.dumps({"smollm2_c3": bench_c3(dev, args.pp_reps)}), flush=True)
         return 0
     cfg = LLAMA_7B
 
@@ -258,18 +271,7 @@ def main() -> int:
         result["mlp_c2_q4_0"] = bench_c2(dev, ws)
     if not args.no_c3:
         log("configs[2]: SmolLM2-360M-shape decoder")
-        w3 = random_weights(SMOLLM2_360M, dev, seed=360)
-        r3, d3 = bench_decoder(w3, dev, 512, 128, 2, args.pp_reps)
-        run3, bytes3 = step_gemv_launches(d3)
-        ms3 = time_graph(run3, 20, warm=3)
-        r3["step_gemvs"] = {"launches": len(bytes3), "us_per_launch": round(ms3 * 1e3 / len(bytes3), 3),
-                            "achieved_GBps": round(sum(bytes3) / (ms3 * 1e-3) / 1e9, 1),
-                            "ms_per_token": round(ms3, 4)}
-        r3["published_context"] = {"pp512_tok_s": 9900, "tg32_tok_s": 160.6,
-                                   "hardware": "NVIDIA RTX 4050 Laptop (reference README.md:243, "
-                                               "docs/benchmarks/ggmlc_vs_llama_cpp.md:121,150)"}
-        result["smollm2_c3"] = r3
-        del d3, w3, run3
+        result["smollm2_c3"] = bench_c3(dev, args.pp_reps)
         torch.cuda.empty_cache()
     if not args.no_c5:
         log("configs[4]: batched paged decode")
@@ -279,6 +281,24 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(w, cfg, args.cpu_seconds, ctx=args.prompt)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def bench_c3(dev, pp_reps: int) -> dict:
+    """the SmolLM2-360M-shape decoder (Q8_0): pp512 and tg128, plus its step
+    GEMVs replayed as one graph."""
+    from ggmlc_amd.model import SMOLLM2_360M, random_weights
+
+    w3 = random_weights(SMOLLM2_360M, dev, seed=360)
+    r3, d3 = bench_decoder(w3, dev, 512, 128, 2, pp_reps)
+    run3, bytes3 = step_gemv_launches(d3)
+    ms3 = time_graph(run3, 20, warm=3)
+    r3["step_gemvs"] = {"launches": len(bytes3), "us_per_launch": round(ms3 * 1e3 / len(bytes3), 3),
+                        "achieved_GBps": round(sum(bytes3) / (ms3 * 1e-3) / 1e9, 1),
+                        "ms_per_token": round(ms3, 4)}
+    r3["published_context"] = {"pp512_tok_s": 9900, "tg32_tok_s": 160.6,
+                               "hardware": "NVIDIA RTX 4050 Laptop (reference README.md:243, "
+                                           "docs/benchmarks/ggmlc_vs_llama_cpp.md:121,150)"}
+    return r3
 
 
 def bench_decoder(w, dev, prompt_len: int, steps: int, warmup: int, pp_reps: int):
@@ -788,6 +808,107 @@ def traffic_probe(w, dev) -> int:
     torch.cuda.synchronize()
     log(f"traffic probe: {3 * len(nbytes)} fused GEMV launches ({sum(nbytes) / len(nbytes):.0f} algorithmic "
         f"bytes per launch), 3 copies of {a.numel()} bytes")
+    return 0
+
+
+ATTN_EVENTS = ("start", "loads issued", "first K row in registers", "rows accumulated", "partial stored",
+               "arrival counted", "merge written", "end")
+
+
+def attn_probe(dev, stamps: bool) -> int:
+    """The decode attention of the configs[3] step at its tg context: 32 heads of 128,
+    the query at position 1099, the 1280-row KV bucket (mask 0 up to the position, -32768
+    after it, as the step builds it), over 16 K/V copies (336 MB, more than the 256 MB
+    Infinity Cache, so each launch reads its rows from HBM as in the step). Without
+    stamps: the product launches eagerly (3 rounds of 16) and 3 x 256 MiB device copies
+    that calibrate FETCH_SIZE / WRITE_SIZE. With stamps: 2 rounds through libgqbench's
+    timestamped build (same source and launch plan), the second round's per-wave event
+    times summarised (µs from the launch's first wave start; s_memrealtime at 100 MHz)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from ggmlc_amd import ops
+
+    Hq = Hkv = 32
+    D, pos, n_kv, copies = 128, 1099, 1280, 16
+    gen = torch.Generator(device=dev).manual_seed(7)
+    ks = [torch.randn((Hkv, n_kv, D), device=dev, generator=gen).half() for _ in range(copies)]
+    vs = [torch.randn((Hkv, n_kv, D), device=dev, generator=gen).half() for _ in range(copies)]
+    q = torch.randn((Hq, 1, D), device=dev, generator=gen)
+    mask = torch.zeros((1, n_kv), dtype=torch.float16, device=dev)
+    mask[0, pos + 1:] = -32768.0
+    out = torch.empty((1, Hq, D), device=dev)
+    ws = ops.Workspace(dev)
+    scale = 1.0 / float(np.sqrt(D))
+    if not stamps:
+        for _ in range(3):
+            for i in range(copies):
+                ops.flash_attn_ext(q, ks[i], vs[i], mask, scale, out=out, ws=ws)
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        c = torch.empty_like(a)
+        for _ in range(3):
+            c.copy_(a)
+        torch.cuda.synchronize()
+        log(f"attention probe: {3 * copies} decode attention launches (Hq {Hq}, D {D}, n_kv {n_kv}, valid rows "
+            f"{pos + 1}, {2 * Hkv * n_kv * D * 2} K/V bytes each), 3 copies of {a.numel()} bytes")
+        return 0
+
+    lib = _probe_lib()
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.gqbench_attn_stamped.restype = ctypes.c_int
+    lib.gqbench_attn_stamped.argtypes = [vp, i64, i64, i64, i64, vp, vp, i64, i64, vp, ctypes.c_float, vp, vp,
+                                         ctypes.c_size_t, vp]
+    lib.gqbench_attn_stamp_slots.restype = ctypes.c_int
+    lib.gqbench_attn_stamps_take.restype = ctypes.c_int
+    lib.gqbench_attn_stamps_take.argtypes = [vp]
+    lib.gqbench_attn_last_error.restype = ctypes.c_char_p
+    host = np.zeros(lib.gqbench_attn_stamp_slots(), dtype=np.uint64)
+    wbytes = 16 << 20
+    wsp = ws.get(wbytes)[0]
+
+    def take():
+        if lib.gqbench_attn_stamps_take(host.ctypes.data) != 0:
+            raise RuntimeError(lib.gqbench_attn_last_error().decode())
+        return host.copy()
+
+    take()
+    runs = []
+    for r in range(2):
+        for i in range(copies):
+            rc = lib.gqbench_attn_stamped(q.data_ptr(), D, 1, Hq, Hkv, ks[i].data_ptr(), vs[i].data_ptr(), n_kv,
+                                          n_kv * D * 2, mask.data_ptr(), scale, out.data_ptr(), wsp, wbytes,
+                                          torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(lib.gqbench_attn_last_error().decode())
+            torch.cuda.synchronize()
+            st = take()
+            if r == 1:
+                runs.append(st.reshape(-1, 8))
+    stamped = out.clone()
+    ref = ops.flash_attn_ext(q, ks[-1], vs[-1], mask, scale)  # libgq on the last launch's copy
+    torch.cuda.synchronize()
+    summary = {"waves": None, "events_us": {}}
+    per_event = {e: [] for e in range(8)}
+    spans, waves = [], []
+    for st in runs:
+        live = st[st[:, 0] != 0].astype(np.int64)
+        waves.append(len(live))
+        t0 = live[:, 0].min()
+        spans.append((live[:, 7].max() - t0) / 100.0)
+        for e in range(8):
+            v = live[:, e]
+            per_event[e].extend(((v[v != 0] - t0) / 100.0).tolist())
+    summary["waves"] = int(np.median(waves))
+    summary["launch_span_us_median"] = round(float(np.median(spans)), 2)
+    for e, name in enumerate(ATTN_EVENTS):
+        v = np.asarray(per_event[e])
+        if v.size:
+            summary["events_us"][name] = {"waves": int(v.size // len(runs)),
+                                          **{f"p{p}": round(float(np.percentile(v, p)), 2) for p in (0, 10, 50, 90, 100)}}
+    summary["bits_equal_to_libgq"] = bool(torch.equal(stamped, ref))
+    print(json.dumps({"attn_stamps": summary}), flush=True)
     return 0
 
 

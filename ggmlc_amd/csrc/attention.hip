@@ -51,6 +51,47 @@ constexpr int ARRIVE_SETS = 16;    // streams with counters of their own
 constexpr int FUSE_MAX_SPLIT = 16;  // splits merged from registers (one round trip)
 __device__ unsigned g_attn_arrive[ARRIVE_SETS * ARRIVE_N];
 
+// Per-wave timestamps of k_attn_dec (s_memrealtime, 100 MHz), compiled only into the
+// benchmark's measurement library (GQ_ATTN_STAMPS; libgq has none of this): event e of
+// wave w of workgroup (x, y) at g_attn_stamps[((y * gridDim.x + x) * 4 + w) * 8 + e];
+// 0 start, 1 K/V loads issued and the query scaled, 2 first K row converted, 3 every row
+// scored and accumulated, 4 partial stored, 5 arrival counted, 6 merge written, 7 end (0:
+// not reached). Stamps 2 and 3 take a register of the data as an asm input, so they cannot
+// be read before the loads they follow have returned.
+#ifdef GQ_ATTN_STAMPS
+constexpr int STAMP_SLOTS = 4096 * 4 * 8;
+__device__ unsigned long long g_attn_stamps[STAMP_SLOTS];
+#define GQ_STAMP(e)                                           \
+    do {                                                      \
+        __builtin_amdgcn_sched_barrier(0);                    \
+        stamp_[e] = __builtin_amdgcn_s_memrealtime();         \
+        __builtin_amdgcn_sched_barrier(0);                    \
+    } while (0)
+#define GQ_STAMP_AFTER(e, x)                                                           \
+    do {                                                                               \
+        unsigned long long t_;                                                         \
+        asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_) : "v"(x)); \
+        stamp_[e] = t_;                                                                \
+    } while (0)
+#define GQ_STAMP_FLUSH()                                                                                 \
+    do {                                                                                                 \
+        GQ_STAMP(7);                                                                                     \
+        const size_t i_ = (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6)) * 8; \
+        if ((threadIdx.x & 63) == 0 && i_ + 8 <= (size_t)STAMP_SLOTS)                                    \
+            for (int e_ = 0; e_ < 8; ++e_) g_attn_stamps[i_ + e_] = stamp_[e_];                          \
+    } while (0)
+#else
+#define GQ_STAMP(e) \
+    do {            \
+    } while (0)
+#define GQ_STAMP_AFTER(e, x) \
+    do {                     \
+    } while (0)
+#define GQ_STAMP_FLUSH() \
+    do {                 \
+    } while (0)
+#endif
+
 // the counter set of a stream (its first fused launch assigns one), or -1 when every set
 // is taken
 int arrive_set(hipStream_t s) {
@@ -256,6 +297,10 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
                                                   float m1, uint32_t n_head_log2, int qmode,
                                                   float* __restrict__ part, PagedKv pg, int fuse) {
     // fuse: 0 separate merge, else 1 + the stream's counter set (arrive_set)
+#ifdef GQ_ATTN_STAMPS
+    unsigned long long stamp_[8] = {};
+#endif
+    GQ_STAMP(0);
     constexpr int LPR = D / 8;       // lanes per row
     constexpr int RPI = 64 / LPR;    // rows per wave instruction
     constexpr int ROWS_IT = 4 * RPI;
@@ -364,6 +409,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
     // the mask values are converted only once every row's loads are in flight (a use
     // right after its load would wait for all loads issued before it)
     __builtin_amdgcn_sched_barrier(0);
+    GQ_STAMP(1);
     float mk[U][NQ];
 #pragma unroll
     for (int t = 0; t < U; ++t) {
@@ -381,6 +427,9 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         for (int t = 0; t < U; ++t) {
             float kf[8];
             h8_to_f(make_uint4(kw[t].x, kw[t].y, kw[t].z, kw[t].w), kf);
+#ifdef GQ_ATTN_STAMPS
+            if (u == 0 && t == 0) GQ_STAMP_AFTER(2, kf[0]);
+#endif
             float acc = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc = fmaf(q[u][e], kf[e], acc);
@@ -406,6 +455,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
         m[u] = mx;
     }
 
+    GQ_STAMP_AFTER(3, o[0][0]);
     // merge the row streams of the wave: partner lanes (xor 8 for D = 64, then xor 16,
     // xor 32) exchanged with DPP / permlane swaps (VALU, no LDS); the merge of two
     // (m, l, o) states is symmetric, so each lane may combine the pair in any order
@@ -454,15 +504,27 @@ __global__ __launch_bounds__(256) void k_attn_dec(AttnArgs a, int G, int nq, int
             }
         }
     }
-    if (!fuse || n_split == 1) return;
-    if (!arrive_last(&g_attn_arrive[(fuse - 1) * ARRIVE_N + seq * Hkv + hk], n_split)) return;
+    GQ_STAMP(4);
+    if (!fuse || n_split == 1) {
+        GQ_STAMP_FLUSH();
+        return;
+    }
+    const bool last = arrive_last(&g_attn_arrive[(fuse - 1) * ARRIVE_N + seq * Hkv + hk], n_split);
+    GQ_STAMP(5);
+    if (!last) {
+        GQ_STAMP_FLUSH();
+        return;
+    }
     const int u = tid / D, d = tid % D;  // one thread per (query vector, dim): nq <= 256 / D
-    if (u >= nq) return;
-    const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;
-    const float mo = merge_splits_ag(part + ((int64_t)hk * nqt + (int64_t)seq * nq + u) * (D + 2),
-                                     (int64_t)Hkv * nqt * (D + 2), n_split, d);
-    const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
-    if (d < a.D) a.dst[(i * a.Hq + h) * a.D + d] = mo;
+    if (u < nq) {
+        const int64_t nqt = PAGED ? (int64_t)pg.B * nq : nq;
+        const float mo = merge_splits_ag(part + ((int64_t)hk * nqt + (int64_t)seq * nq + u) * (D + 2),
+                                         (int64_t)Hkv * nqt * (D + 2), n_split, d);
+        const int64_t h = (int64_t)hk * G + u % G, i = seq + u / G;
+        if (d < a.D) a.dst[(i * a.Hq + h) * a.D + d] = mo;
+    }
+    GQ_STAMP(6);
+    GQ_STAMP_FLUSH();
 }
 
 __device__ __forceinline__ float merge_splits_ag(const float* base, int64_t stride, int n_split, int d) {
