@@ -17,6 +17,7 @@ BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
 
 GQ_OK = 0
 GQ_OPT_ATTN_SEPARATE_MERGE = 1
+GQ_OPT_GEMM_I8_RING = 2
 GQ_ATTN_SCRATCH_BYTES = 16 << 20  # gq_flash_attn_ext_noalloc's static scratch per device
 _ERR_NAMES = {-1: "GQ_ERR_INVALID", -2: "GQ_ERR_UNSUPPORTED", -3: "GQ_ERR_WORKSPACE", -4: "GQ_ERR_DEVICE"}
 

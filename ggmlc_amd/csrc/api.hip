@@ -15,8 +15,10 @@ namespace gq {
 
 static thread_local std::string g_err;
 static std::atomic<int> g_opt_separate_merge{0};
+static std::atomic<int> g_opt_i8_ring{0};
 
 bool option_attn_separate_merge() { return g_opt_separate_merge.load(std::memory_order_relaxed) != 0; }
+bool option_gemm_i8_ring() { return g_opt_i8_ring.load(std::memory_order_relaxed) != 0; }
 
 void set_error(const std::string& msg) { g_err = msg; }
 
@@ -128,6 +130,10 @@ int gq_set_option(int option, int64_t value) {
         case GQ_OPT_ATTN_SEPARATE_MERGE:
             if (value != 0 && value != 1) return fail(GQ_ERR_INVALID, "set_option: value must be 0 or 1");
             g_opt_separate_merge.store((int)value, std::memory_order_relaxed);
+            return GQ_OK;
+        case GQ_OPT_GEMM_I8_RING:
+            if (value != 0 && value != 1) return fail(GQ_ERR_INVALID, "set_option: value must be 0 or 1");
+            g_opt_i8_ring.store((int)value, std::memory_order_relaxed);
             return GQ_OK;
         default:
             return fail(GQ_ERR_INVALID, "set_option: unknown option " + std::to_string(option));

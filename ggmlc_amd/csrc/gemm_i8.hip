@@ -38,6 +38,7 @@ namespace {
 typedef int int4v __attribute__((ext_vector_type(4)));
 
 constexpr int NBS = 8;  // quant blocks per step
+constexpr int GEMM_I8_WHOLE_AC = 8;  // 16-byte pieces per thread of the LDS activation copy (32 KiB)
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any resource: reads 0, no fetch
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
@@ -57,11 +58,18 @@ enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_GLU = 2, EPI_GLU_Q8 = 3 };
 // ORD (KS == 1): the wave sums its K steps in the order of an ORD-part split (part k's
 // steps into their own sum, the parts added in part order), so a launch that needs whole
 // tiles per workgroup gives the bits of the plan's split launch of the same product.
-template <int QT, int KS, int EPI, int ORD = 1>
+// NSW > 0 (KS == 1, NSW steps in the row): the workgroup's activation (quants, scales and
+// block sums of every block, the workspace bytes as they are) is copied into dynamic LDS
+// once, and each wave requests all NSW weight steps of its tile before the first one is
+// used: one memory round trip per wave instead of one per step, the registers of the
+// per-step activation ring going to the weights. Same operations in the same order as the
+// ring, so the same bits.
+template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0>
 __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                     int64_t row_bytes, const uint8_t* __restrict__ act, int64_t M,
                                                     float* __restrict__ dst, int64_t ldd,
                                                     const float* __restrict__ bias, I8Epi epi) {
+    static_assert(NSW == 0 || KS == 1, "the whole-tile request takes one K part");
     static_assert(EPI != EPI_GLU_Q8 || KS == 1, "the quantized SWIGLU rows need 4 whole tiles per workgroup");
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int RB = NBS * BB;           // bytes of a row per step: 272 / 144
@@ -106,19 +114,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
         coff[i] = cval[i] ? (uint32_t)(prow * row_bytes + (c % CPR) * 16) : 0u;
     }
 
-    uint4 wb[2][LPL];
-    u32x2 ab[2][NBS];
-    float db[2][NBS];
-    int sb[2][NBS];
-    auto issue_w = [&](int s, int slot) {
+    auto issue_into = [&](int s, uint4(&wv)[LPL]) {
         const bool live = s < s1;
 #pragma unroll
         for (int i = 0; i < LPL; ++i) {
             const uint32_t off = live && cval[i] ? coff[i] + (uint32_t)s * RB : OOB;
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)off, 0, 0);
-            wb[slot][i] = make_uint4(v.x, v.y, v.z, v.w);
+            wv[i] = make_uint4(v.x, v.y, v.z, v.w);
         }
     };
+    uint4 wb[NSW ? 1 : 2][LPL];
+    u32x2 ab[NSW ? 1 : 2][NBS];
+    float db[NSW ? 1 : 2][NBS];
+    int sb[NSW ? 1 : 2][NBS];
+    auto issue_w = [&](int s, int slot) { issue_into(s, wb[slot]); };
     auto issue_a = [&](int s, int slot) {
         const bool live = s < s1;
 #pragma unroll
@@ -137,12 +146,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
     const int nsh = QT == GQ_TYPE_Q8_0 ? 0 : 4 * (g >> 1);  // Q4_0: low or high nibbles
     // one step from ring slot `slot`: park its weights, refill the slot with step s + 2,
     // then the 8 blocks' MFMAs
-    auto body = [&](int s, int slot) {
-#pragma unroll
-        for (int i = 0; i < LPL; ++i)
-            if (cval[i]) *reinterpret_cast<uint4*>(st + (lane + 64 * i) * 16) = wb[slot][i];
-        wave_lds_sync();
-        issue_w(s + 2, slot);
+    // the 8 blocks of step s from the parked slice; xop(b, xa, dx, sa) gives block b's
+    // activation operand, scale and block sum
+    auto blocks = [&](int s, auto xop) {
 #pragma unroll
         for (int b = 0; b < NBS; ++b) {
             // weight operand: 8 bytes at row lr, block b, quant byte 8 gq (2 + 34 b / 18 b
@@ -164,17 +170,37 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
                 hi = (hi >> nsh) & 0x0f0f0f0fu;
             }
             const long wa = (long)(((uint64_t)hi << 32) | lo);
-            const long xa = (long)(((uint64_t)ab[slot][b].y << 32) | ab[slot][b].x);
+            u32x2 xq;
+            float dx;
+            int sa;
+            xop(b, xq, dx, sa);
+            const long xa = (long)(((uint64_t)xq.y << 32) | xq.x);
             const int4v zero = {0, 0, 0, 0};
             const int4v d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, xa, zero, 0, 0, 0);
-            const float dx = db[slot][b];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float dw = h2f(*reinterpret_cast<const uint16_t*>(st + (4 * g + r) * RB + b * BB));
-                const int isum = QT == GQ_TYPE_Q8_0 ? d[r] : d[r] - 8 * sb[slot][b];
+                const int isum = QT == GQ_TYPE_Q8_0 ? d[r] : d[r] - 8 * sa;
                 acc[r] = __builtin_fmaf((float)isum, dw * dx, acc[r]);
             }
         }
+    };
+    auto park = [&](const uint4(&wv)[LPL]) {
+#pragma unroll
+        for (int i = 0; i < LPL; ++i)
+            if (cval[i]) *reinterpret_cast<uint4*>(st + (lane + 64 * i) * 16) = wv[i];
+        wave_lds_sync();
+    };
+    // one step from ring slot `slot`: park its weights, refill the slot with step s + 2,
+    // then the 8 blocks' MFMAs
+    auto body = [&](int s, int slot) {
+        park(wb[slot]);
+        issue_w(s + 2, slot);
+        blocks(s, [&](int b, u32x2& xq, float& dx, int& sa) {
+            xq = ab[slot][b];
+            dx = db[slot][b];
+            sa = QT == GQ_TYPE_Q8_0 ? 0 : sb[slot][b];
+        });
         wave_lds_sync();  // the slice is read before the next step parks
         issue_a(s + 2, slot);
     };
@@ -197,20 +223,60 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
         }
     };
 
-    issue_w(s0, 0);
-    issue_a(s0, 0);
-    issue_w(s0 + 1, 1);
-    issue_a(s0 + 1, 1);
-    int s = s0;
-    for (; s + 1 < s1; s += 2) {
-        fold(s);
-        body(s, 0);
-        fold(s + 1);
-        body(s + 1, 1);
-    }
-    if (s < s1) {
-        fold(s);
-        body(s, 0);
+    if constexpr (NSW > 0) {
+        // the activation's bytes into LDS (its loads first, so waiting for them leaves the
+        // weight loads in flight), then every weight step of the wave, then the steps in
+        // order as their loads return
+        // Every thread copies AC pieces of 16 bytes whether or not they hold data (pieces
+        // past the bytes read 0 from the resource and land in the buffer's slack, which
+        // the launch sizes to AC * 4096 bytes): a conditional copy lets the compiler sink
+        // the load into the branch, behind the weight loads.
+        extern __shared__ __align__(16) uint8_t s_act[];
+        const int abytes = nb * (QT == GQ_TYPE_Q4_0 ? 640 : 576);
+        const __amdgpu_buffer_rsrc_t ars = rsrc(act, abytes);
+        u32x4 av[GEMM_I8_WHOLE_AC];
+#pragma unroll
+        for (int i = 0; i < GEMM_I8_WHOLE_AC; ++i)
+            av[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, ((int)threadIdx.x + 256 * i) * 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        uint4 wr[NSW][LPL];
+#pragma unroll
+        for (int j = 0; j < NSW; ++j) issue_into(s0 + j, wr[j]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < GEMM_I8_WHOLE_AC; ++i)
+            *reinterpret_cast<u32x4*>(s_act + ((int)threadIdx.x + 256 * i) * 16) = av[i];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NSW; ++j) {
+            const int s = s0 + j;
+            if (s >= s1) break;  // uniform
+            fold(s);
+            park(wr[j]);
+            blocks(s, [&](int b, u32x2& xq, float& dx, int& sa) {
+                const int e = (s * NBS + b) * 16 + lr;  // (block, activation row)
+                xq = *reinterpret_cast<const u32x2*>(s_act + e * 32 + 8 * g);
+                dx = *reinterpret_cast<const float*>(s_act + nb * 512 + e * 4);
+                sa = QT == GQ_TYPE_Q8_0 ? 0 : *reinterpret_cast<const int*>(s_act + nb * 576 + e * 4);
+            });
+            wave_lds_sync();  // the slice is read before the next step parks
+        }
+    } else {
+        issue_w(s0, 0);
+        issue_a(s0, 0);
+        issue_w(s0 + 1, 1);
+        issue_a(s0 + 1, 1);
+        int s = s0;
+        for (; s + 1 < s1; s += 2) {
+            fold(s);
+            body(s, 0);
+            fold(s + 1);
+            body(s + 1, 1);
+        }
+        if (s < s1) {
+            fold(s);
+            body(s, 0);
+        }
     }
     if constexpr (ORD > 1) {  // the last part's sum, then the parts in order (empty ones 0)
         const int kl = (s1 - 1) / spo;
@@ -326,14 +392,35 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
     }
 }
 
+// One-part launches of rows of WHOLE_STEPS steps (K = 1536: the configs[4] gate|up and
+// output head) request each wave's whole tile at once, the activation staged in LDS
+// (measured on the configs[4] shapes; GQ_OPT_GEMM_I8_RING keeps the per-step ring)
+constexpr int WHOLE_STEPS = 6;
+static_assert(GEMM_I8_WHOLE_AC * 4096 >= WHOLE_STEPS * NBS * 640, "the LDS copy covers the activation bytes");
+
+template <int QT, int EPI, int ORD>
+int launch_whole(const dim3& g, const uint8_t* W, int64_t N, int64_t K, int64_t row_bytes, const uint8_t* act,
+                 int64_t M, float* dst, int64_t ldd, hipStream_t s, const float* bias, const I8Epi& e) {
+    const size_t lds = (size_t)GEMM_I8_WHOLE_AC * 4096;  // every thread's pieces, data or not
+    hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, ORD, WHOLE_STEPS>), g, dim3(256), lds, s, W, N, K, row_bytes, act, M,
+                       dst, ldd, bias, e);
+    return check_hip(hipGetLastError(), "gemm_i8 launch");
+}
+
 template <int QT, int EPI>
 int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst, int64_t ldd,
                hipStream_t s, const float* bias, const I8Epi& e) {
     const int64_t row_bytes = (K / QK) * (QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES);
     const GemmI8Plan p = gemm_i8_plan(N, K);
+    const bool whole = K / (QK * NBS) == WHOLE_STEPS && !option_gemm_i8_ring();
     if constexpr (EPI == EPI_GLU_Q8) {  // one quant block (64 logical rows) per workgroup,
         // summed in the order of the plan's split (the bits of the unfused product)
         const dim3 g((unsigned)(N / 64));
+        if (whole) {
+            if (p.ks == 4) return launch_whole<QT, EPI, 4>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+            if (p.ks == 2) return launch_whole<QT, EPI, 2>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+            return launch_whole<QT, EPI, 1>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+        }
         if (p.ks == 4)
             hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, 4>), g, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd,
                                bias, e);
@@ -346,6 +433,7 @@ int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64
         return check_hip(hipGetLastError(), "gemm_i8 launch");
     }
     const dim3 grid((unsigned)p.wgs);
+    if (p.ks == 1 && whole) return launch_whole<QT, EPI, 1>(grid, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
     if (p.ks == 4)
         hipLaunchKernelGGL((k_gemm_i8<QT, 4, EPI == EPI_GLU_Q8 ? EPI_GLU : EPI>), grid, dim3(256), 0, s, W, N, K,
                            row_bytes, act, M, dst, ldd, bias, e);

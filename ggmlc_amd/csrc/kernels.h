@@ -7,6 +7,7 @@ namespace gq {
 
 // api.hip: process-wide switches set through gq_set_option
 bool option_attn_separate_merge();
+bool option_gemm_i8_ring();
 
 // quantize.hip
 int quantize_q8_0_blocks(const float* x, int64_t nrows, int64_t K, int64_t x_stride, void* y,

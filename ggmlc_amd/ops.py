@@ -129,6 +129,19 @@ class separate_attn_merge:
         return False
 
 
+class gemm_i8_ring:
+    """Context manager: the int8 path streams every product's weights through its per-step
+    ring (gq_set_option GQ_OPT_GEMM_I8_RING) inside the block; same bits, for comparisons."""
+
+    def __enter__(self):
+        check(_lib.load().gq_set_option(_lib.GQ_OPT_GEMM_I8_RING, 1))
+        return self
+
+    def __exit__(self, *exc):
+        check(_lib.load().gq_set_option(_lib.GQ_OPT_GEMM_I8_RING, 0))
+        return False
+
+
 def quantize_row_q8_0(x: torch.Tensor) -> torch.Tensor:
     """x: fp32 contiguous, numel % 32 == 0 -> uint8 [..., K/32*34] block_q8_0 bytes."""
     if x.dtype != torch.float32 or not x.is_contiguous():

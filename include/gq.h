@@ -73,9 +73,13 @@ int gq_init(void);
  * they choose between launch plans that give the same bits, so a test or a
  * measurement can compare them. Unknown options or values return GQ_ERR_INVALID.
  *   GQ_OPT_ATTN_SEPARATE_MERGE (0 default / 1): decode attention merges its KV
- *   splits in a second launch instead of inside the decode kernel. */
+ *   splits in a second launch instead of inside the decode kernel.
+ *   GQ_OPT_GEMM_I8_RING (0 default / 1): the int8 path for 1..16 rows streams every
+ *   product's weights through its per-step register ring, also where a wave would
+ *   otherwise request its whole tile at once with the activation staged in LDS. */
 enum gq_option {
     GQ_OPT_ATTN_SEPARATE_MERGE = 1,
+    GQ_OPT_GEMM_I8_RING = 2,
 };
 int gq_set_option(int option, int64_t value);
 

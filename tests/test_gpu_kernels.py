@@ -454,6 +454,42 @@ def test_swiglu_quantized_rows_feed_down_bit_identical(qtype, K, F, M):
         assert torch.equal(got, want), (got - want).abs().max().item()
 
 
+@pytest.mark.parametrize("qtype,N,M,mode", [
+    (O.Q8_0, 65536, 16, "plain"),   # one K part: a wave's whole tile requested at once
+    (O.Q4_0, 65552, 5, "plain"),    # row tiles past N in the last workgroup
+    (O.Q8_0, 17920, 16, "swiglu"),  # Qwen2.5-1.5B gate|up with the quantized rows (2-part order)
+    (O.Q4_0, 1024, 9, "swiglu"),    # 4-part order
+])
+def test_gemm_i8_whole_tile_bits(qtype, N, M, mode):
+    """Rows of 6 steps (K = 1536) on one K part stage the activation in LDS and request each
+    wave's whole tile at once: the bits of the per-step ring (GQ_OPT_GEMM_I8_RING), and
+    within 1e-5 of the oracle."""
+    K = 1536
+    g = torch.Generator(device=DEV)
+    g.manual_seed(N + M)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV)
+
+    def run():
+        if mode == "plain":
+            return [ops.mul_mat(w, x)]
+        q8 = torch.full((ops.q8_rows_bytes(N // 2),), 0x55, dtype=torch.uint8, device=DEV)
+        y = ops.mul_mat_fused(w, x, swiglu=True, out_q8=q8)
+        return [y, q8]
+
+    got = run()
+    with ops.gemm_i8_ring():
+        ring = run()
+    torch.cuda.synchronize()
+    for a, b in zip(got, ring):
+        assert torch.equal(a, b)
+    if mode == "plain":
+        rng = np.random.default_rng(N)
+        sel = np.unique(np.concatenate([rng.choice(N, size=256, replace=False), [0, N - 1]]))
+        want = O.mul_mat(w.data.cpu().numpy()[sel], qtype, K, x.cpu().numpy())
+        assert mar(got[0].cpu().numpy()[:, sel], want) < 1e-5
+
+
 @pytest.mark.parametrize("qtype,K,N", [(O.Q8_0, 1536, 2048), (O.Q4_0, 4096, 4096)])
 @pytest.mark.parametrize("M", [1, 3, 4])
 def test_int8_path_for_few_rows_matches_rows_of_a_batch(qtype, K, N, M):
