@@ -64,30 +64,37 @@ enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_GLU = 2, EPI_GLU_Q8 = 3 };
 // used: one memory round trip per wave instead of one per step, the registers of the
 // per-step activation ring going to the weights. Same operations in the same order as the
 // ring, so the same bits.
-template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0>
-__global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ W, int64_t N, int64_t K,
-                                                    int64_t row_bytes, const uint8_t* __restrict__ act, int64_t M,
-                                                    float* __restrict__ dst, int64_t ldd,
-                                                    const float* __restrict__ bias, I8Epi epi) {
+// KG = 2 (with NSW): workgroups of 8 waves keep the 4 tiles and give each tile's K range to
+// 2 waves, whose sums are added in part order through LDS (the bits of a 2-part split):
+// two waves per SIMD where a quant block's 4 tiles would otherwise leave one.
+template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0, int KG = 1>
+__global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __restrict__ W, int64_t N, int64_t K,
+                                                              int64_t row_bytes, const uint8_t* __restrict__ act,
+                                                              int64_t M, float* __restrict__ dst, int64_t ldd,
+                                                              const float* __restrict__ bias, I8Epi epi) {
     static_assert(NSW == 0 || KS == 1, "the whole-tile request takes one K part");
     static_assert(EPI != EPI_GLU_Q8 || KS == 1, "the quantized SWIGLU rows need 4 whole tiles per workgroup");
+    static_assert(KG == 1 || (NSW > 0 && ORD == 1), "8-wave workgroups only on the whole-tile path");
+    constexpr int NW = 4 * KG;          // waves per workgroup
+    constexpr int PARTS = KS * KG;      // waves per tile (K parts)
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
     constexpr int RB = NBS * BB;           // bytes of a row per step: 272 / 144
     constexpr int CPR = RB / 16;           // 16-byte chunks of a row per step: 17 / 9
     constexpr int CPW = 16 * CPR;          // chunks of a wave's step: 272 / 144
     constexpr int LPL = (CPW + 63) / 64;   // chunk loads per lane per step: 5 / 3
-    __shared__ __align__(16) uint8_t s_stage[4][16 * RB];
-    __shared__ float s_red[KS > 1 ? 4 : 1][64][4];
+    __shared__ __align__(16) uint8_t s_stage[NW][16 * RB];
+    __shared__ float s_red[PARTS > 1 ? NW : 1][64][4];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int g = lane >> 4, lr = lane & 15;
-    const int64_t tile = (int64_t)blockIdx.x * (4 / KS) + wave / KS;
-    const int kp = wave % KS;
+    const int tw = wave / PARTS;  // tile of the workgroup
+    const int64_t tile = (int64_t)blockIdx.x * (4 / KS) + tw;
+    const int kp = wave % PARTS;
     const int64_t n0 = tile * 16;
     const int nb = (int)(K / QK);
     const int nsteps = nb / NBS;
-    const int sp = (nsteps + KS - 1) / KS;
+    const int sp = (nsteps + PARTS - 1) / PARTS;
     const int s0 = min(nsteps, kp * sp), s1 = min(nsteps, s0 + sp);
 
     // the tile's rows of W (rows past N, or a whole tile past N, read 0 without a fetch);
@@ -234,18 +241,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
         extern __shared__ __align__(16) uint8_t s_act[];
         const int abytes = nb * (QT == GQ_TYPE_Q4_0 ? 640 : 576);
         const __amdgpu_buffer_rsrc_t ars = rsrc(act, abytes);
-        u32x4 av[GEMM_I8_WHOLE_AC];
+        constexpr int AC = GEMM_I8_WHOLE_AC / KG;  // pieces per thread
+        u32x4 av[AC];
 #pragma unroll
-        for (int i = 0; i < GEMM_I8_WHOLE_AC; ++i)
-            av[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, ((int)threadIdx.x + 256 * i) * 16, 0, 0);
+        for (int i = 0; i < AC; ++i)
+            av[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, ((int)threadIdx.x + 256 * KG * i) * 16, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         uint4 wr[NSW][LPL];
 #pragma unroll
         for (int j = 0; j < NSW; ++j) issue_into(s0 + j, wr[j]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < GEMM_I8_WHOLE_AC; ++i)
-            *reinterpret_cast<u32x4*>(s_act + ((int)threadIdx.x + 256 * i) * 16) = av[i];
+        for (int i = 0; i < AC; ++i)
+            *reinterpret_cast<u32x4*>(s_act + ((int)threadIdx.x + 256 * KG * i) * 16) = av[i];
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < NSW; ++j) {
@@ -294,13 +302,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
         }
     }
 
-    if constexpr (KS > 1) {
+    // the tile's K parts added in part order in its first wave; with the quantized SWIGLU
+    // rows the other waves stay for the epilogue's barriers
+    const bool first = kp == 0;
+    if constexpr (PARTS > 1) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) s_red[wave][lane][r] = acc[r];
         __syncthreads();
-        if (kp != 0) return;
+        if (EPI != EPI_GLU_Q8 && !first) return;
 #pragma unroll
-        for (int k = 1; k < KS; ++k)
+        for (int k = 1; k < PARTS; ++k)
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] += s_red[wave + k][lane][r];
     }
@@ -343,7 +354,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
             float u[2];
 #pragma unroll
             for (int p = 0; p < 2; ++p) u[p] = swiglu_f(v[p], vp[p]);
-            if (dst && m < M && n0 < N) {
+            if (first && dst && m < M && n0 < N) {
 #pragma unroll
                 for (int p = 0; p < 2; ++p) dst[m * ldd + (n0 >> 1) + 2 * g + p] = u[p];
             }
@@ -357,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
                 float a = fmaxf(fabsf(u[0]), fabsf(u[1]));
                 a = fmaxf(a, __shfl_xor(a, 16, 64));
                 a = fmaxf(a, __shfl_xor(a, 32, 64));
-                if (g == 0) s_amax[wave][lr] = a;
+                if (first && g == 0) s_amax[tw][lr] = a;
                 __syncthreads();
                 float amax = s_amax[0][lr];
 #pragma unroll
@@ -373,14 +384,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
                 int is = q[0] + q[1];
                 is += __shfl_xor(is, 16, 64);
                 is += __shfl_xor(is, 32, 64);
-                if (g == 0) s_isum[wave][lr] = is;
+                if (first && g == 0) s_isum[tw][lr] = is;
                 __syncthreads();
-                if (m >= M || n0 >= N) return;
+                if (!first || m >= M || n0 >= N) return;
                 const int64_t nbq = N / 64;  // blocks of the quantized rows (K = N / 2)
                 const int64_t e = (int64_t)blockIdx.x * 16 + m;  // (block, activation row)
-                *reinterpret_cast<uint16_t*>(epi.q8 + e * 32 + 8 * wave + 2 * g) =
+                *reinterpret_cast<uint16_t*>(epi.q8 + e * 32 + 8 * tw + 2 * g) =
                     (uint16_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8));
-                if (wave == 0 && g == 0) {
+                if (tw == 0 && g == 0) {
                     int isum = s_isum[0][lr];
 #pragma unroll
                     for (int w = 1; w < 4; ++w) isum += s_isum[w][lr];
@@ -398,12 +409,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(const uint8_t* __restrict__ 
 constexpr int WHOLE_STEPS = 6;
 static_assert(GEMM_I8_WHOLE_AC * 4096 >= WHOLE_STEPS * NBS * 640, "the LDS copy covers the activation bytes");
 
-template <int QT, int EPI, int ORD>
+template <int QT, int EPI, int ORD, int KG = 1>
 int launch_whole(const dim3& g, const uint8_t* W, int64_t N, int64_t K, int64_t row_bytes, const uint8_t* act,
                  int64_t M, float* dst, int64_t ldd, hipStream_t s, const float* bias, const I8Epi& e) {
     const size_t lds = (size_t)GEMM_I8_WHOLE_AC * 4096;  // every thread's pieces, data or not
-    hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, ORD, WHOLE_STEPS>), g, dim3(256), lds, s, W, N, K, row_bytes, act, M,
-                       dst, ldd, bias, e);
+    hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, ORD, WHOLE_STEPS / KG, KG>), g, dim3(256 * KG), lds, s, W, N, K,
+                       row_bytes, act, M, dst, ldd, bias, e);
     return check_hip(hipGetLastError(), "gemm_i8 launch");
 }
 
@@ -418,7 +429,8 @@ int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64
         const dim3 g((unsigned)(N / 64));
         if (whole) {
             if (p.ks == 4) return launch_whole<QT, EPI, 4>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
-            if (p.ks == 2) return launch_whole<QT, EPI, 2>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+            // the 2-part split as 8-wave workgroups (two waves per tile)
+            if (p.ks == 2) return launch_whole<QT, EPI, 1, 2>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
             return launch_whole<QT, EPI, 1>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
         }
         if (p.ks == 4)
