@@ -89,6 +89,11 @@ def parse():
     p.add_argument("--attn-stamps", action="store_true",
                    help="with --attn-probe: run the same launches through libgqbench's timestamped build of "
                         "the attention and print the per-wave event times")
+    p.add_argument("--i8-probe", action="store_true",
+                   help="only measure the configs[4] gate|up product on the int8 path (M = 16, K = 1536, SWIGLU "
+                        "and the quantized rows): launch time against the row count (workgroups per CU), "
+                        "per-wave event times from libgqbench's timestamped build, and a streaming read of "
+                        "14 MiB against its workgroup count")
     p.add_argument("--gemm-probe", action="store_true",
                    help="only launch one ubatch's 128 prefill GEMMs (M = 512) eagerly, 3 times (the workload of "
                         "the rocprofv3 --pmc MFMA counter runs)")
@@ -153,6 +158,9 @@ def main() -> int:
         return attn_probe(dev, args.attn_stamps)
     if args.c3_only:
         print(json.dumps({"smollm2_c3": bench_c3(dev, args.pp_reps)}), flush=True)
+        return 0
+    if args.i8_probe:
+        print(json.dumps({"i8_probe": i8_probe(dev)}), flush=True)
         return 0
     cfg = LLAMA_7B
 
@@ -910,6 +918,140 @@ def attn_probe(dev, stamps: bool) -> int:
     summary["bits_equal_to_libgq"] = bool(torch.equal(stamped, ref))
     print(json.dumps({"attn_stamps": summary}), flush=True)
     return 0
+
+
+I8_EVENTS = ["wave start", "activation and weight loads issued", "activation in LDS",
+             "first weight step arrived", "steps accumulated", "K parts added", "quantized rows' barrier passed",
+             "end"]
+
+
+def i8_probe(dev) -> dict:
+    """The configs[4] gate|up product on the int8 path (16 rows, K = 1536, Q8_0, SWIGLU and
+    the down projection's quantized rows; one workgroup of 8 waves per 64 weight rows):
+    * launch time against N (graphs of 64 launches over weight copies totalling >= 600 MB),
+      at and around 256 workgroups (one per CU) and the configs' 17920 rows (280);
+    * per-wave event times (µs from the launch's first wave start; s_memrealtime at 100 MHz)
+      of 16 cold launches through libgqbench's timestamped build (same source and launch
+      plan), second of two rounds, at N = 17920 and 16384, with a bit check against libgq;
+    * a streaming read of 14 MiB (the configs[4] down weights) against its workgroup count,
+      256 threads each, over 32 buffers."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from ggmlc_amd import ops
+
+    K, M = 1536, 16
+    gen = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn((M, K), generator=gen, device=dev)
+    out = {"shape": "gate|up N x 1536 (Q8_0), 16 rows, SWIGLU + quantized rows", "launch_us": {}, "timeline": {},
+           "read_14MiB": {}}
+    for N in (8192, 12288, 16384, 16448, 17920, 20480, 32768, 49152):
+        copies = max(2, int(600e6 // (N * K * 34 // 32)))
+        wts = [ops.quantize_weights(torch.randn((N, K), generator=gen, device=dev) * 0.02, ops.Q8_0)
+               for _ in range(copies)]
+        q8 = torch.empty((ops.q8_rows_bytes(N // 2),), dtype=torch.uint8, device=dev)
+        y = torch.empty((M, N // 2), device=dev)
+
+        def loop():
+            for i in range(64):
+                ops.mul_mat_fused(wts[i % copies], x, out=y, swiglu=True, out_q8=q8)
+
+        us = time_graph(loop, 5) / 64 * 1e3
+        mb = N * K * 34 / 32 / 1e6
+        out["launch_us"][str(N)] = {"workgroups": N // 64, "us": round(us, 2), "MB": round(mb, 1),
+                                    "TBps": round(mb / us, 2)}
+        log(f"  gate|up N={N}: {N // 64} workgroups, {us:.2f} us, {mb / us:.2f} TB/s")
+        del wts
+        torch.cuda.empty_cache()
+
+    lib = _probe_lib()
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.gqbench_gemm_i8_glu_stamped.restype = ctypes.c_int
+    lib.gqbench_gemm_i8_glu_stamped.argtypes = [ctypes.c_int, vp, i64, i64, vp, i64, vp, i64, vp, vp]
+    lib.gqbench_gemm_stamp_slots.restype = ctypes.c_int
+    lib.gqbench_gemm_stamps_take.restype = ctypes.c_int
+    lib.gqbench_gemm_stamps_take.argtypes = [vp]
+    lib.gqbench_gemm_last_error.restype = ctypes.c_char_p
+    lib.gqbench_stream_read_grid.restype = ctypes.c_int
+    lib.gqbench_stream_read_grid.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, vp, vp]
+    host = np.zeros(lib.gqbench_gemm_stamp_slots(), dtype=np.uint64)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def take():
+        if lib.gqbench_gemm_stamps_take(host.ctypes.data) != 0:
+            raise RuntimeError(lib.gqbench_gemm_last_error().decode())
+        return host.copy()
+
+    # the activation in act_prep_i8's layout for K = 1536: the quantized SWIGLU rows of a
+    # 3072-row product
+    w0 = ops.quantize_weights(torch.randn((2 * K, 256), generator=gen, device=dev) * 0.05, ops.Q8_0)
+    act = torch.empty((ops.q8_rows_bytes(K),), dtype=torch.uint8, device=dev)
+    ops.mul_mat_fused(w0, torch.randn((M, 256), generator=gen, device=dev), swiglu=True, out_q8=act, no_out=True)
+    copies = 16
+    for N in (17920, 16384):
+        wts = [ops.quantize_weights(torch.randn((N, K), generator=gen, device=dev) * 0.02, ops.Q8_0)
+               for _ in range(copies)]
+        q8 = torch.empty((ops.q8_rows_bytes(N // 2),), dtype=torch.uint8, device=dev)
+        y = torch.empty((M, N // 2), device=dev)
+        take()
+        runs = []
+        for r in range(2):
+            for i in range(copies):
+                rc = lib.gqbench_gemm_i8_glu_stamped(ops.Q8_0, wts[i].data.data_ptr(), N, K, act.data_ptr(), M,
+                                                     y.data_ptr(), N // 2, q8.data_ptr(), stream)
+                if rc != 0:
+                    raise RuntimeError(lib.gqbench_gemm_last_error().decode())
+                torch.cuda.synchronize()
+                st = take()
+                if r == 1:
+                    runs.append(st.reshape(-1, 8))
+        q8r = torch.empty_like(q8)
+        yr = ops.mul_mat_fused(wts[-1], torch.zeros((M, K), device=dev), swiglu=True, out_q8=q8r, x_q8=act)
+        torch.cuda.synchronize()
+        per = {e: [] for e in range(8)}
+        spans, nw = [], []
+        for st in runs:
+            live = st[st[:, 0] != 0].astype(np.int64)
+            nw.append(len(live))
+            t0 = live[:, 0].min()
+            spans.append((live[:, 7].max() - t0) / 100.0)
+            for e in range(8):
+                v = live[:, e]
+                per[e].extend(((v[v != 0] - t0) / 100.0).tolist())
+        tl = {"workgroups": N // 64, "waves": int(np.median(nw)), "launch_span_us_median": round(float(np.median(spans)), 2),
+              "bits_equal_to_libgq": bool(torch.equal(y, yr) and torch.equal(q8, q8r)), "events_us": {}}
+        for e, name in enumerate(I8_EVENTS):
+            v = np.asarray(per[e])
+            if v.size:
+                tl["events_us"][name] = {f"p{p}": round(float(np.percentile(v, p)), 2) for p in (0, 10, 50, 90, 100)}
+        out["timeline"][str(N)] = tl
+        log(f"  gate|up N={N} timeline: span {tl['launch_span_us_median']} us, bits {tl['bits_equal_to_libgq']}")
+        del wts
+        torch.cuda.empty_cache()
+
+    nbytes, nbuf = 14 << 20, 32
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for grid in (96, 128, 192, 256, 384, 512, 1024, 2048):
+        best = float("inf")
+        for _ in range(5):
+            e0, e1 = _ev(), _ev()
+            e0.record()
+            for b in bufs:
+                rc = lib.gqbench_stream_read_grid(b.data_ptr(), nbytes, grid, sink.data_ptr(), stream)
+                if rc != 0:
+                    raise RuntimeError(f"stream read probe: HIP error {rc}")
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / nbuf)
+        out["read_14MiB"][str(grid)] = {"us": round(best, 2), "TBps": round(nbytes / best / 1e6, 2),
+                                        "GBps_per_workgroup": round(nbytes / best / 1e3 / grid, 1)}
+        log(f"  read 14 MiB with {grid} workgroups: {best:.2f} us")
+    del bufs
+    torch.cuda.empty_cache()
+    return out
 
 
 def gemm_probe(w, dev) -> int:

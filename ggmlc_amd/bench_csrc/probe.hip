@@ -29,15 +29,21 @@ __global__ __launch_bounds__(256) void k_read_probe(const uint4* __restrict__ p,
 
 }  // namespace
 
-// Reads `bytes` (16-byte aligned) of p once; sink: a device uint32 that is (practically)
-// never written. Returns 0, or a HIP error code.
+// Reads `bytes` (16-byte aligned) of p once with `grid` workgroups of 256 threads; sink: a
+// device uint32 that is (practically) never written. Returns 0, or a HIP error code.
+extern "C" int gqbench_stream_read_grid(const void* p, size_t bytes, int grid, uint32_t* sink, hipStream_t s) {
+    if (grid < 1) return (int)hipErrorInvalidValue;
+    const int64_t n16 = (int64_t)(bytes / 16);
+    hipLaunchKernelGGL(k_read_probe, dim3((unsigned)grid), dim3(256), 0, s, reinterpret_cast<const uint4*>(p), n16,
+                       sink);
+    return (int)hipGetLastError();
+}
+
+// The same with 8 workgroups per CU (the grid of the bandwidth calibration)
 extern "C" int gqbench_stream_read(const void* p, size_t bytes, uint32_t* sink, hipStream_t s) {
     int dev = 0, ncu = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return (int)e;
-    const int64_t n16 = (int64_t)(bytes / 16);
-    hipLaunchKernelGGL(k_read_probe, dim3((unsigned)(ncu * 8)), dim3(256), 0, s, reinterpret_cast<const uint4*>(p),
-                       n16, sink);
-    return (int)hipGetLastError();
+    return gqbench_stream_read_grid(p, bytes, ncu * 8, sink, s);
 }

@@ -41,6 +41,49 @@ constexpr int NBS = 8;  // quant blocks per step
 constexpr int GEMM_I8_WHOLE_AC = 8;  // 16-byte pieces per thread of the LDS activation copy (32 KiB)
 constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any resource: reads 0, no fetch
 
+// Per-wave s_memrealtime stamps of the quantized-SWIGLU launches, compiled only into the
+// benchmark's measurement library (GQ_GEMM_STAMPS; libgq has none of this): event e of
+// wave w of workgroup x at g_gemm_stamps[(x * 8 + w) * 8 + e]. Events: 0 start, 1 loads
+// issued, 2 activation in LDS, 3 first weight step arrived, 4 steps accumulated, 5 K parts
+// added, 6 quantized rows written, 7 end.
+#ifdef GQ_GEMM_STAMPS
+constexpr int GSTAMP_SLOTS = 2048 * 8 * 8;
+__device__ unsigned long long g_gemm_stamps[GSTAMP_SLOTS];
+#define GQ_GSTAMP_DECL unsigned long long stamp_[8] = {}
+#define GQ_GSTAMP(e)                                          \
+    do {                                                      \
+        __builtin_amdgcn_sched_barrier(0);                    \
+        stamp_[e] = __builtin_amdgcn_s_memrealtime();         \
+        __builtin_amdgcn_sched_barrier(0);                    \
+    } while (0)
+#define GQ_GSTAMP_AFTER(e, x)                                                          \
+    do {                                                                               \
+        unsigned long long t_;                                                         \
+        asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t_) : "v"(x)); \
+        stamp_[e] = t_;                                                                \
+    } while (0)
+#define GQ_GSTAMP_FLUSH()                                                                  \
+    do {                                                                                   \
+        GQ_GSTAMP(7);                                                                      \
+        const size_t i_ = ((size_t)blockIdx.x * 8 + (threadIdx.x >> 6)) * 8;               \
+        if ((threadIdx.x & 63) == 0 && i_ + 8 <= (size_t)GSTAMP_SLOTS)                     \
+            for (int e_ = 0; e_ < 8; ++e_) g_gemm_stamps[i_ + e_] = stamp_[e_];            \
+    } while (0)
+#else
+#define GQ_GSTAMP_DECL \
+    do {               \
+    } while (0)
+#define GQ_GSTAMP(e) \
+    do {             \
+    } while (0)
+#define GQ_GSTAMP_AFTER(e, x) \
+    do {                      \
+    } while (0)
+#define GQ_GSTAMP_FLUSH() \
+    do {                  \
+    } while (0)
+#endif
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
     const uint64_t base = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
@@ -85,6 +128,8 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
     __shared__ __align__(16) uint8_t s_stage[NW][16 * RB];
     __shared__ float s_red[PARTS > 1 ? NW : 1][64][4];
 
+    GQ_GSTAMP_DECL;
+    GQ_GSTAMP(0);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int g = lane >> 4, lr = lane & 15;
@@ -251,10 +296,13 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
 #pragma unroll
         for (int j = 0; j < NSW; ++j) issue_into(s0 + j, wr[j]);
         __builtin_amdgcn_sched_barrier(0);
+        GQ_GSTAMP(1);
 #pragma unroll
         for (int i = 0; i < AC; ++i)
             *reinterpret_cast<u32x4*>(s_act + ((int)threadIdx.x + 256 * KG * i) * 16) = av[i];
         __syncthreads();
+        GQ_GSTAMP(2);
+        GQ_GSTAMP_AFTER(3, wr[0][0].x);
 #pragma unroll
         for (int j = 0; j < NSW; ++j) {
             const int s = s0 + j;
@@ -269,6 +317,7 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
             });
             wave_lds_sync();  // the slice is read before the next step parks
         }
+        GQ_GSTAMP_AFTER(4, acc[0]);
     } else {
         issue_w(s0, 0);
         issue_a(s0, 0);
@@ -315,6 +364,7 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[r] += s_red[wave + k][lane][r];
     }
+    GQ_GSTAMP_AFTER(5, acc[0]);
     const int64_t m = lr;  // activation row
     if constexpr (EPI == EPI_PLAIN) {
         if (m >= M) return;
@@ -386,7 +436,11 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
                 is += __shfl_xor(is, 32, 64);
                 if (first && g == 0) s_isum[tw][lr] = is;
                 __syncthreads();
-                if (!first || m >= M || n0 >= N) return;
+                GQ_GSTAMP(6);
+                if (!first || m >= M || n0 >= N) {
+                    GQ_GSTAMP_FLUSH();
+                    return;
+                }
                 const int64_t nbq = N / 64;  // blocks of the quantized rows (K = N / 2)
                 const int64_t e = (int64_t)blockIdx.x * 16 + m;  // (block, activation row)
                 *reinterpret_cast<uint16_t*>(epi.q8 + e * 32 + 8 * tw + 2 * g) =
@@ -398,6 +452,7 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
                     *reinterpret_cast<float*>(epi.q8 + nbq * 512 + e * 4) = h2f(f2h(d));
                     *reinterpret_cast<int*>(epi.q8 + nbq * 576 + e * 4) = isum;
                 }
+                GQ_GSTAMP_FLUSH();
             }
         }
     }
