@@ -44,8 +44,9 @@ constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any resource: reads
 // Per-wave s_memrealtime stamps of the quantized-SWIGLU launches, compiled only into the
 // benchmark's measurement library (GQ_GEMM_STAMPS; libgq has none of this): event e of
 // wave w of workgroup x at g_gemm_stamps[(x * 8 + w) * 8 + e]. Events: 0 start, 1 loads
-// issued, 2 activation in LDS, 3 first weight step arrived, 4 steps accumulated, 5 K parts
-// added, 6 quantized rows written, 7 end.
+// issued, 2 activation in LDS, 3 first weight step arrived, 4 steps accumulated (1-4 on the
+// whole-tile path only), 5 K parts added, 6 the quantized rows' barrier passed, 7 end (0: not
+// reached).
 #ifdef GQ_GEMM_STAMPS
 constexpr int GSTAMP_SLOTS = 2048 * 8 * 8;
 __device__ unsigned long long g_gemm_stamps[GSTAMP_SLOTS];
