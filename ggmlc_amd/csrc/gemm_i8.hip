@@ -111,14 +111,21 @@ enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_GLU = 2, EPI_GLU_Q8 = 3 };
 // KG = 2 (with NSW): workgroups of 8 waves keep the 4 tiles and give each tile's K range to
 // 2 waves, whose sums are added in part order through LDS (the bits of a 2-part split):
 // two waves per SIMD where a quant block's 4 tiles would otherwise leave one.
-template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0, int KG = 1>
+// LMH > 0 (ring launches, M <= LMH): the activation rows [0, LMH) of every block are copied
+// into dynamic LDS once per workgroup (LAC 16-byte pieces per thread), and the steps take
+// their activation operands from there instead of loading them per wave and step (where
+// every lane group loads its row's scale and block sum again); the weight ring is unchanged.
+// Same operations in the same order, so the same bits.
+template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0, int KG = 1, int LMH = 0, int LAC = 0>
 __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                               int64_t row_bytes, const uint8_t* __restrict__ act,
                                                               int64_t M, float* __restrict__ dst, int64_t ldd,
                                                               const float* __restrict__ bias, I8Epi epi) {
-    static_assert(NSW == 0 || KS == 1, "the whole-tile request takes one K part");
+    static_assert(NSW == 0 || KS == 1 || LMH > 0, "the whole-tile request of a K part takes the compact copy");
     static_assert(EPI != EPI_GLU_Q8 || KS == 1, "the quantized SWIGLU rows need 4 whole tiles per workgroup");
     static_assert(KG == 1 || (NSW > 0 && ORD == 1), "8-wave workgroups only on the whole-tile path");
+    static_assert(LMH == 0 || (KG == 1 && ORD == 1 && (LMH == 8 || LMH == 16) && LAC > 0),
+                  "the compact activation copy is for 4-wave launches");
     constexpr int NW = 4 * KG;          // waves per workgroup
     constexpr int PARTS = KS * KG;      // waves per tile (K parts)
     constexpr int BB = QT == GQ_TYPE_Q8_0 ? Q8_BYTES : Q4_BYTES;
@@ -276,31 +283,65 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
         }
     };
 
-    if constexpr (NSW > 0) {
-        // the activation's bytes into LDS (its loads first, so waiting for them leaves the
-        // weight loads in flight), then every weight step of the wave, then the steps in
-        // order as their loads return
-        // Every thread copies AC pieces of 16 bytes whether or not they hold data (pieces
-        // past the bytes read 0 from the resource and land in the buffer's slack, which
-        // the launch sizes to AC * 4096 bytes): a conditional copy lets the compiler sink
-        // the load into the branch, behind the weight loads.
-        extern __shared__ __align__(16) uint8_t s_act[];
-        const int abytes = nb * (QT == GQ_TYPE_Q4_0 ? 640 : 576);
-        const __amdgpu_buffer_rsrc_t ars = rsrc(act, abytes);
-        constexpr int AC = GEMM_I8_WHOLE_AC / KG;  // pieces per thread
-        u32x4 av[AC];
+    // The activation copy into dynamic LDS (whole-tile and staged launches): every thread
+    // copies CP pieces of 16 bytes whether or not they hold data (pieces past the data read
+    // 0 from the resource and land in the buffer's slack, which the launch sizes to
+    // CP * 4096 * KG bytes), since a conditional copy lets the compiler sink a load into
+    // the branch, behind the weight loads. Its loads go out before the weight loads and its
+    // stores after them, so waiting for the copy leaves the weights in flight.
+    // LMH == 0: the workspace bytes as they are (16 rows per block); LMH > 0: the compact
+    // copy of rows [0, LMH): quants [nb][LMH][32], scales [nb][LMH] f32, block sums
+    // [nb][LMH] i32 (Q4_0), piece q at byte 16 q.
+    extern __shared__ __align__(16) uint8_t s_act[];
+    constexpr int CP = NSW == 0 && LMH == 0 ? 1 : (LMH ? LAC : GEMM_I8_WHOLE_AC / KG);  // pieces per thread
+    constexpr int RH = LMH ? LMH : 16;  // activation rows held per block
+    auto copy_issue = [&](u32x4(&av)[CP]) {
+        constexpr int QP = RH * 2;  // pieces of a block's quants
+        constexpr int SP = RH / 4;  // pieces of a block's scales, and of its block sums
+        constexpr int PPB = QP + SP * (QT == GQ_TYPE_Q4_0 ? 2 : 1);
+        const int nq = nb * QP, ns = nb * SP;
+        const __amdgpu_buffer_rsrc_t ars = rsrc(act, (int64_t)nb * (QT == GQ_TYPE_Q4_0 ? 640 : 576));
 #pragma unroll
-        for (int i = 0; i < AC; ++i)
-            av[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, ((int)threadIdx.x + 256 * KG * i) * 16, 0, 0);
+        for (int i = 0; i < CP; ++i) {
+            const int q = (int)threadIdx.x + 256 * KG * i;
+            uint32_t off = (uint32_t)q * 16;
+            if constexpr (LMH > 0) {
+                if (q < nq) off = (uint32_t)((q / QP) * 512 + (q % QP) * 16);
+                else if (q < nq + ns) off = (uint32_t)(nb * 512 + ((q - nq) / SP) * 64 + ((q - nq) % SP) * 16);
+                else off = (uint32_t)(nb * 576 + ((q - nq - ns) / SP) * 64 + ((q - nq - ns) % SP) * 16);
+                if (q >= nb * PPB) off = OOB;
+            }
+            av[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, (int)off, 0, 0);
+        }
+    };
+    auto copy_store = [&](const u32x4(&av)[CP]) {
+#pragma unroll
+        for (int i = 0; i < CP; ++i)
+            *reinterpret_cast<u32x4*>(s_act + ((int)threadIdx.x + 256 * KG * i) * 16) = av[i];
+    };
+    const int lra = RH == 16 ? lr : (lr & (RH - 1));  // rows past RH (past M) read row lr - RH
+    // step s's activation operands from the copy
+    auto lds_blocks = [&](int s) {
+        blocks(s, [&](int b, u32x2& xq, float& dx, int& sa) {
+            const int e = (s * NBS + b) * RH + lra;  // (block, activation row)
+            xq = *reinterpret_cast<const u32x2*>(s_act + e * 32 + 8 * g);
+            dx = *reinterpret_cast<const float*>(s_act + nb * RH * 32 + e * 4);
+            sa = QT == GQ_TYPE_Q8_0 ? 0 : *reinterpret_cast<const int*>(s_act + nb * RH * 36 + e * 4);
+        });
+    };
+
+    if constexpr (NSW > 0) {
+        // the activation into LDS, every weight step of the wave, then the steps in order
+        // as their loads return
+        u32x4 av[CP];
+        copy_issue(av);
         __builtin_amdgcn_sched_barrier(0);
         uint4 wr[NSW][LPL];
 #pragma unroll
         for (int j = 0; j < NSW; ++j) issue_into(s0 + j, wr[j]);
         __builtin_amdgcn_sched_barrier(0);
         GQ_GSTAMP(1);
-#pragma unroll
-        for (int i = 0; i < AC; ++i)
-            *reinterpret_cast<u32x4*>(s_act + ((int)threadIdx.x + 256 * KG * i) * 16) = av[i];
+        copy_store(av);
         __syncthreads();
         GQ_GSTAMP(2);
         GQ_GSTAMP_AFTER(3, wr[0][0].x);
@@ -310,15 +351,32 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
             if (s >= s1) break;  // uniform
             fold(s);
             park(wr[j]);
-            blocks(s, [&](int b, u32x2& xq, float& dx, int& sa) {
-                const int e = (s * NBS + b) * 16 + lr;  // (block, activation row)
-                xq = *reinterpret_cast<const u32x2*>(s_act + e * 32 + 8 * g);
-                dx = *reinterpret_cast<const float*>(s_act + nb * 512 + e * 4);
-                sa = QT == GQ_TYPE_Q8_0 ? 0 : *reinterpret_cast<const int*>(s_act + nb * 576 + e * 4);
-            });
+            lds_blocks(s);
             wave_lds_sync();  // the slice is read before the next step parks
         }
         GQ_GSTAMP_AFTER(4, acc[0]);
+    } else if constexpr (LMH > 0) {
+        // the activation into LDS, then the two-step weight ring
+        u32x4 av[CP];
+        copy_issue(av);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_w(s0, 0);
+        issue_w(s0 + 1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        copy_store(av);
+        __syncthreads();
+        auto body_l = [&](int s, int slot) {
+            park(wb[slot]);
+            issue_w(s + 2, slot);
+            lds_blocks(s);
+            wave_lds_sync();  // the slice is read before the next step parks
+        };
+        int s = s0;
+        for (; s + 1 < s1; s += 2) {
+            body_l(s, 0);
+            body_l(s + 1, 1);
+        }
+        if (s < s1) body_l(s, 0);
     } else {
         issue_w(s0, 0);
         issue_a(s0, 0);
@@ -474,6 +532,20 @@ int launch_whole(const dim3& g, const uint8_t* W, int64_t N, int64_t K, int64_t 
     return check_hip(hipGetLastError(), "gemm_i8 launch");
 }
 
+// Ring launches of up to 8 rows with 2 or 4 tiles per workgroup and the activation staged
+// in LDS (LMH = 8): LAC = 10 pieces of 16 bytes per thread hold the compact copy of K <= 4096
+// (20 pieces per block for Q4_0, 18 for Q8_0: 40 KB). Measured at M = 8 (configs[1], Q4_0):
+// gate_up 22016 x 4096 (2 K parts) 26.0 -> 21.7 us. One-tile workgroups (4 K parts) re-read
+// nothing within the workgroup and were slower staged (Qwen2.5-1.5B o at M = 8: 5.4 -> 5.8 us;
+// down, K = 8960, with a 112 KB copy: 11.7 -> 12.4 us).
+template <int QT, int KS, int LAC>
+int launch_lact(const dim3& g, const uint8_t* W, int64_t N, int64_t K, int64_t row_bytes, const uint8_t* act,
+                int64_t M, float* dst, int64_t ldd, hipStream_t s, const float* bias, const I8Epi& e) {
+    hipLaunchKernelGGL((k_gemm_i8<QT, KS, EPI_PLAIN, 1, 0, 1, 8, LAC>), g, dim3(256), (size_t)LAC * 4096, s, W, N, K,
+                       row_bytes, act, M, dst, ldd, bias, e);
+    return check_hip(hipGetLastError(), "gemm_i8 launch");
+}
+
 template <int QT, int EPI>
 int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst, int64_t ldd,
                hipStream_t s, const float* bias, const I8Epi& e) {
@@ -502,6 +574,12 @@ int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64
     }
     const dim3 grid((unsigned)p.wgs);
     if (p.ks == 1 && whole) return launch_whole<QT, EPI, 1>(grid, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+    if constexpr (EPI == EPI_PLAIN) {
+        if (M <= 8 && p.ks <= 2 && (K / QK) * (QT == GQ_TYPE_Q4_0 ? 20 : 18) <= 10 * 256 && !option_gemm_i8_ring()) {
+            if (p.ks == 2) return launch_lact<QT, 2, 10>(grid, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+            return launch_lact<QT, 1, 10>(grid, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
+        }
+    }
     if (p.ks == 4)
         hipLaunchKernelGGL((k_gemm_i8<QT, 4, EPI == EPI_GLU_Q8 ? EPI_GLU : EPI>), grid, dim3(256), 0, s, W, N, K,
                            row_bytes, act, M, dst, ldd, bias, e);

@@ -130,8 +130,9 @@ class separate_attn_merge:
 
 
 class gemm_i8_ring:
-    """Context manager: the int8 path streams every product's weights through its per-step
-    ring (gq_set_option GQ_OPT_GEMM_I8_RING) inside the block; same bits, for comparisons."""
+    """Context manager: the int8 path streams every product's weights and activation through
+    its per-step ring (gq_set_option GQ_OPT_GEMM_I8_RING) inside the block, with no whole-tile
+    requests or LDS-staged activations; same bits, for comparisons."""
 
     def __enter__(self):
         check(_lib.load().gq_set_option(_lib.GQ_OPT_GEMM_I8_RING, 1))

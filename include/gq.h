@@ -75,8 +75,9 @@ int gq_init(void);
  *   GQ_OPT_ATTN_SEPARATE_MERGE (0 default / 1): decode attention merges its KV
  *   splits in a second launch instead of inside the decode kernel.
  *   GQ_OPT_GEMM_I8_RING (0 default / 1): the int8 path for 1..16 rows streams every
- *   product's weights through its per-step register ring, also where a wave would
- *   otherwise request its whole tile at once with the activation staged in LDS. */
+ *   product's weights and activation through its per-step register ring, also where a
+ *   wave would otherwise request its whole tile at once, or take its activation from a
+ *   copy staged in LDS once per workgroup. */
 enum gq_option {
     GQ_OPT_ATTN_SEPARATE_MERGE = 1,
     GQ_OPT_GEMM_I8_RING = 2,

@@ -366,3 +366,60 @@ def test_plan_of_the_configs():
     assert plan(1536, 8960) == (4, 4, 96)        # down
     assert plan(151936, 1536) == (1, 4, 2374)    # tied head
     assert plan(4096, 11008) == (4, 4, 256)      # 7B down
+
+
+def staged_copy(qt, K, lac=10, lmh=8):
+    """k_gemm_i8's compact activation copy (LMH rows of every block, LAC pieces per thread):
+    per piece q of the 256 threads, the workspace offset it loads (None: OOB) and the LDS
+    byte it stores to."""
+    nb = K // QK
+    qp, sp = lmh * 2, lmh // 4
+    ppb = qp + sp * (2 if qt == 2 else 1)
+    nq, ns = nb * qp, nb * sp
+    out = []
+    for i in range(lac):
+        for t in range(256):
+            q = t + 256 * i
+            if q < nq:
+                off = (q // qp) * 512 + (q % qp) * 16
+            elif q < nq + ns:
+                off = nb * 512 + ((q - nq) // sp) * 64 + ((q - nq) % sp) * 16
+            else:
+                off = nb * 576 + ((q - nq - ns) // sp) * 64 + ((q - nq - ns) % sp) * 16
+            out.append((None if q >= nb * ppb else off, q * 16))
+    return out
+
+
+@pytest.mark.parametrize("qt,K", [(2, 4096), (8, 4096), (2, 256), (8, 3840), (2, 2048)])
+def test_staged_activation_copy_and_reads(qt, K):
+    """The copy stays inside the workspace's bytes and the LDS buffer, and every operand the
+    steps read from it (quants, scale, block sum of (block, row) for rows < 8; rows 8..15 read
+    row - 8) is the byte the per-step loads take from the workspace."""
+    nb = K // QK
+    lac, lmh = 10, 8
+    abytes = nb * (640 if qt == 2 else 576)
+    rng = np.random.default_rng(K + qt)
+    ws = rng.integers(0, 256, size=nb * 640, dtype=np.uint8)
+    lds = np.zeros(lac * 4096, dtype=np.uint8)
+    for off, dst in staged_copy(qt, K, lac, lmh):
+        assert dst + 16 <= lds.size
+        if off is None:
+            continue  # reads 0 (out of the resource), lands in the slack
+        assert 0 <= off and off + 16 <= abytes
+        lds[dst:dst + 16] = ws[off:off + 16]
+    assert nb * lmh * (40 if qt == 2 else 36) <= lds.size
+    lane = np.arange(64)
+    g, lr = lane >> 4, lane & 15
+    lra = lr & (lmh - 1)
+    for s in range(nb // NBS):
+        for b in range(NBS):
+            e = (s * NBS + b) * lmh + lra          # compact (block, row)
+            ef = (s * NBS + b) * 16 + lra          # the workspace's (block, row)
+            for j in range(8):
+                assert np.array_equal(lds[e * 32 + 8 * g + j], ws[ef * 32 + 8 * g + j])
+            for j in range(4):
+                assert np.array_equal(lds[nb * lmh * 32 + e * 4 + j], ws[nb * 512 + ef * 4 + j])
+                if qt == 2:
+                    assert np.array_equal(lds[nb * lmh * 36 + e * 4 + j], ws[nb * 576 + ef * 4 + j])
+            assert (e * 32 + 8 * g + 8 <= nb * lmh * 32).all()
+            assert (nb * lmh * 36 + e * 4 + 4 <= nb * lmh * 40).all()

@@ -490,6 +490,33 @@ def test_gemm_i8_whole_tile_bits(qtype, N, M, mode):
         assert mar(got[0].cpu().numpy()[:, sel], want) < 1e-5
 
 
+@pytest.mark.parametrize("qtype,K,N,M", [
+    (O.Q4_0, 4096, 22016, 8),   # configs[1] gate_up at M = 8: 2 K parts, 2 tiles per workgroup
+    (O.Q8_0, 4096, 16384, 7),   # Q8_0, 2 K parts
+    (O.Q8_0, 2048, 65536, 6),   # one K part, 4 tiles per workgroup
+    (O.Q4_0, 256, 70, 8),       # one step, a partial last tile
+    (O.Q4_0, 4096, 8200, 3),    # 3 rows (int8 forced), rows past N in the last workgroup
+    (O.Q8_0, 3840, 9000, 8),    # 15 steps: parts of 8 and 7
+])
+def test_gemm_i8_staged_activation_bits(qtype, K, N, M):
+    """Up to 8 rows on the int8 ring with 2 or 4 tiles per workgroup: the activation copied
+    into LDS once per workgroup gives the bits of the per-step activation loads
+    (GQ_OPT_GEMM_I8_RING), and stays within 1e-5 of the oracle."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M + 3)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV)
+    got = ops.mul_mat_fused(w, x, int8=True)
+    with ops.gemm_i8_ring():
+        ring = ops.mul_mat_fused(w, x, int8=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), ring.view(torch.int32))
+    rng = np.random.default_rng(N + K)
+    sel = np.unique(np.concatenate([rng.choice(N, size=min(N, 192), replace=False), [0, N - 1]]))
+    want = O.mul_mat(w.data.cpu().numpy()[sel], qtype, K, x.cpu().numpy())
+    assert mar(got.cpu().numpy()[:, sel], want) < 1e-5
+
+
 @pytest.mark.parametrize("qtype,K,N", [(O.Q8_0, 1536, 2048), (O.Q4_0, 4096, 4096)])
 @pytest.mark.parametrize("M", [1, 3, 4])
 def test_int8_path_for_few_rows_matches_rows_of_a_batch(qtype, K, N, M):
