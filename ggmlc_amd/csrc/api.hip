@@ -714,6 +714,7 @@ int gq_rope_kv_store(const gq_tensor* q, const gq_tensor* k, const gq_tensor* v,
         return fail(GQ_ERR_INVALID, "rope_kv_store: pos must be I32 [>= s], kv_idx I64 [s]");
     if (mode != 0 && mode != 2) return fail(GQ_ERR_UNSUPPORTED, "rope_kv_store: modes 0 (normal) and 2 (neox) only");
     if (n_dims <= 0 || n_dims % 2 || n_dims > hd) return fail(GQ_ERR_INVALID, "rope_kv_store: bad n_dims");
+    if ((Hq + Hkv) * hd > 0x7fffffffLL) return fail(GQ_ERR_UNSUPPORTED, "rope_kv_store: (Hq + Hkv) * hd past int32");
     RopeKvArgs a{};
     a.q = static_cast<const float*>(q->data), a.qnb1 = (int64_t)q->nb[1], a.qnb2 = (int64_t)q->nb[2];
     a.k = static_cast<const float*>(k->data), a.knb1 = (int64_t)k->nb[1], a.knb2 = (int64_t)k->nb[2];

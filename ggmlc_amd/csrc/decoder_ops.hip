@@ -111,40 +111,58 @@ __global__ __launch_bounds__(256) void k_rope_kv(RopeKvArgs a) {
     const int64_t row = a.idx[i];
     const bool bad = row < 0 || row >= a.rows;
     if (bad && threadIdx.x == 0 && a.n_bad) atomicAdd(a.n_bad, (int)(2 * a.Hkv));
-    // rotated pairs: q heads, then (valid row) k heads
-    const int64_t nq = a.Hq * half, nk = bad ? 0 : a.Hkv * half;
-    for (int64_t e = threadIdx.x; e < nq + nk; e += blockDim.x) {
-        const bool isq = e < nq;
-        const int64_t ee = isq ? e : e - nq;
-        const int64_t h = ee / half;
-        const int j = (int)(ee - h * half);
-        const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
-        const float2 cs = s_cs[j];
-        float y0, y1;
-        if (isq) {
-            const float* xr = reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1));
-            float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1);
-            rope_rotate(cs.x, cs.y, xr[i0], xr[i1], y0, y1);
-            yr[i0] = y0;
-            yr[i1] = y1;
-        } else {
-            const float* xr = reinterpret_cast<const float*>(at(a.k, i * a.knb2 + h * a.knb1));
-            uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + h * a.kcnb2);
-            rope_rotate(cs.x, cs.y, xr[i0], xr[i1], y0, y1);
-            yr[i0] = f2h(y0);
-            yr[i1] = f2h(y1);
+    // rotated pairs: q heads, then (valid row) k heads. Each thread loads RU pairs before it
+    // stores any (the loop otherwise waits for every pair's loads in turn).
+    constexpr int RU = 4;
+    const int nq = (int)a.Hq * half, nk = bad ? 0 : (int)a.Hkv * half;
+    for (int e0 = (int)threadIdx.x; e0 < nq + nk; e0 += (int)blockDim.x * RU) {
+        float x0[RU], x1[RU];
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            x0[u] = x1[u] = 0.0f;
+            if (e >= nq + nk) continue;
+            const bool isq = e < nq;
+            const int ee = isq ? e : e - nq;
+            const int h = ee / half, j = ee - h * half;
+            const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
+            const float* xr = isq ? reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1))
+                                  : reinterpret_cast<const float*>(at(a.k, i * a.knb2 + h * a.knb1));
+            x0[u] = xr[i0];
+            x1[u] = xr[i1];
+        }
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            if (e >= nq + nk) continue;
+            const bool isq = e < nq;
+            const int ee = isq ? e : e - nq;
+            const int h = ee / half, j = ee - h * half;
+            const int i0 = a.neox ? j : 2 * j, i1 = a.neox ? j + half : 2 * j + 1;
+            const float2 cs = s_cs[j];
+            float y0, y1;
+            rope_rotate(cs.x, cs.y, x0[u], x1[u], y0, y1);
+            if (isq) {
+                float* yr = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1);
+                yr[i0] = y0;
+                yr[i1] = y1;
+            } else {
+                uint16_t* yr = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + h * a.kcnb2);
+                yr[i0] = f2h(y0);
+                yr[i1] = f2h(y1);
+            }
         }
     }
     // dims past n_dims pass through (q fp32, k fp16)
-    const int64_t tail = a.hd - a.n_dims;
+    const int tail = (int)a.hd - a.n_dims;
     if (tail > 0) {
-        for (int64_t e = threadIdx.x; e < (a.Hq + (bad ? 0 : a.Hkv)) * tail; e += blockDim.x) {
-            const int64_t h = e / tail, d = a.n_dims + (e - h * tail);
+        for (int e = (int)threadIdx.x; e < (int)(a.Hq + (bad ? 0 : a.Hkv)) * tail; e += (int)blockDim.x) {
+            const int h = e / tail, d = a.n_dims + (e - h * tail);
             if (h < a.Hq) {
                 const float* xr = reinterpret_cast<const float*>(at(a.q, i * a.qnb2 + h * a.qnb1));
                 reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(a.qo) + i * a.qonb2 + h * a.qonb1)[d] = xr[d];
             } else {
-                const int64_t kh = h - a.Hq;
+                const int kh = h - (int)a.Hq;
                 const float* xr = reinterpret_cast<const float*>(at(a.k, i * a.knb2 + kh * a.knb1));
                 reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.kc) + row * a.kcnb1 + kh * a.kcnb2)[d] =
                     f2h(xr[d]);
@@ -152,10 +170,25 @@ __global__ __launch_bounds__(256) void k_rope_kv(RopeKvArgs a) {
         }
     }
     if (bad) return;
-    for (int64_t e = threadIdx.x; e < a.Hkv * a.hd; e += blockDim.x) {
-        const int64_t h = e / a.hd, d = e - h * a.hd;
-        const float* xr = reinterpret_cast<const float*>(at(a.v, i * a.vnb2 + h * a.vnb1));
-        reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.vc) + row * a.vcnb1 + h * a.vcnb2)[d] = f2h(xr[d]);
+    const int hd = (int)a.hd, nv = (int)a.Hkv * hd;
+    constexpr int VU = 8;
+    for (int e0 = (int)threadIdx.x; e0 < nv; e0 += (int)blockDim.x * VU) {
+        float xv[VU];
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            xv[u] = 0.0f;
+            if (e >= nv) continue;
+            const int h = e / hd, d = e - h * hd;
+            xv[u] = reinterpret_cast<const float*>(at(a.v, i * a.vnb2 + h * a.vnb1))[d];
+        }
+#pragma unroll
+        for (int u = 0; u < VU; ++u) {
+            const int e = e0 + u * (int)blockDim.x;
+            if (e >= nv) continue;
+            const int h = e / hd, d = e - h * hd;
+            reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(a.vc) + row * a.vcnb1 + h * a.vcnb2)[d] = f2h(xv[u]);
+        }
     }
 }
 
