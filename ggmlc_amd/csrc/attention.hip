@@ -561,7 +561,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 // Prefill attention on the matrix cores (v_mfma_f32_16x16x32_f16), no ALiBi / softcap.
-// A workgroup owns 64 query vectors of one kv head (4 waves x 16), walks the KV range
+// A workgroup owns 16 WQ query vectors of one kv head (WQ waves x 16), walks the KV range
 // in blocks of 64 keys staged in LDS (K as [key][dim], V transposed to [dim][key]),
 // and keeps an online softmax per query in registers:
 //   S^T (16 keys x 16 queries tiles) = K_blk . Q^T, with Q = q_hi + q_lo split into two
@@ -573,8 +573,9 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 // S^T accumulator of lane l therefore holds query j and keys 16t + 4g + r; used as the
 // B operand of the PV product (K = 32 keys of tiles t0, t1) its 8 values are keys
 // (4g..4g+3, 16+4g..16+4g+3), and the V^T operand is read in that same key order.
-template <int D>
-__global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int q_f16) {
+template <int D, int WQ = 4>
+__global__ __launch_bounds__(64 * WQ) void k_attn_mma(AttnArgs a, int G, int NQ, int q_f16) {
+    static_assert(WQ == 2 || WQ == 4, "2 or 4 waves of 16 query vectors");
     constexpr int BKV = 64;
     constexpr int LDK = D + 8;      // halves per K row in LDS
     constexpr int LDV = BKV + 8;    // halves per V^T row in LDS
@@ -582,12 +583,12 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
     constexpr int DT = D / 16;      // 16-dim tiles of O^T
     __shared__ __align__(16) _Float16 sK[BKV * LDK];
     __shared__ __align__(16) _Float16 sVT[D * LDV];
-    __shared__ int s_vote[2][4];
+    __shared__ int s_vote[2][WQ];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
     const int hk = blockIdx.y;
-    const int qv = blockIdx.x * 64 + wave * 16 + j;  // this lane's query vector
+    const int qv = blockIdx.x * (16 * WQ) + wave * 16 + j;  // this lane's query vector
     const bool qok = qv < NQ;
     const int64_t h = (int64_t)hk * G + (qok ? qv % G : 0);
     const int64_t qi = qok ? qv / G : 0;             // its query row (mask row, output row)
@@ -625,7 +626,7 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
     const __amdgpu_buffer_rsrc_t krs = rsrc(a.k, a.knb2, a.knb1), vrs = rsrc(a.v, a.vnb2, a.vnb1);
     // staging: the block's 64 rows x D halves of K and of V in 16-byte pieces
     constexpr int PPR = D / 8;                 // pieces per row
-    constexpr int NPC = BKV * PPR / 256;       // pieces per thread per matrix (2 or 4)
+    constexpr int NPC = BKV * PPR / (64 * WQ);  // pieces per thread per matrix (2 to 8)
     // thread -> piece column pc of NPC consecutive keys (each wave instruction reads
     // 4 or 8 whole rows), so V is transposed with one NPC-key write per dim
     const int ppc = tid % PPR, pr0 = NPC * (tid / PPR);
@@ -649,7 +650,10 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
 #pragma unroll
             for (int u = 0; u < NPC; ++u) hv[u] = (vreg[u][e >> 1] >> (16 * (e & 1))) & 0xffffu;
             _Float16* dst = &sVT[(ppc * 8 + e) * LDV + pr0];
-            if constexpr (NPC == 4) {
+            if constexpr (NPC == 8) {
+                *reinterpret_cast<uint4*>(dst) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
+                                                            hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+            } else if constexpr (NPC == 4) {
                 *reinterpret_cast<uint2*>(dst) = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
             } else {
                 *reinterpret_cast<uint32_t*>(dst) = hv[0] | (hv[1] << 16);
@@ -720,9 +724,15 @@ __global__ __launch_bounds__(256) void k_attn_mma(AttnArgs a, int G, int NQ, int
         // barrier: the previous block's LDS is fully read; and the skip decision (wave
         // votes in a slot per block parity: the next write to a slot follows a barrier
         // every wave passes only after reading it)
-        if (lane == 0) s_vote[bi & 1][wave] = __any(need) ? 1 : 0;
+        // (the vote is taken by every lane before the branch: inside it, only lane 0 would
+        // vote, and the block would be skipped when lane 0 alone does not need it)
+        const int wneed = __any(need) ? 1 : 0;
+        if (lane == 0) s_vote[bi & 1][wave] = wneed;
         __syncthreads();
-        const bool run = (s_vote[bi & 1][0] | s_vote[bi & 1][1] | s_vote[bi & 1][2] | s_vote[bi & 1][3]) != 0;
+        int vote = 0;
+#pragma unroll
+        for (int w = 0; w < WQ; ++w) vote |= s_vote[bi & 1][w];
+        const bool run = vote != 0;
         if (run) {
             park();
             __syncthreads();
@@ -1554,6 +1564,17 @@ int attention(const AttnArgs& a, void* ws, size_t ws_bytes, hipStream_t s) {
 #undef GQ_DEC_U
 #undef GQ_DEC
     } else if (mma_ok(a)) {
+        // tiles of 32 query vectors where tiles of 64 leave more than half the CUs idle
+        // (Qwen2.5-1.5B shape at 512 tokens, 12 / 2 heads: 96 -> 192 workgroups, 34.1 ->
+        // 29.6 us; the 7B's 256 workgroups of 64 are faster than 512 of 32: 37.3 / 40.7 us)
+        if (cdiv(p.NQ, 64) * a.Hkv < 128) {
+            const dim3 gm((unsigned)cdiv(p.NQ, 32), (unsigned)a.Hkv);
+            if (a.D == 128)
+                hipLaunchKernelGGL((k_attn_mma<128, 2>), gm, dim3(128), 0, s, b, (int)p.G, (int)p.NQ, q_f16);
+            else
+                hipLaunchKernelGGL((k_attn_mma<64, 2>), gm, dim3(128), 0, s, b, (int)p.G, (int)p.NQ, q_f16);
+            return check_hip(hipGetLastError(), "flash_attn_ext (mfma) launch");
+        }
         const dim3 gm((unsigned)cdiv(p.NQ, 64), (unsigned)a.Hkv);
         if (a.D == 128)
             hipLaunchKernelGGL(k_attn_mma<128>, gm, dim3(256), 0, s, b, (int)p.G, (int)p.NQ, q_f16);

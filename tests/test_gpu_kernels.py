@@ -677,6 +677,28 @@ def test_flash_attn_banded_mask_prefill(D, G, masked):
     assert r < 1e-3
 
 
+@pytest.mark.parametrize("D,G", [(128, 1), (64, 1), (128, 6)])
+def test_flash_attn_prefill_block_skip_sees_every_lane(D, G):
+    """The prefill kernel skips a KV block only when no query of its tile needs it: here
+    every query sees the first three blocks, and in the last block only one key of one
+    query row (never the first query of a wave, nor the keys the first lane of a wave
+    reads) is unmasked, so a vote that looked at one lane per wave would drop it."""
+    rng = np.random.default_rng(D * 7 + G)
+    Hkv, S, n_kv = 2, 64, 256
+    Hq = Hkv * G
+    q = rng.standard_normal((Hq, S, D)).astype(np.float32)
+    kc = f16(rng.standard_normal((Hkv, n_kv, D)))
+    vc = f16(rng.standard_normal((Hkv, n_kv, D)))
+    mask = np.full((S, n_kv), 0xF800, dtype=np.uint16)  # -32768
+    mask[:, :192] = 0
+    mask[5, 200] = 0  # row 5: key 8 of the last block (lanes with g = 2 read it)
+    got = _attn_dev(q, kc, vc, n_kv, mask)
+    exact = O.flash_attn_ext_f16(q, kc, vc, n_kv, mask, mode=1)
+    r = mar(got, exact)
+    print(f"D={D} G={G}: vs exact {r:.2e}")
+    assert r < 1e-3
+
+
 @pytest.mark.parametrize("Hq,Hkv,D,S,pos,ctx", [
     (32, 32, 128, 1, 1100, 2048),   # 7B decode: 8 splits of 160 rows per kv head
     (12, 2, 128, 3, 4000, 4352),    # GQA 6 x 3 rows: 8 query vectors, many splits
