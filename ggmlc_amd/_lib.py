@@ -88,6 +88,8 @@ class gq_mul_mat_fusion(ctypes.Structure):
         ("out_q8", ctypes.c_void_p),
         ("b_q8", ctypes.c_void_p),
         ("int8", ctypes.c_int32),
+        ("out_halves", ctypes.c_int32),
+        ("b_add_halves", ctypes.c_int32),
     ]
 
 
@@ -126,6 +128,7 @@ SIGNATURES = {
     "gq_kv_step_inputs": (ctypes.c_int, [_vp, _i64, _vp, _vp, _P, _vp]),
     "gq_kv_advance": (ctypes.c_int, [_vp, _i64, _vp]),
     "gq_mul_mat_fused_workspace_size": (ctypes.c_size_t, [_P, _P, ctypes.POINTER(gq_mul_mat_fusion)]),
+    "gq_mul_mat_fused_halves": (ctypes.c_int, [_P, _P, ctypes.POINTER(gq_mul_mat_fusion)]),
     "gq_flash_attn_paged_workspace_size": (ctypes.c_size_t, [_P, _P, _i64, _i64]),
     "gq_flash_attn_paged": (ctypes.c_int, [_P, _P, _P, _P, _P, _i64, _i64, _f32, _P, _vp, ctypes.c_size_t, _vp]),
     "gq_flash_attn_paged_q8": (ctypes.c_int, [_P, _P, _P, _P, _P, _i64, _i64, _f32, _P, _vp, _vp, ctypes.c_size_t,

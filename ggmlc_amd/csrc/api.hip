@@ -267,6 +267,19 @@ static int fused_bias(const gq_mul_mat_fusion* f, const MulMatPlan& p, const flo
     return GQ_OK;
 }
 
+// a pair of slabs [ne0, M, 2, 1] for b's M rows (b 2-d): slab h at data + h * nb[2], rows
+// at nb[1] within a slab, the slabs apart; *slab = nb[2] in floats
+static int halves_slabs(const gq_tensor* t, int64_t ne0, const gq_tensor* b, const char* what, int64_t* slab) {
+    if (!t || t->type != GQ_TYPE_F32 || !t->data || t->ne[0] != ne0 || t->ne[1] != b->ne[1] || t->ne[2] != 2 ||
+        t->ne[3] != 1 || b->ne[2] != 1 || b->ne[3] != 1 || t->nb[0] != 4 || t->nb[1] % 4 != 0 ||
+        t->nb[2] % 4 != 0 || t->nb[2] < t->nb[1] * (size_t)t->ne[1] || t->nb[1] < (size_t)ne0 * 4)
+        return fail(GQ_ERR_INVALID, std::string("mul_mat_fused: ") + what + " halves must be F32 [" +
+                                        std::to_string(ne0) + ", M, 2, 1] of disjoint slabs (b 2-d): " +
+                                        (t ? shape(t) : std::string("NULL")));
+    *slab = (int64_t)(t->nb[2] / 4);
+    return GQ_OK;
+}
+
 // b as the product's input: with b_swiglu its rows hold 2K values and the input is
 // SWIGLU of their halves, so the plan sees the first half; int8 takes the int8 path for
 // 1..16 rows (also 1..4, where the GEMV is the default)
@@ -294,6 +307,15 @@ static int fused_plan(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_f
 }
 
 size_t gq_q8_rows_bytes(int64_t K) { return K > 0 && K % QK == 0 ? gemm_i8_act_bytes(K) : 0; }
+
+int gq_mul_mat_fused_halves(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f) {
+    MulMatPlan p;
+    if (int rc = fused_plan(a, b, f, p)) return rc;
+    if (p.use_gemv || !p.use_i8 || (reinterpret_cast<uintptr_t>(a->data) & 15) != 0 || f->swiglu || f->rope_kv ||
+        f->add)
+        return 0;
+    return !f->bias && gemm_i8_halves(p.N, p.K) ? 1 : 0;
+}
 
 size_t gq_mul_mat_fused_workspace_size(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f) {
     MulMatPlan p;
@@ -341,7 +363,12 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
     }
     const int64_t n_out = f->swiglu ? p.N / 2 : p.N;
     const bool no_dst = f->rope_kv || (f->out_q8 && !dst);
-    if (!no_dst && (!dst || dst->type != GQ_TYPE_F32 || dst->ne[0] != n_out || dst->ne[1] != b->ne[1] ||
+    if (f->out_halves) {
+        if (!i8 || f->swiglu || f->rope_kv || bias || !gemm_i8_halves(p.N, p.K))
+            return fail(GQ_ERR_INVALID, "mul_mat_fused: out_halves where the int8 path does not take K in halves "
+                                        "(gq_mul_mat_fused_halves)");
+        if (int rc = halves_slabs(dst, p.N, b, "dst", &epi.slab)) return rc;
+    } else if (!no_dst && (!dst || dst->type != GQ_TYPE_F32 || dst->ne[0] != n_out || dst->ne[1] != b->ne[1] ||
                     dst->ne[2] != b->ne[2] || dst->ne[3] != b->ne[3] || dst->nb[0] != 4 || dst->nb[1] % 4 != 0 ||
                     !rows_uniform(dst)))
         return fail(GQ_ERR_INVALID, "mul_mat_fused: dst must be F32 [" + std::to_string(n_out) + ", M, ...]: " +
@@ -352,9 +379,14 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
                f->rms_norm ? 1 : 0, f->b_swiglu ? 1 : 0, f->rms_eps};
     if (f->b_add) {
         const gq_tensor* r = f->b_add;
-        if (r->type != GQ_TYPE_F32 || r->ne[0] != p.K || r->ne[1] != b->ne[1] || r->ne[2] != b->ne[2] ||
-            r->ne[3] != b->ne[3] || r->nb[0] != 4 || r->nb[1] % 4 != 0 || !rows_uniform(r))
+        if (f->b_add_halves) {
+            int64_t slab = 0;
+            if (int rc = halves_slabs(r, p.K, b, "b_add", &slab)) return rc;
+            ap.d2 = static_cast<const float*>(r->data) + slab;
+        } else if (r->type != GQ_TYPE_F32 || r->ne[0] != p.K || r->ne[1] != b->ne[1] || r->ne[2] != b->ne[2] ||
+                   r->ne[3] != b->ne[3] || r->nb[0] != 4 || r->nb[1] % 4 != 0 || !rows_uniform(r)) {
             return fail(GQ_ERR_INVALID, "mul_mat_fused: b_add must be F32 shaped like b: " + shape(r));
+        }
         ap.d = static_cast<const float*>(r->data);
         ap.ds = (int64_t)(r->nb[1] / 4);
         if (f->b_sum) {
@@ -362,13 +394,13 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
             if (o->type != GQ_TYPE_F32 || o->ne[0] != p.K || o->ne[1] != b->ne[1] || o->ne[2] != b->ne[2] ||
                 o->ne[3] != b->ne[3] || o->nb[0] != 4 || o->nb[1] % 4 != 0 || !rows_uniform(o))
                 return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum must be F32 shaped like b: " + shape(o));
-            if (o->data == b->data || o->data == r->data)
+            if (o->data == b->data || o->data == r->data || (ap.d2 && o->data == ap.d2))
                 return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum must not alias b or b_add");
             ap.sum = static_cast<float*>(o->data);
             ap.ss = (int64_t)(o->nb[1] / 4);
         }
-    } else if (f->b_sum) {
-        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum needs b_add");
+    } else if (f->b_sum || f->b_add_halves) {
+        return fail(GQ_ERR_INVALID, "mul_mat_fused: b_sum and b_add_halves need b_add");
     }
     if (p.M == 0) return GQ_OK;
     if (i8) {
@@ -384,7 +416,7 @@ static int mul_mat_fused_gemm(const gq_tensor* a, const gq_tensor* b, gq_tensor*
             act = w;
         }
         return gemm_i8(a->type, static_cast<const uint8_t*>(a->data), p.N, p.K, act, p.M, dp, ldd, s, bias,
-                       (epi.rope || epi.glu) ? &epi : nullptr);
+                       (epi.rope || epi.glu || epi.slab) ? &epi : nullptr);
     }
     if (!f->workspace || f->workspace_bytes < p.ws)
         return fail(GQ_ERR_WORKSPACE, "mul_mat_fused: workspace too small (need " + std::to_string(p.ws) + " bytes)");
@@ -413,8 +445,9 @@ int gq_mul_mat_fused(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, con
     if (rc) return rc;
     if (!p.use_gemv) return mul_mat_fused_gemm(a, b, dst, f, p, (hipStream_t)stream);
     if (f->b_swiglu) return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: b_swiglu needs M > 4 (use swiglu on the producer)");
-    if (f->out_q8 || f->b_q8)
-        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: out_q8 / b_q8 need the int8 path (5..16 rows)");
+    if (f->out_q8 || f->b_q8 || f->out_halves || f->b_add_halves)
+        return fail(GQ_ERR_UNSUPPORTED, "mul_mat_fused: out_q8 / b_q8 / out_halves / b_add_halves need M > 4 or "
+                                        "int8");
     GemvFuse fz;
     rc = fused_bias(f, p, &fz.bias);
     if (rc) return rc;

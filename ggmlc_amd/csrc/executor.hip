@@ -1281,7 +1281,7 @@ struct Executor {
         b.qkv = static_cast<float*>(dmalloc((size_t)n * nq() * 4));
         b.q = static_cast<float*>(dmalloc((size_t)n * qd() * 4));
         b.attn = static_cast<float*>(dmalloc((size_t)n * qd() * 4));
-        b.proj = static_cast<float*>(dmalloc((size_t)n * e * 4));
+        b.proj = static_cast<float*>(dmalloc((size_t)2 * n * e * 4));  // room for a product's two halves of K
         b.gu = static_cast<float*>(dmalloc((size_t)n * 2 * F * 4));
         b.act = static_cast<float*>(dmalloc((size_t)n * F * 4));
         b.logits = static_cast<float*>(dmalloc((size_t)n * m.n_vocab * 4));
@@ -1346,17 +1346,32 @@ struct Executor {
         if (f.swiglu) op += "+SWIGLU";
         if (f.out_q8) op += "+Q8_ROWS";
         if (w.bias) op += "+ADD(bias)";
+        if (f.out_halves) op += "(K halves)";
         count(op);
         ++mm_shapes[std::string(w.type == GQ_TYPE_Q8_0 ? "q8_0" : "q4_0") + " K=" + std::to_string(w.K) + " N=" +
                     std::to_string(w.N) + " M=" + std::to_string(rows) + (f.int8 ? " int8" : "")];
         gq_tensor a = w.d();
         gq_tensor b = desc(x, GQ_TYPE_F32, xK, rows);
-        gq_tensor d = desc(dst, GQ_TYPE_F32, dN, rows);
+        gq_tensor d = desc(dst, GQ_TYPE_F32, dN, rows, f.out_halves ? 2 : 1);
         gq_tensor bias = desc(w.bias, GQ_TYPE_F32, w.N);
         if (w.bias) f.bias = &bias;
         f.workspace = ws;
         f.workspace_bytes = ws_bytes;
         gq_ok(gq_mul_mat_fused(&a, &b, dst ? &d : nullptr, &f, stream));
+    }
+
+    // whether the int8 path takes the plain product w x in two halves of K, so that its
+    // output may stay two slabs for the next prologue's ADD (gq_mul_mat_fused_halves)
+    bool mm_halves(const QW& w, const float* x, int64_t xK, int64_t rows) {
+        gq_tensor a = w.d();
+        gq_tensor b = desc(x, GQ_TYPE_F32, xK, rows);
+        gq_tensor bias = desc(w.bias, GQ_TYPE_F32, w.N);
+        gq_mul_mat_fusion f{};
+        f.int8 = 1;
+        if (w.bias) f.bias = &bias;
+        const int rc = gq_mul_mat_fused_halves(&a, &b, &f);
+        gq_ok(rc < 0 ? rc : GQ_OK);
+        return rc == 1;
     }
 
     void forward(int64_t n, int64_t n_kv, int64_t r0) {
@@ -1509,17 +1524,18 @@ struct Executor {
         float* x = b.x;
         auto other = [&](float* p) { return p == b.x ? b.x_alt : b.x; };
         float* pending = nullptr;
+        bool pend_halves = false;  // pending holds a product's two halves of K (2 slabs of B rows)
         const float scale = 1.0f / std::sqrt((float)hd);
         for (size_t l = 0; l < layers.size(); ++l) {
             const Layer& L = layers[l];
             gq_tensor kpool = desc(kp(l), GQ_TYPE_F16, hd, rows, Hkv);
             gq_tensor vpool = desc(vp(l), GQ_TYPE_F16, hd, rows, Hkv);
-            gq_tensor pend = desc(pending, GQ_TYPE_F32, e, B);
+            gq_tensor pend = desc(pending, GQ_TYPE_F32, e, B, pend_halves ? 2 : 1);
             float* nx = pending ? other(x) : nullptr;
             gq_tensor nxt = desc(nx, GQ_TYPE_F32, e, B);
             gq_mul_mat_fusion f{};
             f.rms_norm = 1, f.rms_eps = m.rms_eps;
-            if (pending) f.b_add = &pend, f.b_sum = &nxt;
+            if (pending) f.b_add = &pend, f.b_sum = &nxt, f.b_add_halves = pend_halves ? 1 : 0;
             gq_tensor qo = desc(b.q, GQ_TYPE_F32, hd, Hq, B);
             if (fused || q8) {  // ADD + RMS_NORM + QKV (+ bias) + ROPE x2 + SET_ROWS x2
                 gq_rope_kv_epilogue ep{};
@@ -1555,21 +1571,27 @@ struct Executor {
                             std::to_string(Hkv) + " B=" + std::to_string(B) + " max_len=" + std::to_string(max_len)];
             }
             float* x2 = other(x);
-            gq_tensor o_t = desc(b.proj, GQ_TYPE_F32, e, B);
+            // int8 path: o and down in two halves of K where it splits them (narrow products),
+            // their slabs added by the next prologue's ADD
+            const bool o_halves = q8 && mm_halves(L.o, b.attn, QD, B);
+            gq_tensor o_t = desc(b.proj, GQ_TYPE_F32, e, B, o_halves ? 2 : 1);
             gq_tensor x2_t = desc(x2, GQ_TYPE_F32, e, B);
             {
                 gq_mul_mat_fusion fo{};
-                if (q8) fo.b_q8 = b.q8_o, fo.int8 = 1;
+                if (q8) fo.b_q8 = b.q8_o, fo.int8 = 1, fo.out_halves = o_halves ? 1 : 0;
                 mm_fused(L.o, b.attn, QD, B, b.proj, e, fo);
             }
+            pend_halves = false;
             if (q8) {  // ADD + RMS_NORM + gate|up + SWIGLU writing down's quantized rows, then down
                 gq_mul_mat_fusion fg{};
                 fg.rms_norm = 1, fg.rms_eps = m.rms_eps, fg.swiglu = 1, fg.b_add = &o_t, fg.b_sum = &x2_t;
+                fg.b_add_halves = o_halves ? 1 : 0;
                 fg.out_q8 = b.q8_d, fg.int8 = 1;
                 mm_fused(L.gate_up, x, e, B, nullptr, F, fg);
                 x = x2;
+                pend_halves = mm_halves(L.down, b.act, F, B);
                 gq_mul_mat_fusion fd{};
-                fd.b_q8 = b.q8_d, fd.int8 = 1;
+                fd.b_q8 = b.q8_d, fd.int8 = 1, fd.out_halves = pend_halves ? 1 : 0;
                 mm_fused(L.down, b.act, F, B, b.proj, e, fd);
             } else if (fused) {
                 gq_mul_mat_fusion fg{};
@@ -1589,10 +1611,17 @@ struct Executor {
             }
             pending = b.proj;
         }
-        gq_tensor pend = desc(pending, GQ_TYPE_F32, e, B);
         gq_mul_mat_fusion fh{};
-        fh.rms_norm = 1, fh.rms_eps = m.rms_eps, fh.b_add = &pend;
+        fh.rms_norm = 1, fh.rms_eps = m.rms_eps;
         fh.int8 = q8 && lm_head.K % 256 == 0 && reinterpret_cast<uintptr_t>(lm_head.data) % 16 == 0 ? 1 : 0;
+        if (pend_halves && !fh.int8 && B <= 4) {  // the GEMV path adds one tensor: the halves' sum first
+            gq_tensor h0 = desc(pending, GQ_TYPE_F32, e, B), h1 = desc(pending + B * e, GQ_TYPE_F32, e, B);
+            gq_ok(gq_add(&h0, &h1, &h0, stream));
+            count("ADD");
+            pend_halves = false;
+        }
+        gq_tensor pend = desc(pending, GQ_TYPE_F32, e, B, pend_halves ? 2 : 1);
+        fh.b_add = &pend, fh.b_add_halves = pend_halves ? 1 : 0;
         mm_fused(lm_head, x, e, B, b.logits, m.n_vocab, fh);
         gq_ok(gq_paged_advance(pg.pos, nullptr, B, stream));
         count("PAGED_ADVANCE");

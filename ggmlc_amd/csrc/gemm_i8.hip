@@ -116,14 +116,29 @@ enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_GLU = 2, EPI_GLU_Q8 = 3 };
 // their activation operands from there instead of loading them per wave and step (where
 // every lane group loads its row's scale and block sum again); the weight ring is unchanged.
 // Same operations in the same order, so the same bits.
-template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0, int KG = 1, int LMH = 0, int LAC = 0>
+// SPL: K in two halves (the first ceil(steps / 2) steps, then the rest), each in 4 parts,
+// summed as (parts of half 0 in order) + (parts of half 1 in order), every epilogue of a
+// gemm_i8_halves product in that order so that fused and unfused chains agree:
+//   SPL = 1, KS = 4: one workgroup of 8 waves per tile (KG = 2) adds both halves;
+//   SPL = 1, KS = 1 (ORD = 8): one wave walks every step and folds the 8 parts' sums;
+//   SPL = 2 (EPI_PLAIN, KS = 4): two workgroups per tile (blockIdx.x & 1 = the half), each
+//   writing its half's sum as a slab of dst (half h at dst + h * epi.slab floats); the
+//   consumer adds slab 0 + slab 1, which gives the bits of SPL = 1. Narrow products on few
+//   workgroups (the configs[4] o and down: 96 row tiles) then stream over twice as many CUs.
+template <int QT, int KS, int EPI, int ORD = 1, int NSW = 0, int KG = 1, int LMH = 0, int LAC = 0, int SPL = 0>
 __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __restrict__ W, int64_t N, int64_t K,
                                                               int64_t row_bytes, const uint8_t* __restrict__ act,
                                                               int64_t M, float* __restrict__ dst, int64_t ldd,
                                                               const float* __restrict__ bias, I8Epi epi) {
     static_assert(NSW == 0 || KS == 1 || LMH > 0, "the whole-tile request of a K part takes the compact copy");
     static_assert(EPI != EPI_GLU_Q8 || KS == 1, "the quantized SWIGLU rows need 4 whole tiles per workgroup");
-    static_assert(KG == 1 || (NSW > 0 && ORD == 1), "8-wave workgroups only on the whole-tile path");
+    static_assert(KG == 1 || (NSW > 0 && ORD == 1) || (SPL == 1 && KS == 4),
+                  "8-wave workgroups on the whole-tile path or halves");
+    static_assert(SPL == 0 ||
+                      (KS == 4 && NSW == 0 && LMH == 0 && ORD == 1 && KG == (SPL == 1 ? 2 : 1) &&
+                       (SPL == 1 || EPI == EPI_PLAIN)) ||
+                      (KS == 1 && SPL == 1 && ORD == 8 && KG == 1 && LMH == 0),
+                  "halves: 4-part ring launches, or the 8-part fold of one-part launches");
     static_assert(LMH == 0 || (KG == 1 && ORD == 1 && (LMH == 8 || LMH == 16) && LAC > 0),
                   "the compact activation copy is for 4-wave launches");
     constexpr int NW = 4 * KG;          // waves per workgroup
@@ -142,13 +157,20 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int g = lane >> 4, lr = lane & 15;
     const int tw = wave / PARTS;  // tile of the workgroup
-    const int64_t tile = (int64_t)blockIdx.x * (4 / KS) + tw;
+    const int64_t tile = (int64_t)(SPL == 2 ? blockIdx.x >> 1 : blockIdx.x) * (4 / KS) + tw;
     const int kp = wave % PARTS;
     const int64_t n0 = tile * 16;
     const int nb = (int)(K / QK);
     const int nsteps = nb / NBS;
-    const int sp = (nsteps + PARTS - 1) / PARTS;
-    const int s0 = min(nsteps, kp * sp), s1 = min(nsteps, s0 + sp);
+    // the wave's steps [s0, s1): part kp of PARTS, or with halves over the waves (HW) part kh
+    // of KS of its half
+    constexpr bool HW = SPL != 0 && KS == 4;
+    const int half = SPL == 2 ? (int)(blockIdx.x & 1) : (HW ? kp / KS : 0);
+    const int kh = HW && SPL == 1 ? kp % KS : kp;
+    const int nhs = (nsteps + 1) / 2;  // steps of half 0
+    const int hbeg = half * nhs, hend = HW ? min(nsteps, hbeg + nhs) : nsteps;
+    const int sp = HW ? (nhs + KS - 1) / KS : (nsteps + PARTS - 1) / PARTS;
+    const int s0 = min(hend, hbeg + kh * sp), s1 = min(hend, s0 + sp);
 
     // the tile's rows of W (rows past N, or a whole tile past N, read 0 without a fetch);
     // paired epilogues: logical row n0 + r is physical row pair_row(n0 + r), the smallest
@@ -271,12 +293,18 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
     for (int k = 0; k < ORD; ++k)
 #pragma unroll
         for (int r = 0; r < 4; ++r) part[k][r] = 0.0f;
-    const int spo = (nsteps + ORD - 1) / ORD;  // steps per part of the emulated split
+    // first step of part k of the emulated split: k * spo, or with SPL the k % 4-th part of
+    // half k / 4 (parts may be empty, their starts then equal: the fold cascades in k order)
+    const int spo = SPL ? (nhs + 3) / 4 : (nsteps + ORD - 1) / ORD;
+    auto pstart = [&](int k) {
+        if constexpr (SPL != 0) return k < 4 ? min(nhs, k * spo) : min(nsteps, nhs + (k - 4) * spo);
+        return k * spo;
+    };
     auto fold = [&](int st) {  // entering step st: the previous part's sum is complete
         if constexpr (ORD > 1) {
 #pragma unroll
             for (int k = 1; k < ORD; ++k)
-                if (st == k * spo) {
+                if (st == pstart(k)) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) part[k - 1][r] = acc[r], acc[r] = 0.0f;
                 }
@@ -395,7 +423,10 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
         }
     }
     if constexpr (ORD > 1) {  // the last part's sum, then the parts in order (empty ones 0)
-        const int kl = (s1 - 1) / spo;
+        int kl = 0;  // the part of the last step
+#pragma unroll
+        for (int k = 1; k < ORD; ++k)
+            if (pstart(k) <= s1 - 1) kl = k;
 #pragma unroll
         for (int k = 0; k < ORD; ++k)
             if (k == kl) {
@@ -404,9 +435,16 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
             }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            acc[r] = part[0][r];
+            if constexpr (SPL != 0) {  // (half 0's parts in order) + (half 1's parts in order)
+                float a0 = part[0][r], a1 = part[4][r];
 #pragma unroll
-            for (int k = 1; k < ORD; ++k) acc[r] += part[k][r];
+                for (int k = 1; k < 4; ++k) a0 += part[k][r], a1 += part[4 + k][r];
+                acc[r] = a0 + a1;
+            } else {
+                acc[r] = part[0][r];
+#pragma unroll
+                for (int k = 1; k < ORD; ++k) acc[r] += part[k][r];
+            }
         }
     }
 
@@ -418,19 +456,35 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
         for (int r = 0; r < 4; ++r) s_red[wave][lane][r] = acc[r];
         __syncthreads();
         if (EPI != EPI_GLU_Q8 && !first) return;
+        if constexpr (HW && SPL == 1) {  // (half 0's parts in order) + (half 1's parts in order)
+            float a1[4];
 #pragma unroll
-        for (int k = 1; k < PARTS; ++k)
+            for (int r = 0; r < 4; ++r) a1[r] = s_red[wave + KS][lane][r];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += s_red[wave + k][lane][r];
+            for (int k = 1; k < KS; ++k)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    acc[r] += s_red[wave + k][lane][r];
+                    a1[r] += s_red[wave + KS + k][lane][r];
+                }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += a1[r];
+        } else {
+#pragma unroll
+            for (int k = 1; k < PARTS; ++k)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] += s_red[wave + k][lane][r];
+        }
     }
     GQ_GSTAMP_AFTER(5, acc[0]);
     const int64_t m = lr;  // activation row
     if constexpr (EPI == EPI_PLAIN) {
         if (m >= M) return;
+        float* const dh = SPL == 2 ? dst + half * epi.slab : dst;  // this half's slab
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t n = n0 + 4 * g + r;
-            if (n < N) dst[m * ldd + n] = bias ? acc[r] + bias[n] : acc[r];
+            if (n < N) dh[m * ldd + n] = bias ? acc[r] + bias[n] : acc[r];
         }
     } else {
         // the lane's two pairs: logical rows (row, row + 1), row = n0 + 4 g + 2 p; the bias is
@@ -523,12 +577,12 @@ __global__ __launch_bounds__(256 * KG, 2 / KG) void k_gemm_i8(const uint8_t* __r
 constexpr int WHOLE_STEPS = 6;
 static_assert(GEMM_I8_WHOLE_AC * 4096 >= WHOLE_STEPS * NBS * 640, "the LDS copy covers the activation bytes");
 
-template <int QT, int EPI, int ORD, int KG = 1>
+template <int QT, int EPI, int ORD, int KG = 1, int SPL = 0>
 int launch_whole(const dim3& g, const uint8_t* W, int64_t N, int64_t K, int64_t row_bytes, const uint8_t* act,
                  int64_t M, float* dst, int64_t ldd, hipStream_t s, const float* bias, const I8Epi& e) {
     const size_t lds = (size_t)GEMM_I8_WHOLE_AC * 4096;  // every thread's pieces, data or not
-    hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, ORD, WHOLE_STEPS / KG, KG>), g, dim3(256 * KG), lds, s, W, N, K,
-                       row_bytes, act, M, dst, ldd, bias, e);
+    hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, ORD, WHOLE_STEPS / KG, KG, 0, 0, SPL>), g, dim3(256 * KG), lds, s, W,
+                       N, K, row_bytes, act, M, dst, ldd, bias, e);
     return check_hip(hipGetLastError(), "gemm_i8 launch");
 }
 
@@ -555,13 +609,18 @@ int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64
     if constexpr (EPI == EPI_GLU_Q8) {  // one quant block (64 logical rows) per workgroup,
         // summed in the order of the plan's split (the bits of the unfused product)
         const dim3 g((unsigned)(N / 64));
+        const bool hv = gemm_i8_halves(N, K);  // the 8 parts of K's two halves
         if (whole) {
+            if (hv) return launch_whole<QT, EPI, 8, 1, 1>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
             if (p.ks == 4) return launch_whole<QT, EPI, 4>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
             // the 2-part split as 8-wave workgroups (two waves per tile)
             if (p.ks == 2) return launch_whole<QT, EPI, 1, 2>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
             return launch_whole<QT, EPI, 1>(g, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
         }
-        if (p.ks == 4)
+        if (hv)
+            hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, 8, 0, 1, 0, 0, 1>), g, dim3(256), 0, s, W, N, K, row_bytes, act,
+                               M, dst, ldd, bias, e);
+        else if (p.ks == 4)
             hipLaunchKernelGGL((k_gemm_i8<QT, 1, EPI, 4>), g, dim3(256), 0, s, W, N, K, row_bytes, act, M, dst, ldd,
                                bias, e);
         else if (p.ks == 2)
@@ -580,6 +639,15 @@ int launch_epi(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64
             return launch_lact<QT, 1, 10>(grid, W, N, K, row_bytes, act, M, dst, ldd, s, bias, e);
         }
     }
+    if (gemm_i8_halves(N, K)) {
+        if (EPI == EPI_PLAIN && e.slab)  // two workgroups per tile, one per half, each writing its own slab
+            hipLaunchKernelGGL((k_gemm_i8<QT, 4, EPI_PLAIN, 1, 0, 1, 0, 0, 2>), dim3((unsigned)(2 * p.wgs)), dim3(256),
+                               0, s, W, N, K, row_bytes, act, M, dst, ldd, bias, e);
+        else  // both halves in one 8-wave workgroup per tile: their sum in the same order, then the epilogue
+            hipLaunchKernelGGL((k_gemm_i8<QT, 4, EPI == EPI_GLU_Q8 ? EPI_GLU : EPI, 1, 0, 2, 0, 0, 1>), grid, dim3(512),
+                               0, s, W, N, K, row_bytes, act, M, dst, ldd, bias, e);
+        return check_hip(hipGetLastError(), "gemm_i8 launch");
+    }
     if (p.ks == 4)
         hipLaunchKernelGGL((k_gemm_i8<QT, 4, EPI == EPI_GLU_Q8 ? EPI_GLU : EPI>), grid, dim3(256), 0, s, W, N, K,
                            row_bytes, act, M, dst, ldd, bias, e);
@@ -596,7 +664,7 @@ template <int QT>
 int launch(const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst, int64_t ldd,
            hipStream_t s, const float* bias, const I8Epi* e) {
     const I8Epi none{};
-    if (!e || (!e->rope && !e->glu)) return launch_epi<QT, EPI_PLAIN>(W, N, K, act, M, dst, ldd, s, bias, none);
+    if (!e || (!e->rope && !e->glu)) return launch_epi<QT, EPI_PLAIN>(W, N, K, act, M, dst, ldd, s, bias, e ? *e : none);
     if (e->rope) return launch_epi<QT, EPI_ROPE>(W, N, K, act, M, dst, ldd, s, bias, *e);
     if (e->q8) return launch_epi<QT, EPI_GLU_Q8>(W, N, K, act, M, dst, ldd, s, bias, *e);
     return launch_epi<QT, EPI_GLU>(W, N, K, act, M, dst, ldd, s, bias, *e);
@@ -617,6 +685,11 @@ GemmI8Plan gemm_i8_plan(int64_t N, int64_t K) {
     return p;
 }
 
+// measured at 16 rows on the Qwen2.5-1.5B shapes (96 row tiles), two workgroups per tile
+// against one: down (K = 8960) 11.76 -> 8.48 us, o (K = 1536) 5.28 -> 4.76 us; a CU streams
+// at most ~20 GB/s, so a launch of fewer workgroups than CUs is bound by its workgroup count
+bool gemm_i8_halves(int64_t N, int64_t K) { return gemm_i8_plan(N, K).ks == 4 && cdiv(N, 16) <= 128; }
+
 int gemm_i8(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst,
             int64_t ldd, hipStream_t s, const float* bias, const I8Epi* epi) {
     if (K % GEMM_I8_K_ALIGN != 0 || M < 1 || M > GEMM_I8_MAX_M)
@@ -633,6 +706,8 @@ int gemm_i8(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act
         if (epi->q8 && (reinterpret_cast<uintptr_t>(epi->q8) & 15) != 0)
             return fail(GQ_ERR_INVALID, "gemm_i8: quantized rows must be 16-byte aligned");
     }
+    if (epi && epi->slab && (epi->rope || epi->glu || bias || !gemm_i8_halves(N, K)))
+        return fail(GQ_ERR_INVALID, "gemm_i8: two output halves only for products gemm_i8_halves splits, no bias");
     if (type == GQ_TYPE_Q8_0) return launch<GQ_TYPE_Q8_0>(W, N, K, act, M, dst, ldd, s, bias, epi);
     return launch<GQ_TYPE_Q4_0>(W, N, K, act, M, dst, ldd, s, bias, epi);
 }

@@ -31,6 +31,7 @@ struct ActPrep {
     int64_t K;
     int rms, glu;
     float eps;
+    const float* d2 = nullptr;  // with d: v = x + (d + d2), d2's rows at the stride ds
 };
 int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, float* rs, hipStream_t s);
 // The same prologue for gemm_i8 (M <= 16): the quants of quantize_row_q8_0 as int8 in
@@ -119,6 +120,11 @@ struct GemmI8Plan {
     int64_t wgs;
 };
 GemmI8Plan gemm_i8_plan(int64_t N, int64_t K);
+// plain products of at most 128 row tiles in 4 K parts take K in two halves (the sum of
+// half 0, then of half 1, then half 0 + half 1, then the bias): one 8-wave workgroup per
+// tile, or without a bias and with I8Epi::slab two workgroups per tile writing one half
+// each for the consumer to add
+bool gemm_i8_halves(int64_t N, int64_t K);
 // Output-side fusions of gemm_i8 (the GEMV's, on the same logical row pairs: pair_row):
 //   rope: ROPE + SET_ROWS of a fused QKV product (rp; dst unused), N % 16 == 0;
 //   glu: SWIGLU of the pairs (gate row c, up row c + N/2) into dst[m * ldd + c] (dst may be
@@ -129,6 +135,7 @@ struct I8Epi {
     int64_t pair_lo = 0, pair_h = 0;
     GemvRope rp{};
     uint8_t* q8 = nullptr;
+    int64_t slab = 0;  // gemm_i8_halves products: half h's sum at dst + h * slab floats (0: their sum at dst)
 };
 int gemm_i8(int type, const uint8_t* W, int64_t N, int64_t K, const uint8_t* act, int64_t M, float* dst,
             int64_t ldd, hipStream_t s, const float* bias = nullptr, const I8Epi* epi = nullptr);

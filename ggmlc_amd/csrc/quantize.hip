@@ -106,7 +106,7 @@ int quantize_q8_0_f16(const float* x, int64_t nrows, int64_t K, int64_t x_stride
 }
 
 // ---- fused activation prologue of the GEMM path ----------------------------------
-// One workgroup per activation row: v = x (+ d, stored to `sum`), then RMS_NORM
+// One workgroup per activation row: v = x (+ d, or + (d + d2), stored to `sum`), then RMS_NORM
 // (v * scale, the sum of squares in the order of k_rms_norm) or SWIGLU of the row's
 // halves (silu(x[c]) * x[K + c], the arithmetic of k_swiglu), then the fp16(d * q)
 // of quantize_row_q8_0 — the bits of ADD -> RMS_NORM -> quantize (or SWIGLU ->
@@ -153,6 +153,12 @@ __global__ __launch_bounds__(256) void k_act_prep(ActPrep a, uint16_t* __restric
             if (a.d) {
                 float w[8];
                 load8<VEC>(a.d + m * a.ds + (int64_t)t * 8, valid, w);
+                if (a.d2) {  // a product left in two halves: their sum first
+                    float w2[8];
+                    load8<VEC>(a.d2 + m * a.ds + (int64_t)t * 8, valid, w2);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) w[i] = w[i] + w2[i];
+                }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + w[i];
                 if (a.sum && valid) {
@@ -240,7 +246,8 @@ int act_prep_i8(const ActPrep& a, int64_t M, uint8_t* y, hipStream_t s) {
     if (M == 0) return GQ_OK;
     if (M > GEMM_I8_MAX_M || a.K > PREP_MAX_K || a.K % QK) return fail(GQ_ERR_UNSUPPORTED, "act_prep_i8: shape");
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.xs % 4 == 0) &&
-                     (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) && a.K % 4 == 0;
+                     (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) &&
+                     (reinterpret_cast<uintptr_t>(a.d2) & 15) == 0 && a.K % 4 == 0;
     uint16_t* yy = reinterpret_cast<uint16_t*>(y);
     const dim3 g((unsigned)M);
     // without RMS_NORM no value spans the row: one workgroup per row and 2048-element chunk
@@ -269,7 +276,8 @@ int act_prep(const ActPrep& a, int64_t M, uint16_t* y, int64_t y_stride, float* 
     if (M == 0) return GQ_OK;
     if (a.K > PREP_MAX_K || a.K % QK) return fail(GQ_ERR_UNSUPPORTED, "act_prep: K too large");
     const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.xs % 4 == 0) &&
-                     (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) && a.K % 4 == 0;
+                     (!a.d || (((reinterpret_cast<uintptr_t>(a.d) & 15) == 0) && a.ds % 4 == 0)) &&
+                     (reinterpret_cast<uintptr_t>(a.d2) & 15) == 0 && a.K % 4 == 0;
     const dim3 g((unsigned)M);
     if (vec) {  // the configs' K: 960 and 1536 (1 chunk), 2560 and 4096 (2), 8960 (5), 11008 (6)
         switch (cdiv(a.K, 2048)) {

@@ -200,7 +200,8 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
     epilogue, the attention's split merge quantizing the o projection's input, and
     gate_up's epilogue writing SWIGLU's rows quantized for down — the quantize steps of
     the unfused ops moved into their producers (bit-identical), 3 launches fewer per
-    layer."""
+    layer; o and down, where the int8 path takes K in two halves (narrow products), leave
+    the halves' sums for the next prologue's ADD to add (bit-identical too)."""
     c = w.cfg
     qd, kvd = c.q_dim, c.kv_dim
     # more than 4 rows without a trace: the GEMM path with ADD / RMS_NORM / SWIGLU fused
@@ -215,6 +216,7 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
     # prologue (x_next = x + proj, stored for the following ADD), alternating buffers
     other = {id(b["x"]): b["x_alt"], id(b["x_alt"]): b["x"]}
     pending = None  # proj still to be added to x
+    pend_halves = False  # pending holds a product's two halves of K ([2, s, n_embd])
     for li, L in enumerate(w.layers):
         if fused:  # ADD + RMS_NORM + QKV + ROPE x2 + SET_ROWS x2 in one launch (bit-identical)
             nx = other[id(x)] if pending is not None else None
@@ -228,7 +230,7 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             ops.mul_mat_fused(L.qkv, x, rms_eps=c.rms_eps, x_add=pending, x_sum=nx, ws=ws, bias=L.qkv_b, int8=True,
                               rope_kv=ops.RopeKv(c.n_head, c.n_head_kv, c.head_dim, b["pos_ids"], c.head_dim, 2,
                                                  c.rope_base, b["kv_idx"], b["q"], k_cache[li], v_cache[li],
-                                                 cache=b["rope_cs"]))
+                                                 cache=b["rope_cs"]), x_add_halves=pend_halves)
             x = nx if nx is not None else x
             q = b["q"]
         else:
@@ -262,15 +264,19 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
         else:
             attend(li, q)
         rec("attn", li, b["attn"])
-        if q8:  # o from the merge's quantized rows; SWIGLU's rows quantized for down
-            o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], x_q8=b["q8_o"], ws=ws, bias=L.o_b,
-                                  int8=True)
+        if q8:  # o from the merge's quantized rows; SWIGLU's rows quantized for down; o and
+            # down in two halves of K where the int8 path splits them
+            av = b["attn"].view(s, qd)
+            oh = ops.mul_mat_halves(L.o, av, L.o_b, int8=True)
+            o = ops.mul_mat_fused(L.o, av, out=b["proj2"] if oh else b["proj"], x_q8=b["q8_o"], ws=ws, bias=L.o_b,
+                                  int8=True, out_halves=oh)
             nx = other[id(x)]
             ops.mul_mat_fused(L.gate_up, x, rms_eps=c.rms_eps, x_add=o, x_sum=nx, swiglu=True, out_q8=b["q8_d"],
-                              no_out=True, ws=ws, bias=L.gate_up_b, int8=True)
+                              no_out=True, ws=ws, bias=L.gate_up_b, int8=True, x_add_halves=oh)
             x = nx
-            pending = ops.mul_mat_fused(L.down, b["act"], out=b["proj"], x_q8=b["q8_d"], ws=ws, bias=L.down_b,
-                                        int8=True)
+            pend_halves = ops.mul_mat_halves(L.down, b["act"], L.down_b, int8=True)
+            pending = ops.mul_mat_fused(L.down, b["act"], out=b["proj2"] if pend_halves else b["proj"],
+                                        x_q8=b["q8_d"], ws=ws, bias=L.down_b, int8=True, out_halves=pend_halves)
         elif fused:
             o = ops.mul_mat_fused(L.o, b["attn"].view(s, qd), out=b["proj"], bias=L.o_b)
             nx = other[id(x)]
@@ -299,9 +305,13 @@ def forward(w: ModelWeights, s: int, b: dict, ids: torch.Tensor, k_cache: list, 
             ops.add(x, d, out=x)
         rec("x_out", li, x)
     if fused or pro:
-        return ops.mul_mat_fused(w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps,
-                                 x_add=pending[r0:] if pending is not None else None, ws=ws,
-                                 int8=q8 and w.lm_head.K % 256 == 0 and w.lm_head.data.data_ptr() % 16 == 0)
+        head8 = q8 and w.lm_head.K % 256 == 0 and w.lm_head.data.data_ptr() % 16 == 0
+        if pend_halves and not head8 and s - r0 <= 4:  # the GEMV path adds one tensor: the halves' sum first
+            pending, pend_halves = ops.add(pending[0], pending[1], out=b["proj"]), False
+        if pending is not None:
+            pending = pending[:, r0:] if pend_halves else pending[r0:]
+        return ops.mul_mat_fused(w.lm_head, x[r0:], out=out, rms_eps=c.rms_eps, x_add=pending, ws=ws, int8=head8,
+                                 x_add_halves=pend_halves)
     h = ops.rms_norm(x[r0:], c.rms_eps, out=b["h"][:s - r0])
     rec("hf", -1, h)
     return ops.mul_mat(w.lm_head, h, out=out, ws=ws)
@@ -343,6 +353,7 @@ class Decoder:
                 "k": torch.empty((1, s, c.n_head_kv, c.head_dim), **f32),
                 "attn": torch.empty((s, c.n_head, c.head_dim), **f32),
                 "proj": torch.empty((s, c.n_embd), **f32),
+                "proj2": torch.empty((2, s, c.n_embd), **f32),  # a product's two halves of K
                 "gu": torch.empty((s, 2 * c.n_ff), **f32),
                 "act": torch.empty((s, c.n_ff), **f32),
                 "logits": torch.empty((1, c.n_vocab), **f32),

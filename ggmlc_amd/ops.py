@@ -204,7 +204,8 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
                   swiglu: bool = False, add: torch.Tensor | None = None, x_add: torch.Tensor | None = None,
                   x_sum: torch.Tensor | None = None, rope_kv: RopeKv | None = None, x_swiglu: bool = False,
                   ws: Workspace | None = None, bias: torch.Tensor | None = None, out_q8: torch.Tensor | None = None,
-                  x_q8: torch.Tensor | None = None, no_out: bool = False, int8: bool = False) -> torch.Tensor | None:
+                  x_q8: torch.Tensor | None = None, no_out: bool = False, int8: bool = False,
+                  out_halves: bool = False, x_add_halves: bool = False) -> torch.Tensor | None:
     """MUL_MAT fused with its graph neighbours, bit-identical to the unfused ops:
     x_add -> x + x_add first (stored to x_sum when given); rms_eps -> RMS_NORM;
     x_swiglu -> the input is SWIGLU of x's two halves (x [..., 2K]); swiglu -> SWIGLU of
@@ -216,14 +217,20 @@ def mul_mat_fused(w: QWeight, x: torch.Tensor, out: torch.Tensor | None = None, 
     K % 256 == 0) also swiglu and rope_kv, plus out_q8 (uint8 [q8_rows_bytes(N / 2)]: with
     swiglu, the result rows quantized for the next product; no_out: only those) and x_q8
     (x's rows already quantized, e.g. another product's out_q8: x gives the shape only);
-    int8 -> the int8 path also for 1..4 rows."""
+    int8 -> the int8 path also for 1..4 rows. out_halves (where :func:`mul_mat_halves`
+    says so; x 2-d): out [2, M, N] holds the sums over K's two halves, out[0] + out[1]
+    being the product's bits; x_add_halves: x_add is such a pair [2, M, K], x + (x_add[0]
+    + x_add[1]) being added."""
     if x.dtype != torch.float32:
         raise ValueError("mul_mat_fused: x must be float32")
     n_out = w.N // 2 if swiglu else w.N
     if out is None and rope_kv is None and not no_out:
-        out = torch.empty(x.shape[:-1] + (n_out,), dtype=torch.float32, device=x.device)
+        out = torch.empty(((2,) if out_halves else ()) + x.shape[:-1] + (n_out,), dtype=torch.float32,
+                          device=x.device)
     f = _lib.gq_mul_mat_fusion()
     f.b_swiglu = 1 if x_swiglu else 0
+    f.out_halves = 1 if out_halves else 0
+    f.b_add_halves = 1 if x_add_halves else 0
     if out_q8 is not None:
         f.out_q8 = out_q8.data_ptr()
     if x_q8 is not None:
@@ -319,6 +326,20 @@ def flash_attn_paged(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
         check(L.gq_flash_attn_paged(qd, kd, vd, _desc(page_table), _desc(seq_len), page_size, max_len, scale, od,
                                     ptr, size, _stream()))
     return out
+
+
+def mul_mat_halves(w: QWeight, x: torch.Tensor, bias: torch.Tensor | None = None, int8: bool = False) -> bool:
+    """Whether the plain product w x (bias optional; int8 as in :func:`mul_mat_fused`)
+    takes K in two halves on the int8 path, so that :func:`mul_mat_fused` accepts
+    out_halves (gq_mul_mat_fused_halves)."""
+    f = _lib.gq_mul_mat_fusion()
+    f.int8 = 1 if int8 else 0
+    bd = _desc(bias) if bias is not None else None
+    if bd is not None:
+        f.bias = ctypes.pointer(bd)
+    rc = _lib.load().gq_mul_mat_fused_halves(w.desc(), _desc(x), ctypes.byref(f))
+    check(min(rc, 0))
+    return rc == 1
 
 
 def q8_rows_bytes(K: int) -> int:

@@ -392,6 +392,7 @@ class BatchDecoder:
                 "k": torch.empty((1, B, c.n_head_kv, c.head_dim), **f32),
                 "attn": torch.empty((B, c.n_head, c.head_dim), **f32),
                 "proj": torch.empty((B, c.n_embd), **f32),
+                "proj2": torch.empty((2, B, c.n_embd), **f32),  # a product's two halves of K
                 "gu": torch.empty((B, 2 * c.n_ff), **f32),
                 "act": torch.empty((B, c.n_ff), **f32),
                 "logits": torch.empty((B, c.n_vocab), **f32),

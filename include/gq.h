@@ -153,6 +153,17 @@ int gq_mul_mat(const gq_tensor* a, const gq_tensor* b, gq_tensor* dst, void* wor
  *             and the input-side fusions are excluded;
  *   int8:     the int8 path also for 1..4 rows (where the GEMV is the default), so a
  *             small batch can use the handoffs above;
+ *   out_halves: plain products the int8 path takes in two halves of K
+ *             (gq_mul_mat_fused_halves() == 1: at most 128 16-row tiles in 4 K parts,
+ *             no bias, no output-side fusion) leave the two halves' sums to the
+ *             consumer, one workgroup per half and tile: dst F32 [N, M, 2, 1] (b 2-d),
+ *             slab h the sum over K's half h; the product is slab 0 + slab 1 in fp32,
+ *             the bits of the call without out_halves. No counterpart in the
+ *             reference: narrow products (the Qwen2.5-1.5B o and down projections) then
+ *             stream on twice as many CUs;
+ *   b_add_halves: b_add is such a pair, F32 [K, M, 2, 1]: the ADD adds slab 0 +
+ *             slab 1 (GEMM path), so b + (slab 0 + slab 1) has the bits of the ADD of
+ *             the unsplit product;
  * add with M > 4, the other output-side fusions off the int8 path, rope_kv shapes
  * outside the conditions above and b_swiglu on the GEMV path return
  * GQ_ERR_UNSUPPORTED and the caller runs those ops unfused. The GEMM path takes
@@ -189,7 +200,13 @@ typedef struct gq_mul_mat_fusion {
     void* out_q8;            /* int8 path with swiglu: the quantized SWIGLU rows, or NULL */
     const void* b_q8;        /* int8 path: b's rows already quantized, or NULL */
     int32_t int8;            /* 1: the int8 path for 1..16 rows, also 1..4 (GQ_ERR_UNSUPPORTED off it) */
+    int32_t out_halves;      /* dst holds the sums of K's two halves (int8 path, see above) */
+    int32_t b_add_halves;    /* b_add holds two slabs whose sum is added (GEMM path) */
 } gq_mul_mat_fusion;
+/* 1 when gq_mul_mat_fused(a, b, ., f) takes K in two halves, so f->out_halves may be
+ * set (out_halves itself is ignored here), 0 when it does not, a negative GQ_ERR_*
+ * when the call is invalid. */
+int gq_mul_mat_fused_halves(const gq_tensor* a, const gq_tensor* b, const gq_mul_mat_fusion* f);
 /* The quantized activation rows of the int8 path (up to 16 rows m of K values, K % 32
  * == 0; no counterpart in the reference, which quantizes src1 inside each MUL_MAT):
  * per quant block j of K, the 32 int8 quants of row m at byte (j * 16 + m) * 32, its

@@ -93,6 +93,61 @@ def test_other_entry_points_validate_on_host(lib):
     assert lib.gq_soft_max(x, None, 1.0, 0.5, _t(_lib.F32, [10, 3, 1, 1], [4, 40, 120, 120]), None) == -1
 
 
+def test_mul_mat_halves_plan_and_rejects_without_device(lib):
+    """gq_mul_mat_fused_halves: plain int8 products of at most 128 row tiles in 4 K parts
+    and no bias take K in two halves; out_halves elsewhere, slabs of the wrong shape and
+    b_add_halves without b_add or off the GEMM path are refused before any launch (a
+    valid request reaches the workspace check)."""
+    w = _t(_lib.Q8_0, [1536, 1536], [34, 1632])     # Qwen2.5-1.5B o: 96 tiles, 6 steps
+    wide = _t(_lib.Q8_0, [1536, 4096], [34, 1632])  # 256 tiles
+    short = _t(_lib.Q8_0, [768, 1536], [34, 816])   # 3 steps: one K part
+    x = _t(_lib.F32, [1536, 16], [4, 6144])
+    i8 = _lib.gq_mul_mat_fusion()
+    i8.int8 = 1
+    assert lib.gq_mul_mat_fused_halves(w, x, ctypes.byref(i8)) == 1
+    assert lib.gq_mul_mat_fused_halves(wide, x, ctypes.byref(i8)) == 0
+    assert lib.gq_mul_mat_fused_halves(short, _t(_lib.F32, [768, 16], [4, 3072]), ctypes.byref(i8)) == 0
+    bias = _t(_lib.F32, [1536, 1, 1, 1], [4, 6144, 6144, 6144])
+    ib = _lib.gq_mul_mat_fusion()
+    ib.int8, ib.bias = 1, ctypes.pointer(bias)
+    assert lib.gq_mul_mat_fused_halves(w, x, ctypes.byref(ib)) == 0
+    sw = _lib.gq_mul_mat_fusion()
+    sw.int8, sw.swiglu = 1, 1
+    assert lib.gq_mul_mat_fused_halves(w, x, ctypes.byref(sw)) == 0
+    assert lib.gq_mul_mat_fused_halves(w, _t(_lib.F32, [1536, 17], [4, 6144]), ctypes.byref(i8)) == -2
+    # M 1..4 without int8: the GEMV path, no halves
+    assert lib.gq_mul_mat_fused_halves(w, _t(_lib.F32, [1536, 2], [4, 6144]), ctypes.byref(_lib.gq_mul_mat_fusion())) == 0
+    two = _t(_lib.F32, [1536, 16, 2, 1], [4, 6144, 98304, 196608])
+    oh = _lib.gq_mul_mat_fusion()
+    oh.int8, oh.out_halves = 1, 1
+    assert lib.gq_mul_mat_fused(w, x, two, ctypes.byref(oh), None) == -3  # accepted: needs the workspace
+    assert lib.gq_mul_mat_fused(wide, x, _t(_lib.F32, [4096, 16, 2, 1], [4, 16384, 262144, 524288]),
+                                ctypes.byref(oh), None) == -1
+    assert b"out_halves" in lib.gq_last_error()
+    one = _t(_lib.F32, [1536, 16, 1, 1], [4, 6144, 98304, 98304])
+    assert lib.gq_mul_mat_fused(w, x, one, ctypes.byref(oh), None) == -1
+    overlap = _t(_lib.F32, [1536, 16, 2, 1], [4, 6144, 6144, 12288])
+    assert lib.gq_mul_mat_fused(w, x, overlap, ctypes.byref(oh), None) == -1
+    ohb = _lib.gq_mul_mat_fusion()
+    ohb.int8, ohb.out_halves, ohb.bias = 1, 1, ctypes.pointer(bias)
+    assert lib.gq_mul_mat_fused(w, x, two, ctypes.byref(ohb), None) == -1
+    # the consumer's ADD of two slabs
+    d = _t(_lib.F32, [1536, 16], [4, 6144])
+    ba = _lib.gq_mul_mat_fusion()
+    ba.int8, ba.rms_norm, ba.rms_eps, ba.b_add_halves = 1, 1, 1e-5, 1
+    assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(ba), None) == -1  # no b_add
+    ba.b_add = ctypes.pointer(one)
+    assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(ba), None) == -1  # one slab
+    ba.b_add = ctypes.pointer(two)
+    assert lib.gq_mul_mat_fused(w, x, d, ctypes.byref(ba), None) == -3  # accepted
+    g1 = _lib.gq_mul_mat_fusion()
+    g1.rms_norm, g1.rms_eps, g1.b_add_halves = 1, 1e-5, 1
+    two1 = _t(_lib.F32, [1536, 1, 2, 1], [4, 6144, 6144, 12288])
+    g1.b_add = ctypes.pointer(two1)
+    assert lib.gq_mul_mat_fused(w, _t(_lib.F32, [1536, 1], [4, 6144]), _t(_lib.F32, [1536, 1], [4, 6144]),
+                                ctypes.byref(g1), None) == -2  # the GEMV path
+
+
 def test_python_binding_raises(lib):
     with pytest.raises(_lib.GQError):
         _lib.check(-1)

@@ -250,6 +250,8 @@ def test_executor_paged_batched_decode_matches_reference(tmp_path, kind):
         summ = ex.runtime_graph_summary()
         assert summ["last_run_replayed"] == (i > 0) and summ["paged_kv"]
         assert summ["n_flash_attn"] == c.n_layer
+        # the int8 chain leaves the o projection (1536 -> 256, 16 tiles) in two halves of K
+        assert any("(K halves)" in k for k in summ["ops"]) == (kind == "qwen"), summ["ops"]
         for b in range(B):
             _check_spread(out[b], *_ref_step(refs[b], singles[b], tid_in, tid_out, toks[b], lens[b] + i), (i, b))
         toks = out.argmax(axis=1).astype(np.int32)

@@ -35,6 +35,27 @@ def plan(N, K):
     return ks, waves, cdiv(tiles, waves // ks)
 
 
+def halves(N, K):
+    """gemm_i8.hip gemm_i8_halves: plain products of at most 128 tiles in 4 K parts"""
+    return plan(N, K)[0] == 4 and cdiv(N, 16) <= 128
+
+
+def half_range(spl, bx, wave, nsteps, ks=4):
+    """k_gemm_i8's steps of a wave with SPL (1: 8 waves per tile; 2: two workgroups per
+    tile, bx & 1 the half): (tile, half, part within the half, s0, s1)"""
+    parts = ks * (2 if spl == 1 else 1)
+    tile = (bx >> 1 if spl == 2 else bx) * (4 // ks) + wave // parts
+    kp = wave % parts
+    half = bx & 1 if spl == 2 else kp // ks
+    kh = kp % ks if spl == 1 else kp
+    nhs = (nsteps + 1) // 2
+    hbeg = half * nhs
+    hend = min(nsteps, hbeg + nhs)
+    sp = cdiv(nhs, ks)
+    s0 = min(hend, hbeg + kh * sp)
+    return tile, half, kh, s0, min(hend, s0 + sp)
+
+
 def wave_range(bx, wave, ks, nsteps, waves=4):
     tile = bx * (waves // ks) + wave // ks
     kp = wave % ks
@@ -358,6 +379,50 @@ def test_emulated_split_order_equals_the_split(nsteps, ord_):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("nsteps", [4, 5, 6, 7, 9, 35, 64])
+def test_emulated_halves_order_equals_the_halves(nsteps):
+    """SPL with ORD = 8 (one-part launches: the quantized SWIGLU rows): one wave walking
+    every step, folding at the starts of the 8 parts of K's two halves (empty parts start
+    where the next one does: the fold cascades in part order), then (half 0's parts in
+    order) + (half 1's parts in order), gives the float32 bits of the halves over waves
+    (8 waves, or two workgroups whose slabs are added)."""
+    rng = np.random.default_rng(nsteps)
+    contrib = (rng.standard_normal((nsteps, 8)) * 10.0 ** rng.integers(-3, 3, (nsteps, 8))).astype(np.float32)
+    # the waves: part kh of half h sums steps half_range(...) from 0
+    sums = {}
+    for wave in range(8):
+        _, h, kh, s0, s1 = half_range(1, 0, wave, nsteps)
+        acc = np.zeros(8, np.float32)
+        for s in range(s0, s1):
+            acc = np.float32(acc + contrib[s])
+        sums[(h, kh)] = acc
+    a0, a1 = sums[(0, 0)], sums[(1, 0)]
+    for k in range(1, 4):
+        a0, a1 = np.float32(a0 + sums[(0, k)]), np.float32(a1 + sums[(1, k)])
+    want = np.float32(a0 + a1)
+    # the one-wave fold (k_gemm_i8's pstart / fold / kl)
+    nhs = (nsteps + 1) // 2
+    spo = cdiv(nhs, 4)
+
+    def pstart(k):
+        return min(nhs, k * spo) if k < 4 else min(nsteps, nhs + (k - 4) * spo)
+
+    part = [np.zeros(8, np.float32) for _ in range(8)]
+    acc = np.zeros(8, np.float32)
+    for s in range(nsteps):
+        for k in range(1, 8):
+            if s == pstart(k):
+                part[k - 1], acc = acc, np.zeros(8, np.float32)
+        acc = np.float32(acc + contrib[s])
+    kl = max([0] + [k for k in range(1, 8) if pstart(k) <= nsteps - 1])
+    part[kl] = acc
+    b0, b1 = part[0], part[4]
+    for k in range(1, 4):
+        b0, b1 = np.float32(b0 + part[k]), np.float32(b1 + part[4 + k])
+    got = np.float32(b0 + b1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_plan_of_the_configs():
     """the launch shapes of the configs' batched-decode products"""
     assert plan(2048, 1536) == (4, 4, 128)       # Qwen2.5-1.5B qkv
@@ -366,6 +431,40 @@ def test_plan_of_the_configs():
     assert plan(1536, 8960) == (4, 4, 96)        # down
     assert plan(151936, 1536) == (1, 4, 2374)    # tied head
     assert plan(4096, 11008) == (4, 4, 256)      # 7B down
+
+
+def test_halves_plan_of_the_configs():
+    """the configs[4] o and down (96 tiles) take K in halves, QKV (128 tiles) would as a
+    plain product; gate|up, the head and the 7B products (256 tiles and more) do not, nor
+    products of fewer than 4 steps"""
+    assert halves(1536, 1536) and halves(1536, 8960) and halves(2048, 1536)
+    assert not halves(17920, 1536) and not halves(151936, 1536) and not halves(4096, 11008)
+    assert not halves(4096, 4096) and not halves(256, 768)
+    assert halves(2048, 1024) and not halves(2064, 1024)
+
+
+@pytest.mark.parametrize("nsteps", [4, 5, 6, 7, 35, 64])
+@pytest.mark.parametrize("spl", [1, 2])
+def test_halves_cover_every_step_once(nsteps, spl):
+    """every tile's waves (8 in one workgroup, or 4 in each of two) cover each step once:
+    half 0 is the first ceil(steps / 2) steps, half 1 the rest, each in 4 consecutive
+    parts in wave order (which is the order the sums are added in)"""
+    tiles = 3
+    wgs = tiles * (2 if spl == 2 else 1)
+    waves = 8 if spl == 1 else 4
+    seen = {t: [] for t in range(tiles)}
+    for bx in range(wgs):
+        for wave in range(waves):
+            tile, half, kh, s0, s1 = half_range(spl, bx, wave, nsteps)
+            assert 0 <= tile < tiles and 0 <= s0 <= s1 <= nsteps
+            seen[tile].append((half, kh, s0, s1))
+    nhs = (nsteps + 1) // 2
+    for t, rs in seen.items():
+        rs.sort()
+        assert [(h, k) for h, k, _, _ in rs] == [(h, k) for h in range(2) for k in range(4)]
+        steps = [s for _, _, s0, s1 in rs for s in range(s0, s1)]
+        assert steps == list(range(nsteps))  # once each, in (half, part) order
+        assert all(s1 <= nhs for h, _, _, s1 in rs if h == 0) and all(s0 >= nhs for h, _, s0, _ in rs if h == 1)
 
 
 def staged_copy(qt, K, lac=10, lmh=8):

@@ -430,6 +430,8 @@ def test_mul_mat_fused_rope_kv_with_bias_bit_identical(M):
     (O.Q8_0, 1536, 8960, 16),   # Qwen2.5-1.5B gate_up -> down at batch 16
     (O.Q8_0, 1536, 8960, 5),
     (O.Q4_0, 4096, 11008, 9),   # 7B MLP, 9 rows
+    (O.Q8_0, 1536, 1024, 16),   # gate_up 2048 x 1536 and down 1536 x 1024 in K halves (whole tiles)
+    (O.Q4_0, 2048, 512, 9),     # gate_up 1024 x 2048 in K halves (the ring)
 ])
 def test_swiglu_quantized_rows_feed_down_bit_identical(qtype, K, F, M):
     """gate_up with SWIGLU in the int8 GEMM's epilogue also writes its rows quantized
@@ -515,6 +517,45 @@ def test_gemm_i8_staged_activation_bits(qtype, K, N, M):
     sel = np.unique(np.concatenate([rng.choice(N, size=min(N, 192), replace=False), [0, N - 1]]))
     want = O.mul_mat(w.data.cpu().numpy()[sel], qtype, K, x.cpu().numpy())
     assert mar(got.cpu().numpy()[:, sel], want) < 1e-5
+
+
+@pytest.mark.parametrize("qtype,K,N,M", [
+    (O.Q8_0, 1536, 1536, 16),   # Qwen2.5-1.5B o at batch 16: halves of 3 steps (a part of each empty)
+    (O.Q8_0, 8960, 1536, 16),   # Qwen2.5-1.5B down: 35 steps, halves of 18 and 17
+    (O.Q4_0, 1024, 2048, 5),    # 4 steps (one per part of each half), 128 tiles
+    (O.Q4_0, 4096, 1000, 9),    # a partial last tile
+    (O.Q8_0, 2048, 256, 3),     # 3 rows (int8 forced)
+])
+def test_gemm_i8_halves_bits(qtype, K, N, M):
+    """Narrow plain products (at most 128 row tiles in 4 K parts) take K in two halves:
+    with out_halves two workgroups per tile leave the halves' sums as two slabs whose fp32
+    sum is the product's bits (one 8-wave workgroup per tile adding them in that order),
+    which stay within 1e-5 of the oracle; the next prologue's ADD of the two slabs
+    (x_add_halves, before RMS_NORM, the sum stored) gives the bits of adding the product."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(K + N + M + 5)
+    w = ops.quantize_weights(torch.randn((N, K), generator=g, device=DEV) * 0.02, qtype)
+    x = torch.randn((M, K), generator=g, device=DEV)
+    assert ops.mul_mat_halves(w, x, int8=True)
+    assert not ops.mul_mat_halves(w, x, torch.zeros(N, device=DEV), int8=True)
+    want = ops.mul_mat_fused(w, x, int8=True)
+    halves = torch.full((2, M, N), float("nan"), device=DEV)
+    ops.mul_mat_fused(w, x, out=halves, int8=True, out_halves=True)
+    torch.cuda.synchronize()
+    assert torch.equal((halves[0] + halves[1]).view(torch.int32), want.view(torch.int32))
+    rng = np.random.default_rng(N + K)
+    sel = np.unique(np.concatenate([rng.choice(N, size=min(N, 192), replace=False), [0, N - 1]]))
+    ref = O.mul_mat(w.data.cpu().numpy()[sel], qtype, K, x.cpu().numpy())
+    assert mar(want.cpu().numpy()[:, sel], ref) < 1e-5
+    if N % 256 == 0:  # the consumer: ADD + RMS_NORM + the next product on the int8 path
+        w2 = ops.quantize_weights(torch.randn((512, N), generator=g, device=DEV) * 0.02, qtype)
+        r = torch.randn((M, N), generator=g, device=DEV) * 3.0
+        s1, s2 = torch.empty_like(r), torch.empty_like(r)
+        y1 = ops.mul_mat_fused(w2, r, rms_eps=1e-5, x_add=want, x_sum=s1, int8=True)
+        y2 = ops.mul_mat_fused(w2, r, rms_eps=1e-5, x_add=halves, x_add_halves=True, x_sum=s2, int8=True)
+        torch.cuda.synchronize()
+        assert torch.equal(s1.view(torch.int32), s2.view(torch.int32))
+        assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
 
 
 @pytest.mark.parametrize("qtype,K,N", [(O.Q8_0, 1536, 2048), (O.Q4_0, 4096, 4096)])

@@ -245,11 +245,11 @@ def _model(cfg, seed=7):
     return w, host
 
 
-def _gqa_cfg(qtype):
+def _gqa_cfg(qtype, n_ff=512):
     from ggmlc_amd.model import LlamaConfig
 
     # configs[4]'s attention shape (12 q heads over 2 kv heads of 128) in a small model
-    return LlamaConfig("tiny-gqa6", 2, 256, 12, 2, 128, 512, 512, qtype)
+    return LlamaConfig("tiny-gqa6", 2, 256, 12, 2, 128, n_ff, 512, qtype)
 
 
 @pytest.mark.skipif(not O.ref_available(), reason="needs oracle/_ref")
@@ -304,15 +304,17 @@ def test_batch_decoder_matches_reference_per_sequence(qtype, B, graphs, q8):
     assert bd.pos_host[:B].tolist() == [n + n_new for n in lens]
 
 
-@pytest.mark.parametrize("qtype,B", [(O.Q8_0, 8), (O.Q4_0, 5), (O.Q8_0, 16)])
-def test_batch_decoder_q8_chain_bit_identical(qtype, B):
+@pytest.mark.parametrize("qtype,B,n_ff", [(O.Q8_0, 8, 512), (O.Q4_0, 5, 512), (O.Q8_0, 16, 512), (O.Q4_0, 16, 1024)])
+def test_batch_decoder_q8_chain_bit_identical(qtype, B, n_ff):
     """The batched decode step with the quantized-row handoffs (rope in the QKV epilogue,
-    the merge quantizing o's input, gate_up quantizing down's input) gives exactly the
-    logits of the same step through the separate prologue and rope launches."""
+    the merge quantizing o's input, gate_up quantizing down's input; o, 1536 -> 256, and
+    with n_ff 1024 down too, left in two halves of K for the next prologue's ADD) gives
+    exactly the logits of the same step through the separate prologue and rope launches."""
     import torch
+    from ggmlc_amd import ops
     from ggmlc_amd.paged import BatchDecoder
 
-    cfg = _gqa_cfg(qtype)
+    cfg = _gqa_cfg(qtype, n_ff)
     w, _ = _model(cfg)
     P, max_ctx = 128, 1024
     rng = np.random.default_rng(11)
@@ -327,6 +329,8 @@ def test_batch_decoder_q8_chain_bit_identical(qtype, B):
             bd.kv.ensure_tokens(b, lens[b] + 3)
             bd.prefill(b, prompts[b])
         decs.append(bd)
+    x = torch.empty((B, cfg.n_ff), device="cuda")
+    assert ops.mul_mat_halves(w.layers[0].down, x, int8=True) == (n_ff == 1024)
     tokens = rng.integers(0, cfg.n_vocab, B).astype(np.int32)
     for i in range(3):
         outs = []
