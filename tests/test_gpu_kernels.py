@@ -525,6 +525,7 @@ def test_gemm_i8_staged_activation_bits(qtype, K, N, M):
     (O.Q4_0, 1024, 2048, 5),    # 4 steps (one per part of each half), 128 tiles
     (O.Q4_0, 4096, 1000, 9),    # a partial last tile
     (O.Q8_0, 2048, 256, 3),     # 3 rows (int8 forced)
+    (O.Q8_0, 2048, 1056, 9),    # the consumer (K = 1056) on the fp16 GEMM path's prologue
 ])
 def test_gemm_i8_halves_bits(qtype, K, N, M):
     """Narrow plain products (at most 128 row tiles in 4 K parts) take K in two halves:
@@ -547,12 +548,13 @@ def test_gemm_i8_halves_bits(qtype, K, N, M):
     sel = np.unique(np.concatenate([rng.choice(N, size=min(N, 192), replace=False), [0, N - 1]]))
     ref = O.mul_mat(w.data.cpu().numpy()[sel], qtype, K, x.cpu().numpy())
     assert mar(want.cpu().numpy()[:, sel], ref) < 1e-5
-    if N % 256 == 0:  # the consumer: ADD + RMS_NORM + the next product on the int8 path
+    if N % 32 == 0:  # the consumer: ADD + RMS_NORM + the next product (int8 path where K % 256 == 0)
+        i8 = N % 256 == 0
         w2 = ops.quantize_weights(torch.randn((512, N), generator=g, device=DEV) * 0.02, qtype)
         r = torch.randn((M, N), generator=g, device=DEV) * 3.0
         s1, s2 = torch.empty_like(r), torch.empty_like(r)
-        y1 = ops.mul_mat_fused(w2, r, rms_eps=1e-5, x_add=want, x_sum=s1, int8=True)
-        y2 = ops.mul_mat_fused(w2, r, rms_eps=1e-5, x_add=halves, x_add_halves=True, x_sum=s2, int8=True)
+        y1 = ops.mul_mat_fused(w2, r, rms_eps=1e-5, x_add=want, x_sum=s1, int8=i8)
+        y2 = ops.mul_mat_fused(w2, r, rms_eps=1e-5, x_add=halves, x_add_halves=True, x_sum=s2, int8=i8)
         torch.cuda.synchronize()
         assert torch.equal(s1.view(torch.int32), s2.view(torch.int32))
         assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
